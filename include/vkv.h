@@ -1,0 +1,281 @@
+/*
+ * vkv.h -- C ABI of the MI355X (gfx950) KV-cache hot path for voxtral.cpp.
+ *
+ * Replaces, for the decoder and encoder KV-cache step only, the ggml nodes the
+ * reference builds inside build_decoder_layer (src/voxtral.cpp:2677-2854),
+ * build_encoder_kv_graph (:2166-2350) and build_encoder_steady_graph
+ * (:2459-2487), and the host driver contract of run_decoder_step
+ * (:5219-5360) / run_decoder_prefill (:5161-5213).  The public voxtral.h /
+ * voxtral-stream.h surface is unchanged; its callers reach this path through
+ * voxtral_ctx_decoder_step_incremental (src/voxtral-internal.h:249).
+ *
+ * Conventions (mirroring include/voxtral.h:97-110 and
+ * src/voxtral-c-api.cpp:612-747):
+ *   - every entry point returns vkv_status; nothing throws across the ABI;
+ *   - out-parameters are cleared before validation;
+ *   - device pointers are plain pointers into HIP device memory owned by the
+ *     caller; the cache handle owns the KV storage it allocates;
+ *   - hot-path calls are asynchronous and ordered on the caller's hipStream_t
+ *     (passed as void*, NULL = the null stream); synchronisation is the
+ *     caller's (one sync per token, as at src/voxtral.cpp:5273);
+ *   - one handle is not thread-safe; distinct handles are independent.
+ */
+#ifndef VKV_H
+#define VKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+#ifndef __cplusplus
+#include <stdbool.h>
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VKV_API_VERSION 1u
+#define VKV_MAX_BATCH_STREAMS 32
+
+/* Status values keep the numbering of voxtral_status (include/voxtral.h:97-110). */
+typedef enum vkv_status {
+    VKV_STATUS_OK = 0,
+    VKV_STATUS_INVALID_ARGUMENT = 1,
+    VKV_STATUS_INVALID_STATE = 2,
+    VKV_STATUS_OUT_OF_MEMORY = 3,
+    VKV_STATUS_BACKEND_ERROR = 9,
+    VKV_STATUS_INTERNAL_ERROR = 10,
+    VKV_STATUS_BUFFER_TOO_SMALL = 11
+} vkv_status;
+
+/* Storage types; values follow ggml_type (GGML_TYPE_F32=0, F16=1, Q8_0=8),
+ * the type the reference selects in kv_type_from_env (src/voxtral.cpp:82-105). */
+typedef enum vkv_dtype {
+    VKV_DTYPE_F32 = 0,
+    VKV_DTYPE_F16 = 1,
+    VKV_DTYPE_Q8_0 = 8
+} vkv_dtype;
+
+/* Decoder ring metadata: voxtral_decoder_kv_ring (src/voxtral-internal.h:195-204).
+ * Storage addressing is modulo capacity; positions are absolute. */
+typedef struct vkv_ring {
+    int64_t capacity;
+    int64_t used;
+    int64_t oldest_absolute_position;
+    int64_t next_absolute_position;
+    int64_t wraps;
+    int64_t evictions;
+    int64_t bytes_moved;
+    int64_t full_buffer_moves;
+} vkv_ring;
+
+/* voxtral_decoder_kv_seg / voxtral_enc_kv_seg (src/voxtral-internal.h:206-209, 390) */
+typedef struct vkv_seg {
+    int32_t slot;
+    int32_t len;
+} vkv_seg;
+
+/* voxtral_decoder_kv_plan_t (src/voxtral-internal.h:211-223) */
+typedef struct vkv_plan {
+    int64_t absolute_start;
+    int32_t n_new;
+    vkv_seg write_seg[2];
+    int32_t write_nseg;
+    vkv_seg read_seg[2]; /* oldest -> newest logical order */
+    int32_t read_nseg;
+    int64_t used_after;
+    int64_t oldest_after;
+    int64_t next_after;
+    int64_t evicted;
+    bool wrapped;
+} vkv_plan;
+
+/* voxtral_enc_kv_plan_t (src/voxtral-internal.h:392-427) */
+typedef struct vkv_enc_plan {
+    int64_t q_start;
+    int32_t n_new;
+    int64_t win_start;
+    int64_t win_end;
+    int32_t win_len;
+    vkv_seg read_seg[2];
+    int32_t read_nseg;
+    bool read_wraps;
+    vkv_seg write_seg[2];
+    int32_t write_nseg;
+    bool write_wraps;
+    int64_t conv_mel_start;
+    int64_t conv_mel_end;
+    int32_t conv_slice_start;
+    int64_t evicted;
+} vkv_enc_plan;
+
+/* ---------------------------------------------------------------------------
+ * Ring planners (host only; no device work).
+ * ------------------------------------------------------------------------- */
+
+/* voxtral_decoder_kv_plan (src/voxtral.cpp:1615-1644).  INVALID_ARGUMENT
+ * where the reference returns false (discontinuity, n_new out of (0, capacity],
+ * inconsistent ring). */
+vkv_status vkv_decoder_plan(const vkv_ring *ring, int64_t absolute_start, int32_t n_new,
+                            vkv_plan *out);
+/* decoder_kv_commit_plan (src/voxtral.cpp:1646-1656); bytes_moved stays 0. */
+vkv_status vkv_decoder_commit(vkv_ring *ring, const vkv_plan *plan);
+/* clear_kv_cache (src/voxtral.cpp:1590-1602): metadata-only invalidation. */
+vkv_status vkv_decoder_clear(vkv_ring *ring, int64_t capacity);
+/* voxtral_enc_kv_plan (src/voxtral.cpp:3653-3692). */
+vkv_status vkv_enc_plan_build(int64_t q_start, int32_t n_new, int32_t capacity, int32_t window,
+                              vkv_enc_plan *out);
+/* voxtral_enc_kv_mask_allows (src/voxtral.cpp:3636-3638): 1 if allowed. */
+int32_t vkv_enc_mask_allows(int64_t kv_abs, int64_t q_abs, int32_t window);
+
+/* ---------------------------------------------------------------------------
+ * KV cache storage.
+ * Layout in HBM (one allocation each for K and V):
+ *   [stream][layer][slot][kv_head][head_dim] in `dtype`,
+ * i.e. the reference's ggml tensor [kv_dim, capacity, layers] (ne0 fastest,
+ * src/voxtral.cpp:1443-1454) repeated per stream.  Q8_0 rows are ggml
+ * block_q8_0 arrays (kv_dim/32 blocks of 34 bytes).  Zero-filled once at
+ * creation (src/voxtral.cpp:1456-1464); never cleared per stream.
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_cache vkv_cache;
+
+typedef struct vkv_cache_params {
+    uint32_t struct_size;  /* sizeof(vkv_cache_params) */
+    int32_t n_streams;     /* independent rings sharing the allocation (>=1) */
+    int32_t n_layers;      /* decoder 26, encoder 32 */
+    int32_t capacity;      /* backing slots per (stream, layer): 8192 / 878 */
+    int32_t n_kv_heads;    /* decoder 8, encoder 32 */
+    int32_t head_dim;      /* decoder 128, encoder 64 */
+    int32_t n_q_heads;     /* attention heads (multiple of n_kv_heads): 32 */
+    int32_t dtype;         /* vkv_dtype */
+    int32_t device;        /* HIP device ordinal */
+} vkv_cache_params;
+
+typedef struct vkv_cache_layout {
+    uint64_t row_bytes;    /* bytes per (slot) row = kv_dim elements */
+    uint64_t layer_bytes;  /* capacity * row_bytes */
+    uint64_t stream_bytes; /* n_layers * layer_bytes */
+    uint64_t total_bytes;  /* n_streams * stream_bytes (per K or V) */
+    void *k_base;          /* device pointers */
+    void *v_base;
+} vkv_cache_layout;
+
+vkv_status vkv_cache_create(const vkv_cache_params *params, vkv_cache **out);
+vkv_status vkv_cache_destroy(vkv_cache *cache);
+vkv_status vkv_cache_get_layout(const vkv_cache *cache, vkv_cache_layout *out);
+/* Synchronous device->host copy of rows [slot0, slot0+n_slots) of one
+ * (K or V, stream, layer); which: 0 = K, 1 = V.  For state checks only. */
+vkv_status vkv_cache_read_rows(const vkv_cache *cache, int32_t which, int32_t stream,
+                               int32_t layer, int32_t slot0, int32_t n_slots, void *host_dst,
+                               size_t dst_bytes);
+/* Zero the whole cache (stream-ordered fill kernel, capture-safe). */
+vkv_status vkv_cache_zero(vkv_cache *cache, void *hip_stream);
+
+/* ---------------------------------------------------------------------------
+ * Hot path.  All pointers are device pointers.  Rows are f32 [.. ][kv_dim].
+ * ------------------------------------------------------------------------- */
+
+/* Append: ggml_set_rows / ggml_cpy of projected K/V into the cache
+ * (src/voxtral.cpp:2682-2713 decoder, :2166-2185 encoder).  Rows
+ * src[layer][i] for i in [0, sum(write_seg.len)) are laid down in logical
+ * order across the <=2 write segments, converted once to the cache dtype
+ * (F16: IEEE round-to-nearest-even; Q8_0: block quantizer).  layer_stride is
+ * the distance in floats between consecutive layers of k_src/v_src (0 =
+ * packed).  Layers [layer0, layer0+n_layers) are written in one launch. */
+vkv_status vkv_append(vkv_cache *cache, int32_t stream, int32_t layer0, int32_t n_layers,
+                      const vkv_seg *write_seg, int32_t write_nseg, const float *k_src,
+                      const float *v_src, int64_t layer_stride, void *hip_stream);
+
+/* Ring gather: the logical window concat(read_seg[0], read_seg[1]) of one
+ * layer copied, bit-exact and in the cache dtype, into contiguous rows
+ * (src/voxtral.cpp:2774-2799 decoder oracle, :2285-2331 encoder P>=32). */
+vkv_status vkv_gather(const vkv_cache *cache, int32_t stream, int32_t layer,
+                      const vkv_seg *read_seg, int32_t read_nseg, void *k_dst, void *v_dst,
+                      void *hip_stream);
+
+/* Single-query GQA decode attention over the ring (ggml_flash_attn_ext at
+ * src/voxtral.cpp:2749-2819).  For each stream s in [stream0, stream0+n_streams)
+ * and layer l in [layer0, layer0+n_layers):
+ *   out[s][l][h] = sum_j softmax_j(scale * q[s][l][h] . K[j][h/G]) V[j][h/G]
+ * over the slots of plans[s - stream0].read_seg (the logical window; slot
+ * order is irrelevant, which is the permutation argument of :2801-2807).
+ * q/out: f32 [stream][layer][n_q_heads][head_dim], packed. */
+vkv_status vkv_decode_attn(vkv_cache *cache, int32_t stream0, int32_t n_streams,
+                           int32_t layer0, int32_t n_layers, const vkv_plan *plans,
+                           const float *q, float *out, int32_t n_q_heads, float scale,
+                           void *hip_stream);
+
+/* One decoder KV step for a batch of streams, the KV part of run_decoder_step
+ * (src/voxtral.cpp:5219-5360): plan every ring at positions[s] with n_new=1
+ * (INVALID_ARGUMENT and nothing launched or committed if any plan is
+ * invalid), append k/v (f32 [stream][layer][kv_dim]) at slot pos % capacity,
+ * run decode attention over the post-append window, then commit each ring
+ * (decoder_kv_commit_plan, :1646-1656).  Append and attention are fused in
+ * one launch.  plans_out (optional, host) receives the plans used. */
+vkv_status vkv_decoder_step(vkv_cache *cache, int32_t stream0, int32_t n_streams,
+                            vkv_ring *rings, const int64_t *positions, int32_t layer0,
+                            int32_t n_layers, const float *q, const float *k, const float *v,
+                            float *out, int32_t n_q_heads, float scale, vkv_plan *plans_out,
+                            void *hip_stream);
+
+/* Multi-token causal prefill of one stream (run_decoder_prefill,
+ * src/voxtral.cpp:5161-5213; causal mask :3316-3323): plan n_tokens from
+ * ring->next_absolute_position, append k/v ([layer][n_tokens][kv_dim]), then
+ * attention of q ([layer][n_tokens][n_q_heads][head_dim]) where token t at
+ * absolute position a attends every retained key with position <= a; commit.
+ * Requires the post-append window to be one read segment (as the reference's
+ * one-segment path, :2763-2773). */
+vkv_status vkv_decoder_prefill(vkv_cache *cache, int32_t stream, vkv_ring *ring, int32_t layer0,
+                               int32_t n_layers, int32_t n_tokens, const float *q,
+                               const float *k, const float *v, float *out, int32_t n_q_heads,
+                               float scale, void *hip_stream);
+
+/* Encoder KV step for one stream (build_encoder_kv_graph ring write +
+ * window attention, src/voxtral.cpp:2166-2284; mask :4259-4279): write the
+ * plan's n_new K/V rows ([layer][n_new][kv_dim] f32) through write_seg, then
+ * for query i (absolute position q_start+i) attend the keys of the window
+ * [win_start, win_end) allowed by voxtral_enc_kv_mask_allows(kv, q, window).
+ * q/out: [layer][n_new][n_q_heads][head_dim]. */
+vkv_status vkv_enc_step(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
+                        int32_t window, int32_t layer0, int32_t n_layers, const float *q,
+                        const float *k, const float *v, float *out, int32_t n_q_heads,
+                        float scale, void *hip_stream);
+
+/* Window attention without append: n_q queries with absolute positions
+ * q_pos[0] + i, over keys whose absolute positions are key_pos0 + j for the
+ * logical window described by read_seg (j counts across the segments);
+ * allowed iff kv <= q and (window <= 0 or kv >= q - (window-1)). */
+vkv_status vkv_window_attn(vkv_cache *cache, int32_t stream, int32_t layer0, int32_t n_layers,
+                           const vkv_seg *read_seg, int32_t read_nseg, int64_t key_pos0,
+                           int64_t q_pos0, int32_t n_q, int32_t window, const float *q,
+                           float *out, int32_t n_q_heads, float scale, void *hip_stream);
+
+/* ---------------------------------------------------------------------------
+ * q8_0 KV pack/unpack (ggml block_q8_0 {fp16 d; int8 qs[32]}); n % 32 == 0.
+ * Quantizer: amax = max|x|, d = amax/127, id = d ? 1/d : 0,
+ * qs = round-half-away(x*id), d stored as fp16 (RNE).
+ * ------------------------------------------------------------------------- */
+vkv_status vkv_q8_0_pack(const float *x, void *blocks, int64_t n, void *hip_stream);
+vkv_status vkv_q8_0_unpack(const void *blocks, float *y, int64_t n, void *hip_stream);
+
+/* ---------------------------------------------------------------------------
+ * Seeded synthetic rows (integer Irwin-Hall N(0,1), bit-identical to the CPU
+ * generator used by the tests).  Row (s, l, p) = key(seed, tag, s0+i, l0+j,
+ * p0+k) is written at dst + (i*s_stride + j*l_stride + k*p_stride) * row_len.
+ * ------------------------------------------------------------------------- */
+vkv_status vkv_synth_rows(float *dst, int32_t row_len, uint64_t seed, uint32_t tag, int64_t s0,
+                          int32_t ns, int64_t s_stride, int64_t l0, int32_t nl, int64_t l_stride,
+                          int64_t p0, int32_t np, int64_t p_stride, void *hip_stream);
+
+/* ---------------------------------------------------------------------------
+ * Diagnostics.
+ * ------------------------------------------------------------------------- */
+uint32_t vkv_api_version(void);
+/* Message of the last failing call on this thread ("" if none). */
+const char *vkv_last_error(void);
+/* hipError_t of the last BACKEND_ERROR on this thread (0 if none). */
+int32_t vkv_last_backend_code(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

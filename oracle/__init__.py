@@ -1,0 +1,283 @@
+"""CPU oracle for the KV-cache hot path -- TEST INFRASTRUCTURE ONLY.
+
+Loads oracle/liboracle.so (built by oracle/Makefile) and exposes numpy-friendly
+wrappers.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+may import this package; the product (voxtral.cpp_amd/) never does.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+F32, F16, Q8_0 = 0, 1, 8
+TAG_K, TAG_V, TAG_Q = 1, 2, 3
+TAG_EK, TAG_EV, TAG_EQ = 11, 12, 13
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return LIB_PATH
+
+
+if not os.path.exists(LIB_PATH):
+    build()
+
+lib = ctypes.CDLL(LIB_PATH)
+
+
+class Ring(ctypes.Structure):
+    _fields_ = [("capacity", ctypes.c_int64), ("used", ctypes.c_int64),
+                ("oldest_absolute_position", ctypes.c_int64),
+                ("next_absolute_position", ctypes.c_int64), ("wraps", ctypes.c_int64),
+                ("evictions", ctypes.c_int64), ("bytes_moved", ctypes.c_int64),
+                ("full_buffer_moves", ctypes.c_int64)]
+
+
+class Seg(ctypes.Structure):
+    _fields_ = [("slot", ctypes.c_int32), ("len", ctypes.c_int32)]
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [("absolute_start", ctypes.c_int64), ("n_new", ctypes.c_int32),
+                ("write_seg", Seg * 2), ("write_nseg", ctypes.c_int32),
+                ("read_seg", Seg * 2), ("read_nseg", ctypes.c_int32),
+                ("used_after", ctypes.c_int64), ("oldest_after", ctypes.c_int64),
+                ("next_after", ctypes.c_int64), ("evicted", ctypes.c_int64),
+                ("wrapped", ctypes.c_bool)]
+
+
+class EncPlan(ctypes.Structure):
+    _fields_ = [("q_start", ctypes.c_int64), ("n_new", ctypes.c_int32),
+                ("win_start", ctypes.c_int64), ("win_end", ctypes.c_int64),
+                ("win_len", ctypes.c_int32), ("read_seg", Seg * 2),
+                ("read_nseg", ctypes.c_int32), ("read_wraps", ctypes.c_bool),
+                ("write_seg", Seg * 2), ("write_nseg", ctypes.c_int32),
+                ("write_wraps", ctypes.c_bool), ("conv_mel_start", ctypes.c_int64),
+                ("conv_mel_end", ctypes.c_int64), ("conv_slice_start", ctypes.c_int32),
+                ("evicted", ctypes.c_int64)]
+
+
+_P = ctypes.POINTER
+_vp = ctypes.c_void_p
+_i32, _i64, _u64, _u32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint32
+_f32, _f64 = ctypes.c_float, ctypes.c_double
+
+_protos = {
+    "orc_decoder_plan": (ctypes.c_bool, [_P(Ring), _i64, _i32, _P(Plan)]),
+    "orc_decoder_commit": (None, [_P(Ring), _P(Plan)]),
+    "orc_decoder_clear": (None, [_P(Ring), _i64]),
+    "orc_enc_plan": (ctypes.c_bool, [_i64, _i32, _i32, _i32, _P(EncPlan)]),
+    "orc_enc_mask_allows": (ctypes.c_bool, [_i64, _i64, _i32]),
+    "orc_f32_to_f16_n": (None, [_vp, _vp, _i64]),
+    "orc_f16_to_f32_n": (None, [_vp, _vp, _i64]),
+    "orc_q8_0_quantize": (None, [_vp, _vp, _i64]),
+    "orc_q8_0_dequantize": (None, [_vp, _vp, _i64]),
+    "orc_row_bytes": (_i64, [ctypes.c_int, _i64]),
+    "orc_row_to_f32": (None, [ctypes.c_int, _vp, _vp, _i64]),
+    "orc_row_from_f32": (None, [ctypes.c_int, _vp, _vp, _i64]),
+    "orc_mix64": (_u64, [_u64]),
+    "orc_row_key": (_u64, [_u64, _u32, _i64, _i64, _i64]),
+    "orc_synth_value": (_f32, [_u64, _i64]),
+    "orc_synth_row": (None, [_u64, _vp, _i64]),
+    "orc_append": (None, [ctypes.c_int, _vp, _i64, _i32, _P(Seg), _i32, _vp]),
+    "orc_gather": (None, [_vp, _i64, _P(Seg), _i32, _vp]),
+    "orc_expected_layer": (None, [ctypes.c_int, _vp, _i64, _i64, _i32, _i64, _u64, _u32, _i64,
+                                  _i64]),
+    "orc_decode_attn_f64": (None, [ctypes.c_int, _vp, _vp, _i64, _vp, _i32, _vp, _i32, _i32,
+                                   _i32, _f64, _vp]),
+    "orc_decode_attn_mimic": (None, [ctypes.c_int, _vp, _vp, _i64, _vp, _i32, _vp, _i32, _i32,
+                                     _i32, _f32, _vp]),
+    "orc_window_attn_f64": (None, [ctypes.c_int, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32,
+                                   _i32, _i32, _i32, _i32, _f64, _vp]),
+    "orc_decode_step_mimic_mt": (_f64, [ctypes.c_int, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
+                                        _i32, _i32, _i32, _f32, _vp, _vp, _vp, _i32, _i32]),
+}
+for _n, (_r, _a) in _protos.items():
+    _f = getattr(lib, _n)
+    _f.restype = _r
+    _f.argtypes = _a
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def row_bytes(dtype, n):
+    return int(lib.orc_row_bytes(dtype, n))
+
+
+# ---- planners ----
+def new_ring(capacity):
+    r = Ring()
+    lib.orc_decoder_clear(ctypes.byref(r), capacity)
+    return r
+
+
+def decoder_plan(ring, start, n_new):
+    p = Plan()
+    ok = lib.orc_decoder_plan(ctypes.byref(ring), start, n_new, ctypes.byref(p))
+    return p if ok else None
+
+
+def decoder_commit(ring, plan):
+    lib.orc_decoder_commit(ctypes.byref(ring), ctypes.byref(plan))
+
+
+def enc_plan(q_start, n_new, capacity, window):
+    p = EncPlan()
+    ok = lib.orc_enc_plan(q_start, n_new, capacity, window, ctypes.byref(p))
+    return p if ok else None
+
+
+def enc_mask_allows(kv, q, window):
+    return bool(lib.orc_enc_mask_allows(kv, q, window))
+
+
+def segs_of(segs, n):
+    return [(segs[i].slot, segs[i].len) for i in range(n)]
+
+
+# ---- numerics ----
+def f32_to_f16_bits(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib.orc_f32_to_f16_n(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def f16_bits_to_f32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.float32)
+    lib.orc_f16_to_f32_n(_ptr(h), _ptr(y), h.size)
+    return y
+
+
+def q8_0_quantize(x):
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(x.size // 32 * 34, dtype=np.uint8)
+    lib.orc_q8_0_quantize(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def q8_0_dequantize(blocks, n):
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+    y = np.empty(n, dtype=np.float32)
+    lib.orc_q8_0_dequantize(_ptr(blocks), _ptr(y), n)
+    return y
+
+
+def rows_to_f32(dtype, raw, kv_dim):
+    """raw row bytes (n_rows * row_bytes) -> float32 [n_rows, kv_dim]"""
+    raw = np.frombuffer(raw, dtype=np.uint8) if isinstance(raw, (bytes, bytearray)) else raw
+    rb = row_bytes(dtype, kv_dim)
+    n = raw.size // rb
+    out = np.empty((n, kv_dim), dtype=np.float32)
+    raw = np.ascontiguousarray(raw)
+    lib.orc_row_to_f32(dtype, _ptr(raw), _ptr(out), n * kv_dim)
+    return out
+
+
+def rows_from_f32(dtype, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    kv_dim = x.shape[-1]
+    n = x.size // kv_dim
+    out = np.empty(n * row_bytes(dtype, kv_dim), dtype=np.uint8)
+    lib.orc_row_from_f32(dtype, _ptr(x), _ptr(out), x.size)
+    return out
+
+
+# ---- generator ----
+def row_key(seed, tag, stream, layer, pos):
+    return int(lib.orc_row_key(seed, tag, stream, layer, pos))
+
+
+def synth_row(seed, tag, stream, layer, pos, n):
+    out = np.empty(n, dtype=np.float32)
+    lib.orc_synth_row(lib.orc_row_key(seed, tag, stream, layer, pos), _ptr(out), n)
+    return out
+
+
+def synth_rows(seed, tag, stream, layer, positions, n):
+    return np.stack([synth_row(seed, tag, stream, layer, int(p), n) for p in positions])
+
+
+# ---- cache image ----
+def append(dtype, layer_img, row_b, kv_dim, segs, src):
+    arr = (Seg * 2)()
+    for i, (s, n) in enumerate(segs):
+        arr[i].slot, arr[i].len = s, n
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    lib.orc_append(dtype, _ptr(layer_img), row_b, kv_dim, arr, len(segs), _ptr(src))
+
+
+def gather(layer_img, row_b, segs):
+    arr = (Seg * 2)()
+    total = 0
+    for i, (s, n) in enumerate(segs):
+        arr[i].slot, arr[i].len = s, n
+        total += n
+    out = np.empty(total * row_b, dtype=np.uint8)
+    lib.orc_gather(_ptr(layer_img), row_b, arr, len(segs), _ptr(out))
+    return out
+
+
+def expected_layer(dtype, backing, capacity, kv_dim, next_pos, seed, tag, stream, layer):
+    rb = row_bytes(dtype, kv_dim)
+    out = np.empty(backing * rb, dtype=np.uint8)
+    lib.orc_expected_layer(dtype, _ptr(out), backing, capacity, kv_dim, next_pos, seed, tag,
+                           stream, layer)
+    return out
+
+
+# ---- attention ----
+def decode_attn_f64(dtype, k_img, v_img, row_b, slots, q, n_kv_heads, head_dim, scale):
+    slots = np.ascontiguousarray(slots, dtype=np.int32)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n_q_heads = q.size // head_dim
+    out = np.empty(n_q_heads * head_dim, dtype=np.float64)
+    lib.orc_decode_attn_f64(dtype, _ptr(k_img), _ptr(v_img), row_b, _ptr(slots), slots.size,
+                            _ptr(q), n_q_heads, n_kv_heads, head_dim, scale, _ptr(out))
+    return out.reshape(n_q_heads, head_dim)
+
+
+def decode_attn_mimic(dtype, k_img, v_img, row_b, slots, q, n_kv_heads, head_dim, scale):
+    slots = np.ascontiguousarray(slots, dtype=np.int32)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n_q_heads = q.size // head_dim
+    out = np.empty(n_q_heads * head_dim, dtype=np.float32)
+    lib.orc_decode_attn_mimic(dtype, _ptr(k_img), _ptr(v_img), row_b, _ptr(slots), slots.size,
+                              _ptr(q), n_q_heads, n_kv_heads, head_dim, scale, _ptr(out))
+    return out.reshape(n_q_heads, head_dim)
+
+
+def window_attn_f64(dtype, k_img, v_img, row_b, k_slot, k_pos, q, q_pos, n_q_heads, n_kv_heads,
+                    head_dim, window, scale):
+    k_slot = np.ascontiguousarray(k_slot, dtype=np.int32)
+    k_pos = np.ascontiguousarray(k_pos, dtype=np.int64)
+    q_pos = np.ascontiguousarray(q_pos, dtype=np.int64)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n_q = q_pos.size
+    out = np.empty(n_q * n_q_heads * head_dim, dtype=np.float64)
+    lib.orc_window_attn_f64(dtype, _ptr(k_img), _ptr(v_img), row_b, _ptr(k_slot), _ptr(k_pos),
+                            k_slot.size, _ptr(q), _ptr(q_pos), n_q, n_q_heads, n_kv_heads,
+                            head_dim, window, scale, _ptr(out))
+    return out.reshape(n_q, n_q_heads, head_dim)
+
+
+def decode_step_mimic_mt(dtype, k_cache, v_cache, layer_bytes, row_b, n_layers, n_valid, q,
+                         n_q_heads, n_kv_heads, head_dim, scale, n_threads, k_new=None,
+                         v_new=None, new_slot=0):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.empty(n_layers * n_q_heads * head_dim, dtype=np.float32)
+    kn_arr = np.ascontiguousarray(k_new, dtype=np.float32) if k_new is not None else None
+    vn_arr = np.ascontiguousarray(v_new, dtype=np.float32) if v_new is not None else None
+    kn = _ptr(kn_arr) if kn_arr is not None else None
+    vn = _ptr(vn_arr) if vn_arr is not None else None
+    secs = lib.orc_decode_step_mimic_mt(dtype, _ptr(k_cache), _ptr(v_cache), layer_bytes, row_b,
+                                        n_layers, n_valid, _ptr(q), n_q_heads, n_kv_heads,
+                                        head_dim, scale, _ptr(out), kn, vn, new_slot, n_threads)
+    return secs, out.reshape(n_layers, n_q_heads, head_dim)

@@ -1,0 +1,136 @@
+"""The C ABI boundary without a GPU: libvkv.so loads, exports exactly the
+functions include/vkv.h declares, its struct layouts match the ctypes mirror
+(and the reference's field order), and argument errors come back as statuses
+(never exceptions) with the out-parameters cleared."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+import oracle
+import vkv
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "vkv.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vkv_\w+)\s*\(", text)))
+
+
+def test_exports_match_header():
+    declared = header_functions()
+    out = subprocess.run(["nm", "-D", "--defined-only", vkv.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = sorted(set(re.findall(r" T (vkv_\w+)$", out, flags=re.M)))
+    assert declared == exported
+    assert sorted(vkv.PROTOTYPES) == declared
+    for name in declared:
+        assert hasattr(vkv.lib, name)
+
+
+def test_struct_layout_matches_c():
+    """sizeof/offsetof from a C compilation of vkv.h == the ctypes mirror ==
+    the oracle's restatement of the reference structs."""
+    structs = {
+        "vkv_ring": (vkv.Ring, oracle.Ring),
+        "vkv_seg": (vkv.Seg, oracle.Seg),
+        "vkv_plan": (vkv.Plan, oracle.Plan),
+        "vkv_enc_plan": (vkv.EncPlan, oracle.EncPlan),
+        "vkv_cache_params": (vkv.CacheParams, None),
+        "vkv_cache_layout": (vkv.CacheLayout, None),
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "vkv.h"', "int main(void){"]
+    for cname, (py, _) in structs.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _t in py._fields_:
+            lines.append(f'printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("return 0;}")
+    with tempfile.TemporaryDirectory() as td:
+        src = os.path.join(td, "layout.c")
+        exe = os.path.join(td, "layout")
+        open(src, "w").write("\n".join(lines))
+        subprocess.run(["gcc", "-std=c11", "-I", os.path.join(REPO, "include"), src, "-o", exe],
+                       check=True)
+        got = subprocess.run([exe], capture_output=True, text=True, check=True).stdout.split("\n")
+    table = {}
+    for line in got:
+        if line:
+            name, field, val = line.split()
+            table[(name, field)] = int(val)
+    for cname, (py, orc) in structs.items():
+        assert table[(cname, "size")] == ctypes.sizeof(py), cname
+        if orc is not None:
+            assert ctypes.sizeof(orc) == ctypes.sizeof(py)
+        for f, _t in py._fields_:
+            assert table[(cname, f)] == getattr(py, f).offset, (cname, f)
+            if orc is not None:
+                assert getattr(orc, f).offset == getattr(py, f).offset
+
+
+def test_api_version():
+    assert vkv.lib.vkv_api_version() == 1
+
+
+def test_error_statuses_without_device():
+    L = vkv.lib
+    # planner errors mirror the reference's `false` returns
+    r = vkv.new_ring(8)
+    p = vkv.Plan()
+    p.n_new = 77
+    assert L.vkv_decoder_plan(ctypes.byref(r), 1, 1, ctypes.byref(p)) == vkv.INVALID_ARGUMENT
+    assert p.n_new == 0                                  # out-param cleared first
+    assert "invalid absolute position" in vkv.last_error()
+    assert L.vkv_decoder_plan(None, 0, 1, ctypes.byref(p)) == vkv.INVALID_ARGUMENT
+    assert L.vkv_decoder_plan(ctypes.byref(r), 0, 1, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_decoder_commit(None, None) == vkv.INVALID_ARGUMENT
+    e = vkv.EncPlan()
+    assert L.vkv_enc_plan_build(0, 129, 878, 750, ctypes.byref(e)) == vkv.INVALID_ARGUMENT
+    assert L.vkv_enc_plan_build(-1, 4, 878, 750, ctypes.byref(e)) == vkv.INVALID_ARGUMENT
+    # cache creation: bad shapes are rejected before touching a device
+    h = ctypes.c_void_p(1234)
+    bad = vkv.CacheParams(ctypes.sizeof(vkv.CacheParams), 1, 1, 8, 8, 100, 32, vkv.Q8_0, 0)
+    assert L.vkv_cache_create(ctypes.byref(bad), ctypes.byref(h)) == vkv.INVALID_ARGUMENT
+    assert not h.value
+    small = vkv.CacheParams(8, 1, 1, 8, 8, 128, 32, vkv.F16, 0)
+    assert L.vkv_cache_create(ctypes.byref(small), ctypes.byref(h)) == vkv.INVALID_ARGUMENT
+    odd = vkv.CacheParams(ctypes.sizeof(vkv.CacheParams), 1, 1, 8, 8, 128, 30, vkv.F16, 0)
+    assert L.vkv_cache_create(ctypes.byref(odd), ctypes.byref(h)) == vkv.INVALID_ARGUMENT
+    badtype = vkv.CacheParams(ctypes.sizeof(vkv.CacheParams), 1, 1, 8, 8, 128, 32, 2, 0)
+    assert L.vkv_cache_create(ctypes.byref(badtype), ctypes.byref(h)) == vkv.INVALID_ARGUMENT
+    # hot-path calls on a null cache
+    segs = (vkv.Seg * 2)()
+    assert L.vkv_append(None, 0, 0, 1, segs, 1, None, None, 0, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_gather(None, 0, 0, segs, 1, None, None, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_decode_attn(None, 0, 1, 0, 1, None, None, None, 32, 1.0, None) == vkv.INVALID_ARGUMENT
+    rings = (vkv.Ring * 1)()
+    pos = (ctypes.c_int64 * 1)()
+    plans = (vkv.Plan * 1)()
+    plans[0].n_new = 5
+    assert L.vkv_decoder_step(None, 0, 1, rings, pos, 0, 1, None, None, None, None, 32, 1.0,
+                              plans, None) == vkv.INVALID_ARGUMENT
+    assert plans[0].n_new == 0
+    assert L.vkv_q8_0_pack(None, None, 33, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_q8_0_unpack(None, None, -32, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_synth_rows(None, 4, 1, 1, 0, 1, 1, 0, 1, 1, 0, 1, 1, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_cache_destroy(None) == vkv.OK
+    with pytest.raises(vkv.VkvError) as ei:
+        vkv.decoder_plan(r, 5, 1)
+    assert ei.value.status == vkv.INVALID_ARGUMENT
+
+
+def test_product_does_not_reference_the_oracle():
+    """The shipped library and package neither link nor import the oracle."""
+    out = subprocess.run(["ldd", vkv.LIB_PATH], capture_output=True, text=True).stdout
+    assert "oracle" not in out
+    pkg = os.path.join(REPO, "voxtral.cpp_amd")
+    for root, _dirs, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".cpp", ".hip", ".h")):
+                text = open(os.path.join(root, f)).read()
+                assert "import oracle" not in text and "liboracle" not in text, f

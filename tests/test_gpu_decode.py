@@ -1,0 +1,235 @@
+"""GPU parity of the decoder KV step (append + single-query GQA attention)
+against the oracle, at the decoder shapes: cache state bit-exact, attention
+within 2e-3 (F16 KV) / 1e-2 (q8_0 KV) of the exact fp64 attention and of the
+ggml-mimic reduction order."""
+import ctypes
+import os
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import vkv
+from gpu_util import (SEED, empty_f32, expected_image, layer_image, oracle_decode, plan_slots,
+                      step_inputs, stream_ptr, synth)
+
+pytestmark = pytest.mark.gpu
+
+TOL = {vkv.F16: 2e-3, vkv.F32: 1e-4, vkv.Q8_0: 1e-2}
+SCALE = 1.0 / np.sqrt(128.0)
+POOL = ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
+
+
+def check_cache_state(c, streams, layers, ring_capacity, next_pos):
+    """every listed (stream, layer, K|V) image equals the oracle's closed form"""
+    jobs = [(s, l, w) for s in streams for l in layers for w in (0, 1)]
+    wants = POOL.map(lambda j: expected_image(c, j[2], j[0], j[1], ring_capacity, next_pos[j[0]]), jobs)
+    for (s, l, w), want in zip(jobs, wants):
+        got = layer_image(c, w, s, l)
+        assert np.array_equal(got, want), f"stream {s} layer {l} {'KV'[w]} differs at next={next_pos[s]}"
+
+
+def prefill_by_append(c, ring, stream, n, layers):
+    """positions [next, next+n) written through the planned append path"""
+    start = ring.next_absolute_position
+    plan = vkv.decoder_plan(ring, start, n)
+    k = synth(None, c.kv_dim, vkv.TAG_K, s0=stream, l0=0, nl=layers, p0=start, np_=n)
+    v = synth(None, c.kv_dim, vkv.TAG_V, s0=stream, l0=0, nl=layers, p0=start, np_=n)
+    c.append(stream, 0, layers, vkv.plan_segs(plan.write_seg, plan.write_nseg), k.data_ptr(),
+             v.data_ptr(), hip_stream=stream_ptr())
+    vkv.decoder_commit(ring, plan)
+    return plan
+
+
+@pytest.mark.parametrize("dtype", [vkv.F16, vkv.F32, vkv.Q8_0])
+@pytest.mark.parametrize("capacity", [8192, 1025])
+def test_single_layer_append_then_attend(dtype, capacity):
+    """One decoder layer: 1024 positions prefilled, append position 1024, then
+    1-query attention over all 1025 positions."""
+    with vkv.Cache(n_streams=1, n_layers=1, capacity=capacity, dtype=dtype) as c:
+        ring = vkv.new_ring(capacity)
+        prefill_by_append(c, ring, 0, 1024, 1)
+        q, k, v = step_inputs(c, [1024], n_layers=1)
+        out = empty_f32(1, 1, 4096)
+        rings = (vkv.Ring * 1)(ring)
+        plans = c.decoder_step(0, rings, [1024], 0, 1, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                               out.data_ptr(), SCALE, hip_stream=stream_ptr())
+        assert rings[0].next_absolute_position == 1025 and rings[0].used == 1025
+        check_cache_state(c, [0], [0], capacity, {0: 1025})
+        slots = plan_slots(plans[0])
+        assert len(slots) == 1025
+        q_row = q[0, 0].cpu().numpy()
+        got = out[0, 0].cpu().numpy().reshape(32, 128)
+        exact = oracle_decode(c, 0, 0, slots, q_row)
+        mimic = oracle_decode(c, 0, 0, slots, q_row, mimic=True)
+        assert np.max(np.abs(got - exact)) <= TOL[dtype]
+        assert np.max(np.abs(got - mimic)) <= TOL[dtype]
+        # the unfused attention entry point over the same window agrees bit for bit
+        out2 = empty_f32(1, 1, 4096)
+        c.decode_attn(0, [plans[0]], 0, 1, q.data_ptr(), out2.data_ptr(), SCALE, hip_stream=stream_ptr())
+        torch.cuda.synchronize()
+        assert torch.equal(out, out2)
+
+
+def test_empty_and_tiny_windows():
+    with vkv.Cache(n_streams=1, n_layers=2, capacity=64, dtype=vkv.F16) as c:
+        q = synth(None, 4096, vkv.TAG_Q, nl=2)
+        out = empty_f32(2, 4096)
+        empty = vkv.Plan()
+        c.decode_attn(0, [empty], 0, 2, q.data_ptr(), out.data_ptr(), SCALE, hip_stream=stream_ptr())
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(out) == 0          # no keys -> 0, as ggml's S=0 case
+        ring = vkv.new_ring(64)
+        rings = (vkv.Ring * 1)(ring)
+        for pos in range(3):
+            qq, k, v = step_inputs(c, [pos], n_layers=2)
+            plans = c.decoder_step(0, rings, [pos], 0, 2, qq.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   out.data_ptr(), SCALE, hip_stream=stream_ptr())
+            for layer in range(2):
+                want = oracle_decode(c, 0, layer, plan_slots(plans[0]), qq[0, layer].cpu().numpy())
+                got = out[layer].cpu().numpy().reshape(32, 128)
+                assert np.max(np.abs(got - want)) <= 2e-3
+        # one key: the output is that key's value row exactly (softmax weight 1)
+        vrow = oracle.f16_bits_to_f32(np.frombuffer(c.read_rows(1, 0, 0, 0, 1), np.uint16))
+        c.decode_attn(0, [vkv.decoder_plan(vkv.new_ring(64), 0, 1)], 0, 1, q.data_ptr(),
+                      out.data_ptr(), SCALE, hip_stream=stream_ptr())
+        torch.cuda.synchronize()
+        got = out[0].cpu().numpy().reshape(32, 128)
+        assert np.array_equal(got, np.repeat(vrow.reshape(8, 128), 4, axis=0))
+
+
+def test_decoder_stream_4096_steps_no_wrap():
+    """26 layers, 4096 consecutive steps from an empty 8192 ring."""
+    with vkv.Cache(n_streams=1, n_layers=26, capacity=8192, dtype=vkv.F16) as c:
+        rings = (vkv.Ring * 1)(vkv.new_ring(8192))
+        out = empty_f32(1, 26, 4096)
+        for pos in range(4096):
+            q, k, v = step_inputs(c, [pos])
+            plans = c.decoder_step(0, rings, [pos], 0, 26, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   out.data_ptr(), SCALE, hip_stream=stream_ptr())
+            if pos in (0, 1, 4095):
+                check_cache_state(c, [0], range(26), 8192, {0: pos + 1})
+            if pos in (0, 1, 2047, 4095):
+                for layer in (0, 13, 25):
+                    want = oracle_decode(c, 0, layer, plan_slots(plans[0]), q[0, layer].cpu().numpy())
+                    got = out[0, layer].cpu().numpy().reshape(32, 128)
+                    assert np.max(np.abs(got - want)) <= 2e-3, (pos, layer)
+        assert rings[0].wraps == 0 and rings[0].used == 4096
+
+
+def test_longform_ring_32768_steps():
+    """26 layers, 8192-slot ring, 32768 single-token steps (the ring wraps 3x):
+    ring metadata, full cache state and attention at steps 8191, 8192, 16500,
+    32767."""
+    meta = {8191: (8192, 0, 8192, 0, 0), 8192: (8192, 1, 8193, 1, 1),
+            16500: (8192, 8309, 16501, 2, 8309), 32767: (8192, 24576, 32768, 3, 24576)}
+    with vkv.Cache(n_streams=1, n_layers=26, capacity=8192, dtype=vkv.F16) as c:
+        rings = (vkv.Ring * 1)(vkv.new_ring(8192))
+        out = empty_f32(1, 26, 4096)
+        for pos in range(32768):
+            q, k, v = step_inputs(c, [pos])
+            plans = c.decoder_step(0, rings, [pos], 0, 26, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   out.data_ptr(), SCALE, hip_stream=stream_ptr())
+            if pos in meta:
+                r = rings[0]
+                assert (r.used, r.oldest_absolute_position, r.next_absolute_position, r.wraps,
+                        r.evictions) == meta[pos]
+                assert r.bytes_moved == 0 and r.full_buffer_moves == 0
+                check_cache_state(c, [0], range(26), 8192, {0: pos + 1})
+                for layer in (0, 25):
+                    want = oracle_decode(c, 0, layer, plan_slots(plans[0]), q[0, layer].cpu().numpy())
+                    got = out[0, layer].cpu().numpy().reshape(32, 128)
+                    assert np.max(np.abs(got - want)) <= 2e-3, (pos, layer)
+                print(f"longform step {pos} ok", flush=True)
+
+
+def test_test_capacity_seam_64_of_8192():
+    """A logical ring of 64 slots over the 8192-slot backing store
+    (VOXTRAL_DECODER_KV_TEST_CAPACITY, src/voxtral.cpp:1537-1545): slots >= 64
+    are never touched; wraps every 64 steps."""
+    with vkv.Cache(n_streams=1, n_layers=2, capacity=8192, dtype=vkv.F16) as c:
+        rings = (vkv.Ring * 1)(vkv.new_ring(64))
+        out = empty_f32(1, 2, 4096)
+        for pos in range(200):
+            q, k, v = step_inputs(c, [pos], n_layers=2)
+            plans = c.decoder_step(0, rings, [pos], 0, 2, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   out.data_ptr(), SCALE, hip_stream=stream_ptr())
+            if pos in (63, 64, 130, 199):
+                check_cache_state(c, [0], [0, 1], 64, {0: pos + 1})
+                for layer in (0, 1):
+                    want = oracle_decode(c, 0, layer, plan_slots(plans[0]), q[0, layer].cpu().numpy())
+                    got = out[0, layer].cpu().numpy().reshape(32, 128)
+                    assert np.max(np.abs(got - want)) <= 2e-3
+        assert rings[0].wraps == 3 and rings[0].evictions == 200 - 64
+
+
+def test_invalid_step_is_rejected_before_any_device_work():
+    with vkv.Cache(n_streams=2, n_layers=1, capacity=16, dtype=vkv.F16) as c:
+        rings = (vkv.Ring * 2)(vkv.new_ring(16), vkv.new_ring(16))
+        q, k, v = step_inputs(c, [0, 0], n_layers=1)
+        out = empty_f32(2, 1, 4096)
+        with pytest.raises(vkv.VkvError) as ei:
+            c.decoder_step(0, rings, [0, 5], 0, 1, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                           out.data_ptr(), SCALE, hip_stream=stream_ptr())
+        assert ei.value.status == vkv.INVALID_ARGUMENT
+        assert "stream 1" in ei.value.message
+        assert rings[0].next_absolute_position == 0 and rings[1].next_absolute_position == 0
+        assert not layer_image(c, 0, 0, 0).any() and not layer_image(c, 1, 1, 0).any()
+        big = (vkv.Ring * 1)(vkv.new_ring(17))
+        with pytest.raises(vkv.VkvError):
+            c.decoder_step(0, big, [0], 0, 1, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                           out.data_ptr(), SCALE, hip_stream=stream_ptr())
+
+
+@pytest.mark.parametrize("dtype", [vkv.F16, vkv.Q8_0])
+def test_multi_stream_batch_mixed_fill(dtype):
+    """Independent streams at different fill levels (one wrapped) in one launch."""
+    ns, nl, cap = 5, 3, 512
+    fills = [0, 1, 300, 512, 1500]
+    with vkv.Cache(n_streams=ns, n_layers=nl, capacity=cap, dtype=dtype) as c:
+        rings = (vkv.Ring * ns)(*[vkv.new_ring(cap) for _ in range(ns)])
+        for s, n in enumerate(fills):
+            left = n
+            while left:
+                m = min(cap, left)
+                prefill_by_append(c, rings[s], s, m, nl)
+                left -= m
+        q, k, v = step_inputs(c, fills)
+        out = empty_f32(ns, nl, 4096)
+        plans = c.decoder_step(0, rings, fills, 0, nl, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                               out.data_ptr(), SCALE, hip_stream=stream_ptr())
+        check_cache_state(c, range(ns), range(nl), cap, {s: fills[s] + 1 for s in range(ns)})
+        for s in range(ns):
+            for layer in range(nl):
+                want = oracle_decode(c, s, layer, plan_slots(plans[s]), q[s, layer].cpu().numpy())
+                got = out[s, layer].cpu().numpy().reshape(32, 128)
+                assert np.max(np.abs(got - want)) <= TOL[dtype], (s, layer)
+
+
+def test_q8_0_eight_streams_full_window():
+    """q8_0 KV, 8 independent streams, 26 layers, 8192 window: fast-forward each
+    ring with planned multi-row appends to just before the checkpoints, then
+    single decode steps; cache bit-exact and attention within 1e-2."""
+    ns = 8
+    with vkv.Cache(n_streams=ns, n_layers=26, capacity=8192, dtype=vkv.Q8_0) as c:
+        rings = (vkv.Ring * ns)(*[vkv.new_ring(8192) for _ in range(ns)])
+        out = empty_f32(ns, 26, 4096)
+        pos = 0
+        for target in (8191, 8192, 16500, 32767):
+            while pos < target:
+                m = min(8192, target - pos)
+                for s in range(ns):
+                    prefill_by_append(c, rings[s], s, m, 26)
+                pos += m
+            q, k, v = step_inputs(c, [pos] * ns)
+            plans = c.decoder_step(0, rings, [pos] * ns, 0, 26, q.data_ptr(), k.data_ptr(),
+                                   v.data_ptr(), out.data_ptr(), SCALE, hip_stream=stream_ptr())
+            pos += 1
+            check_cache_state(c, [0, ns - 1], range(0, 26, 5), 8192, {0: pos, ns - 1: pos})
+            for s in (0, 3, ns - 1):
+                want = oracle_decode(c, s, 25, plan_slots(plans[s]), q[s, 25].cpu().numpy())
+                got = out[s, 25].cpu().numpy().reshape(32, 128)
+                assert np.max(np.abs(got - want)) <= 1e-2, (target, s)
+            print(f"q8_0 8-stream step {target} ok", flush=True)

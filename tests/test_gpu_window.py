@@ -1,0 +1,127 @@
+"""GPU parity of the multi-query window attention: the encoder's causal
+sliding window over the 878-slot ring (32 layers, 32 heads x 64, window 750,
+16-frame chunks) and the decoder's causal prefill, against the oracle's fp64
+window attention; ring state bit-exact."""
+import os
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import vkv
+from gpu_util import SEED, empty_f32, layer_image, stream_ptr, synth
+
+pytestmark = pytest.mark.gpu
+
+POOL = ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
+EH, ED, ECAP, EWIN, EL = 32, 64, 878, 750, 32
+TOL = {vkv.F16: 2e-3, vkv.F32: 2e-3, vkv.Q8_0: 1e-2}
+
+
+def enc_inputs(layers, q_start, n):
+    q = synth(None, EH * ED, vkv.TAG_EQ, nl=layers, p0=q_start, np_=n)
+    k = synth(None, EH * ED, vkv.TAG_EK, nl=layers, p0=q_start, np_=n)
+    v = synth(None, EH * ED, vkv.TAG_EV, nl=layers, p0=q_start, np_=n)
+    return q, k, v
+
+
+def oracle_window(c, layer, key_pos, q_rows, q_pos, n_q_heads, n_kv_heads, head_dim, window,
+                  scale, ring_capacity):
+    kimg = layer_image(c, 0, 0, layer)
+    vimg = layer_image(c, 1, 0, layer)
+    key_pos = np.asarray(key_pos, np.int64)
+    return oracle.window_attn_f64(c.dtype, kimg, vimg, int(c.row_bytes),
+                                  (key_pos % ring_capacity).astype(np.int32), key_pos, q_rows,
+                                  np.asarray(q_pos, np.int64), n_q_heads, n_kv_heads, head_dim,
+                                  window, scale)
+
+
+@pytest.mark.parametrize("dtype,frames", [(vkv.F16, 6000), (vkv.F32, 1200), (vkv.Q8_0, 1200)])
+def test_encoder_window_chunks(dtype, frames):
+    """16 new frames per chunk as a 16-query block against the window."""
+    P = 16
+    n_chunks = frames // P
+    checks = {0, 1, 46, 47, 54, 55, 56, n_chunks - 1}      # first wrap at frame 878 is in chunk 54
+    with vkv.Cache(n_streams=1, n_layers=EL, capacity=ECAP, n_kv_heads=EH, head_dim=ED,
+                   n_q_heads=EH, dtype=dtype) as c:
+        out = empty_f32(EL, P, EH * ED)
+        for ch in range(n_chunks):
+            q_start = ch * P
+            plan = vkv.enc_plan(q_start, P, ECAP, EWIN)
+            q, k, v = enc_inputs(EL, q_start, P)
+            c.enc_step(0, plan, EWIN, 0, EL, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                       out.data_ptr(), 0.125, hip_stream=stream_ptr())
+            if ch not in checks:
+                continue
+            torch.cuda.synchronize()
+            layers = [0, 13, 31]
+            wants = list(POOL.map(lambda jw: oracle.expected_layer(
+                dtype, ECAP, ECAP, EH * ED, plan.win_end, SEED,
+                (vkv.TAG_EK, vkv.TAG_EV)[jw[1]], 0, jw[0]), [(l, w) for l in layers for w in (0, 1)]))
+            for (l, w), want in zip([(l, w) for l in layers for w in (0, 1)], wants):
+                assert np.array_equal(layer_image(c, w, 0, l), want), (ch, l, w)
+            key_pos = np.arange(plan.win_start, plan.win_end)
+            q_pos = np.arange(q_start, q_start + P)
+            for l in (0, 31):
+                want = oracle_window(c, l, key_pos, q[0, l].cpu().numpy().reshape(P, EH, ED), q_pos,
+                                     EH, EH, ED, EWIN, 0.125, ECAP)
+                got = out[l].cpu().numpy().reshape(P, EH, ED)
+                assert np.max(np.abs(got - want)) <= TOL[dtype], (ch, l)
+            print(f"encoder chunk {ch} ok", flush=True)
+
+
+@pytest.mark.parametrize("dtype", [vkv.F16, vkv.Q8_0])
+def test_decoder_prefill_then_steps(dtype):
+    """38-token causal prefill at positions 0..37 (the stream prompt), a second
+    10-token prefill, then single decode steps over the same cache."""
+    L = 4
+    with vkv.Cache(n_streams=1, n_layers=L, capacity=8192, dtype=dtype) as c:
+        ring = vkv.new_ring(8192)
+        for n in (38, 10):
+            start = ring.next_absolute_position
+            q = synth(None, 4096, vkv.TAG_Q, nl=L, p0=start, np_=n)
+            k = synth(None, 1024, vkv.TAG_K, nl=L, p0=start, np_=n)
+            v = synth(None, 1024, vkv.TAG_V, nl=L, p0=start, np_=n)
+            out = empty_f32(L, n, 4096)
+            c.decoder_prefill(0, ring, 0, L, n, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                              out.data_ptr(), 1 / np.sqrt(128), hip_stream=stream_ptr())
+            torch.cuda.synchronize()
+            assert ring.next_absolute_position == start + n
+            for l in range(L):
+                for w in (0, 1):
+                    want = oracle.expected_layer(dtype, 8192, 8192, 1024, start + n, SEED,
+                                                 (vkv.TAG_K, vkv.TAG_V)[w], 0, l)
+                    assert np.array_equal(layer_image(c, w, 0, l), want)
+                want = oracle_window(c, l, np.arange(0, start + n), q[0, l].cpu().numpy().reshape(n, 32, 128),
+                                     np.arange(start, start + n), 32, 8, 128, 0, 1 / np.sqrt(128), 8192)
+                got = out[l].cpu().numpy().reshape(n, 32, 128)
+                assert np.max(np.abs(got - want)) <= TOL[dtype], (start, l)
+
+
+def test_window_attn_entry_point_over_wrapped_segments():
+    """vkv_window_attn over an explicitly wrapped two-segment window with an
+    arbitrary absolute key origin."""
+    cap = 100
+    with vkv.Cache(n_streams=1, n_layers=2, capacity=cap, n_kv_heads=4, head_dim=64,
+                   n_q_heads=8, dtype=vkv.F16) as c:
+        k = synth(None, 256, vkv.TAG_K, nl=2, p0=0, np_=cap)
+        v = synth(None, 256, vkv.TAG_V, nl=2, p0=0, np_=cap)
+        c.append(0, 0, 2, [(0, cap)], k.data_ptr(), v.data_ptr(), hip_stream=stream_ptr())
+        segs = [(70, 30), (0, 50)]            # logical window of 80 keys, positions 1000..1079
+        n_q = 7
+        q = synth(None, 8 * 64, vkv.TAG_Q, nl=2, p0=0, np_=n_q)
+        out = empty_f32(2, n_q, 8 * 64)
+        c.window_attn(0, 0, 2, segs, 1000, 1070, n_q, 25, q.data_ptr(), out.data_ptr(), 0.125,
+                      hip_stream=stream_ptr())
+        torch.cuda.synchronize()
+        slots = np.r_[np.arange(70, 100), np.arange(0, 50)].astype(np.int32)
+        key_pos = np.arange(1000, 1080)
+        for l in range(2):
+            kimg, vimg = layer_image(c, 0, 0, l), layer_image(c, 1, 0, l)
+            want = oracle.window_attn_f64(vkv.F16, kimg, vimg, int(c.row_bytes), slots, key_pos,
+                                          q[0, l].cpu().numpy().reshape(n_q, 8, 64),
+                                          np.arange(1070, 1070 + n_q), 8, 4, 64, 25, 0.125)
+            got = out[l].cpu().numpy().reshape(n_q, 8, 64)
+            assert np.max(np.abs(got - want)) <= 2e-3

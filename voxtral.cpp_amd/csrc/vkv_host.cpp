@@ -1,0 +1,737 @@
+// Host side of the gfx950 KV-cache hot path: ring planners, cache ownership,
+// argument validation and the decoder/encoder step drivers behind vkv.h.
+//
+// The planners restate the reference's integer ring arithmetic
+// (src/voxtral.cpp:1590-1656 decoder, :3636-3692 encoder); the step drivers
+// keep run_decoder_step's contract (src/voxtral.cpp:5219-5360): plan first,
+// reject an invalid plan before any device work, launch, then commit.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <initializer_list>
+#include <new>
+#include <string>
+
+#include "vkv.h"
+#include "vkv_internal.h"
+
+using namespace vkv;
+
+struct vkv_cache {
+    vkv_cache_params p{};
+    int64_t row_bytes = 0;
+    int64_t layer_bytes = 0;
+    int64_t stream_bytes = 0;
+    int64_t total_bytes = 0;
+    uint8_t *k = nullptr;
+    uint8_t *v = nullptr;
+    // split-K workspace: partial outputs and (max, sum) per work group/head
+    float *part_o = nullptr;
+    float *part_ml = nullptr;
+    int64_t part_heads_budget = 0;   // capacity of part_ml in (head, chunk) units
+    int32_t *counters = nullptr;     // [stream][layer][kv head] arrival counters (self-resetting)
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+thread_local int32_t g_last_backend = 0;
+
+vkv_status fail(vkv_status st, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    if (st != VKV_STATUS_BACKEND_ERROR) g_last_backend = 0;
+    return st;
+}
+
+vkv_status hip_fail(hipError_t e, const char *what) {
+    g_last_backend = (int32_t)e;
+    return fail(VKV_STATUS_BACKEND_ERROR, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+vkv_status ok() {
+    g_last_error.clear();
+    g_last_backend = 0;
+    return VKV_STATUS_OK;
+}
+
+// Run device work on the cache's device; restores the caller's device.
+struct DeviceGuard {
+    int prev = -1;
+    bool changed = false;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) == hipSuccess && prev != dev) {
+            changed = hipSetDevice(dev) == hipSuccess;
+        }
+    }
+    ~DeviceGuard() {
+        if (changed) (void)hipSetDevice(prev);
+    }
+};
+
+int64_t row_bytes_for(int dtype, int64_t n) {
+    switch (dtype) {
+    case VKV_DTYPE_F32: return n * 4;
+    case VKV_DTYPE_F16: return n * 2;
+    case VKV_DTYPE_Q8_0: return (n / 32) * 34;
+    default: return -1;
+    }
+}
+
+// <=2 physical segments of [abs_start, abs_start+len) modulo capacity
+// (src/voxtral.cpp:1604-1613 and :3642-3651 apply the same rule).
+int32_t ring_segments(int64_t abs_start, int32_t len, int32_t capacity, vkv_seg out[2]) {
+    if (len <= 0) return 0;
+    const int32_t slot = (int32_t)(abs_start % capacity);
+    const int32_t first = std::min(len, capacity - slot);
+    out[0] = {slot, first};
+    if (first >= len) return 1;
+    out[1] = {0, len - first};
+    return 2;
+}
+
+SegPair seg_pair(const vkv_seg *segs, int32_t nseg) {
+    SegPair sp{0, 0, 0, 0};
+    if (nseg >= 1) { sp.s0 = segs[0].slot; sp.n0 = segs[0].len; }
+    if (nseg >= 2) { sp.s1 = segs[1].slot; sp.n1 = segs[1].len; }
+    return sp;
+}
+
+vkv_status check_segs(const vkv_cache *c, const vkv_seg *segs, int32_t nseg, const char *what) {
+    if (nseg < 0 || nseg > 2) return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: nseg=%d", what, nseg);
+    if (nseg > 0 && !segs) return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: null segments", what);
+    int64_t total = 0;
+    for (int32_t i = 0; i < nseg; ++i) {
+        if (segs[i].len < 0 || segs[i].slot < 0 ||
+            (int64_t)segs[i].slot + segs[i].len > c->p.capacity)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: segment %d [%d,+%d) outside capacity %d",
+                        what, i, segs[i].slot, segs[i].len, c->p.capacity);
+        total += segs[i].len;
+    }
+    if (total > c->p.capacity)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: %lld rows exceed capacity %d", what,
+                    (long long)total, c->p.capacity);
+    return VKV_STATUS_OK;
+}
+
+vkv_status check_cache(const vkv_cache *c, const char *what) {
+    if (!c) return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: null cache", what);
+    return VKV_STATUS_OK;
+}
+
+vkv_status check_span(const vkv_cache *c, int32_t s0, int32_t ns, int32_t l0, int32_t nl,
+                      const char *what) {
+    if (s0 < 0 || ns < 1 || (int64_t)s0 + ns > c->p.n_streams)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: streams [%d,+%d) outside [0,%d)", what, s0,
+                    ns, c->p.n_streams);
+    if (l0 < 0 || nl < 1 || (int64_t)l0 + nl > c->p.n_layers)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: layers [%d,+%d) outside [0,%d)", what, l0,
+                    nl, c->p.n_layers);
+    return VKV_STATUS_OK;
+}
+
+vkv_status check_heads(const vkv_cache *c, int32_t n_q_heads, const char *what) {
+    if (n_q_heads < c->p.n_kv_heads || n_q_heads % c->p.n_kv_heads != 0 ||
+        n_q_heads > c->p.n_q_heads)
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "%s: n_q_heads=%d must be a multiple of n_kv_heads=%d and <= %d", what,
+                    n_q_heads, c->p.n_kv_heads, c->p.n_q_heads);
+    return VKV_STATUS_OK;
+}
+
+hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Device f32 arrays read with 16-byte vector loads must be 16-byte aligned.
+vkv_status check_aligned(const char *what, std::initializer_list<const void *> ptrs) {
+    for (const void *p : ptrs)
+        if (p && !aligned16(p))
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: device arrays must be 16-byte aligned", what);
+    return VKV_STATUS_OK;
+}
+
+uint8_t *stream_layer_base(const vkv_cache *c, uint8_t *base, int32_t stream, int32_t layer) {
+    return base + (int64_t)stream * c->stream_bytes + (int64_t)layer * c->layer_bytes;
+}
+
+vkv_status do_append(vkv_cache *c, int32_t stream, int32_t layer0, int32_t n_layers,
+                     const vkv_seg *segs, int32_t nseg, const float *k, const float *v,
+                     int64_t layer_stride, hipStream_t st) {
+    AppendArgs a{};
+    a.k = stream_layer_base(c, c->k, stream, layer0);
+    a.v = stream_layer_base(c, c->v, stream, layer0);
+    a.layer_bytes = c->layer_bytes;
+    a.row_bytes = c->row_bytes;
+    a.k_src = k;
+    a.v_src = v;
+    a.kv_dim = c->p.n_kv_heads * c->p.head_dim;
+    a.seg = seg_pair(segs, nseg);
+    a.n_rows = a.seg.n0 + a.seg.n1;
+    a.src_lstride = layer_stride ? layer_stride : (int64_t)a.n_rows * a.kv_dim;
+    if (a.n_rows == 0) return VKV_STATUS_OK;
+    hipError_t e = launch_append(c->p.dtype, a, n_layers, st);
+    if (e != hipSuccess) return hip_fail(e, "append launch");
+    return VKV_STATUS_OK;
+}
+
+// VKV_SPLIT_COMBINE=1 merges the split-K partials in a second kernel instead
+// of in the decode kernel's last work group (kept for A/B measurement).
+bool split_combine() {
+    static const bool v = [] {
+        const char *e = std::getenv("VKV_SPLIT_COMBINE");
+        return e && e[0] == '1';
+    }();
+    return v;
+}
+
+// Chunk size (logical slots per work group) for decode attention: the largest
+// of 256/128/64 that still gives >= 2048 work groups, within the workspace.
+int32_t pick_chunk(const vkv_cache *c, int64_t units, int32_t n_kv_max, int32_t gqa,
+                   int32_t *n_chunks_out) {
+    int32_t chunk = 256;
+    while (chunk > 64 && units * ((n_kv_max + chunk - 1) / chunk) < 2048) chunk /= 2;
+    for (;;) {
+        const int32_t nc = std::max(1, (n_kv_max + chunk - 1) / chunk);
+        if (units * nc * gqa <= c->part_heads_budget || chunk >= (1 << 30)) {
+            *n_chunks_out = nc;
+            return chunk;
+        }
+        chunk *= 2;
+    }
+}
+
+vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t layer0,
+                     int32_t n_layers, const SegPair *segs, const float *q, float *out,
+                     int32_t n_q_heads, float scale, const float *k_new, const float *v_new,
+                     hipStream_t st) {
+    const int32_t D = c->p.head_dim;
+    const int32_t G = c->p.n_kv_heads;
+    const int32_t gqa = n_q_heads / G;
+    if (D != 128 || gqa != 4)
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "decode attention supports head_dim 128 and 4 query heads per KV head "
+                    "(got head_dim %d, group %d)", D, gqa);
+    int32_t n_kv_max = 0;
+    for (int32_t s = 0; s < n_streams; ++s) n_kv_max = std::max(n_kv_max, segs[s].n0 + segs[s].n1);
+    DecodeArgs a{};
+    a.k = stream_layer_base(c, c->k, stream0, layer0);
+    a.v = stream_layer_base(c, c->v, stream0, layer0);
+    a.k_w = stream_layer_base(c, c->k, stream0, layer0);
+    a.v_w = stream_layer_base(c, c->v, stream0, layer0);
+    a.stream_bytes = c->stream_bytes;
+    a.layer_bytes = c->layer_bytes;
+    a.row_bytes = c->row_bytes;
+    a.q = q;
+    a.q_lstride = (int64_t)n_q_heads * D;
+    a.q_sstride = (int64_t)n_layers * a.q_lstride;
+    a.part_o = c->part_o;
+    a.part_ml = c->part_ml;
+    a.n_layers = n_layers;
+    a.n_kv_heads = G;
+    a.n_q_heads = n_q_heads;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.new_lstride = (int64_t)G * D;
+    a.new_sstride = (int64_t)n_layers * a.new_lstride;
+    for (int32_t s = 0; s < n_streams; ++s) a.seg[s] = segs[s];
+    const int64_t units = (int64_t)n_streams * n_layers * G;
+    a.chunk = pick_chunk(c, units, n_kv_max, gqa, &a.n_chunks);
+    // Arrival counters are indexed [s][layer][g] relative to the call (at most
+    // the cache's extent); they return to zero after every call, so
+    // stream-ordered calls can share them.
+    const bool fused = !split_combine();
+    a.counters = fused ? c->counters : nullptr;
+    a.out = out;
+    hipError_t e = launch_decode(c->p.dtype, gqa, k_new != nullptr, n_streams, a, st);
+    if (e != hipSuccess) return hip_fail(e, "decode launch");
+    if (fused) return VKV_STATUS_OK;
+    CombineArgs cb{};
+    cb.part_o = c->part_o;
+    cb.part_ml = c->part_ml;
+    cb.out = out;
+    cb.n_chunks = a.n_chunks;
+    cb.n_q_heads = n_q_heads;
+    cb.n_layers = n_layers;
+    cb.head_dim = D;
+    e = launch_combine(cb, n_streams, st);
+    if (e != hipSuccess) return hip_fail(e, "combine launch");
+    return VKV_STATUS_OK;
+}
+
+vkv_status do_window(vkv_cache *c, int32_t stream, int32_t layer0, int32_t n_layers,
+                     const vkv_seg *segs, int32_t nseg, int64_t key_pos0, int64_t q_pos0,
+                     int32_t n_q, int32_t window, const float *q, float *out, int32_t n_q_heads,
+                     float scale, hipStream_t st) {
+    if (c->p.head_dim % 8 != 0 || c->p.head_dim > 128)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "window attention: head_dim %d unsupported",
+                    c->p.head_dim);
+    if (n_q <= 0) return VKV_STATUS_OK;
+    WindowArgs a{};
+    a.k = stream_layer_base(c, c->k, stream, layer0);
+    a.v = stream_layer_base(c, c->v, stream, layer0);
+    a.layer_bytes = c->layer_bytes;
+    a.row_bytes = c->row_bytes;
+    a.q = q;
+    a.out = out;
+    a.q_lstride = (int64_t)n_q * n_q_heads * c->p.head_dim;
+    a.n_q = n_q;
+    a.n_q_heads = n_q_heads;
+    a.n_kv_heads = c->p.n_kv_heads;
+    a.head_dim = c->p.head_dim;
+    a.n_layers = n_layers;
+    a.q_pos0 = q_pos0;
+    a.key_pos0 = key_pos0;
+    a.window = window;
+    a.scale_log2 = scale * 1.4426950408889634f;
+    a.seg = seg_pair(segs, nseg);
+    hipError_t e = launch_window(c->p.dtype, a, st);
+    if (e != hipSuccess) return hip_fail(e, "window attention launch");
+    return VKV_STATUS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t vkv_api_version(void) { return VKV_API_VERSION; }
+
+const char *vkv_last_error(void) { return g_last_error.c_str(); }
+
+int32_t vkv_last_backend_code(void) { return g_last_backend; }
+
+// src/voxtral.cpp:1615-1644
+vkv_status vkv_decoder_plan(const vkv_ring *ring, int64_t absolute_start, int32_t n_new,
+                            vkv_plan *out) {
+    if (!out) return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder plan: null out");
+    std::memset(out, 0, sizeof(*out));
+    if (!ring) return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder plan: null ring");
+    if (ring->capacity <= 0 || ring->capacity > INT32_MAX || ring->used < 0 ||
+        ring->used > ring->capacity || ring->oldest_absolute_position < 0 ||
+        ring->next_absolute_position < 0 ||
+        ring->oldest_absolute_position + ring->used != ring->next_absolute_position)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder plan: inconsistent ring metadata");
+    if (absolute_start != ring->next_absolute_position)
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "decoder plan: invalid absolute position %lld (next=%lld)",
+                    (long long)absolute_start, (long long)ring->next_absolute_position);
+    if (n_new <= 0 || n_new > ring->capacity)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder plan: n_new=%d outside (0, %lld]", n_new,
+                    (long long)ring->capacity);
+    const int32_t cap = (int32_t)ring->capacity;
+    out->absolute_start = absolute_start;
+    out->n_new = n_new;
+    out->write_nseg = ring_segments(absolute_start, n_new, cap, out->write_seg);
+    out->next_after = absolute_start + n_new;
+    out->used_after = std::min<int64_t>(ring->capacity, ring->used + n_new);
+    out->oldest_after = out->next_after - out->used_after;
+    out->evicted = std::max<int64_t>(0, ring->used + n_new - ring->capacity);
+    out->read_nseg = ring_segments(out->oldest_after, (int32_t)out->used_after, cap, out->read_seg);
+    // A wrap is a crossing of a capacity cycle boundary by the appended span,
+    // including the single-token write exactly at slot zero.
+    const int64_t previous_cycle = absolute_start == 0 ? 0 : (absolute_start - 1) / ring->capacity;
+    const int64_t newest_cycle = (out->next_after - 1) / ring->capacity;
+    out->wrapped = newest_cycle > previous_cycle;
+    return ok();
+}
+
+// src/voxtral.cpp:1646-1656
+vkv_status vkv_decoder_commit(vkv_ring *ring, const vkv_plan *plan) {
+    if (!ring || !plan) return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder commit: null argument");
+    ring->used = plan->used_after;
+    ring->oldest_absolute_position = plan->oldest_after;
+    ring->next_absolute_position = plan->next_after;
+    ring->evictions += plan->evicted;
+    if (plan->wrapped) ++ring->wraps;
+    return ok();
+}
+
+// src/voxtral.cpp:1590-1602
+vkv_status vkv_decoder_clear(vkv_ring *ring, int64_t capacity) {
+    if (!ring) return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder clear: null ring");
+    std::memset(ring, 0, sizeof(*ring));
+    ring->capacity = capacity;
+    return ok();
+}
+
+// src/voxtral.cpp:3636-3638
+int32_t vkv_enc_mask_allows(int64_t kv_abs, int64_t q_abs, int32_t window) {
+    return kv_abs <= q_abs && kv_abs >= q_abs - (int64_t)(window - 1);
+}
+
+// src/voxtral.cpp:3653-3692
+vkv_status vkv_enc_plan_build(int64_t q_start, int32_t n_new, int32_t capacity, int32_t window,
+                              vkv_enc_plan *out) {
+    if (!out) return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder plan: null out");
+    std::memset(out, 0, sizeof(*out));
+    if (n_new <= 0 || capacity <= 0 || window <= 0)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder plan: n_new=%d capacity=%d window=%d",
+                    n_new, capacity, window);
+    if (n_new > capacity - window)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder plan: n_new=%d exceeds headroom %d",
+                    n_new, capacity - window);
+    if (q_start < 0) return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder plan: q_start < 0");
+    out->q_start = q_start;
+    out->n_new = n_new;
+    out->win_start = std::max<int64_t>(0, q_start - (int64_t)(window - 1));
+    out->win_end = q_start + n_new;
+    out->win_len = (int32_t)(out->win_end - out->win_start);
+    out->read_nseg = ring_segments(out->win_start, out->win_len, capacity, out->read_seg);
+    out->read_wraps = out->read_nseg > 1;
+    out->write_nseg = ring_segments(q_start, n_new, capacity, out->write_seg);
+    out->write_wraps = out->write_nseg > 1;
+    out->conv_mel_start = std::max<int64_t>(0, 2 * (q_start - 2));
+    out->conv_mel_end = 2 * (q_start + n_new);
+    out->conv_slice_start = (int32_t)(q_start - out->conv_mel_start / 2);
+    const int64_t old_lo = std::max<int64_t>(0, q_start - (int64_t)window);
+    const int64_t new_lo = std::max<int64_t>(0, out->win_end - (int64_t)window);
+    out->evicted = new_lo - old_lo;
+    return ok();
+}
+
+vkv_status vkv_cache_create(const vkv_cache_params *params, vkv_cache **out) {
+    if (!out) return fail(VKV_STATUS_INVALID_ARGUMENT, "cache create: null out");
+    *out = nullptr;
+    if (!params || params->struct_size < sizeof(vkv_cache_params))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "cache create: params missing or struct_size too small");
+    const vkv_cache_params &p = *params;
+    if (p.n_streams < 1 || p.n_layers < 1 || p.capacity < 1 || p.n_kv_heads < 1 ||
+        p.head_dim < 8 || p.head_dim % 8 != 0 || p.n_q_heads < p.n_kv_heads ||
+        p.n_q_heads % p.n_kv_heads != 0)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "cache create: invalid shape");
+    const int64_t kv_dim = (int64_t)p.n_kv_heads * p.head_dim;
+    if (p.dtype != VKV_DTYPE_F32 && p.dtype != VKV_DTYPE_F16 && p.dtype != VKV_DTYPE_Q8_0)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "cache create: dtype %d unsupported", p.dtype);
+    if (p.dtype == VKV_DTYPE_Q8_0 && p.head_dim % 32 != 0)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "cache create: q8_0 needs head_dim %% 32 == 0");
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess) return hip_fail(e, "cache create: hipGetDeviceCount");
+    if (p.device < 0 || p.device >= ndev)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "cache create: device %d not in [0,%d)", p.device, ndev);
+
+    vkv_cache *c = new (std::nothrow) vkv_cache();
+    if (!c) return fail(VKV_STATUS_OUT_OF_MEMORY, "cache create: host allocation");
+    c->p = p;
+    c->row_bytes = row_bytes_for(p.dtype, kv_dim);
+    c->layer_bytes = c->row_bytes * p.capacity;
+    c->stream_bytes = c->layer_bytes * p.n_layers;
+    c->total_bytes = c->stream_bytes * p.n_streams;
+    // decode workspace: every (stream, layer, kv head) at 256-slot chunks, and
+    // at least 8192 work groups for small jobs; per work group GQA heads.
+    const int64_t gqa = p.n_q_heads / p.n_kv_heads;
+    const int64_t units = (int64_t)p.n_streams * p.n_layers * p.n_kv_heads;
+    const int64_t wg = std::max<int64_t>(units * ((p.capacity + 255) / 256), 8192);
+    c->part_heads_budget = wg * gqa;
+
+    DeviceGuard guard(p.device);
+    if ((e = hipMalloc(&c->k, (size_t)c->total_bytes)) != hipSuccess ||
+        (e = hipMalloc(&c->v, (size_t)c->total_bytes)) != hipSuccess ||
+        (e = hipMalloc(&c->part_o, (size_t)(c->part_heads_budget * p.head_dim * 4))) != hipSuccess ||
+        (e = hipMalloc(&c->part_ml, (size_t)(c->part_heads_budget * 2 * 4))) != hipSuccess ||
+        (e = hipMalloc(&c->counters, (size_t)units * 4)) != hipSuccess) {
+        const bool oom = e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation;
+        vkv_cache_destroy(c);
+        if (oom) return fail(VKV_STATUS_OUT_OF_MEMORY, "cache create: device allocation failed");
+        return hip_fail(e, "cache create: hipMalloc");
+    }
+    // Zero once at allocation (src/voxtral.cpp:1456-1464); never per stream.
+    if ((e = launch_fill_zero(c->k, c->total_bytes, nullptr)) != hipSuccess ||
+        (e = launch_fill_zero(c->v, c->total_bytes, nullptr)) != hipSuccess ||
+        (e = launch_fill_zero(c->counters, units * 4, nullptr)) != hipSuccess ||
+        (e = hipDeviceSynchronize()) != hipSuccess) {
+        vkv_cache_destroy(c);
+        return hip_fail(e, "cache create: zero fill");
+    }
+    *out = c;
+    return ok();
+}
+
+vkv_status vkv_cache_destroy(vkv_cache *cache) {
+    if (!cache) return ok();
+    DeviceGuard guard(cache->p.device);
+    hipError_t first = hipSuccess;
+    for (void *p : {(void *)cache->k, (void *)cache->v, (void *)cache->part_o,
+                    (void *)cache->part_ml, (void *)cache->counters}) {
+        if (!p) continue;
+        hipError_t e = hipFree(p);
+        if (e != hipSuccess && first == hipSuccess) first = e;
+    }
+    delete cache;
+    if (first != hipSuccess) return hip_fail(first, "cache destroy: hipFree");
+    return ok();
+}
+
+vkv_status vkv_cache_get_layout(const vkv_cache *cache, vkv_cache_layout *out) {
+    if (!out) return fail(VKV_STATUS_INVALID_ARGUMENT, "cache layout: null out");
+    std::memset(out, 0, sizeof(*out));
+    if (vkv_status st = check_cache(cache, "cache layout")) return st;
+    out->row_bytes = (uint64_t)cache->row_bytes;
+    out->layer_bytes = (uint64_t)cache->layer_bytes;
+    out->stream_bytes = (uint64_t)cache->stream_bytes;
+    out->total_bytes = (uint64_t)cache->total_bytes;
+    out->k_base = cache->k;
+    out->v_base = cache->v;
+    return ok();
+}
+
+vkv_status vkv_cache_read_rows(const vkv_cache *cache, int32_t which, int32_t stream,
+                               int32_t layer, int32_t slot0, int32_t n_slots, void *host_dst,
+                               size_t dst_bytes) {
+    if (vkv_status st = check_cache(cache, "cache read")) return st;
+    if (which != 0 && which != 1) return fail(VKV_STATUS_INVALID_ARGUMENT, "cache read: which=%d", which);
+    if (vkv_status st = check_span(cache, stream, 1, layer, 1, "cache read")) return st;
+    if (slot0 < 0 || n_slots < 0 || (int64_t)slot0 + n_slots > cache->p.capacity)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "cache read: slots [%d,+%d) outside capacity", slot0, n_slots);
+    const size_t bytes = (size_t)n_slots * (size_t)cache->row_bytes;
+    if (!host_dst && bytes) return fail(VKV_STATUS_INVALID_ARGUMENT, "cache read: null destination");
+    if (dst_bytes < bytes)
+        return fail(VKV_STATUS_BUFFER_TOO_SMALL, "cache read: need %zu bytes, have %zu", bytes, dst_bytes);
+    if (!bytes) return ok();
+    DeviceGuard guard(cache->p.device);
+    const uint8_t *src = stream_layer_base(cache, which ? cache->v : cache->k, stream, layer) +
+                         (int64_t)slot0 * cache->row_bytes;
+    hipError_t e = hipMemcpy(host_dst, src, bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "cache read: hipMemcpy");
+    return ok();
+}
+
+vkv_status vkv_cache_zero(vkv_cache *cache, void *hip_stream) {
+    if (vkv_status st = check_cache(cache, "cache zero")) return st;
+    DeviceGuard guard(cache->p.device);
+    hipError_t e;
+    if ((e = launch_fill_zero(cache->k, cache->total_bytes, as_stream(hip_stream))) != hipSuccess ||
+        (e = launch_fill_zero(cache->v, cache->total_bytes, as_stream(hip_stream))) != hipSuccess)
+        return hip_fail(e, "cache zero");
+    return ok();
+}
+
+vkv_status vkv_append(vkv_cache *cache, int32_t stream, int32_t layer0, int32_t n_layers,
+                      const vkv_seg *write_seg, int32_t write_nseg, const float *k_src,
+                      const float *v_src, int64_t layer_stride, void *hip_stream) {
+    if (vkv_status st = check_cache(cache, "append")) return st;
+    if (vkv_status st = check_span(cache, stream, 1, layer0, n_layers, "append")) return st;
+    if (vkv_status st = check_segs(cache, write_seg, write_nseg, "append")) return st;
+    if (!k_src || !v_src) return fail(VKV_STATUS_INVALID_ARGUMENT, "append: null source");
+    if (layer_stride < 0 || layer_stride % 4 != 0)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "append: layer stride must be a non-negative multiple of 4");
+    if (!aligned16(k_src) || !aligned16(v_src))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "append: sources must be 16-byte aligned");
+    DeviceGuard guard(cache->p.device);
+    if (vkv_status st = do_append(cache, stream, layer0, n_layers, write_seg, write_nseg, k_src,
+                                  v_src, layer_stride, as_stream(hip_stream)))
+        return st;
+    return ok();
+}
+
+vkv_status vkv_gather(const vkv_cache *cache, int32_t stream, int32_t layer,
+                      const vkv_seg *read_seg, int32_t read_nseg, void *k_dst, void *v_dst,
+                      void *hip_stream) {
+    if (vkv_status st = check_cache(cache, "gather")) return st;
+    if (vkv_status st = check_span(cache, stream, 1, layer, 1, "gather")) return st;
+    if (vkv_status st = check_segs(cache, read_seg, read_nseg, "gather")) return st;
+    if (!k_dst && !v_dst) return fail(VKV_STATUS_INVALID_ARGUMENT, "gather: null destinations");
+    DeviceGuard guard(cache->p.device);
+    const SegPair sp = seg_pair(read_seg, read_nseg);
+    hipError_t e = hipSuccess;
+    if (k_dst)
+        e = launch_gather(stream_layer_base(cache, cache->k, stream, layer), cache->row_bytes, sp,
+                          (uint8_t *)k_dst, as_stream(hip_stream));
+    if (e == hipSuccess && v_dst)
+        e = launch_gather(stream_layer_base(cache, cache->v, stream, layer), cache->row_bytes, sp,
+                          (uint8_t *)v_dst, as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "gather launch");
+    return ok();
+}
+
+vkv_status vkv_decode_attn(vkv_cache *cache, int32_t stream0, int32_t n_streams, int32_t layer0,
+                           int32_t n_layers, const vkv_plan *plans, const float *q, float *out,
+                           int32_t n_q_heads, float scale, void *hip_stream) {
+    if (vkv_status st = check_cache(cache, "decode attention")) return st;
+    if (vkv_status st = check_span(cache, stream0, n_streams, layer0, n_layers, "decode attention"))
+        return st;
+    if (n_streams > kMaxStreams)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decode attention: at most %d streams per call", kMaxStreams);
+    if (vkv_status st = check_heads(cache, n_q_heads, "decode attention")) return st;
+    if (!plans || !q || !out) return fail(VKV_STATUS_INVALID_ARGUMENT, "decode attention: null argument");
+    if (vkv_status st = check_aligned("decode attention", {q, out})) return st;
+    if (!std::isfinite(scale)) return fail(VKV_STATUS_INVALID_ARGUMENT, "decode attention: scale");
+    SegPair segs[kMaxStreams];
+    for (int32_t s = 0; s < n_streams; ++s) {
+        if (vkv_status st = check_segs(cache, plans[s].read_seg, plans[s].read_nseg, "decode attention"))
+            return st;
+        segs[s] = seg_pair(plans[s].read_seg, plans[s].read_nseg);
+    }
+    DeviceGuard guard(cache->p.device);
+    if (vkv_status st = do_decode(cache, stream0, n_streams, layer0, n_layers, segs, q, out,
+                                  n_q_heads, scale, nullptr, nullptr, as_stream(hip_stream)))
+        return st;
+    return ok();
+}
+
+vkv_status vkv_decoder_step(vkv_cache *cache, int32_t stream0, int32_t n_streams, vkv_ring *rings,
+                            const int64_t *positions, int32_t layer0, int32_t n_layers,
+                            const float *q, const float *k, const float *v, float *out,
+                            int32_t n_q_heads, float scale, vkv_plan *plans_out,
+                            void *hip_stream) {
+    if (plans_out && n_streams > 0) std::memset(plans_out, 0, sizeof(vkv_plan) * (size_t)n_streams);
+    if (vkv_status st = check_cache(cache, "decoder step")) return st;
+    if (vkv_status st = check_span(cache, stream0, n_streams, layer0, n_layers, "decoder step"))
+        return st;
+    if (n_streams > kMaxStreams)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder step: at most %d streams per call", kMaxStreams);
+    if (vkv_status st = check_heads(cache, n_q_heads, "decoder step")) return st;
+    if (!rings || !positions || !q || !k || !v || !out)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder step: null argument");
+    if (vkv_status st = check_aligned("decoder step", {q, k, v, out})) return st;
+    if (!std::isfinite(scale)) return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder step: scale");
+    vkv_plan plans[kMaxStreams];
+    SegPair segs[kMaxStreams];
+    for (int32_t s = 0; s < n_streams; ++s) {
+        if (rings[s].capacity > cache->p.capacity)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder step: ring capacity %lld exceeds backing %d",
+                        (long long)rings[s].capacity, cache->p.capacity);
+        if (vkv_status st = vkv_decoder_plan(&rings[s], positions[s], 1, &plans[s])) {
+            char msg[600];
+            std::snprintf(msg, sizeof(msg), "decoder step (stream %d): %s", stream0 + s, g_last_error.c_str());
+            return fail(st, "%s", msg);
+        }
+        segs[s] = seg_pair(plans[s].read_seg, plans[s].read_nseg);
+        // The appended row is the newest logical index of the window.
+        const int32_t n_kv = segs[s].n0 + segs[s].n1;
+        const int32_t newest = n_kv - 1 < segs[s].n0 ? segs[s].s0 + n_kv - 1 : segs[s].s1 + (n_kv - 1 - segs[s].n0);
+        if (n_kv < 1 || newest != plans[s].write_seg[0].slot)
+            return fail(VKV_STATUS_INTERNAL_ERROR, "decoder step: plan window does not end at the new row");
+    }
+    DeviceGuard guard(cache->p.device);
+    if (vkv_status st = do_decode(cache, stream0, n_streams, layer0, n_layers, segs, q, out,
+                                  n_q_heads, scale, k, v, as_stream(hip_stream)))
+        return st;
+    for (int32_t s = 0; s < n_streams; ++s) {
+        vkv_decoder_commit(&rings[s], &plans[s]);
+        if (plans_out) plans_out[s] = plans[s];
+    }
+    return ok();
+}
+
+vkv_status vkv_decoder_prefill(vkv_cache *cache, int32_t stream, vkv_ring *ring, int32_t layer0,
+                               int32_t n_layers, int32_t n_tokens, const float *q, const float *k,
+                               const float *v, float *out, int32_t n_q_heads, float scale,
+                               void *hip_stream) {
+    if (vkv_status st = check_cache(cache, "decoder prefill")) return st;
+    if (vkv_status st = check_span(cache, stream, 1, layer0, n_layers, "decoder prefill")) return st;
+    if (vkv_status st = check_heads(cache, n_q_heads, "decoder prefill")) return st;
+    if (!ring || !q || !k || !v || !out)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prefill: null argument");
+    if (vkv_status st = check_aligned("decoder prefill", {q, k, v, out})) return st;
+    if (ring->capacity > cache->p.capacity)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prefill: ring capacity exceeds backing");
+    vkv_plan plan;
+    if (vkv_status st = vkv_decoder_plan(ring, ring->next_absolute_position, n_tokens, &plan))
+        return st;
+    if (plan.read_nseg != 1)
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "decoder prefill: the post-append window must be one segment (got %d)", plan.read_nseg);
+    DeviceGuard guard(cache->p.device);
+    hipStream_t st = as_stream(hip_stream);
+    if (vkv_status s = do_append(cache, stream, layer0, n_layers, plan.write_seg, plan.write_nseg,
+                                 k, v, 0, st))
+        return s;
+    if (vkv_status s = do_window(cache, stream, layer0, n_layers, plan.read_seg, plan.read_nseg,
+                                 plan.oldest_after, plan.absolute_start, n_tokens, 0, q, out,
+                                 n_q_heads, scale, st))
+        return s;
+    vkv_decoder_commit(ring, &plan);
+    return ok();
+}
+
+vkv_status vkv_enc_step(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
+                        int32_t window, int32_t layer0, int32_t n_layers, const float *q,
+                        const float *k, const float *v, float *out, int32_t n_q_heads,
+                        float scale, void *hip_stream) {
+    if (vkv_status st = check_cache(cache, "encoder step")) return st;
+    if (vkv_status st = check_span(cache, stream, 1, layer0, n_layers, "encoder step")) return st;
+    if (vkv_status st = check_heads(cache, n_q_heads, "encoder step")) return st;
+    if (!plan || !q || !k || !v || !out)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder step: null argument");
+    if (vkv_status st = check_aligned("encoder step", {q, k, v, out})) return st;
+    if (window <= 0) return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder step: window %d", window);
+    if (vkv_status st = check_segs(cache, plan->write_seg, plan->write_nseg, "encoder step write"))
+        return st;
+    if (vkv_status st = check_segs(cache, plan->read_seg, plan->read_nseg, "encoder step read"))
+        return st;
+    if (plan->write_seg[0].len + (plan->write_nseg > 1 ? plan->write_seg[1].len : 0) != plan->n_new)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder step: write segments do not cover n_new");
+    DeviceGuard guard(cache->p.device);
+    hipStream_t st = as_stream(hip_stream);
+    if (vkv_status s = do_append(cache, stream, layer0, n_layers, plan->write_seg, plan->write_nseg,
+                                 k, v, 0, st))
+        return s;
+    if (vkv_status s = do_window(cache, stream, layer0, n_layers, plan->read_seg, plan->read_nseg,
+                                 plan->win_start, plan->q_start, plan->n_new, window, q, out,
+                                 n_q_heads, scale, st))
+        return s;
+    return ok();
+}
+
+vkv_status vkv_window_attn(vkv_cache *cache, int32_t stream, int32_t layer0, int32_t n_layers,
+                           const vkv_seg *read_seg, int32_t read_nseg, int64_t key_pos0,
+                           int64_t q_pos0, int32_t n_q, int32_t window, const float *q, float *out,
+                           int32_t n_q_heads, float scale, void *hip_stream) {
+    if (vkv_status st = check_cache(cache, "window attention")) return st;
+    if (vkv_status st = check_span(cache, stream, 1, layer0, n_layers, "window attention")) return st;
+    if (vkv_status st = check_heads(cache, n_q_heads, "window attention")) return st;
+    if (vkv_status st = check_segs(cache, read_seg, read_nseg, "window attention")) return st;
+    if (n_q < 0 || (n_q > 0 && (!q || !out)))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "window attention: bad queries");
+    if (vkv_status st = check_aligned("window attention", {q, out})) return st;
+    DeviceGuard guard(cache->p.device);
+    if (vkv_status s = do_window(cache, stream, layer0, n_layers, read_seg, read_nseg, key_pos0,
+                                 q_pos0, n_q, window, q, out, n_q_heads, scale,
+                                 as_stream(hip_stream)))
+        return s;
+    return ok();
+}
+
+vkv_status vkv_q8_0_pack(const float *x, void *blocks, int64_t n, void *hip_stream) {
+    if (n < 0 || n % 32 != 0) return fail(VKV_STATUS_INVALID_ARGUMENT, "q8_0 pack: n %% 32 != 0");
+    if (n == 0) return ok();
+    if (!x || !blocks) return fail(VKV_STATUS_INVALID_ARGUMENT, "q8_0 pack: null argument");
+    hipError_t e = launch_q8_0_pack(x, (uint8_t *)blocks, n, as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "q8_0 pack launch");
+    return ok();
+}
+
+vkv_status vkv_q8_0_unpack(const void *blocks, float *y, int64_t n, void *hip_stream) {
+    if (n < 0 || n % 32 != 0) return fail(VKV_STATUS_INVALID_ARGUMENT, "q8_0 unpack: n %% 32 != 0");
+    if (n == 0) return ok();
+    if (!blocks || !y) return fail(VKV_STATUS_INVALID_ARGUMENT, "q8_0 unpack: null argument");
+    hipError_t e = launch_q8_0_unpack((const uint8_t *)blocks, y, n, as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "q8_0 unpack launch");
+    return ok();
+}
+
+vkv_status vkv_synth_rows(float *dst, int32_t row_len, uint64_t seed, uint32_t tag, int64_t s0,
+                          int32_t ns, int64_t s_stride, int64_t l0, int32_t nl, int64_t l_stride,
+                          int64_t p0, int32_t np, int64_t p_stride, void *hip_stream) {
+    if (row_len < 0 || ns < 0 || nl < 0 || np < 0)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "synth: negative extent");
+    if ((int64_t)row_len * ns * nl * np == 0) return ok();
+    if (!dst) return fail(VKV_STATUS_INVALID_ARGUMENT, "synth: null destination");
+    hipError_t e = launch_synth(dst, row_len, seed, tag, s0, ns, s_stride, l0, nl, l_stride, p0, np,
+                                p_stride, as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "synth launch");
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,104 @@
+// Internal interface between the C++ host layer (vkv_host.cpp) and the gfx950
+// kernels (vkv_kernels.hip).  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "vkv.h"
+
+namespace vkv {
+
+constexpr int kMaxStreams = VKV_MAX_BATCH_STREAMS;
+
+// Logical window of one stream: logical index i maps to physical slot
+// s0 + i for i < n0, else s1 + (i - n0)  (the <=2 read segments of a plan).
+struct SegPair {
+    int32_t s0, n0, s1, n1;
+};
+
+struct CacheGeom {
+    uint8_t *k;            // cache base (stream 0, layer 0, slot 0)
+    uint8_t *v;
+    int64_t stream_bytes;
+    int64_t layer_bytes;
+    int64_t row_bytes;
+    int32_t kv_dim;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t dtype;
+};
+
+// Decode attention (split over slot chunks, merged by the combine kernel).
+struct DecodeArgs {
+    const uint8_t *k;      // base of stream0, layer0
+    const uint8_t *v;
+    int64_t stream_bytes, layer_bytes, row_bytes;
+    const float *q;        // [stream][layer][n_q_heads][head_dim]
+    int64_t q_sstride, q_lstride;
+    float *part_o;         // [stream][layer][n_q_heads][n_chunks][head_dim]
+    float *part_ml;        // [stream][layer][n_q_heads][n_chunks][2]
+    // fused combine: the last work group of each (stream, layer, kv head)
+    // merges the chunk partials; arrival counters self-reset to zero.
+    int32_t *counters;     // [stream][layer][n_kv_heads]; nullptr -> k_combine
+    float *out;            // [stream][layer][n_q_heads][head_dim]
+    int32_t n_chunks, chunk;
+    int32_t n_layers, n_kv_heads, n_q_heads;
+    float scale_log2;      // scale * log2(e)
+    // fused append (decoder step): new rows [stream][layer][kv_dim] f32
+    uint8_t *k_w;          // writable aliases of k/v for the fused append
+    uint8_t *v_w;
+    const float *k_new;
+    const float *v_new;
+    int64_t new_sstride, new_lstride;
+    SegPair seg[kMaxStreams];
+};
+
+struct CombineArgs {
+    const float *part_o;
+    const float *part_ml;
+    float *out;            // [stream][layer][n_q_heads][head_dim]
+    int32_t n_chunks, n_q_heads, n_layers, head_dim;
+};
+
+struct AppendArgs {
+    uint8_t *k;            // base of the stream, layer0
+    uint8_t *v;
+    int64_t layer_bytes, row_bytes;
+    const float *k_src;
+    const float *v_src;
+    int64_t src_lstride;   // floats between layers of the source
+    int32_t kv_dim, n_rows;
+    SegPair seg;           // write segments in logical order
+};
+
+struct WindowArgs {
+    const uint8_t *k;      // base of stream, layer0
+    const uint8_t *v;
+    int64_t layer_bytes, row_bytes;
+    const float *q;        // [layer][n_q][n_q_heads][head_dim]
+    float *out;
+    int64_t q_lstride;     // floats between layers of q/out
+    int32_t n_q, n_q_heads, n_kv_heads, head_dim, n_layers;
+    int64_t q_pos0, key_pos0;
+    int32_t window;        // <= 0: unbounded (causal only)
+    float scale_log2;
+    SegPair seg;           // logical key window
+};
+
+hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st);
+hipError_t launch_gather(const uint8_t *src, int64_t row_bytes, SegPair seg, uint8_t *dst,
+                         hipStream_t st);
+hipError_t launch_decode(int dtype, int gqa, bool fuse_append, int n_streams,
+                         const DecodeArgs &a, hipStream_t st);
+hipError_t launch_combine(const CombineArgs &a, int n_streams, hipStream_t st);
+hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st);
+hipError_t launch_q8_0_pack(const float *x, uint8_t *blocks, int64_t n, hipStream_t st);
+hipError_t launch_q8_0_unpack(const uint8_t *blocks, float *y, int64_t n, hipStream_t st);
+hipError_t launch_fill_zero(void *dst, int64_t bytes, hipStream_t st);
+hipError_t launch_synth(float *dst, int32_t row_len, uint64_t seed, uint32_t tag, int64_t s0,
+                        int32_t ns, int64_t s_stride, int64_t l0, int32_t nl, int64_t l_stride,
+                        int64_t p0, int32_t np, int64_t p_stride, hipStream_t st);
+
+}  // namespace vkv

@@ -1,0 +1,760 @@
+// gfx950 (MI355X, CDNA4, wave64) kernels of the voxtral.cpp KV-cache hot path.
+//
+//   k_append    -- ggml_set_rows / ggml_cpy of projected K/V rows into the ring
+//                  (src/voxtral.cpp:2682-2713, 2166-2185); f32 -> f16 RNE, f32
+//                  copy, or q8_0 block quantization, 8 elements per lane.
+//   k_gather    -- logical-window copy of <=2 read segments (src/voxtral.cpp:
+//                  2774-2799, 2285-2331), 16-byte vector copies.
+//   k_decode    -- single-query GQA decode attention (ggml_flash_attn_ext at
+//                  src/voxtral.cpp:2749-2819), split over slot chunks:
+//                  16 lanes x 16 B cover one 256-byte K/V head row, the 4 query
+//                  heads of a GQA group share every K/V load, QK partials and
+//                  softmax maxima are reduced with DPP / cross-lane shuffles,
+//                  online softmax in exp2 domain; optional fused append of the
+//                  step's new row (run_decoder_step's SET_ROWS, :2682-2694).
+//   k_combine   -- merge of the per-chunk (max, sum, unnormalised output).
+//   k_window    -- multi-query causal / sliding-window attention for the
+//                  encoder window (src/voxtral.cpp:2201-2284) and the decoder
+//                  prefill (:2893-2961).
+//   k_q8_pack / k_q8_unpack, k_fill_zero, k_synth.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "vkv_internal.h"
+
+namespace vkv {
+namespace {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ half2_t as_h2(uint32_t w) { return __builtin_bit_cast(half2_t, w); }
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// DPP row-local lane exchange; CTRL: 0xB1 = quad xor1, 0x4E = quad xor2,
+// 0x141 = row_half_mirror, 0x140 = row_mirror.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane receives the total.
+__device__ __forceinline__ float row_sum16(float x) {
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    x += dpp<0x141>(x);
+    x += dpp<0x140>(x);
+    return x;
+}
+
+// Max over the 4 lanes of a quad.
+__device__ __forceinline__ float quad_max(float x) {
+    x = fmaxf(x, dpp<0xB1>(x));
+    x = fmaxf(x, dpp<0x4E>(x));
+    return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float round_half_away(float v) {
+    float t = truncf(v);
+    float r = v - t;
+    if (r >= 0.5f) t += 1.0f;
+    else if (r <= -0.5f) t -= 1.0f;
+    return t;
+}
+
+__device__ __forceinline__ int slot_of(const SegPair &sp, int idx) {
+    return idx < sp.n0 ? sp.s0 + idx : sp.s1 + (idx - sp.n0);
+}
+
+// ---------------------------------------------------------------------------
+// Storage formats.  A fragment is the 8 consecutive elements [e, e+8) of a row
+// held by one lane (e is a multiple of 8).
+// ---------------------------------------------------------------------------
+
+struct FmtF16 {
+    struct Frag { uint32_t w[4]; };
+    struct QFrag { uint32_t w[4]; };
+    static __device__ __forceinline__ Frag load(const uint8_t *row, int e) {
+        const uint4 x = *reinterpret_cast<const uint4 *>(row + (int64_t)e * 2);
+        return Frag{{x.x, x.y, x.z, x.w}};
+    }
+    static __device__ __forceinline__ void store(uint8_t *row, int e, const Frag &f) {
+        *reinterpret_cast<uint4 *>(row + (int64_t)e * 2) = make_uint4(f.w[0], f.w[1], f.w[2], f.w[3]);
+    }
+    // IEEE binary16 round-to-nearest-even (v_cvt_f16_f32 in the default mode).
+    static __device__ __forceinline__ Frag from_f32(const float *x) {
+        Frag f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            half2_t h;
+            h.x = (_Float16)x[2 * i];
+            h.y = (_Float16)x[2 * i + 1];
+            f.w[i] = as_u32(h);
+        }
+        return f;
+    }
+    static __device__ __forceinline__ QFrag make_q(const float *x) {
+        Frag f = from_f32(x);
+        return QFrag{{f.w[0], f.w[1], f.w[2], f.w[3]}};
+    }
+    static __device__ __forceinline__ float dot(const Frag &k, const QFrag &q) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_fdot2(as_h2(k.w[i]), as_h2(q.w[i]), s, false);
+        return s;
+    }
+    static __device__ __forceinline__ void to_f32(const Frag &v, float *o) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            half2_t h = as_h2(v.w[i]);
+            o[2 * i] = (float)h.x;
+            o[2 * i + 1] = (float)h.y;
+        }
+    }
+};
+
+struct FmtF32 {
+    struct Frag { float x[8]; };
+    struct QFrag { float x[8]; };
+    static __device__ __forceinline__ Frag load(const uint8_t *row, int e) {
+        const float4 *p = reinterpret_cast<const float4 *>(row + (int64_t)e * 4);
+        const float4 a = p[0], b = p[1];
+        return Frag{{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w}};
+    }
+    static __device__ __forceinline__ void store(uint8_t *row, int e, const Frag &f) {
+        float4 *p = reinterpret_cast<float4 *>(row + (int64_t)e * 4);
+        p[0] = make_float4(f.x[0], f.x[1], f.x[2], f.x[3]);
+        p[1] = make_float4(f.x[4], f.x[5], f.x[6], f.x[7]);
+    }
+    static __device__ __forceinline__ Frag from_f32(const float *x) {
+        Frag f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f.x[i] = x[i];
+        return f;
+    }
+    static __device__ __forceinline__ QFrag make_q(const float *x) {
+        QFrag f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f.x[i] = x[i];
+        return f;
+    }
+    static __device__ __forceinline__ float dot(const Frag &k, const QFrag &q) {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s = fmaf(k.x[i], q.x[i], s);
+        return s;
+    }
+    static __device__ __forceinline__ void to_f32(const Frag &v, float *o) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = v.x[i];
+    }
+};
+
+// ggml block_q8_0 {fp16 d; int8 qs[32]} (34 bytes).  Element e lives in block
+// e/32 at byte 34*(e/32) + 2 + e%32; every field is 2-byte aligned, so loads
+// and stores use 16-bit accesses.  A block spans the 4 lanes of a quad, so
+// quantization (amax) reduces over the quad: callers keep quads converged.
+struct FmtQ8 {
+    struct Frag { uint32_t lo, hi; float d; };
+    struct QFrag { uint32_t lo, hi; float d; };
+    static __device__ __forceinline__ const uint8_t *blk(const uint8_t *row, int e) {
+        return row + (int64_t)(e >> 5) * 34;
+    }
+    static __device__ __forceinline__ Frag load(const uint8_t *row, int e) {
+        const uint8_t *b = blk(row, e);
+        const uint16_t *qs = reinterpret_cast<const uint16_t *>(b + 2 + (e & 31));
+        const uint16_t dh = *reinterpret_cast<const uint16_t *>(b);
+        Frag f;
+        f.lo = (uint32_t)qs[0] | ((uint32_t)qs[1] << 16);
+        f.hi = (uint32_t)qs[2] | ((uint32_t)qs[3] << 16);
+        f.d = (float)__builtin_bit_cast(_Float16, dh);
+        return f;
+    }
+    // Quantize 8 values; the quad holding one block cooperates on amax, so
+    // every lane of the quad must call this (no early exit before it).
+    static __device__ __forceinline__ Frag from_f32(const float *x) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+        amax = quad_max(amax);
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t b[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) b[i] = (uint32_t)((int)round_half_away(x[i] * id)) & 0xffu;
+        Frag f;
+        f.lo = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+        f.hi = b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24);
+        f.d = (float)(_Float16)d;   // the stored scale, exactly
+        return f;
+    }
+    static __device__ __forceinline__ void store(uint8_t *row, int e, const Frag &f) {
+        uint8_t *b = row + (int64_t)(e >> 5) * 34;
+        uint16_t *qs = reinterpret_cast<uint16_t *>(b + 2 + (e & 31));
+        qs[0] = (uint16_t)f.lo;
+        qs[1] = (uint16_t)(f.lo >> 16);
+        qs[2] = (uint16_t)f.hi;
+        qs[3] = (uint16_t)(f.hi >> 16);
+        if ((e & 31) == 0)
+            *reinterpret_cast<uint16_t *>(b) = __builtin_bit_cast(uint16_t, (_Float16)f.d);
+    }
+    static __device__ __forceinline__ QFrag make_q(const float *x) {
+        const Frag f = from_f32(x);
+        return QFrag{f.lo, f.hi, f.d};
+    }
+    static __device__ __forceinline__ float dot(const Frag &k, const QFrag &q) {
+        int s = __builtin_amdgcn_sdot4((int)k.lo, (int)q.lo, 0, false);
+        s = __builtin_amdgcn_sdot4((int)k.hi, (int)q.hi, s, false);
+        return (float)s * (k.d * q.d);
+    }
+    static __device__ __forceinline__ void to_f32(const Frag &v, float *o) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o[i] = (float)(int8_t)(v.lo >> (8 * i)) * v.d;
+            o[4 + i] = (float)(int8_t)(v.hi >> (8 * i)) * v.d;
+        }
+    }
+};
+
+// Convert 8 new f32 elements (called by every lane: Q8 quantization is
+// quad-cooperative) and store them when `ok`.
+template <class F>
+__device__ __forceinline__ typename F::Frag store_new(uint8_t *row, int e, const float *x, bool ok) {
+    const typename F::Frag f = F::from_f32(x);
+    if (ok) F::store(row, e, f);
+    return f;
+}
+
+// ---------------------------------------------------------------------------
+// Append.  Thread t converts elements [8t, 8t+8) of the flattened
+// [n_rows][kv_dim] source of one (layer, K|V).
+// ---------------------------------------------------------------------------
+template <class F>
+__global__ void __launch_bounds__(256) k_append(AppendArgs a) {
+    const int layer = blockIdx.y;
+    const int which = blockIdx.z;
+    const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    const int64_t total = (int64_t)a.n_rows * a.kv_dim;
+    const bool ok = e0 < total;
+    const int row = ok ? (int)(e0 / a.kv_dim) : 0;
+    const int col = ok ? (int)(e0 % a.kv_dim) : 0;
+    float x[8];
+    if (ok) {
+        const float *src = (which ? a.v_src : a.k_src) + (int64_t)layer * a.src_lstride +
+                           (int64_t)row * a.kv_dim + col;
+        const float4 p0 = reinterpret_cast<const float4 *>(src)[0];
+        const float4 p1 = reinterpret_cast<const float4 *>(src)[1];
+        x[0] = p0.x; x[1] = p0.y; x[2] = p0.z; x[3] = p0.w;
+        x[4] = p1.x; x[5] = p1.y; x[6] = p1.z; x[7] = p1.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = 0.0f;
+    }
+    const int slot = slot_of(a.seg, row);
+    uint8_t *dst = (which ? a.v : a.k) + (int64_t)layer * a.layer_bytes + (int64_t)slot * a.row_bytes;
+    store_new<F>(dst, col, x, ok);
+}
+
+// ---------------------------------------------------------------------------
+// Gather: logical window rows -> contiguous rows, bit-exact.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void __launch_bounds__(256) k_gather(const uint8_t *src, int64_t row_bytes, SegPair seg,
+                                                uint8_t *dst) {
+    const int64_t per_row = row_bytes / (int64_t)sizeof(T);
+    const int64_t total = (int64_t)(seg.n0 + seg.n1) * per_row;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * 256) {
+        const int row = (int)(t / per_row);
+        const int64_t w = t % per_row;
+        const int slot = slot_of(seg, row);
+        reinterpret_cast<T *>(dst)[t] =
+            reinterpret_cast<const T *>(src + (int64_t)slot * row_bytes)[w];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention.  Workgroup = 4 waves on (stream, layer, kv head g, chunk
+// of `chunk` logical slots).  Lane (grp = lane/16, c = lane%16) holds elements
+// [8c, 8c+8) of one slot's head row; a wave covers 4 slots per load, 16 slots
+// per batch (4 loads of K and of V in flight per lane).
+// ---------------------------------------------------------------------------
+template <class F, int GQA, bool FUSE>
+__global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
+    constexpr int D = 128;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int grp = lane >> 4;
+    const int c = lane & 15;
+    const int g = blockIdx.x % a.n_kv_heads;
+    const int chunk = blockIdx.x / a.n_kv_heads;
+    const int layer = blockIdx.y;
+    const int s = blockIdx.z;
+    const SegPair sp = a.seg[s];
+    const int n_kv = sp.n0 + sp.n1;
+    const int64_t base = (int64_t)s * a.stream_bytes + (int64_t)layer * a.layer_bytes;
+    const uint8_t *kl = a.k + base;
+    const uint8_t *vl = a.v + base;
+    const int e = g * D + c * 8;
+
+    typename F::QFrag qf[GQA];
+    {
+        const float *qp = a.q + (int64_t)s * a.q_sstride + (int64_t)layer * a.q_lstride +
+                          (int64_t)(g * GQA) * D + c * 8;
+#pragma unroll
+        for (int j = 0; j < GQA; ++j) {
+            const float4 q0 = reinterpret_cast<const float4 *>(qp + j * D)[0];
+            const float4 q1 = reinterpret_cast<const float4 *>(qp + j * D)[1];
+            const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            qf[j] = F::make_q(qv);
+        }
+    }
+
+    float m[GQA], l[GQA], acc[GQA][8];
+#pragma unroll
+    for (int j = 0; j < GQA; ++j) {
+        m[j] = -INFINITY;
+        l[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[j][i] = 0.0f;
+    }
+
+    const int i_begin = chunk * a.chunk;
+    const int i_end = min(i_begin + a.chunk, n_kv);
+    for (int b0 = i_begin + wave * 16; b0 < i_end; b0 += 64) {
+        typename F::Frag kf[4], vf[4];
+        int idx[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            idx[u] = b0 + u * 4 + grp;
+            const int slot = idx[u] < i_end ? slot_of(sp, idx[u]) : sp.s0;
+            kf[u] = F::load(kl + (int64_t)slot * a.row_bytes, e);
+            vf[u] = F::load(vl + (int64_t)slot * a.row_bytes, e);
+        }
+        if (FUSE) {
+            // The step's new row is the newest logical index: convert it once,
+            // store it into the ring, and attend with the stored values.
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                if (idx[u] == n_kv - 1) {
+                    const int slot = slot_of(sp, idx[u]);
+                    const float *kn = a.k_new + (int64_t)s * a.new_sstride +
+                                      (int64_t)layer * a.new_lstride + e;
+                    const float *vn = a.v_new + (int64_t)s * a.new_sstride +
+                                      (int64_t)layer * a.new_lstride + e;
+                    float xk[8], xv[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) { xk[i] = kn[i]; xv[i] = vn[i]; }
+                    uint8_t *krow = a.k_w + base + (int64_t)slot * a.row_bytes;
+                    uint8_t *vrow = a.v_w + base + (int64_t)slot * a.row_bytes;
+                    kf[u] = store_new<F>(krow, e, xk, true);
+                    vf[u] = store_new<F>(vrow, e, xv, true);
+                }
+            }
+        }
+        float sc[4][GQA];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+            for (int j = 0; j < GQA; ++j) {
+                const float p = row_sum16(F::dot(kf[u], qf[j]));
+                sc[u][j] = idx[u] < i_end ? p * a.scale_log2 : -INFINITY;
+            }
+        }
+        float vv[4][8];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) F::to_f32(vf[u], vv[u]);
+#pragma unroll
+        for (int j = 0; j < GQA; ++j) {
+            float bm = fmaxf(fmaxf(sc[0][j], sc[1][j]), fmaxf(sc[2][j], sc[3][j]));
+            bm = fmaxf(bm, __shfl_xor(bm, 16));
+            bm = fmaxf(bm, __shfl_xor(bm, 32));
+            const float mn = fmaxf(m[j], bm);
+            if (mn != -INFINITY) {
+                const float alpha = fast_exp2(m[j] - mn);
+                float pu[4], ps = 0.0f;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    pu[u] = fast_exp2(sc[u][j] - mn);
+                    ps += pu[u];
+                }
+                l[j] = l[j] * alpha + ps;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    float o = acc[j][i] * alpha;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) o = fmaf(pu[u], vv[u][i], o);
+                    acc[j][i] = o;
+                }
+                m[j] = mn;
+            }
+        }
+    }
+
+    // Merge the 4 lane groups (they share m).
+#pragma unroll
+    for (int j = 0; j < GQA; ++j) {
+        l[j] += __shfl_xor(l[j], 16);
+        l[j] += __shfl_xor(l[j], 32);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            acc[j][i] += __shfl_xor(acc[j][i], 16);
+            acc[j][i] += __shfl_xor(acc[j][i], 32);
+        }
+    }
+
+    // Merge the 4 waves through LDS and write this chunk's partial.
+    __shared__ float sm_m[4][GQA], sm_l[4][GQA];
+    __shared__ float sm_o[4][GQA][D];
+    if (grp == 0) {
+#pragma unroll
+        for (int j = 0; j < GQA; ++j) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sm_o[wave][j][c * 8 + i] = acc[j][i];
+            if (c == 0) {
+                sm_m[wave][j] = m[j];
+                sm_l[wave][j] = l[j];
+            }
+        }
+    }
+    __syncthreads();
+    const int64_t head0 = ((int64_t)s * a.n_layers + layer) * a.n_q_heads + (int64_t)g * GQA;
+    for (int t = threadIdx.x; t < GQA * D; t += 256) {
+        const int j = t / D;
+        const int d = t % D;
+        float M = fmaxf(fmaxf(sm_m[0][j], sm_m[1][j]), fmaxf(sm_m[2][j], sm_m[3][j]));
+        float O = 0.0f, L = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float sc_w = fast_exp2(sm_m[w][j] - M);
+                O = fmaf(sm_o[w][j][d], sc_w, O);
+                L = fmaf(sm_l[w][j], sc_w, L);
+            }
+        }
+        const int64_t pidx = (head0 + j) * a.n_chunks + chunk;
+        a.part_o[pidx * D + d] = O;
+        if (d == 0) {
+            a.part_ml[pidx * 2] = M;
+            a.part_ml[pidx * 2 + 1] = L;
+        }
+    }
+    if (a.counters == nullptr) return;
+
+    // Fused combine: publish this chunk's partial, count arrivals; the last
+    // work group of the (stream, layer, kv head) merges all chunks.  No work
+    // group ever waits for another.
+    __shared__ int sm_last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int32_t *cnt = a.counters + ((int64_t)s * a.n_layers + layer) * a.n_kv_heads + g;
+        const int old = atomicAdd(cnt, 1);
+        sm_last = old == a.n_chunks - 1;
+        if (sm_last) atomicExch(cnt, 0);
+    }
+    __syncthreads();
+    if (!sm_last) return;
+    __threadfence();
+    for (int t = threadIdx.x; t < GQA * D; t += 256) {
+        const int j = t / D;
+        const int d = t % D;
+        const int64_t p0 = (head0 + j) * a.n_chunks;
+        float M = -INFINITY;
+        for (int c2 = 0; c2 < a.n_chunks; ++c2) M = fmaxf(M, __builtin_nontemporal_load(&a.part_ml[(p0 + c2) * 2]));
+        float O = 0.0f, L = 0.0f;
+        if (M != -INFINITY) {
+            for (int c2 = 0; c2 < a.n_chunks; ++c2) {
+                const float w = fast_exp2(__builtin_nontemporal_load(&a.part_ml[(p0 + c2) * 2]) - M);
+                L = fmaf(__builtin_nontemporal_load(&a.part_ml[(p0 + c2) * 2 + 1]), w, L);
+                O = fmaf(__builtin_nontemporal_load(&a.part_o[(p0 + c2) * D + d]), w, O);
+            }
+        }
+        a.out[(head0 + j) * D + d] = L > 0.0f ? O / L : 0.0f;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_combine(CombineArgs a) {
+    const int h = blockIdx.x;
+    const int layer = blockIdx.y;
+    const int s = blockIdx.z;
+    const int64_t head = ((int64_t)s * a.n_layers + layer) * a.n_q_heads + h;
+    const int64_t p0 = head * a.n_chunks;
+    for (int d = threadIdx.x; d < a.head_dim; d += blockDim.x) {
+        float M = -INFINITY;
+        for (int c = 0; c < a.n_chunks; ++c) M = fmaxf(M, a.part_ml[(p0 + c) * 2]);
+        float O = 0.0f, L = 0.0f;
+        if (M != -INFINITY) {
+            for (int c = 0; c < a.n_chunks; ++c) {
+                const float w = fast_exp2(a.part_ml[(p0 + c) * 2] - M);
+                L = fmaf(a.part_ml[(p0 + c) * 2 + 1], w, L);
+                O = fmaf(a.part_o[(p0 + c) * a.head_dim + d], w, O);
+            }
+        }
+        a.out[head * a.head_dim + d] = L > 0.0f ? O / L : 0.0f;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Window attention (one wave per (query, head, layer)): two passes over the
+// allowed keys -- max, then exp-weights through LDS and a lane-per-dimension
+// P.V accumulation.
+// ---------------------------------------------------------------------------
+template <class F>
+__global__ void __launch_bounds__(64) k_window(WindowArgs a) {
+    const int lane = threadIdx.x;
+    const int qi = blockIdx.x / a.n_q_heads;
+    const int h = blockIdx.x % a.n_q_heads;
+    const int layer = blockIdx.y;
+    const int g = h / (a.n_q_heads / a.n_kv_heads);
+    const int D = a.head_dim;
+    const int n_keys = a.seg.n0 + a.seg.n1;
+    const int64_t q_abs = a.q_pos0 + qi;
+    const uint8_t *kl = a.k + (int64_t)layer * a.layer_bytes;
+    const uint8_t *vl = a.v + (int64_t)layer * a.layer_bytes;
+    __shared__ float sq[256];
+    __shared__ float sp[64];
+    const float *qp = a.q + (int64_t)layer * a.q_lstride + ((int64_t)qi * a.n_q_heads + h) * D;
+    for (int d = lane; d < D; d += 64) sq[d] = qp[d];
+    __syncthreads();
+
+    // allowed keys form one contiguous logical range [j_lo, j_hi)
+    const int64_t lo = a.window > 0 ? q_abs - (a.window - 1) : -((int64_t)1 << 62);
+    const int64_t j_lo64 = lo - a.key_pos0;
+    const int64_t j_hi64 = q_abs - a.key_pos0 + 1;
+    const int j_lo = (int)max<int64_t>(0, j_lo64);
+    const int j_hi = (int)min<int64_t>(n_keys, j_hi64);
+
+    auto score = [&](int j) -> float {
+        const uint8_t *row = kl + (int64_t)slot_of(a.seg, j) * a.row_bytes;
+        float s = 0.0f;
+        for (int e0 = 0; e0 < D; e0 += 8) {
+            float kv[8];
+            F::to_f32(F::load(row, g * D + e0), kv);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s = fmaf(kv[i], sq[e0 + i], s);
+        }
+        return s * a.scale_log2;
+    };
+
+    float M = -INFINITY;
+    for (int j = j_lo + lane; j < j_hi; j += 64) M = fmaxf(M, score(j));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+
+    float o0 = 0.0f, o1 = 0.0f, L = 0.0f;
+    for (int jb = j_lo; jb < j_hi; jb += 64) {
+        const int j = jb + lane;
+        const float p = j < j_hi ? fast_exp2(score(j) - M) : 0.0f;
+        __syncthreads();
+        sp[lane] = p;
+        __syncthreads();
+        const int nb = min(64, j_hi - jb);
+        for (int kk = 0; kk < nb; ++kk) {
+            const float pk = sp[kk];
+            L += pk;
+            const uint8_t *row = vl + (int64_t)slot_of(a.seg, jb + kk) * a.row_bytes;
+            // lane holds dims lane and lane+64 (D <= 128)
+            float vv[8];
+            const int d0 = lane;
+            if (d0 < D) {
+                F::to_f32(F::load(row, g * D + (d0 & ~7)), vv);
+                o0 = fmaf(pk, vv[d0 & 7], o0);
+            }
+            const int d1 = lane + 64;
+            if (d1 < D) {
+                F::to_f32(F::load(row, g * D + (d1 & ~7)), vv);
+                o1 = fmaf(pk, vv[d1 & 7], o1);
+            }
+        }
+    }
+    float *op = a.out + (int64_t)layer * a.q_lstride + ((int64_t)qi * a.n_q_heads + h) * D;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    if (lane < D) op[lane] = o0 * inv;
+    if (lane + 64 < D) op[lane + 64] = o1 * inv;
+}
+
+// ---------------------------------------------------------------------------
+// q8_0 pack / unpack of flat f32 arrays (n % 32 == 0); 8 elements per lane.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_q8_pack(const float *x, uint8_t *blocks, int64_t n) {
+    const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    const bool ok = e0 < n;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = ok ? x[e0 + i] : 0.0f;
+    store_new<FmtQ8>(blocks + (e0 >> 5) * 34, (int)(e0 & 31), v, ok);
+}
+
+__global__ void __launch_bounds__(256) k_q8_unpack(const uint8_t *blocks, float *y, int64_t n) {
+    const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (e0 >= n) return;
+    const FmtQ8::Frag f = FmtQ8::load(blocks + (e0 >> 5) * 34, (int)(e0 & 31));
+    float o[8];
+    FmtQ8::to_f32(f, o);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[e0 + i] = o[i];
+}
+
+__global__ void __launch_bounds__(256) k_fill_zero(uint8_t *dst, int64_t bytes) {
+    const int64_t n16 = bytes / 16;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < n16; t += (int64_t)gridDim.x * 256)
+        reinterpret_cast<uint4 *>(dst)[t] = make_uint4(0u, 0u, 0u, 0u);
+    const int64_t tail = bytes - n16 * 16;
+    if (blockIdx.x == 0 && threadIdx.x < tail) dst[n16 * 16 + threadIdx.x] = 0;
+}
+
+// ---------------------------------------------------------------------------
+// Seeded synthetic N(0,1): splitmix64 output function, twelve 16-bit uniforms
+// summed (integer Irwin-Hall), exact in f32.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+struct SynthArgs {
+    float *dst;
+    uint64_t seed;
+    uint32_t tag;
+    int32_t row_len, ns, nl, np;
+    int64_t s0, l0, p0, s_stride, l_stride, p_stride;
+};
+
+__global__ void __launch_bounds__(256) k_synth(SynthArgs a) {
+    const int64_t rows = (int64_t)a.ns * a.nl * a.np;
+    const int64_t total = rows * a.row_len;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * 256) {
+        const int64_t r = t / a.row_len;
+        const int64_t i = t % a.row_len;
+        const int64_t kp = r % a.np;
+        const int64_t jl = (r / a.np) % a.nl;
+        const int64_t is = r / ((int64_t)a.np * a.nl);
+        uint64_t key = mix64(a.seed ^ ((uint64_t)a.tag << 32));
+        key = mix64(key ^ (uint64_t)(a.s0 + is));
+        key = mix64(key ^ (uint64_t)(a.l0 + jl));
+        key = mix64(key ^ (uint64_t)(a.p0 + kp));
+        const uint64_t b = key ^ ((uint64_t)i * 0xD1B54A32D192ED03ull);
+        int32_t sum = 0;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const uint64_t hsh = mix64(b + (uint64_t)k * 0x9E3779B97F4A7C15ull);
+            sum += (int32_t)(hsh & 0xffffu) + (int32_t)((hsh >> 16) & 0xffffu) +
+                   (int32_t)((hsh >> 32) & 0xffffu) + (int32_t)(hsh >> 48);
+        }
+        const int64_t drow = is * a.s_stride + jl * a.l_stride + kp * a.p_stride;
+        a.dst[drow * a.row_len + i] = (float)(sum - 393210) * (1.0f / 65536.0f);
+    }
+}
+
+inline unsigned grid_for(int64_t work, int64_t per_block, int64_t cap = 1 << 20) {
+    int64_t g = (work + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > cap) g = cap;
+    return (unsigned)g;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Launchers.
+// ---------------------------------------------------------------------------
+hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st) {
+    const int64_t threads = ((int64_t)a.n_rows * a.kv_dim + 7) / 8;
+    dim3 grid(grid_for(threads, 256, INT32_MAX), (unsigned)n_layers, 2);
+    switch (dtype) {
+    case VKV_DTYPE_F16: hipLaunchKernelGGL(k_append<FmtF16>, grid, dim3(256), 0, st, a); break;
+    case VKV_DTYPE_F32: hipLaunchKernelGGL(k_append<FmtF32>, grid, dim3(256), 0, st, a); break;
+    case VKV_DTYPE_Q8_0: hipLaunchKernelGGL(k_append<FmtQ8>, grid, dim3(256), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gather(const uint8_t *src, int64_t row_bytes, SegPair seg, uint8_t *dst,
+                         hipStream_t st) {
+    const int64_t rows = seg.n0 + seg.n1;
+    if (rows == 0) return hipSuccess;
+    if (row_bytes % 16 == 0 && ((uintptr_t)dst % 16) == 0 && ((uintptr_t)src % 16) == 0) {
+        hipLaunchKernelGGL(k_gather<uint4>, dim3(grid_for(rows * row_bytes / 16, 256, 65536)),
+                           dim3(256), 0, st, src, row_bytes, seg, dst);
+    } else {
+        hipLaunchKernelGGL(k_gather<uint16_t>, dim3(grid_for(rows * row_bytes / 2, 256, 65536)),
+                           dim3(256), 0, st, src, row_bytes, seg, dst);
+    }
+    return hipGetLastError();
+}
+
+template <class F, int GQA>
+static void launch_decode_fmt(bool fuse, dim3 grid, const DecodeArgs &a, hipStream_t st) {
+    if (fuse) hipLaunchKernelGGL((k_decode<F, GQA, true>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((k_decode<F, GQA, false>), grid, dim3(256), 0, st, a);
+}
+
+hipError_t launch_decode(int dtype, int gqa, bool fuse_append, int n_streams, const DecodeArgs &a,
+                         hipStream_t st) {
+    dim3 grid((unsigned)(a.n_chunks * a.n_kv_heads), (unsigned)a.n_layers, (unsigned)n_streams);
+    if (gqa != 4) return hipErrorInvalidValue;
+    switch (dtype) {
+    case VKV_DTYPE_F16: launch_decode_fmt<FmtF16, 4>(fuse_append, grid, a, st); break;
+    case VKV_DTYPE_F32: launch_decode_fmt<FmtF32, 4>(fuse_append, grid, a, st); break;
+    case VKV_DTYPE_Q8_0: launch_decode_fmt<FmtQ8, 4>(fuse_append, grid, a, st); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const CombineArgs &a, int n_streams, hipStream_t st) {
+    dim3 grid((unsigned)a.n_q_heads, (unsigned)a.n_layers, (unsigned)n_streams);
+    hipLaunchKernelGGL(k_combine, grid, dim3(128), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st) {
+    dim3 grid((unsigned)(a.n_q * a.n_q_heads), (unsigned)a.n_layers);
+    switch (dtype) {
+    case VKV_DTYPE_F16: hipLaunchKernelGGL(k_window<FmtF16>, grid, dim3(64), 0, st, a); break;
+    case VKV_DTYPE_F32: hipLaunchKernelGGL(k_window<FmtF32>, grid, dim3(64), 0, st, a); break;
+    case VKV_DTYPE_Q8_0: hipLaunchKernelGGL(k_window<FmtQ8>, grid, dim3(64), 0, st, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_0_pack(const float *x, uint8_t *blocks, int64_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_q8_pack, dim3(grid_for(n / 8, 256, INT32_MAX)), dim3(256), 0, st, x,
+                       blocks, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_0_unpack(const uint8_t *blocks, float *y, int64_t n, hipStream_t st) {
+    hipLaunchKernelGGL(k_q8_unpack, dim3(grid_for(n / 8, 256, INT32_MAX)), dim3(256), 0, st,
+                       blocks, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(void *dst, int64_t bytes, hipStream_t st) {
+    if (bytes <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_fill_zero, dim3(grid_for(bytes / 16 + 1, 256, 65536)), dim3(256), 0, st,
+                       (uint8_t *)dst, bytes);
+    return hipGetLastError();
+}
+
+hipError_t launch_synth(float *dst, int32_t row_len, uint64_t seed, uint32_t tag, int64_t s0,
+                        int32_t ns, int64_t s_stride, int64_t l0, int32_t nl, int64_t l_stride,
+                        int64_t p0, int32_t np, int64_t p_stride, hipStream_t st) {
+    SynthArgs a{dst, seed, tag, row_len, ns, nl, np, s0, l0, p0, s_stride, l_stride, p_stride};
+    const int64_t total = (int64_t)ns * nl * np * row_len;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_synth, dim3(grid_for(total, 256, 65536)), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace vkv

@@ -1,0 +1,310 @@
+"""ctypes binding of libvkv.so (include/vkv.h), the gfx950 KV-cache hot path.
+
+Structures mirror the C ABI field for field; every wrapper raises VkvError on a
+non-OK status with the library's own message.  Device pointers are plain
+integers (e.g. torch's ``tensor.data_ptr()``); ``hip_stream`` is a raw
+hipStream_t (``torch.cuda.current_stream().cuda_stream``) or 0.
+
+There is no CPU fallback: if libvkv.so is missing, importing this module
+raises.
+"""
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libvkv.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"{LIB_PATH} is missing: build it with `python voxtral.cpp_amd/build.py` "
+        "(or __graft_entry__.build()); the KV path has no fallback")
+
+lib = ctypes.CDLL(LIB_PATH)
+
+# status / dtype ---------------------------------------------------------
+OK = 0
+INVALID_ARGUMENT = 1
+INVALID_STATE = 2
+OUT_OF_MEMORY = 3
+BACKEND_ERROR = 9
+INTERNAL_ERROR = 10
+BUFFER_TOO_SMALL = 11
+
+F32 = 0
+F16 = 1
+Q8_0 = 8
+MAX_BATCH_STREAMS = 32
+
+
+def row_bytes(dtype, n):
+    return {F32: 4 * n, F16: 2 * n, Q8_0: (n // 32) * 34}[dtype]
+
+
+class VkvError(RuntimeError):
+    def __init__(self, status, message, backend_code=0):
+        super().__init__(f"vkv status {status}: {message}")
+        self.status = status
+        self.message = message
+        self.backend_code = backend_code
+
+
+# structures (field-for-field with include/vkv.h) ---------------------------
+class Ring(ctypes.Structure):
+    _fields_ = [("capacity", ctypes.c_int64), ("used", ctypes.c_int64),
+                ("oldest_absolute_position", ctypes.c_int64),
+                ("next_absolute_position", ctypes.c_int64), ("wraps", ctypes.c_int64),
+                ("evictions", ctypes.c_int64), ("bytes_moved", ctypes.c_int64),
+                ("full_buffer_moves", ctypes.c_int64)]
+
+
+class Seg(ctypes.Structure):
+    _fields_ = [("slot", ctypes.c_int32), ("len", ctypes.c_int32)]
+
+
+class Plan(ctypes.Structure):
+    _fields_ = [("absolute_start", ctypes.c_int64), ("n_new", ctypes.c_int32),
+                ("write_seg", Seg * 2), ("write_nseg", ctypes.c_int32),
+                ("read_seg", Seg * 2), ("read_nseg", ctypes.c_int32),
+                ("used_after", ctypes.c_int64), ("oldest_after", ctypes.c_int64),
+                ("next_after", ctypes.c_int64), ("evicted", ctypes.c_int64),
+                ("wrapped", ctypes.c_bool)]
+
+
+class EncPlan(ctypes.Structure):
+    _fields_ = [("q_start", ctypes.c_int64), ("n_new", ctypes.c_int32),
+                ("win_start", ctypes.c_int64), ("win_end", ctypes.c_int64),
+                ("win_len", ctypes.c_int32), ("read_seg", Seg * 2),
+                ("read_nseg", ctypes.c_int32), ("read_wraps", ctypes.c_bool),
+                ("write_seg", Seg * 2), ("write_nseg", ctypes.c_int32),
+                ("write_wraps", ctypes.c_bool), ("conv_mel_start", ctypes.c_int64),
+                ("conv_mel_end", ctypes.c_int64), ("conv_slice_start", ctypes.c_int32),
+                ("evicted", ctypes.c_int64)]
+
+
+class CacheParams(ctypes.Structure):
+    _fields_ = [("struct_size", ctypes.c_uint32), ("n_streams", ctypes.c_int32),
+                ("n_layers", ctypes.c_int32), ("capacity", ctypes.c_int32),
+                ("n_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("n_q_heads", ctypes.c_int32), ("dtype", ctypes.c_int32),
+                ("device", ctypes.c_int32)]
+
+
+class CacheLayout(ctypes.Structure):
+    _fields_ = [("row_bytes", ctypes.c_uint64), ("layer_bytes", ctypes.c_uint64),
+                ("stream_bytes", ctypes.c_uint64), ("total_bytes", ctypes.c_uint64),
+                ("k_base", ctypes.c_void_p), ("v_base", ctypes.c_void_p)]
+
+
+_P = ctypes.POINTER
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
+_u32 = ctypes.c_uint32
+_f32 = ctypes.c_float
+
+# prototypes: name -> (restype, argtypes); exactly the functions of include/vkv.h
+PROTOTYPES = {
+    "vkv_decoder_plan": (_i32, [_P(Ring), _i64, _i32, _P(Plan)]),
+    "vkv_decoder_commit": (_i32, [_P(Ring), _P(Plan)]),
+    "vkv_decoder_clear": (_i32, [_P(Ring), _i64]),
+    "vkv_enc_plan_build": (_i32, [_i64, _i32, _i32, _i32, _P(EncPlan)]),
+    "vkv_enc_mask_allows": (_i32, [_i64, _i64, _i32]),
+    "vkv_cache_create": (_i32, [_P(CacheParams), _P(_vp)]),
+    "vkv_cache_destroy": (_i32, [_vp]),
+    "vkv_cache_get_layout": (_i32, [_vp, _P(CacheLayout)]),
+    "vkv_cache_read_rows": (_i32, [_vp, _i32, _i32, _i32, _i32, _i32, _vp, ctypes.c_size_t]),
+    "vkv_cache_zero": (_i32, [_vp, _vp]),
+    "vkv_append": (_i32, [_vp, _i32, _i32, _i32, _P(Seg), _i32, _vp, _vp, _i64, _vp]),
+    "vkv_gather": (_i32, [_vp, _i32, _i32, _P(Seg), _i32, _vp, _vp, _vp]),
+    "vkv_decode_attn": (_i32, [_vp, _i32, _i32, _i32, _i32, _P(Plan), _vp, _vp, _i32, _f32, _vp]),
+    "vkv_decoder_step": (_i32, [_vp, _i32, _i32, _P(Ring), _P(_i64), _i32, _i32, _vp, _vp, _vp,
+                                _vp, _i32, _f32, _P(Plan), _vp]),
+    "vkv_decoder_prefill": (_i32, [_vp, _i32, _P(Ring), _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                   _i32, _f32, _vp]),
+    "vkv_enc_step": (_i32, [_vp, _i32, _P(EncPlan), _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32,
+                            _f32, _vp]),
+    "vkv_window_attn": (_i32, [_vp, _i32, _i32, _i32, _P(Seg), _i32, _i64, _i64, _i32, _i32,
+                               _vp, _vp, _i32, _f32, _vp]),
+    "vkv_q8_0_pack": (_i32, [_vp, _vp, _i64, _vp]),
+    "vkv_q8_0_unpack": (_i32, [_vp, _vp, _i64, _vp]),
+    "vkv_synth_rows": (_i32, [_vp, _i32, _u64, _u32, _i64, _i32, _i64, _i64, _i32, _i64, _i64,
+                              _i32, _i64, _vp]),
+    "vkv_api_version": (_u32, []),
+    "vkv_last_error": (ctypes.c_char_p, []),
+    "vkv_last_backend_code": (_i32, []),
+}
+
+for _name, (_res, _args) in PROTOTYPES.items():
+    _fn = getattr(lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+def last_error():
+    return lib.vkv_last_error().decode()
+
+
+def check(status):
+    if status != OK:
+        raise VkvError(status, last_error(), lib.vkv_last_backend_code())
+    return status
+
+
+def _segs(segs):
+    arr = (Seg * 2)()
+    for i, (slot, n) in enumerate(segs):
+        arr[i].slot, arr[i].len = slot, n
+    return arr, len(segs)
+
+
+def plan_segs(segs, nseg):
+    return [(segs[i].slot, segs[i].len) for i in range(nseg)]
+
+
+# planners -----------------------------------------------------------------
+def decoder_plan(ring, absolute_start, n_new):
+    p = Plan()
+    check(lib.vkv_decoder_plan(ctypes.byref(ring), absolute_start, n_new, ctypes.byref(p)))
+    return p
+
+
+def decoder_commit(ring, plan):
+    check(lib.vkv_decoder_commit(ctypes.byref(ring), ctypes.byref(plan)))
+
+
+def new_ring(capacity):
+    r = Ring()
+    check(lib.vkv_decoder_clear(ctypes.byref(r), capacity))
+    return r
+
+
+def enc_plan(q_start, n_new, capacity, window):
+    p = EncPlan()
+    check(lib.vkv_enc_plan_build(q_start, n_new, capacity, window, ctypes.byref(p)))
+    return p
+
+
+def enc_mask_allows(kv_abs, q_abs, window):
+    return bool(lib.vkv_enc_mask_allows(kv_abs, q_abs, window))
+
+
+# cache --------------------------------------------------------------------
+class Cache:
+    """Owns one vkv_cache handle (K and V storage on the device)."""
+
+    def __init__(self, n_streams=1, n_layers=26, capacity=8192, n_kv_heads=8, head_dim=128,
+                 n_q_heads=32, dtype=F16, device=0):
+        p = CacheParams(ctypes.sizeof(CacheParams), n_streams, n_layers, capacity, n_kv_heads,
+                        head_dim, n_q_heads, dtype, device)
+        h = _vp()
+        check(lib.vkv_cache_create(ctypes.byref(p), ctypes.byref(h)))
+        self.handle = h
+        self.params = p
+        self.n_streams, self.n_layers, self.capacity = n_streams, n_layers, capacity
+        self.n_kv_heads, self.head_dim, self.n_q_heads = n_kv_heads, head_dim, n_q_heads
+        self.kv_dim = n_kv_heads * head_dim
+        self.dtype = dtype
+        lay = CacheLayout()
+        check(lib.vkv_cache_get_layout(h, ctypes.byref(lay)))
+        self.layout = lay
+        self.row_bytes = lay.row_bytes
+
+    def close(self):
+        if self.handle:
+            check(lib.vkv_cache_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def read_rows(self, which, stream, layer, slot0, n_slots):
+        """Synchronous copy of raw row bytes -> bytes object."""
+        n = int(n_slots * self.row_bytes)
+        buf = ctypes.create_string_buffer(max(n, 1))
+        check(lib.vkv_cache_read_rows(self.handle, which, stream, layer, slot0, n_slots, buf, n))
+        return buf.raw[:n]
+
+    def zero(self, hip_stream=0):
+        check(lib.vkv_cache_zero(self.handle, hip_stream))
+
+    def append(self, stream, layer0, n_layers, segs, k_ptr, v_ptr, layer_stride=0, hip_stream=0):
+        arr, n = _segs(segs)
+        check(lib.vkv_append(self.handle, stream, layer0, n_layers, arr, n, k_ptr, v_ptr,
+                             layer_stride, hip_stream))
+
+    def gather(self, stream, layer, segs, k_dst, v_dst, hip_stream=0):
+        arr, n = _segs(segs)
+        check(lib.vkv_gather(self.handle, stream, layer, arr, n, k_dst, v_dst, hip_stream))
+
+    def decode_attn(self, stream0, plans, layer0, n_layers, q_ptr, out_ptr, scale, hip_stream=0,
+                    n_q_heads=None):
+        arr = (Plan * len(plans))(*plans)
+        check(lib.vkv_decode_attn(self.handle, stream0, len(plans), layer0, n_layers, arr, q_ptr,
+                                  out_ptr, n_q_heads or self.n_q_heads, scale, hip_stream))
+
+    def decoder_step(self, stream0, rings, positions, layer0, n_layers, q_ptr, k_ptr, v_ptr,
+                     out_ptr, scale, hip_stream=0, n_q_heads=None):
+        """rings: ctypes array of Ring (updated in place on success)."""
+        ns = len(rings)
+        pos = (_i64 * ns)(*positions)
+        plans = (Plan * ns)()
+        check(lib.vkv_decoder_step(self.handle, stream0, ns, rings, pos, layer0, n_layers, q_ptr,
+                                   k_ptr, v_ptr, out_ptr, n_q_heads or self.n_q_heads, scale,
+                                   plans, hip_stream))
+        return plans
+
+    def decoder_prefill(self, stream, ring, layer0, n_layers, n_tokens, q_ptr, k_ptr, v_ptr,
+                        out_ptr, scale, hip_stream=0, n_q_heads=None):
+        check(lib.vkv_decoder_prefill(self.handle, stream, ctypes.byref(ring), layer0, n_layers,
+                                      n_tokens, q_ptr, k_ptr, v_ptr, out_ptr,
+                                      n_q_heads or self.n_q_heads, scale, hip_stream))
+
+    def enc_step(self, stream, plan, window, layer0, n_layers, q_ptr, k_ptr, v_ptr, out_ptr,
+                 scale, hip_stream=0, n_q_heads=None):
+        check(lib.vkv_enc_step(self.handle, stream, ctypes.byref(plan), window, layer0, n_layers,
+                               q_ptr, k_ptr, v_ptr, out_ptr, n_q_heads or self.n_q_heads, scale,
+                               hip_stream))
+
+    def window_attn(self, stream, layer0, n_layers, segs, key_pos0, q_pos0, n_q, window, q_ptr,
+                    out_ptr, scale, hip_stream=0, n_q_heads=None):
+        arr, n = _segs(segs)
+        check(lib.vkv_window_attn(self.handle, stream, layer0, n_layers, arr, n, key_pos0, q_pos0,
+                                  n_q, window, q_ptr, out_ptr, n_q_heads or self.n_q_heads, scale,
+                                  hip_stream))
+
+
+def q8_0_pack(x_ptr, blocks_ptr, n, hip_stream=0):
+    check(lib.vkv_q8_0_pack(x_ptr, blocks_ptr, n, hip_stream))
+
+
+def q8_0_unpack(blocks_ptr, y_ptr, n, hip_stream=0):
+    check(lib.vkv_q8_0_unpack(blocks_ptr, y_ptr, n, hip_stream))
+
+
+# tags of the synthetic inputs (shared with the oracle's generator)
+TAG_K, TAG_V, TAG_Q = 1, 2, 3
+TAG_EK, TAG_EV, TAG_EQ = 11, 12, 13
+
+
+def synth_rows(dst_ptr, row_len, seed, tag, s0=0, ns=1, s_stride=0, l0=0, nl=1, l_stride=0,
+               p0=0, np_=1, p_stride=0, hip_stream=0):
+    """Rows (s0+i, l0+j, p0+k) at dst + (i*s_stride + j*l_stride + k*p_stride)*row_len.
+    Zero strides default to a packed [s][l][p] layout."""
+    if p_stride == 0:
+        p_stride = 1
+    if l_stride == 0:
+        l_stride = np_ * p_stride
+    if s_stride == 0:
+        s_stride = nl * l_stride
+    check(lib.vkv_synth_rows(dst_ptr, row_len, seed, tag, s0, ns, s_stride, l0, nl, l_stride, p0,
+                             np_, p_stride, hip_stream))
