@@ -6,11 +6,14 @@ ring that is full and wrapping (every step evicts the oldest position), F16 KV,
 32 query / 8 KV heads x 128, one stream.  One step = one token = for every
 layer, append the token's K/V row (f32 -> f16) at pos % 8192 and run the
 single-query GQA attention over all 8192 retained positions, through the
-vkv_decoder_step C entry point (one fused kernel per step).  Inputs (Q, K, V
-for every timed step) are generated on the device before timing.
+vkv_decoder_step C entry point: one decode kernel (append fused in its
+prologue, split-K attention over slot chunks) plus a small kernel merging the
+chunk partials.  Inputs (Q, K, V for every timed step) are generated on the
+device before timing.
 
-Prints one JSON line: tokens/s, the roofline of the decode kernel (algorithmic
-bytes / average kernel time from HIP events on the launch stream), and the CPU
+Prints one JSON line: tokens/s, the roofline of the decode step (algorithmic
+bytes / average step time from HIP events on the launch stream, bracketing
+both kernels of the step, so it understates the decode kernel alone), and the CPU
 baseline (the oracle's threaded restatement of ggml's CPU flash-attention
 step, timed on a bounded sample on this host).
 """
@@ -148,11 +151,32 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB 20 times (scales rocprof "
+                         "FETCH_SIZE/WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n * 4, "launches": 20}), flush=True)
+        return
     if args.gpus != 1:
         print(f"bench.py measures the single-GPU KV step; --gpus {args.gpus} is not supported "
               "(this path has no multi-GPU leg)", file=sys.stderr)
         sys.exit(2)
+
+    traffic = None
+    pmc = os.path.join(ROOT, "profiles", "decode_f16_26x8192_pmc.json")
+    if os.path.exists(pmc):
+        # HBM bytes per decode launch from the committed rocprofv3 FETCH_SIZE /
+        # WRITE_SIZE runs of this same workload (scaled by a plain-copy calibration)
+        with open(pmc) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
 
     total_ms, kern_ms, wall = gpu_leg(args.steps, args.warmup)
     ms_per_step = total_ms / args.steps
@@ -180,8 +204,10 @@ def main():
         "hbm_gbps": round(bytes_step / (ms_per_step * 1e-3) / 1e9, 1),
         "pct_hbm_peak": round(100 * bytes_step / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "k_decode<FmtF16,4,fused-append>", "bytes_per_launch": bytes_step,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": round(traffic) if traffic else None,
+                     "kernel": "k_decode<FmtF16,4,fused append> + k_combine (one step)",
+                     "bytes_per_launch": bytes_step,
                      "avg_launch_ms": round(kern_avg, 5)},
         "wall_s": round(wall, 3),
     }

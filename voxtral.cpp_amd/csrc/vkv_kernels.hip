@@ -58,7 +58,10 @@ __device__ __forceinline__ float quad_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Round half away from zero.  Contraction stays off: the quantizer rounds the
+// product x*id first, exactly like the CPU quantizer.
 __device__ __forceinline__ float round_half_away(float v) {
+#pragma clang fp contract(off)
     float t = truncf(v);
     float r = v - t;
     if (r >= 0.5f) t += 1.0f;
@@ -155,28 +158,31 @@ struct FmtF32 {
 };
 
 // ggml block_q8_0 {fp16 d; int8 qs[32]} (34 bytes).  Element e lives in block
-// e/32 at byte 34*(e/32) + 2 + e%32; every field is 2-byte aligned, so loads
-// and stores use 16-bit accesses.  A block spans the 4 lanes of a quad, so
-// quantization (amax) reduces over the quad: callers keep quads converged.
+// e/32 at byte 34*(e/32) + 2 + e%32.  A lane's 8 quants start 2 bytes into a
+// dword or on a dword boundary; they are read as three aligned dwords and
+// funnel-shifted (every cache allocation carries a 256-byte tail pad so the
+// third dword never leaves it).  Quantization spans the 4 lanes of a quad
+// (amax), so callers keep quads converged.
 struct FmtQ8 {
     struct Frag { uint32_t lo, hi; float d; };
-    struct QFrag { uint32_t lo, hi; float d; };
-    static __device__ __forceinline__ const uint8_t *blk(const uint8_t *row, int e) {
-        return row + (int64_t)(e >> 5) * 34;
-    }
+    struct QFrag { uint32_t w[4]; };   // the query stays f16 (RNE), not quantized
     static __device__ __forceinline__ Frag load(const uint8_t *row, int e) {
-        const uint8_t *b = blk(row, e);
-        const uint16_t *qs = reinterpret_cast<const uint16_t *>(b + 2 + (e & 31));
+        const uint8_t *b = row + (int64_t)(e >> 5) * 34;
         const uint16_t dh = *reinterpret_cast<const uint16_t *>(b);
+        const uintptr_t qa = reinterpret_cast<uintptr_t>(b + 2 + (e & 31));
+        const uint32_t *w = reinterpret_cast<const uint32_t *>(qa & ~(uintptr_t)3);
+        const uint32_t sh = (uint32_t)(qa & 3);   // 0 or 2
+        const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
         Frag f;
-        f.lo = (uint32_t)qs[0] | ((uint32_t)qs[1] << 16);
-        f.hi = (uint32_t)qs[2] | ((uint32_t)qs[3] << 16);
+        f.lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
+        f.hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
         f.d = (float)__builtin_bit_cast(_Float16, dh);
         return f;
     }
     // Quantize 8 values; the quad holding one block cooperates on amax, so
     // every lane of the quad must call this (no early exit before it).
     static __device__ __forceinline__ Frag from_f32(const float *x) {
+#pragma clang fp contract(off)
         float amax = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
@@ -203,13 +209,24 @@ struct FmtQ8 {
             *reinterpret_cast<uint16_t *>(b) = __builtin_bit_cast(uint16_t, (_Float16)f.d);
     }
     static __device__ __forceinline__ QFrag make_q(const float *x) {
-        const Frag f = from_f32(x);
-        return QFrag{f.lo, f.hi, f.d};
+        const FmtF16::Frag h = FmtF16::from_f32(x);
+        return QFrag{{h.w[0], h.w[1], h.w[2], h.w[3]}};
+    }
+    // int8 pair -> exact half2: bias to unsigned, splice under the f16
+    // exponent of 1024 (ulp 1), subtract 1024+128.
+    static __device__ __forceinline__ half2_t i8x2_to_h2(uint32_t biased, uint32_t sel) {
+        const half2_t t = as_h2(__builtin_amdgcn_perm(0x64646464u, biased, sel));
+        const half2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+        return t - off;
     }
     static __device__ __forceinline__ float dot(const Frag &k, const QFrag &q) {
-        int s = __builtin_amdgcn_sdot4((int)k.lo, (int)q.lo, 0, false);
-        s = __builtin_amdgcn_sdot4((int)k.hi, (int)q.hi, s, false);
-        return (float)s * (k.d * q.d);
+        const uint32_t lo = k.lo ^ 0x80808080u, hi = k.hi ^ 0x80808080u;
+        float s = 0.0f;
+        s = __builtin_amdgcn_fdot2(i8x2_to_h2(lo, 0x05010400u), as_h2(q.w[0]), s, false);
+        s = __builtin_amdgcn_fdot2(i8x2_to_h2(lo, 0x05030402u), as_h2(q.w[1]), s, false);
+        s = __builtin_amdgcn_fdot2(i8x2_to_h2(hi, 0x05010400u), as_h2(q.w[2]), s, false);
+        s = __builtin_amdgcn_fdot2(i8x2_to_h2(hi, 0x05030402u), as_h2(q.w[3]), s, false);
+        return s * k.d;
     }
     static __device__ __forceinline__ void to_f32(const Frag &v, float *o) {
 #pragma unroll
@@ -219,6 +236,21 @@ struct FmtQ8 {
         }
     }
 };
+
+// Word-wise select between two fragments (constant indices only, so the
+// fragment arrays stay in registers).
+template <class T>
+__device__ __forceinline__ T select_frag(bool c, const T &a, const T &b) {
+    static_assert(sizeof(T) % 4 == 0, "fragments are whole dwords");
+    uint32_t wa[sizeof(T) / 4], wb[sizeof(T) / 4];
+    __builtin_memcpy(wa, &a, sizeof(T));
+    __builtin_memcpy(wb, &b, sizeof(T));
+#pragma unroll
+    for (unsigned i = 0; i < sizeof(T) / 4; ++i) wa[i] = c ? wa[i] : wb[i];
+    T r;
+    __builtin_memcpy(&r, wa, sizeof(T));
+    return r;
+}
 
 // Convert 8 new f32 elements (called by every lane: Q8 quantization is
 // quad-cooperative) and store them when `ok`.
@@ -277,17 +309,97 @@ __global__ void __launch_bounds__(256) k_gather(const uint8_t *src, int64_t row_
     }
 }
 
+
+// Transposing sum over the 16 lanes of a DPP row: lane c holds 16 partials
+// v[0..15]; on return it holds sum over the row of v[c].  Each step pairs lanes
+// that differ in one bit (row_mirror, row_half_mirror, quad reverse, xor 1):
+// the lane keeps the half of its list selected by that bit and adds the
+// partner's copy of it.  8+4+2+1 exchanges instead of 16x4.
+__device__ __forceinline__ float transpose_sum16(const float *v, int c) {
+    float a8[8], a4[4], a2[2];
+    const bool b3 = c & 8, b2 = c & 4, b1 = c & 2, b0 = c & 1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float keep = b3 ? v[k + 8] : v[k];
+        const float send = b3 ? v[k] : v[k + 8];
+        a8[k] = keep + dpp<0x140>(send);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float keep = b2 ? a8[k + 4] : a8[k];
+        const float send = b2 ? a8[k] : a8[k + 4];
+        a4[k] = keep + dpp<0x141>(send);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const float keep = b1 ? a4[k + 2] : a4[k];
+        const float send = b1 ? a4[k] : a4[k + 2];
+        a2[k] = keep + dpp<0x1B>(send);
+    }
+    const float keep = b0 ? a2[1] : a2[0];
+    const float send = b0 ? a2[0] : a2[1];
+    return keep + dpp<0xB1>(send);
+}
+
+// acc[j][i] += sum_u p[u][j] * v_u[i].  F16: slot pairs (u, u+1) are packed
+// into half2 lanes and accumulated with v_dot2_f32_f16 (f32 accumulation);
+// other formats use f32 FMAs on the dequantised values.
+template <class F>
+__device__ __forceinline__ void pv_accumulate(float (&acc)[4][8], const typename F::Frag (&vf)[4],
+                                              const float4 (&pw)[4]) {
+    float vv[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) F::to_f32(vf[u], vv[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const float pu[4] = {pw[u].x, pw[u].y, pw[u].z, pw[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[j][i] = fmaf(pu[j], vv[u][i], acc[j][i]);
+    }
+}
+
+template <>
+__device__ __forceinline__ void pv_accumulate<FmtF16>(float (&acc)[4][8], const FmtF16::Frag (&vf)[4],
+                                                      const float4 (&pw)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; u += 2) {
+        const float p0[4] = {pw[u].x, pw[u].y, pw[u].z, pw[u].w};
+        const float p1[4] = {pw[u + 1].x, pw[u + 1].y, pw[u + 1].z, pw[u + 1].w};
+        half2_t pp[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            pp[j].x = (_Float16)p0[j];
+            pp[j].y = (_Float16)p1[j];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // (v_u[2i], v_u+1[2i]) and (v_u[2i+1], v_u+1[2i+1])
+            const half2_t lo = as_h2(__builtin_amdgcn_perm(vf[u + 1].w[i], vf[u].w[i], 0x05040100u));
+            const half2_t hi = as_h2(__builtin_amdgcn_perm(vf[u + 1].w[i], vf[u].w[i], 0x07060302u));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[j][2 * i] = __builtin_amdgcn_fdot2(lo, pp[j], acc[j][2 * i], false);
+                acc[j][2 * i + 1] = __builtin_amdgcn_fdot2(hi, pp[j], acc[j][2 * i + 1], false);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Decode attention.  Workgroup = 4 waves on (stream, layer, kv head g, chunk
 // of `chunk` logical slots).  Lane (grp = lane/16, c = lane%16) holds elements
 // [8c, 8c+8) of one slot's head row; a wave covers 4 slots per load, 16 slots
-// per batch (4 loads of K and of V in flight per lane).
+// per batch (4 loads of K and of V in flight per lane), and the 4 query heads
+// of the GQA group share every K/V load.
 // ---------------------------------------------------------------------------
 template <class F, int GQA, bool FUSE>
 __global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
     constexpr int D = 128;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave index as a scalar: loop bounds derived from it stay uniform
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane >> 4;
     const int c = lane & 15;
     const int g = blockIdx.x % a.n_kv_heads;
@@ -314,92 +426,129 @@ __global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
         }
     }
 
-    float m[GQA], l[GQA], acc[GQA][8];
+    static_assert(GQA == 4, "the score transposition maps 4 slots x 4 heads onto 16 lanes");
+    // Running softmax state.  After the score transposition lane c of a group
+    // owns slot-of-batch u = c>>2 and query head j = c&3: m and l are that
+    // head's running max and (partial) sum.  acc[j][i] is the unnormalised
+    // output of head j at dimension 8c+i over this lane group's slots.
+    const int hj = c & 3;
+    const int hu = c >> 2;
+    const uint32_t row_bytes24 = (uint32_t)a.row_bytes;
+    float m = -INFINITY, l = 0.0f;
+    float acc[GQA][8];
 #pragma unroll
-    for (int j = 0; j < GQA; ++j) {
-        m[j] = -INFINITY;
-        l[j] = 0.0f;
+    for (int j = 0; j < GQA; ++j)
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[j][i] = 0.0f;
-    }
+    __shared__ float4 sm_p[4][16];   // per wave: p[slot of batch][head]
 
     const int i_begin = chunk * a.chunk;
     const int i_end = min(i_begin + a.chunk, n_kv);
-    for (int b0 = i_begin + wave * 16; b0 < i_end; b0 += 64) {
-        typename F::Frag kf[4], vf[4];
-        int idx[4];
+    // Software pipeline: the next batch's K/V loads are in flight while the
+    // current batch is reduced.
+    auto load_batch = [&](int b, typename F::Frag (&kf)[4], typename F::Frag (&vf)[4])
+                          __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            idx[u] = b0 + u * 4 + grp;
-            const int slot = idx[u] < i_end ? slot_of(sp, idx[u]) : sp.s0;
-            kf[u] = F::load(kl + (int64_t)slot * a.row_bytes, e);
-            vf[u] = F::load(vl + (int64_t)slot * a.row_bytes, e);
+            // past the chunk end: reload the last valid slot (masked later)
+            const int ix = min(b + u * 4 + grp, i_end - 1);
+            const int slot = slot_of(sp, ix);
+            // slot < 2^24 and row_bytes < 2^24 (host-checked): 24-bit multiply
+            const uint32_t off = __umul24((uint32_t)slot, row_bytes24);
+            kf[u] = F::load(kl + off, e);
+            vf[u] = F::load(vl + off, e);
         }
-        if (FUSE) {
-            // The step's new row is the newest logical index: convert it once,
-            // store it into the ring, and attend with the stored values.
+    };
+    // Software pipeline over two register sets (no copies, so the wave never
+    // waits on the batch it has just requested): batch A is reduced while B's
+    // K/V loads are in flight, then the roles swap.
+    // (always inlined: the fragment arrays must stay in registers)
+    auto process = [&](typename F::Frag (&kf)[4], typename F::Frag (&vf)[4], const int b0)
+                       __attribute__((always_inline)) {
+        // QK partials over this lane's 8 dimensions, then a transposing
+        // reduction over the 16 lanes of the group: lane c ends with the full
+        // score of (slot u = c>>2, head j = c&3).
+        float part[16];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                if (idx[u] == n_kv - 1) {
-                    const int slot = slot_of(sp, idx[u]);
-                    const float *kn = a.k_new + (int64_t)s * a.new_sstride +
-                                      (int64_t)layer * a.new_lstride + e;
-                    const float *vn = a.v_new + (int64_t)s * a.new_sstride +
-                                      (int64_t)layer * a.new_lstride + e;
-                    float xk[8], xv[8];
+        for (int u = 0; u < 4; ++u)
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) { xk[i] = kn[i]; xv[i] = vn[i]; }
-                    uint8_t *krow = a.k_w + base + (int64_t)slot * a.row_bytes;
-                    uint8_t *vrow = a.v_w + base + (int64_t)slot * a.row_bytes;
-                    kf[u] = store_new<F>(krow, e, xk, true);
-                    vf[u] = store_new<F>(vrow, e, xv, true);
-                }
-            }
+            for (int j = 0; j < GQA; ++j) part[u * 4 + j] = F::dot(kf[u], qf[j]);
+        const int my_idx = b0 + hu * 4 + grp;
+        float sc = transpose_sum16(part, c) * a.scale_log2;
+        if (my_idx >= i_end) sc = -INFINITY;
+
+        // batch max of head j: lanes {j, j+4, j+8, j+12} of the row, then groups
+        float bm = fmaxf(sc, dpp<0x124>(sc));
+        bm = fmaxf(bm, dpp<0x128>(bm));
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        // Lazy rescale: the reference max only moves when a head's batch max
+        // exceeds it by more than 2^8, so p <= 256 and rescaling is rare.
+        if (__any(bm > m + 8.0f)) {
+            const float mn = fmaxf(m, bm);
+            const float alpha = mn == -INFINITY ? 1.0f : fast_exp2(m - mn);
+            l *= alpha;
+            float al[GQA];
+            al[0] = dpp<0x00>(alpha);    // quad broadcast of head 0..3's alpha
+            al[1] = dpp<0x55>(alpha);
+            al[2] = dpp<0xAA>(alpha);
+            al[3] = dpp<0xFF>(alpha);
+#pragma unroll
+            for (int j = 0; j < GQA; ++j)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[j][i] *= al[j];
+            m = mn;
         }
-        float sc[4][GQA];
+        const float p = sc == -INFINITY ? 0.0f : fast_exp2(sc - m);
+        l += p;
+        // hand every lane of the group the 4 heads' weights of each of its slots
+        reinterpret_cast<float *>(&sm_p[wave][hu * 4 + grp])[hj] = p;
+        __builtin_amdgcn_wave_barrier();
+        float4 pw[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < 4; ++u) pw[u] = sm_p[wave][u * 4 + grp];
+        __builtin_amdgcn_wave_barrier();
+        pv_accumulate<F>(acc, vf, pw);
+    };
+    if (FUSE) {
+        // The step's new row is the newest logical index n_kv-1.  Lane group 0
+        // of wave 0 in the work group whose chunk holds it converts the f32 row
+        // once and stores it into the ring; after the barrier every wave reads
+        // it back like any other slot.  Other work groups never touch the slot.
+        if (n_kv >= 1 && n_kv - 1 >= i_begin && n_kv - 1 < i_end && wave == 0 && grp == 0) {
+            const int slot = slot_of(sp, n_kv - 1);
+            const float *kn = a.k_new + (int64_t)s * a.new_sstride + (int64_t)layer * a.new_lstride + e;
+            const float *vn = a.v_new + (int64_t)s * a.new_sstride + (int64_t)layer * a.new_lstride + e;
+            float xk[8], xv[8];
 #pragma unroll
-            for (int j = 0; j < GQA; ++j) {
-                const float p = row_sum16(F::dot(kf[u], qf[j]));
-                sc[u][j] = idx[u] < i_end ? p * a.scale_log2 : -INFINITY;
-            }
+            for (int i = 0; i < 8; ++i) { xk[i] = kn[i]; xv[i] = vn[i]; }
+            store_new<F>(a.k_w + base + (int64_t)slot * a.row_bytes, e, xk, true);
+            store_new<F>(a.v_w + base + (int64_t)slot * a.row_bytes, e, xv, true);
         }
-        float vv[4][8];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) F::to_f32(vf[u], vv[u]);
-#pragma unroll
-        for (int j = 0; j < GQA; ++j) {
-            float bm = fmaxf(fmaxf(sc[0][j], sc[1][j]), fmaxf(sc[2][j], sc[3][j]));
-            bm = fmaxf(bm, __shfl_xor(bm, 16));
-            bm = fmaxf(bm, __shfl_xor(bm, 32));
-            const float mn = fmaxf(m[j], bm);
-            if (mn != -INFINITY) {
-                const float alpha = fast_exp2(m[j] - mn);
-                float pu[4], ps = 0.0f;
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    pu[u] = fast_exp2(sc[u][j] - mn);
-                    ps += pu[u];
-                }
-                l[j] = l[j] * alpha + ps;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    float o = acc[j][i] * alpha;
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) o = fmaf(pu[u], vv[u][i], o);
-                    acc[j][i] = o;
-                }
-                m[j] = mn;
-            }
-        }
+        __syncthreads();
     }
 
-    // Merge the 4 lane groups (they share m).
+    // The loop body always handles two batches and the prefetches are
+    // unconditional (indices clamp to the last valid slot, an L2 hit; batches
+    // past the end are fully masked), so the wait counts stay exact.
+    typename F::Frag ka[4], va[4], kb[4], vb[4];
+    int b0 = i_begin + wave * 16;
+    if (b0 < i_end) load_batch(b0, ka, va);
+    for (; b0 < i_end; b0 += 128) {
+        load_batch(b0 + 64, kb, vb);
+        process(ka, va, b0);
+        load_batch(b0 + 128, ka, va);
+        process(kb, vb, b0 + 64);
+    }
+
+    // Merge the 4 lane groups (they share m): every lane of head j sums l
+    // over its row and the groups; acc over the groups.
+    l += dpp<0x124>(l);
+    l += dpp<0x128>(l);
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
 #pragma unroll
     for (int j = 0; j < GQA; ++j) {
-        l[j] += __shfl_xor(l[j], 16);
-        l[j] += __shfl_xor(l[j], 32);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             acc[j][i] += __shfl_xor(acc[j][i], 16);
@@ -412,13 +561,12 @@ __global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
     __shared__ float sm_o[4][GQA][D];
     if (grp == 0) {
 #pragma unroll
-        for (int j = 0; j < GQA; ++j) {
+        for (int j = 0; j < GQA; ++j)
 #pragma unroll
             for (int i = 0; i < 8; ++i) sm_o[wave][j][c * 8 + i] = acc[j][i];
-            if (c == 0) {
-                sm_m[wave][j] = m[j];
-                sm_l[wave][j] = l[j];
-            }
+        if (c < GQA) {
+            sm_m[wave][c] = m;
+            sm_l[wave][c] = l;
         }
     }
     __syncthreads();

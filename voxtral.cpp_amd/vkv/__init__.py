@@ -11,6 +11,14 @@ raises.
 import ctypes
 import os
 
+try:
+    # torch ships its own HIP runtime under the same soname (libamdhip64.so.7);
+    # whichever loads first serves the whole process.  Load torch's first when
+    # it is installed so that torch tensors and this library share one runtime.
+    import torch  # noqa: F401
+except ImportError:
+    pass
+
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libvkv.so")
 
