@@ -21,6 +21,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 
 #include "vkv_internal.h"
 
@@ -727,6 +728,182 @@ __global__ void __launch_bounds__(64) k_window(WindowArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Window attention on the matrix cores (F16 cache): the encoder's 16-query
+// block against its sliding window (src/voxtral.cpp:2201-2284) and the
+// decoder's causal prefill (:2893-2961).  Work group = 4 waves on (layer,
+// kv head g, tile of 16 query rows); a query row is (token, head of the GQA
+// group).  The waves split the window's 16-key blocks round-robin.
+//
+// Per key block, with v_mfma_f32_16x16x16f16:
+//   S^T[key][row] = K[key][:] . Q[row][:]   A = K (keys as M, loaded straight
+//                   from the ring), B = Q^T (registers); the head dimension is
+//                   permuted so each lane reads one contiguous D/4 run of a key.
+//   O^T[d][row]  += V^T[d][key] P^T[key][row]   A = V^T (through a padded LDS
+//                   tile: the one transpose), B = P^T -- exactly S^T's output
+//                   layout, so P never leaves registers and each lane's
+//                   online-softmax rescale is its own row's.
+// ---------------------------------------------------------------------------
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+
+template <int D>
+__global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
+    constexpr int KB = D / 16;          // k-blocks of the QK product, d-tiles of PV
+    constexpr int DL = D / 4;           // contiguous head dims per lane
+    constexpr int VS = 2 * D + 8;       // padded LDS row stride of the V tile (bytes)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lg = lane >> 4;           // lane group 0..3
+    const int lr = lane & 15;
+    const int gqa = a.n_q_heads / a.n_kv_heads;
+    const int g = blockIdx.x % a.n_kv_heads;
+    const int tile = blockIdx.x / a.n_kv_heads;
+    const int layer = blockIdx.y;
+    const int n_rows = a.n_q * gqa;
+    const int n_keys = a.seg.n0 + a.seg.n1;
+    const uint8_t *kl = a.k + (int64_t)layer * a.layer_bytes;
+    const uint8_t *vl = a.v + (int64_t)layer * a.layer_bytes;
+
+    __shared__ __align__(16) uint8_t sm_v[4][16 * VS];   // VS % 8 == 0
+    __shared__ float sm_o[4][16][D + 1];
+    __shared__ float sm_m[4][16], sm_l[4][16];
+
+    // ---- Q^T operand: lane holds row lr, dims [DL*lg, DL*lg + DL) as f16 ----
+    const int row = tile * 16 + lr;
+    const bool row_ok = row < n_rows;
+    const int tok = row_ok ? row / gqa : 0;
+    const int64_t q_abs = a.q_pos0 + tok;
+    half4_t qb[KB];
+    {
+        const float *qp = a.q + (int64_t)layer * a.q_lstride +
+                          ((int64_t)tok * a.n_q_heads + g * gqa + (row_ok ? row % gqa : 0)) * D + DL * lg;
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            const float4 v4 = row_ok ? reinterpret_cast<const float4 *>(qp)[kb] : make_float4(0, 0, 0, 0);
+            qb[kb] = half4_t{(_Float16)v4.x, (_Float16)v4.y, (_Float16)v4.z, (_Float16)v4.w};
+        }
+    }
+
+    // ---- the key range any row of this tile may attend ----
+    const int row0 = tile * 16;
+    const int row1 = min(row0 + 16, n_rows) - 1;
+    const int64_t qa_lo = a.q_pos0 + row0 / gqa;
+    const int64_t qa_hi = a.q_pos0 + row1 / gqa;
+    const int64_t lo = a.window > 0 ? qa_lo - (a.window - 1) : -((int64_t)1 << 62);
+    const int j_lo = (int)max<int64_t>(0, lo - a.key_pos0);
+    const int j_hi = (int)min<int64_t>(n_keys, qa_hi - a.key_pos0 + 1);
+    const int64_t my_lo = a.window > 0 ? q_abs - (a.window - 1) : -((int64_t)1 << 62);
+
+    float m = -INFINITY, l = 0.0f;
+    float4_t o[KB];
+#pragma unroll
+    for (int t = 0; t < KB; ++t) o[t] = float4_t{0, 0, 0, 0};
+
+    for (int jb = j_lo + wave * 16; jb < j_hi; jb += 64) {
+        // K and V of key jb+lr, dims [DL*lg, +DL): one contiguous run per lane
+        const int jk = min(jb + lr, j_hi - 1);
+        const uint32_t off = (uint32_t)slot_of(a.seg, jk) * (uint32_t)a.row_bytes +
+                             (uint32_t)(g * D + DL * lg) * 2u;
+        uint4 kr[DL / 8], vr[DL / 8];
+#pragma unroll
+        for (int t = 0; t < DL / 8; ++t) {
+            kr[t] = reinterpret_cast<const uint4 *>(kl + off)[t];
+            vr[t] = reinterpret_cast<const uint4 *>(vl + off)[t];
+        }
+        // V rows into this wave's LDS tile (row lr, bytes [2*DL*lg, +2*DL));
+        // the padded stride keeps rows 8-byte aligned: 8-byte stores
+#pragma unroll
+        for (int t = 0; t < DL / 8; ++t) {
+            uint2 *dst = reinterpret_cast<uint2 *>(&sm_v[wave][lr * VS + 2 * DL * lg + 16 * t]);
+            dst[0] = make_uint2(vr[t].x, vr[t].y);
+            dst[1] = make_uint2(vr[t].z, vr[t].w);
+        }
+
+        // S^T = K Q^T
+        float4_t st = float4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+            const uint32_t w0 = (&kr[0].x)[2 * kb], w1 = (&kr[0].x)[2 * kb + 1];
+            const half4_t ka = __builtin_bit_cast(half4_t, (uint64_t)w0 | ((uint64_t)w1 << 32));
+            st = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qb[kb], st, 0, 0, 0);
+        }
+        // lane holds keys jb + 4*lg + i (i = 0..3) for row lr
+        float sc[4];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = jb + 4 * lg + i;
+            const int64_t kabs = a.key_pos0 + j;
+            const bool ok = row_ok && j < j_hi && kabs <= q_abs && kabs >= my_lo;
+            sc[i] = ok ? st[i] * a.scale_log2 : -INFINITY;
+            bm = fmaxf(bm, sc[i]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        if (__any(bm > m + 8.0f)) {
+            const float mn = fmaxf(m, bm);
+            const float alpha = mn == -INFINITY ? 1.0f : fast_exp2(m - mn);
+            l *= alpha;
+#pragma unroll
+            for (int t = 0; t < KB; ++t) o[t] *= alpha;
+            m = mn;
+        }
+        half4_t pb;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float p = sc[i] == -INFINITY ? 0.0f : fast_exp2(sc[i] - m);
+            l += p;
+            pb[i] = (_Float16)p;
+        }
+        // V^T operand: lane reads V[key 4*lg+i][d = 16*t + lr] from the tile
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int t = 0; t < KB; ++t) {
+            half4_t va;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                va[i] = *reinterpret_cast<const _Float16 *>(&sm_v[wave][(4 * lg + i) * VS + 2 * (16 * t + lr)]);
+            o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[t], 0, 0, 0);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+
+    // row sums over the 4 lane groups (they share m)
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    // O^T tile t: lane holds d = 16*t + 4*lg + i of row lr
+#pragma unroll
+    for (int t = 0; t < KB; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sm_o[wave][lr][16 * t + 4 * lg + i] = o[t][i];
+    if (lg == 0) {
+        sm_m[wave][lr] = m;
+        sm_l[wave][lr] = l;
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < 16 * D; t += 256) {
+        const int r = t / D;
+        const int d = t % D;
+        const int rr = tile * 16 + r;
+        if (rr >= n_rows) continue;
+        const float M = fmaxf(fmaxf(sm_m[0][r], sm_m[1][r]), fmaxf(sm_m[2][r], sm_m[3][r]));
+        float O = 0.0f, L = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float f = fast_exp2(sm_m[w][r] - M);
+                O = fmaf(sm_o[w][r][d], f, O);
+                L = fmaf(sm_l[w][r], f, L);
+            }
+        }
+        const int tk = rr / gqa;
+        float *op = a.out + (int64_t)layer * a.q_lstride +
+                    ((int64_t)tk * a.n_q_heads + g * gqa + rr % gqa) * D + d;
+        *op = L > 0.0f ? O / L : 0.0f;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // q8_0 pack / unpack of flat f32 arrays (n % 32 == 0); 8 elements per lane.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) k_q8_pack(const float *x, uint8_t *blocks, int64_t n) {
@@ -814,6 +991,16 @@ inline unsigned grid_for(int64_t work, int64_t per_block, int64_t cap = 1 << 20)
 // ---------------------------------------------------------------------------
 // Launchers.
 // ---------------------------------------------------------------------------
+// VKV_WINDOW_VALU=1 routes F16 window attention to the scalar-ALU kernel
+// instead of the matrix-core tile (cross-check and A/B measurement).
+static bool window_valu_forced() {
+    static const bool v = [] {
+        const char *e = getenv("VKV_WINDOW_VALU");
+        return e && e[0] == '1';
+    }();
+    return v;
+}
+
 hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st) {
     const int64_t threads = ((int64_t)a.n_rows * a.kv_dim + 7) / 8;
     dim3 grid(grid_for(threads, 256, INT32_MAX), (unsigned)n_layers, 2);
@@ -866,6 +1053,14 @@ hipError_t launch_combine(const CombineArgs &a, int n_streams, hipStream_t st) {
 }
 
 hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st) {
+    if (dtype == VKV_DTYPE_F16 && !window_valu_forced() && (a.head_dim == 64 || a.head_dim == 128)) {
+        const int gqa = a.n_q_heads / a.n_kv_heads;
+        const int tiles = (a.n_q * gqa + 15) / 16;
+        dim3 g2((unsigned)(tiles * a.n_kv_heads), (unsigned)a.n_layers);
+        if (a.head_dim == 64) hipLaunchKernelGGL(k_window_mfma<64>, g2, dim3(256), 0, st, a);
+        else hipLaunchKernelGGL(k_window_mfma<128>, g2, dim3(256), 0, st, a);
+        return hipGetLastError();
+    }
     dim3 grid((unsigned)(a.n_q * a.n_q_heads), (unsigned)a.n_layers);
     switch (dtype) {
     case VKV_DTYPE_F16: hipLaunchKernelGGL(k_window<FmtF16>, grid, dim3(64), 0, st, a); break;
