@@ -105,6 +105,8 @@ struct FmtF16 {
         Frag f = from_f32(x);
         return QFrag{{f.w[0], f.w[1], f.w[2], f.w[3]}};
     }
+    using KPrep = Frag;
+    static __device__ __forceinline__ const Frag &prep(const Frag &k) { return k; }
     static __device__ __forceinline__ float dot(const Frag &k, const QFrag &q) {
         float s = 0.0f;
 #pragma unroll
@@ -146,6 +148,8 @@ struct FmtF32 {
         for (int i = 0; i < 8; ++i) f.x[i] = x[i];
         return f;
     }
+    using KPrep = Frag;
+    static __device__ __forceinline__ const Frag &prep(const Frag &k) { return k; }
     static __device__ __forceinline__ float dot(const Frag &k, const QFrag &q) {
         float s = 0.0f;
 #pragma unroll
@@ -167,12 +171,15 @@ struct FmtF32 {
 struct FmtQ8 {
     struct Frag { uint32_t lo, hi; float d; };
     struct QFrag { uint32_t w[4]; };   // the query stays f16 (RNE), not quantized
+    // Rows start 4-byte aligned (row_bytes = 34 * kv_dim/32 with kv_dim % 64
+    // == 0 is a multiple of 4); offsets stay integers so the loads keep the
+    // global address space.
     static __device__ __forceinline__ Frag load(const uint8_t *row, int e) {
-        const uint8_t *b = row + (int64_t)(e >> 5) * 34;
-        const uint16_t dh = *reinterpret_cast<const uint16_t *>(b);
-        const uintptr_t qa = reinterpret_cast<uintptr_t>(b + 2 + (e & 31));
-        const uint32_t *w = reinterpret_cast<const uint32_t *>(qa & ~(uintptr_t)3);
-        const uint32_t sh = (uint32_t)(qa & 3);   // 0 or 2
+        const int bo = (e >> 5) * 34;
+        const int qo = bo + 2 + (e & 31);
+        const uint32_t sh = (uint32_t)(qo & 3);   // 0 or 2
+        const uint16_t dh = *reinterpret_cast<const uint16_t *>(row + bo);
+        const uint32_t *w = reinterpret_cast<const uint32_t *>(row + (qo - (int)sh));
         const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
         Frag f;
         f.lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
@@ -220,13 +227,22 @@ struct FmtQ8 {
         const half2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
         return t - off;
     }
-    static __device__ __forceinline__ float dot(const Frag &k, const QFrag &q) {
+    // K dequantised once per slot: 8 quants as exact half2 pairs + scale.
+    struct KPrep { uint32_t w[4]; float d; };
+    static __device__ __forceinline__ KPrep prep(const Frag &k) {
         const uint32_t lo = k.lo ^ 0x80808080u, hi = k.hi ^ 0x80808080u;
+        KPrep r;
+        r.w[0] = as_u32(i8x2_to_h2(lo, 0x05010400u));
+        r.w[1] = as_u32(i8x2_to_h2(lo, 0x05030402u));
+        r.w[2] = as_u32(i8x2_to_h2(hi, 0x05010400u));
+        r.w[3] = as_u32(i8x2_to_h2(hi, 0x05030402u));
+        r.d = k.d;
+        return r;
+    }
+    static __device__ __forceinline__ float dot(const KPrep &k, const QFrag &q) {
         float s = 0.0f;
-        s = __builtin_amdgcn_fdot2(i8x2_to_h2(lo, 0x05010400u), as_h2(q.w[0]), s, false);
-        s = __builtin_amdgcn_fdot2(i8x2_to_h2(lo, 0x05030402u), as_h2(q.w[1]), s, false);
-        s = __builtin_amdgcn_fdot2(i8x2_to_h2(hi, 0x05010400u), as_h2(q.w[2]), s, false);
-        s = __builtin_amdgcn_fdot2(i8x2_to_h2(hi, 0x05030402u), as_h2(q.w[3]), s, false);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_fdot2(as_h2(k.w[i]), as_h2(q.w[i]), s, false);
         return s * k.d;
     }
     static __device__ __forceinline__ void to_f32(const Frag &v, float *o) {
@@ -388,6 +404,43 @@ __device__ __forceinline__ void pv_accumulate<FmtF16>(float (&acc)[4][8], const 
     }
 }
 
+// q8_0: slot pairs (u, u+1) are spliced byte-wise into biased half2 pairs
+// (1024 + 128 + q, exact) and the block scale is folded into the weights:
+// acc += (p_u d_u, p_u+1 d_u+1) . (q_u - 0, q_u+1 - 0) with f32 accumulation.
+template <>
+__device__ __forceinline__ void pv_accumulate<FmtQ8>(float (&acc)[4][8], const FmtQ8::Frag (&vf)[4],
+                                                     const float4 (&pw)[4]) {
+    const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+#pragma unroll
+    for (int u = 0; u < 4; u += 2) {
+        const float p0[4] = {pw[u].x, pw[u].y, pw[u].z, pw[u].w};
+        const float p1[4] = {pw[u + 1].x, pw[u + 1].y, pw[u + 1].z, pw[u + 1].w};
+        half2_t pp[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            pp[j].x = (_Float16)(p0[j] * vf[u].d);
+            pp[j].y = (_Float16)(p1[j] * vf[u + 1].d);
+        }
+        const uint32_t x0[2] = {vf[u].lo ^ 0x80808080u, vf[u].hi ^ 0x80808080u};
+        const uint32_t x1[2] = {vf[u + 1].lo ^ 0x80808080u, vf[u + 1].hi ^ 0x80808080u};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            // A = (u.b0, u.b1, u1.b0, u1.b1), B = (u.b2, u.b3, u1.b2, u1.b3)
+            const uint32_t A = __builtin_amdgcn_perm(x1[h], x0[h], 0x05040100u);
+            const uint32_t B = __builtin_amdgcn_perm(x1[h], x0[h], 0x07060302u);
+            const uint32_t w[4] = {(A & 0x00FF00FFu) | 0x64006400u, ((A >> 8) & 0x00FF00FFu) | 0x64006400u,
+                                   (B & 0x00FF00FFu) | 0x64006400u, ((B >> 8) & 0x00FF00FFu) | 0x64006400u};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const half2_t v2 = as_h2(w[t]) - bias;
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[j][4 * h + t] = __builtin_amdgcn_fdot2(v2, pp[j], acc[j][4 * h + t], false);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Decode attention.  Workgroup = 4 waves on (stream, layer, kv head g, chunk
 // of `chunk` logical slots).  Lane (grp = lane/16, c = lane%16) holds elements
@@ -471,9 +524,11 @@ __global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
         // score of (slot u = c>>2, head j = c&3).
         float part[16];
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < 4; ++u) {
+            const typename F::KPrep kp = F::prep(kf[u]);
 #pragma unroll
-            for (int j = 0; j < GQA; ++j) part[u * 4 + j] = F::dot(kf[u], qf[j]);
+            for (int j = 0; j < GQA; ++j) part[u * 4 + j] = F::dot(kp, qf[j]);
+        }
         const int my_idx = b0 + hu * 4 + grp;
         float sc = transpose_sum16(part, c) * a.scale_log2;
         if (my_idx >= i_end) sc = -INFINITY;
