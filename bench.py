@@ -1,21 +1,29 @@
 #!/usr/bin/env python3
-"""Decoder KV-cache step benchmark on one MI355X.
+"""KV-cache hot-path benchmark on one MI355X.
 
-Workload: the longform streaming decoder -- 26 layers, an 8192-slot sliding
-ring that is full and wrapping (every step evicts the oldest position), F16 KV,
-32 query / 8 KV heads x 128, one stream.  One step = one token = for every
-layer, append the token's K/V row (f32 -> f16) at pos % 8192 and run the
-single-query GQA attention over all 8192 retained positions, through the
-vkv_decoder_step C entry point: one decode kernel (append fused in its
-prologue, split-K attention over slot chunks) plus a small kernel merging the
-chunk partials.  Inputs (Q, K, V for every timed step) are generated on the
-device before timing.
+Default workload (the headline line): the longform streaming decoder -- 26
+layers, an 8192-slot sliding ring that is full and wrapping (every step evicts
+the oldest position), F16 KV, 32 query / 8 KV heads x 128, one stream.  One
+step = one token = for every layer, append the token's K/V row (f32 -> f16) at
+pos % 8192 and run the single-query GQA attention over all 8192 retained
+positions, through the vkv_decoder_step C entry point: one k_decode launch per
+step (append fused in its prologue; one work group per (layer, kv head) owns
+the whole window, so there are no split partials to merge).  Inputs (Q, K, V
+for every timed step) are generated on the device before timing.
 
-Prints one JSON line: tokens/s, the roofline of the decode step (algorithmic
-bytes / average step time from HIP events on the launch stream, bracketing
-both kernels of the step, so it understates the decode kernel alone), and the CPU
-baseline (the oracle's threaded restatement of ggml's CPU flash-attention
-step, timed on a bounded sample on this host).
+Other workloads (--workload), reported on the same contract:
+  q8_0_batch8  the same decoder shape with q8_0 K/V (quantize-on-append,
+               dequantize-in-register attention), 8 independent streams per
+               step; tokens/s counts all 8 streams.
+  encoder_f16  the encoder's streaming window: 32 layers, 32 heads x 64, an
+               878-slot ring, window 750, 16 new frames per chunk appended and
+               attended as a 16-query block (MFMA tile); frames/s.
+
+Prints one JSON line: throughput, the roofline of the step (algorithmic bytes /
+average step time from HIP events on the launch stream), the HBM traffic from
+the committed rocprofv3 counter runs, and the CPU baseline (the oracle's
+threaded restatement of ggml's CPU flash-attention step, timed on a bounded
+sample on this host; decode workloads only).
 """
 import argparse
 import json
@@ -29,56 +37,47 @@ sys.path.insert(0, ROOT)
 
 LAYERS, CAP, KVH, HD, QH = 26, 8192, 8, 128, 32
 KV_DIM, Q_DIM = KVH * HD, QH * HD
+E_LAYERS, E_CAP, E_HEADS, E_HD, E_WIN, E_CHUNK = 32, 878, 32, 64, 750, 16
+E_DIM = E_HEADS * E_HD
 SEED = 20261201
 HBM_PEAK_GBPS = 8000.0
+METRIC = "decode attn+KV-append tokens/s and achieved HBM GB/s (% of peak) at 8192 window"
+
+# F16 = 1, Q8_0 = 8 (ggml_type numbering, as in include/vkv.h)
+WORKLOADS = {
+    "longform_f16": dict(dtype=1, dtype_name="f16", streams=1,
+                         pmc="decode_f16_26x8192_pmc.json"),
+    "q8_0_batch8": dict(dtype=8, dtype_name="q8_0", streams=8,
+                        pmc="decode_q8_0_8x26x8192_pmc.json"),
+    "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
+                        pmc="encoder_f16_32x750_pmc.json"),
+}
 
 
-def algorithmic_bytes_per_step(n_valid, elem_bytes):
-    """K+V read of the window, new K/V f32 read, appended row write, Q read,
-    output write -- per layer, times the layer count."""
-    per_layer = (n_valid * 2 * KV_DIM * elem_bytes + 2 * KV_DIM * 4 + 2 * KV_DIM * elem_bytes +
-                 Q_DIM * 4 + Q_DIM * 4)
-    return LAYERS * per_layer
+def elem_bytes(dtype):
+    return 2.0 if dtype == 1 else 34.0 / 32.0
 
 
-def gpu_leg(steps, warmup):
+def decode_bytes_per_stream_token(n_valid, dtype):
+    """Per layer: K+V read of the window, new K/V f32 read, appended row write,
+    Q read, output write -- times the layer count."""
+    e = elem_bytes(dtype)
+    per_layer = (n_valid * 2 * KV_DIM * e + 2 * KV_DIM * 4 + 2 * KV_DIM * e + Q_DIM * 4 +
+                 Q_DIM * 4)
+    return int(LAYERS * per_layer)
+
+
+def encoder_bytes_per_chunk(n_keys):
+    """Per layer: K+V read of the window keys, new K/V f32 read, appended rows
+    (f16) write, Q read, output write -- times the layer count."""
+    P = E_CHUNK
+    per_layer = (n_keys * 2 * E_DIM * 2 + P * E_DIM * 4 * 2 + P * E_DIM * 2 * 2 + P * E_DIM * 4 +
+                 P * E_DIM * 4)
+    return E_LAYERS * per_layer
+
+
+def timed_loop(step, steps, warmup, st):
     import torch
-    import vkv
-
-    st = torch.cuda.current_stream()
-    sp = st.cuda_stream
-    cache = vkv.Cache(n_streams=1, n_layers=LAYERS, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
-                      n_q_heads=QH, dtype=vkv.F16)
-    ring = vkv.new_ring(CAP)
-    # fill the ring: positions [0, 8192) through the planned append path
-    plan = vkv.decoder_plan(ring, 0, CAP)
-    k0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
-    v0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
-    vkv.synth_rows(k0.data_ptr(), KV_DIM, SEED, vkv.TAG_K, nl=LAYERS, p0=0, np_=CAP, hip_stream=sp)
-    vkv.synth_rows(v0.data_ptr(), KV_DIM, SEED, vkv.TAG_V, nl=LAYERS, p0=0, np_=CAP, hip_stream=sp)
-    cache.append(0, 0, LAYERS, vkv.plan_segs(plan.write_seg, plan.write_nseg), k0.data_ptr(),
-                 v0.data_ptr(), hip_stream=sp)
-    vkv.decoder_commit(ring, plan)
-    del k0, v0
-    # resident per-step inputs, [step][layer][...]
-    T = warmup + steps
-    q = torch.empty(T, LAYERS, Q_DIM, device="cuda")
-    k = torch.empty(T, LAYERS, KV_DIM, device="cuda")
-    v = torch.empty(T, LAYERS, KV_DIM, device="cuda")
-    for t, tag, n in ((q, vkv.TAG_Q, Q_DIM), (k, vkv.TAG_K, KV_DIM), (v, vkv.TAG_V, KV_DIM)):
-        vkv.synth_rows(t.data_ptr(), n, SEED, tag, nl=LAYERS, l_stride=1, p0=CAP, np_=T,
-                       p_stride=LAYERS, hip_stream=sp)
-    out = torch.empty(T, LAYERS, Q_DIM, device="cuda")
-    rings = (vkv.Ring * 1)(ring)
-    scale = 1.0 / (HD ** 0.5)
-    pos = CAP
-
-    def step(i):
-        nonlocal pos
-        cache.decoder_step(0, rings, [pos], 0, LAYERS, q[i].data_ptr(), k[i].data_ptr(),
-                           v[i].data_ptr(), out[i].data_ptr(), scale, hip_stream=sp)
-        pos += 1
-
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -96,15 +95,96 @@ def gpu_leg(steps, warmup):
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_start.elapsed_time(t_end)
-    kern_ms = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(steps)]
-    ring_after = rings[0]
-    assert ring_after.used == CAP and ring_after.next_absolute_position == CAP + T
+    step_ms = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(steps)]
+    return total_ms, step_ms, wall
+
+
+def gpu_decode(dtype, ns, steps, warmup):
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    cache = vkv.Cache(n_streams=ns, n_layers=LAYERS, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
+                      n_q_heads=QH, dtype=dtype)
+    rings = (vkv.Ring * ns)(*[vkv.new_ring(CAP) for _ in range(ns)])
+    # fill every ring: positions [0, 8192) through the planned append path
+    k0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
+    v0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
+    for s in range(ns):
+        plan = vkv.decoder_plan(rings[s], 0, CAP)
+        vkv.synth_rows(k0.data_ptr(), KV_DIM, SEED, vkv.TAG_K, s0=s, nl=LAYERS, p0=0, np_=CAP,
+                       hip_stream=sp)
+        vkv.synth_rows(v0.data_ptr(), KV_DIM, SEED, vkv.TAG_V, s0=s, nl=LAYERS, p0=0, np_=CAP,
+                       hip_stream=sp)
+        cache.append(s, 0, LAYERS, vkv.plan_segs(plan.write_seg, plan.write_nseg), k0.data_ptr(),
+                     v0.data_ptr(), hip_stream=sp)
+        vkv.decoder_commit(rings[s], plan)
+    torch.cuda.synchronize()
+    del k0, v0
+    # resident per-step inputs, [step][stream][layer][...]
+    T = warmup + steps
+    q = torch.empty(T, ns, LAYERS, Q_DIM, device="cuda")
+    k = torch.empty(T, ns, LAYERS, KV_DIM, device="cuda")
+    v = torch.empty(T, ns, LAYERS, KV_DIM, device="cuda")
+    for t, tag, n in ((q, vkv.TAG_Q, Q_DIM), (k, vkv.TAG_K, KV_DIM), (v, vkv.TAG_V, KV_DIM)):
+        vkv.synth_rows(t.data_ptr(), n, SEED, tag, s0=0, ns=ns, s_stride=LAYERS, nl=LAYERS,
+                       l_stride=1, p0=CAP, np_=T, p_stride=ns * LAYERS, hip_stream=sp)
+    out = torch.empty(T, ns, LAYERS, Q_DIM, device="cuda")
+    scale = 1.0 / (HD ** 0.5)
+    pos = [CAP]
+
+    def step(i):
+        cache.decoder_step(0, rings, [pos[0]] * ns, 0, LAYERS, q[i].data_ptr(), k[i].data_ptr(),
+                           v[i].data_ptr(), out[i].data_ptr(), scale, hip_stream=sp)
+        pos[0] += 1
+
+    total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
+    for s in range(ns):
+        assert rings[s].used == CAP and rings[s].next_absolute_position == CAP + T
     assert bool(torch.isfinite(out).all())
     cache.close()
-    return total_ms, kern_ms, wall
+    return total_ms, step_ms, wall
 
 
-def cpu_leg(target_seconds):
+def gpu_encoder(steps, warmup):
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    cache = vkv.Cache(n_streams=1, n_layers=E_LAYERS, capacity=E_CAP, n_kv_heads=E_HEADS,
+                      head_dim=E_HD, n_q_heads=E_HEADS, dtype=vkv.F16)
+    # chunks from frame 0; the window is full (765 keys) from frame 752 on
+    first = (E_WIN + E_CHUNK - 1) // E_CHUNK + 1
+    T = first + warmup + steps
+    rows = E_LAYERS * E_CHUNK * E_DIM
+    q = torch.empty(T, rows, device="cuda")
+    k = torch.empty(T, rows, device="cuda")
+    v = torch.empty(T, rows, device="cuda")
+    for t, tag in ((q, vkv.TAG_EQ), (k, vkv.TAG_EK), (v, vkv.TAG_EV)):
+        # [chunk][layer][frame][dim], one chunk of 16 frames at a time
+        for c in range(T):
+            vkv.synth_rows(t[c].data_ptr(), E_DIM, SEED, tag, nl=E_LAYERS, p0=c * E_CHUNK,
+                           np_=E_CHUNK, hip_stream=sp)
+    out = torch.empty(E_LAYERS, E_CHUNK, E_DIM, device="cuda")
+    plans = [vkv.enc_plan(c * E_CHUNK, E_CHUNK, E_CAP, E_WIN) for c in range(T)]
+
+    def chunk(c):
+        cache.enc_step(0, plans[c], E_WIN, 0, E_LAYERS, q[c].data_ptr(), k[c].data_ptr(),
+                       v[c].data_ptr(), out.data_ptr(), 1.0 / (E_HD ** 0.5), hip_stream=sp)
+
+    for c in range(first):
+        chunk(c)
+    total_ms, step_ms, wall = timed_loop(lambda i: chunk(first + i), steps, warmup, st)
+    n_keys = plans[first].win_end - plans[first].win_start
+    assert n_keys == E_WIN + E_CHUNK - 1
+    assert bool(torch.isfinite(out).all())
+    cache.close()
+    return total_ms, step_ms, wall, n_keys
+
+
+def cpu_leg(dtype, target_seconds):
     """The oracle's threaded ggml-CPU restatement of the same step (append +
     attention over 8192 positions, 26 layers) on a bounded number of tokens."""
     from concurrent.futures import ThreadPoolExecutor
@@ -114,7 +194,7 @@ def cpu_leg(target_seconds):
     import oracle
 
     threads = min(os.cpu_count() or 1, 16)
-    rb = oracle.row_bytes(oracle.F16, KV_DIM)
+    rb = oracle.row_bytes(dtype, KV_DIM)
     layer_bytes = rb * CAP
     kimg = np.empty(LAYERS * layer_bytes, np.uint8)
     vimg = np.empty(LAYERS * layer_bytes, np.uint8)
@@ -122,7 +202,7 @@ def cpu_leg(target_seconds):
     def fill(job):
         img, tag, l = job
         img[l * layer_bytes:(l + 1) * layer_bytes] = oracle.expected_layer(
-            oracle.F16, CAP, CAP, KV_DIM, CAP, SEED, tag, 0, l)
+            dtype, CAP, CAP, KV_DIM, CAP, SEED, tag, 0, l)
 
     with ThreadPoolExecutor(threads) as pool:
         list(pool.map(fill, [(img, tag, l) for img, tag in ((kimg, oracle.TAG_K), (vimg, oracle.TAG_V))
@@ -134,14 +214,26 @@ def cpu_leg(target_seconds):
         qs = np.stack([oracle.synth_row(SEED, oracle.TAG_Q, 0, l, pos, Q_DIM) for l in range(LAYERS)])
         ks = np.stack([oracle.synth_row(SEED, oracle.TAG_K, 0, l, pos, KV_DIM) for l in range(LAYERS)])
         vs = np.stack([oracle.synth_row(SEED, oracle.TAG_V, 0, l, pos, KV_DIM) for l in range(LAYERS)])
-        dt, _ = oracle.decode_step_mimic_mt(oracle.F16, kimg, vimg, layer_bytes, rb, LAYERS, CAP, qs,
+        dt, _ = oracle.decode_step_mimic_mt(dtype, kimg, vimg, layer_bytes, rb, LAYERS, CAP, qs,
                                             QH, KVH, HD, scale, threads, ks, vs, pos % CAP)
         secs += dt
         n += 1
+    name = "f16" if dtype == 1 else "q8_0"
     return {"value": n / secs, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps (26 layers, 8192-position window, f16 KV) of the oracle's "
-                      f"restatement of ggml's CPU flash-attention step, {threads} threads, "
-                      f"{secs:.1f} s"}
+            "sample": f"{n} decode steps (26 layers, 8192-position window, {name} KV, 1 stream) "
+                      f"of the oracle's restatement of ggml's CPU flash-attention step, "
+                      f"{threads} threads, {secs:.1f} s"}
+
+
+def load_traffic(name):
+    pmc = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(pmc):
+        return None
+    # HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    # FETCH_SIZE / WRITE_SIZE runs of this same workload (scaled by a
+    # plain-copy calibration)
+    with open(pmc) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
 
 
 def main():
@@ -149,6 +241,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="longform_f16")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -170,23 +263,38 @@ def main():
               "(this path has no multi-GPU leg)", file=sys.stderr)
         sys.exit(2)
 
-    traffic = None
-    pmc = os.path.join(ROOT, "profiles", "decode_f16_26x8192_pmc.json")
-    if os.path.exists(pmc):
-        # HBM bytes per decode launch from the committed rocprofv3 FETCH_SIZE /
-        # WRITE_SIZE runs of this same workload (scaled by a plain-copy calibration)
-        with open(pmc) as f:
-            traffic = json.load(f).get("traffic_bytes_per_launch")
-
-    total_ms, kern_ms, wall = gpu_leg(args.steps, args.warmup)
+    wl = WORKLOADS[args.workload]
+    traffic = load_traffic(wl["pmc"])
+    if args.workload == "encoder_f16":
+        total_ms, step_ms, wall, n_keys = gpu_encoder(args.steps, args.warmup)
+        bytes_step = encoder_bytes_per_chunk(n_keys)
+        units_per_step = E_CHUNK
+        res = {"metric": "encoder sliding-window attention + ring append frames/s at window 750",
+               "unit": "frames/s"}
+        config = {"workload": "encoder streaming window: 32 layers, 32 heads x 64, 878-slot ring "
+                              "(f16), window 750, 16 new frames appended and attended per chunk "
+                              "as a 16-query block",
+                  "layers": E_LAYERS, "window": E_WIN, "heads": E_HEADS, "head_dim": E_HD,
+                  "ring": E_CAP, "frames_per_chunk": E_CHUNK, "keys_per_query_block": n_keys}
+        kernel = "k_window_mfma<64> + k_append<FmtF16> (one chunk)"
+    else:
+        ns = wl["streams"]
+        total_ms, step_ms, wall = gpu_decode(wl["dtype"], ns, args.steps, args.warmup)
+        bytes_step = ns * decode_bytes_per_stream_token(CAP, wl["dtype"])
+        units_per_step = ns
+        res = {"metric": METRIC, "unit": "tokens/s"}
+        config = {"workload": f"decoder KV step: 26 layers, 8192-slot ring full and wrapping, "
+                              f"{wl['dtype_name']} KV, 32 q / 8 kv heads x 128, {ns} stream"
+                              f"{'s' if ns > 1 else ''}, append + 1-query attention per layer",
+                  "layers": LAYERS, "window": CAP, "kv_heads": KVH, "q_heads": QH,
+                  "head_dim": HD, "streams": ns}
+        fmt = "FmtF16" if wl["dtype"] == 1 else "FmtQ8"
+        kernel = f"k_decode<{fmt}> (append fused; one pass per (stream, layer, kv head))"
     ms_per_step = total_ms / args.steps
-    kern_avg = sum(kern_ms) / len(kern_ms)
-    bytes_step = algorithmic_bytes_per_step(CAP, 2)
-    achieved = bytes_step / (kern_avg * 1e-3) / 1e9
-    res = {
-        "metric": "decode attn+KV-append tokens/s and achieved HBM GB/s (% of peak) at 8192 window",
-        "value": round(args.steps / (total_ms * 1e-3), 2),
-        "unit": "tokens/s",
+    step_avg = sum(step_ms) / len(step_ms)
+    achieved = bytes_step / (step_avg * 1e-3) / 1e9
+    res.update({
+        "value": round(units_per_step * args.steps / (total_ms * 1e-3), 2),
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -194,25 +302,21 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": wl["dtype_name"],
         "data": "synthetic (seeded integer Irwin-Hall N(0,1) Q/K/V, generated on device)",
-        "config": {"workload": "decoder KV step: 26 layers, 8192-slot ring full and wrapping, "
-                               "f16 KV, 32 q / 8 kv heads x 128, 1 stream, append + 1-query "
-                               "attention per layer",
-                   "layers": LAYERS, "window": CAP, "kv_heads": KVH, "q_heads": QH,
-                   "head_dim": HD, "streams": 1},
+        "config": config,
         "hbm_gbps": round(bytes_step / (ms_per_step * 1e-3) / 1e9, 1),
         "pct_hbm_peak": round(100 * bytes_step / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": round(traffic) if traffic else None,
-                     "kernel": "k_decode<FmtF16,4,fused append> + k_combine (one step)",
+                     "kernel": kernel,
                      "bytes_per_launch": bytes_step,
-                     "avg_launch_ms": round(kern_avg, 5)},
+                     "avg_launch_ms": round(step_avg, 5)},
         "wall_s": round(wall, 3),
-    }
-    if not args.no_cpu:
-        res["cpu_baseline"] = cpu_leg(args.cpu_seconds)
+    })
+    if not args.no_cpu and args.workload != "encoder_f16":
+        res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds)
     print(json.dumps(res), flush=True)
 
 

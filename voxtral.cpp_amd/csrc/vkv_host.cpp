@@ -34,7 +34,7 @@ struct vkv_cache {
     float *part_o = nullptr;
     float *part_ml = nullptr;
     int64_t part_heads_budget = 0;   // capacity of part_ml in (head, chunk) units
-    int32_t *counters = nullptr;     // [stream][layer][kv head] arrival counters (self-resetting)
+    int32_t n_cus = 256;             // compute units of the cache's device
 };
 
 namespace {
@@ -184,36 +184,58 @@ vkv_status do_append(vkv_cache *c, int32_t stream, int32_t layer0, int32_t n_lay
     return VKV_STATUS_OK;
 }
 
-// Split-K merge strategy.  Default: a second, tiny kernel merges the chunk
-// partials.  VKV_FUSED_COMBINE=1 instead lets the last work group of each
-// (stream, layer, kv head) merge them in the decode kernel, which costs every
-// work group a device-scope release fence (an L2 write-back on its XCD).
-bool split_combine() {
-    static const bool v = [] {
-        const char *e = std::getenv("VKV_FUSED_COMBINE");
-        return !(e && e[0] == '1');
-    }();
-    return v;
+// VKV_DECODE_CHUNK: fixed slots per decode work group (multiple of 64);
+// unset = automatic.  VKV_DECODE_WAVES: waves per decode work group (4, 8 or
+// 16); unset = automatic.
+int32_t env_int(const char *name) {
+    const char *e = std::getenv(name);
+    return e ? (int32_t)std::strtol(e, nullptr, 10) : 0;
 }
 
-// VKV_DECODE_CHUNK: fixed slots per decode work group (multiple of 64);
-// unset = automatic.
 int32_t forced_chunk() {
     static const int32_t v = [] {
-        const char *e = std::getenv("VKV_DECODE_CHUNK");
-        const int32_t c = e ? (int32_t)std::strtol(e, nullptr, 10) : 0;
+        const int32_t c = env_int("VKV_DECODE_CHUNK");
         return (c >= 64 && c % 64 == 0) ? c : 0;
     }();
     return v;
 }
 
-// Chunk size (logical slots per work group) for decode attention: the largest
-// of 1024..64 that still gives >= 1536 work groups (about two waves of work
-// groups over 256 CUs at 3 per CU), within the workspace.  Larger chunks
-// amortise the per-work-group prologue and partial merge; measured on MI355X
-// at 26 layers x 8192 slots, 1024 beats 256 by ~7%.
+int32_t forced_waves() {
+    static const int32_t v = [] {
+        const int32_t w = env_int("VKV_DECODE_WAVES");
+        return (w == 4 || w == 8) ? w : 0;
+    }();
+    return v;
+}
+
+// VKV_DECODE_STAGES: K/V batches in flight per wave (2..4 with 4 waves, 2..3
+// with 8); unset = automatic.
+int32_t forced_stages() {
+    static const int32_t v = [] {
+        const int32_t n = env_int("VKV_DECODE_STAGES");
+        return (n >= 2 && n <= 4) ? n : 0;
+    }();
+    return v;
+}
+
+// Chunk size (logical slots per work group) for decode attention.
+//
+// One pass: when the (stream, layer, kv head) units number between 3/4 of the
+// CUs and the CUs, one work group per unit owns the whole window (no split,
+// no merge kernel) and each lands on a CU of its own.  Measured on MI355X at
+// 26 layers x 8 kv heads x 8192 slots (208 units): the window streams at ~85%
+// of HBM peak against ~81% for 1024-slot chunks, and the partials and the
+// merge launch go away.  With more units than CUs the last round of such
+// long work groups would leave most CUs idle, so the window is split.
+//
+// Split: the largest of 1024..64 that still gives >= 1536 work groups (about
+// two waves of work groups over 256 CUs at 3 per CU), within the workspace.
 int32_t pick_chunk(const vkv_cache *c, int64_t units, int32_t n_kv_max, int32_t gqa,
                    int32_t *n_chunks_out) {
+    if (!forced_chunk() && 4 * units >= 3 * (int64_t)c->n_cus && units <= c->n_cus) {
+        *n_chunks_out = 1;
+        return std::max(n_kv_max, 1);
+    }
     int32_t chunk = 1024;
     while (chunk > 64 && units * ((n_kv_max + chunk - 1) / chunk) < 1536) chunk /= 2;
     if (forced_chunk()) chunk = forced_chunk();
@@ -234,8 +256,11 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     const int32_t D = c->p.head_dim;
     const int32_t G = c->p.n_kv_heads;
     const int32_t gqa = n_q_heads / G;
-    if (c->row_bytes >= (1 << 24) || c->p.capacity >= (1 << 24))
-        return fail(VKV_STATUS_INVALID_ARGUMENT, "decode attention: rows or capacity beyond 2^24");
+    // the kernel forms slot offsets with a 24x24-bit multiply into 32 bits
+    if (c->row_bytes >= (1 << 24) || c->p.capacity >= (1 << 24) ||
+        c->layer_bytes > (int64_t)UINT32_MAX)
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "decode attention: rows or capacity beyond 2^24, or a layer beyond 4 GiB");
     if (D != 128 || gqa != 4)
         return fail(VKV_STATUS_INVALID_ARGUMENT,
                     "decode attention supports head_dim 128 and 4 query heads per KV head "
@@ -266,15 +291,20 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     for (int32_t s = 0; s < n_streams; ++s) a.seg[s] = segs[s];
     const int64_t units = (int64_t)n_streams * n_layers * G;
     a.chunk = pick_chunk(c, units, n_kv_max, gqa, &a.n_chunks);
-    // Arrival counters are indexed [s][layer][g] relative to the call (at most
-    // the cache's extent); they return to zero after every call, so
-    // stream-ordered calls can share them.
-    const bool fused = !split_combine();
-    a.counters = fused ? c->counters : nullptr;
     a.out = out;
-    hipError_t e = launch_decode(c->p.dtype, gqa, k_new != nullptr, n_streams, a, st);
+    // XCD-grouped order: q8_0 head segments (136 B) share cache lines with
+    // their neighbours.  VKV_XCD_SWIZZLE=0/1 overrides.
+    const int64_t n_wg = units * a.n_chunks;
+    const int32_t sw_env = env_int("VKV_XCD_SWIZZLE");
+    const bool sw_want = std::getenv("VKV_XCD_SWIZZLE") ? sw_env == 1
+                                                         : c->p.dtype == VKV_DTYPE_Q8_0;
+    a.xcd_swizzle = (sw_want && G == 8 && n_wg % 64 == 0) ? 1 : 0;
+    const int32_t waves = forced_waves() ? forced_waves() : 4;
+    const int32_t stages = forced_stages() ? forced_stages() : 2;
+    hipError_t e =
+        launch_decode(c->p.dtype, gqa, waves, stages, k_new != nullptr, n_streams, a, st);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
-    if (fused) return VKV_STATUS_OK;
+    if (a.n_chunks == 1) return VKV_STATUS_OK;
     CombineArgs cb{};
     cb.part_o = c->part_o;
     cb.part_ml = c->part_ml;
@@ -454,13 +484,18 @@ vkv_status vkv_cache_create(const vkv_cache_params *params, vkv_cache **out) {
     c->part_heads_budget = wg * gqa;
 
     DeviceGuard guard(p.device);
+    {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, p.device) ==
+                hipSuccess && cus > 0)
+            c->n_cus = cus;
+    }
     // 256-byte tail pad: vector loads of the last q8_0 row may read a few
     // bytes past its end (never used).
     if ((e = hipMalloc(&c->k, (size_t)c->total_bytes + 256)) != hipSuccess ||
         (e = hipMalloc(&c->v, (size_t)c->total_bytes + 256)) != hipSuccess ||
         (e = hipMalloc(&c->part_o, (size_t)(c->part_heads_budget * p.head_dim * 4))) != hipSuccess ||
-        (e = hipMalloc(&c->part_ml, (size_t)(c->part_heads_budget * 2 * 4))) != hipSuccess ||
-        (e = hipMalloc(&c->counters, (size_t)units * 4)) != hipSuccess) {
+        (e = hipMalloc(&c->part_ml, (size_t)(c->part_heads_budget * 2 * 4))) != hipSuccess) {
         const bool oom = e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation;
         vkv_cache_destroy(c);
         if (oom) return fail(VKV_STATUS_OUT_OF_MEMORY, "cache create: device allocation failed");
@@ -469,7 +504,6 @@ vkv_status vkv_cache_create(const vkv_cache_params *params, vkv_cache **out) {
     // Zero once at allocation (src/voxtral.cpp:1456-1464); never per stream.
     if ((e = launch_fill_zero(c->k, c->total_bytes, nullptr)) != hipSuccess ||
         (e = launch_fill_zero(c->v, c->total_bytes, nullptr)) != hipSuccess ||
-        (e = launch_fill_zero(c->counters, units * 4, nullptr)) != hipSuccess ||
         (e = hipDeviceSynchronize()) != hipSuccess) {
         vkv_cache_destroy(c);
         return hip_fail(e, "cache create: zero fill");
@@ -483,7 +517,7 @@ vkv_status vkv_cache_destroy(vkv_cache *cache) {
     DeviceGuard guard(cache->p.device);
     hipError_t first = hipSuccess;
     for (void *p : {(void *)cache->k, (void *)cache->v, (void *)cache->part_o,
-                    (void *)cache->part_ml, (void *)cache->counters}) {
+                    (void *)cache->part_ml}) {
         if (!p) continue;
         hipError_t e = hipFree(p);
         if (e != hipSuccess && first == hipSuccess) first = e;

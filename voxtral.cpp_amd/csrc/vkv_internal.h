@@ -39,11 +39,9 @@ struct DecodeArgs {
     int64_t q_sstride, q_lstride;
     float *part_o;         // [stream][layer][n_q_heads][n_chunks][head_dim]
     float *part_ml;        // [stream][layer][n_q_heads][n_chunks][2]
-    // fused combine: the last work group of each (stream, layer, kv head)
-    // merges the chunk partials; arrival counters self-reset to zero.
-    int32_t *counters;     // [stream][layer][n_kv_heads]; nullptr -> k_combine
-    float *out;            // [stream][layer][n_q_heads][head_dim]
+    float *out;            // [stream][layer][n_q_heads][head_dim] (n_chunks == 1)
     int32_t n_chunks, chunk;
+    int32_t xcd_swizzle;   // 1: XCD-grouped work-group order (8 kv heads, grid % 64 == 0)
     int32_t n_layers, n_kv_heads, n_q_heads;
     float scale_log2;      // scale * log2(e)
     // fused append (decoder step): new rows [stream][layer][kv_dim] f32
@@ -90,8 +88,8 @@ struct WindowArgs {
 hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st);
 hipError_t launch_gather(const uint8_t *src, int64_t row_bytes, SegPair seg, uint8_t *dst,
                          hipStream_t st);
-hipError_t launch_decode(int dtype, int gqa, bool fuse_append, int n_streams,
-                         const DecodeArgs &a, hipStream_t st);
+hipError_t launch_decode(int dtype, int gqa, int waves, int stages, bool fuse_append,
+                         int n_streams, const DecodeArgs &a, hipStream_t st);
 hipError_t launch_combine(const CombineArgs &a, int n_streams, hipStream_t st);
 hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st);
 hipError_t launch_q8_0_pack(const float *x, uint8_t *blocks, int64_t n, hipStream_t st);

@@ -194,14 +194,17 @@ struct FmtQ8 {
     // Rows start 4-byte aligned (row_bytes = 34 * kv_dim/32 with kv_dim % 64
     // == 0 is a multiple of 4); offsets stay integers so the loads keep the
     // global address space.
+    // The streaming hint is not applied: the three dword loads and the scale
+    // load of neighbouring lanes share cache lines, which must stay resident
+    // between those instructions.
     template <bool NT = false>
     static __device__ __forceinline__ Frag load(const uint8_t *row, int e) {
         const int bo = (e >> 5) * 34;
         const int qo = bo + 2 + (e & 31);
         const uint32_t sh = (uint32_t)(qo & 3);   // 0 or 2
-        const uint16_t dh = ldw<NT>(reinterpret_cast<const uint16_t *>(row + bo));
+        const uint16_t dh = *reinterpret_cast<const uint16_t *>(row + bo);
         const uint32_t *w = reinterpret_cast<const uint32_t *>(row + (qo - (int)sh));
-        const uint32_t w0 = ldw<NT>(w), w1 = ldw<NT>(w + 1), w2 = ldw<NT>(w + 2);
+        const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
         Frag f;
         f.lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
         f.hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
@@ -463,24 +466,37 @@ __device__ __forceinline__ void pv_accumulate<FmtQ8>(float (&acc)[4][8], const F
 }
 
 // ---------------------------------------------------------------------------
-// Decode attention.  Workgroup = 4 waves on (stream, layer, kv head g, chunk
+// Decode attention.  Workgroup = W waves on (stream, layer, kv head g, chunk
 // of `chunk` logical slots).  Lane (grp = lane/16, c = lane%16) holds elements
 // [8c, 8c+8) of one slot's head row; a wave covers 4 slots per load, 16 slots
 // per batch (4 loads of K and of V in flight per lane), and the 4 query heads
-// of the GQA group share every K/V load.
+// of the GQA group share every K/V load.  With one chunk per (stream, layer,
+// kv head) the work group owns the whole window and writes the normalised
+// output itself; otherwise it writes a (max, sum, unnormalised output)
+// partial for k_combine.
 // ---------------------------------------------------------------------------
-template <class F, int GQA, bool FUSE>
-__global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
+template <class F, int GQA, bool FUSE, int W, int NS>
+__global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
     constexpr int D = 128;
     const int lane = threadIdx.x & 63;
     // wave index as a scalar: loop bounds derived from it stay uniform
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane >> 4;
     const int c = lane & 15;
-    const int g = blockIdx.x % a.n_kv_heads;
-    const int chunk = blockIdx.x / a.n_kv_heads;
-    const int layer = blockIdx.y;
-    const int s = blockIdx.z;
+    int item = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    if (a.xcd_swizzle) {
+        // Work groups go round-robin over the 8 XCDs (linear id i runs on XCD
+        // i % 8), each with its own L2.  Give the 8 kv heads of one (stream,
+        // layer, chunk) -- neighbouring segments of the same rows -- to one
+        // XCD, back to back, so lines two heads share are fetched once.
+        // (Host-checked: 8 kv heads, work-group count a multiple of 64.)
+        const int xcd = item & 7, k = item >> 3;
+        item = (((k >> 3) << 3) + xcd) * 8 + (k & 7);
+    }
+    const int g = item % a.n_kv_heads;
+    const int chunk = (item / a.n_kv_heads) % a.n_chunks;
+    const int layer = (item / (a.n_kv_heads * a.n_chunks)) % a.n_layers;
+    const int s = item / (a.n_kv_heads * a.n_chunks * a.n_layers);
     const SegPair sp = a.seg[s];
     const int n_kv = sp.n0 + sp.n1;
     const int64_t base = (int64_t)s * a.stream_bytes + (int64_t)layer * a.layer_bytes;
@@ -515,7 +531,7 @@ __global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
     for (int j = 0; j < GQA; ++j)
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[j][i] = 0.0f;
-    __shared__ float4 sm_p[4][16];   // per wave: p[slot of batch][head]
+    __shared__ float4 sm_p[W][16];   // per wave: p[slot of batch][head]
 
     const int i_begin = chunk * a.chunk;
     const int i_end = min(i_begin + a.chunk, n_kv);
@@ -534,9 +550,6 @@ __global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
             vf[u] = F::template load<true>(vl + off, e);
         }
     };
-    // Software pipeline over two register sets (no copies, so the wave never
-    // waits on the batch it has just requested): batch A is reduced while B's
-    // K/V loads are in flight, then the roles swap.
     // (always inlined: the fragment arrays must stay in registers)
     auto process = [&](typename F::Frag (&kf)[4], typename F::Frag (&vf)[4], const int b0)
                        __attribute__((always_inline)) {
@@ -605,17 +618,25 @@ __global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
         __syncthreads();
     }
 
-    // The loop body always handles two batches and the prefetches are
-    // unconditional (indices clamp to the last valid slot, an L2 hit; batches
-    // past the end are fully masked), so the wait counts stay exact.
-    typename F::Frag ka[4], va[4], kb[4], vb[4];
+    // Software pipeline over NS register sets (no copies, so the wave never
+    // waits on a batch it has just requested): while batch p is reduced, the
+    // loads of the next NS-1 batches are in flight.  The loop body always
+    // handles NS batches and the prefetches are unconditional (indices clamp
+    // to the last valid slot, an L2 hit; batches past the end are fully
+    // masked), so the wait counts stay exact.
+    typename F::Frag kf[NS][4], vf[NS][4];
+    constexpr int kStep = W * 16;   // slots covered by one batch of all waves
     int b0 = i_begin + wave * 16;
-    if (b0 < i_end) load_batch(b0, ka, va);
-    for (; b0 < i_end; b0 += 128) {
-        load_batch(b0 + 64, kb, vb);
-        process(ka, va, b0);
-        load_batch(b0 + 128, ka, va);
-        process(kb, vb, b0 + 64);
+    if (i_begin < i_end) {   // i_end >= 1: every clamped index is a valid slot
+#pragma unroll
+        for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
+    }
+    for (; b0 < i_end; b0 += NS * kStep) {
+#pragma unroll
+        for (int p = 0; p < NS; ++p) {
+            load_batch(b0 + (p + NS - 1) * kStep, kf[(p + NS - 1) % NS], vf[(p + NS - 1) % NS]);
+            process(kf[p], vf[p], b0 + p * kStep);
+        }
     }
 
     // Merge the 4 lane groups (they share m): every lane of head j sums l
@@ -633,9 +654,10 @@ __global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
         }
     }
 
-    // Merge the 4 waves through LDS and write this chunk's partial.
-    __shared__ float sm_m[4][GQA], sm_l[4][GQA];
-    __shared__ float sm_o[4][GQA][D];
+    // Merge the W waves through LDS; write the normalised output (one chunk)
+    // or this chunk's partial.
+    __shared__ float sm_m[W][GQA], sm_l[W][GQA];
+    __shared__ float sm_o[W][GQA][D];
     if (grp == 0) {
 #pragma unroll
         for (int j = 0; j < GQA; ++j)
@@ -648,58 +670,31 @@ __global__ void __launch_bounds__(256) k_decode(DecodeArgs a) {
     }
     __syncthreads();
     const int64_t head0 = ((int64_t)s * a.n_layers + layer) * a.n_q_heads + (int64_t)g * GQA;
-    for (int t = threadIdx.x; t < GQA * D; t += 256) {
+    for (int t = threadIdx.x; t < GQA * D; t += W * 64) {
         const int j = t / D;
         const int d = t % D;
-        float M = fmaxf(fmaxf(sm_m[0][j], sm_m[1][j]), fmaxf(sm_m[2][j], sm_m[3][j]));
+        float M = sm_m[0][j];
+#pragma unroll
+        for (int w = 1; w < W; ++w) M = fmaxf(M, sm_m[w][j]);
         float O = 0.0f, L = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
+            for (int w = 0; w < W; ++w) {
                 const float sc_w = fast_exp2(sm_m[w][j] - M);
                 O = fmaf(sm_o[w][j][d], sc_w, O);
                 L = fmaf(sm_l[w][j], sc_w, L);
             }
         }
-        const int64_t pidx = (head0 + j) * a.n_chunks + chunk;
-        a.part_o[pidx * D + d] = O;
-        if (d == 0) {
-            a.part_ml[pidx * 2] = M;
-            a.part_ml[pidx * 2 + 1] = L;
-        }
-    }
-    if (a.counters == nullptr) return;
-
-    // Fused combine: publish this chunk's partial, count arrivals; the last
-    // work group of the (stream, layer, kv head) merges all chunks.  No work
-    // group ever waits for another.
-    __shared__ int sm_last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int32_t *cnt = a.counters + ((int64_t)s * a.n_layers + layer) * a.n_kv_heads + g;
-        const int old = atomicAdd(cnt, 1);
-        sm_last = old == a.n_chunks - 1;
-        if (sm_last) atomicExch(cnt, 0);
-    }
-    __syncthreads();
-    if (!sm_last) return;
-    __threadfence();
-    for (int t = threadIdx.x; t < GQA * D; t += 256) {
-        const int j = t / D;
-        const int d = t % D;
-        const int64_t p0 = (head0 + j) * a.n_chunks;
-        float M = -INFINITY;
-        for (int c2 = 0; c2 < a.n_chunks; ++c2) M = fmaxf(M, __builtin_nontemporal_load(&a.part_ml[(p0 + c2) * 2]));
-        float O = 0.0f, L = 0.0f;
-        if (M != -INFINITY) {
-            for (int c2 = 0; c2 < a.n_chunks; ++c2) {
-                const float w = fast_exp2(__builtin_nontemporal_load(&a.part_ml[(p0 + c2) * 2]) - M);
-                L = fmaf(__builtin_nontemporal_load(&a.part_ml[(p0 + c2) * 2 + 1]), w, L);
-                O = fmaf(__builtin_nontemporal_load(&a.part_o[(p0 + c2) * D + d]), w, O);
+        if (a.n_chunks == 1) {
+            a.out[(head0 + j) * D + d] = L > 0.0f ? O / L : 0.0f;
+        } else {
+            const int64_t pidx = (head0 + j) * a.n_chunks + chunk;
+            a.part_o[pidx * D + d] = O;
+            if (d == 0) {
+                a.part_ml[pidx * 2] = M;
+                a.part_ml[pidx * 2 + 1] = L;
             }
         }
-        a.out[(head0 + j) * D + d] = L > 0.0f ? O / L : 0.0f;
     }
 }
 
@@ -1103,22 +1098,43 @@ hipError_t launch_gather(const uint8_t *src, int64_t row_bytes, SegPair seg, uin
     return hipGetLastError();
 }
 
-template <class F, int GQA>
-static void launch_decode_fmt(bool fuse, dim3 grid, const DecodeArgs &a, hipStream_t st) {
-    if (fuse) hipLaunchKernelGGL((k_decode<F, GQA, true>), grid, dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((k_decode<F, GQA, false>), grid, dim3(256), 0, st, a);
+template <class F, int GQA, int W, int NS>
+static void launch_decode_w(bool fuse, dim3 grid, const DecodeArgs &a, hipStream_t st) {
+    if (fuse) hipLaunchKernelGGL((k_decode<F, GQA, true, W, NS>), grid, dim3(W * 64), 0, st, a);
+    else hipLaunchKernelGGL((k_decode<F, GQA, false, W, NS>), grid, dim3(W * 64), 0, st, a);
 }
 
-hipError_t launch_decode(int dtype, int gqa, bool fuse_append, int n_streams, const DecodeArgs &a,
-                         hipStream_t st) {
+template <class F, int GQA>
+static bool launch_decode_fmt(int waves, int stages, bool fuse, dim3 grid, const DecodeArgs &a,
+                              hipStream_t st) {
+    switch (waves * 16 + stages) {
+    case 4 * 16 + 2: launch_decode_w<F, GQA, 4, 2>(fuse, grid, a, st); return true;
+    case 4 * 16 + 3: launch_decode_w<F, GQA, 4, 3>(fuse, grid, a, st); return true;
+    case 4 * 16 + 4: launch_decode_w<F, GQA, 4, 4>(fuse, grid, a, st); return true;
+    case 8 * 16 + 2: launch_decode_w<F, GQA, 8, 2>(fuse, grid, a, st); return true;
+    case 8 * 16 + 3: launch_decode_w<F, GQA, 8, 3>(fuse, grid, a, st); return true;
+    default: return false;
+    }
+}
+
+hipError_t launch_decode(int dtype, int gqa, int waves, int stages, bool fuse_append,
+                         int n_streams, const DecodeArgs &a, hipStream_t st) {
     dim3 grid((unsigned)(a.n_chunks * a.n_kv_heads), (unsigned)a.n_layers, (unsigned)n_streams);
     if (gqa != 4) return hipErrorInvalidValue;
+    bool ok = false;
     switch (dtype) {
-    case VKV_DTYPE_F16: launch_decode_fmt<FmtF16, 4>(fuse_append, grid, a, st); break;
-    case VKV_DTYPE_F32: launch_decode_fmt<FmtF32, 4>(fuse_append, grid, a, st); break;
-    case VKV_DTYPE_Q8_0: launch_decode_fmt<FmtQ8, 4>(fuse_append, grid, a, st); break;
-    default: return hipErrorInvalidValue;
+    case VKV_DTYPE_F16:
+        ok = launch_decode_fmt<FmtF16, 4>(waves, stages, fuse_append, grid, a, st);
+        break;
+    case VKV_DTYPE_F32:
+        ok = launch_decode_fmt<FmtF32, 4>(waves, stages, fuse_append, grid, a, st);
+        break;
+    case VKV_DTYPE_Q8_0:
+        ok = launch_decode_fmt<FmtQ8, 4>(waves, stages, fuse_append, grid, a, st);
+        break;
+    default: break;
     }
+    if (!ok) return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
