@@ -300,7 +300,7 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
                                                          : c->p.dtype == VKV_DTYPE_Q8_0;
     a.xcd_swizzle = (sw_want && G == 8 && n_wg % 64 == 0) ? 1 : 0;
     const int32_t waves = forced_waves() ? forced_waves() : 4;
-    const int32_t stages = forced_stages() ? forced_stages() : 2;
+    const int32_t stages = std::min(forced_stages() ? forced_stages() : 2, waves == 8 ? 3 : 4);
     hipError_t e =
         launch_decode(c->p.dtype, gqa, waves, stages, k_new != nullptr, n_streams, a, st);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
