@@ -1,7 +1,9 @@
 """GPU parity of the decoder KV step (append + single-query GQA attention)
-against the oracle, at the decoder shapes: cache state bit-exact, attention
-within 2e-3 (F16 KV) / 1e-2 (q8_0 KV) of the exact fp64 attention and of the
-ggml-mimic reduction order."""
+against the oracle, at the decoder shapes: cache state bit-exact; attention
+within 2e-3 (F16 KV) / 1e-2 (q8_0 KV) of the ggml-mimic, the oracle's
+restatement of the reference's CPU flash-attention path (for q8_0 K that path
+quantizes Q to q8_0 blocks and takes integer block sums, as the GPU does), and
+close to the exact fp64 attention (EXACT_TOL)."""
 import ctypes
 import os
 from concurrent.futures import ThreadPoolExecutor
@@ -18,6 +20,10 @@ from gpu_util import (SEED, empty_f32, expected_image, layer_image, oracle_decod
 pytestmark = pytest.mark.gpu
 
 TOL = {vkv.F16: 2e-3, vkv.F32: 1e-4, vkv.Q8_0: 1e-2}
+# Distance to the exact attention: for q8_0 the quantization of Q to q8_0
+# blocks (ggml's q8_0 dot product) moves the output by up to ~1.5e-2 on
+# windows of a few keys.
+EXACT_TOL = {vkv.F16: 2e-3, vkv.F32: 1e-4, vkv.Q8_0: 3e-2}
 SCALE = 1.0 / np.sqrt(128.0)
 POOL = ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
 
@@ -64,7 +70,7 @@ def test_single_layer_append_then_attend(dtype, capacity):
         got = out[0, 0].cpu().numpy().reshape(32, 128)
         exact = oracle_decode(c, 0, 0, slots, q_row)
         mimic = oracle_decode(c, 0, 0, slots, q_row, mimic=True)
-        assert np.max(np.abs(got - exact)) <= TOL[dtype]
+        assert np.max(np.abs(got - exact)) <= EXACT_TOL[dtype]
         assert np.max(np.abs(got - mimic)) <= TOL[dtype]
         # the unfused attention entry point over the same window agrees bit for bit
         out2 = empty_f32(1, 1, 4096)
@@ -203,9 +209,12 @@ def test_multi_stream_batch_mixed_fill(dtype):
         check_cache_state(c, range(ns), range(nl), cap, {s: fills[s] + 1 for s in range(ns)})
         for s in range(ns):
             for layer in range(nl):
-                want = oracle_decode(c, s, layer, plan_slots(plans[s]), q[s, layer].cpu().numpy())
+                slots, q_row = plan_slots(plans[s]), q[s, layer].cpu().numpy()
                 got = out[s, layer].cpu().numpy().reshape(32, 128)
-                assert np.max(np.abs(got - want)) <= TOL[dtype], (s, layer)
+                mimic = oracle_decode(c, s, layer, slots, q_row, mimic=True)
+                exact = oracle_decode(c, s, layer, slots, q_row)
+                assert np.max(np.abs(got - mimic)) <= TOL[dtype], (s, layer)
+                assert np.max(np.abs(got - exact)) <= EXACT_TOL[dtype], (s, layer)
 
 
 def test_q8_0_eight_streams_full_window():
@@ -229,7 +238,10 @@ def test_q8_0_eight_streams_full_window():
             pos += 1
             check_cache_state(c, [0, ns - 1], range(0, 26, 5), 8192, {0: pos, ns - 1: pos})
             for s in (0, 3, ns - 1):
-                want = oracle_decode(c, s, 25, plan_slots(plans[s]), q[s, 25].cpu().numpy())
+                slots, q_row = plan_slots(plans[s]), q[s, 25].cpu().numpy()
                 got = out[s, 25].cpu().numpy().reshape(32, 128)
-                assert np.max(np.abs(got - want)) <= 1e-2, (target, s)
+                mimic = oracle_decode(c, s, 25, slots, q_row, mimic=True)
+                exact = oracle_decode(c, s, 25, slots, q_row)
+                assert np.max(np.abs(got - mimic)) <= 1e-2, (target, s)
+                assert np.max(np.abs(got - exact)) <= EXACT_TOL[vkv.Q8_0], (target, s)
             print(f"q8_0 8-stream step {target} ok", flush=True)

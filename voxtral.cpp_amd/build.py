@@ -21,6 +21,10 @@ def hipcc_command(out=OUT):
         "-Wall", "-Wno-unused-function",
         # never let the compiler emit packed fp32 arithmetic
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # MFMA accumulators in ordinary VGPRs: the decode kernels rescale and
+        # read them with VALU every batch, which the AGPR form turns into
+        # accvgpr copies
+        "-mllvm", "-amdgpu-mfma-vgpr-form",
         "-I", os.path.join(ROOT, "include"), "-I", CSRC,
         *[os.path.join(CSRC, s) for s in SOURCES],
         "-o", out,

@@ -301,8 +301,10 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     a.xcd_swizzle = (sw_want && G == 8 && n_wg % 64 == 0) ? 1 : 0;
     const int32_t waves = forced_waves() ? forced_waves() : 4;
     const int32_t stages = std::min(forced_stages() ? forced_stages() : 2, waves == 8 ? 3 : 4);
-    hipError_t e =
-        launch_decode(c->p.dtype, gqa, waves, stages, k_new != nullptr, n_streams, a, st);
+    // q8_0: the matrix-core kernel unless VKV_DECODE_MFMA=0
+    const bool mfma = !(std::getenv("VKV_DECODE_MFMA") && env_int("VKV_DECODE_MFMA") == 0);
+    hipError_t e = launch_decode(c->p.dtype, gqa, waves, stages, mfma, k_new != nullptr,
+                                 n_streams, a, st);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     if (a.n_chunks == 1) return VKV_STATUS_OK;
     CombineArgs cb{};

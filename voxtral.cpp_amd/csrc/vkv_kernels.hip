@@ -465,6 +465,116 @@ __device__ __forceinline__ void pv_accumulate<FmtQ8>(float (&acc)[4][8], const F
     }
 }
 
+// Work item of a decode work group: (stream s, layer, kv head g, chunk).
+struct DecodeItem {
+    int g, chunk, layer, s;
+};
+
+__device__ __forceinline__ DecodeItem decode_item(const DecodeArgs &a) {
+    int item = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    if (a.xcd_swizzle) {
+        // Work groups go round-robin over the 8 XCDs (linear id i runs on XCD
+        // i % 8), each with its own L2.  Give the 8 kv heads of one (stream,
+        // layer, chunk) -- neighbouring segments of the same rows -- to one
+        // XCD, back to back, so lines two heads share are fetched once.
+        // (Host-checked: 8 kv heads, work-group count a multiple of 64.)
+        const int xcd = item & 7, k = item >> 3;
+        item = (((k >> 3) << 3) + xcd) * 8 + (k & 7);
+    }
+    DecodeItem it;
+    it.g = item % a.n_kv_heads;
+    it.chunk = (item / a.n_kv_heads) % a.n_chunks;
+    it.layer = (item / (a.n_kv_heads * a.n_chunks)) % a.n_layers;
+    it.s = item / (a.n_kv_heads * a.n_chunks * a.n_layers);
+    return it;
+}
+
+// Fused append of the step's new row (run_decoder_step's SET_ROWS,
+// src/voxtral.cpp:2682-2694).  The new row is the newest logical index
+// n_kv-1; lane group 0 of wave 0 in the work group whose chunk holds it
+// converts head g's part once and stores it into the ring.  The caller's
+// barrier then makes it visible to every wave, which reads it back like any
+// other slot; other work groups never touch the slot.
+template <class F>
+__device__ __forceinline__ void fused_append(const DecodeArgs &a, const SegPair &sp, int s,
+                                             int layer, int64_t base, int e, int i_begin,
+                                             int i_end, bool leader) {
+    const int n_kv = sp.n0 + sp.n1;
+    if (n_kv >= 1 && n_kv - 1 >= i_begin && n_kv - 1 < i_end && leader) {
+        const int slot = slot_of(sp, n_kv - 1);
+        const float *kn = a.k_new + (int64_t)s * a.new_sstride + (int64_t)layer * a.new_lstride + e;
+        const float *vn = a.v_new + (int64_t)s * a.new_sstride + (int64_t)layer * a.new_lstride + e;
+        float xk[8], xv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) { xk[i] = kn[i]; xv[i] = vn[i]; }
+        store_new<F>(a.k_w + base + (int64_t)slot * a.row_bytes, e, xk, true);
+        store_new<F>(a.v_w + base + (int64_t)slot * a.row_bytes, e, xv, true);
+    }
+}
+
+// Merge of the W waves of a decode work group through LDS, then the
+// normalised output (one chunk) or this chunk's partial.
+template <int W, int GQA>
+struct MergeSmem {
+    float m[W][GQA], l[W][GQA];
+    float o[W][GQA][128];
+};
+
+template <int W, int GQA>
+__device__ __forceinline__ void decode_merge_finish(const DecodeArgs &a, const DecodeItem &it,
+                                                    const MergeSmem<W, GQA> &sm) {
+    constexpr int D = 128;
+    __syncthreads();
+    const int64_t head0 =
+        ((int64_t)it.s * a.n_layers + it.layer) * a.n_q_heads + (int64_t)it.g * GQA;
+    for (int t = threadIdx.x; t < GQA * D; t += W * 64) {
+        const int j = t / D;
+        const int d = t % D;
+        float M = sm.m[0][j];
+#pragma unroll
+        for (int w = 1; w < W; ++w) M = fmaxf(M, sm.m[w][j]);
+        float O = 0.0f, L = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < W; ++w) {
+                const float sc_w = fast_exp2(sm.m[w][j] - M);
+                O = fmaf(sm.o[w][j][d], sc_w, O);
+                L = fmaf(sm.l[w][j], sc_w, L);
+            }
+        }
+        if (a.n_chunks == 1) {
+            a.out[(head0 + j) * D + d] = L > 0.0f ? O / L : 0.0f;
+        } else {
+            const int64_t pidx = (head0 + j) * a.n_chunks + it.chunk;
+            a.part_o[pidx * D + d] = O;
+            if (d == 0) {
+                a.part_ml[pidx * 2] = M;
+                a.part_ml[pidx * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// Lanes 0..15 hold acc[j][8*lane .. +8) (summed over the lane groups) and
+// lanes 0..3 the running max m and sum l of head `lane`.
+template <int W, int GQA>
+__device__ __forceinline__ void decode_merge(const DecodeArgs &a, const DecodeItem &it, int wave,
+                                             int lane, float m, float l,
+                                             const float (&acc)[GQA][8]) {
+    __shared__ MergeSmem<W, GQA> sm;
+    if (lane < 16) {
+#pragma unroll
+        for (int j = 0; j < GQA; ++j)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sm.o[wave][j][lane * 8 + i] = acc[j][i];
+        if (lane < GQA) {
+            sm.m[wave][lane] = m;
+            sm.l[wave][lane] = l;
+        }
+    }
+    decode_merge_finish<W, GQA>(a, it, sm);
+}
+
 // ---------------------------------------------------------------------------
 // Decode attention.  Workgroup = W waves on (stream, layer, kv head g, chunk
 // of `chunk` logical slots).  Lane (grp = lane/16, c = lane%16) holds elements
@@ -483,20 +593,8 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int grp = lane >> 4;
     const int c = lane & 15;
-    int item = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-    if (a.xcd_swizzle) {
-        // Work groups go round-robin over the 8 XCDs (linear id i runs on XCD
-        // i % 8), each with its own L2.  Give the 8 kv heads of one (stream,
-        // layer, chunk) -- neighbouring segments of the same rows -- to one
-        // XCD, back to back, so lines two heads share are fetched once.
-        // (Host-checked: 8 kv heads, work-group count a multiple of 64.)
-        const int xcd = item & 7, k = item >> 3;
-        item = (((k >> 3) << 3) + xcd) * 8 + (k & 7);
-    }
-    const int g = item % a.n_kv_heads;
-    const int chunk = (item / a.n_kv_heads) % a.n_chunks;
-    const int layer = (item / (a.n_kv_heads * a.n_chunks)) % a.n_layers;
-    const int s = item / (a.n_kv_heads * a.n_chunks * a.n_layers);
+    const DecodeItem it = decode_item(a);
+    const int g = it.g, chunk = it.chunk, layer = it.layer, s = it.s;
     const SegPair sp = a.seg[s];
     const int n_kv = sp.n0 + sp.n1;
     const int64_t base = (int64_t)s * a.stream_bytes + (int64_t)layer * a.layer_bytes;
@@ -601,20 +699,7 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
         pv_accumulate<F>(acc, vf, pw);
     };
     if (FUSE) {
-        // The step's new row is the newest logical index n_kv-1.  Lane group 0
-        // of wave 0 in the work group whose chunk holds it converts the f32 row
-        // once and stores it into the ring; after the barrier every wave reads
-        // it back like any other slot.  Other work groups never touch the slot.
-        if (n_kv >= 1 && n_kv - 1 >= i_begin && n_kv - 1 < i_end && wave == 0 && grp == 0) {
-            const int slot = slot_of(sp, n_kv - 1);
-            const float *kn = a.k_new + (int64_t)s * a.new_sstride + (int64_t)layer * a.new_lstride + e;
-            const float *vn = a.v_new + (int64_t)s * a.new_sstride + (int64_t)layer * a.new_lstride + e;
-            float xk[8], xv[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i) { xk[i] = kn[i]; xv[i] = vn[i]; }
-            store_new<F>(a.k_w + base + (int64_t)slot * a.row_bytes, e, xk, true);
-            store_new<F>(a.v_w + base + (int64_t)slot * a.row_bytes, e, xv, true);
-        }
+        fused_append<F>(a, sp, s, layer, base, e, i_begin, i_end, wave == 0 && grp == 0);
         __syncthreads();
     }
 
@@ -654,48 +739,241 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
         }
     }
 
-    // Merge the W waves through LDS; write the normalised output (one chunk)
-    // or this chunk's partial.
-    __shared__ float sm_m[W][GQA], sm_l[W][GQA];
-    __shared__ float sm_o[W][GQA][D];
-    if (grp == 0) {
+    decode_merge<W, GQA>(a, it, wave, lane, m, l, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Decode attention over a q8_0 cache on the matrix cores, in ggml's q8_0
+// arithmetic for QK: Q is quantized per 32-element block with the cache's own
+// quantizer and each v_mfma_i32_16x16x32_i8 contracts exactly one block, so
+// the block sums are exact integers; score = sum_t sumi_t * d_k[t] * d_q[t].
+// Per 16-slot batch of a wave:
+//   - K and V rows arrive with k_decode's q8_0 loads (lane group kg holds
+//     slots 4kg + u, lane r quants [8r, 8r+8) of the head and their block
+//     scale; one address computation serves both), and are written to
+//     per-wave LDS tiles with the quants de-interleaved from the scales
+//     (128 contiguous quant bytes per slot).
+//   - QK: A = K quants (lane (kg, r): block t quants [8kg, +8) of slot r, one
+//     ds_read_b64), B = Q quants (heads as columns 0..3).  Lane (kg, n < 4)
+//     receives slots 4kg + i (i = 0..3) of head n.
+//   - P.V: O^T[d][head] += V^T[d][slot] P^T[slot][head] with
+//     v_mfma_f32_16x16x16f16 per 16-dim tile.  B = p * d_v in f16 -- exactly
+//     the score lanes' layout, so p never leaves registers.  A = V^T comes
+//     from ds_read_b64_tr_b8: within each 16-lane group, output lane j byte k
+//     is byte j%8 of source lane 2k + j/8, so one transpose read hands every
+//     lane the 4 slots x 2 tiles of int8 values it needs for a block; they
+//     are spliced into f16 exactly (1024 + 128 + q under the f16 exponent).
+// ---------------------------------------------------------------------------
+typedef int int4v_t __attribute__((ext_vector_type(4)));
+typedef int int2v_t __attribute__((ext_vector_type(2)));
+typedef float float4v_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half4v_t __attribute__((ext_vector_type(4)));
+
+// 4 int8 values (one per byte) -> exact f16x4
+__device__ __forceinline__ half4v_t i8x4_to_h4(uint32_t x) {
+    const uint32_t b = x ^ 0x80808080u;
+    const half2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const half2_t lo = as_h2(__builtin_amdgcn_perm(0x64646464u, b, 0x05010400u)) - off;
+    const half2_t hi = as_h2(__builtin_amdgcn_perm(0x64646464u, b, 0x05030402u)) - off;
+    return half4v_t{lo.x, lo.y, hi.x, hi.y};
+}
+
+template <bool FUSE, int NS>
+__global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
+    constexpr int D = 128, GQA = 4, W = 4;
+    constexpr int QS = D + 8;             // LDS row stride of the quant tiles (bytes)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kg = lane >> 4;
+    const int r = lane & 15;
+    const DecodeItem it = decode_item(a);
+    const int g = it.g, layer = it.layer, s = it.s;
+    const SegPair sp = a.seg[s];
+    const int n_kv = sp.n0 + sp.n1;
+    const int64_t base = (int64_t)s * a.stream_bytes + (int64_t)layer * a.layer_bytes;
+    const uint8_t *kl = a.k + base;
+    const uint8_t *vl = a.v + base;
+    const int e = g * D + r * 8;          // quants [8r, 8r+8) of head g
+    const bool score_lane = r < GQA;
+
+    // Q of head r, block t, quants [8kg, 8kg+8): the B operand of QK,
+    // quantized as the cache is (d = amax/127, id = 1/d, round half away from
+    // zero, d kept in f16); the block's amax spans the 4 lane groups.
+    int64_t qb[4];
+    float dq[4];
+    {
+        const float *qp = a.q + (int64_t)s * a.q_sstride + (int64_t)layer * a.q_lstride +
+                          (int64_t)(g * GQA + (score_lane ? r : 0)) * D + kg * 8;
 #pragma unroll
-        for (int j = 0; j < GQA; ++j)
+        for (int t = 0; t < 4; ++t) {
+#pragma clang fp contract(off)
+            float x[8];
+            const float4 q0 = score_lane ? reinterpret_cast<const float4 *>(qp + 32 * t)[0]
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 q1 = score_lane ? reinterpret_cast<const float4 *>(qp + 32 * t)[1]
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            x[0] = q0.x; x[1] = q0.y; x[2] = q0.z; x[3] = q0.w;
+            x[4] = q1.x; x[5] = q1.y; x[6] = q1.z; x[7] = q1.w;
+            float amax = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) sm_o[wave][j][c * 8 + i] = acc[j][i];
-        if (c < GQA) {
-            sm_m[wave][c] = m;
-            sm_l[wave][c] = l;
+            for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+            amax = fmaxf(amax, __shfl_xor(amax, 16));
+            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            uint64_t w = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                w |= (uint64_t)((uint32_t)((int)round_half_away(x[i] * id)) & 0xffu) << (8 * i);
+            qb[t] = (int64_t)w;
+            dq[t] = (float)(_Float16)d;
         }
     }
-    __syncthreads();
-    const int64_t head0 = ((int64_t)s * a.n_layers + layer) * a.n_q_heads + (int64_t)g * GQA;
-    for (int t = threadIdx.x; t < GQA * D; t += W * 64) {
-        const int j = t / D;
-        const int d = t % D;
-        float M = sm_m[0][j];
+
+    // Score lanes (r < 4): running max m and partial sum l of head r, and
+    // o[T] = O^T tile T: dims 16T + 4kg + i of head r.
+    const uint32_t row_bytes24 = (uint32_t)a.row_bytes;
+    float m = -INFINITY, l = 0.0f;
+    float4v_t o[8];
 #pragma unroll
-        for (int w = 1; w < W; ++w) M = fmaxf(M, sm_m[w][j]);
-        float O = 0.0f, L = 0.0f;
-        if (M != -INFINITY) {
+    for (int t = 0; t < 8; ++t) o[t] = float4v_t{0.0f, 0.0f, 0.0f, 0.0f};
+    __shared__ __align__(16) uint8_t sm_kq[W][16 * QS];
+    __shared__ __align__(16) uint8_t sm_vq[W][16 * QS];
+    __shared__ float4 sm_dk[W][16];      // per wave: d_k[slot][block]
+    __shared__ float4 sm_dv[W][16];      // per wave: d_v[slot][block]
+
+    const int i_begin = it.chunk * a.chunk;
+    const int i_end = min(i_begin + a.chunk, n_kv);
+    auto load_batch = [&](int b, FmtQ8::Frag (&kf)[4], FmtQ8::Frag (&vf)[4])
+                          __attribute__((always_inline)) {
 #pragma unroll
-            for (int w = 0; w < W; ++w) {
-                const float sc_w = fast_exp2(sm_m[w][j] - M);
-                O = fmaf(sm_o[w][j][d], sc_w, O);
-                L = fmaf(sm_l[w][j], sc_w, L);
-            }
+        for (int u = 0; u < 4; ++u) {
+            // past the chunk end: reload the last valid slot (masked later)
+            const int ix = min(b + 4 * kg + u, i_end - 1);
+            const uint32_t off = __umul24((uint32_t)slot_of(sp, ix), row_bytes24);
+            kf[u] = FmtQ8::load(kl + off, e);
+            vf[u] = FmtQ8::load(vl + off, e);
         }
-        if (a.n_chunks == 1) {
-            a.out[(head0 + j) * D + d] = L > 0.0f ? O / L : 0.0f;
-        } else {
-            const int64_t pidx = (head0 + j) * a.n_chunks + chunk;
-            a.part_o[pidx * D + d] = O;
-            if (d == 0) {
-                a.part_ml[pidx * 2] = M;
-                a.part_ml[pidx * 2 + 1] = L;
-            }
+    };
+    auto process = [&](const FmtQ8::Frag (&kf)[4], const FmtQ8::Frag (&vf)[4], const int b0)
+                       __attribute__((always_inline)) {
+        uint8_t *kt = sm_kq[wave];
+        uint8_t *vt = sm_vq[wave];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int row = (4 * kg + u) * QS + 8 * r;
+            *reinterpret_cast<uint2 *>(kt + row) = make_uint2(kf[u].lo, kf[u].hi);
+            *reinterpret_cast<uint2 *>(vt + row) = make_uint2(vf[u].lo, vf[u].hi);
+            // the 4 lanes of a block write the same scale
+            reinterpret_cast<float *>(&sm_dk[wave][4 * kg + u])[r >> 2] = kf[u].d;
+            reinterpret_cast<float *>(&sm_dv[wave][4 * kg + u])[r >> 2] = vf[u].d;
+        }
+        __builtin_amdgcn_wave_barrier();
+        // QK: one MFMA per block t
+        int4v_t ci[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint2 ka = *reinterpret_cast<const uint2 *>(kt + r * QS + 32 * t + 8 * kg);
+            ci[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                (int64_t)(((uint64_t)ka.y << 32) | ka.x), qb[t], int4v_t{0, 0, 0, 0}, 0, 0, 0);
+        }
+        // V^T operands, block P: lane 2k+h of a group reads quants
+        // [32P + 16(k>>2) + 8h, +8) of slot 4kg + (k&3)
+        int2v_t vt8[4];
+        {
+            const int k = r >> 1, h = r & 1;
+            const uint8_t *src = vt + (4 * kg + (k & 3)) * QS + 16 * (k >> 2) + 8 * h;
+#pragma unroll
+            for (int P = 0; P < 4; ++P)
+                vt8[P] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                    (__attribute__((address_space(3))) int2v_t *)(src + 32 * P));
+        }
+        float sc[4];
+        float bm = -INFINITY;
+        float4 dvs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 dk = sm_dk[wave][4 * kg + i];
+            dvs[i] = sm_dv[wave][4 * kg + i];
+            float x = 0.0f;
+            x = fmaf((float)ci[0][i], dk.x * dq[0], x);
+            x = fmaf((float)ci[1][i], dk.y * dq[1], x);
+            x = fmaf((float)ci[2][i], dk.z * dq[2], x);
+            x = fmaf((float)ci[3][i], dk.w * dq[3], x);
+            const bool ok = score_lane && b0 + 4 * kg + i < i_end;
+            sc[i] = ok ? x * a.scale_log2 : -INFINITY;
+            bm = fmaxf(bm, sc[i]);
+        }
+        __builtin_amdgcn_wave_barrier();
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        // Lazy rescale: the reference max only moves when a head's batch max
+        // exceeds it by more than 2^8, so p <= 256 and rescaling is rare.
+        if (__any(bm > m + 8.0f)) {
+            const float mn = fmaxf(m, bm);
+            const float alpha = mn == -INFINITY ? 1.0f : fast_exp2(m - mn);
+            l *= alpha;
+            m = mn;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) o[t] *= alpha;
+        }
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            p[i] = sc[i] == -INFINITY ? 0.0f : fast_exp2(sc[i] - m);
+            l += p[i];
+        }
+        // P.V per block P: B = p * d_v[.][P] (f16), two 16-dim tiles
+#pragma unroll
+        for (int P = 0; P < 4; ++P) {
+            const float dv0 = reinterpret_cast<const float *>(&dvs[0])[P];
+            const float dv1 = reinterpret_cast<const float *>(&dvs[1])[P];
+            const float dv2 = reinterpret_cast<const float *>(&dvs[2])[P];
+            const float dv3 = reinterpret_cast<const float *>(&dvs[3])[P];
+            const half4v_t pb = {(_Float16)(p[0] * dv0), (_Float16)(p[1] * dv1),
+                                 (_Float16)(p[2] * dv2), (_Float16)(p[3] * dv3)};
+            o[2 * P] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4((uint32_t)vt8[P].x), pb,
+                                                             o[2 * P], 0, 0, 0);
+            o[2 * P + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4((uint32_t)vt8[P].y), pb,
+                                                                 o[2 * P + 1], 0, 0, 0);
+        }
+    };
+    if (FUSE) {
+        fused_append<FmtQ8>(a, sp, s, layer, base, e, i_begin, i_end, wave == 0 && kg == 0);
+        __syncthreads();
+    }
+
+    FmtQ8::Frag kf[NS][4], vf[NS][4];
+    constexpr int kStep = W * 16;
+    int b0 = i_begin + wave * 16;
+    if (i_begin < i_end) {   // i_end >= 1: every clamped index is a valid slot
+#pragma unroll
+        for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
+    }
+    for (; b0 < i_end; b0 += NS * kStep) {
+#pragma unroll
+        for (int p = 0; p < NS; ++p) {
+            load_batch(b0 + (p + NS - 1) * kStep, kf[(p + NS - 1) % NS], vf[(p + NS - 1) % NS]);
+            process(kf[p], vf[p], b0 + p * kStep);
         }
     }
+
+    // l over the 4 lane groups of each head; publish O^T (score lanes) for
+    // the merge of the waves
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    __shared__ MergeSmem<W, GQA> msm;
+    if (score_lane) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) msm.o[wave][r][16 * t + 4 * kg + i] = o[t][i];
+        if (kg == 0) {
+            msm.m[wave][r] = m;
+            msm.l[wave][r] = l;
+        }
+    }
+    decode_merge_finish<W, GQA>(a, it, msm);
 }
 
 __global__ void __launch_bounds__(256) k_combine(CombineArgs a) {
@@ -1117,10 +1395,20 @@ static bool launch_decode_fmt(int waves, int stages, bool fuse, dim3 grid, const
     }
 }
 
-hipError_t launch_decode(int dtype, int gqa, int waves, int stages, bool fuse_append,
+hipError_t launch_decode(int dtype, int gqa, int waves, int stages, bool mfma, bool fuse_append,
                          int n_streams, const DecodeArgs &a, hipStream_t st) {
     dim3 grid((unsigned)(a.n_chunks * a.n_kv_heads), (unsigned)a.n_layers, (unsigned)n_streams);
     if (gqa != 4) return hipErrorInvalidValue;
+    if (mfma && dtype == VKV_DTYPE_Q8_0 && waves == 4) {
+        if (stages == 3) {
+            if (fuse_append) hipLaunchKernelGGL((k_decode_q8mfma<true, 3>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_decode_q8mfma<false, 3>), grid, dim3(256), 0, st, a);
+        } else {
+            if (fuse_append) hipLaunchKernelGGL((k_decode_q8mfma<true, 2>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_decode_q8mfma<false, 2>), grid, dim3(256), 0, st, a);
+        }
+        return hipGetLastError();
+    }
     bool ok = false;
     switch (dtype) {
     case VKV_DTYPE_F16:
