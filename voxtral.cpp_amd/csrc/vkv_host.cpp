@@ -228,15 +228,18 @@ int32_t forced_stages() {
 // merge launch go away.  With more units than CUs the last round of such
 // long work groups would leave most CUs idle, so the window is split.
 //
-// Split: the largest of 1024..64 that still gives >= 1536 work groups (about
+// Split: the largest of 2048..64 that still gives >= 1536 work groups (about
 // two waves of work groups over 256 CUs at 3 per CU), within the workspace.
+// Measured on MI355X at 8 streams x 26 layers x 8192 slots (q8_0): 2048-slot
+// chunks beat 1024 by 3% (the per-work-group prologue and merge amortise
+// over more batches) and 4096 by 8% (too few work groups per CU).
 int32_t pick_chunk(const vkv_cache *c, int64_t units, int32_t n_kv_max, int32_t gqa,
                    int32_t *n_chunks_out) {
     if (!forced_chunk() && 4 * units >= 3 * (int64_t)c->n_cus && units <= c->n_cus) {
         *n_chunks_out = 1;
         return std::max(n_kv_max, 1);
     }
-    int32_t chunk = 1024;
+    int32_t chunk = 2048;
     while (chunk > 64 && units * ((n_kv_max + chunk - 1) / chunk) < 1536) chunk /= 2;
     if (forced_chunk()) chunk = forced_chunk();
     for (;;) {
@@ -320,10 +323,14 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     return VKV_STATUS_OK;
 }
 
+// Window attention of n_q queries; with k_new, the n_q new rows are first
+// written through wsegs (fused into the matrix-core kernel).
 vkv_status do_window(vkv_cache *c, int32_t stream, int32_t layer0, int32_t n_layers,
                      const vkv_seg *segs, int32_t nseg, int64_t key_pos0, int64_t q_pos0,
                      int32_t n_q, int32_t window, const float *q, float *out, int32_t n_q_heads,
-                     float scale, hipStream_t st) {
+                     float scale, hipStream_t st, const float *k_new = nullptr,
+                     const float *v_new = nullptr, const vkv_seg *wsegs = nullptr,
+                     int32_t wnseg = 0) {
     if (c->p.head_dim % 8 != 0 || c->p.head_dim > 128)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "window attention: head_dim %d unsupported",
                     c->p.head_dim);
@@ -346,6 +353,14 @@ vkv_status do_window(vkv_cache *c, int32_t stream, int32_t layer0, int32_t n_lay
     a.window = window;
     a.scale_log2 = scale * 1.4426950408889634f;
     a.seg = seg_pair(segs, nseg);
+    a.k_w = stream_layer_base(c, c->k, stream, layer0);
+    a.v_w = stream_layer_base(c, c->v, stream, layer0);
+    if (k_new) {
+        a.k_new = k_new;
+        a.v_new = v_new;
+        a.n_new = n_q;
+        a.wseg = seg_pair(wsegs, wnseg);
+    }
     hipError_t e = launch_window(c->p.dtype, a, st);
     if (e != hipSuccess) return hip_fail(e, "window attention launch");
     return VKV_STATUS_OK;
@@ -701,12 +716,9 @@ vkv_status vkv_decoder_prefill(vkv_cache *cache, int32_t stream, vkv_ring *ring,
                     "decoder prefill: the post-append window must be one segment (got %d)", plan.read_nseg);
     DeviceGuard guard(cache->p.device);
     hipStream_t st = as_stream(hip_stream);
-    if (vkv_status s = do_append(cache, stream, layer0, n_layers, plan.write_seg, plan.write_nseg,
-                                 k, v, 0, st))
-        return s;
     if (vkv_status s = do_window(cache, stream, layer0, n_layers, plan.read_seg, plan.read_nseg,
                                  plan.oldest_after, plan.absolute_start, n_tokens, 0, q, out,
-                                 n_q_heads, scale, st))
+                                 n_q_heads, scale, st, k, v, plan.write_seg, plan.write_nseg))
         return s;
     vkv_decoder_commit(ring, &plan);
     return ok();
@@ -731,12 +743,9 @@ vkv_status vkv_enc_step(vkv_cache *cache, int32_t stream, const vkv_enc_plan *pl
         return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder step: write segments do not cover n_new");
     DeviceGuard guard(cache->p.device);
     hipStream_t st = as_stream(hip_stream);
-    if (vkv_status s = do_append(cache, stream, layer0, n_layers, plan->write_seg, plan->write_nseg,
-                                 k, v, 0, st))
-        return s;
     if (vkv_status s = do_window(cache, stream, layer0, n_layers, plan->read_seg, plan->read_nseg,
                                  plan->win_start, plan->q_start, plan->n_new, window, q, out,
-                                 n_q_heads, scale, st))
+                                 n_q_heads, scale, st, k, v, plan->write_seg, plan->write_nseg))
         return s;
     return ok();
 }

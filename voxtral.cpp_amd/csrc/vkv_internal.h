@@ -83,6 +83,14 @@ struct WindowArgs {
     int32_t window;        // <= 0: unbounded (causal only)
     float scale_log2;
     SegPair seg;           // logical key window
+    // Optional append of n_new rows ([layer][n_new][kv_dim] f32) through the
+    // write segments wseg before the attention (k_new == nullptr: none).
+    const float *k_new;
+    const float *v_new;
+    uint8_t *k_w;          // writable aliases of k/v
+    uint8_t *v_w;
+    int32_t n_new;
+    SegPair wseg;
 };
 
 hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st);

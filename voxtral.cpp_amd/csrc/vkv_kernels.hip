@@ -778,7 +778,32 @@ __device__ __forceinline__ half4v_t i8x4_to_h4(uint32_t x) {
     return half4v_t{lo.x, lo.y, hi.x, hi.y};
 }
 
-template <bool FUSE, int NS>
+// q8_0 fragment loads through a buffer resource: the layer base sits in the
+// descriptor (SGPRs) and each lane adds a 32-bit offset, so no 64-bit address
+// arithmetic per load.  Lane-constant part of element e's offsets:
+struct Q8LaneOff {
+    uint32_t q;    // first dword holding the 8 quants
+    uint32_t d;    // the block scale
+    uint32_t sh;   // byte shift of the quants in that dword (0 or 2)
+};
+__device__ __forceinline__ Q8LaneOff q8_lane_off(int e) {
+    const uint32_t bo = (uint32_t)(e >> 5) * 34u;
+    const uint32_t qo = bo + 2u + (uint32_t)(e & 31);
+    return Q8LaneOff{qo & ~3u, bo, qo & 3u};
+}
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+__device__ __forceinline__ FmtQ8::Frag q8_load_buf(__amdgpu_buffer_rsrc_t rs, uint32_t row_off,
+                                                   const Q8LaneOff &lo) {
+    const u32x3_t w = __builtin_amdgcn_raw_buffer_load_b96(rs, row_off + lo.q, 0, 0);
+    const uint16_t dh = __builtin_amdgcn_raw_buffer_load_b16(rs, row_off + lo.d, 0, 0);
+    FmtQ8::Frag f;
+    f.lo = __builtin_amdgcn_alignbyte(w.y, w.x, lo.sh);
+    f.hi = __builtin_amdgcn_alignbyte(w.z, w.y, lo.sh);
+    f.d = (float)__builtin_bit_cast(_Float16, dh);
+    return f;
+}
+
+template <bool FUSE, int NS, int SB>
 __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
     constexpr int D = 128, GQA = 4, W = 4;
     constexpr int QS = D + 8;             // LDS row stride of the quant tiles (bytes)
@@ -795,6 +820,15 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
     const uint8_t *vl = a.v + base;
     const int e = g * D + r * 8;          // quants [8r, 8r+8) of head g
     const bool score_lane = r < GQA;
+    // Buffer descriptors of this (stream, layer)'s K and V: the records
+    // extend 256 bytes past the layer (the next layer, or the allocation's
+    // tail pad), covering the third quant dword of the last row.
+    const uint32_t n_rec = (uint32_t)min<int64_t>(a.layer_bytes + 256, (int64_t)UINT32_MAX);
+    const __amdgpu_buffer_rsrc_t k_rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)kl, (short)0, (int)n_rec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t v_rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)vl, (short)0, (int)n_rec, 0x00020000);
+    const Q8LaneOff qlo = q8_lane_off(e);
 
     // Q of head r, block t, quants [8kg, 8kg+8): the B operand of QK,
     // quantized as the cache is (d = amax/127, id = 1/d, round half away from
@@ -837,73 +871,85 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
     float4v_t o[8];
 #pragma unroll
     for (int t = 0; t < 8; ++t) o[t] = float4v_t{0.0f, 0.0f, 0.0f, 0.0f};
-    __shared__ __align__(16) uint8_t sm_kq[W][16 * QS];
-    __shared__ __align__(16) uint8_t sm_vq[W][16 * QS];
-    __shared__ float4 sm_dk[W][16];      // per wave: d_k[slot][block]
-    __shared__ float4 sm_dv[W][16];      // per wave: d_v[slot][block]
+    __shared__ __align__(16) uint8_t sm_kq[W][SB][16 * QS];
+    __shared__ __align__(16) uint8_t sm_vq[W][SB][16 * QS];
+    __shared__ float4 sm_dk[W][SB][16];  // per wave: d_k[slot][block]
+    __shared__ float4 sm_dv[W][SB][16];  // per wave: d_v[slot][block]
 
     const int i_begin = it.chunk * a.chunk;
     const int i_end = min(i_begin + a.chunk, n_kv);
-    auto load_batch = [&](int b, FmtQ8::Frag (&kf)[4], FmtQ8::Frag (&vf)[4])
-                          __attribute__((always_inline)) {
+    // A step of a wave covers SB sub-batches of 16 slots: [b, b + 16 SB).
+    using Frags = FmtQ8::Frag[SB][4];
+    auto load_step = [&](int b, Frags &kf, Frags &vf) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            // past the chunk end: reload the last valid slot (masked later)
-            const int ix = min(b + 4 * kg + u, i_end - 1);
-            const uint32_t off = __umul24((uint32_t)slot_of(sp, ix), row_bytes24);
-            kf[u] = FmtQ8::load(kl + off, e);
-            vf[u] = FmtQ8::load(vl + off, e);
-        }
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                // past the chunk end: reload the last valid slot (masked later)
+                const int ix = min(b + 16 * sb + 4 * kg + u, i_end - 1);
+                const uint32_t off = __umul24((uint32_t)slot_of(sp, ix), row_bytes24);
+                kf[sb][u] = q8_load_buf(k_rs, off, qlo);
+                vf[sb][u] = q8_load_buf(v_rs, off, qlo);
+            }
     };
-    auto process = [&](const FmtQ8::Frag (&kf)[4], const FmtQ8::Frag (&vf)[4], const int b0)
+    // The sub-batches are independent up to the softmax, which takes one
+    // joint max (one cross-lane chain) and one rescale decision per step.
+    auto process = [&](const Frags &kf, const Frags &vf, const int b0)
                        __attribute__((always_inline)) {
-        uint8_t *kt = sm_kq[wave];
-        uint8_t *vt = sm_vq[wave];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int row = (4 * kg + u) * QS + 8 * r;
-            *reinterpret_cast<uint2 *>(kt + row) = make_uint2(kf[u].lo, kf[u].hi);
-            *reinterpret_cast<uint2 *>(vt + row) = make_uint2(vf[u].lo, vf[u].hi);
-            // the 4 lanes of a block write the same scale
-            reinterpret_cast<float *>(&sm_dk[wave][4 * kg + u])[r >> 2] = kf[u].d;
-            reinterpret_cast<float *>(&sm_dv[wave][4 * kg + u])[r >> 2] = vf[u].d;
-        }
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int row = (4 * kg + u) * QS + 8 * r;
+                *reinterpret_cast<uint2 *>(sm_kq[wave][sb] + row) = make_uint2(kf[sb][u].lo, kf[sb][u].hi);
+                *reinterpret_cast<uint2 *>(sm_vq[wave][sb] + row) = make_uint2(vf[sb][u].lo, vf[sb][u].hi);
+                // the 4 lanes of a block write the same scale
+                reinterpret_cast<float *>(&sm_dk[wave][sb][4 * kg + u])[r >> 2] = kf[sb][u].d;
+                reinterpret_cast<float *>(&sm_dv[wave][sb][4 * kg + u])[r >> 2] = vf[sb][u].d;
+            }
         __builtin_amdgcn_wave_barrier();
         // QK: one MFMA per block t
-        int4v_t ci[4];
+        int4v_t ci[SB][4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint2 ka = *reinterpret_cast<const uint2 *>(kt + r * QS + 32 * t + 8 * kg);
-            ci[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                (int64_t)(((uint64_t)ka.y << 32) | ka.x), qb[t], int4v_t{0, 0, 0, 0}, 0, 0, 0);
-        }
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint2 ka =
+                    *reinterpret_cast<const uint2 *>(sm_kq[wave][sb] + r * QS + 32 * t + 8 * kg);
+                ci[sb][t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                    (int64_t)(((uint64_t)ka.y << 32) | ka.x), qb[t], int4v_t{0, 0, 0, 0}, 0, 0, 0);
+            }
         // V^T operands, block P: lane 2k+h of a group reads quants
         // [32P + 16(k>>2) + 8h, +8) of slot 4kg + (k&3)
-        int2v_t vt8[4];
+        int2v_t vt8[SB][4];
         {
             const int k = r >> 1, h = r & 1;
-            const uint8_t *src = vt + (4 * kg + (k & 3)) * QS + 16 * (k >> 2) + 8 * h;
+            const int src = (4 * kg + (k & 3)) * QS + 16 * (k >> 2) + 8 * h;
 #pragma unroll
-            for (int P = 0; P < 4; ++P)
-                vt8[P] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                    (__attribute__((address_space(3))) int2v_t *)(src + 32 * P));
+            for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+                for (int P = 0; P < 4; ++P)
+                    vt8[sb][P] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                        (__attribute__((address_space(3))) int2v_t *)(sm_vq[wave][sb] + src + 32 * P));
         }
-        float sc[4];
+        float sc[SB][4];
         float bm = -INFINITY;
-        float4 dvs[4];
+        float4 dvs[SB][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 dk = sm_dk[wave][4 * kg + i];
-            dvs[i] = sm_dv[wave][4 * kg + i];
-            float x = 0.0f;
-            x = fmaf((float)ci[0][i], dk.x * dq[0], x);
-            x = fmaf((float)ci[1][i], dk.y * dq[1], x);
-            x = fmaf((float)ci[2][i], dk.z * dq[2], x);
-            x = fmaf((float)ci[3][i], dk.w * dq[3], x);
-            const bool ok = score_lane && b0 + 4 * kg + i < i_end;
-            sc[i] = ok ? x * a.scale_log2 : -INFINITY;
-            bm = fmaxf(bm, sc[i]);
-        }
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 dk = sm_dk[wave][sb][4 * kg + i];
+                dvs[sb][i] = sm_dv[wave][sb][4 * kg + i];
+                float x = 0.0f;
+                x = fmaf((float)ci[sb][0][i], dk.x * dq[0], x);
+                x = fmaf((float)ci[sb][1][i], dk.y * dq[1], x);
+                x = fmaf((float)ci[sb][2][i], dk.z * dq[2], x);
+                x = fmaf((float)ci[sb][3][i], dk.w * dq[3], x);
+                const bool ok = score_lane && b0 + 16 * sb + 4 * kg + i < i_end;
+                sc[sb][i] = ok ? x * a.scale_log2 : -INFINITY;
+                bm = fmaxf(bm, sc[sb][i]);
+            }
         __builtin_amdgcn_wave_barrier();
         bm = fmaxf(bm, __shfl_xor(bm, 16));
         bm = fmaxf(bm, __shfl_xor(bm, 32));
@@ -917,43 +963,47 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
 #pragma unroll
             for (int t = 0; t < 8; ++t) o[t] *= alpha;
         }
-        float p[4];
+        float p[SB][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            p[i] = sc[i] == -INFINITY ? 0.0f : fast_exp2(sc[i] - m);
-            l += p[i];
-        }
-        // P.V per block P: B = p * d_v[.][P] (f16), two 16-dim tiles
+        for (int sb = 0; sb < SB; ++sb)
 #pragma unroll
-        for (int P = 0; P < 4; ++P) {
-            const float dv0 = reinterpret_cast<const float *>(&dvs[0])[P];
-            const float dv1 = reinterpret_cast<const float *>(&dvs[1])[P];
-            const float dv2 = reinterpret_cast<const float *>(&dvs[2])[P];
-            const float dv3 = reinterpret_cast<const float *>(&dvs[3])[P];
-            const half4v_t pb = {(_Float16)(p[0] * dv0), (_Float16)(p[1] * dv1),
-                                 (_Float16)(p[2] * dv2), (_Float16)(p[3] * dv3)};
-            o[2 * P] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4((uint32_t)vt8[P].x), pb,
-                                                             o[2 * P], 0, 0, 0);
-            o[2 * P + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4((uint32_t)vt8[P].y), pb,
-                                                                 o[2 * P + 1], 0, 0, 0);
-        }
+            for (int i = 0; i < 4; ++i) {
+                p[sb][i] = sc[sb][i] == -INFINITY ? 0.0f : fast_exp2(sc[sb][i] - m);
+                l += p[sb][i];
+            }
+        // P.V per block P: B = p * d_v[.][P] (f16), two 16-dim tiles; the
+        // sub-batches alternate so that dependent MFMAs are 8 apart
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+            for (int P = 0; P < 4; ++P) {
+                const half4v_t pb = {
+                    (_Float16)(p[sb][0] * reinterpret_cast<const float *>(&dvs[sb][0])[P]),
+                    (_Float16)(p[sb][1] * reinterpret_cast<const float *>(&dvs[sb][1])[P]),
+                    (_Float16)(p[sb][2] * reinterpret_cast<const float *>(&dvs[sb][2])[P]),
+                    (_Float16)(p[sb][3] * reinterpret_cast<const float *>(&dvs[sb][3])[P])};
+                o[2 * P] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                    i8x4_to_h4((uint32_t)vt8[sb][P].x), pb, o[2 * P], 0, 0, 0);
+                o[2 * P + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                    i8x4_to_h4((uint32_t)vt8[sb][P].y), pb, o[2 * P + 1], 0, 0, 0);
+            }
     };
     if (FUSE) {
         fused_append<FmtQ8>(a, sp, s, layer, base, e, i_begin, i_end, wave == 0 && kg == 0);
         __syncthreads();
     }
 
-    FmtQ8::Frag kf[NS][4], vf[NS][4];
-    constexpr int kStep = W * 16;
-    int b0 = i_begin + wave * 16;
+    Frags kf[NS], vf[NS];
+    constexpr int kStep = W * 16 * SB;
+    int b0 = i_begin + wave * 16 * SB;
     if (i_begin < i_end) {   // i_end >= 1: every clamped index is a valid slot
 #pragma unroll
-        for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
+        for (int p = 0; p < NS - 1; ++p) load_step(b0 + p * kStep, kf[p], vf[p]);
     }
     for (; b0 < i_end; b0 += NS * kStep) {
 #pragma unroll
         for (int p = 0; p < NS; ++p) {
-            load_batch(b0 + (p + NS - 1) * kStep, kf[(p + NS - 1) % NS], vf[(p + NS - 1) % NS]);
+            load_step(b0 + (p + NS - 1) * kStep, kf[(p + NS - 1) % NS], vf[(p + NS - 1) % NS]);
             process(kf[p], vf[p], b0 + p * kStep);
         }
     }
@@ -1117,6 +1167,36 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
     __shared__ float sm_o[4][16][D + 1];
     __shared__ float sm_m[4][16], sm_l[4][16];
 
+    // Fused ring write (the encoder step's and the prefill's append): this
+    // work group converts kv head g's part of the n_new new rows (F16 RNE)
+    // and stores them through the write segments; the barrier makes them
+    // visible to its waves, which attend them like any other key.  Several
+    // tiles of one head (GQA prefill) store identical bytes.
+    if (a.k_new) {
+        const int kv_dim = a.n_kv_heads * D;
+        const int64_t src0 = (int64_t)layer * a.n_new * kv_dim;
+        uint8_t *kw = a.k_w + (int64_t)layer * a.layer_bytes;
+        uint8_t *vw = a.v_w + (int64_t)layer * a.layer_bytes;
+        for (int t = threadIdx.x; t < a.n_new * (D / 8); t += 256) {
+            const int row = t / (D / 8);
+            const int col = g * D + (t % (D / 8)) * 8;
+            const int64_t so = src0 + (int64_t)row * kv_dim + col;
+            const int64_t dst = (int64_t)slot_of(a.wseg, row) * a.row_bytes;
+            float xk[8], xv[8];
+            const float4 k0 = reinterpret_cast<const float4 *>(a.k_new + so)[0];
+            const float4 k1 = reinterpret_cast<const float4 *>(a.k_new + so)[1];
+            const float4 v0 = reinterpret_cast<const float4 *>(a.v_new + so)[0];
+            const float4 v1 = reinterpret_cast<const float4 *>(a.v_new + so)[1];
+            xk[0] = k0.x; xk[1] = k0.y; xk[2] = k0.z; xk[3] = k0.w;
+            xk[4] = k1.x; xk[5] = k1.y; xk[6] = k1.z; xk[7] = k1.w;
+            xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
+            xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+            FmtF16::store(kw + dst, col, FmtF16::from_f32(xk));
+            FmtF16::store(vw + dst, col, FmtF16::from_f32(xv));
+        }
+        __syncthreads();
+    }
+
     // ---- Q^T operand: lane holds row lr, dims [DL*lg, DL*lg + DL) as f16 ----
     const int row = tile * 16 + lr;
     const bool row_ok = row < n_rows;
@@ -1204,15 +1284,21 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
             l += p;
             pb[i] = (_Float16)p;
         }
-        // V^T operand: lane reads V[key 4*lg+i][d = 16*t + lr] from the tile
+        // V^T operand: lane (lg, lr) needs V[key 4lg+i][d = 16t + lr], i =
+        // 0..3.  ds_read_b64_tr_b16 gives output lane j of a 16-lane group
+        // element k = element j%4 of source lane 4k + j/4, so source lane
+        // (lg, 4i+q) reads V[key 4lg+i][16t + 4q, +4).
         __builtin_amdgcn_wave_barrier();
+        {
+            const uint8_t *vsrc = &sm_v[wave][(4 * lg + (lr >> 2)) * VS + 8 * (lr & 3)];
 #pragma unroll
-        for (int t = 0; t < KB; ++t) {
-            half4_t va;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                va[i] = *reinterpret_cast<const _Float16 *>(&sm_v[wave][(4 * lg + i) * VS + 2 * (16 * t + lr)]);
-            o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[t], 0, 0, 0);
+            for (int t = 0; t < KB; ++t) {
+                typedef short short4_t __attribute__((ext_vector_type(4)));
+                const half4_t va = __builtin_bit_cast(
+                    half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                 (__attribute__((address_space(3))) short4_t *)(vsrc + 32 * t)));
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, o[t], 0, 0, 0);
+            }
         }
         __builtin_amdgcn_wave_barrier();
     }
@@ -1400,12 +1486,17 @@ hipError_t launch_decode(int dtype, int gqa, int waves, int stages, bool mfma, b
     dim3 grid((unsigned)(a.n_chunks * a.n_kv_heads), (unsigned)a.n_layers, (unsigned)n_streams);
     if (gqa != 4) return hipErrorInvalidValue;
     if (mfma && dtype == VKV_DTYPE_Q8_0 && waves == 4) {
+        // stages: 2 = two 16-slot sub-batches per step, one step in flight;
+        // 3 = one sub-batch per step, two steps in flight
         if (stages == 3) {
-            if (fuse_append) hipLaunchKernelGGL((k_decode_q8mfma<true, 3>), grid, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((k_decode_q8mfma<false, 3>), grid, dim3(256), 0, st, a);
+            if (fuse_append) hipLaunchKernelGGL((k_decode_q8mfma<true, 3, 1>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_decode_q8mfma<false, 3, 1>), grid, dim3(256), 0, st, a);
+        } else if (stages == 4) {
+            if (fuse_append) hipLaunchKernelGGL((k_decode_q8mfma<true, 2, 1>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_decode_q8mfma<false, 2, 1>), grid, dim3(256), 0, st, a);
         } else {
-            if (fuse_append) hipLaunchKernelGGL((k_decode_q8mfma<true, 2>), grid, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL((k_decode_q8mfma<false, 2>), grid, dim3(256), 0, st, a);
+            if (fuse_append) hipLaunchKernelGGL((k_decode_q8mfma<true, 2, 2>), grid, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL((k_decode_q8mfma<false, 2, 2>), grid, dim3(256), 0, st, a);
         }
         return hipGetLastError();
     }
@@ -1433,7 +1524,25 @@ hipError_t launch_combine(const CombineArgs &a, int n_streams, hipStream_t st) {
 }
 
 hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st) {
-    if (dtype == VKV_DTYPE_F16 && !window_valu_forced() && (a.head_dim == 64 || a.head_dim == 128)) {
+    const bool mfma =
+        dtype == VKV_DTYPE_F16 && !window_valu_forced() && (a.head_dim == 64 || a.head_dim == 128);
+    if (a.k_new && !mfma) {
+        // the scalar-ALU kernel has no fused write: append first
+        AppendArgs ap{};
+        ap.k = a.k_w;
+        ap.v = a.v_w;
+        ap.layer_bytes = a.layer_bytes;
+        ap.row_bytes = a.row_bytes;
+        ap.k_src = a.k_new;
+        ap.v_src = a.v_new;
+        ap.kv_dim = a.n_kv_heads * a.head_dim;
+        ap.n_rows = a.n_new;
+        ap.src_lstride = (int64_t)a.n_new * ap.kv_dim;
+        ap.seg = a.wseg;
+        hipError_t e = launch_append(dtype, ap, a.n_layers, st);
+        if (e != hipSuccess) return e;
+    }
+    if (mfma) {
         const int gqa = a.n_q_heads / a.n_kv_heads;
         const int tiles = (a.n_q * gqa + 15) / 16;
         dim3 g2((unsigned)(tiles * a.n_kv_heads), (unsigned)a.n_layers);
