@@ -334,6 +334,9 @@ vkv_status do_window(vkv_cache *c, int32_t stream, int32_t layer0, int32_t n_lay
     if (c->p.head_dim % 8 != 0 || c->p.head_dim > 128)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "window attention: head_dim %d unsupported",
                     c->p.head_dim);
+    // the kernels form slot offsets in 32 bits
+    if (c->layer_bytes > (int64_t)UINT32_MAX)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "window attention: a layer beyond 4 GiB");
     if (n_q <= 0) return VKV_STATUS_OK;
     WindowArgs a{};
     a.k = stream_layer_base(c, c->k, stream, layer0);

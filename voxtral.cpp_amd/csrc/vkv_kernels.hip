@@ -1228,17 +1228,23 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
 #pragma unroll
     for (int t = 0; t < KB; ++t) o[t] = float4_t{0, 0, 0, 0};
 
-    for (int jb = j_lo + wave * 16; jb < j_hi; jb += 64) {
+    // Software pipeline over two register sets: the next key block's K/V
+    // loads are in flight while the current one is reduced; indices clamp
+    // to the last key (blocks past the end are fully masked).
+    auto load_kv = [&](int jb, uint4 (&kr)[DL / 8], uint4 (&vr)[DL / 8])
+                       __attribute__((always_inline)) {
         // K and V of key jb+lr, dims [DL*lg, +DL): one contiguous run per lane
         const int jk = min(jb + lr, j_hi - 1);
         const uint32_t off = (uint32_t)slot_of(a.seg, jk) * (uint32_t)a.row_bytes +
                              (uint32_t)(g * D + DL * lg) * 2u;
-        uint4 kr[DL / 8], vr[DL / 8];
 #pragma unroll
         for (int t = 0; t < DL / 8; ++t) {
             kr[t] = reinterpret_cast<const uint4 *>(kl + off)[t];
             vr[t] = reinterpret_cast<const uint4 *>(vl + off)[t];
         }
+    };
+    auto process = [&](const uint4 (&kr)[DL / 8], const uint4 (&vr)[DL / 8], int jb)
+                       __attribute__((always_inline)) {
         // V rows into this wave's LDS tile (row lr, bytes [2*DL*lg, +2*DL));
         // the padded stride keeps rows 8-byte aligned: 8-byte stores
 #pragma unroll
@@ -1301,6 +1307,15 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
             }
         }
         __builtin_amdgcn_wave_barrier();
+        };
+    uint4 ka_[DL / 8], va_[DL / 8], kb_[DL / 8], vb_[DL / 8];
+    int jb0 = j_lo + wave * 16;
+    if (j_lo < j_hi) load_kv(jb0, ka_, va_);   // j_hi >= 1: clamped keys are valid
+    for (; jb0 < j_hi; jb0 += 128) {
+        load_kv(jb0 + 64, kb_, vb_);
+        process(ka_, va_, jb0);
+        load_kv(jb0 + 128, ka_, va_);
+        process(kb_, vb_, jb0 + 64);
     }
 
     // row sums over the 4 lane groups (they share m)
