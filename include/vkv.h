@@ -35,6 +35,11 @@ extern "C" {
 
 #define VKV_API_VERSION 1u
 #define VKV_MAX_BATCH_STREAMS 32
+/* Encoder streaming constants: VOXTRAL_ENC_WINDOW (include/voxtral.h:44),
+ * VOXTRAL_ENC_KV_MAX_NEW and VOXTRAL_ENC_KV_CAP (src/voxtral.cpp:39-40). */
+#define VKV_ENC_WINDOW 750
+#define VKV_ENC_MAX_NEW 128
+#define VKV_ENC_KV_CAP (VKV_ENC_WINDOW + VKV_ENC_MAX_NEW)
 
 /* Status values keep the numbering of voxtral_status (include/voxtral.h:97-110). */
 typedef enum vkv_status {
@@ -126,6 +131,47 @@ vkv_status vkv_enc_plan_build(int64_t q_start, int32_t n_new, int32_t capacity, 
                               vkv_enc_plan *out);
 /* voxtral_enc_kv_mask_allows (src/voxtral.cpp:3636-3638): 1 if allowed. */
 int32_t vkv_enc_mask_allows(int64_t kv_abs, int64_t q_abs, int32_t window);
+
+/* ---------------------------------------------------------------------------
+ * Encoder run scheduling (host only): which blocks of new encoder frames a
+ * streaming caller submits to vkv_enc_step, as encoder_kv_drive does
+ * (src/voxtral.cpp:4379-4426).  `logical` frames form one submission during
+ * feed; `physical` is the query block a submission never crosses (the
+ * reference's graph row count; this library needs no padding rows, so it only
+ * shapes the schedule).
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_enc_schedule {
+    int32_t logical;
+    int32_t physical;
+} vkv_enc_schedule;
+
+typedef struct vkv_enc_run {
+    int64_t q0;            /* first new frame of the run */
+    int32_t n;             /* frames in the run; 0 = nothing to submit now */
+    int32_t physical;      /* query block containing [q0, q0+n) */
+    int32_t warmup;        /* 1 for the 128-frame startup block */
+} vkv_enc_run;
+
+/* normalize_physical_rows (src/voxtral.cpp:104-111): the smallest of
+ * 4/8/16/32/64/128 not below rows (128 above). */
+int32_t vkv_enc_normalize_physical(int32_t rows);
+/* encoder_kv_schedule_from_env (src/voxtral.cpp:125-154) with the environment
+ * passed in: throughput != 0 is VOXTRAL_ENC_KV_MODE=throughput|offline; grid,
+ * logical, physical are VOXTRAL_ENC_KV_GRID, _LOGICAL_BATCH, _PHYSICAL_ROWS
+ * (<= 0 = unset).  Defaults 4/4. */
+vkv_status vkv_enc_schedule_make(int32_t throughput, int32_t grid, int32_t logical,
+                                 int32_t physical, vkv_enc_schedule *out);
+/* enc_frames_realizable (src/voxtral.cpp:3700-3702): encoder frames a Mel
+ * prefix of mel_frames yields. */
+int64_t vkv_enc_frames_realizable(int64_t mel_frames);
+/* One iteration of encoder_kv_drive (src/voxtral.cpp:4379-4426): the next run
+ * after `emitted` frames when `target` are realizable.  final != 0 is the
+ * finish flush; batch_terminal != 0 flushes in blocks of finish_physical
+ * (4/8/16/32/128; the reference's default is 8).  out->n == 0: stop (wait for
+ * more input, or done).  INVALID_ARGUMENT where the reference fails. */
+vkv_status vkv_enc_drive_next(int64_t emitted, int64_t target, int32_t final,
+                              const vkv_enc_schedule *schedule, int32_t finish_physical,
+                              int32_t batch_terminal, vkv_enc_run *out);
 
 /* ---------------------------------------------------------------------------
  * KV cache storage.

@@ -61,6 +61,11 @@ class EncPlan(ctypes.Structure):
                 ("evicted", ctypes.c_int64)]
 
 
+class EncRun(ctypes.Structure):
+    _fields_ = [("q0", ctypes.c_int64), ("n", ctypes.c_int32), ("physical", ctypes.c_int32),
+                ("warmup", ctypes.c_int32)]
+
+
 _P = ctypes.POINTER
 _vp = ctypes.c_void_p
 _i32, _i64, _u64, _u32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint32
@@ -72,6 +77,11 @@ _protos = {
     "orc_decoder_clear": (None, [_P(Ring), _i64]),
     "orc_enc_plan": (ctypes.c_bool, [_i64, _i32, _i32, _i32, _P(EncPlan)]),
     "orc_enc_mask_allows": (ctypes.c_bool, [_i64, _i64, _i32]),
+    "orc_enc_normalize_physical": (_i32, [_i32]),
+    "orc_enc_schedule": (None, [_i32, _i32, _i32, _i32, _P(_i32), _P(_i32)]),
+    "orc_enc_frames_realizable": (_i64, [_i64]),
+    "orc_enc_drive_next": (ctypes.c_bool, [_i64, _i64, ctypes.c_bool, _i32, _i32, _i32,
+                                           ctypes.c_bool, _P(EncRun)]),
     "orc_f32_to_f16_n": (None, [_vp, _vp, _i64]),
     "orc_f16_to_f32_n": (None, [_vp, _vp, _i64]),
     "orc_q8_0_quantize": (None, [_vp, _vp, _i64]),
@@ -135,6 +145,29 @@ def enc_plan(q_start, n_new, capacity, window):
 
 def enc_mask_allows(kv, q, window):
     return bool(lib.orc_enc_mask_allows(kv, q, window))
+
+
+def enc_normalize_physical(rows):
+    return int(lib.orc_enc_normalize_physical(rows))
+
+
+def enc_schedule(throughput=0, grid=0, logical=0, physical=0):
+    lg, ph = _i32(), _i32()
+    lib.orc_enc_schedule(throughput, grid, logical, physical, ctypes.byref(lg), ctypes.byref(ph))
+    return lg.value, ph.value
+
+
+def enc_frames_realizable(mel_frames):
+    return int(lib.orc_enc_frames_realizable(mel_frames))
+
+
+def enc_drive_next(emitted, target, final, logical, physical, finish_physical=8,
+                   batch_terminal=False):
+    """(q0, n, physical, warmup); n == 0: stop.  None where the reference fails."""
+    r = EncRun()
+    ok = lib.orc_enc_drive_next(emitted, target, bool(final), logical, physical, finish_physical,
+                                bool(batch_terminal), ctypes.byref(r))
+    return (r.q0, r.n, r.physical, r.warmup) if ok else None
 
 
 def segs_of(segs, n):

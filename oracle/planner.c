@@ -6,9 +6,15 @@
  *            decoder_kv_commit_plan   (src/voxtral.cpp:1590-1656)
  *   encoder: voxtral_enc_kv_mask_allows / enc_kv_ring_segments /
  *            voxtral_enc_kv_plan      (src/voxtral.cpp:3636-3692)
+ *   encoder run scheduling: normalize_physical_rows (:104-111),
+ *            encoder_kv_schedule_from_env (:125-154), enc_frames_realizable
+ *            (:3700-3702), encoder_kv_drive (:4379-4426)
  * Pinned by the known-answer vectors of tests/cpp/test_decoder_kv.cpp and
  * tests/cpp/test_encoder_kv.cpp (restated in tests/test_planner.py) and by a
- * brute-force slot->absolute-position ring model.
+ * brute-force slot->absolute-position ring model; the scheduling by closed
+ * forms and by the invariants the reference states for the drive (startup
+ * block, full logical batches during feed, no run across a query block, runs
+ * independent of the audio chunking), tests/test_enc_drive.py.
  */
 #include "vkv_oracle.h"
 
@@ -102,5 +108,77 @@ bool orc_enc_plan(int64_t q_start, int32_t n_new, int32_t capacity, int32_t wind
         int64_t new_lo = orc_max64(0, out->win_end - (int64_t)window);
         out->evicted = new_lo - old_lo;
     }
+    return true;
+}
+
+/* src/voxtral.cpp:104-111 */
+int32_t orc_enc_normalize_physical(int32_t rows) {
+    static const int32_t steps[] = {4, 8, 16, 32, 64};
+    for (int i = 0; i < 5; ++i)
+        if (rows <= steps[i]) return steps[i];
+    return 128;
+}
+
+/* src/voxtral.cpp:125-154 */
+void orc_enc_schedule(int32_t throughput, int32_t grid, int32_t logical, int32_t physical,
+                      int32_t *out_logical, int32_t *out_physical) {
+    const int32_t max_new = 128;
+    int32_t lg = 4, ph = 4;
+    if (throughput) {
+        *out_logical = *out_physical = max_new;
+        return;
+    }
+    if (grid > 0) {
+        lg = grid < max_new ? grid : max_new;
+        if (grid >= 32) ph = orc_enc_normalize_physical(grid);
+    }
+    if (logical > 0) lg = logical;
+    if (lg > max_new) lg = max_new;
+    ph = orc_enc_normalize_physical(physical > 0 ? physical : ph);
+    if (lg < 1) lg = 1;
+    if (lg > ph || ph % lg != 0) {
+        if (lg > ph) lg = ph;
+        while (lg > 1 && ph % lg != 0) --lg;
+    }
+    *out_logical = lg;
+    *out_physical = ph;
+}
+
+/* src/voxtral.cpp:3700-3702 */
+int64_t orc_enc_frames_realizable(int64_t mel_frames) {
+    if (mel_frames < 2) return 0;
+    return (mel_frames - 2) / 2 + 1;
+}
+
+/* src/voxtral.cpp:4379-4426: the body of the drive loop once; n = 0 where the
+ * loop breaks or ends. */
+bool orc_enc_drive_next(int64_t emitted, int64_t target, bool final, int32_t logical,
+                        int32_t physical, int32_t finish_physical, bool batch_terminal,
+                        orc_enc_run *out) {
+    const int32_t max_new = 128;
+    memset(out, 0, sizeof(*out));
+    if (!(emitted < target)) return true;
+    const int64_t rem = target - emitted;
+    if (emitted == 0 && !final && target < max_new) return true;
+    if (emitted == 0 && target >= max_new) {
+        out->q0 = 0;
+        out->n = max_new;
+        out->physical = max_new;
+        out->warmup = 1;
+        return true;
+    }
+    if (!final && rem < logical) return true;
+    const bool terminal = final && batch_terminal;
+    const int32_t p = terminal ? finish_physical : physical;
+    const int32_t lg = terminal ? finish_physical : logical;
+    if (p <= 0) return false;
+    const int32_t q_offset = (int32_t)(emitted % p);
+    int64_t n = lg;
+    if (p - q_offset < n) n = p - q_offset;
+    if (rem < n) n = rem;
+    if (n <= 0) return false;
+    out->q0 = emitted;
+    out->n = (int32_t)n;
+    out->physical = p;
     return true;
 }

@@ -97,6 +97,25 @@ void orc_decoder_clear(orc_ring *ring, int64_t capacity);
 bool orc_enc_plan(int64_t q_start, int32_t n_new, int32_t capacity, int32_t window, orc_enc_plan_t *out);
 bool orc_enc_mask_allows(int64_t kv_abs, int64_t q_abs, int32_t window);
 
+/* Encoder run scheduling (src/voxtral.cpp:104-111 normalize_physical_rows,
+ * :125-154 encoder_kv_schedule_from_env with the variables passed in (<= 0 =
+ * unset), :3700-3702 enc_frames_realizable, :4379-4426 one iteration of
+ * encoder_kv_drive). */
+typedef struct orc_enc_run {
+    int64_t q0;
+    int32_t n;          /* 0: stop */
+    int32_t physical;
+    int32_t warmup;
+} orc_enc_run;
+int32_t orc_enc_normalize_physical(int32_t rows);
+void orc_enc_schedule(int32_t throughput, int32_t grid, int32_t logical, int32_t physical,
+                      int32_t *out_logical, int32_t *out_physical);
+int64_t orc_enc_frames_realizable(int64_t mel_frames);
+/* false where the reference's drive fails */
+bool orc_enc_drive_next(int64_t emitted, int64_t target, bool final, int32_t logical,
+                        int32_t physical, int32_t finish_physical, bool batch_terminal,
+                        orc_enc_run *out);
+
 /* ---- numerics ---- */
 uint16_t orc_f32_to_f16(float f);
 float orc_f16_to_f32(uint16_t h);

@@ -42,6 +42,8 @@ def test_struct_layout_matches_c():
         "vkv_seg": (vkv.Seg, oracle.Seg),
         "vkv_plan": (vkv.Plan, oracle.Plan),
         "vkv_enc_plan": (vkv.EncPlan, oracle.EncPlan),
+        "vkv_enc_schedule": (vkv.EncSchedule, None),
+        "vkv_enc_run": (vkv.EncRun, oracle.EncRun),
         "vkv_cache_params": (vkv.CacheParams, None),
         "vkv_cache_layout": (vkv.CacheLayout, None),
     }

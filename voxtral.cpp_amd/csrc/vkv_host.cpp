@@ -438,6 +438,81 @@ int32_t vkv_enc_mask_allows(int64_t kv_abs, int64_t q_abs, int32_t window) {
     return kv_abs <= q_abs && kv_abs >= q_abs - (int64_t)(window - 1);
 }
 
+// src/voxtral.cpp:104-111
+int32_t vkv_enc_normalize_physical(int32_t rows) {
+    for (int32_t p = 4; p <= 64; p *= 2)
+        if (rows <= p) return p;
+    return VKV_ENC_MAX_NEW;
+}
+
+// src/voxtral.cpp:125-154; arguments <= 0 stand for unset variables
+vkv_status vkv_enc_schedule_make(int32_t throughput, int32_t grid, int32_t logical,
+                                 int32_t physical, vkv_enc_schedule *out) {
+    if (!out) return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder schedule: null out");
+    vkv_enc_schedule sc{4, 4};
+    if (throughput) {
+        sc.logical = sc.physical = VKV_ENC_MAX_NEW;
+        *out = sc;
+        return ok();
+    }
+    if (grid > 0) {   // the legacy grid knob: logical rows, a full grid from 32 up
+        sc.logical = std::min(grid, VKV_ENC_MAX_NEW);
+        if (grid >= 32) sc.physical = vkv_enc_normalize_physical(grid);
+    }
+    sc.logical = std::min(logical > 0 ? logical : sc.logical, VKV_ENC_MAX_NEW);
+    sc.physical = vkv_enc_normalize_physical(physical > 0 ? physical : sc.physical);
+    sc.logical = std::max(1, sc.logical);
+    // a physical block holds a whole number of logical batches
+    if (sc.logical > sc.physical || sc.physical % sc.logical != 0) {
+        sc.logical = std::min(sc.logical, sc.physical);
+        while (sc.logical > 1 && sc.physical % sc.logical != 0) --sc.logical;
+    }
+    *out = sc;
+    return ok();
+}
+
+// src/voxtral.cpp:3700-3702
+int64_t vkv_enc_frames_realizable(int64_t mel_frames) {
+    return mel_frames < 2 ? 0 : (mel_frames - 2) / 2 + 1;
+}
+
+// src/voxtral.cpp:4379-4426, one iteration of the loop
+vkv_status vkv_enc_drive_next(int64_t emitted, int64_t target, int32_t final,
+                              const vkv_enc_schedule *schedule, int32_t finish_physical,
+                              int32_t batch_terminal, vkv_enc_run *out) {
+    if (!out) return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder drive: null out");
+    std::memset(out, 0, sizeof(*out));
+    if (!schedule || schedule->logical <= 0 || schedule->physical <= 0 || emitted < 0)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder drive: bad schedule or position");
+    if (emitted >= target) return ok();   // done
+    const int64_t rem = target - emitted;
+    if (emitted == 0) {
+        // the 128-frame startup block runs once, as soon as it is realizable;
+        // nothing runs before it during feed
+        if (target >= VKV_ENC_MAX_NEW) {
+            out->q0 = 0;
+            out->n = VKV_ENC_MAX_NEW;
+            out->physical = VKV_ENC_MAX_NEW;
+            out->warmup = 1;
+            return ok();
+        }
+        if (!final) return ok();
+    }
+    if (!final && rem < schedule->logical) return ok();   // wait for a full logical batch
+    const bool terminal = final && batch_terminal;
+    const int32_t physical = terminal ? finish_physical : schedule->physical;
+    const int32_t logical = terminal ? finish_physical : schedule->logical;
+    if (physical <= 0)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder drive: finish block %d", physical);
+    const int32_t room = physical - (int32_t)(emitted % physical);
+    const int32_t n = (int32_t)std::min<int64_t>(std::min(logical, room), rem);
+    if (n <= 0) return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder drive: empty run");
+    out->q0 = emitted;
+    out->n = n;
+    out->physical = physical;
+    return ok();
+}
+
 // src/voxtral.cpp:3653-3692
 vkv_status vkv_enc_plan_build(int64_t q_start, int32_t n_new, int32_t capacity, int32_t window,
                               vkv_enc_plan *out) {

@@ -89,6 +89,15 @@ class EncPlan(ctypes.Structure):
                 ("evicted", ctypes.c_int64)]
 
 
+class EncSchedule(ctypes.Structure):
+    _fields_ = [("logical", ctypes.c_int32), ("physical", ctypes.c_int32)]
+
+
+class EncRun(ctypes.Structure):
+    _fields_ = [("q0", ctypes.c_int64), ("n", ctypes.c_int32), ("physical", ctypes.c_int32),
+                ("warmup", ctypes.c_int32)]
+
+
 class CacheParams(ctypes.Structure):
     _fields_ = [("struct_size", ctypes.c_uint32), ("n_streams", ctypes.c_int32),
                 ("n_layers", ctypes.c_int32), ("capacity", ctypes.c_int32),
@@ -118,6 +127,10 @@ PROTOTYPES = {
     "vkv_decoder_clear": (_i32, [_P(Ring), _i64]),
     "vkv_enc_plan_build": (_i32, [_i64, _i32, _i32, _i32, _P(EncPlan)]),
     "vkv_enc_mask_allows": (_i32, [_i64, _i64, _i32]),
+    "vkv_enc_normalize_physical": (_i32, [_i32]),
+    "vkv_enc_schedule_make": (_i32, [_i32, _i32, _i32, _i32, _P(EncSchedule)]),
+    "vkv_enc_frames_realizable": (_i64, [_i64]),
+    "vkv_enc_drive_next": (_i32, [_i64, _i64, _i32, _P(EncSchedule), _i32, _i32, _P(EncRun)]),
     "vkv_cache_create": (_i32, [_P(CacheParams), _P(_vp)]),
     "vkv_cache_destroy": (_i32, [_vp]),
     "vkv_cache_get_layout": (_i32, [_vp, _P(CacheLayout)]),
@@ -195,6 +208,32 @@ def enc_plan(q_start, n_new, capacity, window):
 
 def enc_mask_allows(kv_abs, q_abs, window):
     return bool(lib.vkv_enc_mask_allows(kv_abs, q_abs, window))
+
+
+ENC_WINDOW, ENC_MAX_NEW = 750, 128
+ENC_KV_CAP = ENC_WINDOW + ENC_MAX_NEW
+
+
+def enc_normalize_physical(rows):
+    return int(lib.vkv_enc_normalize_physical(rows))
+
+
+def enc_schedule(throughput=0, grid=0, logical=0, physical=0):
+    sc = EncSchedule()
+    check(lib.vkv_enc_schedule_make(throughput, grid, logical, physical, ctypes.byref(sc)))
+    return sc
+
+
+def enc_frames_realizable(mel_frames):
+    return int(lib.vkv_enc_frames_realizable(mel_frames))
+
+
+def enc_drive_next(emitted, target, final, schedule, finish_physical=8, batch_terminal=False):
+    """Next encoder run (EncRun; n == 0: stop), as encoder_kv_drive."""
+    r = EncRun()
+    check(lib.vkv_enc_drive_next(emitted, target, int(bool(final)), ctypes.byref(schedule),
+                                 finish_physical, int(bool(batch_terminal)), ctypes.byref(r)))
+    return r
 
 
 # cache --------------------------------------------------------------------
