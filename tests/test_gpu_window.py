@@ -125,3 +125,54 @@ def test_window_attn_entry_point_over_wrapped_segments():
                                           np.arange(1070, 1070 + n_q), 8, 4, 64, 25, 0.125)
             got = out[l].cpu().numpy().reshape(n_q, 8, 64)
             assert np.max(np.abs(got - want)) <= 2e-3
+
+
+@pytest.mark.parametrize("sched,batch_terminal", [((0, 0, 0, 0), True), ((0, 0, 8, 32), False)])
+def test_encoder_stream_driven_by_the_schedule(sched, batch_terminal):
+    """A streaming encoder over the ring, run by run as vkv_enc_drive_next
+    schedules it: the 128-frame startup block (16-row tiles x 8), small feed
+    batches, the finish flush, and the first ring wrap (frame 878); ring state
+    bit-exact and attention within 2e-3 of the oracle at sampled runs."""
+    L = 4
+    sc = vkv.enc_schedule(*sched)
+    mel_total, right_pad = 2000, 72
+    with vkv.Cache(n_streams=1, n_layers=L, capacity=ECAP, n_kv_heads=EH, head_dim=ED,
+                   n_q_heads=EH, dtype=vkv.F16) as c:
+        emitted, runs_done = 0, 0
+        chunks = [160] * (mel_total // 160) + [mel_total % 160]
+        fed = 0
+
+        def run_until_stop(target, final):
+            nonlocal emitted, runs_done
+            while True:
+                r = vkv.enc_drive_next(emitted, target, final, sc, 8, batch_terminal)
+                if r.n == 0:
+                    return
+                plan = vkv.enc_plan(r.q0, r.n, ECAP, EWIN)
+                q, k, v = enc_inputs(L, r.q0, r.n)
+                out = empty_f32(L, r.n, EH * ED)
+                c.enc_step(0, plan, EWIN, 0, L, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                           out.data_ptr(), 0.125, hip_stream=stream_ptr())
+                emitted += r.n
+                runs_done += 1
+                if r.warmup or runs_done % 37 == 0 or (r.q0 < ECAP <= r.q0 + r.n) or final:
+                    torch.cuda.synchronize()
+                    for l in (0, L - 1):
+                        for w in (0, 1):
+                            want = oracle.expected_layer(vkv.F16, ECAP, ECAP, EH * ED, emitted,
+                                                         SEED, (vkv.TAG_EK, vkv.TAG_EV)[w], 0, l)
+                            assert np.array_equal(layer_image(c, w, 0, l), want), (r.q0, l, w)
+                        want = oracle_window(c, l, np.arange(plan.win_start, plan.win_end),
+                                             q[0, l].cpu().numpy().reshape(r.n, EH, ED),
+                                             np.arange(r.q0, r.q0 + r.n), EH, EH, ED, EWIN, 0.125,
+                                             ECAP)
+                        got = out[l].cpu().numpy().reshape(r.n, EH, ED)
+                        assert np.max(np.abs(got - want)) <= 2e-3, (r.q0, r.n, l)
+
+        for ch in chunks:
+            fed += ch
+            run_until_stop(vkv.enc_frames_realizable(fed), False)
+        target = vkv.enc_frames_realizable(mel_total + right_pad)
+        run_until_stop(target, True)
+        assert emitted == target
+        print(f"encoder stream: {runs_done} runs, {emitted} frames", flush=True)
