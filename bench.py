@@ -12,6 +12,11 @@ the whole window, so there are no split partials to merge).  Inputs (Q, K, V
 for every timed step) are generated on the device before timing.
 
 Other workloads (--workload), reported on the same contract:
+  stream4096_f16  the decoder from an empty ring: steps 0..4095 (append at
+               pos, attend pos+1 keys; no wrap), every step timed; tokens/s
+               over the whole run, bytes summed over the growing windows.
+  layer1_f16   one decoder layer, 1024 positions prefilled, then one step per
+               token (append + attention over 1025 positions): a latency case.
   q8_0_batch8  the same decoder shape with q8_0 K/V (quantize-on-append,
                dequantize-in-register attention), 8 independent streams per
                step; tokens/s counts all 8 streams.
@@ -47,6 +52,8 @@ METRIC = "decode attn+KV-append tokens/s and achieved HBM GB/s (% of peak) at 81
 WORKLOADS = {
     "longform_f16": dict(dtype=1, dtype_name="f16", streams=1,
                          pmc="decode_f16_26x8192_pmc.json"),
+    "stream4096_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
+    "layer1_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "q8_0_batch8": dict(dtype=8, dtype_name="q8_0", streams=8,
                         pmc="decode_q8_0_8x26x8192_pmc.json"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
@@ -142,6 +149,48 @@ def gpu_decode(dtype, ns, steps, warmup):
     total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
     for s in range(ns):
         assert rings[s].used == CAP and rings[s].next_absolute_position == CAP + T
+    assert bool(torch.isfinite(out).all())
+    cache.close()
+    return total_ms, step_ms, wall
+
+
+def gpu_stream_from_empty(n_steps, layers, prefill):
+    """Decode steps at positions [prefill, prefill + n_steps) over an 8192 ring
+    holding positions [0, prefill) (no wrap); every step is timed."""
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    cache = vkv.Cache(n_streams=1, n_layers=layers, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
+                      n_q_heads=QH, dtype=vkv.F16)
+    rings = (vkv.Ring * 1)(vkv.new_ring(CAP))
+    if prefill:
+        plan = vkv.decoder_plan(rings[0], 0, prefill)
+        k0 = torch.empty(layers, prefill, KV_DIM, device="cuda")
+        v0 = torch.empty(layers, prefill, KV_DIM, device="cuda")
+        vkv.synth_rows(k0.data_ptr(), KV_DIM, SEED, vkv.TAG_K, nl=layers, p0=0, np_=prefill,
+                       hip_stream=sp)
+        vkv.synth_rows(v0.data_ptr(), KV_DIM, SEED, vkv.TAG_V, nl=layers, p0=0, np_=prefill,
+                       hip_stream=sp)
+        cache.append(0, 0, layers, vkv.plan_segs(plan.write_seg, plan.write_nseg), k0.data_ptr(),
+                     v0.data_ptr(), hip_stream=sp)
+        vkv.decoder_commit(rings[0], plan)
+    q = torch.empty(n_steps, layers, Q_DIM, device="cuda")
+    k = torch.empty(n_steps, layers, KV_DIM, device="cuda")
+    v = torch.empty(n_steps, layers, KV_DIM, device="cuda")
+    for t, tag, n in ((q, vkv.TAG_Q, Q_DIM), (k, vkv.TAG_K, KV_DIM), (v, vkv.TAG_V, KV_DIM)):
+        vkv.synth_rows(t.data_ptr(), n, SEED, tag, nl=layers, l_stride=1, p0=prefill, np_=n_steps,
+                       p_stride=layers, hip_stream=sp)
+    out = torch.empty(n_steps, layers, Q_DIM, device="cuda")
+    scale = 1.0 / (HD ** 0.5)
+
+    def step(i):
+        cache.decoder_step(0, rings, [prefill + i], 0, layers, q[i].data_ptr(), k[i].data_ptr(),
+                           v[i].data_ptr(), out[i].data_ptr(), scale, hip_stream=sp)
+
+    total_ms, step_ms, wall = timed_loop(step, n_steps, 0, st)
+    assert rings[0].next_absolute_position == prefill + n_steps
     assert bool(torch.isfinite(out).all())
     cache.close()
     return total_ms, step_ms, wall
@@ -264,8 +313,29 @@ def main():
         sys.exit(2)
 
     wl = WORKLOADS[args.workload]
-    traffic = load_traffic(wl["pmc"])
-    if args.workload == "encoder_f16":
+    traffic = load_traffic(wl["pmc"]) if wl["pmc"] else None
+    if args.workload in ("stream4096_f16", "layer1_f16"):
+        layers, prefill = (LAYERS, 0) if args.workload == "stream4096_f16" else (1, 1024)
+        n_steps = 4096 if args.workload == "stream4096_f16" else args.steps
+        total_ms, step_ms, wall = gpu_stream_from_empty(n_steps, layers, prefill)
+        args.steps, args.warmup = n_steps, 0
+        per_layer_fixed = 2 * KV_DIM * 4 + 2 * KV_DIM * 2 + Q_DIM * 4 + Q_DIM * 4
+        total_bytes = sum(layers * ((prefill + i + 1) * 2 * KV_DIM * 2 + per_layer_fixed)
+                          for i in range(n_steps))
+        bytes_step = total_bytes // n_steps
+        units_per_step = 1
+        res = {"metric": METRIC if args.workload == "stream4096_f16" else
+               "single-layer decode step latency (append + attention over 1025 positions)",
+               "unit": "tokens/s"}
+        config = {"workload": ("decoder KV stream: 26 layers, 4096 consecutive steps from an "
+                               "empty 8192-slot ring (no wrap), f16 KV, 32 q / 8 kv heads x 128")
+                  if args.workload == "stream4096_f16" else
+                  ("one decoder layer, 1024 positions prefilled, append position 1024.. and "
+                   "attend 1025.. positions, f16 KV, 32 q / 8 kv heads x 128"),
+                  "layers": layers, "window": CAP, "kv_heads": KVH, "q_heads": QH,
+                  "head_dim": HD, "streams": 1, "bytes": "mean over the steps"}
+        kernel = "k_decode<FmtF16> (append fused)"
+    elif args.workload == "encoder_f16":
         total_ms, step_ms, wall, n_keys = gpu_encoder(args.steps, args.warmup)
         bytes_step = encoder_bytes_per_chunk(n_keys)
         units_per_step = E_CHUNK
