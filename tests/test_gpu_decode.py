@@ -245,3 +245,27 @@ def test_q8_0_eight_streams_full_window():
                 assert np.max(np.abs(got - mimic)) <= 1e-2, (target, s)
                 assert np.max(np.abs(got - exact)) <= EXACT_TOL[vkv.Q8_0], (target, s)
             print(f"q8_0 8-stream step {target} ok", flush=True)
+
+
+@pytest.mark.parametrize("dtype", [vkv.F32, vkv.Q8_0])
+def test_one_pass_full_ring(dtype):
+    """26 layers x 8192 slots, one stream: 208 (layer, kv head) units take the
+    one-pass decode (one work group per unit, no merge kernel).  Three steps
+    across the first wrap; cache bit-exact, attention against the oracle."""
+    with vkv.Cache(n_streams=1, n_layers=26, capacity=8192, dtype=dtype) as c:
+        rings = (vkv.Ring * 1)(vkv.new_ring(8192))
+        prefill_by_append(c, rings[0], 0, 8191, 26)
+        out = empty_f32(1, 26, 4096)
+        for pos in (8191, 8192, 8193):
+            q, k, v = step_inputs(c, [pos])
+            plans = c.decoder_step(0, rings, [pos], 0, 26, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   out.data_ptr(), SCALE, hip_stream=stream_ptr())
+            check_cache_state(c, [0], [0, 25], 8192, {0: pos + 1})
+            for layer in (0, 13, 25):
+                slots, q_row = plan_slots(plans[0]), q[0, layer].cpu().numpy()
+                got = out[0, layer].cpu().numpy().reshape(32, 128)
+                mimic = oracle_decode(c, 0, layer, slots, q_row, mimic=True)
+                exact = oracle_decode(c, 0, layer, slots, q_row)
+                assert np.max(np.abs(got - mimic)) <= TOL[dtype], (pos, layer)
+                assert np.max(np.abs(got - exact)) <= EXACT_TOL[dtype], (pos, layer)
+            print(f"one-pass {dtype} step {pos} ok", flush=True)
