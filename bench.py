@@ -12,6 +12,9 @@ the whole window, so there are no split partials to merge).  Inputs (Q, K, V
 for every timed step) are generated on the device before timing.
 
 Other workloads (--workload), reported on the same contract:
+  longform_rope_f16  the default workload through vkv_decoder_step_rope: Q and
+               K arrive before RoPE (ggml mode 0, theta 1e6) and are rotated
+               inside the step.
   stream4096_f16  the decoder from an empty ring: steps 0..4095 (append at
                pos, attend pos+1 keys; no wrap), every step timed; tokens/s
                over the whole run, bytes summed over the growing windows.
@@ -52,6 +55,7 @@ METRIC = "decode attn+KV-append tokens/s and achieved HBM GB/s (% of peak) at 81
 WORKLOADS = {
     "longform_f16": dict(dtype=1, dtype_name="f16", streams=1,
                          pmc="decode_f16_26x8192_pmc.json"),
+    "longform_rope_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "stream4096_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "layer1_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "q8_0_batch8": dict(dtype=8, dtype_name="q8_0", streams=8,
@@ -106,7 +110,7 @@ def timed_loop(step, steps, warmup, st):
     return total_ms, step_ms, wall
 
 
-def gpu_decode(dtype, ns, steps, warmup):
+def gpu_decode(dtype, ns, steps, warmup, rope_theta=None):
     import torch
     import vkv
 
@@ -142,8 +146,14 @@ def gpu_decode(dtype, ns, steps, warmup):
     pos = [CAP]
 
     def step(i):
-        cache.decoder_step(0, rings, [pos[0]] * ns, 0, LAYERS, q[i].data_ptr(), k[i].data_ptr(),
-                           v[i].data_ptr(), out[i].data_ptr(), scale, hip_stream=sp)
+        if rope_theta is None:
+            cache.decoder_step(0, rings, [pos[0]] * ns, 0, LAYERS, q[i].data_ptr(),
+                               k[i].data_ptr(), v[i].data_ptr(), out[i].data_ptr(), scale,
+                               hip_stream=sp)
+        else:
+            cache.decoder_step_rope(0, rings, [pos[0]] * ns, 0, LAYERS, q[i].data_ptr(),
+                                    k[i].data_ptr(), v[i].data_ptr(), out[i].data_ptr(), scale,
+                                    rope_theta, hip_stream=sp)
         pos[0] += 1
 
     total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
@@ -349,7 +359,8 @@ def main():
         kernel = "k_window_mfma<64> + k_append<FmtF16> (one chunk)"
     else:
         ns = wl["streams"]
-        total_ms, step_ms, wall = gpu_decode(wl["dtype"], ns, args.steps, args.warmup)
+        rope = 1.0e6 if args.workload == "longform_rope_f16" else None
+        total_ms, step_ms, wall = gpu_decode(wl["dtype"], ns, args.steps, args.warmup, rope)
         bytes_step = ns * decode_bytes_per_stream_token(CAP, wl["dtype"])
         units_per_step = ns
         res = {"metric": METRIC, "unit": "tokens/s"}

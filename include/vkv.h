@@ -263,6 +263,25 @@ vkv_status vkv_decoder_step(vkv_cache *cache, int32_t stream0, int32_t n_streams
                             float *out, int32_t n_q_heads, float scale, vkv_plan *plans_out,
                             void *hip_stream);
 
+/* vkv_decoder_step with the decoder's RoPE fused in: q and k are the
+ * projections before RoPE, as build_decoder_layer rotates them
+ * (ggml_rope_ext mode 0, src/voxtral.cpp:2667-2671): pairs (2i, 2i+1) of
+ * each head turn by theta_i = position * rope_theta^(-2i/head_dim), with
+ * ggml's f32 running product for theta_i; cos/sin are evaluated in double and
+ * rounded to f32.  The new K row is rotated before it is stored, Q before the
+ * attention; V is stored as given.  Positions < 2^24. */
+vkv_status vkv_decoder_step_rope(vkv_cache *cache, int32_t stream0, int32_t n_streams,
+                                 vkv_ring *rings, const int64_t *positions, int32_t layer0,
+                                 int32_t n_layers, const float *q, const float *k, const float *v,
+                                 float *out, int32_t n_q_heads, float scale, float rope_theta,
+                                 vkv_plan *plans_out, void *hip_stream);
+
+/* The same RoPE in place on f32 rows x[n_outer][n_rows][row_len] (row_len a
+ * multiple of head_dim, head_dim % 8 == 0); row r is at position pos0 + r.
+ * For the prefill's q and k before vkv_decoder_prefill. */
+vkv_status vkv_rope(float *x, int64_t n_outer, int64_t n_rows, int32_t row_len, int32_t head_dim,
+                    int64_t pos0, float theta, void *hip_stream);
+
 /* Multi-token causal prefill of one stream (run_decoder_prefill,
  * src/voxtral.cpp:5161-5213; causal mask :3316-3323): plan n_tokens from
  * ring->next_absolute_position, append k/v ([layer][n_tokens][kv_dim]), then

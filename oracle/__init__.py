@@ -77,6 +77,7 @@ _protos = {
     "orc_decoder_clear": (None, [_P(Ring), _i64]),
     "orc_enc_plan": (ctypes.c_bool, [_i64, _i32, _i32, _i32, _P(EncPlan)]),
     "orc_enc_mask_allows": (ctypes.c_bool, [_i64, _i64, _i32]),
+    "orc_rope_f32": (None, [_vp, _i64, _i64, _i32, _i32, _i64, _f32]),
     "orc_enc_normalize_physical": (_i32, [_i32]),
     "orc_enc_schedule": (None, [_i32, _i32, _i32, _i32, _P(_i32), _P(_i32)]),
     "orc_enc_frames_realizable": (_i64, [_i64]),
@@ -145,6 +146,16 @@ def enc_plan(q_start, n_new, capacity, window):
 
 def enc_mask_allows(kv, q, window):
     return bool(lib.orc_enc_mask_allows(kv, q, window))
+
+
+def rope(x, head_dim, pos0, theta):
+    """ggml mode-0 RoPE of float32 rows x[..., n_rows, row_len] (row r at
+    position pos0 + r), returned as a new array."""
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    n_rows, row_len = y.shape[-2], y.shape[-1]
+    n_outer = y.size // (n_rows * row_len) if y.size else 0
+    lib.orc_rope_f32(_ptr(y), n_outer, n_rows, row_len, head_dim, pos0, theta)
+    return y
 
 
 def enc_normalize_physical(rows):

@@ -20,6 +20,7 @@
 #include "vkv_oracle.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 static uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
@@ -211,4 +212,33 @@ void orc_expected_layer(int dtype, uint8_t *dst, int64_t backing, int64_t capaci
         orc_synth_row(orc_row_key(seed, tag, stream, layer, pos), tmp, kv_dim);
         orc_row_from_f32(dtype, tmp, dst + s * row_bytes, kv_dim);
     }
+}
+
+/* ggml's CPU rope, mode 0 (src/voxtral.cpp:2667-2671 -> ggml_rope_ext):
+ * rope cache theta = p; theta *= theta_scale per pair; rotation
+ * x0*cos - x1*sin, x0*sin + x1*cos.  The Makefile builds without contraction. */
+void orc_rope_f32(float *x, int64_t n_outer, int64_t n_rows, int32_t row_len, int32_t head_dim,
+                  int64_t pos0, float theta) {
+    const float theta_scale = powf(theta, -2.0f / (float)head_dim);
+    const int32_t n_pairs = head_dim / 2;
+    float *cs = (float *)malloc(sizeof(float) * 2 * (size_t)n_pairs);
+    for (int64_t o = 0; o < n_outer; ++o) {
+        for (int64_t r = 0; r < n_rows; ++r) {
+            float th = (float)(pos0 + r);
+            for (int32_t i = 0; i < n_pairs; ++i) {
+                cs[2 * i] = (float)cos((double)th);
+                cs[2 * i + 1] = (float)sin((double)th);
+                th *= theta_scale;
+            }
+            float *row = x + (o * n_rows + r) * (int64_t)row_len;
+            for (int32_t h0 = 0; h0 < row_len; h0 += head_dim) {
+                for (int32_t i = 0; i < n_pairs; ++i) {
+                    const float x0 = row[h0 + 2 * i], x1 = row[h0 + 2 * i + 1];
+                    row[h0 + 2 * i] = x0 * cs[2 * i] - x1 * cs[2 * i + 1];
+                    row[h0 + 2 * i + 1] = x0 * cs[2 * i + 1] + x1 * cs[2 * i];
+                }
+            }
+        }
+    }
+    free(cs);
 }

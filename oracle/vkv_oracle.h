@@ -97,6 +97,15 @@ void orc_decoder_clear(orc_ring *ring, int64_t capacity);
 bool orc_enc_plan(int64_t q_start, int32_t n_new, int32_t capacity, int32_t window, orc_enc_plan_t *out);
 bool orc_enc_mask_allows(int64_t kv_abs, int64_t q_abs, int32_t window);
 
+/* ggml_rope_ext mode 0 as the reference's decoder applies it
+ * (src/voxtral.cpp:2667-2671), in place on x[n_outer][n_rows][row_len]; row r
+ * at position pos0 + r; pairs (2i, 2i+1) of each head_dim-wide head turn by
+ * theta_i, with theta_0 = position and theta_{i+1} = theta_i * powf(theta,
+ * -2/head_dim) in f32 (ggml's CPU rope cache); cos/sin in double rounded to
+ * f32. */
+void orc_rope_f32(float *x, int64_t n_outer, int64_t n_rows, int32_t row_len, int32_t head_dim,
+                  int64_t pos0, float theta);
+
 /* Encoder run scheduling (src/voxtral.cpp:104-111 normalize_physical_rows,
  * :125-154 encoder_kv_schedule_from_env with the variables passed in (<= 0 =
  * unset), :3700-3702 enc_frames_realizable, :4379-4426 one iteration of

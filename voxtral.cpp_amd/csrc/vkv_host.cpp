@@ -252,10 +252,17 @@ int32_t pick_chunk(const vkv_cache *c, int64_t units, int32_t n_kv_max, int32_t 
     }
 }
 
+// ggml's RoPE frequency step: powf(freq_base, -2/n_dims) (host libm, as the
+// reference's CPU path evaluates it)
+float rope_theta_scale(float theta, int32_t head_dim) {
+    return std::pow(theta, -2.0f / (float)head_dim);
+}
+
 vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t layer0,
                      int32_t n_layers, const SegPair *segs, const float *q, float *out,
                      int32_t n_q_heads, float scale, const float *k_new, const float *v_new,
-                     hipStream_t st) {
+                     hipStream_t st, const float *rope_theta = nullptr,
+                     const int64_t *rope_pos = nullptr) {
     const int32_t D = c->p.head_dim;
     const int32_t G = c->p.n_kv_heads;
     const int32_t gqa = n_q_heads / G;
@@ -292,6 +299,11 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     a.new_lstride = (int64_t)G * D;
     a.new_sstride = (int64_t)n_layers * a.new_lstride;
     for (int32_t s = 0; s < n_streams; ++s) a.seg[s] = segs[s];
+    if (rope_theta) {
+        a.rope = 1;
+        a.rope_theta_scale = rope_theta_scale(*rope_theta, D);
+        for (int32_t s = 0; s < n_streams; ++s) a.rope_pos[s] = (float)rope_pos[s];
+    }
     const int64_t units = (int64_t)n_streams * n_layers * G;
     a.chunk = pick_chunk(c, units, n_kv_max, gqa, &a.n_chunks);
     a.out = out;
@@ -729,11 +741,12 @@ vkv_status vkv_decode_attn(vkv_cache *cache, int32_t stream0, int32_t n_streams,
     return ok();
 }
 
-vkv_status vkv_decoder_step(vkv_cache *cache, int32_t stream0, int32_t n_streams, vkv_ring *rings,
-                            const int64_t *positions, int32_t layer0, int32_t n_layers,
-                            const float *q, const float *k, const float *v, float *out,
-                            int32_t n_q_heads, float scale, vkv_plan *plans_out,
-                            void *hip_stream) {
+namespace {
+vkv_status decoder_step_impl(vkv_cache *cache, int32_t stream0, int32_t n_streams,
+                             vkv_ring *rings, const int64_t *positions, int32_t layer0,
+                             int32_t n_layers, const float *q, const float *k, const float *v,
+                             float *out, int32_t n_q_heads, float scale, const float *rope_theta,
+                             vkv_plan *plans_out, void *hip_stream) {
     if (plans_out && n_streams > 0) std::memset(plans_out, 0, sizeof(vkv_plan) * (size_t)n_streams);
     if (vkv_status st = check_cache(cache, "decoder step")) return st;
     if (vkv_status st = check_span(cache, stream0, n_streams, layer0, n_layers, "decoder step"))
@@ -763,14 +776,64 @@ vkv_status vkv_decoder_step(vkv_cache *cache, int32_t stream0, int32_t n_streams
         if (n_kv < 1 || newest != plans[s].write_seg[0].slot)
             return fail(VKV_STATUS_INTERNAL_ERROR, "decoder step: plan window does not end at the new row");
     }
+    if (rope_theta) {
+        if (!(std::isfinite(*rope_theta) && *rope_theta > 0.0f))
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder step: rope theta");
+        for (int32_t s = 0; s < n_streams; ++s)
+            if (positions[s] >= (1 << 24))
+                return fail(VKV_STATUS_INVALID_ARGUMENT,
+                            "decoder step: rope position %lld beyond exact f32 (2^24)",
+                            (long long)positions[s]);
+    }
     DeviceGuard guard(cache->p.device);
     if (vkv_status st = do_decode(cache, stream0, n_streams, layer0, n_layers, segs, q, out,
-                                  n_q_heads, scale, k, v, as_stream(hip_stream)))
+                                  n_q_heads, scale, k, v, as_stream(hip_stream), rope_theta,
+                                  positions))
         return st;
     for (int32_t s = 0; s < n_streams; ++s) {
         vkv_decoder_commit(&rings[s], &plans[s]);
         if (plans_out) plans_out[s] = plans[s];
     }
+    return ok();
+}
+}  // namespace
+
+vkv_status vkv_decoder_step(vkv_cache *cache, int32_t stream0, int32_t n_streams, vkv_ring *rings,
+                            const int64_t *positions, int32_t layer0, int32_t n_layers,
+                            const float *q, const float *k, const float *v, float *out,
+                            int32_t n_q_heads, float scale, vkv_plan *plans_out,
+                            void *hip_stream) {
+    return decoder_step_impl(cache, stream0, n_streams, rings, positions, layer0, n_layers, q, k,
+                             v, out, n_q_heads, scale, nullptr, plans_out, hip_stream);
+}
+
+// src/voxtral.cpp:2667-2671 (RoPE of q and k) through :2854 (attention)
+vkv_status vkv_decoder_step_rope(vkv_cache *cache, int32_t stream0, int32_t n_streams,
+                                 vkv_ring *rings, const int64_t *positions, int32_t layer0,
+                                 int32_t n_layers, const float *q, const float *k, const float *v,
+                                 float *out, int32_t n_q_heads, float scale, float rope_theta,
+                                 vkv_plan *plans_out, void *hip_stream) {
+    return decoder_step_impl(cache, stream0, n_streams, rings, positions, layer0, n_layers, q, k,
+                             v, out, n_q_heads, scale, &rope_theta, plans_out, hip_stream);
+}
+
+// ggml_rope_ext mode 0 (src/voxtral.cpp:2667-2671) on f32 rows in place
+vkv_status vkv_rope(float *x, int64_t n_outer, int64_t n_rows, int32_t row_len, int32_t head_dim,
+                    int64_t pos0, float theta, void *hip_stream) {
+    if (n_outer < 0 || n_rows < 0 || row_len <= 0 || head_dim <= 0 || head_dim % 8 != 0 ||
+        row_len % head_dim != 0)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "rope: shape (row_len %d, head_dim %d)", row_len,
+                    head_dim);
+    if (!(std::isfinite(theta) && theta > 0.0f))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "rope: theta");
+    if (pos0 < 0 || pos0 + n_rows > (1 << 24))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "rope: positions beyond exact f32 (2^24)");
+    if (n_outer == 0 || n_rows == 0) return ok();
+    if (!x || (reinterpret_cast<uintptr_t>(x) & 15) != 0)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "rope: null or unaligned rows");
+    hipError_t e = launch_rope(x, n_outer, n_rows, row_len, head_dim, pos0,
+                               rope_theta_scale(theta, head_dim), as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "rope launch");
     return ok();
 }
 

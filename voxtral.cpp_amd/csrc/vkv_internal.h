@@ -50,6 +50,12 @@ struct DecodeArgs {
     const float *k_new;
     const float *v_new;
     int64_t new_sstride, new_lstride;
+    // RoPE of the step's Q and new K row (rope != 0): ggml mode 0 with
+    // theta_i = pos * theta_scale^i; the query/key of stream s sit at
+    // position rope_pos[s]
+    int32_t rope;
+    float rope_theta_scale;
+    float rope_pos[kMaxStreams];
     SegPair seg[kMaxStreams];
 };
 
@@ -104,6 +110,9 @@ hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st);
 hipError_t launch_q8_0_pack(const float *x, uint8_t *blocks, int64_t n, hipStream_t st);
 hipError_t launch_q8_0_unpack(const uint8_t *blocks, float *y, int64_t n, hipStream_t st);
 hipError_t launch_fill_zero(void *dst, int64_t bytes, hipStream_t st);
+// RoPE in place of x [n_outer][n_rows][row_len] f32; row r at position pos0 + r
+hipError_t launch_rope(float *x, int64_t n_outer, int64_t n_rows, int32_t row_len, int32_t head_dim,
+                       int64_t pos0, float theta_scale, hipStream_t st);
 hipError_t launch_synth(float *dst, int32_t row_len, uint64_t seed, uint32_t tag, int64_t s0,
                         int32_t ns, int64_t s_stride, int64_t l0, int32_t nl, int64_t l_stride,
                         int64_t p0, int32_t np, int64_t p_stride, hipStream_t st);

@@ -465,6 +465,70 @@ __device__ __forceinline__ void pv_accumulate<FmtQ8>(float (&acc)[4][8], const F
     }
 }
 
+// RoPE as ggml computes it on the CPU (mode 0: pairs (2i, 2i+1) of a head),
+// for the 4 pairs [pair0, pair0+4) held in x[8]: theta starts at the position
+// and is multiplied by theta_scale once per pair in f32 (ggml's running
+// product, so theta_i carries i roundings); cos/sin are evaluated in double
+// and rounded to f32; no contraction in the rotation.
+__device__ __forceinline__ void rope8(float (&x)[8], int pair0, float pos, float theta_scale) {
+#pragma clang fp contract(off)
+    float theta = pos;
+    for (int i = 0; i < pair0; ++i) theta *= theta_scale;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float c = (float)cos((double)theta);
+        const float sn = (float)sin((double)theta);
+        const float x0 = x[2 * j], x1 = x[2 * j + 1];
+        x[2 * j] = x0 * c - x1 * sn;
+        x[2 * j + 1] = x0 * sn + x1 * c;
+        theta *= theta_scale;
+    }
+}
+
+// The same angles once per work group: lane i of wave 0 computes pair i's
+// (cos, sin) with i steps of the running product (64 pairs = head_dim 128);
+// the caller synchronises before reading tab.
+__device__ __forceinline__ void rope_table(float2 *tab, float pos, float theta_scale) {
+#pragma clang fp contract(off)
+    if (threadIdx.x < 64) {
+        float theta = pos;
+        for (int i = 0; i < (int)threadIdx.x; ++i) theta *= theta_scale;
+        tab[threadIdx.x] = make_float2((float)cos((double)theta), (float)sin((double)theta));
+    }
+}
+
+// Rotation of the 4 pairs [pair0, pair0+4) held in x[8] by a rope_table.
+__device__ __forceinline__ void rope8_tab(float (&x)[8], int pair0, const float2 *tab) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float2 cs = tab[pair0 + j];
+        const float x0 = x[2 * j], x1 = x[2 * j + 1];
+        x[2 * j] = x0 * cs.x - x1 * cs.y;
+        x[2 * j + 1] = x0 * cs.y + x1 * cs.x;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_rope(float *x, int64_t n_outer, int64_t n_rows,
+                                              int32_t row_len, int32_t head_dim, int64_t pos0,
+                                              float theta_scale) {
+    const int64_t per_row = row_len / 8;
+    const int64_t total = n_outer * n_rows * per_row;
+    for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * 256) {
+        const int64_t row = (t / per_row) % n_rows;
+        const int e = (int)(t % per_row) * 8;
+        float v[8];
+        float4 *p = reinterpret_cast<float4 *>(x + (t / per_row) * row_len + e);
+        const float4 a = p[0], b = p[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        rope8(v, (e % head_dim) / 2, (float)(pos0 + row), theta_scale);
+        p[0] = make_float4(v[0], v[1], v[2], v[3]);
+        p[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
 // Work item of a decode work group: (stream s, layer, kv head g, chunk).
 struct DecodeItem {
     int g, chunk, layer, s;
@@ -498,7 +562,7 @@ __device__ __forceinline__ DecodeItem decode_item(const DecodeArgs &a) {
 template <class F>
 __device__ __forceinline__ void fused_append(const DecodeArgs &a, const SegPair &sp, int s,
                                              int layer, int64_t base, int e, int i_begin,
-                                             int i_end, bool leader) {
+                                             int i_end, bool leader, const float2 *rope_tab) {
     const int n_kv = sp.n0 + sp.n1;
     if (n_kv >= 1 && n_kv - 1 >= i_begin && n_kv - 1 < i_end && leader) {
         const int slot = slot_of(sp, n_kv - 1);
@@ -507,6 +571,7 @@ __device__ __forceinline__ void fused_append(const DecodeArgs &a, const SegPair 
         float xk[8], xv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) { xk[i] = kn[i]; xv[i] = vn[i]; }
+        if (a.rope) rope8_tab(xk, (e & 127) >> 1, rope_tab);
         store_new<F>(a.k_w + base + (int64_t)slot * a.row_bytes, e, xk, true);
         store_new<F>(a.v_w + base + (int64_t)slot * a.row_bytes, e, xv, true);
     }
@@ -601,36 +666,7 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
     const uint8_t *kl = a.k + base;
     const uint8_t *vl = a.v + base;
     const int e = g * D + c * 8;
-
-    typename F::QFrag qf[GQA];
-    {
-        const float *qp = a.q + (int64_t)s * a.q_sstride + (int64_t)layer * a.q_lstride +
-                          (int64_t)(g * GQA) * D + c * 8;
-#pragma unroll
-        for (int j = 0; j < GQA; ++j) {
-            const float4 q0 = reinterpret_cast<const float4 *>(qp + j * D)[0];
-            const float4 q1 = reinterpret_cast<const float4 *>(qp + j * D)[1];
-            const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-            qf[j] = F::make_q(qv);
-        }
-    }
-
-    static_assert(GQA == 4, "the score transposition maps 4 slots x 4 heads onto 16 lanes");
-    // Running softmax state.  After the score transposition lane c of a group
-    // owns slot-of-batch u = c>>2 and query head j = c&3: m and l are that
-    // head's running max and (partial) sum.  acc[j][i] is the unnormalised
-    // output of head j at dimension 8c+i over this lane group's slots.
-    const int hj = c & 3;
-    const int hu = c >> 2;
     const uint32_t row_bytes24 = (uint32_t)a.row_bytes;
-    float m = -INFINITY, l = 0.0f;
-    float acc[GQA][8];
-#pragma unroll
-    for (int j = 0; j < GQA; ++j)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[j][i] = 0.0f;
-    __shared__ float4 sm_p[W][16];   // per wave: p[slot of batch][head]
-
     const int i_begin = chunk * a.chunk;
     const int i_end = min(i_begin + a.chunk, n_kv);
     // Software pipeline: the next batch's K/V loads are in flight while the
@@ -648,6 +684,52 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
             vf[u] = F::template load<true>(vl + off, e);
         }
     };
+    typename F::Frag kf[NS][4], vf[NS][4];
+    constexpr int kStep = W * 16;   // slots covered by one batch of all waves
+    int b0 = i_begin + wave * 16;
+    // The first batches are requested before the prologue (RoPE table, Q,
+    // fused append) whenever none of them can hold the step's new row, the
+    // newest logical index n_kv-1; clamped indices then stay below it too.
+    const bool early = !FUSE || i_begin + (NS - 1) * kStep <= n_kv - 1;
+    if (early && i_begin < i_end) {   // i_end >= 1: every clamped index is a valid slot
+#pragma unroll
+        for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
+    }
+    __shared__ float2 sm_rope[64];
+    if (a.rope) {
+        rope_table(sm_rope, a.rope_pos[s], a.rope_theta_scale);
+        __syncthreads();
+    }
+
+    typename F::QFrag qf[GQA];
+    {
+        const float *qp = a.q + (int64_t)s * a.q_sstride + (int64_t)layer * a.q_lstride +
+                          (int64_t)(g * GQA) * D + c * 8;
+#pragma unroll
+        for (int j = 0; j < GQA; ++j) {
+            const float4 q0 = reinterpret_cast<const float4 *>(qp + j * D)[0];
+            const float4 q1 = reinterpret_cast<const float4 *>(qp + j * D)[1];
+            float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            if (a.rope) rope8_tab(qv, 4 * c, sm_rope);
+            qf[j] = F::make_q(qv);
+        }
+    }
+
+    static_assert(GQA == 4, "the score transposition maps 4 slots x 4 heads onto 16 lanes");
+    // Running softmax state.  After the score transposition lane c of a group
+    // owns slot-of-batch u = c>>2 and query head j = c&3: m and l are that
+    // head's running max and (partial) sum.  acc[j][i] is the unnormalised
+    // output of head j at dimension 8c+i over this lane group's slots.
+    const int hj = c & 3;
+    const int hu = c >> 2;
+    float m = -INFINITY, l = 0.0f;
+    float acc[GQA][8];
+#pragma unroll
+    for (int j = 0; j < GQA; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[j][i] = 0.0f;
+    __shared__ float4 sm_p[W][16];   // per wave: p[slot of batch][head]
+
     // (always inlined: the fragment arrays must stay in registers)
     auto process = [&](typename F::Frag (&kf)[4], typename F::Frag (&vf)[4], const int b0)
                        __attribute__((always_inline)) {
@@ -699,7 +781,7 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
         pv_accumulate<F>(acc, vf, pw);
     };
     if (FUSE) {
-        fused_append<F>(a, sp, s, layer, base, e, i_begin, i_end, wave == 0 && grp == 0);
+        fused_append<F>(a, sp, s, layer, base, e, i_begin, i_end, wave == 0 && grp == 0, sm_rope);
         __syncthreads();
     }
 
@@ -709,10 +791,7 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
     // handles NS batches and the prefetches are unconditional (indices clamp
     // to the last valid slot, an L2 hit; batches past the end are fully
     // masked), so the wait counts stay exact.
-    typename F::Frag kf[NS][4], vf[NS][4];
-    constexpr int kStep = W * 16;   // slots covered by one batch of all waves
-    int b0 = i_begin + wave * 16;
-    if (i_begin < i_end) {   // i_end >= 1: every clamped index is a valid slot
+    if (!early && i_begin < i_end) {
 #pragma unroll
         for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
     }
@@ -829,6 +908,39 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
     const __amdgpu_buffer_rsrc_t v_rs =
         __builtin_amdgcn_make_buffer_rsrc((void *)vl, (short)0, (int)n_rec, 0x00020000);
     const Q8LaneOff qlo = q8_lane_off(e);
+    const uint32_t row_bytes24 = (uint32_t)a.row_bytes;
+    const int i_begin = it.chunk * a.chunk;
+    const int i_end = min(i_begin + a.chunk, n_kv);
+    // A step of a wave covers SB sub-batches of 16 slots: [b, b + 16 SB).
+    using Frags = FmtQ8::Frag[SB][4];
+    auto load_step = [&](int b, Frags &kf, Frags &vf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int sb = 0; sb < SB; ++sb)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                // past the chunk end: reload the last valid slot (masked later)
+                const int ix = min(b + 16 * sb + 4 * kg + u, i_end - 1);
+                const uint32_t off = __umul24((uint32_t)slot_of(sp, ix), row_bytes24);
+                kf[sb][u] = q8_load_buf(k_rs, off, qlo);
+                vf[sb][u] = q8_load_buf(v_rs, off, qlo);
+            }
+    };
+    Frags kf[NS], vf[NS];
+    constexpr int kStep = W * 16 * SB;
+    int b0 = i_begin + wave * 16 * SB;
+    // The first steps are requested before the prologue (RoPE table, Q,
+    // fused append) whenever none of them can hold the step's new row, the
+    // newest logical index n_kv-1; clamped indices then stay below it too.
+    const bool early = !FUSE || i_begin + (NS - 1) * kStep <= n_kv - 1;
+    if (early && i_begin < i_end) {   // i_end >= 1: every clamped index is a valid slot
+#pragma unroll
+        for (int p = 0; p < NS - 1; ++p) load_step(b0 + p * kStep, kf[p], vf[p]);
+    }
+    __shared__ float2 sm_rope[64];
+    if (a.rope) {
+        rope_table(sm_rope, a.rope_pos[s], a.rope_theta_scale);
+        __syncthreads();
+    }
 
     // Q of head r, block t, quants [8kg, 8kg+8): the B operand of QK,
     // quantized as the cache is (d = amax/127, id = 1/d, round half away from
@@ -848,6 +960,7 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
                                          : make_float4(0.f, 0.f, 0.f, 0.f);
             x[0] = q0.x; x[1] = q0.y; x[2] = q0.z; x[3] = q0.w;
             x[4] = q1.x; x[5] = q1.y; x[6] = q1.z; x[7] = q1.w;
+            if (a.rope) rope8_tab(x, 16 * t + 4 * kg, sm_rope);
             float amax = 0.0f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
@@ -866,7 +979,6 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
 
     // Score lanes (r < 4): running max m and partial sum l of head r, and
     // o[T] = O^T tile T: dims 16T + 4kg + i of head r.
-    const uint32_t row_bytes24 = (uint32_t)a.row_bytes;
     float m = -INFINITY, l = 0.0f;
     float4v_t o[8];
 #pragma unroll
@@ -876,22 +988,6 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
     __shared__ float4 sm_dk[W][SB][16];  // per wave: d_k[slot][block]
     __shared__ float4 sm_dv[W][SB][16];  // per wave: d_v[slot][block]
 
-    const int i_begin = it.chunk * a.chunk;
-    const int i_end = min(i_begin + a.chunk, n_kv);
-    // A step of a wave covers SB sub-batches of 16 slots: [b, b + 16 SB).
-    using Frags = FmtQ8::Frag[SB][4];
-    auto load_step = [&](int b, Frags &kf, Frags &vf) __attribute__((always_inline)) {
-#pragma unroll
-        for (int sb = 0; sb < SB; ++sb)
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                // past the chunk end: reload the last valid slot (masked later)
-                const int ix = min(b + 16 * sb + 4 * kg + u, i_end - 1);
-                const uint32_t off = __umul24((uint32_t)slot_of(sp, ix), row_bytes24);
-                kf[sb][u] = q8_load_buf(k_rs, off, qlo);
-                vf[sb][u] = q8_load_buf(v_rs, off, qlo);
-            }
-    };
     // The sub-batches are independent up to the softmax, which takes one
     // joint max (one cross-lane chain) and one rescale decision per step.
     auto process = [&](const Frags &kf, const Frags &vf, const int b0)
@@ -989,14 +1085,12 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
             }
     };
     if (FUSE) {
-        fused_append<FmtQ8>(a, sp, s, layer, base, e, i_begin, i_end, wave == 0 && kg == 0);
+        fused_append<FmtQ8>(a, sp, s, layer, base, e, i_begin, i_end, wave == 0 && kg == 0,
+                            sm_rope);
         __syncthreads();
     }
 
-    Frags kf[NS], vf[NS];
-    constexpr int kStep = W * 16 * SB;
-    int b0 = i_begin + wave * 16 * SB;
-    if (i_begin < i_end) {   // i_end >= 1: every clamped index is a valid slot
+    if (!early && i_begin < i_end) {
 #pragma unroll
         for (int p = 0; p < NS - 1; ++p) load_step(b0 + p * kStep, kf[p], vf[p]);
     }
@@ -1568,6 +1662,15 @@ hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st) {
     case VKV_DTYPE_Q8_0: hipLaunchKernelGGL(k_window<FmtQ8>, grid, dim3(64), 0, st, a); break;
     default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(float *x, int64_t n_outer, int64_t n_rows, int32_t row_len, int32_t head_dim,
+                       int64_t pos0, float theta_scale, hipStream_t st) {
+    const int64_t n = n_outer * n_rows * (row_len / 8);
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_rope, dim3(grid_for(n, 256, 65536)), dim3(256), 0, st, x, n_outer, n_rows,
+                       row_len, head_dim, pos0, theta_scale);
     return hipGetLastError();
 }
 

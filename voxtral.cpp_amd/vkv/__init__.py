@@ -127,6 +127,10 @@ PROTOTYPES = {
     "vkv_decoder_clear": (_i32, [_P(Ring), _i64]),
     "vkv_enc_plan_build": (_i32, [_i64, _i32, _i32, _i32, _P(EncPlan)]),
     "vkv_enc_mask_allows": (_i32, [_i64, _i64, _i32]),
+    "vkv_decoder_step_rope": (_i32, [_vp, _i32, _i32, _P(Ring), _P(_i64), _i32, _i32, _vp, _vp,
+                                     _vp, _vp, _i32, ctypes.c_float, ctypes.c_float, _P(Plan),
+                                     _vp]),
+    "vkv_rope": (_i32, [_vp, _i64, _i64, _i32, _i32, _i64, ctypes.c_float, _vp]),
     "vkv_enc_normalize_physical": (_i32, [_i32]),
     "vkv_enc_schedule_make": (_i32, [_i32, _i32, _i32, _i32, _P(EncSchedule)]),
     "vkv_enc_frames_realizable": (_i64, [_i64]),
@@ -310,6 +314,17 @@ class Cache:
                                    plans, hip_stream))
         return plans
 
+    def decoder_step_rope(self, stream0, rings, positions, layer0, n_layers, q_ptr, k_ptr, v_ptr,
+                          out_ptr, scale, rope_theta, hip_stream=0, n_q_heads=None):
+        """decoder_step with q/k before RoPE (rotated inside, ggml mode 0)."""
+        ns = len(rings)
+        pos = (_i64 * ns)(*positions)
+        plans = (Plan * ns)()
+        check(lib.vkv_decoder_step_rope(self.handle, stream0, ns, rings, pos, layer0, n_layers,
+                                        q_ptr, k_ptr, v_ptr, out_ptr, n_q_heads or self.n_q_heads,
+                                        scale, rope_theta, plans, hip_stream))
+        return plans
+
     def decoder_prefill(self, stream, ring, layer0, n_layers, n_tokens, q_ptr, k_ptr, v_ptr,
                         out_ptr, scale, hip_stream=0, n_q_heads=None):
         check(lib.vkv_decoder_prefill(self.handle, stream, ctypes.byref(ring), layer0, n_layers,
@@ -328,6 +343,11 @@ class Cache:
         check(lib.vkv_window_attn(self.handle, stream, layer0, n_layers, arr, n, key_pos0, q_pos0,
                                   n_q, window, q_ptr, out_ptr, n_q_heads or self.n_q_heads, scale,
                                   hip_stream))
+
+
+def rope(x_ptr, n_outer, n_rows, row_len, head_dim, pos0, theta, hip_stream=0):
+    """RoPE (ggml mode 0) in place on device f32 rows [n_outer][n_rows][row_len]."""
+    check(lib.vkv_rope(x_ptr, n_outer, n_rows, row_len, head_dim, pos0, theta, hip_stream))
 
 
 def q8_0_pack(x_ptr, blocks_ptr, n, hip_stream=0):
