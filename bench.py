@@ -26,6 +26,11 @@ Other workloads (--workload), reported on the same contract:
   encoder_f16  the encoder's streaming window: 32 layers, 32 heads x 64, an
                878-slot ring, window 750, 16 new frames per chunk appended and
                attended as a 16-query block (MFMA tile); frames/s.
+  decoder_weights_q4km  the decoder step's projections on Q4_K_M weights
+               (random valid blocks): per layer RMSNorm+Q/K/V (one call), O +
+               residual, RMSNorm*(1+ada)+SwiGLU W1/W3, W2 + residual; then the
+               final norm + the 131072-row Q6_K logits -- 105 vkv_matvec
+               calls, 2.24 GB of weights per token; tokens/s.
 
 Prints one JSON line: throughput, the roofline of the step (algorithmic bytes /
 average step time from HIP events on the launch stream), the HBM traffic from
@@ -62,7 +67,133 @@ WORKLOADS = {
                         pmc="decode_q8_0_8x26x8192_pmc.json"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
                         pmc="encoder_f16_32x750_pmc.json"),
+    "decoder_weights_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k (int8 dot)", streams=1,
+                                 pmc="matvec_q4km_26l_pmc.json",
+                                 data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs, "
+                                      "generated on device)"),
 }
+
+# decoder projections: (name, dtype, rows, n_in); ggml Q4_K = 12, Q6_K = 14
+DIM, HIDDEN, VOCAB = 3072, 9216, 131072
+LAYER_MATS = [("attn_q", 12, Q_DIM, DIM), ("attn_k", 12, KV_DIM, DIM), ("attn_v", 14, KV_DIM, DIM),
+              ("attn_o", 12, DIM, Q_DIM), ("ffn_w1", 12, HIDDEN, DIM), ("ffn_w3", 12, HIDDEN, DIM),
+              ("ffn_w2", 14, DIM, HIDDEN)]
+KQ_BLOCK = {12: 144, 14: 210}
+
+
+def mat_bytes(dtype, rows, n_in):
+    return rows * (n_in // 256) * KQ_BLOCK[dtype]
+
+
+def weights_bytes_per_token():
+    per_layer = sum(mat_bytes(dt, r, n) for _, dt, r, n in LAYER_MATS)
+    return LAYERS * per_layer + mat_bytes(14, VOCAB, DIM)
+
+
+def random_kq_device(dtype, rows, n_in, gen):
+    """Random valid k-quant blocks on the device: random bytes, fp16 scales set
+    to finite moderate values."""
+    import torch
+    nb = rows * (n_in // 256)
+    w = torch.randint(0, 256, (nb, KQ_BLOCK[dtype]), dtype=torch.uint8, device="cuda",
+                      generator=gen)
+    if dtype == 12:
+        w[:, 0:2] = torch.empty(nb, dtype=torch.float16, device="cuda").uniform_(
+            2e-4, 4e-3, generator=gen).view(torch.uint8).view(nb, 2)
+        w[:, 2:4] = torch.empty(nb, dtype=torch.float16, device="cuda").uniform_(
+            1e-4, 2e-3, generator=gen).view(torch.uint8).view(nb, 2)
+    else:
+        w[:, 208:210] = torch.empty(nb, dtype=torch.float16, device="cuda").uniform_(
+            1e-5, 2e-4, generator=gen).view(torch.uint8).view(nb, 2)
+    return w.view(-1)
+
+
+def gpu_weights(steps, warmup):
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED)
+    layers = [{name: random_kq_device(dt, r, n, gen) for name, dt, r, n in LAYER_MATS}
+              for _ in range(LAYERS)]
+    logits_w = random_kq_device(14, VOCAB, DIM, gen)
+    norms = torch.empty(LAYERS * 2 + 1, DIM, device="cuda").uniform_(0.5, 1.5, generator=gen)
+    ada = torch.empty(LAYERS, DIM, device="cuda").uniform_(-0.3, 0.3, generator=gen)
+    x0 = torch.randn(DIM, device="cuda", generator=gen)
+    attn = torch.randn(Q_DIM, device="cuda", generator=gen)   # stands in for attention output
+    x = torch.empty(DIM, device="cuda")
+    q, k, v = (torch.empty(n, device="cuda") for n in (Q_DIM, KV_DIM, KV_DIM))
+    h = torch.empty(HIDDEN, device="cuda")
+    logits = torch.empty(VOCAB, device="cuda")
+    eps = 1e-5
+
+    def step(_):
+        x.copy_(x0)
+        xp = x.data_ptr()
+        for l, L in enumerate(layers):
+            vkv.matvec(xp, DIM, [(L["attn_q"].data_ptr(), 12, Q_DIM, q.data_ptr()),
+                                 (L["attn_k"].data_ptr(), 12, KV_DIM, k.data_ptr()),
+                                 (L["attn_v"].data_ptr(), 14, KV_DIM, v.data_ptr())],
+                       norm_w_ptr=norms[2 * l].data_ptr(), eps=eps, hip_stream=sp)
+            vkv.matvec(attn.data_ptr(), Q_DIM,
+                       [(L["attn_o"].data_ptr(), 12, DIM, xp, xp)], hip_stream=sp)
+            vkv.matvec(xp, DIM, [(L["ffn_w1"].data_ptr(), 12, HIDDEN, h.data_ptr()),
+                                 (L["ffn_w3"].data_ptr(), 12, HIDDEN, None)],
+                       norm_w_ptr=norms[2 * l + 1].data_ptr(), ada_ptr=ada[l].data_ptr(),
+                       eps=eps, epilogue=vkv.MV_SWIGLU, hip_stream=sp)
+            vkv.matvec(h.data_ptr(), HIDDEN, [(L["ffn_w2"].data_ptr(), 14, DIM, xp, xp)],
+                       hip_stream=sp)
+        vkv.matvec(xp, DIM, [(logits_w.data_ptr(), 14, VOCAB, logits.data_ptr())],
+                   norm_w_ptr=norms[2 * LAYERS].data_ptr(), eps=eps, hip_stream=sp)
+
+    total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
+    assert bool(torch.isfinite(logits).all()) and bool(torch.isfinite(x).all())
+    return total_ms, step_ms, wall
+
+
+def cpu_weights_leg(target_seconds):
+    """The oracle's restatement of ggml's CPU matvec (Q8_K input, generic
+    per-block integer dots), threaded over rows, on one layer's seven matrices
+    and the logits matrix; a token's time = 26 x layer + logits."""
+    import numpy as np
+
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(SEED)
+
+    def mat(dt, r, n):
+        w = rng.integers(0, 256, size=(r * (n // 256), KQ_BLOCK[dt]), dtype=np.uint8)
+        if dt == 12:
+            w[:, 0:2] = rng.uniform(2e-4, 4e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+            w[:, 2:4] = rng.uniform(1e-4, 2e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        else:
+            w[:, 208:210] = rng.uniform(1e-5, 2e-4, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        return w.reshape(-1)
+
+    mats = [(dt, r, n, mat(dt, r, n)) for _, dt, r, n in LAYER_MATS]
+    lw = mat(14, VOCAB, DIM)
+    xs = {n: rng.standard_normal(n).astype(np.float32) for n in (DIM, Q_DIM, HIDDEN)}
+    t_layer = t_logits = 0.0
+    reps = 0
+    t0 = time.perf_counter()
+    while reps < 1 or (time.perf_counter() - t0 < target_seconds and reps < 20):
+        a = time.perf_counter()
+        for dt, r, n, w in mats:
+            oracle.matvec(dt, w, r, n, xs[n], n_threads=threads)
+        b = time.perf_counter()
+        oracle.matvec(14, lw, VOCAB, DIM, xs[DIM], n_threads=threads)
+        c = time.perf_counter()
+        t_layer += b - a
+        t_logits += c - b
+        reps += 1
+    token_s = (LAYERS * t_layer + t_logits) / reps
+    return {"value": 1.0 / token_s, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} x (one layer's 7 projections + the 131072-row logits) of the "
+                      f"oracle's restatement of ggml's generic CPU q4_K/q6_K x q8_K matvec, "
+                      f"{threads} threads; token = 26 x layer + logits"}
 
 
 def elem_bytes(dtype):
@@ -345,6 +476,19 @@ def main():
                   "layers": layers, "window": CAP, "kv_heads": KVH, "q_heads": QH,
                   "head_dim": HD, "streams": 1, "bytes": "mean over the steps"}
         kernel = "k_decode<FmtF16> (append fused)"
+    elif args.workload == "decoder_weights_q4km":
+        total_ms, step_ms, wall = gpu_weights(args.steps, args.warmup)
+        bytes_step = weights_bytes_per_token()
+        units_per_step = 1
+        res = {"metric": "decoder projection tokens/s and HBM GB/s on Q4_K_M weights "
+                         "(26 layers + logits)", "unit": "tokens/s"}
+        config = {"workload": "decoder step projections, one token: 26 x (RMSNorm + Q/K/V, "
+                              "O + residual, RMSNorm*(1+ada) + SwiGLU W1/W3, W2 + residual) + "
+                              "final norm + 131072-row logits; Q4_K_M mix (attn_v, ffn_w2, "
+                              "output Q6_K; others Q4_K)",
+                  "layers": LAYERS, "dim": DIM, "hidden": HIDDEN, "vocab": VOCAB,
+                  "weight_bytes_per_token": bytes_step, "calls_per_token": 4 * LAYERS + 1}
+        kernel = "k_matvec (105 launches per token)"
     elif args.workload == "encoder_f16":
         total_ms, step_ms, wall, n_keys = gpu_encoder(args.steps, args.warmup)
         bytes_step = encoder_bytes_per_chunk(n_keys)
@@ -384,7 +528,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": wl["dtype_name"],
-        "data": "synthetic (seeded integer Irwin-Hall N(0,1) Q/K/V, generated on device)",
+        "data": wl.get("data", "synthetic (seeded integer Irwin-Hall N(0,1) Q/K/V, generated on "
+                               "device)"),
         "config": config,
         "hbm_gbps": round(bytes_step / (ms_per_step * 1e-3) / 1e9, 1),
         "pct_hbm_peak": round(100 * bytes_step / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
@@ -396,7 +541,9 @@ def main():
                      "avg_launch_ms": round(step_avg, 5)},
         "wall_s": round(wall, 3),
     })
-    if not args.no_cpu and args.workload != "encoder_f16":
+    if not args.no_cpu and args.workload == "decoder_weights_q4km":
+        res["cpu_baseline"] = cpu_weights_leg(args.cpu_seconds)
+    elif not args.no_cpu and args.workload != "encoder_f16":
         res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds)
     print(json.dumps(res), flush=True)
 

@@ -57,7 +57,11 @@ typedef enum vkv_status {
 typedef enum vkv_dtype {
     VKV_DTYPE_F32 = 0,
     VKV_DTYPE_F16 = 1,
-    VKV_DTYPE_Q8_0 = 8
+    VKV_DTYPE_Q8_0 = 8,
+    /* decoder weights (ggml block formats, 256 elements per block) */
+    VKV_DTYPE_Q4_K = 12,   /* 144 B: fp16 d, fp16 dmin, 6-bit scales/mins, 4-bit codes */
+    VKV_DTYPE_Q6_K = 14,   /* 210 B: 4+2-bit codes, int8 scales per 16, fp16 d */
+    VKV_DTYPE_Q8_K = 15    /* 292 B: f32 d, int8 codes, int16 sums per 16 (activations) */
 } vkv_dtype;
 
 /* Decoder ring metadata: voxtral_decoder_kv_ring (src/voxtral-internal.h:195-204).
@@ -321,6 +325,52 @@ vkv_status vkv_window_attn(vkv_cache *cache, int32_t stream, int32_t layer0, int
  * ------------------------------------------------------------------------- */
 vkv_status vkv_q8_0_pack(const float *x, void *blocks, int64_t n, void *hip_stream);
 vkv_status vkv_q8_0_unpack(const void *blocks, float *y, int64_t n, void *hip_stream);
+
+/* ---------------------------------------------------------------------------
+ * Decoder projections on ggml Q4_K / Q6_K weights: ggml_mul_mat(W, x) for one
+ * token (src/voxtral.cpp:2656-2659 Q/K/V, :2857 O, :2879-2883 SwiGLU FFN),
+ * with the RMSNorm that precedes them (:2653-2654, :2861-2862) and the ada
+ * time conditioning (:2864-2874) fused into the input side.
+ *
+ * The input is formed as the CPU path forms it: h = rms_norm(x, eps) * norm_w
+ * (sum of squares in double, mean rounded to f32, scale = 1/sqrtf(mean+eps)),
+ * then h + h * ada; or h = x when norm_w is NULL.  h is quantized to Q8_K
+ * (ggml quantize_row_q8_K_ref) and every row is an integer dot product per
+ * 256-block, scaled by fp16(d) * d_x (Q4_K: minus fp16(dmin) * d_x * the
+ * mins against 32-element sums).  Rows are W's rows in ggml's row-major block
+ * layout, i.e. a GGUF tensor's bytes unchanged.
+ * ------------------------------------------------------------------------- */
+#define VKV_MV_MAX_IN 12288      /* n_in limit (multiple of 256) */
+#define VKV_MV_MAX_OUTS 4        /* matrices per call */
+
+typedef struct vkv_mv_out {
+    const void *w;        /* [n_rows][n_in/256] Q4_K or Q6_K blocks, device memory */
+    int32_t dtype;        /* VKV_DTYPE_Q4_K or VKV_DTYPE_Q6_K */
+    int32_t n_rows;
+    float *y;             /* [n_rows] */
+    const float *add;     /* NULL, or the residual: y = add + W h (may alias y) */
+} vkv_mv_out;
+
+#define VKV_MV_STORE 0
+#define VKV_MV_SWIGLU 1   /* n_outs = 2, equal rows and dtype: outs[0].y = silu(W0 h) * (W1 h) */
+
+/* y_k = W_k h for up to VKV_MV_MAX_OUTS matrices reading the same input (the
+ * Q/K/V projections in one call).  x, norm_w, ada: 16-byte aligned device
+ * arrays of n_in floats; ada requires norm_w. */
+vkv_status vkv_matvec(const float *x, int64_t n_in, const float *norm_w, const float *ada,
+                      float eps, const vkv_mv_out *outs, int32_t n_outs, int32_t epilogue,
+                      void *hip_stream);
+
+/* The input side alone: h quantized to n/256 ggml block_q8_K (292 B each,
+ * 4-byte aligned device memory); n <= VKV_MV_MAX_IN. */
+vkv_status vkv_quantize_q8_k(const float *x, int64_t n, const float *norm_w, const float *ada,
+                             float eps, void *blocks, void *hip_stream);
+
+/* ggml dequantize_row_q4_K / _q6_K of n elements (n % 256 == 0) to f32: the
+ * token-embedding lookup (ggml_get_rows on tok_embeddings, src/voxtral.cpp:
+ * 3008) for one row of the table. */
+vkv_status vkv_dequantize(int32_t dtype, const void *blocks, int64_t n, float *y,
+                          void *hip_stream);
 
 /* ---------------------------------------------------------------------------
  * Seeded synthetic rows (integer Irwin-Hall N(0,1), bit-identical to the CPU

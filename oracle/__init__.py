@@ -14,6 +14,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liboracle.so")
 
 F32, F16, Q8_0 = 0, 1, 8
+Q4_K, Q6_K, Q8_K = 12, 14, 15
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_K: 292}
 TAG_K, TAG_V, TAG_Q = 1, 2, 3
 TAG_EK, TAG_EV, TAG_EQ = 11, 12, 13
 
@@ -104,6 +106,17 @@ _protos = {
                                      _i32, _f32, _vp]),
     "orc_window_attn_f64": (None, [ctypes.c_int, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32,
                                    _i32, _i32, _i32, _i32, _f64, _vp]),
+    "orc_q4_k_dequantize": (None, [_vp, _vp, _i64]),
+    "orc_q6_k_dequantize": (None, [_vp, _vp, _i64]),
+    "orc_q8_k_quantize": (None, [_vp, _vp, _i64]),
+    "orc_q8_k_dequantize": (None, [_vp, _vp, _i64]),
+    "orc_vec_dot_q4_k_q8_k": (_f32, [_i64, _vp, _vp]),
+    "orc_vec_dot_q6_k_q8_k": (_f32, [_i64, _vp, _vp]),
+    "orc_rms_norm": (None, [_vp, _vp, _i64, _f32]),
+    "orc_norm_act": (None, [_vp, _i64, _vp, _vp, _f32, _vp]),
+    "orc_silu": (_f32, [_f32]),
+    "orc_wrow_bytes": (_i64, [ctypes.c_int, _i64]),
+    "orc_matvec": (None, [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, ctypes.c_int]),
     "orc_decode_step_mimic_mt": (_f64, [ctypes.c_int, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
                                         _i32, _i32, _i32, _f32, _vp, _vp, _vp, _i32, _i32]),
 }
@@ -325,3 +338,64 @@ def decode_step_mimic_mt(dtype, k_cache, v_cache, layer_bytes, row_b, n_layers, 
                                         n_layers, n_valid, _ptr(q), n_q_heads, n_kv_heads,
                                         head_dim, scale, _ptr(out), kn, vn, new_slot, n_threads)
     return secs, out.reshape(n_layers, n_q_heads, head_dim)
+
+
+# ---- decoder weights: ggml Q4_K / Q6_K, Q8_K activations ----
+def _u8(a):
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+def _f32a(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def dequantize(dtype, blocks, n):
+    """ggml dequantize_row_q4_K / _q6_K / _q8_K of n elements -> f32."""
+    blocks = _u8(blocks)
+    y = np.empty(n, dtype=np.float32)
+    fn = {Q4_K: lib.orc_q4_k_dequantize, Q6_K: lib.orc_q6_k_dequantize,
+          Q8_K: lib.orc_q8_k_dequantize}[dtype]
+    fn(_ptr(blocks), _ptr(y), n)
+    return y
+
+
+def q8_k_quantize(x):
+    x = _f32a(x).ravel()
+    out = np.empty(x.size // 256 * 292, dtype=np.uint8)
+    lib.orc_q8_k_quantize(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def vec_dot(dtype, w_row, xq, n):
+    w_row, xq = _u8(w_row), _u8(xq)
+    fn = lib.orc_vec_dot_q4_k_q8_k if dtype == Q4_K else lib.orc_vec_dot_q6_k_q8_k
+    return fn(n, _ptr(w_row), _ptr(xq))
+
+
+def norm_act(x, norm_w=None, ada=None, eps=1e-5):
+    x = _f32a(x)
+    y = np.empty_like(x)
+    nw = _f32a(norm_w) if norm_w is not None else None
+    ad = _f32a(ada) if ada is not None else None
+    lib.orc_norm_act(_ptr(x), x.size, _ptr(nw) if nw is not None else None,
+                     _ptr(ad) if ad is not None else None, eps, _ptr(y))
+    return y
+
+
+def silu(v):
+    return np.array([lib.orc_silu(float(t)) for t in np.asarray(v, np.float32).ravel()],
+                    dtype=np.float32)
+
+
+def wrow_bytes(dtype, n_in):
+    return n_in // 256 * BLOCK_BYTES[dtype]
+
+
+def matvec(dtype, w, n_rows, n_in, x, n_threads=1):
+    """ggml_mul_mat(W, x) as the CPU path computes it: x (already normalised)
+    quantized to Q8_K, one vec_dot per row."""
+    w, x = _u8(w), _f32a(x)
+    assert w.size >= n_rows * wrow_bytes(dtype, n_in) and x.size == n_in
+    y = np.empty(n_rows, dtype=np.float32)
+    lib.orc_matvec(dtype, _ptr(w), n_rows, n_in, _ptr(x), _ptr(y), n_threads)
+    return y

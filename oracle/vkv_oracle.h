@@ -21,7 +21,10 @@
  *     mask built at :4259-4279) and the causal decoder prefill
  *     (src/voxtral.cpp:2893-2961, mask :3316-3323),
  *   - q8_0 KV block pack/unpack (absent from the reference; ggml's
- *     block_q8_0 format with the reference-quantizer rounding rule).
+ *     block_q8_0 format with the reference-quantizer rounding rule),
+ *   - the decoder's weight formats (ggml Q4_K / Q6_K), the Q8_K activation
+ *     quantizer, RMSNorm and the CPU matrix-vector product of ggml_mul_mat on
+ *     them (src/voxtral.cpp:2653-2659, 2856-2886).
  *
  * Struct layouts are field-for-field identical to src/voxtral-internal.h.
  */
@@ -88,7 +91,7 @@ typedef struct orc_enc_plan_t {
     int64_t evicted;
 } orc_enc_plan_t;
 
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q8_0 = 8, ORC_Q4_K = 12, ORC_Q6_K = 14, ORC_Q8_K = 15 };
 
 /* ---- planners ---- */
 bool orc_decoder_plan(const orc_ring *ring, int64_t absolute_start, int32_t n_new, orc_plan_t *out);
@@ -191,6 +194,24 @@ double orc_decode_step_mimic_mt(int dtype, const uint8_t *k_cache, const uint8_t
                                 int32_t n_kv_heads, int32_t head_dim, float scale,
                                 float *out, const float *k_new, const float *v_new,
                                 int32_t new_slot, int32_t n_threads);
+
+/* ---- decoder weights (kquants.c): ggml Q4_K (144 B / 256), Q6_K (210 B),
+ * Q8_K activations (292 B: f32 d, i8 qs[256], i16 bsums[16]) ---- */
+void orc_q4_k_dequantize(const uint8_t *blocks, float *y, int64_t n);
+void orc_q6_k_dequantize(const uint8_t *blocks, float *y, int64_t n);
+void orc_q8_k_quantize(const float *x, uint8_t *blocks, int64_t n);
+void orc_q8_k_dequantize(const uint8_t *blocks, float *y, int64_t n);
+float orc_vec_dot_q4_k_q8_k(int64_t n, const uint8_t *w, const uint8_t *x);
+float orc_vec_dot_q6_k_q8_k(int64_t n, const uint8_t *w, const uint8_t *x);
+void orc_rms_norm(const float *x, float *y, int64_t n, float eps);
+/* rms_norm(x) * norm_w, then h + h * ada when ada is given; a copy of x when
+ * norm_w is NULL */
+void orc_norm_act(const float *x, int64_t n, const float *norm_w, const float *ada, float eps,
+                  float *y);
+float orc_silu(float x);
+int64_t orc_wrow_bytes(int dtype, int64_t n_in);
+void orc_matvec(int dtype, const uint8_t *w, int64_t n_rows, int64_t n_in, const float *x,
+                float *y, int n_threads);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,7 @@ def test_struct_layout_matches_c():
         "vkv_enc_run": (vkv.EncRun, oracle.EncRun),
         "vkv_cache_params": (vkv.CacheParams, None),
         "vkv_cache_layout": (vkv.CacheLayout, None),
+        "vkv_mv_out": (vkv.MvOut, None),
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "vkv.h"', "int main(void){"]
     for cname, (py, _) in structs.items():
@@ -120,6 +121,29 @@ def test_error_statuses_without_device():
     assert L.vkv_q8_0_pack(None, None, 33, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_q8_0_unpack(None, None, -32, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_synth_rows(None, 4, 1, 1, 0, 1, 1, 0, 1, 1, 0, 1, 1, None) == vkv.INVALID_ARGUMENT
+    # matrix-vector products: shapes, dtypes and pointers checked on the host
+    outs = (vkv.MvOut * 2)()
+    outs[0] = vkv.MvOut(16, vkv.Q4_K, 8, 16, None)
+    outs[1] = vkv.MvOut(16, vkv.Q6_K, 8, 16, None)
+    x = ctypes.c_void_p(4096)
+    assert L.vkv_matvec(x, 300, None, None, 1e-5, outs, 1, 0, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_matvec(x, 12288 + 256, None, None, 1e-5, outs, 1, 0, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_matvec(x, 3072, None, 4096, 1e-5, outs, 1, 0, None) == vkv.INVALID_ARGUMENT
+    assert "ada requires norm_w" in vkv.last_error()
+    assert L.vkv_matvec(ctypes.c_void_p(4100), 3072, None, None, 1e-5, outs, 1, 0,
+                        None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_matvec(x, 3072, None, None, 1e-5, outs, 5, 0, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_matvec(x, 3072, None, None, 1e-5, outs, 2, 7, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_matvec(x, 3072, None, None, 1e-5, outs, 2, vkv.MV_SWIGLU,
+                        None) == vkv.INVALID_ARGUMENT          # SwiGLU needs equal dtypes
+    wrong = (vkv.MvOut * 1)(vkv.MvOut(16, vkv.Q8_0, 8, 16, None))
+    assert L.vkv_matvec(x, 3072, None, None, 1e-5, wrong, 1, 0, None) == vkv.INVALID_ARGUMENT
+    huge = (vkv.MvOut * 1)(vkv.MvOut(16, vkv.Q6_K, 1 << 30, 16, None))
+    assert L.vkv_matvec(x, 3072, None, None, 1e-5, huge, 1, 0, None) == vkv.INVALID_ARGUMENT
+    assert "4 GiB" in vkv.last_error()
+    assert L.vkv_quantize_q8_k(x, 3072, None, None, 1e-5, 4098, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_dequantize(vkv.Q8_0, 16, 256, 16, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_dequantize(vkv.Q4_K, 16, 255, 16, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_cache_destroy(None) == vkv.OK
     with pytest.raises(vkv.VkvError) as ei:
         vkv.decoder_plan(r, 5, 1)

@@ -928,6 +928,122 @@ vkv_status vkv_q8_0_unpack(const void *blocks, float *y, int64_t n, void *hip_st
     return ok();
 }
 
+// ---- decoder projections on k-quant weights ----
+
+namespace {
+
+int device_cus() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] <= 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
+int64_t kq_block_bytes(int32_t dtype) {
+    return dtype == VKV_DTYPE_Q4_K ? 144 : dtype == VKV_DTYPE_Q6_K ? 210 : 0;
+}
+
+vkv_status check_mv_input(const char *what, const float *x, int64_t n_in, const float *norm_w,
+                          const float *ada) {
+    if (n_in < 256 || n_in % 256 != 0 || n_in > VKV_MV_MAX_IN)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: n_in=%lld must be a multiple of 256 in [256, %d]",
+                    what, (long long)n_in, VKV_MV_MAX_IN);
+    if (!x) return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: null input", what);
+    if (ada && !norm_w) return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: ada requires norm_w", what);
+    return check_aligned(what, {x, norm_w, ada});
+}
+
+}  // namespace
+
+vkv_status vkv_matvec(const float *x, int64_t n_in, const float *norm_w, const float *ada,
+                      float eps, const vkv_mv_out *outs, int32_t n_outs, int32_t epilogue,
+                      void *hip_stream) {
+    if (vkv_status st = check_mv_input("matvec", x, n_in, norm_w, ada)) return st;
+    if (!outs || n_outs < 1 || n_outs > VKV_MV_MAX_OUTS)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: n_outs=%d outside [1, %d]", n_outs,
+                    VKV_MV_MAX_OUTS);
+    if (epilogue != VKV_MV_STORE && epilogue != VKV_MV_SWIGLU)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: unknown epilogue %d", epilogue);
+    const bool swiglu = epilogue == VKV_MV_SWIGLU;
+    if (swiglu && (n_outs != 2 || outs[0].n_rows != outs[1].n_rows ||
+                   outs[0].dtype != outs[1].dtype))
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "matvec: SwiGLU takes two matrices of equal rows and dtype");
+    int64_t total = 0;
+    for (int32_t k = 0; k < n_outs; ++k) {
+        const vkv_mv_out &o = outs[k];
+        const int64_t bb = kq_block_bytes(o.dtype);
+        if (!bb) return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: weight dtype %d", o.dtype);
+        if (!o.w || (!o.y && !(swiglu && k == 1)) || o.n_rows < 1)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: matrix %d: null pointer or no rows", k);
+        if ((int64_t)o.n_rows * (n_in / 256) * bb > (int64_t)0xFFFFFE00)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: matrix %d exceeds 4 GiB", k);
+        if (reinterpret_cast<uintptr_t>(o.w) & 3u)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: weights must be 4-byte aligned");
+        if (swiglu && o.add)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: SwiGLU has no residual add");
+        total += o.n_rows;
+    }
+    if (swiglu) total = outs[0].n_rows;
+    const int cus = device_cus();
+    int64_t rpw = (total + 8LL * cus - 1) / (8LL * cus);
+    const int32_t forced = env_int("VKV_MV_ROWS");
+    if (forced > 0) rpw = forced;
+    rpw = std::max<int64_t>(1, std::min<int64_t>(rpw, 1 << 20));
+    MvArgs a{};
+    a.x = x;
+    a.norm_w = norm_w;
+    a.ada = ada;
+    a.eps = eps;
+    a.n_in = (int32_t)n_in;
+    a.n_outs = n_outs;
+    a.rows_per_wg = (int32_t)(4 * rpw);
+    a.swiglu = swiglu ? 1 : 0;
+    int64_t wg = 0;
+    for (int32_t k = 0; k < n_outs; ++k) {
+        a.out[k] = MvOut{(const uint8_t *)outs[k].w, outs[k].y, outs[k].add, outs[k].dtype,
+                         outs[k].n_rows, (int32_t)wg};
+        if (!swiglu || k == 0) wg += (outs[k].n_rows + a.rows_per_wg - 1) / a.rows_per_wg;
+    }
+    if (swiglu) a.out[1].wg0 = 0x7fffffff;
+    for (int32_t k = n_outs; k < VKV_MV_MAX_OUTS; ++k) a.out[k].wg0 = 0x7fffffff;
+    if (wg > 0x7fffffff) return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: grid too large");
+    hipError_t e = launch_matvec(a, (int)wg, as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "matvec launch");
+    return ok();
+}
+
+vkv_status vkv_quantize_q8_k(const float *x, int64_t n, const float *norm_w, const float *ada,
+                             float eps, void *blocks, void *hip_stream) {
+    if (vkv_status st = check_mv_input("q8_K quantize", x, n, norm_w, ada)) return st;
+    if (!blocks || (reinterpret_cast<uintptr_t>(blocks) & 3u))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "q8_K quantize: output null or not 4-byte aligned");
+    hipError_t e = launch_q8k_quant(x, (int)n, norm_w, ada, eps, (uint8_t *)blocks,
+                                    as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "q8_K quantize launch");
+    return ok();
+}
+
+vkv_status vkv_dequantize(int32_t dtype, const void *blocks, int64_t n, float *y,
+                          void *hip_stream) {
+    if (!kq_block_bytes(dtype)) return fail(VKV_STATUS_INVALID_ARGUMENT, "dequantize: dtype %d", dtype);
+    if (n < 0 || n % 256 != 0) return fail(VKV_STATUS_INVALID_ARGUMENT, "dequantize: n %% 256 != 0");
+    if (n == 0) return ok();
+    if (!blocks || !y) return fail(VKV_STATUS_INVALID_ARGUMENT, "dequantize: null argument");
+    if (n / 8 > (int64_t)0x7fffffff * 256)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "dequantize: n too large");
+    hipError_t e = launch_kq_dequant(dtype, (const uint8_t *)blocks, n, y, as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    return ok();
+}
+
 vkv_status vkv_synth_rows(float *dst, int32_t row_len, uint64_t seed, uint32_t tag, int64_t s0,
                           int32_t ns, int64_t s_stride, int64_t l0, int32_t nl, int64_t l_stride,
                           int64_t p0, int32_t np, int64_t p_stride, void *hip_stream) {

@@ -99,6 +99,34 @@ struct WindowArgs {
     SegPair wseg;
 };
 
+// Matrix-vector products on ggml Q4_K / Q6_K rows (vkv_matvec.hip).
+constexpr int kMvMaxIn = VKV_MV_MAX_IN;
+constexpr int kMvMaxOuts = VKV_MV_MAX_OUTS;
+
+struct MvOut {
+    const uint8_t *w;      // [n_rows][n_in / 256 blocks]
+    float *y;
+    const float *add;      // nullable: y = add + W x
+    int32_t dtype, n_rows;
+    int32_t wg0;           // first work group of this matrix
+};
+
+struct MvArgs {
+    const float *x;
+    const float *norm_w;   // nullable: x := rms_norm(x) * norm_w
+    const float *ada;      // nullable: then x := x + x * ada
+    float eps;
+    int32_t n_in, n_outs;
+    int32_t rows_per_wg;   // multiple of 4 (one contiguous quarter per wave)
+    int32_t swiglu;        // out[0].y = silu(W0 x) * (W1 x), rows paired
+    MvOut out[kMvMaxOuts];
+};
+
+hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st);
+hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const float *ada, float eps,
+                            uint8_t *out, hipStream_t st);
+hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, float *y, hipStream_t st);
+
 hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st);
 hipError_t launch_gather(const uint8_t *src, int64_t row_bytes, SegPair seg, uint8_t *dst,
                          hipStream_t st);

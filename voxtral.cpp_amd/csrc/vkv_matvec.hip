@@ -1,0 +1,590 @@
+// gfx950 matrix-vector products of the decoder step on ggml k-quant weights.
+//
+// ggml_mul_mat(W, x) with one token (src/voxtral.cpp:2656-2659 Q/K/V, :2857
+// O-projection, :2879-2883 SwiGLU FFN) on Q4_K / Q6_K rows
+// (src/voxtral-quantize.cpp:148-159), computed the way ggml's CPU path does:
+// x is quantized to Q8_K (f32 scale per 256, int8 codes, 16-element sums) and
+// each row is an integer dot product per block, scaled by fp16(d) * d_x (and
+// for Q4_K minus fp16(dmin) * d_x * sum of mins x 32-element sums).
+//
+//   k_matvec     -- one launch for up to four matrices that read the same x:
+//                   prologue = optional RMSNorm x weight (x (1 + ada)) and the
+//                   Q8_K quantization, into LDS, while the first weight loads
+//                   are in flight; body = each wave streams whole rows, each
+//                   lane one quarter of a 256-weight block (64 weights) with
+//                   v_dot4_i32_i8, the row sum by a wave reduction; epilogue =
+//                   store, residual add, or silu(W0 x) * (W1 x).
+//   k_q8k_quant  -- the same prologue alone, to global memory in ggml's
+//                   block_q8_K layout.
+//   k_kq_dequant -- ggml dequantize_row_q4_K / _q6_K (get_rows on the token
+//                   embedding table, src/voxtral.cpp:3008).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <type_traits>
+
+#include "vkv_internal.h"
+
+namespace vkv {
+namespace {
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kQ4Bytes = 144;
+constexpr int kQ6Bytes = 210;
+constexpr uint32_t kOob = 0xFFFFFF00u;   // buffer offset past every resource: loads read 0
+
+// Q8_K image of the input vector, per work group.
+struct ActSmem {
+    int8_t xq[kMvMaxIn];                 // codes
+    int32_t bs32[kMvMaxIn / 32];         // sums of 32 codes (Q4_K sub-blocks)
+    int32_t bs16[kMvMaxIn / 16];         // sums of 16 codes, order [b][n][h][g] (Q6_K)
+    float dx[kMvMaxIn / 256];            // block scales
+    double red[4];
+};
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+
+// Cross-lane reductions by DPP inside each 16-lane row (0xB1 / 0x4E = quad
+// xor 1 / 2, 0x141 = half-row mirror, 0x140 = row mirror) and readlane across
+// the four rows: no LDS traffic, a uniform result.
+template <int CTRL>
+__device__ __forceinline__ int dppi(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+    return __builtin_bit_cast(float, dppi<CTRL>(__builtin_bit_cast(int, v)));
+}
+template <int CTRL>
+__device__ __forceinline__ double dppd(double v) {
+    int2 p = __builtin_bit_cast(int2, v);
+    p.x = dppi<CTRL>(p.x);
+    p.y = dppi<CTRL>(p.y);
+    return __builtin_bit_cast(double, p);
+}
+__device__ __forceinline__ int lane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __builtin_bit_cast(float, lane_i(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ double lane_d(double v, int l) {
+    int2 p = __builtin_bit_cast(int2, v);
+    return __builtin_bit_cast(double, int2{lane_i(p.x, l), lane_i(p.y, l)});
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+    v += dppd<0xB1>(v);
+    v += dppd<0x4E>(v);
+    v += dppd<0x141>(v);
+    v += dppd<0x140>(v);
+    return (lane_d(v, 0) + lane_d(v, 16)) + (lane_d(v, 32) + lane_d(v, 48));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dppf<0xB1>(v);
+    v += dppf<0x4E>(v);
+    v += dppf<0x141>(v);
+    v += dppf<0x140>(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+    int x = (int)v;
+    x = (int)max((uint32_t)x, (uint32_t)dppi<0xB1>(x));
+    x = (int)max((uint32_t)x, (uint32_t)dppi<0x4E>(x));
+    x = (int)max((uint32_t)x, (uint32_t)dppi<0x141>(x));
+    x = (int)max((uint32_t)x, (uint32_t)dppi<0x140>(x));
+    return max(max((uint32_t)lane_i(x, 0), (uint32_t)lane_i(x, 16)),
+               max((uint32_t)lane_i(x, 32), (uint32_t)lane_i(x, 48)));
+}
+
+__device__ __forceinline__ int wave_min_i(int x) {
+    x = min(x, dppi<0xB1>(x));
+    x = min(x, dppi<0x4E>(x));
+    x = min(x, dppi<0x141>(x));
+    x = min(x, dppi<0x140>(x));
+    return min(min(lane_i(x, 0), lane_i(x, 16)), min(lane_i(x, 32), lane_i(x, 48)));
+}
+
+// Q8_K quantization of rms_norm(x) * norm_w (* (1 + ada)), or of x itself
+// (norm_w == nullptr).  Wave w handles blocks w, w + 4, ...; each lane 4
+// consecutive elements of a block.  Rounding follows the CPU path step by
+// step: the squares are f32 products summed in double, mean = f32(sum / n),
+// scale = 1 / sqrtf(mean + eps), h = (x * scale) * w, then h + h * ada;
+// iscale = -127 / (first element of largest |h|), code = min(127,
+// rint(iscale * h)), d = 1 / iscale.
+//
+// Split in two so that a caller can issue its own loads between them: the
+// input loads of act_load retire first (vmcnt counts in issue order), and
+// act_finish then waits for them alone.  NBW = most blocks per wave; with
+// NORM_EARLY the norm weights are loaded up front too.
+template <int NBW, bool NORM_EARLY>
+struct ActRegs {
+    float4 x[NBW];
+    float4 w[NORM_EARLY ? NBW : 1];
+    float4 a[NORM_EARLY ? NBW : 1];
+};
+
+template <int NBW, bool NE>
+__device__ __forceinline__ void act_load(ActRegs<NBW, NE> &r, const float *__restrict__ x, int n,
+                                         const float *__restrict__ nw,
+                                         const float *__restrict__ ada) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nb = n >> 8;
+    const float *wp = nw ? nw : x, *ap = ada ? ada : x;
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+        const int b = wave + 4 * i < nb ? wave + 4 * i : 0;
+        const int e0 = 256 * b + 4 * lane;
+        r.x[i] = *reinterpret_cast<const float4 *>(x + e0);
+        if (NE) {
+            r.w[i] = *reinterpret_cast<const float4 *>(wp + e0);
+            r.a[i] = *reinterpret_cast<const float4 *>(ap + e0);
+        }
+    }
+}
+
+template <int NBW, bool NE>
+__device__ __forceinline__ void act_finish(const ActRegs<NBW, NE> &r, int n,
+                                           const float *__restrict__ nw,
+                                           const float *__restrict__ ada, float eps, ActSmem &sm,
+                                           uint8_t *__restrict__ gout) {
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nb = n >> 8;
+    float scale = 1.0f;
+    if (nw) {
+        double s = 0.0;
+#pragma unroll
+        for (int i = 0; i < NBW; ++i)
+            if (wave + 4 * i < nb) {
+                const float4 v = r.x[i];
+                s += (double)(v.x * v.x);
+                s += (double)(v.y * v.y);
+                s += (double)(v.z * v.z);
+                s += (double)(v.w * v.w);
+            }
+        s = wave_sum_d(s);
+        if (lane == 0) sm.red[wave] = s;
+        __syncthreads();
+        const double tot = (sm.red[0] + sm.red[1]) + (sm.red[2] + sm.red[3]);
+        const float mean = (float)(tot / (double)n);
+        scale = 1.0f / sqrtf(mean + eps);
+    }
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+        const int b = wave + 4 * i;
+        if (b >= nb) break;
+        const int e0 = 256 * b + 4 * lane;
+        float e[4] = {r.x[i].x, r.x[i].y, r.x[i].z, r.x[i].w};
+        if (nw) {
+            const float4 w4 = NE ? r.w[i] : *reinterpret_cast<const float4 *>(nw + e0);
+            const float w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                e[k] = e[k] * scale;
+                e[k] = e[k] * w[k];
+            }
+            if (ada) {
+                const float4 a4 = NE ? r.a[i] : *reinterpret_cast<const float4 *>(ada + e0);
+                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const float t = e[k] * av[k];
+                    e[k] = e[k] + t;
+                }
+            }
+        }
+        // first element of largest magnitude (|h| > running max, in order)
+        float am = 0.0f;
+        int ai = 0x7fffffff;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (fabsf(e[k]) > am) {
+                am = fabsf(e[k]);
+                ai = 4 * lane + k;
+            }
+        const uint32_t wm = wave_max_u(__builtin_bit_cast(uint32_t, am));
+        const int wi = wave_min_i((__builtin_bit_cast(uint32_t, am) == wm && wm != 0u) ? ai
+                                                                                        : 0x7fffffff);
+        int q[4] = {0, 0, 0, 0};
+        float d = 0.0f;
+        if (wm != 0u) {
+            const int k = wi & 3;
+            const float mine = k == 0 ? e[0] : k == 1 ? e[1] : k == 2 ? e[2] : e[3];
+            const float mx = lane_f(mine, wi >> 2);
+            const float iscale = -127.0f / mx;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) q[j] = min(127, (int)__builtin_rintf(iscale * e[j]));
+            d = 1.0f / iscale;
+        }
+        const uint32_t packed = (uint32_t)(q[0] & 255) | (uint32_t)(q[1] & 255) << 8 |
+                                (uint32_t)(q[2] & 255) << 16 | (uint32_t)(q[3] & 255) << 24;
+        int s = q[0] + q[1] + q[2] + q[3];
+        s += dppi<0xB1>(s);
+        s += dppi<0x4E>(s);               // sum of 16 (lanes 4k..4k+3)
+        const int s32 = s + dppi<0x141>(s);
+        const int k16 = lane >> 2;        // 16-group 8n + 2g + h
+        if (gout) {
+            uint8_t *blk = gout + (size_t)b * 292;
+            *reinterpret_cast<uint32_t *>(blk + 4 + 4 * lane) = packed;
+            if ((lane & 3) == 0) *reinterpret_cast<int16_t *>(blk + 260 + 2 * k16) = (int16_t)s;
+            if (lane == 0) *reinterpret_cast<float *>(blk) = d;
+        } else {
+            *reinterpret_cast<uint32_t *>(&sm.xq[e0]) = packed;
+            if ((lane & 3) == 0)
+                sm.bs16[16 * b + 8 * (k16 >> 3) + 4 * (k16 & 1) + ((k16 >> 1) & 3)] = s;
+            if ((lane & 7) == 0) sm.bs32[8 * b + (lane >> 3)] = s32;
+            if (lane == 0) sm.dx[b] = d;
+        }
+    }
+    __syncthreads();
+}
+
+// Raw bytes of one lane's quarter block.  Q4_K: a, b = 32 code bytes, c = the
+// 16-byte header (d, dmin, scales).  Q6_K (blocks are only 2-byte aligned):
+// a, b, c = 16 bytes of ql (low), ql (high), qh read from the dword-aligned
+// address below, with one more dword each in ax, bx, cx; s = 12 bytes
+// covering the lane's 8 scales; dh = fp16 d.
+struct FragQ4 {
+    u32x4_t a, b, c;
+};
+struct FragQ6 {
+    u32x4_t a, b, c;
+    uint32_t ax, bx, cx;
+    u32x2_t s01;
+    uint32_t s2, dh;
+};
+
+__device__ __forceinline__ FragQ4 load_q4(__amdgpu_buffer_rsrc_t rs, uint32_t off, int c) {
+    FragQ4 f;
+    f.a = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 + 32 * c, 0, 0));
+    f.b = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 32 + 32 * c, 0, 0));
+    f.c = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    return f;
+}
+
+__device__ __forceinline__ FragQ6 load_q6(__amdgpu_buffer_rsrc_t rs, uint32_t off, int n, int h) {
+    FragQ6 f;
+    const uint32_t al = off & ~3u;     // off is even: al = off or off - 2
+    const uint32_t o0 = al + 64 * n + 16 * h, o1 = o0 + 32, oh = al + 128 + 32 * n + 16 * h;
+    const uint32_t os = al + 192 + 8 * n;
+    f.a = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, o0, 0, 0));
+    f.ax = __builtin_amdgcn_raw_buffer_load_b32(rs, o0 + 16, 0, 0);
+    f.b = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, o1, 0, 0));
+    f.bx = __builtin_amdgcn_raw_buffer_load_b32(rs, o1 + 16, 0, 0);
+    f.c = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, oh, 0, 0));
+    f.cx = __builtin_amdgcn_raw_buffer_load_b32(rs, oh + 16, 0, 0);
+    f.s01 = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs, os, 0, 0));
+    f.s2 = __builtin_amdgcn_raw_buffer_load_b32(rs, os + 8, 0, 0);
+    f.dh = __builtin_amdgcn_raw_buffer_load_b16(rs, off + 208, 0, 0);
+    return f;
+}
+
+// The activation side of one lane's task for a step (same for every row).
+struct XFrag {
+    i32x4_t x[4];     // 64 codes
+    int32_t bs[4];    // Q4_K: bs[0..1] = sums of sub-blocks 2c, 2c+1; Q6_K: g = 0..3
+    float dx;
+};
+
+__device__ __forceinline__ XFrag x_q4(const ActSmem &sm, int t) {
+    const int b = t >> 2, c = t & 3;
+    XFrag f;
+    const i32x4_t *p = reinterpret_cast<const i32x4_t *>(&sm.xq[256 * b + 64 * c]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.x[i] = p[i];
+    const u32x2_t s = *reinterpret_cast<const u32x2_t *>(&sm.bs32[8 * b + 2 * c]);
+    f.bs[0] = (int32_t)s.x;
+    f.bs[1] = (int32_t)s.y;
+    f.bs[2] = f.bs[3] = 0;
+    f.dx = sm.dx[b];
+    return f;
+}
+
+__device__ __forceinline__ XFrag x_q6(const ActSmem &sm, int t) {
+    const int b = t >> 2, n = (t >> 1) & 1, h = t & 1;
+    XFrag f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+        f.x[g] = *reinterpret_cast<const i32x4_t *>(&sm.xq[256 * b + 128 * n + 32 * g + 16 * h]);
+    const i32x4_t s = *reinterpret_cast<const i32x4_t *>(&sm.bs16[16 * b + 8 * n + 4 * h]);
+    f.bs[0] = s.x;
+    f.bs[1] = s.y;
+    f.bs[2] = s.z;
+    f.bs[3] = s.w;
+    f.dx = sm.dx[b];
+    return f;
+}
+
+__device__ __forceinline__ int dot16(const uint32_t (&w)[4], const i32x4_t &x, int acc) {
+    acc = __builtin_amdgcn_sdot4((int)w[0], x.x, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w[1], x.y, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)w[2], x.z, acc, false);
+    return __builtin_amdgcn_sdot4((int)w[3], x.w, acc, false);
+}
+
+__device__ __forceinline__ float compute_q4(const FragQ4 &f, const XFrag &x, int c) {
+    const uint32_t u0 = f.c.y, u1 = f.c.z, u2 = f.c.w;
+    const uint32_t sc_lo = u0 & 0x3f3f3f3fu, mn_lo = u1 & 0x3f3f3f3fu;
+    const uint32_t sc_hi = (u2 & 0x0f0f0f0fu) | ((u0 >> 2) & 0x30303030u);
+    const uint32_t mn_hi = ((u2 >> 4) & 0x0f0f0f0fu) | ((u1 >> 2) & 0x30303030u);
+    const uint32_t scw = c < 2 ? sc_lo : sc_hi, mnw = c < 2 ? mn_lo : mn_hi;
+    const uint32_t sh = 16u * (uint32_t)(c & 1);
+    const int sc_a = (int)((scw >> sh) & 255u), sc_b = (int)((scw >> (sh + 8)) & 255u);
+    const int m_a = (int)((mnw >> sh) & 255u), m_b = (int)((mnw >> (sh + 8)) & 255u);
+    const uint32_t w[8] = {f.a.x, f.a.y, f.a.z, f.a.w, f.b.x, f.b.y, f.b.z, f.b.w};
+    uint32_t lo[2][4], hi[2][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        lo[i >> 2][i & 3] = w[i] & 0x0f0f0f0fu;
+        hi[i >> 2][i & 3] = (w[i] >> 4) & 0x0f0f0f0fu;
+    }
+    const int dot_a = dot16(lo[1], x.x[1], dot16(lo[0], x.x[0], 0));
+    const int dot_b = dot16(hi[1], x.x[3], dot16(hi[0], x.x[2], 0));
+    const int isum = sc_a * dot_a + sc_b * dot_b;
+    const int imin = m_a * x.bs[0] + m_b * x.bs[1];
+    const float d = h2f(f.c.x & 0xffffu) * x.dx, dmin = h2f(f.c.x >> 16) * x.dx;
+    return d * (float)isum - dmin * (float)imin;
+}
+
+__device__ __forceinline__ float compute_q6(const FragQ6 &f, const XFrag &x, uint32_t mis, int h) {
+    uint32_t l0[4], l1[4], qh[4];
+    const uint32_t a[5] = {f.a.x, f.a.y, f.a.z, f.a.w, f.ax};
+    const uint32_t b[5] = {f.b.x, f.b.y, f.b.z, f.b.w, f.bx};
+    const uint32_t c[5] = {f.c.x, f.c.y, f.c.z, f.c.w, f.cx};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        l0[i] = __builtin_amdgcn_alignbyte(a[i + 1], a[i], mis);
+        l1[i] = __builtin_amdgcn_alignbyte(b[i + 1], b[i], mis);
+        qh[i] = __builtin_amdgcn_alignbyte(c[i + 1], c[i], mis);
+    }
+    const uint32_t s_lo = __builtin_amdgcn_alignbyte(f.s01.y, f.s01.x, mis);
+    const uint32_t s_hi = __builtin_amdgcn_alignbyte(f.s2, f.s01.y, mis);
+    uint32_t q[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        q[0][i] = (l0[i] & 0x0f0f0f0fu) | ((qh[i] << 4) & 0x30303030u);
+        q[1][i] = (l1[i] & 0x0f0f0f0fu) | ((qh[i] << 2) & 0x30303030u);
+        q[2][i] = ((l0[i] >> 4) & 0x0f0f0f0fu) | (qh[i] & 0x30303030u);
+        q[3][i] = ((l1[i] >> 4) & 0x0f0f0f0fu) | ((qh[i] >> 2) & 0x30303030u);
+    }
+    const uint32_t hs = 8u * (uint32_t)h;
+    const int sc[4] = {(int)(int8_t)(s_lo >> hs), (int)(int8_t)(s_lo >> (hs + 16)),
+                       (int)(int8_t)(s_hi >> hs), (int)(int8_t)(s_hi >> (hs + 16))};
+    int isum = 0;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) isum += sc[g] * (dot16(q[g], x.x[g], 0) - 32 * x.bs[g]);
+    return (h2f(f.dh) * x.dx) * (float)isum;
+}
+
+
+__device__ __forceinline__ XFrag xfrag(const ActSmem &sm, bool q4, int t) {
+    return q4 ? x_q4(sm, t) : x_q6(sm, t);
+}
+
+// Where unit u of a wave reads its weights.  The buffer descriptor is built
+// per load from a uniform pointer and size (a select between two descriptors
+// is lowered through scratch memory).
+struct UnitMap {
+    const uint8_t *w0, *w1;
+    uint32_t n0, n1;
+    int row0;
+    uint32_t rbytes, bbytes;
+    int tasks, lane, mats;
+    bool swiglu;
+
+    template <int S, bool Q4>
+    __device__ __forceinline__ auto load(int u) const {
+        const int step = u % S;
+        const bool second = swiglu && ((u / S) & 1);
+        const int row = row0 + u / (S * mats);
+        const int t = 64 * step + lane;
+        const uint32_t off = t < tasks ? (uint32_t)row * rbytes + (uint32_t)(t >> 2) * bbytes : kOob;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(second ? w1 : w0), (short)0, (int)(second ? n1 : n0), 0x00020000);
+        if constexpr (Q4) return load_q4(rs, off, t & 3);
+        else return load_q6(rs, off, (t >> 1) & 1, t & 1);
+    }
+};
+
+// a.out[k] for a uniform k without indexing the kernel-argument array (a
+// dynamic index makes the compiler copy the array to scratch)
+__device__ __forceinline__ MvOut out_at(const MvArgs &a, int k) {
+    MvOut o = a.out[0];
+    if (k == 1) o = a.out[1];
+    if (k == 2) o = a.out[2];
+    if (k == 3) o = a.out[3];
+    return o;
+}
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+// Unit u of a wave = (row, step): step s of a row covers lane tasks
+// [64 s, 64 s + 64) of the row's 4 * nb quarter blocks.  With SWIGLU the rows
+// alternate between the two matrices: u -> (pair u / 2S, matrix (u / S) & 1).
+// Unit u of a wave = (row, step): step s of a row covers lane tasks
+// [64 s, 64 s + 64) of the row's 4 * nb quarter blocks.  With SWIGLU the rows
+// alternate between the two matrices: u -> (pair u / 2S, matrix (u / S) & 1).
+// Q4 (the work group's weight dtype) is a template parameter so that every
+// load writes its final registers (a load feeding a merge of two paths would
+// be copied, and the copy waits for the load).
+template <int S, int D0, bool Q4>
+__device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, const MvOut &ob,
+                                            int row0, int nrow, ActSmem &sm) {
+    const int lane = threadIdx.x & 63;
+    const bool swiglu = a.swiglu != 0;
+    const int mats = swiglu ? 2 : 1;
+    const int units = nrow * S * mats;
+    const int nb = a.n_in >> 8, tasks = 4 * nb;
+    const uint32_t bbytes = Q4 ? kQ4Bytes : kQ6Bytes;
+    const uint32_t rbytes = (uint32_t)nb * bbytes;
+    const UnitMap um{o0.w, ob.w, rbytes * (uint32_t)o0.n_rows, rbytes * (uint32_t)ob.n_rows, row0,
+                     rbytes, bbytes, tasks, lane, mats, swiglu};
+
+    constexpr int D = Q4 ? D0 : 2;            // units in flight (Q6_K fragments are larger)
+    constexpr int NBW = S == 1 ? 4 : 4 * S;   // n_in <= 4096 / 12288
+    ActRegs<NBW, false> ar;
+    act_load(ar, a.x, a.n_in, a.norm_w, a.ada);
+    using Frag = std::conditional_t<Q4, FragQ4, FragQ6>;
+    Frag f[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+        if (k < units) f[k] = um.load<S, Q4>(k);
+    act_finish(ar, a.n_in, a.norm_w, a.ada, a.eps, sm, nullptr);
+
+    const XFrag xr = xfrag(sm, Q4, min(lane, tasks - 1));   // the only step when S == 1
+
+    float acc = 0.0f, first = 0.0f;
+    for (int u0 = 0; u0 < units; u0 += D) {
+#pragma unroll
+        for (int k = 0; k < D; ++k) {
+            const int u = u0 + k;
+            if (u >= units) break;
+            const Frag cur = f[k];
+            if (u + D < units) f[k] = um.load<S, Q4>(u + D);
+            const int step = u % S, m = swiglu ? (u / S) & 1 : 0;
+            const int row = row0 + u / (S * mats);
+            const int t = 64 * step + lane;
+            const XFrag xf = S == 1 ? xr : xfrag(sm, Q4, min(t, tasks - 1));
+            float c;
+            if constexpr (Q4) {
+                c = compute_q4(cur, xf, t & 3);
+            } else {
+                // Q6_K block (row, b) starts at 210 (row nb + b): 2 mod 4 when odd
+                const uint32_t mis = 2u * (uint32_t)((row * nb + (t >> 2)) & 1);
+                c = compute_q6(cur, xf, mis, t & 1);
+            }
+            acc += t < tasks ? c : 0.0f;
+            if (step == S - 1) {
+                const float r = wave_sum(acc);
+                acc = 0.0f;
+                if (!swiglu) {
+                    if (lane == 0) o0.y[row] = o0.add ? o0.add[row] + r : r;
+                } else if (m == 0) {
+                    first = r;
+                } else if (lane == 0) {
+                    o0.y[row] = silu(first) * r;
+                }
+            }
+        }
+    }
+}
+
+template <int S, int D>
+__global__ void __launch_bounds__(256) k_matvec(MvArgs a) {
+    __shared__ ActSmem sm;
+    const int wave = threadIdx.x >> 6;
+    int seg = 0;
+#pragma unroll
+    for (int k = 1; k < kMvMaxOuts; ++k)
+        if (k < a.n_outs && (int)blockIdx.x >= a.out[k].wg0) seg = k;
+    const MvOut o0 = out_at(a, seg);
+    const MvOut ob = a.swiglu ? a.out[1] : o0;
+    const int row0 = ((int)blockIdx.x - o0.wg0) * a.rows_per_wg + wave * (a.rows_per_wg >> 2);
+    const int nrow = max(0, min(a.rows_per_wg >> 2, o0.n_rows - row0));
+    if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D, true>(a, o0, ob, row0, nrow, sm);
+    else matvec_body<S, D, false>(a, o0, ob, row0, nrow, sm);
+}
+
+__global__ void __launch_bounds__(256) k_q8k_quant(const float *x, int n, const float *nw,
+                                                   const float *ada, float eps, uint8_t *out) {
+    __shared__ ActSmem sm;
+    ActRegs<kMvMaxIn / 1024, false> r;
+    act_load(r, x, n, nw, ada);
+    act_finish(r, n, nw, ada, eps, sm, out);
+}
+
+// ggml dequantize_row_q4_K / _q6_K; one thread per 8 consecutive elements.
+__global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__restrict__ src,
+                                                    int64_t n, float *__restrict__ y) {
+#pragma clang fp contract(off)
+    const int64_t i8 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i8 >= n) return;
+    const int64_t b = i8 >> 8;
+    const int e0 = (int)(i8 & 255);
+    float out[8];
+    if (dtype == VKV_DTYPE_Q4_K) {
+        const uint8_t *blk = src + b * kQ4Bytes;
+        const float d = h2f(blk[0] | blk[1] << 8), dmin = h2f(blk[2] | blk[3] << 8);
+        const uint8_t *s = blk + 4;
+        const int j = e0 >> 5;
+        int sc, m;
+        if (j < 4) {
+            sc = s[j] & 63;
+            m = s[j + 4] & 63;
+        } else {
+            sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+            m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+        }
+        const float d1 = d * (float)sc, m1 = dmin * (float)m;
+        const uint8_t *qs = blk + 16 + 32 * (j >> 1) + (e0 & 31);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int q = (j & 1) ? (qs[i] >> 4) : (qs[i] & 15);
+            out[i] = d1 * (float)q - m1;
+        }
+    } else {
+        const uint8_t *blk = src + b * kQ6Bytes;
+        const float d = h2f(blk[208] | blk[209] << 8);
+        const int n2 = e0 >> 7, g = (e0 >> 5) & 3, l0 = e0 & 31;
+        const float ds = d * (float)(int8_t)blk[192 + 8 * n2 + 2 * g + (l0 >> 4)];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int l = l0 + i;
+            const uint8_t lo = blk[64 * n2 + 32 * (g & 1) + l];
+            const int nib = g < 2 ? (lo & 15) : (lo >> 4);
+            const int q = nib | (((blk[128 + 32 * n2 + l] >> (2 * g)) & 3) << 4);
+            out[i] = ds * (float)(q - 32);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i8 + i] = out[i];
+}
+
+}  // namespace
+
+hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st) {
+    const int S = (a.n_in / 256 * 4 + 63) / 64;
+    if (S == 1) k_matvec<1, 3><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 2) k_matvec<2, 2><<<n_wg, 256, 0, st>>>(a);
+    else k_matvec<3, 2><<<n_wg, 256, 0, st>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const float *ada, float eps,
+                            uint8_t *out, hipStream_t st) {
+    k_q8k_quant<<<1, 256, 0, st>>>(x, n, norm_w, ada, eps, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, float *y, hipStream_t st) {
+    const int64_t threads = n / 8;
+    k_kq_dequant<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(dtype, src, n, y);
+    return hipGetLastError();
+}
+
+}  // namespace vkv

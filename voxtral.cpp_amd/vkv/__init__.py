@@ -41,7 +41,14 @@ BUFFER_TOO_SMALL = 11
 F32 = 0
 F16 = 1
 Q8_0 = 8
+Q4_K = 12
+Q6_K = 14
+Q8_K = 15
 MAX_BATCH_STREAMS = 32
+KQ_BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_K: 292}
+MV_MAX_IN = 12288
+MV_MAX_OUTS = 4
+MV_STORE, MV_SWIGLU = 0, 1
 
 
 def row_bytes(dtype, n):
@@ -120,6 +127,10 @@ _u64 = ctypes.c_uint64
 _u32 = ctypes.c_uint32
 _f32 = ctypes.c_float
 
+
+class MvOut(ctypes.Structure):
+    _fields_ = [("w", _vp), ("dtype", _i32), ("n_rows", _i32), ("y", _vp), ("add", _vp)]
+
 # prototypes: name -> (restype, argtypes); exactly the functions of include/vkv.h
 PROTOTYPES = {
     "vkv_decoder_plan": (_i32, [_P(Ring), _i64, _i32, _P(Plan)]),
@@ -153,6 +164,9 @@ PROTOTYPES = {
                                _vp, _vp, _i32, _f32, _vp]),
     "vkv_q8_0_pack": (_i32, [_vp, _vp, _i64, _vp]),
     "vkv_q8_0_unpack": (_i32, [_vp, _vp, _i64, _vp]),
+    "vkv_matvec": (_i32, [_vp, _i64, _vp, _vp, _f32, _P(MvOut), _i32, _i32, _vp]),
+    "vkv_quantize_q8_k": (_i32, [_vp, _i64, _vp, _vp, _f32, _vp, _vp]),
+    "vkv_dequantize": (_i32, [_i32, _vp, _i64, _vp, _vp]),
     "vkv_synth_rows": (_i32, [_vp, _i32, _u64, _u32, _i64, _i32, _i64, _i64, _i32, _i64, _i64,
                               _i32, _i64, _vp]),
     "vkv_api_version": (_u32, []),
@@ -356,6 +370,27 @@ def q8_0_pack(x_ptr, blocks_ptr, n, hip_stream=0):
 
 def q8_0_unpack(blocks_ptr, y_ptr, n, hip_stream=0):
     check(lib.vkv_q8_0_unpack(blocks_ptr, y_ptr, n, hip_stream))
+
+
+def matvec(x_ptr, n_in, outs, norm_w_ptr=None, ada_ptr=None, eps=1e-5, epilogue=MV_STORE,
+           hip_stream=0):
+    """y = W h for each (w_ptr, dtype, n_rows, y_ptr[, add_ptr]) in outs (device
+    pointers); h = x, or rms_norm(x) * norm_w (* (1 + ada))."""
+    arr = (MvOut * len(outs))()
+    for i, o in enumerate(outs):
+        w, dt, n, y = o[:4]
+        add = o[4] if len(o) > 4 else None
+        arr[i] = MvOut(w, dt, n, y, add)
+    check(lib.vkv_matvec(x_ptr, n_in, norm_w_ptr, ada_ptr, eps, arr, len(outs), epilogue,
+                         hip_stream))
+
+
+def quantize_q8_k(x_ptr, n, blocks_ptr, norm_w_ptr=None, ada_ptr=None, eps=1e-5, hip_stream=0):
+    check(lib.vkv_quantize_q8_k(x_ptr, n, norm_w_ptr, ada_ptr, eps, blocks_ptr, hip_stream))
+
+
+def dequantize(dtype, blocks_ptr, n, y_ptr, hip_stream=0):
+    check(lib.vkv_dequantize(dtype, blocks_ptr, n, y_ptr, hip_stream))
 
 
 # tags of the synthetic inputs (shared with the oracle's generator)
