@@ -31,6 +31,11 @@ Other workloads (--workload), reported on the same contract:
                residual, RMSNorm*(1+ada)+SwiGLU W1/W3, W2 + residual; then the
                final norm + the 131072-row Q6_K logits -- 105 vkv_matvec
                calls, 2.24 GB of weights per token; tokens/s.
+  decoder_token_q4km  one whole decoder token through vkv_decoder_token:
+               embedding + audio row, 26 x (RMSNorm+QKV, RoPE + K/V append +
+               attention over the full 8192-slot F16 ring, O + residual,
+               RMSNorm*(1+ada) + SwiGLU, W2 + residual), final norm, logits,
+               argmax; tokens/s.
 
 Prints one JSON line: throughput, the roofline of the step (algorithmic bytes /
 average step time from HIP events on the launch stream), the HBM traffic from
@@ -67,6 +72,10 @@ WORKLOADS = {
                         pmc="decode_q8_0_8x26x8192_pmc.json"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
                         pmc="encoder_f16_32x750_pmc.json"),
+    "decoder_token_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights, f16 KV",
+                               streams=1, pmc="",
+                               data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs and "
+                                    "KV rows, generated on device)"),
     "decoder_weights_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k (int8 dot)", streams=1,
                                  pmc="matvec_q4km_26l_pmc.json",
                                  data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs, "
@@ -151,6 +160,90 @@ def gpu_weights(steps, warmup):
     total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
     assert bool(torch.isfinite(logits).all()) and bool(torch.isfinite(x).all())
     return total_ms, step_ms, wall
+
+
+def device_model(gen):
+    """Random Q4_K_M decoder weights on the device and the vkv_dec_model
+    describing them (tied output = tok_embeddings)."""
+    import torch
+    import vkv
+    keep = []
+    layers = (vkv.DecLayer * LAYERS)()
+    for l in range(LAYERS):
+        w = {name: random_kq_device(dt, r, n, gen) for name, dt, r, n in LAYER_MATS}
+        norms = torch.empty(2, DIM, device="cuda").uniform_(0.5, 1.5, generator=gen)
+        ada = torch.empty(DIM, device="cuda").uniform_(-0.3, 0.3, generator=gen)
+        keep += list(w.values()) + [norms, ada]
+        layers[l] = vkv.DecLayer(norms[0].data_ptr(), w["attn_q"].data_ptr(), w["attn_k"].data_ptr(),
+                                 w["attn_v"].data_ptr(), w["attn_o"].data_ptr(), 12, 12, 14, 12,
+                                 norms[1].data_ptr(), ada.data_ptr(), w["ffn_w1"].data_ptr(),
+                                 w["ffn_w2"].data_ptr(), w["ffn_w3"].data_ptr(), 12, 14, 12)
+    table = random_kq_device(14, VOCAB, DIM, gen)
+    out_norm = torch.empty(DIM, device="cuda").uniform_(0.5, 1.5, generator=gen)
+    keep += [table, out_norm]
+    model = vkv.DecModel(LAYERS, DIM, HIDDEN, QH, KVH, HD, VOCAB, 1e-5, 1.0e6, table.data_ptr(), 14,
+                         out_norm.data_ptr(), table.data_ptr(), 14, layers)
+    return model, (keep, layers)
+
+
+def gpu_token(steps, warmup):
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED)
+    model, keep = device_model(gen)
+    cache = vkv.Cache(n_streams=1, n_layers=LAYERS, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
+                      n_q_heads=QH, dtype=vkv.F16)
+    ring = vkv.new_ring(CAP)
+    plan = vkv.decoder_plan(ring, 0, CAP)
+    k0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
+    v0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
+    vkv.synth_rows(k0.data_ptr(), KV_DIM, SEED, vkv.TAG_K, nl=LAYERS, p0=0, np_=CAP, hip_stream=sp)
+    vkv.synth_rows(v0.data_ptr(), KV_DIM, SEED, vkv.TAG_V, nl=LAYERS, p0=0, np_=CAP, hip_stream=sp)
+    cache.append(0, 0, LAYERS, vkv.plan_segs(plan.write_seg, plan.write_nseg), k0.data_ptr(),
+                 v0.data_ptr(), hip_stream=sp)
+    vkv.decoder_commit(ring, plan)
+    torch.cuda.synchronize()
+    del k0, v0
+    audio = torch.randn(warmup + steps, DIM, device="cuda", generator=gen) * 0.1
+    logits = torch.empty(VOCAB, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws_bytes = vkv.decoder_token_workspace(model)
+    ws = torch.empty(ws_bytes // 4 + 64, device="cuda")
+    ws_ptr = (ws.data_ptr() + 255) & ~255
+    tokens = torch.randint(0, VOCAB, (warmup + steps,), generator=torch.Generator().manual_seed(1))
+
+    def step(i):
+        vkv.decoder_token(cache, 0, ring, model, int(tokens[i]), audio[i].data_ptr(),
+                          logits.data_ptr(), tok.data_ptr(), ws_ptr, ws_bytes, hip_stream=sp)
+
+    total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
+    assert bool(torch.isfinite(logits).all())
+    assert ring.next_absolute_position == CAP + warmup + steps
+    cache.close()
+    del keep
+    return total_ms, step_ms, wall
+
+
+def token_bytes():
+    """Weights + the KV window read (26 layers x 8192 x 2 x 1024 f16) + the
+    appended rows and the per-layer activations (small)."""
+    return weights_bytes_per_token() + decode_bytes_per_stream_token(CAP, 1)
+
+
+def cpu_token_leg(target_seconds):
+    """The oracle's CPU restatement of a token: 26 x (one layer's projections +
+    the attention step of one layer) + logits, from timed samples of each."""
+    w = cpu_weights_leg(target_seconds / 2)
+    a = cpu_leg(1, target_seconds / 2)
+    t_proj = 1.0 / w["value"]           # 26 layers' projections + logits
+    t_attn = 1.0 / a["value"]           # 26 layers' append + attention
+    return {"value": 1.0 / (t_proj + t_attn), "unit": "tokens/s", "cores": w["cores"],
+            "kind": "port",
+            "sample": f"projections: {w['sample']}; attention: {a['sample']}; token = sum"}
 
 
 def cpu_weights_leg(target_seconds):
@@ -476,6 +569,20 @@ def main():
                   "layers": layers, "window": CAP, "kv_heads": KVH, "q_heads": QH,
                   "head_dim": HD, "streams": 1, "bytes": "mean over the steps"}
         kernel = "k_decode<FmtF16> (append fused)"
+    elif args.workload == "decoder_token_q4km":
+        total_ms, step_ms, wall = gpu_token(args.steps, args.warmup)
+        bytes_step = token_bytes()
+        units_per_step = 1
+        res = {"metric": "decoder tokens/s (whole step: Q4_K_M projections + f16 KV attention at "
+                         "the 8192 window, 26 layers, logits, argmax) and HBM GB/s",
+               "unit": "tokens/s"}
+        config = {"workload": "one decoder token through vkv_decoder_token: embedding + audio, "
+                              "26 x (RMSNorm + Q/K/V, RoPE + append + attention over the full "
+                              "8192-slot f16 ring, O + residual, RMSNorm*(1+ada) + SwiGLU, W2 + "
+                              "residual), final norm, 131072-row logits, argmax",
+                  "layers": LAYERS, "dim": DIM, "hidden": HIDDEN, "vocab": VOCAB, "window": CAP,
+                  "bytes_per_token": bytes_step, "launches_per_token": 5 * LAYERS + 3}
+        kernel = "k_matvec + k_decode (133 launches per token)"
     elif args.workload == "decoder_weights_q4km":
         total_ms, step_ms, wall = gpu_weights(args.steps, args.warmup)
         bytes_step = weights_bytes_per_token()
@@ -543,6 +650,8 @@ def main():
     })
     if not args.no_cpu and args.workload == "decoder_weights_q4km":
         res["cpu_baseline"] = cpu_weights_leg(args.cpu_seconds)
+    elif not args.no_cpu and args.workload == "decoder_token_q4km":
+        res["cpu_baseline"] = cpu_token_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload != "encoder_f16":
         res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds)
     print(json.dumps(res), flush=True)

@@ -280,6 +280,20 @@ vkv_status vkv_decoder_step_rope(vkv_cache *cache, int32_t stream0, int32_t n_st
                                  float *out, int32_t n_q_heads, float scale, float rope_theta,
                                  vkv_plan *plans_out, void *hip_stream);
 
+/* One layer range of a decoder step whose one-row plan the caller made for
+ * the token with vkv_decoder_plan(ring, position, 1, plan): append k/v
+ * ([layer][kv_dim]) at the plan's slot, rotate q and k by RoPE at `position`
+ * when rope_theta > 0, and attend over the plan's read window; the caller
+ * calls vkv_decoder_commit once after the last layer (run_decoder_step,
+ * src/voxtral.cpp:5227-5232 and :5358).  This is the per-layer form that
+ * build_decoder_layer needs (:2629-2887): layer l+1's projections read layer
+ * l's attention output. */
+vkv_status vkv_decoder_layer_step(vkv_cache *cache, int32_t stream, const vkv_plan *plan,
+                                  int64_t position, int32_t layer0, int32_t n_layers,
+                                  const float *q, const float *k, const float *v, float *out,
+                                  int32_t n_q_heads, float scale, float rope_theta,
+                                  void *hip_stream);
+
 /* The same RoPE in place on f32 rows x[n_outer][n_rows][row_len] (row_len a
  * multiple of head_dim, head_dim % 8 == 0); row r is at position pos0 + r.
  * For the prefill's q and k before vkv_decoder_prefill. */
@@ -371,6 +385,64 @@ vkv_status vkv_quantize_q8_k(const float *x, int64_t n, const float *norm_w, con
  * 3008) for one row of the table. */
 vkv_status vkv_dequantize(int32_t dtype, const void *blocks, int64_t n, float *y,
                           void *hip_stream);
+
+/* The decoder step's input row: ggml_get_rows(tok_embeddings, token) +
+ * audio embedding (src/voxtral.cpp:3008-3019): row `token` of a Q4_K/Q6_K
+ * table [n_rows][n_cols], dequantized, plus add[] when add is not NULL. */
+vkv_status vkv_embed(int32_t dtype, const void *table, int32_t n_rows, int64_t n_cols,
+                     int32_t token, const float *add, float *y, void *hip_stream);
+
+/* ggml_argmax of f32 logits (emit_logits_argmax, src/voxtral.cpp:2966-2972):
+ * the last index of the maximum (ggml_vec_argmax_f32 keeps updating the index
+ * while x[i] equals the running max); NaN input gives an unspecified index.
+ * x: 16-byte aligned device array; out: one int32 in device memory. */
+vkv_status vkv_argmax(const float *x, int64_t n, int32_t *out, void *hip_stream);
+
+/* ---------------------------------------------------------------------------
+ * One decoder token (run_decoder_step's graph, src/voxtral.cpp:2981-3040 and
+ * build_decoder_layer :2629-2887): x = get_rows(tok_embeddings, token) +
+ * audio_emb; per layer h = rms_norm(x) * attn_norm, q/k/v = W h, RoPE of q
+ * and k at the token's position, K/V append at the ring slot, attention over
+ * the window, x += W_o attn, h = rms_norm(x) * ffn_norm (* (1 + ada)),
+ * x += W2 (silu(W1 h) * (W3 h)); logits = output (rms_norm(x) * out_norm);
+ * argmax.  Weights are GGUF tensors' bytes in device memory (Q4_K / Q6_K);
+ * norms and ada scales f32.  The ring is planned once and committed after
+ * the last layer.
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_dec_layer {
+    const float *attn_norm;        /* [dim] */
+    const void *attn_q, *attn_k, *attn_v, *attn_o;
+    int32_t attn_q_type, attn_k_type, attn_v_type, attn_o_type;
+    const float *ffn_norm;         /* [dim] */
+    const float *ada_scale;        /* [dim] ada_mlp(time_emb) of this layer, or NULL */
+    const void *ffn_w1, *ffn_w2, *ffn_w3;
+    int32_t ffn_w1_type, ffn_w2_type, ffn_w3_type;
+} vkv_dec_layer;
+
+typedef struct vkv_dec_model {
+    int32_t n_layers, dim, hidden, n_q_heads, n_kv_heads, head_dim, vocab;
+    float norm_eps, rope_theta;
+    const void *tok_embeddings;    /* [vocab][dim] */
+    int32_t tok_embeddings_type;
+    const float *out_norm;         /* [dim] */
+    const void *output;            /* [vocab][dim]; the tied model passes tok_embeddings */
+    int32_t output_type;
+    const vkv_dec_layer *layers;   /* host array of n_layers */
+} vkv_dec_model;
+
+/* Device workspace the token needs (bytes); 256-byte aligned by the caller. */
+size_t vkv_decoder_token_workspace(const vkv_dec_model *model);
+
+/* Runs the token at position ring->next_absolute_position of `stream` in the
+ * cache (whose n_layers / heads must match the model).  audio_emb: [dim] f32
+ * device row or NULL; logits: [vocab] f32 device; token_out: one int32 in
+ * device memory (the greedy token).  plan_out (host, may be NULL) receives
+ * the committed plan.  The workspace keeps, after the call, x (the final
+ * residual stream) at offset 0 as dim floats. */
+vkv_status vkv_decoder_token(vkv_cache *cache, int32_t stream, vkv_ring *ring,
+                             const vkv_dec_model *model, int32_t token, const float *audio_emb,
+                             float *logits, int32_t *token_out, void *workspace,
+                             size_t workspace_bytes, vkv_plan *plan_out, void *hip_stream);
 
 /* ---------------------------------------------------------------------------
  * Seeded synthetic rows (integer Irwin-Hall N(0,1), bit-identical to the CPU

@@ -115,6 +115,7 @@ _protos = {
     "orc_rms_norm": (None, [_vp, _vp, _i64, _f32]),
     "orc_norm_act": (None, [_vp, _i64, _vp, _vp, _f32, _vp]),
     "orc_silu": (_f32, [_f32]),
+    "orc_argmax": (_i32, [_vp, _i64]),
     "orc_wrow_bytes": (_i64, [ctypes.c_int, _i64]),
     "orc_matvec": (None, [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, ctypes.c_int]),
     "orc_decode_step_mimic_mt": (_f64, [ctypes.c_int, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
@@ -385,6 +386,12 @@ def norm_act(x, norm_w=None, ada=None, eps=1e-5):
 def silu(v):
     return np.array([lib.orc_silu(float(t)) for t in np.asarray(v, np.float32).ravel()],
                     dtype=np.float32)
+
+
+def argmax(x):
+    """ggml_argmax: the last index of the maximum (finite input)."""
+    x = _f32a(x).ravel()
+    return lib.orc_argmax(_ptr(x), x.size)
 
 
 def wrow_bytes(dtype, n_in):

@@ -238,6 +238,18 @@ void orc_norm_act(const float *x, int64_t n, const float *norm_w, const float *a
 
 float orc_silu(float x) { return x / (1.0f + expf(-x)); }
 
+/* ggml_vec_argmax_f32: max = MAX(max, x[i]) with MAX(a, b) = a > b ? a : b,
+ * and idx = i whenever max == x[i] (ggml_argmax, src/voxtral.cpp:2970) */
+int32_t orc_argmax(const float *x, int64_t n) {
+    float max = -INFINITY;
+    int32_t idx = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        max = max > x[i] ? max : x[i];
+        if (max == x[i]) idx = (int32_t)i;
+    }
+    return idx;
+}
+
 int64_t orc_wrow_bytes(int dtype, int64_t n_in) {
     return (n_in / QK) * (dtype == ORC_Q4_K ? 144 : dtype == ORC_Q6_K ? 210 : 292);
 }

@@ -209,6 +209,7 @@ void orc_rms_norm(const float *x, float *y, int64_t n, float eps);
 void orc_norm_act(const float *x, int64_t n, const float *norm_w, const float *ada, float eps,
                   float *y);
 float orc_silu(float x);
+int32_t orc_argmax(const float *x, int64_t n);
 int64_t orc_wrow_bytes(int dtype, int64_t n_in);
 void orc_matvec(int dtype, const uint8_t *w, int64_t n_rows, int64_t n_in, const float *x,
                 float *y, int n_threads);

@@ -47,6 +47,8 @@ def test_struct_layout_matches_c():
         "vkv_cache_params": (vkv.CacheParams, None),
         "vkv_cache_layout": (vkv.CacheLayout, None),
         "vkv_mv_out": (vkv.MvOut, None),
+        "vkv_dec_layer": (vkv.DecLayer, None),
+        "vkv_dec_model": (vkv.DecModel, None),
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "vkv.h"', "int main(void){"]
     for cname, (py, _) in structs.items():
@@ -143,6 +145,16 @@ def test_error_statuses_without_device():
     assert "4 GiB" in vkv.last_error()
     assert L.vkv_quantize_q8_k(x, 3072, None, None, 1e-5, 4098, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_dequantize(vkv.Q8_0, 16, 256, 16, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_embed(vkv.Q6_K, 16, 10, 3072, 10, None, 16, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_embed(vkv.Q6_K, 16, 10, 3072, -1, None, 16, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_argmax(x, 0, 16, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_argmax(ctypes.c_void_p(4100), 10, 16, None) == vkv.INVALID_ARGUMENT
+    m = vkv.DecModel()
+    assert L.vkv_decoder_token_workspace(ctypes.byref(m)) == 0
+    assert L.vkv_decoder_token(None, 0, None, ctypes.byref(m), 0, None, None, None, None, 0,
+                               None, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_decoder_layer_step(None, 0, None, 0, 0, 1, None, None, None, None, 32, 1.0,
+                                    1e6, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_dequantize(vkv.Q4_K, 16, 255, 16, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_cache_destroy(None) == vkv.OK
     with pytest.raises(vkv.VkvError) as ei:

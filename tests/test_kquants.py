@@ -224,3 +224,15 @@ def test_silu_closed_form():
     v = np.array([-20.0, -1.0, 0.0, 0.5, 3.0, 30.0], np.float32)
     want = v.astype(np.float64) / (1 + np.exp(-v.astype(np.float64)))
     np.testing.assert_allclose(oracle.silu(v), want, rtol=1e-6, atol=1e-12)
+
+
+def test_argmax_last_index_of_the_maximum():
+    x = np.array([1.0, 3.0, -2.0, 3.0, 0.5], np.float32)
+    assert oracle.argmax(x) == 3                    # ties: the later index
+    assert oracle.argmax(np.full(7, -np.inf, np.float32)) == 6
+    assert oracle.argmax(np.array([2.0], np.float32)) == 0
+    rng = np.random.default_rng(11)
+    for _ in range(20):
+        v = rng.integers(-50, 50, 4096).astype(np.float32)   # many ties
+        want = v.size - 1 - int(np.argmax(v[::-1]))
+        assert oracle.argmax(v) == want

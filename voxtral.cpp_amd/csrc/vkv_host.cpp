@@ -239,8 +239,11 @@ int32_t pick_chunk(const vkv_cache *c, int64_t units, int32_t n_kv_max, int32_t 
         *n_chunks_out = 1;
         return std::max(n_kv_max, 1);
     }
+    // the largest chunk (2048 .. 64 slots) that still gives every CU a work
+    // group: fewer, longer chunks amortise each work group's prologue and
+    // leave less to merge
     int32_t chunk = 2048;
-    while (chunk > 64 && units * ((n_kv_max + chunk - 1) / chunk) < 1536) chunk /= 2;
+    while (chunk > 64 && units * ((n_kv_max + chunk - 1) / chunk) < c->n_cus) chunk /= 2;
     if (forced_chunk()) chunk = forced_chunk();
     for (;;) {
         const int32_t nc = std::max(1, (n_kv_max + chunk - 1) / chunk);
@@ -742,22 +745,59 @@ vkv_status vkv_decode_attn(vkv_cache *cache, int32_t stream0, int32_t n_streams,
 }
 
 namespace {
+// Checks shared by the planned decode steps: the cache span, heads, pointers,
+// scale and the RoPE arguments.
+vkv_status check_step_args(vkv_cache *cache, int32_t stream0, int32_t n_streams, int32_t layer0,
+                           int32_t n_layers, const float *q, const float *k, const float *v,
+                           float *out, int32_t n_q_heads, float scale, const float *rope_theta,
+                           const int64_t *positions, const char *what) {
+    if (vkv_status st = check_cache(cache, what)) return st;
+    if (vkv_status st = check_span(cache, stream0, n_streams, layer0, n_layers, what)) return st;
+    if (n_streams > kMaxStreams)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: at most %d streams per call", what, kMaxStreams);
+    if (vkv_status st = check_heads(cache, n_q_heads, what)) return st;
+    if (!positions || !q || !k || !v || !out)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: null argument", what);
+    if (vkv_status st = check_aligned(what, {q, k, v, out})) return st;
+    if (!std::isfinite(scale)) return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: scale", what);
+    if (rope_theta) {
+        if (!(std::isfinite(*rope_theta) && *rope_theta > 0.0f))
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: rope theta", what);
+        for (int32_t s = 0; s < n_streams; ++s)
+            if (positions[s] < 0 || positions[s] >= (1 << 24))
+                return fail(VKV_STATUS_INVALID_ARGUMENT,
+                            "%s: rope position %lld outside [0, 2^24)", what,
+                            (long long)positions[s]);
+    }
+    return VKV_STATUS_OK;
+}
+
+// The read window of a one-row plan, checked to end at the appended row.
+vkv_status planned_window(const vkv_cache *cache, const vkv_plan &plan, SegPair *seg,
+                          const char *what) {
+    if (plan.n_new != 1 || plan.write_nseg != 1 || plan.write_seg[0].len != 1)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: the plan must append exactly one row", what);
+    if (vkv_status st = check_segs(cache, plan.read_seg, plan.read_nseg, what)) return st;
+    if (plan.write_seg[0].slot < 0 || plan.write_seg[0].slot >= cache->p.capacity)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: write slot outside the cache", what);
+    *seg = seg_pair(plan.read_seg, plan.read_nseg);
+    const int32_t n_kv = seg->n0 + seg->n1;
+    const int32_t newest = n_kv - 1 < seg->n0 ? seg->s0 + n_kv - 1 : seg->s1 + (n_kv - 1 - seg->n0);
+    if (n_kv < 1 || newest != plan.write_seg[0].slot)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: plan window does not end at the new row", what);
+    return VKV_STATUS_OK;
+}
+
 vkv_status decoder_step_impl(vkv_cache *cache, int32_t stream0, int32_t n_streams,
                              vkv_ring *rings, const int64_t *positions, int32_t layer0,
                              int32_t n_layers, const float *q, const float *k, const float *v,
                              float *out, int32_t n_q_heads, float scale, const float *rope_theta,
                              vkv_plan *plans_out, void *hip_stream) {
     if (plans_out && n_streams > 0) std::memset(plans_out, 0, sizeof(vkv_plan) * (size_t)n_streams);
-    if (vkv_status st = check_cache(cache, "decoder step")) return st;
-    if (vkv_status st = check_span(cache, stream0, n_streams, layer0, n_layers, "decoder step"))
+    if (vkv_status st = check_step_args(cache, stream0, n_streams, layer0, n_layers, q, k, v, out,
+                                        n_q_heads, scale, rope_theta, positions, "decoder step"))
         return st;
-    if (n_streams > kMaxStreams)
-        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder step: at most %d streams per call", kMaxStreams);
-    if (vkv_status st = check_heads(cache, n_q_heads, "decoder step")) return st;
-    if (!rings || !positions || !q || !k || !v || !out)
-        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder step: null argument");
-    if (vkv_status st = check_aligned("decoder step", {q, k, v, out})) return st;
-    if (!std::isfinite(scale)) return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder step: scale");
+    if (!rings) return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder step: null argument");
     vkv_plan plans[kMaxStreams];
     SegPair segs[kMaxStreams];
     for (int32_t s = 0; s < n_streams; ++s) {
@@ -769,21 +809,8 @@ vkv_status decoder_step_impl(vkv_cache *cache, int32_t stream0, int32_t n_stream
             std::snprintf(msg, sizeof(msg), "decoder step (stream %d): %s", stream0 + s, g_last_error.c_str());
             return fail(st, "%s", msg);
         }
-        segs[s] = seg_pair(plans[s].read_seg, plans[s].read_nseg);
-        // The appended row is the newest logical index of the window.
-        const int32_t n_kv = segs[s].n0 + segs[s].n1;
-        const int32_t newest = n_kv - 1 < segs[s].n0 ? segs[s].s0 + n_kv - 1 : segs[s].s1 + (n_kv - 1 - segs[s].n0);
-        if (n_kv < 1 || newest != plans[s].write_seg[0].slot)
+        if (planned_window(cache, plans[s], &segs[s], "decoder step"))
             return fail(VKV_STATUS_INTERNAL_ERROR, "decoder step: plan window does not end at the new row");
-    }
-    if (rope_theta) {
-        if (!(std::isfinite(*rope_theta) && *rope_theta > 0.0f))
-            return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder step: rope theta");
-        for (int32_t s = 0; s < n_streams; ++s)
-            if (positions[s] >= (1 << 24))
-                return fail(VKV_STATUS_INVALID_ARGUMENT,
-                            "decoder step: rope position %lld beyond exact f32 (2^24)",
-                            (long long)positions[s]);
     }
     DeviceGuard guard(cache->p.device);
     if (vkv_status st = do_decode(cache, stream0, n_streams, layer0, n_layers, segs, q, out,
@@ -815,6 +842,33 @@ vkv_status vkv_decoder_step_rope(vkv_cache *cache, int32_t stream0, int32_t n_st
                                  vkv_plan *plans_out, void *hip_stream) {
     return decoder_step_impl(cache, stream0, n_streams, rings, positions, layer0, n_layers, q, k,
                              v, out, n_q_heads, scale, &rope_theta, plans_out, hip_stream);
+}
+
+// build_decoder_layer's RoPE, SET_ROWS and attention (src/voxtral.cpp:2667-2854)
+// for a layer range under a plan made once for the token (run_decoder_step,
+// :5227-5232); the caller commits after the last layer (:5358).
+vkv_status vkv_decoder_layer_step(vkv_cache *cache, int32_t stream, const vkv_plan *plan,
+                                  int64_t position, int32_t layer0, int32_t n_layers,
+                                  const float *q, const float *k, const float *v, float *out,
+                                  int32_t n_q_heads, float scale, float rope_theta,
+                                  void *hip_stream) {
+    const float *theta = rope_theta > 0.0f ? &rope_theta : nullptr;
+    if (!(rope_theta <= 0.0f || std::isfinite(rope_theta)))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder layer step: rope theta");
+    if (vkv_status st = check_step_args(cache, stream, 1, layer0, n_layers, q, k, v, out, n_q_heads,
+                                        scale, theta, &position, "decoder layer step"))
+        return st;
+    if (!plan) return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder layer step: null plan");
+    SegPair seg;
+    if (vkv_status st = planned_window(cache, *plan, &seg, "decoder layer step")) return st;
+    if (plan->absolute_start != position)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder layer step: position %lld is not the plan's %lld",
+                    (long long)position, (long long)plan->absolute_start);
+    DeviceGuard guard(cache->p.device);
+    if (vkv_status st = do_decode(cache, stream, 1, layer0, n_layers, &seg, q, out, n_q_heads, scale,
+                                  k, v, as_stream(hip_stream), theta, &position))
+        return st;
+    return ok();
 }
 
 // ggml_rope_ext mode 0 (src/voxtral.cpp:2667-2671) on f32 rows in place
@@ -1039,8 +1093,152 @@ vkv_status vkv_dequantize(int32_t dtype, const void *blocks, int64_t n, float *y
     if (!blocks || !y) return fail(VKV_STATUS_INVALID_ARGUMENT, "dequantize: null argument");
     if (n / 8 > (int64_t)0x7fffffff * 256)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "dequantize: n too large");
-    hipError_t e = launch_kq_dequant(dtype, (const uint8_t *)blocks, n, y, as_stream(hip_stream));
+    hipError_t e = launch_kq_dequant(dtype, (const uint8_t *)blocks, n, nullptr, y,
+                                     as_stream(hip_stream));
     if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+    return ok();
+}
+
+vkv_status vkv_embed(int32_t dtype, const void *table, int32_t n_rows, int64_t n_cols,
+                     int32_t token, const float *add, float *y, void *hip_stream) {
+    const int64_t bb = kq_block_bytes(dtype);
+    if (!bb) return fail(VKV_STATUS_INVALID_ARGUMENT, "embed: dtype %d", dtype);
+    if (n_cols < 256 || n_cols % 256 != 0 || n_cols > ((int64_t)1 << 30))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "embed: n_cols=%lld", (long long)n_cols);
+    if (token < 0 || token >= n_rows)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "embed: token %d outside [0, %d)", token, n_rows);
+    if (!table || !y) return fail(VKV_STATUS_INVALID_ARGUMENT, "embed: null argument");
+    const uint8_t *row = (const uint8_t *)table + (int64_t)token * (n_cols / 256) * bb;
+    hipError_t e = launch_kq_dequant(dtype, row, n_cols, add, y, as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "embed launch");
+    return ok();
+}
+
+vkv_status vkv_argmax(const float *x, int64_t n, int32_t *out, void *hip_stream) {
+    if (n < 1 || n > 0x7fffffff) return fail(VKV_STATUS_INVALID_ARGUMENT, "argmax: n=%lld", (long long)n);
+    if (!x || !out) return fail(VKV_STATUS_INVALID_ARGUMENT, "argmax: null argument");
+    if (vkv_status st = check_aligned("argmax", {x})) return st;
+    hipError_t e = launch_argmax(x, (int)n, out, as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "argmax launch");
+    return ok();
+}
+
+// ---- one decoder token ----
+
+namespace {
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+struct TokenBuffers {
+    float *x, *q, *k, *v, *attn, *ffn;
+    size_t bytes;
+};
+
+TokenBuffers token_buffers(const vkv_dec_model &m, uint8_t *base) {
+    TokenBuffers t{};
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        float *p = base ? reinterpret_cast<float *>(base + off) : nullptr;
+        off += align256(n * sizeof(float));
+        return p;
+    };
+    const size_t qd = (size_t)m.n_q_heads * m.head_dim, kd = (size_t)m.n_kv_heads * m.head_dim;
+    t.x = take((size_t)m.dim);
+    t.q = take(qd);
+    t.k = take(kd);
+    t.v = take(kd);
+    t.attn = take(qd);
+    t.ffn = take((size_t)m.hidden);
+    t.bytes = off;
+    return t;
+}
+
+vkv_status check_model(const vkv_dec_model *m) {
+    if (!m || !m->layers || m->n_layers < 1)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: null model or no layers");
+    if (m->dim < 256 || m->dim % 256 || m->hidden < 256 || m->hidden % 256 || m->head_dim < 8 ||
+        m->n_q_heads < 1 || m->n_kv_heads < 1 || m->vocab < 1 ||
+        (int64_t)m->n_q_heads * m->head_dim % 256)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: model dimensions");
+    if (!m->tok_embeddings || !m->output || !m->out_norm)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: null embedding/output/norm");
+    for (int32_t l = 0; l < m->n_layers; ++l) {
+        const vkv_dec_layer &L = m->layers[l];
+        if (!L.attn_norm || !L.ffn_norm || !L.attn_q || !L.attn_k || !L.attn_v || !L.attn_o ||
+            !L.ffn_w1 || !L.ffn_w2 || !L.ffn_w3)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: layer %d has a null tensor", l);
+    }
+    return VKV_STATUS_OK;
+}
+
+}  // namespace
+
+size_t vkv_decoder_token_workspace(const vkv_dec_model *model) {
+    if (check_model(model)) return 0;
+    return token_buffers(*model, nullptr).bytes;
+}
+
+vkv_status vkv_decoder_token(vkv_cache *cache, int32_t stream, vkv_ring *ring,
+                             const vkv_dec_model *model, int32_t token, const float *audio_emb,
+                             float *logits, int32_t *token_out, void *workspace,
+                             size_t workspace_bytes, vkv_plan *plan_out, void *hip_stream) {
+    if (plan_out) std::memset(plan_out, 0, sizeof(*plan_out));
+    if (vkv_status st = check_model(model)) return st;
+    const vkv_dec_model &m = *model;
+    if (vkv_status st = check_cache(cache, "decoder token")) return st;
+    if (m.n_layers != cache->p.n_layers || m.n_kv_heads != cache->p.n_kv_heads ||
+        m.head_dim != cache->p.head_dim || m.n_q_heads > cache->p.n_q_heads)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: model and cache shapes differ");
+    if (!ring || !logits || !token_out || !workspace)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: null argument");
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: workspace not 256-byte aligned");
+    const TokenBuffers t = token_buffers(m, (uint8_t *)workspace);
+    if (workspace_bytes < t.bytes)
+        return fail(VKV_STATUS_BUFFER_TOO_SMALL, "decoder token: workspace %zu < %zu bytes",
+                    workspace_bytes, t.bytes);
+    if (ring->capacity > cache->p.capacity)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: ring capacity exceeds the cache");
+    const int64_t pos = ring->next_absolute_position;
+    vkv_plan plan;
+    if (vkv_status st = vkv_decoder_plan(ring, pos, 1, &plan)) return st;
+    const int32_t qd = m.n_q_heads * m.head_dim, kd = m.n_kv_heads * m.head_dim;
+    const float scale = 1.0f / std::sqrt((float)m.head_dim);
+    void *st = hip_stream;
+    if (vkv_status s = vkv_embed(m.tok_embeddings_type, m.tok_embeddings, m.vocab, m.dim, token,
+                                 audio_emb, t.x, st))
+        return s;
+    for (int32_t l = 0; l < m.n_layers; ++l) {
+        const vkv_dec_layer &L = m.layers[l];
+        const vkv_mv_out qkv[3] = {{L.attn_q, L.attn_q_type, qd, t.q, nullptr},
+                                   {L.attn_k, L.attn_k_type, kd, t.k, nullptr},
+                                   {L.attn_v, L.attn_v_type, kd, t.v, nullptr}};
+        if (vkv_status s = vkv_matvec(t.x, m.dim, L.attn_norm, nullptr, m.norm_eps, qkv, 3,
+                                      VKV_MV_STORE, st))
+            return s;
+        if (vkv_status s = vkv_decoder_layer_step(cache, stream, &plan, pos, l, 1, t.q, t.k, t.v,
+                                                  t.attn, m.n_q_heads, scale, m.rope_theta, st))
+            return s;
+        const vkv_mv_out o[1] = {{L.attn_o, L.attn_o_type, m.dim, t.x, t.x}};
+        if (vkv_status s = vkv_matvec(t.attn, qd, nullptr, nullptr, m.norm_eps, o, 1, VKV_MV_STORE, st))
+            return s;
+        const vkv_mv_out gu[2] = {{L.ffn_w1, L.ffn_w1_type, m.hidden, t.ffn, nullptr},
+                                  {L.ffn_w3, L.ffn_w3_type, m.hidden, nullptr, nullptr}};
+        if (vkv_status s = vkv_matvec(t.x, m.dim, L.ffn_norm, L.ada_scale, m.norm_eps, gu, 2,
+                                      VKV_MV_SWIGLU, st))
+            return s;
+        const vkv_mv_out down[1] = {{L.ffn_w2, L.ffn_w2_type, m.dim, t.x, t.x}};
+        if (vkv_status s = vkv_matvec(t.ffn, m.hidden, nullptr, nullptr, m.norm_eps, down, 1,
+                                      VKV_MV_STORE, st))
+            return s;
+    }
+    const vkv_mv_out head[1] = {{m.output, m.output_type, m.vocab, logits, nullptr}};
+    if (vkv_status s = vkv_matvec(t.x, m.dim, m.out_norm, nullptr, m.norm_eps, head, 1,
+                                  VKV_MV_STORE, st))
+        return s;
+    if (vkv_status s = vkv_argmax(logits, m.vocab, token_out, st)) return s;
+    vkv_decoder_commit(ring, &plan);
+    if (plan_out) *plan_out = plan;
     return ok();
 }
 

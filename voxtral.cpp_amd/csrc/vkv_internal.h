@@ -125,7 +125,9 @@ struct MvArgs {
 hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st);
 hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const float *ada, float eps,
                             uint8_t *out, hipStream_t st);
-hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, float *y, hipStream_t st);
+hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const float *add, float *y,
+                             hipStream_t st);
+hipError_t launch_argmax(const float *x, int n, int32_t *out, hipStream_t st);
 
 hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st);
 hipError_t launch_gather(const uint8_t *src, int64_t row_bytes, SegPair seg, uint8_t *dst,

@@ -1120,25 +1120,58 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
     decode_merge_finish<W, GQA>(a, it, msm);
 }
 
-__global__ void __launch_bounds__(256) k_combine(CombineArgs a) {
-    const int h = blockIdx.x;
-    const int layer = blockIdx.y;
-    const int s = blockIdx.z;
-    const int64_t head = ((int64_t)s * a.n_layers + layer) * a.n_q_heads + h;
+// One work group of head_dim (128) threads per (stream, layer, query head):
+// the chunk maxima, weights exp2(m_c - M) and the weighted sum of l_c are
+// reduced once for the group; each thread then accumulates its dimension over
+// the chunks with the partial loads batched (they do not depend on each
+// other), 128 chunk weights at a time through LDS.
+__global__ void __launch_bounds__(128) k_combine(CombineArgs a) {
+    __shared__ float sw[128];
+    __shared__ float red[2][2];
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int64_t head = ((int64_t)blockIdx.z * a.n_layers + blockIdx.y) * a.n_q_heads + blockIdx.x;
     const int64_t p0 = head * a.n_chunks;
-    for (int d = threadIdx.x; d < a.head_dim; d += blockDim.x) {
-        float M = -INFINITY;
-        for (int c = 0; c < a.n_chunks; ++c) M = fmaxf(M, a.part_ml[(p0 + c) * 2]);
-        float O = 0.0f, L = 0.0f;
-        if (M != -INFINITY) {
-            for (int c = 0; c < a.n_chunks; ++c) {
-                const float w = fast_exp2(a.part_ml[(p0 + c) * 2] - M);
-                L = fmaf(a.part_ml[(p0 + c) * 2 + 1], w, L);
-                O = fmaf(a.part_o[(p0 + c) * a.head_dim + d], w, O);
-            }
-        }
-        a.out[head * a.head_dim + d] = L > 0.0f ? O / L : 0.0f;
+    const float *ml = a.part_ml + p0 * 2;
+    const float *po = a.part_o + p0 * a.head_dim + t;
+    const int n = a.n_chunks;
+    float m = -INFINITY;
+    for (int c = t; c < n; c += 128) m = fmaxf(m, ml[2 * c]);
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if (lane == 0) red[0][wave] = m;
+    __syncthreads();
+    const float M = fmaxf(red[0][0], red[0][1]);
+    if (M == -INFINITY) {
+        a.out[head * a.head_dim + t] = 0.0f;
+        return;
     }
+    float O = 0.0f, l = 0.0f;
+    for (int c0 = 0; c0 < n; c0 += 128) {
+        const int c = c0 + t;
+        float w = 0.0f;
+        if (c < n) {
+            w = fast_exp2(ml[2 * c] - M);
+            l = fmaf(ml[2 * c + 1], w, l);
+        }
+        sw[t] = w;
+        __syncthreads();
+        const int cn = min(128, n - c0);
+        int j = 0;
+        for (; j + 8 <= cn; j += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = po[(int64_t)(c0 + j + u) * a.head_dim];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) O = fmaf(v[u], sw[j + u], O);
+        }
+        for (; j < cn; ++j) O = fmaf(po[(int64_t)(c0 + j) * a.head_dim], sw[j], O);
+        __syncthreads();
+    }
+    for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+    if (lane == 0) red[1][wave] = l;
+    __syncthreads();
+    const float L = red[1][0] + red[1][1];
+    a.out[head * a.head_dim + t] = L > 0.0f ? O / L : 0.0f;
 }
 
 // ---------------------------------------------------------------------------

@@ -17,7 +17,9 @@
 //   k_q8k_quant  -- the same prologue alone, to global memory in ggml's
 //                   block_q8_K layout.
 //   k_kq_dequant -- ggml dequantize_row_q4_K / _q6_K (get_rows on the token
-//                   embedding table, src/voxtral.cpp:3008).
+//                   embedding table, src/voxtral.cpp:3008, + the audio
+//                   embedding, :3019).
+//   k_argmax     -- ggml_argmax of the logits (src/voxtral.cpp:2970).
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -518,9 +520,11 @@ __global__ void __launch_bounds__(256) k_q8k_quant(const float *x, int n, const 
     act_finish(r, n, nw, ada, eps, sm, out);
 }
 
-// ggml dequantize_row_q4_K / _q6_K; one thread per 8 consecutive elements.
+// ggml dequantize_row_q4_K / _q6_K, plus add[i] when add is given (the
+// token embedding + audio embedding sum); one thread per 8 elements.
 __global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__restrict__ src,
-                                                    int64_t n, float *__restrict__ y) {
+                                                    int64_t n, const float *__restrict__ add,
+                                                    float *__restrict__ y) {
 #pragma clang fp contract(off)
     const int64_t i8 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
     if (i8 >= n) return;
@@ -562,7 +566,49 @@ __global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__
         }
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) y[i8 + i] = out[i];
+    for (int i = 0; i < 8; ++i) y[i8 + i] = add ? out[i] + add[i8 + i] : out[i];
+}
+
+// ggml_argmax of f32 (ggml_vec_argmax_f32: the running max MAX(max, x[i]) and
+// idx = i whenever x[i] equals it), i.e. for finite input the last index of
+// the maximum.  One work group; (value, index) pairs reduce by larger value,
+// then larger index, so the visiting order does not matter.
+__global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, int n,
+                                                 int32_t *__restrict__ out) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    float bv = -INFINITY;
+    int bi = -1;
+    auto take = [&](float v, int i) {
+        if (v > bv || (v == bv && i > bi)) {
+            bv = v;
+            bi = i;
+        }
+    };
+    const int n4 = n >> 2;
+    for (int j = threadIdx.x; j < n4; j += 1024) {
+        const float4 v = reinterpret_cast<const float4 *>(x)[j];
+        take(v.x, 4 * j);
+        take(v.y, 4 * j + 1);
+        take(v.z, 4 * j + 2);
+        take(v.w, 4 * j + 3);
+    }
+    for (int i = 4 * n4 + threadIdx.x; i < n; i += 1024) take(x[i], i);
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        take(ov, oi);
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 0; w < 16; ++w) take(sv[w], si[w]);
+        out[0] = bi < 0 ? 0 : bi;
+    }
 }
 
 }  // namespace
@@ -581,9 +627,15 @@ hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const fl
     return hipGetLastError();
 }
 
-hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, float *y, hipStream_t st) {
+hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const float *add, float *y,
+                             hipStream_t st) {
     const int64_t threads = n / 8;
-    k_kq_dequant<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(dtype, src, n, y);
+    k_kq_dequant<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(dtype, src, n, add, y);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float *x, int n, int32_t *out, hipStream_t st) {
+    k_argmax<<<1, 1024, 0, st>>>(x, n, out);
     return hipGetLastError();
 }
 

@@ -131,6 +131,22 @@ _f32 = ctypes.c_float
 class MvOut(ctypes.Structure):
     _fields_ = [("w", _vp), ("dtype", _i32), ("n_rows", _i32), ("y", _vp), ("add", _vp)]
 
+
+class DecLayer(ctypes.Structure):
+    _fields_ = [("attn_norm", _vp), ("attn_q", _vp), ("attn_k", _vp), ("attn_v", _vp),
+                ("attn_o", _vp), ("attn_q_type", _i32), ("attn_k_type", _i32),
+                ("attn_v_type", _i32), ("attn_o_type", _i32), ("ffn_norm", _vp),
+                ("ada_scale", _vp), ("ffn_w1", _vp), ("ffn_w2", _vp), ("ffn_w3", _vp),
+                ("ffn_w1_type", _i32), ("ffn_w2_type", _i32), ("ffn_w3_type", _i32)]
+
+
+class DecModel(ctypes.Structure):
+    _fields_ = [("n_layers", _i32), ("dim", _i32), ("hidden", _i32), ("n_q_heads", _i32),
+                ("n_kv_heads", _i32), ("head_dim", _i32), ("vocab", _i32), ("norm_eps", _f32),
+                ("rope_theta", _f32), ("tok_embeddings", _vp), ("tok_embeddings_type", _i32),
+                ("out_norm", _vp), ("output", _vp), ("output_type", _i32),
+                ("layers", _P(DecLayer))]
+
 # prototypes: name -> (restype, argtypes); exactly the functions of include/vkv.h
 PROTOTYPES = {
     "vkv_decoder_plan": (_i32, [_P(Ring), _i64, _i32, _P(Plan)]),
@@ -167,6 +183,13 @@ PROTOTYPES = {
     "vkv_matvec": (_i32, [_vp, _i64, _vp, _vp, _f32, _P(MvOut), _i32, _i32, _vp]),
     "vkv_quantize_q8_k": (_i32, [_vp, _i64, _vp, _vp, _f32, _vp, _vp]),
     "vkv_dequantize": (_i32, [_i32, _vp, _i64, _vp, _vp]),
+    "vkv_decoder_layer_step": (_i32, [_vp, _i32, _P(Plan), _i64, _i32, _i32, _vp, _vp, _vp, _vp,
+                                      _i32, _f32, _f32, _vp]),
+    "vkv_decoder_token_workspace": (ctypes.c_size_t, [_P(DecModel)]),
+    "vkv_decoder_token": (_i32, [_vp, _i32, _P(Ring), _P(DecModel), _i32, _vp, _vp, _vp, _vp,
+                                 ctypes.c_size_t, _P(Plan), _vp]),
+    "vkv_embed": (_i32, [_i32, _vp, _i32, _i64, _i32, _vp, _vp, _vp]),
+    "vkv_argmax": (_i32, [_vp, _i64, _vp, _vp]),
     "vkv_synth_rows": (_i32, [_vp, _i32, _u64, _u32, _i64, _i32, _i64, _i64, _i32, _i64, _i64,
                               _i32, _i64, _vp]),
     "vkv_api_version": (_u32, []),
@@ -339,6 +362,15 @@ class Cache:
                                         scale, rope_theta, plans, hip_stream))
         return plans
 
+    def decoder_layer_step(self, stream, plan, position, layer0, n_layers, q_ptr, k_ptr, v_ptr,
+                           out_ptr, scale, rope_theta=0.0, hip_stream=0, n_q_heads=None):
+        """One layer range of a token planned once with decoder_plan(ring,
+        position, 1); commit after the last layer."""
+        check(lib.vkv_decoder_layer_step(self.handle, stream, ctypes.byref(plan), position, layer0,
+                                         n_layers, q_ptr, k_ptr, v_ptr, out_ptr,
+                                         n_q_heads or self.n_q_heads, scale, rope_theta,
+                                         hip_stream))
+
     def decoder_prefill(self, stream, ring, layer0, n_layers, n_tokens, q_ptr, k_ptr, v_ptr,
                         out_ptr, scale, hip_stream=0, n_q_heads=None):
         check(lib.vkv_decoder_prefill(self.handle, stream, ctypes.byref(ring), layer0, n_layers,
@@ -391,6 +423,29 @@ def quantize_q8_k(x_ptr, n, blocks_ptr, norm_w_ptr=None, ada_ptr=None, eps=1e-5,
 
 def dequantize(dtype, blocks_ptr, n, y_ptr, hip_stream=0):
     check(lib.vkv_dequantize(dtype, blocks_ptr, n, y_ptr, hip_stream))
+
+
+def embed(dtype, table_ptr, n_rows, n_cols, token, y_ptr, add_ptr=None, hip_stream=0):
+    check(lib.vkv_embed(dtype, table_ptr, n_rows, n_cols, token, add_ptr, y_ptr, hip_stream))
+
+
+def decoder_token_workspace(model):
+    return lib.vkv_decoder_token_workspace(ctypes.byref(model))
+
+
+def decoder_token(cache, stream, ring, model, token, audio_ptr, logits_ptr, token_out_ptr,
+                  ws_ptr, ws_bytes, hip_stream=0):
+    """One decoder token (embedding .. argmax) through vkv_decoder_token;
+    returns the committed plan."""
+    plan = Plan()
+    check(lib.vkv_decoder_token(cache.handle, stream, ctypes.byref(ring), ctypes.byref(model),
+                                token, audio_ptr, logits_ptr, token_out_ptr, ws_ptr, ws_bytes,
+                                ctypes.byref(plan), hip_stream))
+    return plan
+
+
+def argmax(x_ptr, n, out_ptr, hip_stream=0):
+    check(lib.vkv_argmax(x_ptr, n, out_ptr, hip_stream))
 
 
 # tags of the synthetic inputs (shared with the oracle's generator)
