@@ -1016,9 +1016,12 @@ vkv_status check_mv_input(const char *what, const float *x, int64_t n_in, const 
 
 }  // namespace
 
-vkv_status vkv_matvec(const float *x, int64_t n_in, const float *norm_w, const float *ada,
-                      float eps, const vkv_mv_out *outs, int32_t n_outs, int32_t epilogue,
-                      void *hip_stream) {
+namespace {
+// vkv_matvec; with amax (one matrix, no SwiGLU) the argmax of its output is
+// fused into the same launch (amax: two zeroed 8-byte words, see k_matvec)
+vkv_status matvec_impl(const float *x, int64_t n_in, const float *norm_w, const float *ada,
+                       float eps, const vkv_mv_out *outs, int32_t n_outs, int32_t epilogue,
+                       void *hip_stream, unsigned long long *amax, int32_t *amax_out) {
     if (vkv_status st = check_mv_input("matvec", x, n_in, norm_w, ada)) return st;
     if (!outs || n_outs < 1 || n_outs > VKV_MV_MAX_OUTS)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: n_outs=%d outside [1, %d]", n_outs,
@@ -1069,9 +1072,22 @@ vkv_status vkv_matvec(const float *x, int64_t n_in, const float *norm_w, const f
     if (swiglu) a.out[1].wg0 = 0x7fffffff;
     for (int32_t k = n_outs; k < VKV_MV_MAX_OUTS; ++k) a.out[k].wg0 = 0x7fffffff;
     if (wg > 0x7fffffff) return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: grid too large");
+    if (amax) {
+        a.amax = amax;
+        a.amax_count = reinterpret_cast<unsigned int *>(amax + 1);
+        a.amax_out = amax_out;
+    }
     hipError_t e = launch_matvec(a, (int)wg, as_stream(hip_stream));
     if (e != hipSuccess) return hip_fail(e, "matvec launch");
     return ok();
+}
+}  // namespace
+
+vkv_status vkv_matvec(const float *x, int64_t n_in, const float *norm_w, const float *ada,
+                      float eps, const vkv_mv_out *outs, int32_t n_outs, int32_t epilogue,
+                      void *hip_stream) {
+    return matvec_impl(x, n_in, norm_w, ada, eps, outs, n_outs, epilogue, hip_stream, nullptr,
+                       nullptr);
 }
 
 vkv_status vkv_quantize_q8_k(const float *x, int64_t n, const float *norm_w, const float *ada,
@@ -1131,6 +1147,7 @@ size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct TokenBuffers {
     float *x, *q, *k, *v, *attn, *ffn;
+    unsigned long long *amax;   // fused argmax: key + finished-work-group count
     size_t bytes;
 };
 
@@ -1149,6 +1166,7 @@ TokenBuffers token_buffers(const vkv_dec_model &m, uint8_t *base) {
     t.v = take(kd);
     t.attn = take(qd);
     t.ffn = take((size_t)m.hidden);
+    t.amax = reinterpret_cast<unsigned long long *>(take(4));
     t.bytes = off;
     return t;
 }
@@ -1205,9 +1223,18 @@ vkv_status vkv_decoder_token(vkv_cache *cache, int32_t stream, vkv_ring *ring,
     const int32_t qd = m.n_q_heads * m.head_dim, kd = m.n_kv_heads * m.head_dim;
     const float scale = 1.0f / std::sqrt((float)m.head_dim);
     void *st = hip_stream;
-    if (vkv_status s = vkv_embed(m.tok_embeddings_type, m.tok_embeddings, m.vocab, m.dim, token,
-                                 audio_emb, t.x, st))
-        return s;
+    if (token < 0 || token >= m.vocab)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: token %d outside [0, %d)", token,
+                    m.vocab);
+    {
+        // embedding row + audio; its first work group also clears the argmax words
+        const int64_t bb = kq_block_bytes(m.tok_embeddings_type);
+        if (!bb) return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: embedding dtype");
+        const uint8_t *row = (const uint8_t *)m.tok_embeddings + (int64_t)token * (m.dim / 256) * bb;
+        hipError_t e = launch_kq_dequant(m.tok_embeddings_type, row, m.dim, audio_emb, t.x,
+                                         as_stream(st), t.amax);
+        if (e != hipSuccess) return hip_fail(e, "decoder token: embedding launch");
+    }
     for (int32_t l = 0; l < m.n_layers; ++l) {
         const vkv_dec_layer &L = m.layers[l];
         const vkv_mv_out qkv[3] = {{L.attn_q, L.attn_q_type, qd, t.q, nullptr},
@@ -1233,10 +1260,9 @@ vkv_status vkv_decoder_token(vkv_cache *cache, int32_t stream, vkv_ring *ring,
             return s;
     }
     const vkv_mv_out head[1] = {{m.output, m.output_type, m.vocab, logits, nullptr}};
-    if (vkv_status s = vkv_matvec(t.x, m.dim, m.out_norm, nullptr, m.norm_eps, head, 1,
-                                  VKV_MV_STORE, st))
+    if (vkv_status s = matvec_impl(t.x, m.dim, m.out_norm, nullptr, m.norm_eps, head, 1,
+                                   VKV_MV_STORE, st, t.amax, token_out))
         return s;
-    if (vkv_status s = vkv_argmax(logits, m.vocab, token_out, st)) return s;
     vkv_decoder_commit(ring, &plan);
     if (plan_out) *plan_out = plan;
     return ok();

@@ -120,13 +120,20 @@ struct MvArgs {
     int32_t rows_per_wg;   // multiple of 4 (one contiguous quarter per wave)
     int32_t swiglu;        // out[0].y = silu(W0 x) * (W1 x), rows paired
     MvOut out[kMvMaxOuts];
+    // Fused argmax of out[0].y (one matrix, no SwiGLU): each work group
+    // atomically maxes its best (order key of the value, row) into *amax;
+    // the last one (by *amax_count) writes the row to *amax_out and resets
+    // both words to 0 for the next use.  nullptr: none.
+    unsigned long long *amax;
+    unsigned int *amax_count;
+    int32_t *amax_out;
 };
 
 hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st);
 hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const float *ada, float eps,
                             uint8_t *out, hipStream_t st);
 hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const float *add, float *y,
-                             hipStream_t st);
+                             hipStream_t st, unsigned long long *zero_words = nullptr);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, hipStream_t st);
 
 hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st);

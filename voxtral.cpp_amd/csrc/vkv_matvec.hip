@@ -425,16 +425,43 @@ __device__ __forceinline__ MvOut out_at(const MvArgs &a, int k) {
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 
-// Unit u of a wave = (row, step): step s of a row covers lane tasks
-// [64 s, 64 s + 64) of the row's 4 * nb quarter blocks.  With SWIGLU the rows
-// alternate between the two matrices: u -> (pair u / 2S, matrix (u / S) & 1).
+// The fused argmax's end: the work group's best key (waves through LDS) is
+// maxed into *a.amax with one 64-bit atomic; the work group that finishes last
+// (the counter) reads the result, writes the row, and clears both words.  The
+// counter add is issued only after the max has returned, so every earlier
+// work group's max is in place when the last one reads.  Keys order values
+// as floats (sign-flipped bits) and, between equal values, the larger row
+// wins: ggml_vec_argmax_f32's last index of the maximum.
+__device__ __forceinline__ void argmax_publish(const MvArgs &a, unsigned long long best) {
+    __shared__ unsigned long long wbest[4];
+    __shared__ int last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) wbest[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = wbest[0];
+        for (int w = 1; w < 4; ++w) b = wbest[w] > b ? wbest[w] : b;
+        const unsigned long long prev = atomicMax(a.amax, b);
+        asm volatile("" ::"v"(prev));   // the max has returned before the count
+        const unsigned int done = atomicAdd(a.amax_count, 1u);
+        last = done == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (last && threadIdx.x == 0) {
+        const unsigned long long k = atomicMax(a.amax, 0ull);
+        a.amax_out[0] = (int32_t)(uint32_t)(k & 0xffffffffull);
+        atomicExch(a.amax, 0ull);
+        atomicExch(a.amax_count, 0u);
+    }
+}
+
 // Unit u of a wave = (row, step): step s of a row covers lane tasks
 // [64 s, 64 s + 64) of the row's 4 * nb quarter blocks.  With SWIGLU the rows
 // alternate between the two matrices: u -> (pair u / 2S, matrix (u / S) & 1).
 // Q4 (the work group's weight dtype) is a template parameter so that every
 // load writes its final registers (a load feeding a merge of two paths would
 // be copied, and the copy waits for the load).
-template <int S, int D0, bool Q4>
+template <int S, int D0, bool Q4, bool AMAX>
 __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, const MvOut &ob,
                                             int row0, int nrow, ActSmem &sm) {
     const int lane = threadIdx.x & 63;
@@ -461,6 +488,7 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
     const XFrag xr = xfrag(sm, Q4, min(lane, tasks - 1));   // the only step when S == 1
 
     float acc = 0.0f, first = 0.0f;
+    unsigned long long best = 0;   // argmax key: order key of the value << 32 | row
     for (int u0 = 0; u0 < units; u0 += D) {
 #pragma unroll
         for (int k = 0; k < D; ++k) {
@@ -485,7 +513,14 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
                 const float r = wave_sum(acc);
                 acc = 0.0f;
                 if (!swiglu) {
-                    if (lane == 0) o0.y[row] = o0.add ? o0.add[row] + r : r;
+                    const float yv = o0.add ? o0.add[row] + r : r;
+                    if (lane == 0) o0.y[row] = yv;
+                    if constexpr (AMAX) {
+                        const uint32_t b = __builtin_bit_cast(uint32_t, yv);
+                        const uint32_t ok = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+                        const unsigned long long key = ((unsigned long long)ok << 32) | (uint32_t)row;
+                        best = key > best ? key : best;
+                    }
                 } else if (m == 0) {
                     first = r;
                 } else if (lane == 0) {
@@ -494,9 +529,10 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
             }
         }
     }
+    if constexpr (AMAX) argmax_publish(a, best);
 }
 
-template <int S, int D>
+template <int S, int D, bool AMAX>
 __global__ void __launch_bounds__(256) k_matvec(MvArgs a) {
     __shared__ ActSmem sm;
     const int wave = threadIdx.x >> 6;
@@ -508,8 +544,8 @@ __global__ void __launch_bounds__(256) k_matvec(MvArgs a) {
     const MvOut ob = a.swiglu ? a.out[1] : o0;
     const int row0 = ((int)blockIdx.x - o0.wg0) * a.rows_per_wg + wave * (a.rows_per_wg >> 2);
     const int nrow = max(0, min(a.rows_per_wg >> 2, o0.n_rows - row0));
-    if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D, true>(a, o0, ob, row0, nrow, sm);
-    else matvec_body<S, D, false>(a, o0, ob, row0, nrow, sm);
+    if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D, true, AMAX>(a, o0, ob, row0, nrow, sm);
+    else matvec_body<S, D, false, AMAX>(a, o0, ob, row0, nrow, sm);
 }
 
 __global__ void __launch_bounds__(256) k_q8k_quant(const float *x, int n, const float *nw,
@@ -524,9 +560,12 @@ __global__ void __launch_bounds__(256) k_q8k_quant(const float *x, int n, const 
 // token embedding + audio embedding sum); one thread per 8 elements.
 __global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__restrict__ src,
                                                     int64_t n, const float *__restrict__ add,
-                                                    float *__restrict__ y) {
+                                                    float *__restrict__ y,
+                                                    unsigned long long *zero_words) {
 #pragma clang fp contract(off)
     const int64_t i8 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    // the decoder token's argmax words start each token at zero
+    if (zero_words && blockIdx.x == 0 && threadIdx.x < 2) zero_words[threadIdx.x] = 0ull;
     if (i8 >= n) return;
     const int64_t b = i8 >> 8;
     const int e0 = (int)(i8 & 255);
@@ -615,9 +654,12 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, in
 
 hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st) {
     const int S = (a.n_in / 256 * 4 + 63) / 64;
-    if (S == 1) k_matvec<1, 3><<<n_wg, 256, 0, st>>>(a);
-    else if (S == 2) k_matvec<2, 2><<<n_wg, 256, 0, st>>>(a);
-    else k_matvec<3, 2><<<n_wg, 256, 0, st>>>(a);
+    // the fused argmax only serves the logits (one step per row)
+    if (a.amax && S != 1) return hipErrorInvalidValue;
+    if (a.amax) k_matvec<1, 3, true><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 1) k_matvec<1, 3, false><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 2) k_matvec<2, 2, false><<<n_wg, 256, 0, st>>>(a);
+    else k_matvec<3, 2, false><<<n_wg, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
@@ -628,9 +670,10 @@ hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const fl
 }
 
 hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const float *add, float *y,
-                             hipStream_t st) {
+                             hipStream_t st, unsigned long long *zero_words) {
     const int64_t threads = n / 8;
-    k_kq_dequant<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(dtype, src, n, add, y);
+    k_kq_dequant<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(dtype, src, n, add, y,
+                                                                    zero_words);
     return hipGetLastError();
 }
 
