@@ -73,7 +73,7 @@ WORKLOADS = {
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
                         pmc="encoder_f16_32x750_pmc.json"),
     "decoder_token_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights, f16 KV",
-                               streams=1, pmc="",
+                               streams=1, pmc="decoder_token_q4km_pmc.json",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs and "
                                     "KV rows, generated on device)"),
     "decoder_weights_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k (int8 dot)", streams=1,

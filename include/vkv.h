@@ -342,7 +342,7 @@ vkv_status vkv_q8_0_unpack(const void *blocks, float *y, int64_t n, void *hip_st
 
 /* ---------------------------------------------------------------------------
  * Decoder projections on ggml Q4_K / Q6_K weights: ggml_mul_mat(W, x) for one
- * token (src/voxtral.cpp:2656-2659 Q/K/V, :2857 O, :2879-2883 SwiGLU FFN),
+ * token (src/voxtral.cpp:2656-2659 Q/K/V, :2857 O, :2878-2882 SwiGLU FFN),
  * with the RMSNorm that precedes them (:2653-2654, :2861-2862) and the ada
  * time conditioning (:2864-2874) fused into the input side.
  *

@@ -3,7 +3,7 @@
  * (TEST INFRASTRUCTURE ONLY).
  *
  * The decoder's projections are ggml_mul_mat(W, x) on GGUF weights
- * (src/voxtral.cpp:2656-2659 Q/K/V, :2857 O, :2879-2883 SwiGLU FFN); in the
+ * (src/voxtral.cpp:2656-2659 Q/K/V, :2857 O, :2878-2882 SwiGLU FFN); in the
  * Q4_K_M files the quantizer writes, attn_v / ffn_w2 / tok_embeddings / output
  * are Q6_K and the other decoder matrices Q4_K (src/voxtral-quantize.cpp:
  * 148-159).  The block formats and the CPU arithmetic belong to ggml, which the

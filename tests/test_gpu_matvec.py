@@ -1,6 +1,6 @@
 """GPU parity of the decoder projections on ggml k-quant weights
 (ggml_mul_mat at src/voxtral.cpp:2656-2659 Q/K/V, :2857 O + residual,
-:2879-2883 SwiGLU FFN, :2955/:2968 logits; RMSNorm :2653-2654, :2861-2862;
+:2878-2882 SwiGLU FFN, :2955/:2968 logits; RMSNorm :2653-2654, :2861-2862;
 ada conditioning :2864-2874; get_rows :3008) against the oracle's restatement
 of ggml's CPU path.
 

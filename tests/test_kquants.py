@@ -1,6 +1,6 @@
 """Decoder weight formats and the CPU matrix-vector product (ggml Q4_K / Q6_K
 weights, Q8_K activations; ggml_mul_mat at src/voxtral.cpp:2656-2659, 2857,
-2879-2883, quantization mix src/voxtral-quantize.cpp:148-159).
+2878-2882, quantization mix src/voxtral-quantize.cpp:148-159).
 
 Checks of the oracle that do not restate it: blocks are packed here from
 chosen scales and codes by an independent writer of the byte layout, and

@@ -1,7 +1,7 @@
 // gfx950 matrix-vector products of the decoder step on ggml k-quant weights.
 //
 // ggml_mul_mat(W, x) with one token (src/voxtral.cpp:2656-2659 Q/K/V, :2857
-// O-projection, :2879-2883 SwiGLU FFN) on Q4_K / Q6_K rows
+// O-projection, :2878-2882 SwiGLU FFN) on Q4_K / Q6_K rows
 // (src/voxtral-quantize.cpp:148-159), computed the way ggml's CPU path does:
 // x is quantized to Q8_K (f32 scale per 256, int8 codes, 16-element sums) and
 // each row is an integer dot product per block, scaled by fp16(d) * d_x (and
