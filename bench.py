@@ -31,6 +31,11 @@ Other workloads (--workload), reported on the same contract:
                residual, RMSNorm*(1+ada)+SwiGLU W1/W3, W2 + residual; then the
                final norm + the 131072-row Q6_K logits -- 105 vkv_matvec
                calls, 2.24 GB of weights per token; tokens/s.
+  encoder_chunk_q4km  the encoder's transformer for one 16-frame chunk through
+               vkv_encoder_chunk: 32 layers x (RMSNorm + Q/K/V with biases,
+               RoPE, ring append + window-750 attention, O + bias + residual,
+               RMSNorm + SwiGLU, W2 + bias + residual) + final norm, on Q4_K_M
+               weights (539 MB per chunk), steady state; frames/s.
   decoder_token_q4km  one whole decoder token through vkv_decoder_token:
                embedding + audio row, 26 x (RMSNorm+QKV, RoPE + K/V append +
                attention over the full 8192-slot F16 ring, O + residual,
@@ -72,6 +77,10 @@ WORKLOADS = {
                         pmc="decode_q8_0_8x26x8192_pmc.json"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
                         pmc="encoder_f16_32x750_pmc.json"),
+    "encoder_chunk_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights (MFMA int8), f16 KV",
+                               streams=1, pmc="encoder_chunk_q4km_pmc.json",
+                               data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) frames and "
+                                    "KV rows, generated on device)"),
     "decoder_token_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights, f16 KV",
                                streams=1, pmc="decoder_token_q4km_pmc.json",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs and "
@@ -160,6 +169,81 @@ def gpu_weights(steps, warmup):
     total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
     assert bool(torch.isfinite(logits).all()) and bool(torch.isfinite(x).all())
     return total_ms, step_ms, wall
+
+
+E_HID = 5120
+ENC_MATS = [("attn_q", 12, E_DIM, 1280), ("attn_k", 12, E_DIM, 1280), ("attn_v", 14, E_DIM, 1280),
+            ("attn_o", 12, 1280, E_DIM), ("ffn_w1", 12, E_HID, 1280), ("ffn_w3", 12, E_HID, 1280),
+            ("ffn_w2", 14, 1280, E_HID)]
+
+
+def encoder_chunk_bytes(n_keys):
+    """weights of 32 layers + the window attention's bytes for one chunk"""
+    w = E_LAYERS * sum(mat_bytes(dt, r, n) for _, dt, r, n in ENC_MATS)
+    return w + encoder_bytes_per_chunk(n_keys)
+
+
+def gpu_encoder_chunk(steps, warmup):
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED)
+    keep = []
+    layers = (vkv.EncLayer * E_LAYERS)()
+
+    def vec(n, lo, hi):
+        t = torch.empty(n, device="cuda").uniform_(lo, hi, generator=gen)
+        keep.append(t)
+        return t.data_ptr()
+
+    for l in range(E_LAYERS):
+        w = {name: random_kq_device(dt, r, n, gen) for name, dt, r, n in ENC_MATS}
+        keep.extend(w.values())
+        layers[l] = vkv.EncLayer(vec(1280, 0.5, 1.5), vec(1280, -0.1, 0.1), w["attn_q"].data_ptr(),
+                                 w["attn_k"].data_ptr(), w["attn_v"].data_ptr(),
+                                 w["attn_o"].data_ptr(), 12, 12, 14, 12, vec(E_DIM, -0.1, 0.1),
+                                 vec(E_DIM, -0.1, 0.1), vec(1280, -0.1, 0.1), vec(1280, 0.5, 1.5),
+                                 vec(1280, -0.1, 0.1), w["ffn_w1"].data_ptr(),
+                                 w["ffn_w2"].data_ptr(), w["ffn_w3"].data_ptr(), 12, 14, 12,
+                                 vec(1280, -0.1, 0.1))
+    model = vkv.EncModel(E_LAYERS, 1280, E_HID, E_HEADS, E_HD, 1e-5, 1.0e6, vec(1280, 0.5, 1.5),
+                         vec(1280, -0.1, 0.1), layers)
+    cache = vkv.Cache(n_streams=1, n_layers=E_LAYERS, capacity=E_CAP, n_kv_heads=E_HEADS,
+                      head_dim=E_HD, n_q_heads=E_HEADS, dtype=vkv.F16)
+    # steady state: the ring holds frames [0, 768) before the first timed chunk
+    first = (E_WIN + E_CHUNK - 1) // E_CHUNK + 1
+    for c in range(first):
+        plan = vkv.enc_plan(c * E_CHUNK, E_CHUNK, E_CAP, E_WIN)
+        k = torch.empty(E_LAYERS, E_CHUNK, E_DIM, device="cuda")
+        v = torch.empty(E_LAYERS, E_CHUNK, E_DIM, device="cuda")
+        vkv.synth_rows(k.data_ptr(), E_DIM, SEED, vkv.TAG_EK, nl=E_LAYERS, p0=c * E_CHUNK,
+                       np_=E_CHUNK, hip_stream=sp)
+        vkv.synth_rows(v.data_ptr(), E_DIM, SEED, vkv.TAG_EV, nl=E_LAYERS, p0=c * E_CHUNK,
+                       np_=E_CHUNK, hip_stream=sp)
+        cache.append(0, 0, E_LAYERS, vkv.plan_segs(plan.write_seg, plan.write_nseg), k.data_ptr(),
+                     v.data_ptr(), hip_stream=sp)
+    T = warmup + steps
+    x0 = torch.randn(T, E_CHUNK, 1280, device="cuda", generator=gen)
+    x = torch.empty(E_CHUNK, 1280, device="cuda")
+    ws_bytes = vkv.encoder_chunk_workspace(model, E_CHUNK)
+    ws = torch.empty(ws_bytes // 4 + 64, device="cuda")
+    ws_ptr = (ws.data_ptr() + 255) & ~255
+    plans = [vkv.enc_plan((first + i) * E_CHUNK, E_CHUNK, E_CAP, E_WIN) for i in range(T)]
+
+    def step(i):
+        x.copy_(x0[i])
+        vkv.encoder_chunk(cache, 0, plans[i], E_WIN, model, x.data_ptr(), ws_ptr, ws_bytes,
+                          hip_stream=sp)
+
+    total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
+    assert bool(torch.isfinite(x).all())
+    n_keys = plans[0].win_end - plans[0].win_start
+    cache.close()
+    del keep
+    return total_ms, step_ms, wall, n_keys
 
 
 def device_model(gen):
@@ -569,6 +653,20 @@ def main():
                   "layers": layers, "window": CAP, "kv_heads": KVH, "q_heads": QH,
                   "head_dim": HD, "streams": 1, "bytes": "mean over the steps"}
         kernel = "k_decode<FmtF16> (append fused)"
+    elif args.workload == "encoder_chunk_q4km":
+        total_ms, step_ms, wall, n_keys = gpu_encoder_chunk(args.steps, args.warmup)
+        bytes_step = encoder_chunk_bytes(n_keys)
+        units_per_step = E_CHUNK
+        res = {"metric": "encoder transformer frames/s (Q4_K_M projections on the matrix cores + "
+                         "window-750 attention, 32 layers, 16-frame chunks) and HBM GB/s",
+               "unit": "frames/s"}
+        config = {"workload": "one 16-frame encoder chunk through vkv_encoder_chunk: 32 x "
+                              "(RMSNorm + Q/K/V + biases, RoPE, ring append + window-750 "
+                              "attention, O + bias + residual, RMSNorm + SwiGLU, W2 + bias + "
+                              "residual) + final norm; dim 1280, 32 heads x 64, hidden 5120",
+                  "layers": E_LAYERS, "window": E_WIN, "frames_per_chunk": E_CHUNK,
+                  "bytes_per_chunk": bytes_step, "keys_per_query_block": n_keys}
+        kernel = "k_q8k_rows + k_gemm_kq + k_rope + k_window_mfma (11 launches per layer)"
     elif args.workload == "decoder_token_q4km":
         total_ms, step_ms, wall = gpu_token(args.steps, args.warmup)
         bytes_step = token_bytes()
@@ -652,7 +750,7 @@ def main():
         res["cpu_baseline"] = cpu_weights_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload == "decoder_token_q4km":
         res["cpu_baseline"] = cpu_token_leg(args.cpu_seconds)
-    elif not args.no_cpu and args.workload != "encoder_f16":
+    elif not args.no_cpu and args.workload not in ("encoder_f16", "encoder_chunk_q4km"):
         res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds)
     print(json.dumps(res), flush=True)
 

@@ -386,6 +386,66 @@ vkv_status vkv_quantize_q8_k(const float *x, int64_t n, const float *norm_w, con
 vkv_status vkv_dequantize(int32_t dtype, const void *blocks, int64_t n, float *y,
                           void *hip_stream);
 
+/* ---------------------------------------------------------------------------
+ * The same products for several input rows at once: the encoder's P new
+ * frames per chunk (build_encoder_kv_graph, src/voxtral.cpp:2147-2370) and the
+ * decoder prefill.  x: [n_cols][n_in] f32 (one input row per frame/token);
+ * every row is formed and quantized to Q8_K as in vkv_matvec, with the
+ * norm's optional bias added after the weight (enc_apply_norm, :1855-1861).
+ * y: [n_cols][n_rows] per matrix, plus bias[r], plus add (same layout) when
+ * given.  SwiGLU pairs the rows of two matrices as vkv_matvec does.  The Q8_K
+ * image of x lives in the caller's workspace (vkv_matmul_workspace bytes,
+ * 256-byte aligned); matrices of one call may mix Q4_K and Q6_K.
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_mm_out {
+    const void *w;        /* [n_rows][n_in/256] Q4_K or Q6_K blocks */
+    int32_t dtype;
+    int32_t n_rows;
+    float *y;             /* [n_cols][n_rows] */
+    const float *add;     /* NULL, or the residual [n_cols][n_rows] (may alias y) */
+    const float *bias;    /* NULL, or [n_rows] added before the residual */
+} vkv_mm_out;
+
+size_t vkv_matmul_workspace(int32_t n_cols, int64_t n_in);
+vkv_status vkv_matmul(const float *x, int32_t n_cols, int64_t n_in, const float *norm_w,
+                      const float *norm_b, const float *ada, float eps, const vkv_mm_out *outs,
+                      int32_t n_outs, int32_t epilogue, void *workspace, size_t workspace_bytes,
+                      void *hip_stream);
+
+/* ---------------------------------------------------------------------------
+ * One encoder chunk through every layer (build_encoder_kv_graph's transformer,
+ * src/voxtral.cpp:2144-2370): for the plan's n_new frames x ([n_new][dim], the
+ * conv stem's output, replaced in place by the output), per layer
+ * h = rms_norm(x) * attn_norm + attn_norm_b; q = Wq h + bq ([n_heads *
+ * head_dim] rows), k = Wk h, v = Wv h + bv (the cache's kv width);
+ * RoPE of q and k at positions q_start..; K/V append to the
+ * ring and causal sliding-window attention (vkv_enc_step); x += Wo a + bo;
+ * h = rms_norm(x) * ffn_norm + ffn_norm_b; x += W2 (silu(W1 h) * (W3 h)) + b2;
+ * finally x = rms_norm(x) * out_norm + out_norm_b.  Bias pointers may be NULL.
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_enc_layer {
+    const float *attn_norm, *attn_norm_b;
+    const void *attn_q, *attn_k, *attn_v, *attn_o;
+    int32_t attn_q_type, attn_k_type, attn_v_type, attn_o_type;
+    const float *attn_q_b, *attn_v_b, *attn_o_b;
+    const float *ffn_norm, *ffn_norm_b;
+    const void *ffn_w1, *ffn_w2, *ffn_w3;
+    int32_t ffn_w1_type, ffn_w2_type, ffn_w3_type;
+    const float *ffn_w2_b;
+} vkv_enc_layer;
+
+typedef struct vkv_enc_model {
+    int32_t n_layers, dim, hidden, n_heads, head_dim;
+    float norm_eps, rope_theta;
+    const float *out_norm, *out_norm_b;
+    const vkv_enc_layer *layers;   /* host array of n_layers */
+} vkv_enc_model;
+
+size_t vkv_encoder_chunk_workspace(const vkv_enc_model *model, int32_t n_new);
+vkv_status vkv_encoder_chunk(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
+                             int32_t window, const vkv_enc_model *model, float *x,
+                             void *workspace, size_t workspace_bytes, void *hip_stream);
+
 /* The decoder step's input row: ggml_get_rows(tok_embeddings, token) +
  * audio embedding (src/voxtral.cpp:3008-3019): row `token` of a Q4_K/Q6_K
  * table [n_rows][n_cols], dequantized, plus add[] when add is not NULL. */

@@ -114,6 +114,7 @@ _protos = {
     "orc_vec_dot_q6_k_q8_k": (_f32, [_i64, _vp, _vp]),
     "orc_rms_norm": (None, [_vp, _vp, _i64, _f32]),
     "orc_norm_act": (None, [_vp, _i64, _vp, _vp, _f32, _vp]),
+    "orc_norm_act_b": (None, [_vp, _i64, _vp, _vp, _vp, _f32, _vp]),
     "orc_silu": (_f32, [_f32]),
     "orc_argmax": (_i32, [_vp, _i64]),
     "orc_wrow_bytes": (_i64, [ctypes.c_int, _i64]),
@@ -373,13 +374,13 @@ def vec_dot(dtype, w_row, xq, n):
     return fn(n, _ptr(w_row), _ptr(xq))
 
 
-def norm_act(x, norm_w=None, ada=None, eps=1e-5):
+def norm_act(x, norm_w=None, ada=None, eps=1e-5, norm_b=None):
+    """rms_norm(x) * norm_w (+ norm_b) (then + h * ada); x itself without norm_w."""
     x = _f32a(x)
     y = np.empty_like(x)
-    nw = _f32a(norm_w) if norm_w is not None else None
-    ad = _f32a(ada) if ada is not None else None
-    lib.orc_norm_act(_ptr(x), x.size, _ptr(nw) if nw is not None else None,
-                     _ptr(ad) if ad is not None else None, eps, _ptr(y))
+    arrs = [_f32a(a) if a is not None else None for a in (norm_w, norm_b, ada)]
+    ptrs = [_ptr(a) if a is not None else None for a in arrs]
+    lib.orc_norm_act_b(_ptr(x), x.size, ptrs[0], ptrs[1], ptrs[2], eps, _ptr(y))
     return y
 
 

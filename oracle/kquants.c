@@ -221,19 +221,26 @@ void orc_rms_norm(const float *x, float *y, int64_t n, float eps) {
     for (int64_t i = 0; i < n; ++i) y[i] = x[i] * scale;
 }
 
-void orc_norm_act(const float *x, int64_t n, const float *norm_w, const float *ada, float eps,
-                  float *y) {
+void orc_norm_act_b(const float *x, int64_t n, const float *norm_w, const float *norm_b,
+                    const float *ada, float eps, float *y) {
     if (!norm_w) {
         memcpy(y, x, (size_t)n * sizeof(float));
         return;
     }
     orc_rms_norm(x, y, n, eps);
     for (int64_t i = 0; i < n; ++i) y[i] = y[i] * norm_w[i];
+    if (norm_b) /* enc_apply_norm's bias (src/voxtral.cpp:1855-1861) */
+        for (int64_t i = 0; i < n; ++i) y[i] = y[i] + norm_b[i];
     if (ada)
         for (int64_t i = 0; i < n; ++i) {
             const float t = y[i] * ada[i];
             y[i] = y[i] + t;
         }
+}
+
+void orc_norm_act(const float *x, int64_t n, const float *norm_w, const float *ada, float eps,
+                  float *y) {
+    orc_norm_act_b(x, n, norm_w, NULL, ada, eps, y);
 }
 
 float orc_silu(float x) { return x / (1.0f + expf(-x)); }

@@ -208,6 +208,9 @@ void orc_rms_norm(const float *x, float *y, int64_t n, float eps);
  * norm_w is NULL */
 void orc_norm_act(const float *x, int64_t n, const float *norm_w, const float *ada, float eps,
                   float *y);
+/* rms_norm(x) * norm_w + norm_b (enc_apply_norm), then + h * ada */
+void orc_norm_act_b(const float *x, int64_t n, const float *norm_w, const float *norm_b,
+                    const float *ada, float eps, float *y);
 float orc_silu(float x);
 int32_t orc_argmax(const float *x, int64_t n);
 int64_t orc_wrow_bytes(int dtype, int64_t n_in);

@@ -47,6 +47,9 @@ def test_struct_layout_matches_c():
         "vkv_cache_params": (vkv.CacheParams, None),
         "vkv_cache_layout": (vkv.CacheLayout, None),
         "vkv_mv_out": (vkv.MvOut, None),
+        "vkv_mm_out": (vkv.MmOut, None),
+        "vkv_enc_layer": (vkv.EncLayer, None),
+        "vkv_enc_model": (vkv.EncModel, None),
         "vkv_dec_layer": (vkv.DecLayer, None),
         "vkv_dec_model": (vkv.DecModel, None),
     }
@@ -144,11 +147,24 @@ def test_error_statuses_without_device():
     assert L.vkv_matvec(x, 3072, None, None, 1e-5, huge, 1, 0, None) == vkv.INVALID_ARGUMENT
     assert "4 GiB" in vkv.last_error()
     assert L.vkv_quantize_q8_k(x, 3072, None, None, 1e-5, 4098, None) == vkv.INVALID_ARGUMENT
+    mo = (vkv.MmOut * 1)(vkv.MmOut(16, vkv.Q4_K, 8, 16, None, None))
+    assert L.vkv_matmul_workspace(16, 1280) > 16 * 1280
+    assert L.vkv_matmul_workspace(0, 1280) == 0
+    assert L.vkv_matmul(x, 16, 1280, None, None, None, 1e-5, mo, 1, 0, None, 0,
+                        None) == vkv.INVALID_ARGUMENT                 # no workspace
+    assert L.vkv_matmul(x, 16, 1280, None, 4096, None, 1e-5, mo, 1, 0, 4096, 1 << 20,
+                        None) == vkv.INVALID_ARGUMENT                 # norm_b without norm_w
+    assert L.vkv_matmul(x, 16, 1280, None, None, None, 1e-5, mo, 1, 0, 4096, 16,
+                        None) == vkv.BUFFER_TOO_SMALL
     assert L.vkv_dequantize(vkv.Q8_0, 16, 256, 16, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_embed(vkv.Q6_K, 16, 10, 3072, 10, None, 16, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_embed(vkv.Q6_K, 16, 10, 3072, -1, None, 16, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_argmax(x, 0, 16, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_argmax(ctypes.c_void_p(4100), 10, 16, None) == vkv.INVALID_ARGUMENT
+    em = vkv.EncModel()
+    assert L.vkv_encoder_chunk_workspace(ctypes.byref(em), 16) == 0
+    assert L.vkv_encoder_chunk(None, 0, None, 750, ctypes.byref(em), None, None, 0,
+                               None) == vkv.INVALID_ARGUMENT
     m = vkv.DecModel()
     assert L.vkv_decoder_token_workspace(ctypes.byref(m)) == 0
     assert L.vkv_decoder_token(None, 0, None, ctypes.byref(m), 0, None, None, None, None, 0,

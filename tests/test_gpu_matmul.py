@@ -1,0 +1,147 @@
+"""GPU parity of the multi-row products (the encoder's P frames per chunk,
+build_encoder_kv_graph src/voxtral.cpp:2147-2370: Q/K/V with biases :2150-2152,
+O + bias + residual :2358-2359, SwiGLU :2362-2366 with the optional W2 bias;
+enc_apply_norm with its bias :1855-1861; the decoder prefill's projections)
+against the oracle's restatement of ggml's CPU path, one input row at a time.
+
+The Q8_K image of every input row is bit-exact; every output within
+1e-5 x sum_e |w_e| |x_e| of the oracle (f32 combination of exact integer
+block sums in another order), plus the f32 rounding of bias / residual adds."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import vkv
+from gpu_util import dev, stream_ptr
+from kq_util import random_matrix
+
+pytestmark = pytest.mark.gpu
+
+EPS = 1e-5
+REL = 1e-5
+
+
+def to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev())
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def workspace(n_cols, n_in):
+    b = vkv.matmul_workspace(n_cols, n_in)
+    assert b > 0
+    t = torch.empty(b // 4 + 64, dtype=torch.float32, device=dev())
+    return t, (t.data_ptr() + 255) & ~255, b
+
+
+def rows_ref(dtype, w, n_rows, n_in, hs):
+    """oracle outputs [n_cols][n_rows] and magnitudes sum |w||x| (x = Q8_K image)"""
+    out = np.stack([oracle.matvec(dtype, w, n_rows, n_in, h, n_threads=8) for h in hs])
+    wd = np.abs(oracle.dequantize(dtype, w, n_rows * n_in).reshape(n_rows, n_in))
+    ax = np.stack([np.abs(oracle.dequantize(oracle.Q8_K, oracle.q8_k_quantize(h), n_in)) for h in hs])
+    return out, ax @ wd.T
+
+
+def check(got, want, mag, extra=0.0):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    tol = REL * mag + extra + 1e-30
+    assert np.all(err <= tol), f"{int((err > tol).sum())} outputs off, worst {float((err / tol).max()):.2f}x tol"
+
+
+@pytest.mark.parametrize("P", [1, 4, 16, 17, 38, 128])
+def test_encoder_qkv_with_norm_bias_and_biases(P):
+    rng = np.random.default_rng(2150 + P)
+    n_in = 1280
+    mats = [(vkv.Q4_K, 1280, True), (vkv.Q4_K, 1280, False), (vkv.Q6_K, 1280, True)]
+    ws = [random_matrix(rng, dt, n, n_in, 0.05) for dt, n, _ in mats]
+    bs = [rng.standard_normal(n).astype(np.float32) if hb else None for _, n, hb in mats]
+    x = rng.standard_normal((P, n_in)).astype(np.float32) * 3
+    nw = rng.uniform(0.5, 1.5, n_in).astype(np.float32)
+    nb = rng.uniform(-0.3, 0.3, n_in).astype(np.float32)
+    xd, nwd, nbd = to_dev(x), to_dev(nw), to_dev(nb)
+    wds = [to_dev(w) for w in ws]
+    bds = [to_dev(b) if b is not None else None for b in bs]
+    ys = [torch.full((P, n), np.nan, device=dev()) for _, n, _ in mats]
+    t, ws_ptr, ws_b = workspace(P, n_in)
+    vkv.matmul(xd.data_ptr(), P, n_in,
+               [(wd.data_ptr(), dt, n, y.data_ptr(), None, bd.data_ptr() if bd is not None else None)
+                for wd, (dt, n, _), y, bd in zip(wds, mats, ys, bds)],
+               ws_ptr, ws_b, norm_w_ptr=nwd.data_ptr(), norm_b_ptr=nbd.data_ptr(), eps=EPS,
+               hip_stream=stream_ptr())
+    hs = [oracle.norm_act(x[p], nw, eps=EPS, norm_b=nb) for p in range(P)]
+    # the Q8_K image (codes at the workspace start, [P][n_in]) is the oracle's, bit for bit
+    codes = host(t).view(np.uint8)[ws_ptr - t.data_ptr():][:P * n_in].reshape(P, n_in)
+    for p in range(P):
+        want = oracle.q8_k_quantize(hs[p]).reshape(-1, 292)[:, 4:260].ravel()
+        assert np.array_equal(codes[p], want)
+    for w, (dt, n, _), y, b in zip(ws, mats, ys, bs):
+        want, mag = rows_ref(dt, w, n, n_in, hs)
+        if b is not None:
+            want = want + b[None, :]
+        check(host(y), want, mag, extra=6e-8 * np.abs(want))
+
+
+@pytest.mark.parametrize("dtype,n_rows,n_in,P", [(vkv.Q4_K, 1280, 1280, 16),   # encoder O
+                                                  (vkv.Q6_K, 1280, 5120, 16),   # encoder W2
+                                                  (vkv.Q6_K, 1280, 5120, 5),
+                                                  (vkv.Q4_K, 3072, 4096, 38)])  # decoder prefill O
+def test_bias_and_residual_in_place(dtype, n_rows, n_in, P):
+    rng = np.random.default_rng(n_rows + n_in + P)
+    w = random_matrix(rng, dtype, n_rows, n_in, 0.05)
+    b = rng.standard_normal(n_rows).astype(np.float32)
+    x = rng.standard_normal((P, n_in)).astype(np.float32)
+    res = rng.standard_normal((P, n_rows)).astype(np.float32)
+    xd, wd, bd, r = to_dev(x), to_dev(w), to_dev(b), to_dev(res)
+    t, ws_ptr, ws_b = workspace(P, n_in)
+    vkv.matmul(xd.data_ptr(), P, n_in, [(wd.data_ptr(), dtype, n_rows, r.data_ptr(), r.data_ptr(),
+                                          bd.data_ptr())], ws_ptr, ws_b, hip_stream=stream_ptr())
+    proj, mag = rows_ref(dtype, w, n_rows, n_in, list(x))
+    want = res + (proj + b[None, :])
+    check(host(r), want, mag, extra=1.2e-7 * (np.abs(res) + np.abs(proj) + np.abs(b)[None, :]))
+
+
+@pytest.mark.parametrize("P", [3, 16])
+def test_encoder_swiglu(P):
+    rng = np.random.default_rng(2362 + P)
+    n_in, hid = 1280, 5120
+    w1 = random_matrix(rng, vkv.Q4_K, hid, n_in, 0.02)
+    w3 = random_matrix(rng, vkv.Q4_K, hid, n_in, 0.02)
+    x = rng.standard_normal((P, n_in)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, n_in).astype(np.float32)
+    xd, nwd, w1d, w3d = to_dev(x), to_dev(nw), to_dev(w1), to_dev(w3)
+    y = torch.full((P, hid), np.nan, device=dev())
+    t, ws_ptr, ws_b = workspace(P, n_in)
+    vkv.matmul(xd.data_ptr(), P, n_in, [(w1d.data_ptr(), vkv.Q4_K, hid, y.data_ptr()),
+                                        (w3d.data_ptr(), vkv.Q4_K, hid, None)],
+               ws_ptr, ws_b, norm_w_ptr=nwd.data_ptr(), eps=EPS, epilogue=vkv.MV_SWIGLU,
+               hip_stream=stream_ptr())
+    hs = [oracle.norm_act(x[p], nw, eps=EPS) for p in range(P)]
+    g, m1 = rows_ref(vkv.Q4_K, w1, hid, n_in, hs)
+    u, m3 = rows_ref(vkv.Q4_K, w3, hid, n_in, hs)
+    g, u = g.astype(np.float64), u.astype(np.float64)
+    sg = g / (1 + np.exp(-g))
+    want = sg * u
+    bound = REL * (1.1 * m1 * np.abs(u) + np.abs(sg) * m3) + 1e-6 * np.abs(want)
+    assert np.all(np.abs(host(y) - want) <= bound + 1e-30)
+
+
+def test_matches_the_single_row_kernel():
+    """n_cols = 1 agrees with vkv_matvec within the same bound"""
+    rng = np.random.default_rng(1)
+    n_rows, n_in = 4096, 3072
+    w = random_matrix(rng, vkv.Q4_K, n_rows, n_in)
+    x = rng.standard_normal(n_in).astype(np.float32)
+    xd, wd = to_dev(x), to_dev(w)
+    y1 = torch.empty(n_rows, device=dev())
+    y2 = torch.empty(n_rows, device=dev())
+    vkv.matvec(xd.data_ptr(), n_in, [(wd.data_ptr(), vkv.Q4_K, n_rows, y1.data_ptr())],
+               hip_stream=stream_ptr())
+    t, ws_ptr, ws_b = workspace(1, n_in)
+    vkv.matmul(xd.data_ptr(), 1, n_in, [(wd.data_ptr(), vkv.Q4_K, n_rows, y2.data_ptr())],
+               ws_ptr, ws_b, hip_stream=stream_ptr())
+    _, mag = rows_ref(vkv.Q4_K, w, n_rows, n_in, [x])
+    check(host(y2), host(y1), 2 * mag[0])

@@ -236,3 +236,12 @@ def test_argmax_last_index_of_the_maximum():
         v = rng.integers(-50, 50, 4096).astype(np.float32)   # many ties
         want = v.size - 1 - int(np.argmax(v[::-1]))
         assert oracle.argmax(v) == want
+
+
+def test_norm_bias_closed_form():
+    rng = np.random.default_rng(1855)
+    x = rng.standard_normal(1280).astype(np.float32)
+    w = rng.uniform(0.5, 1.5, 1280).astype(np.float32)
+    b = rng.uniform(-0.2, 0.2, 1280).astype(np.float32)
+    y = oracle.norm_act(x, w, eps=1e-5, norm_b=b)
+    np.testing.assert_array_equal(y, oracle.norm_act(x, w, eps=1e-5) + b)   # f32 add after the weight

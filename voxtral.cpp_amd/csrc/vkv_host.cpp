@@ -1090,6 +1090,92 @@ vkv_status vkv_matvec(const float *x, int64_t n_in, const float *norm_w, const f
                        nullptr);
 }
 
+namespace {
+struct MmImage {
+    int8_t *codes;
+    float *xd;
+    int32_t *bs32;
+    size_t bytes;
+};
+MmImage mm_image(int32_t n_cols, int64_t n_in, uint8_t *base) {
+    MmImage im{};
+    size_t off = 0;
+    auto take = [&](size_t b) {
+        uint8_t *p = base ? base + off : nullptr;
+        off += (b + 255) & ~(size_t)255;
+        return p;
+    };
+    im.codes = (int8_t *)take((size_t)n_cols * n_in);
+    im.xd = (float *)take((size_t)n_cols * (n_in / 256) * 4);
+    im.bs32 = (int32_t *)take((size_t)n_cols * (n_in / 32) * 4);
+    im.bytes = off;
+    return im;
+}
+}  // namespace
+
+size_t vkv_matmul_workspace(int32_t n_cols, int64_t n_in) {
+    if (n_cols < 1 || n_in < 256 || n_in % 256 || n_in > VKV_MV_MAX_IN) return 0;
+    return mm_image(n_cols, n_in, nullptr).bytes;
+}
+
+vkv_status vkv_matmul(const float *x, int32_t n_cols, int64_t n_in, const float *norm_w,
+                      const float *norm_b, const float *ada, float eps, const vkv_mm_out *outs,
+                      int32_t n_outs, int32_t epilogue, void *workspace, size_t workspace_bytes,
+                      void *hip_stream) {
+    if (vkv_status st = check_mv_input("matmul", x, n_in, norm_w, ada)) return st;
+    if (norm_b && !norm_w) return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: norm_b requires norm_w");
+    if (vkv_status st = check_aligned("matmul", {norm_b})) return st;
+    if (n_cols < 1 || n_cols > 65535 * 16)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: n_cols=%d", n_cols);
+    if (!outs || n_outs < 1 || n_outs > VKV_MV_MAX_OUTS)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: n_outs=%d outside [1, %d]", n_outs,
+                    VKV_MV_MAX_OUTS);
+    if (epilogue != VKV_MV_STORE && epilogue != VKV_MV_SWIGLU)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: unknown epilogue %d", epilogue);
+    const bool swiglu = epilogue == VKV_MV_SWIGLU;
+    if (swiglu && (n_outs != 2 || outs[0].n_rows != outs[1].n_rows || outs[0].dtype != outs[1].dtype))
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "matmul: SwiGLU takes two matrices of equal rows and dtype");
+    int64_t tiles = 0;
+    MmArgs a{};
+    for (int32_t k = 0; k < n_outs; ++k) {
+        const vkv_mm_out &o = outs[k];
+        const int64_t bb = kq_block_bytes(o.dtype);
+        if (!bb) return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: weight dtype %d", o.dtype);
+        if (!o.w || (!o.y && !(swiglu && k == 1)) || o.n_rows < 1)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: matrix %d: null pointer or no rows", k);
+        if ((int64_t)o.n_rows * (n_in / 256) * bb > (int64_t)0xFFFFFE00)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: matrix %d exceeds 4 GiB", k);
+        if (reinterpret_cast<uintptr_t>(o.w) & 3u)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: weights must be 4-byte aligned");
+        if (swiglu && o.add) return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: SwiGLU has no residual add");
+        a.out[k] = MmOut{(const uint8_t *)o.w, o.y, o.add, o.bias, o.dtype, o.n_rows, (int32_t)tiles};
+        if (!swiglu || k == 0) tiles += (o.n_rows + 15) / 16;
+    }
+    if (swiglu) a.out[1].tile0 = 0x7fffffff;
+    for (int32_t k = n_outs; k < VKV_MV_MAX_OUTS; ++k) a.out[k].tile0 = 0x7fffffff;
+    if (tiles > 0x7fffffff) return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: grid too large");
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: workspace null or not 256-byte aligned");
+    const MmImage im = mm_image(n_cols, n_in, (uint8_t *)workspace);
+    if (workspace_bytes < im.bytes)
+        return fail(VKV_STATUS_BUFFER_TOO_SMALL, "matmul: workspace %zu < %zu bytes", workspace_bytes,
+                    im.bytes);
+    hipError_t e = launch_q8k_rows(x, n_in, n_cols, (int)n_in, norm_w, norm_b, ada, eps, im.codes,
+                                   im.xd, im.bs32, as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "matmul input launch");
+    a.xq = im.codes;
+    a.xd = im.xd;
+    a.xbs = im.bs32;
+    a.n_in = (int32_t)n_in;
+    a.n_cols = n_cols;
+    a.n_outs = n_outs;
+    a.swiglu = swiglu ? 1 : 0;
+    e = launch_gemm_kq(a, (int)tiles, (n_cols + 15) / 16, as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "matmul launch");
+    return ok();
+}
+
 vkv_status vkv_quantize_q8_k(const float *x, int64_t n, const float *norm_w, const float *ada,
                              float eps, void *blocks, void *hip_stream) {
     if (vkv_status st = check_mv_input("q8_K quantize", x, n, norm_w, ada)) return st;
@@ -1265,6 +1351,131 @@ vkv_status vkv_decoder_token(vkv_cache *cache, int32_t stream, vkv_ring *ring,
         return s;
     vkv_decoder_commit(ring, &plan);
     if (plan_out) *plan_out = plan;
+    return ok();
+}
+
+// ---- one encoder chunk ----
+
+namespace {
+
+struct EncBuffers {
+    float *qk, *v, *attn, *ffn;   // qk: q rows [n_new][qd] then k rows [n_new][kvd]
+    uint8_t *image;               // vkv_matmul workspace
+    size_t image_bytes, bytes;
+};
+
+EncBuffers enc_buffers(const vkv_enc_model &m, int32_t kvd, int32_t n_new, uint8_t *base) {
+    EncBuffers t{};
+    size_t off = 0;
+    auto take = [&](size_t b) {
+        uint8_t *p = base ? base + off : nullptr;
+        off += (b + 255) & ~(size_t)255;
+        return p;
+    };
+    const size_t rows = (size_t)n_new, qd = (size_t)m.n_heads * m.head_dim;
+    t.qk = (float *)take(rows * (qd + (size_t)kvd) * 4);
+    t.v = (float *)take(rows * (size_t)kvd * 4);
+    t.attn = (float *)take(rows * qd * 4);
+    t.ffn = (float *)take(rows * m.hidden * 4);
+    t.image_bytes = std::max({vkv_matmul_workspace(n_new, m.dim), vkv_matmul_workspace(n_new, (int64_t)qd),
+                              vkv_matmul_workspace(n_new, m.hidden)});
+    t.image = take(t.image_bytes);
+    t.bytes = off;
+    return t;
+}
+
+vkv_status check_enc_model(const vkv_enc_model *m) {
+    if (!m || !m->layers || m->n_layers < 1)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder chunk: null model or no layers");
+    const int64_t qd = (int64_t)m->n_heads * m->head_dim;
+    if (m->dim < 256 || m->dim % 256 || m->hidden < 256 || m->hidden % 256 ||
+        m->hidden > VKV_MV_MAX_IN || m->dim > VKV_MV_MAX_IN || m->n_heads < 1 ||
+        m->head_dim < 8 || qd % 256 || qd > VKV_MV_MAX_IN)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder chunk: model dimensions");
+    if (!m->out_norm) return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder chunk: null output norm");
+    for (int32_t l = 0; l < m->n_layers; ++l) {
+        const vkv_enc_layer &L = m->layers[l];
+        if (!L.attn_norm || !L.ffn_norm || !L.attn_q || !L.attn_k || !L.attn_v || !L.attn_o ||
+            !L.ffn_w1 || !L.ffn_w2 || !L.ffn_w3)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder chunk: layer %d has a null tensor", l);
+    }
+    return VKV_STATUS_OK;
+}
+
+}  // namespace
+
+size_t vkv_encoder_chunk_workspace(const vkv_enc_model *model, int32_t n_new) {
+    if (check_enc_model(model) || n_new < 1) return 0;
+    // the K/V width is the cache's; an MHA encoder's equals the query width
+    return enc_buffers(*model, model->n_heads * model->head_dim, n_new, nullptr).bytes;
+}
+
+vkv_status vkv_encoder_chunk(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
+                             int32_t window, const vkv_enc_model *model, float *x,
+                             void *workspace, size_t workspace_bytes, void *hip_stream) {
+    if (vkv_status st = check_enc_model(model)) return st;
+    const vkv_enc_model &m = *model;
+    if (vkv_status st = check_cache(cache, "encoder chunk")) return st;
+    if (!plan || !x || !workspace)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder chunk: null argument");
+    const int32_t qd = m.n_heads * m.head_dim, kvd = cache->p.n_kv_heads * cache->p.head_dim;
+    if (m.n_layers != cache->p.n_layers || m.head_dim != cache->p.head_dim ||
+        m.n_heads > cache->p.n_q_heads || kvd % 256 || kvd > qd)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder chunk: model and cache shapes differ");
+    const int32_t N = plan->n_new;
+    if (N < 1) return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder chunk: empty plan");
+    if (plan->q_start + N > (1 << 24))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder chunk: rope position beyond 2^24");
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder chunk: workspace not 256-byte aligned");
+    if (vkv_status st = check_aligned("encoder chunk", {x})) return st;
+    const EncBuffers t = enc_buffers(m, kvd, N, (uint8_t *)workspace);
+    if (workspace_bytes < t.bytes)
+        return fail(VKV_STATUS_BUFFER_TOO_SMALL, "encoder chunk: workspace %zu < %zu bytes",
+                    workspace_bytes, t.bytes);
+    const float scale = 1.0f / std::sqrt((float)m.head_dim);
+    float *q = t.qk, *k = t.qk + (size_t)N * qd;
+    for (int32_t l = 0; l < m.n_layers; ++l) {
+        const vkv_enc_layer &L = m.layers[l];
+        const vkv_mm_out qkv[3] = {{L.attn_q, L.attn_q_type, qd, q, nullptr, L.attn_q_b},
+                                   {L.attn_k, L.attn_k_type, kvd, k, nullptr, nullptr},
+                                   {L.attn_v, L.attn_v_type, kvd, t.v, nullptr, L.attn_v_b}};
+        if (vkv_status s = vkv_matmul(x, N, m.dim, L.attn_norm, L.attn_norm_b, nullptr, m.norm_eps,
+                                      qkv, 3, VKV_MV_STORE, t.image, t.image_bytes, hip_stream))
+            return s;
+        // RoPE of the q and k rows at positions q_start + r (one launch when the
+        // widths agree, as in the MHA encoder)
+        if (qd == kvd) {
+            if (vkv_status s = vkv_rope(t.qk, 2, N, qd, m.head_dim, plan->q_start, m.rope_theta,
+                                        hip_stream))
+                return s;
+        } else {
+            if (vkv_status s = vkv_rope(q, 1, N, qd, m.head_dim, plan->q_start, m.rope_theta, hip_stream))
+                return s;
+            if (vkv_status s = vkv_rope(k, 1, N, kvd, m.head_dim, plan->q_start, m.rope_theta, hip_stream))
+                return s;
+        }
+        if (vkv_status s = vkv_enc_step(cache, stream, plan, window, l, 1, q, k, t.v, t.attn,
+                                        m.n_heads, scale, hip_stream))
+            return s;
+        const vkv_mm_out o[1] = {{L.attn_o, L.attn_o_type, m.dim, x, x, L.attn_o_b}};
+        if (vkv_status s = vkv_matmul(t.attn, N, qd, nullptr, nullptr, nullptr, m.norm_eps, o, 1,
+                                      VKV_MV_STORE, t.image, t.image_bytes, hip_stream))
+            return s;
+        const vkv_mm_out gu[2] = {{L.ffn_w1, L.ffn_w1_type, m.hidden, t.ffn, nullptr, nullptr},
+                                  {L.ffn_w3, L.ffn_w3_type, m.hidden, nullptr, nullptr, nullptr}};
+        if (vkv_status s = vkv_matmul(x, N, m.dim, L.ffn_norm, L.ffn_norm_b, nullptr, m.norm_eps, gu,
+                                      2, VKV_MV_SWIGLU, t.image, t.image_bytes, hip_stream))
+            return s;
+        const vkv_mm_out down[1] = {{L.ffn_w2, L.ffn_w2_type, m.dim, x, x, L.ffn_w2_b}};
+        if (vkv_status s = vkv_matmul(t.ffn, N, m.hidden, nullptr, nullptr, nullptr, m.norm_eps,
+                                      down, 1, VKV_MV_STORE, t.image, t.image_bytes, hip_stream))
+            return s;
+    }
+    if (vkv_status st = check_aligned("encoder chunk", {m.out_norm, m.out_norm_b})) return st;
+    hipError_t e = launch_rms_norm_rows(x, N, m.dim, m.out_norm, m.out_norm_b, m.norm_eps, x,
+                                        as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "encoder chunk: final norm launch");
     return ok();
 }
 

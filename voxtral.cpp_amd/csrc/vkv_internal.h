@@ -130,11 +130,36 @@ struct MvArgs {
 };
 
 hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st);
+
+// Several input rows (vkv_matvec.hip, k_gemm_kq): Y[p][r] for 16 x 16 tiles.
+struct MmOut {
+    const uint8_t *w;      // [n_rows][n_in / 256 blocks]
+    float *y;              // [n_cols][n_rows]
+    const float *add;      // nullable: y = add + (W h + bias), same layout as y
+    const float *bias;     // nullable: [n_rows]
+    int32_t dtype, n_rows;
+    int32_t tile0;         // first 16-row tile of this matrix
+};
+
+struct MmArgs {
+    const int8_t *xq;      // Q8_K image: codes [n_cols][n_in]
+    const float *xd;       // block scales [n_cols][n_in / 256]
+    const int32_t *xbs;    // 32-element sums [n_cols][n_in / 32]
+    int32_t n_in, n_cols, n_outs, swiglu;
+    MmOut out[kMvMaxOuts];
+};
+
+hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int n_rows, int n, const float *norm_w,
+                           const float *norm_b, const float *ada, float eps, int8_t *codes,
+                           float *xd, int32_t *bs32, hipStream_t st);
+hipError_t launch_gemm_kq(const MmArgs &a, int n_tiles, int n_col_tiles, hipStream_t st);
 hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const float *ada, float eps,
                             uint8_t *out, hipStream_t st);
 hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const float *add, float *y,
                              hipStream_t st, unsigned long long *zero_words = nullptr);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, hipStream_t st);
+hipError_t launch_rms_norm_rows(const float *x, int n_rows, int n, const float *w, const float *b,
+                                float eps, float *y, hipStream_t st);
 
 hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st);
 hipError_t launch_gather(const uint8_t *src, int64_t row_bytes, SegPair seg, uint8_t *dst,

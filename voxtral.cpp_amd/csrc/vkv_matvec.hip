@@ -34,6 +34,7 @@ namespace {
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
 
 constexpr int kQ4Bytes = 144;
 constexpr int kQ6Bytes = 210;
@@ -154,7 +155,8 @@ template <int NBW, bool NE>
 __device__ __forceinline__ void act_finish(const ActRegs<NBW, NE> &r, int n,
                                            const float *__restrict__ nw,
                                            const float *__restrict__ ada, float eps, ActSmem &sm,
-                                           uint8_t *__restrict__ gout) {
+                                           uint8_t *__restrict__ gout,
+                                           const float *__restrict__ nbias = nullptr) {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nb = n >> 8;
     float scale = 1.0f;
@@ -189,6 +191,14 @@ __device__ __forceinline__ void act_finish(const ActRegs<NBW, NE> &r, int n,
             for (int k = 0; k < 4; ++k) {
                 e[k] = e[k] * scale;
                 e[k] = e[k] * w[k];
+            }
+            if (nbias) {
+                // + the norm's bias (the encoder's norms, src/voxtral.cpp:1855-1861)
+                const float4 b4 = *reinterpret_cast<const float4 *>(nbias + e0);
+                e[0] = e[0] + b4.x;
+                e[1] = e[1] + b4.y;
+                e[2] = e[2] + b4.z;
+                e[3] = e[3] + b4.w;
             }
             if (ada) {
                 const float4 a4 = NE ? r.a[i] : *reinterpret_cast<const float4 *>(ada + e0);
@@ -608,6 +618,34 @@ __global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__
     for (int i = 0; i < 8; ++i) y[i8 + i] = add ? out[i] + add[i8 + i] : out[i];
 }
 
+// rms_norm(x_p) * w (+ b) per row, f32 out (the encoder's final norm,
+// enc_apply_norm at src/voxtral.cpp:2368): the CPU path's rounding -- squares
+// summed in double, mean rounded to f32, scale = 1/sqrtf(mean + eps),
+// (x * scale) * w, then + b.  One work group per row.
+__global__ void __launch_bounds__(256) k_rms_norm_rows(const float *__restrict__ x, int n,
+                                                       const float *__restrict__ w,
+                                                       const float *__restrict__ b, float eps,
+                                                       float *__restrict__ y) {
+#pragma clang fp contract(off)
+    __shared__ double red[4];
+    const float *xr = x + (int64_t)blockIdx.x * n;
+    float *yr = y + (int64_t)blockIdx.x * n;
+    double s = 0.0;
+    for (int i = threadIdx.x; i < n; i += 256) s += (double)(xr[i] * xr[i]);
+    s = wave_sum_d(s);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = s;
+    __syncthreads();
+    const double tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float mean = (float)(tot / (double)n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int i = threadIdx.x; i < n; i += 256) {
+        float v = xr[i] * scale;
+        v = v * w[i];
+        if (b) v = v + b[i];
+        yr[i] = v;
+    }
+}
+
 // ggml_argmax of f32 (ggml_vec_argmax_f32: the running max MAX(max, x[i]) and
 // idx = i whenever x[i] equals it), i.e. for finite input the last index of
 // the maximum.  One work group; (value, index) pairs reduce by larger value,
@@ -650,6 +688,310 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, in
     }
 }
 
+// ---------------------------------------------------------------------------
+// Products with several input rows (the encoder's P frames per chunk,
+// src/voxtral.cpp:2147-2370; the decoder prefill): Y[p][r] = sum_k W[r][k] h_p[k]
+// in the CPU path's arithmetic (each h_p quantized to Q8_K, integer block
+// sums), on the matrix cores.
+//
+//   k_q8k_rows -- the Q8_K image of every input row (one work group per row,
+//                 same input side as k_matvec), to global memory: codes
+//                 [p][K], block scales [p][K/256], 32-element sums [p][K/32].
+//   k_gemm_kq  -- a work group owns 16 weight rows x 16 input rows; its eight
+//                 waves split the 256-blocks of K (each with the next block's
+//                 loads in flight) and meet in LDS.  One
+//                 v_mfma_i32_16x16x32_i8 per 32 weights: A = 16 rows' codes
+//                 (lane (kg, r): row r, k = 8kg..8kg+7), B = 16 input rows'
+//                 Q8_K codes, C = exact int32 sums, row m = 4kg + i of lane
+//                 (kg, n) for input n.  Q4_K: one MFMA per sub-block, then its
+//                 6-bit scale and min; Q6_K: codes recentred to int8 (q - 32),
+//                 one MFMA per 16-element scale group (the other half of the
+//                 k window zeroed).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, int64_t x_stride,
+                                                  int n, const float *nw, const float *nbias,
+                                                  const float *ada, float eps,
+                                                  int8_t *__restrict__ codes, float *__restrict__ xd,
+                                                  int32_t *__restrict__ bs32) {
+    __shared__ ActSmem sm;
+    const int p = blockIdx.x;
+    ActRegs<kMvMaxIn / 1024, false> r;
+    act_load(r, x + (int64_t)p * x_stride, n, nw, ada);
+    act_finish(r, n, nw, ada, eps, sm, nullptr, nbias);
+    int4 *dst = reinterpret_cast<int4 *>(codes + (int64_t)p * n);
+    for (int i = threadIdx.x; i < n / 16; i += 256) dst[i] = reinterpret_cast<const int4 *>(sm.xq)[i];
+    for (int i = threadIdx.x; i < n / 256; i += 256) xd[(int64_t)p * (n / 256) + i] = sm.dx[i];
+    for (int i = threadIdx.x; i < n / 32; i += 256) bs32[(int64_t)p * (n / 32) + i] = sm.bs32[i];
+}
+
+// 8 bytes at an even byte offset of a buffer (Q6_K blocks are 2-byte
+// aligned): one 8-byte load when the offset is 4-aligned, else 12 bytes from
+// 2 below, realigned -- never past off + 10
+__device__ __forceinline__ uint64_t ld8_even(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    if ((off & 3u) == 0) {
+        const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+        return ((uint64_t)v.y << 32) | v.x;
+    }
+    const u32x3_t w = __builtin_amdgcn_raw_buffer_load_b96(rs, off - 2u, 0, 0);
+    const uint32_t lo = __builtin_amdgcn_alignbyte(w.y, w.x, 2u);
+    const uint32_t hi = __builtin_amdgcn_alignbyte(w.z, w.y, 2u);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// 6-bit codes c (one per byte) -> c - 32 as int8: t = c ^ 0x20 is c - 32 when
+// c >= 32 and c + 32 (bit 5 set) when c < 32; the latter needs bits 6 and 7
+// set as well (x6 moves 0x20 to 0xC0 inside each byte)
+__device__ __forceinline__ uint32_t recentre6(uint32_t c) {
+    const uint32_t t = c ^ 0x20202020u;
+    return t | ((t & 0x20202020u) * 6u);
+}
+
+__device__ __forceinline__ i32x4_t mfma_i8(uint64_t a, uint64_t b, i32x4_t c) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8((int64_t)a, (int64_t)b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ MmOut mm_out_at(const MmArgs &a, int k) {
+    MmOut o = a.out[0];
+    if (k == 1) o = a.out[1];
+    if (k == 2) o = a.out[2];
+    if (k == 3) o = a.out[3];
+    return o;
+}
+
+// One 256-block of one matrix for a lane: the loads (a set of registers per
+// block in flight) and the arithmetic that adds the block to acc[i] (weight
+// row 4kg + i of the tile, input row n = lane & 15).
+struct GFragQ4 {
+    uint64_t qs[4];   // codes of sub-blocks 2c / 2c+1 (low / high nibbles), k = 8kg..8kg+7
+    u32x4_t h;        // the lane's row header: d|dmin, scales[12]
+};
+struct GFragQ6 {
+    uint64_t ql[2][2], qh[2];   // [half n][low / high ql], [half n], k = 8kg..8kg+7
+    uint64_t s0, s1;            // the row's 16 int8 scales
+    uint32_t dh;                // fp16 d
+};
+struct GFragX {
+    uint64_t xb[8];   // Q8_K codes of input row n, k window 32j + 8kg
+    int32_t bsx[8];   // their 32-element sums (Q4_K mins)
+    float dx;
+};
+
+template <bool Q4>
+__device__ __forceinline__ auto gemm_load_w(__amdgpu_buffer_rsrc_t rs, uint32_t boff, int kg) {
+    if constexpr (Q4) {
+        GFragQ4 f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const u32x2_t v = __builtin_bit_cast(
+                u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs, boff + 16 + 32 * c + 8 * kg, 0, 0));
+            f.qs[c] = ((uint64_t)v.y << 32) | v.x;
+        }
+        f.h = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, boff, 0, 0));
+        return f;
+    } else {
+        GFragQ6 f;
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            f.ql[n][0] = ld8_even(rs, boff + 64 * n + 8 * kg);
+            f.ql[n][1] = ld8_even(rs, boff + 64 * n + 32 + 8 * kg);
+            f.qh[n] = ld8_even(rs, boff + 128 + 32 * n + 8 * kg);
+        }
+        f.s0 = ld8_even(rs, boff + 192);
+        f.s1 = ld8_even(rs, boff + 200);
+        f.dh = __builtin_amdgcn_raw_buffer_load_b16(rs, boff + 208, 0, 0);
+        return f;
+    }
+}
+
+template <bool Q4>
+__device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, int col, int b, int kg) {
+    GFragX x;
+    const int K = a.n_in;
+    const int8_t *xc = a.xq + (int64_t)col * K + 256 * b + 8 * kg;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x.xb[j] = *reinterpret_cast<const uint64_t *>(xc + 32 * j);
+    if constexpr (Q4) {
+        const int4 *bs = reinterpret_cast<const int4 *>(a.xbs + (int64_t)col * (K / 32) + 8 * b);
+        const int4 s0 = bs[0], s1 = bs[1];
+        x.bsx[0] = s0.x; x.bsx[1] = s0.y; x.bsx[2] = s0.z; x.bsx[3] = s0.w;
+        x.bsx[4] = s1.x; x.bsx[5] = s1.y; x.bsx[6] = s1.z; x.bsx[7] = s1.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x.bsx[j] = 0;
+    }
+    x.dx = a.xd[(int64_t)col * (K >> 8) + b];
+    return x;
+}
+
+__device__ __forceinline__ void gemm_compute(const GFragQ4 &f, const GFragX &x, uint32_t (*hdr)[6],
+                                             int kg, int rr, float (&acc)[4]) {
+    const i32x4_t z = {0, 0, 0, 0};
+    if (kg == 0) {
+        // this lane's row: d|dmin, then the 6-bit scales and mins one per byte
+        hdr[rr][0] = f.h.x;
+        hdr[rr][1] = f.h.y & 0x3f3f3f3fu;
+        hdr[rr][2] = (f.h.w & 0x0f0f0f0fu) | ((f.h.y >> 2) & 0x30303030u);
+        hdr[rr][3] = f.h.z & 0x3f3f3f3fu;
+        hdr[rr][4] = ((f.h.w >> 4) & 0x0f0f0f0fu) | ((f.h.z >> 2) & 0x30303030u);
+    }
+    // (a wave's LDS accesses complete in order: the rows' headers are in place)
+    uint32_t hd[4][5];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int w = 0; w < 5; ++w) hd[i][w] = hdr[4 * kg + i][w];
+    int isum[4] = {0, 0, 0, 0}, imin[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const uint64_t q = (j & 1) ? (f.qs[j >> 1] >> 4) & 0x0f0f0f0f0f0f0f0full
+                                   : f.qs[j >> 1] & 0x0f0f0f0f0f0f0f0full;
+        const i32x4_t c = mfma_i8(q, x.xb[j], z);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t sh = 8 * (j & 3);
+            const int sc = (int)(((j < 4 ? hd[i][1] : hd[i][2]) >> sh) & 255u);
+            const int mn = (int)(((j < 4 ? hd[i][3] : hd[i][4]) >> sh) & 255u);
+            isum[i] += sc * c[i];
+            imin[i] += mn * x.bsx[j];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float d = h2f(hd[i][0] & 0xffffu) * x.dx, dmin = h2f(hd[i][0] >> 16) * x.dx;
+        acc[i] += d * (float)isum[i] - dmin * (float)imin[i];
+    }
+}
+
+__device__ __forceinline__ void gemm_compute(const GFragQ6 &f, const GFragX &x, uint32_t (*hdr)[6],
+                                             int kg, int rr, float (&acc)[4]) {
+    const i32x4_t z = {0, 0, 0, 0};
+    if (kg == 0) {
+        hdr[rr][0] = f.dh;
+        hdr[rr][1] = (uint32_t)f.s0;
+        hdr[rr][2] = (uint32_t)(f.s0 >> 32);
+        hdr[rr][3] = (uint32_t)f.s1;
+        hdr[rr][4] = (uint32_t)(f.s1 >> 32);
+    }
+    uint32_t hd[4][5];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int w = 0; w < 5; ++w) hd[i][w] = hdr[4 * kg + i][w];
+    int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const uint64_t lo = f.ql[n][g & 1];
+            const uint64_t nib = g < 2 ? lo & 0x0f0f0f0f0f0f0f0full : (lo >> 4) & 0x0f0f0f0f0f0f0f0full;
+            const uint64_t hb = ((f.qh[n] >> (2 * g)) & 0x0303030303030303ull) << 4;
+            const uint64_t cc = nib | hb;
+            const uint64_t q = ((uint64_t)recentre6((uint32_t)(cc >> 32)) << 32) | recentre6((uint32_t)cc);
+            // the window's two 16-element scale groups: lanes kg < 2 hold the first
+            const i32x4_t c0 = mfma_i8(kg < 2 ? q : 0ull, x.xb[4 * n + g], z);
+            const i32x4_t c1 = mfma_i8(kg < 2 ? 0ull : q, x.xb[4 * n + g], z);
+            const int t = 8 * n + 2 * g;   // scale index of the first group
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int s0 = (int)(int8_t)(hd[i][1 + (t >> 2)] >> (8 * (t & 3)));
+                const int s1 = (int)(int8_t)(hd[i][1 + ((t + 1) >> 2)] >> (8 * ((t + 1) & 3)));
+                isum[i] += s0 * c0[i] + s1 * c1[i];
+            }
+        }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += (h2f(hd[i][0]) * x.dx) * (float)isum[i];
+}
+
+constexpr int kGemmWaves = 8;
+
+template <bool Q4>
+__device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, const MmOut &o1,
+                                          uint32_t (*hdr)[16][6],
+                                          float (*red)[kGemmWaves][16][17]) {
+    constexpr int W = kGemmWaves;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kg = lane >> 4, rr = lane & 15;
+    const bool swiglu = a.swiglu != 0;
+    const int mats = swiglu ? 2 : 1;
+    const int K = a.n_in, nb = K >> 8;
+    const uint32_t bbytes = Q4 ? kQ4Bytes : kQ6Bytes, rbytes = (uint32_t)nb * bbytes;
+    const int row0 = ((int)blockIdx.x - o0.tile0) * 16, col0 = (int)blockIdx.y * 16;
+    const int row = min(row0 + rr, o0.n_rows - 1);
+    const int col = min(col0 + rr, a.n_cols - 1);
+    const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(o0.w), (short)0, (int)(rbytes * (uint32_t)o0.n_rows), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t *>(o1.w), (short)0, (int)(rbytes * (uint32_t)o1.n_rows), 0x00020000);
+    // SwiGLU: waves 0..W/2-1 take W1, the others W3; otherwise all W waves
+    // split K.  A wave holds one matrix's registers either way.
+    const int kw = swiglu ? W / 2 : W;
+    const int m = swiglu ? wave / kw : 0, wm = wave - m * kw;
+    const __amdgpu_buffer_rsrc_t rs = m ? rs1 : rs0;
+    float acc[4] = {0, 0, 0, 0};
+    using GF = std::conditional_t<Q4, GFragQ4, GFragQ6>;
+    // two register sets, A and B, alternate between the wave's blocks
+    // b, b + kw, b + 2 kw, ...: the next block's loads are in flight while the
+    // current one is computed, and no set is copied
+    GF wa, wb;
+    GFragX xa, xb;
+    auto boff = [&](int b) { return (uint32_t)row * rbytes + (uint32_t)b * bbytes; };
+    int b = wm;
+    if (b < nb) {
+        wa = gemm_load_w<Q4>(rs, boff(b), kg);
+        xa = gemm_load_x<Q4>(a, col, b, kg);
+    }
+    for (; b < nb; b += 2 * kw) {
+        if (b + kw < nb) {
+            wb = gemm_load_w<Q4>(rs, boff(b + kw), kg);
+            xb = gemm_load_x<Q4>(a, col, b + kw, kg);
+        }
+        gemm_compute(wa, xa, hdr[wave], kg, rr, acc);
+        if (b + kw >= nb) break;
+        if (b + 2 * kw < nb) {
+            wa = gemm_load_w<Q4>(rs, boff(b + 2 * kw), kg);
+            xa = gemm_load_x<Q4>(a, col, b + 2 * kw, kg);
+        }
+        gemm_compute(wb, xb, hdr[wave], kg, rr, acc);
+    }
+    // the waves' partial sums meet in LDS: red[matrix][wave of that matrix][row][input row]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[m][wm][4 * kg + i][rr] = acc[i];
+    (void)mats;
+    __syncthreads();
+    const int t = threadIdx.x;
+    if (t < 256) {
+        const int c = t >> 4, r = t & 15;   // 16 consecutive rows per input row
+        const int orow = row0 + r, ocol = col0 + c;
+        if (orow < o0.n_rows && ocol < a.n_cols) {
+            float v0 = 0.0f, v1 = 0.0f;
+            for (int w = 0; w < kw; ++w) v0 += red[0][w][r][c];
+            if (o0.bias) v0 = v0 + o0.bias[orow];
+            float y;
+            if (swiglu) {
+                for (int w = 0; w < kw; ++w) v1 += red[1][w][r][c];
+                if (o1.bias) v1 = v1 + o1.bias[orow];
+                y = silu(v0) * v1;
+            } else {
+                y = o0.add ? o0.add[(int64_t)ocol * o0.n_rows + orow] + v0 : v0;
+            }
+            o0.y[(int64_t)ocol * o0.n_rows + orow] = y;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(64 * kGemmWaves) k_gemm_kq(MmArgs a) {
+    __shared__ uint32_t hdr[kGemmWaves][16][6];
+    __shared__ float red[2][kGemmWaves][16][17];
+    int seg = 0;
+#pragma unroll
+    for (int k = 1; k < kMvMaxOuts; ++k)
+        if (k < a.n_outs && (int)blockIdx.x >= a.out[k].tile0) seg = k;
+    const MmOut o0 = mm_out_at(a, seg);
+    const MmOut o1 = a.swiglu ? a.out[1] : o0;
+    // one weight dtype per work group (both SwiGLU matrices share it)
+    if (o0.dtype == VKV_DTYPE_Q4_K) gemm_body<true>(a, o0, o1, hdr, red);
+    else gemm_body<false>(a, o0, o1, hdr, red);
+}
+
 }  // namespace
 
 hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st) {
@@ -674,6 +1016,25 @@ hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const flo
     const int64_t threads = n / 8;
     k_kq_dequant<<<(unsigned)((threads + 255) / 256), 256, 0, st>>>(dtype, src, n, add, y,
                                                                     zero_words);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int n_rows, int n, const float *norm_w,
+                           const float *norm_b, const float *ada, float eps, int8_t *codes,
+                           float *xd, int32_t *bs32, hipStream_t st) {
+    k_q8k_rows<<<n_rows, 256, 0, st>>>(x, x_stride, n, norm_w, norm_b, ada, eps, codes, xd, bs32);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_kq(const MmArgs &a, int n_tiles, int n_col_tiles, hipStream_t st) {
+    const dim3 grid((unsigned)n_tiles, (unsigned)n_col_tiles);
+    k_gemm_kq<<<grid, 64 * kGemmWaves, 0, st>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_rows(const float *x, int n_rows, int n, const float *w, const float *b,
+                                float eps, float *y, hipStream_t st) {
+    k_rms_norm_rows<<<n_rows, 256, 0, st>>>(x, n, w, b, eps, y);
     return hipGetLastError();
 }
 

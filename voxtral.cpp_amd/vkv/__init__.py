@@ -132,6 +132,26 @@ class MvOut(ctypes.Structure):
     _fields_ = [("w", _vp), ("dtype", _i32), ("n_rows", _i32), ("y", _vp), ("add", _vp)]
 
 
+class MmOut(ctypes.Structure):
+    _fields_ = [("w", _vp), ("dtype", _i32), ("n_rows", _i32), ("y", _vp), ("add", _vp),
+                ("bias", _vp)]
+
+
+class EncLayer(ctypes.Structure):
+    _fields_ = [("attn_norm", _vp), ("attn_norm_b", _vp), ("attn_q", _vp), ("attn_k", _vp),
+                ("attn_v", _vp), ("attn_o", _vp), ("attn_q_type", _i32), ("attn_k_type", _i32),
+                ("attn_v_type", _i32), ("attn_o_type", _i32), ("attn_q_b", _vp), ("attn_v_b", _vp),
+                ("attn_o_b", _vp), ("ffn_norm", _vp), ("ffn_norm_b", _vp), ("ffn_w1", _vp),
+                ("ffn_w2", _vp), ("ffn_w3", _vp), ("ffn_w1_type", _i32), ("ffn_w2_type", _i32),
+                ("ffn_w3_type", _i32), ("ffn_w2_b", _vp)]
+
+
+class EncModel(ctypes.Structure):
+    _fields_ = [("n_layers", _i32), ("dim", _i32), ("hidden", _i32), ("n_heads", _i32),
+                ("head_dim", _i32), ("norm_eps", _f32), ("rope_theta", _f32), ("out_norm", _vp),
+                ("out_norm_b", _vp), ("layers", _P(EncLayer))]
+
+
 class DecLayer(ctypes.Structure):
     _fields_ = [("attn_norm", _vp), ("attn_q", _vp), ("attn_k", _vp), ("attn_v", _vp),
                 ("attn_o", _vp), ("attn_q_type", _i32), ("attn_k_type", _i32),
@@ -181,6 +201,12 @@ PROTOTYPES = {
     "vkv_q8_0_pack": (_i32, [_vp, _vp, _i64, _vp]),
     "vkv_q8_0_unpack": (_i32, [_vp, _vp, _i64, _vp]),
     "vkv_matvec": (_i32, [_vp, _i64, _vp, _vp, _f32, _P(MvOut), _i32, _i32, _vp]),
+    "vkv_matmul_workspace": (ctypes.c_size_t, [_i32, _i64]),
+    "vkv_encoder_chunk_workspace": (ctypes.c_size_t, [_P(EncModel), _i32]),
+    "vkv_encoder_chunk": (_i32, [_vp, _i32, _P(EncPlan), _i32, _P(EncModel), _vp, _vp,
+                                 ctypes.c_size_t, _vp]),
+    "vkv_matmul": (_i32, [_vp, _i32, _i64, _vp, _vp, _vp, _f32, _P(MmOut), _i32, _i32, _vp,
+                          ctypes.c_size_t, _vp]),
     "vkv_quantize_q8_k": (_i32, [_vp, _i64, _vp, _vp, _f32, _vp, _vp]),
     "vkv_dequantize": (_i32, [_i32, _vp, _i64, _vp, _vp]),
     "vkv_decoder_layer_step": (_i32, [_vp, _i32, _P(Plan), _i64, _i32, _i32, _vp, _vp, _vp, _vp,
@@ -415,6 +441,32 @@ def matvec(x_ptr, n_in, outs, norm_w_ptr=None, ada_ptr=None, eps=1e-5, epilogue=
         arr[i] = MvOut(w, dt, n, y, add)
     check(lib.vkv_matvec(x_ptr, n_in, norm_w_ptr, ada_ptr, eps, arr, len(outs), epilogue,
                          hip_stream))
+
+
+def encoder_chunk_workspace(model, n_new):
+    return lib.vkv_encoder_chunk_workspace(ctypes.byref(model), n_new)
+
+
+def encoder_chunk(cache, stream, plan, window, model, x_ptr, ws_ptr, ws_bytes, hip_stream=0):
+    check(lib.vkv_encoder_chunk(cache.handle, stream, ctypes.byref(plan), window,
+                                ctypes.byref(model), x_ptr, ws_ptr, ws_bytes, hip_stream))
+
+
+def matmul_workspace(n_cols, n_in):
+    return lib.vkv_matmul_workspace(n_cols, n_in)
+
+
+def matmul(x_ptr, n_cols, n_in, outs, ws_ptr, ws_bytes, norm_w_ptr=None, norm_b_ptr=None,
+           ada_ptr=None, eps=1e-5, epilogue=MV_STORE, hip_stream=0):
+    """Y = W h for n_cols input rows; outs: (w_ptr, dtype, n_rows, y_ptr[, add_ptr[, bias_ptr]])."""
+    arr = (MmOut * len(outs))()
+    for i, o in enumerate(outs):
+        w, dt, n, y = o[:4]
+        add = o[4] if len(o) > 4 else None
+        bias = o[5] if len(o) > 5 else None
+        arr[i] = MmOut(w, dt, n, y, add, bias)
+    check(lib.vkv_matmul(x_ptr, n_cols, n_in, norm_w_ptr, norm_b_ptr, ada_ptr, eps, arr, len(outs),
+                         epilogue, ws_ptr, ws_bytes, hip_stream))
 
 
 def quantize_q8_k(x_ptr, n, blocks_ptr, norm_w_ptr=None, ada_ptr=None, eps=1e-5, hip_stream=0):
