@@ -31,7 +31,8 @@ Other workloads (--workload), reported on the same contract:
                residual, RMSNorm*(1+ada)+SwiGLU W1/W3, W2 + residual; then the
                final norm + the 131072-row Q6_K logits -- 105 vkv_matvec
                calls, 2.24 GB of weights per token; tokens/s.
-  encoder_chunk_q4km  the encoder's transformer for one 16-frame chunk through
+  encoder_chunk_q4km  the encoder for one 16-frame chunk: the conv stem over
+               the chunk's Mel window (vkv_enc_conv_stem), then
                vkv_encoder_chunk: 32 layers x (RMSNorm + Q/K/V with biases,
                RoPE, ring append + window-750 attention, O + bias + residual,
                RMSNorm + SwiGLU, W2 + bias + residual) + final norm, on Q4_K_M
@@ -178,9 +179,11 @@ ENC_MATS = [("attn_q", 12, E_DIM, 1280), ("attn_k", 12, E_DIM, 1280), ("attn_v",
 
 
 def encoder_chunk_bytes(n_keys):
-    """weights of 32 layers + the window attention's bytes for one chunk"""
+    """conv stem weights (f16) + 32 layers' weights + the window attention's
+    bytes for one chunk"""
+    conv = 2 * 1280 * 3 * (128 + 1280)
     w = E_LAYERS * sum(mat_bytes(dt, r, n) for _, dt, r, n in ENC_MATS)
-    return w + encoder_bytes_per_chunk(n_keys)
+    return conv + w + encoder_bytes_per_chunk(n_keys)
 
 
 def gpu_encoder_chunk(steps, warmup):
@@ -226,15 +229,26 @@ def gpu_encoder_chunk(steps, warmup):
         cache.append(0, 0, E_LAYERS, vkv.plan_segs(plan.write_seg, plan.write_nseg), k.data_ptr(),
                      v.data_ptr(), hip_stream=sp)
     T = warmup + steps
-    x0 = torch.randn(T, E_CHUNK, 1280, device="cuda", generator=gen)
+    plans = [vkv.enc_plan((first + i) * E_CHUNK, E_CHUNK, E_CAP, E_WIN) for i in range(T)]
+    # the conv stem's f16 weights and each chunk's Mel window [128][2 * 16 + 4]
+    w0 = (torch.randn(1280, 128, 3, device="cuda", generator=gen) * 0.05).half()
+    w1 = (torch.randn(1280, 1280, 3, device="cuda", generator=gen) * 0.02).half()
+    b0 = torch.randn(1280, device="cuda", generator=gen) * 0.1
+    b1 = torch.randn(1280, device="cuda", generator=gen) * 0.1
+    conv_len = plans[0].conv_mel_end - plans[0].conv_mel_start
+    mel = torch.randn(T, 128, conv_len, device="cuda", generator=gen)
     x = torch.empty(E_CHUNK, 1280, device="cuda")
     ws_bytes = vkv.encoder_chunk_workspace(model, E_CHUNK)
     ws = torch.empty(ws_bytes // 4 + 64, device="cuda")
     ws_ptr = (ws.data_ptr() + 255) & ~255
-    plans = [vkv.enc_plan((first + i) * E_CHUNK, E_CHUNK, E_CAP, E_WIN) for i in range(T)]
+    cb = vkv.enc_conv_stem_workspace(conv_len, 128, 1280, E_CHUNK)
+    cws = torch.empty(cb // 4 + 64, device="cuda")
+    cws_ptr = (cws.data_ptr() + 255) & ~255
 
     def step(i):
-        x.copy_(x0[i])
+        vkv.enc_conv_stem(mel[i].data_ptr(), 128, plans[i], w0.data_ptr(), b0.data_ptr(),
+                          w1.data_ptr(), b1.data_ptr(), 1280, x.data_ptr(), cws_ptr, cb,
+                          hip_stream=sp)
         vkv.encoder_chunk(cache, 0, plans[i], E_WIN, model, x.data_ptr(), ws_ptr, ws_bytes,
                           hip_stream=sp)
 
@@ -660,13 +674,15 @@ def main():
         res = {"metric": "encoder transformer frames/s (Q4_K_M projections on the matrix cores + "
                          "window-750 attention, 32 layers, 16-frame chunks) and HBM GB/s",
                "unit": "frames/s"}
-        config = {"workload": "one 16-frame encoder chunk through vkv_encoder_chunk: 32 x "
+        config = {"workload": "one 16-frame encoder chunk: conv stem (128 Mel bins -> 1280, "
+                              "kernel 3, strides 1 and 2, GELU) + vkv_encoder_chunk: 32 x "
                               "(RMSNorm + Q/K/V + biases, RoPE, ring append + window-750 "
                               "attention, O + bias + residual, RMSNorm + SwiGLU, W2 + bias + "
                               "residual) + final norm; dim 1280, 32 heads x 64, hidden 5120",
                   "layers": E_LAYERS, "window": E_WIN, "frames_per_chunk": E_CHUNK,
                   "bytes_per_chunk": bytes_step, "keys_per_query_block": n_keys}
-        kernel = "k_q8k_rows + k_gemm_kq + k_rope + k_window_mfma (11 launches per layer)"
+        kernel = ("conv stem (k_im2col_f16 + k_gemm_f16, x2) + 32 x (k_q8k_rows + k_gemm_kq, x4; "
+                  "k_rope; k_window_mfma) + final norm")
     elif args.workload == "decoder_token_q4km":
         total_ms, step_ms, wall = gpu_token(args.steps, args.warmup)
         bytes_step = token_bytes()

@@ -441,6 +441,19 @@ typedef struct vkv_enc_model {
     const vkv_enc_layer *layers;   /* host array of n_layers */
 } vkv_enc_model;
 
+/* The conv stem for an encoder plan (build_encoder_kv_graph, src/voxtral.cpp:
+ * 2094-2126): mel is the plan's Mel window [n_mel][conv_len] (bins major,
+ * frames contiguous, conv_len = conv_mel_end - conv_mel_start); conv0
+ * (kernel 3, stride 1, n_mel -> dim, causal pad 2) + bias + GELU(erf), conv1
+ * (kernel 3, stride 2, dim -> dim, causal pad 1) + bias + GELU(erf), both as
+ * ggml computes them (im2col in f16, f16 weights [out][in][3], f32 sums); the
+ * plan's n_new frames from conv_slice_start go to x [n_new][dim]. */
+size_t vkv_enc_conv_stem_workspace(int32_t conv_len, int32_t n_mel, int32_t dim, int32_t n_new);
+vkv_status vkv_enc_conv_stem(const float *mel, int32_t n_mel, const vkv_enc_plan *plan,
+                             const void *conv0_w, const float *conv0_b, const void *conv1_w,
+                             const float *conv1_b, int32_t dim, float *x, void *workspace,
+                             size_t workspace_bytes, void *hip_stream);
+
 size_t vkv_encoder_chunk_workspace(const vkv_enc_model *model, int32_t n_new);
 vkv_status vkv_encoder_chunk(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
                              int32_t window, const vkv_enc_model *model, float *x,

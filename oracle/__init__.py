@@ -117,6 +117,10 @@ _protos = {
     "orc_norm_act_b": (None, [_vp, _i64, _vp, _vp, _vp, _f32, _vp]),
     "orc_silu": (_f32, [_f32]),
     "orc_argmax": (_i32, [_vp, _i64]),
+    "orc_conv_dims": (None, [_i32, _i32, _i32, _P(_i32), _P(_i32)]),
+    "orc_conv1d": (None, [_vp, _i64, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
+                          _i32, _vp]),
+    "orc_conv_stem": (None, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp]),
     "orc_wrow_bytes": (_i64, [ctypes.c_int, _i64]),
     "orc_matvec": (None, [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, ctypes.c_int]),
     "orc_decode_step_mimic_mt": (_f64, [ctypes.c_int, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
@@ -406,4 +410,37 @@ def matvec(dtype, w, n_rows, n_in, x, n_threads=1):
     assert w.size >= n_rows * wrow_bytes(dtype, n_in) and x.size == n_in
     y = np.empty(n_rows, dtype=np.float32)
     lib.orc_matvec(dtype, _ptr(w), n_rows, n_in, _ptr(x), _ptr(y), n_threads)
+    return y
+
+
+# ---- the encoder conv stem ----
+def conv_dims(in_len, kernel, stride):
+    pad, out = _i32(), _i32()
+    lib.orc_conv_dims(in_len, kernel, stride, ctypes.byref(pad), ctypes.byref(out))
+    return pad.value, out.value
+
+
+def conv_stem(mel, slice_start, n_new, w0, b0, w1, b1):
+    """mel [n_mel][conv_len] f32; w0 [dim][n_mel][3] / w1 [dim][dim][3] as f16
+    bits (uint16); returns x [n_new][dim]."""
+    mel = _f32a(mel)
+    n_mel, conv_len = mel.shape
+    w0 = np.ascontiguousarray(w0, np.uint16)
+    w1 = np.ascontiguousarray(w1, np.uint16)
+    dim = w0.shape[0]
+    b0, b1 = _f32a(b0), _f32a(b1)
+    x = np.empty((n_new, dim), np.float32)
+    lib.orc_conv_stem(_ptr(mel), n_mel, conv_len, slice_start, n_new, _ptr(w0), _ptr(b0),
+                      _ptr(w1), _ptr(b1), dim, _ptr(x))
+    return x
+
+
+def conv1d(inp, stride_c, stride_t, in_len, n_ch, w, b, stride, pad, t0, n_out, gelu=True):
+    """one causal conv (f16 im2col of inp read with the given strides), y [n_out][out_ch]"""
+    inp = _f32a(inp)
+    w = np.ascontiguousarray(w, np.uint16)
+    b = _f32a(b)
+    y = np.empty((n_out, w.shape[0]), np.float32)
+    lib.orc_conv1d(_ptr(inp), stride_c, stride_t, in_len, n_ch, _ptr(w), _ptr(b), w.shape[0],
+                   stride, pad, t0, n_out, 1 if gelu else 0, _ptr(y))
     return y

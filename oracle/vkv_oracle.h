@@ -217,6 +217,16 @@ int64_t orc_wrow_bytes(int dtype, int64_t n_in);
 void orc_matvec(int dtype, const uint8_t *w, int64_t n_rows, int64_t n_in, const float *x,
                 float *y, int n_threads);
 
+/* ---- the encoder conv stem (conv.c) ---- */
+void orc_conv_dims(int32_t in_len, int32_t kernel, int32_t stride, int32_t *pad_left,
+                   int32_t *out_len);
+void orc_conv1d(const float *in, int64_t stride_c, int64_t stride_t, int32_t in_len, int32_t n_ch,
+                const uint16_t *w, const float *b, int32_t n_out_ch, int32_t stride, int32_t pad,
+                int32_t t0, int32_t n_out, int32_t gelu, float *y);
+void orc_conv_stem(const float *mel, int32_t n_mel, int32_t conv_len, int32_t slice_start,
+                   int32_t n_new, const uint16_t *w0, const float *b0, const uint16_t *w1,
+                   const float *b1, int32_t dim, float *x);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1354,6 +1354,97 @@ vkv_status vkv_decoder_token(vkv_cache *cache, int32_t stream, vkv_ring *ring,
     return ok();
 }
 
+// ---- the encoder conv stem ----
+
+namespace {
+
+// compute_causal_conv1d_dims (src/voxtral.cpp:1670-1687)
+struct ConvDims {
+    int32_t pad_left, pad_right, padded_len, out_len;
+};
+ConvDims causal_conv1d_dims(int32_t in_len, int32_t kernel, int32_t stride) {
+    ConvDims d{0, 0, 0, 0};
+    if (in_len <= 0 || kernel <= 0 || stride <= 0) return d;
+    const int32_t padding_total = kernel - stride;
+    const float n_frames = ((float)(in_len - kernel + padding_total) / (float)stride) + 1.0f;
+    const int32_t target = ((int32_t)std::ceil(n_frames) - 1) * stride + (kernel - padding_total);
+    d.pad_left = padding_total;
+    d.pad_right = std::max<int32_t>(0, target - in_len);
+    d.padded_len = in_len + d.pad_left + d.pad_right;
+    d.out_len = (d.padded_len - kernel) / stride + 1;
+    return d;
+}
+
+struct ConvBuffers {
+    void *cols0;
+    float *y0;
+    void *cols1;
+    size_t bytes;
+};
+ConvBuffers conv_buffers(int32_t conv_len, int32_t n_mel, int32_t dim, int32_t n_new, uint8_t *base) {
+    ConvBuffers b{};
+    size_t off = 0;
+    auto take = [&](size_t n) {
+        uint8_t *p = base ? base + off : nullptr;
+        off += (n + 255) & ~(size_t)255;
+        return p;
+    };
+    b.cols0 = take((size_t)conv_len * n_mel * 3 * 2);
+    b.y0 = (float *)take((size_t)conv_len * dim * 4);
+    b.cols1 = take((size_t)n_new * dim * 3 * 2);
+    b.bytes = off;
+    return b;
+}
+
+}  // namespace
+
+size_t vkv_enc_conv_stem_workspace(int32_t conv_len, int32_t n_mel, int32_t dim, int32_t n_new) {
+    if (conv_len < 1 || n_mel < 1 || dim < 1 || n_new < 1) return 0;
+    return conv_buffers(conv_len, n_mel, dim, n_new, nullptr).bytes;
+}
+
+vkv_status vkv_enc_conv_stem(const float *mel, int32_t n_mel, const vkv_enc_plan *plan,
+                             const void *conv0_w, const float *conv0_b, const void *conv1_w,
+                             const float *conv1_b, int32_t dim, float *x, void *workspace,
+                             size_t workspace_bytes, void *hip_stream) {
+    if (!mel || !plan || !conv0_w || !conv0_b || !conv1_w || !conv1_b || !x || !workspace)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "conv stem: null argument");
+    if (n_mel < 1 || (n_mel * 3) % 32 || dim < 16 || (dim * 3) % 32 || dim % 16)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "conv stem: n_mel %d / dim %d unsupported", n_mel, dim);
+    const int64_t conv_len64 = plan->conv_mel_end - plan->conv_mel_start;
+    if (conv_len64 < 1 || conv_len64 > (1 << 20) || plan->n_new < 1)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "conv stem: empty or oversized Mel window");
+    const int32_t conv_len = (int32_t)conv_len64, n = plan->n_new;
+    const ConvDims d0 = causal_conv1d_dims(conv_len, 3, 1);
+    const ConvDims d1 = causal_conv1d_dims(d0.out_len, 3, 2);
+    if (plan->conv_slice_start < 0 || plan->conv_slice_start + n > d1.out_len)
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "conv stem: frames [%d, +%d) outside the %d conv outputs of the window",
+                    plan->conv_slice_start, n, d1.out_len);
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "conv stem: workspace not 256-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(conv0_w) | reinterpret_cast<uintptr_t>(conv1_w)) & 15u)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "conv stem: weights must be 16-byte aligned");
+    const ConvBuffers b = conv_buffers(conv_len, n_mel, dim, n, (uint8_t *)workspace);
+    if (workspace_bytes < b.bytes)
+        return fail(VKV_STATUS_BUFFER_TOO_SMALL, "conv stem: workspace %zu < %zu bytes",
+                    workspace_bytes, b.bytes);
+    hipStream_t st = as_stream(hip_stream);
+    hipError_t e;
+    // conv0 over the whole window: Mel is [bin][frame]
+    if ((e = launch_im2col_f16(mel, conv_len, 1, conv_len, n_mel, 1, d0.pad_left, 0, d0.out_len,
+                               b.cols0, st)) != hipSuccess ||
+        (e = launch_gemm_f16(conv0_w, b.cols0, conv0_b, b.y0, dim, d0.out_len, n_mel * 3, true, st)) !=
+            hipSuccess)
+        return hip_fail(e, "conv stem: conv0 launch");
+    // conv1 at the sliced frames only: y0 is [frame][channel]
+    if ((e = launch_im2col_f16(b.y0, 1, dim, d0.out_len, dim, 2, d1.pad_left, plan->conv_slice_start, n,
+                               b.cols1, st)) != hipSuccess ||
+        (e = launch_gemm_f16(conv1_w, b.cols1, conv1_b, x, dim, n, dim * 3, true, st)) != hipSuccess)
+        return hip_fail(e, "conv stem: conv1 launch");
+    return ok();
+}
+
 // ---- one encoder chunk ----
 
 namespace {

@@ -203,6 +203,9 @@ PROTOTYPES = {
     "vkv_matvec": (_i32, [_vp, _i64, _vp, _vp, _f32, _P(MvOut), _i32, _i32, _vp]),
     "vkv_matmul_workspace": (ctypes.c_size_t, [_i32, _i64]),
     "vkv_encoder_chunk_workspace": (ctypes.c_size_t, [_P(EncModel), _i32]),
+    "vkv_enc_conv_stem_workspace": (ctypes.c_size_t, [_i32, _i32, _i32, _i32]),
+    "vkv_enc_conv_stem": (_i32, [_vp, _i32, _P(EncPlan), _vp, _vp, _vp, _vp, _i32, _vp, _vp,
+                                 ctypes.c_size_t, _vp]),
     "vkv_encoder_chunk": (_i32, [_vp, _i32, _P(EncPlan), _i32, _P(EncModel), _vp, _vp,
                                  ctypes.c_size_t, _vp]),
     "vkv_matmul": (_i32, [_vp, _i32, _i64, _vp, _vp, _vp, _f32, _P(MmOut), _i32, _i32, _vp,
@@ -441,6 +444,16 @@ def matvec(x_ptr, n_in, outs, norm_w_ptr=None, ada_ptr=None, eps=1e-5, epilogue=
         arr[i] = MvOut(w, dt, n, y, add)
     check(lib.vkv_matvec(x_ptr, n_in, norm_w_ptr, ada_ptr, eps, arr, len(outs), epilogue,
                          hip_stream))
+
+
+def enc_conv_stem_workspace(conv_len, n_mel, dim, n_new):
+    return lib.vkv_enc_conv_stem_workspace(conv_len, n_mel, dim, n_new)
+
+
+def enc_conv_stem(mel_ptr, n_mel, plan, w0_ptr, b0_ptr, w1_ptr, b1_ptr, dim, x_ptr, ws_ptr,
+                  ws_bytes, hip_stream=0):
+    check(lib.vkv_enc_conv_stem(mel_ptr, n_mel, ctypes.byref(plan), w0_ptr, b0_ptr, w1_ptr,
+                                b1_ptr, dim, x_ptr, ws_ptr, ws_bytes, hip_stream))
 
 
 def encoder_chunk_workspace(model, n_new):
