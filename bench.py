@@ -86,6 +86,14 @@ WORKLOADS = {
                                streams=1, pmc="decoder_token_q4km_pmc.json",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs and "
                                     "KV rows, generated on device)"),
+    "adapter_q4km": dict(dtype=12, dtype_name="q4_k x q8_k weights (MFMA int8), f32 rings",
+                         streams=1, pmc="adapter_q4km_pmc.json", groups=32,
+                         data="synthetic (random valid Q4_K blocks, N(0,1) encoder frames, "
+                              "generated on device)"),
+    "adapter_group_q4km": dict(dtype=12, dtype_name="q4_k x q8_k weights (int8 dot), f32 rings",
+                               streams=1, pmc="", groups=1,
+                               data="synthetic (random valid Q4_K blocks, N(0,1) encoder "
+                                    "frames, generated on device)"),
     "decoder_weights_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k (int8 dot)", streams=1,
                                  pmc="matvec_q4km_26l_pmc.json",
                                  data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs, "
@@ -176,6 +184,74 @@ E_HID = 5120
 ENC_MATS = [("attn_q", 12, E_DIM, 1280), ("attn_k", 12, E_DIM, 1280), ("attn_v", 14, E_DIM, 1280),
             ("attn_o", 12, 1280, E_DIM), ("ffn_w1", 12, E_HID, 1280), ("ffn_w3", 12, E_HID, 1280),
             ("ffn_w2", 14, 1280, E_HID)]
+
+
+A_ENC, A_DOWN, A_RING = 1280, 4, 256
+
+
+def adapter_bytes(n_groups):
+    """both adapter matrices (Q4_K) + the groups' encoder rows read and audio
+    rows written"""
+    return (mat_bytes(12, DIM, A_ENC * A_DOWN) + mat_bytes(12, DIM, DIM) +
+            n_groups * (A_ENC * A_DOWN + DIM) * 4)
+
+
+def gpu_adapter(n_groups, steps, warmup):
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED)
+    w0 = random_kq_device(12, DIM, A_ENC * A_DOWN, gen)
+    w2 = random_kq_device(12, DIM, DIM, gen)
+    enc = torch.randn(A_RING, A_ENC, device="cuda", generator=gen)
+    aemb = torch.zeros(A_RING, DIM, device="cuda")
+    enc_r = vkv.RowRing(enc.data_ptr(), A_RING, A_ENC)
+    aemb_r = vkv.RowRing(aemb.data_ptr(), A_RING, DIM)
+    ad = vkv.Adapter(w0.data_ptr(), w2.data_ptr(), 12, 12, A_ENC, DIM, A_DOWN)
+    ws_bytes = vkv.adapter_workspace(ad, n_groups)
+    ws = torch.empty(ws_bytes // 4 + 64, device="cuda")
+    ws_ptr = (ws.data_ptr() + 255) & ~255
+
+    def step(i):
+        vkv.adapter_commit(ad, enc_r, aemb_r, i * n_groups, n_groups, ws_ptr, ws_bytes,
+                           hip_stream=sp)
+
+    total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
+    assert bool(torch.isfinite(aemb).all())
+    return total_ms, step_ms, wall
+
+
+def cpu_adapter_leg(n_groups, target_seconds):
+    """The oracle's adapter (gather, ggml's generic CPU q4_K x q8_K matvec,
+    GELU, matvec) on the same shapes, threaded over rows."""
+    import numpy as np
+
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(SEED)
+
+    def mat(r, n):
+        w = rng.integers(0, 256, size=(r * (n // 256), 144), dtype=np.uint8)
+        w[:, 0:2] = rng.uniform(2e-4, 4e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        w[:, 2:4] = rng.uniform(1e-4, 2e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        return w.reshape(-1)
+
+    w0, w2 = mat(DIM, A_ENC * A_DOWN), mat(DIM, DIM)
+    enc = rng.standard_normal((A_RING, A_ENC)).astype(np.float32)
+    aemb = np.zeros((A_RING, DIM), np.float32)
+    groups = 0
+    t0 = time.perf_counter()
+    while groups < 1 or (time.perf_counter() - t0 < target_seconds and groups < 4096):
+        oracle.adapter_commit(enc, aemb, groups, 1, 12, w0, 12, w2, n_threads=threads)
+        groups += 1
+    secs = time.perf_counter() - t0
+    return {"value": groups / secs, "unit": "audio embeddings/s", "cores": threads, "kind": "port",
+            "sample": f"{groups} adapter groups (4 x 1280 -> 3072 -> 3072, Q4_K) of the oracle's "
+                      f"restatement of ggml's CPU path, {threads} threads, {secs:.1f} s"}
 
 
 def encoder_chunk_bytes(n_keys):
@@ -683,6 +759,20 @@ def main():
                   "bytes_per_chunk": bytes_step, "keys_per_query_block": n_keys}
         kernel = ("conv stem (k_im2col_f16 + k_gemm_f16, x2) + 32 x (k_q8k_rows + k_gemm_kq, x4; "
                   "k_rope; k_window_mfma) + final norm")
+    elif args.workload in ("adapter_q4km", "adapter_group_q4km"):
+        ng = wl["groups"]
+        total_ms, step_ms, wall = gpu_adapter(ng, args.steps, args.warmup)
+        bytes_step = adapter_bytes(ng)
+        units_per_step = ng
+        res = {"metric": "adapter audio embeddings/s (4 encoder frames -> 3072, Q4_K_M adapter "
+                         "on the device rings) and HBM GB/s", "unit": "audio embeddings/s"}
+        config = {"workload": f"vkv_adapter_commit of {ng} group{'s' if ng > 1 else ''}: encoder-"
+                              "output ring rows (4 x 1280 f32 per group) -> adapter.0 (3072 x "
+                              "5120 Q4_K) -> GELU(erf) -> adapter.2 (3072 x 3072 Q4_K) -> "
+                              "audio-embedding ring rows; 256-row rings",
+                  "groups_per_commit": ng, "bytes_per_commit": bytes_step}
+        kernel = ("k_q8k_rows + k_gemm_kq (GELU) + k_q8k_rows + k_gemm_kq" if ng > 1 else
+                  "k_matvec (GELU) + k_matvec")
     elif args.workload == "decoder_token_q4km":
         total_ms, step_ms, wall = gpu_token(args.steps, args.warmup)
         bytes_step = token_bytes()
@@ -766,7 +856,10 @@ def main():
         res["cpu_baseline"] = cpu_weights_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload == "decoder_token_q4km":
         res["cpu_baseline"] = cpu_token_leg(args.cpu_seconds)
-    elif not args.no_cpu and args.workload not in ("encoder_f16", "encoder_chunk_q4km"):
+    elif not args.no_cpu and args.workload in ("adapter_q4km", "adapter_group_q4km"):
+        res["cpu_baseline"] = cpu_adapter_leg(wl["groups"], args.cpu_seconds)
+    elif not args.no_cpu and args.workload not in ("encoder_f16", "encoder_chunk_q4km",
+                                                   "adapter_q4km", "adapter_group_q4km"):
         res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds)
     print(json.dumps(res), flush=True)
 

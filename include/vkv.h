@@ -367,6 +367,7 @@ typedef struct vkv_mv_out {
 
 #define VKV_MV_STORE 0
 #define VKV_MV_SWIGLU 1   /* n_outs = 2, equal rows and dtype: outs[0].y = silu(W0 h) * (W1 h) */
+#define VKV_MV_GELU 2     /* every y = gelu_erf(W h) (+ bias first in vkv_matmul); no residual */
 
 /* y_k = W_k h for up to VKV_MV_MAX_OUTS matrices reading the same input (the
  * Q/K/V projections in one call).  x, norm_w, ada: 16-byte aligned device
@@ -458,6 +459,62 @@ size_t vkv_encoder_chunk_workspace(const vkv_enc_model *model, int32_t n_new);
 vkv_status vkv_encoder_chunk(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
                              int32_t window, const vkv_enc_model *model, float *x,
                              void *workspace, size_t workspace_bytes, void *hip_stream);
+
+/* ---------------------------------------------------------------------------
+ * The realtime rings between encoder, adapter and decoder (src/voxtral.cpp:
+ * 42-55, 388-404, 1467-1485): the encoder-output ring holds encoder frames
+ * ([256][1280] f32) until the adapter consumes them DOWNSAMPLE (4) at a time;
+ * the audio-embedding ring holds one adapter output per group ([256][3072]
+ * f32) until the decoder step reads it (audio position p at row p % 256).
+ * Logical row r lives at row r % capacity.  The caller owns the memory
+ * (capacity * width floats of 16-byte aligned device memory).
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_row_ring {
+    float *rows;          /* [capacity][width] */
+    int32_t capacity;     /* rows */
+    int32_t width;        /* floats per row */
+} vkv_row_ring;
+
+/* src rows i -> logical rows row_start + i, n_rows <= capacity
+ * (copy_chunk_to_enc_out_ring, src/voxtral.cpp:4018-4043: one device copy
+ * per contiguous segment, at most two). */
+vkv_status vkv_row_ring_write(vkv_row_ring *ring, int64_t row_start, const float *src,
+                              int32_t n_rows, void *hip_stream);
+
+/* Logical rows row_start.. -> dst (host or device memory), 1 <= n_rows <=
+ * capacity (read_realtime_ring_rows, src/voxtral.cpp:5530-5554); returns
+ * after the copy has completed. */
+vkv_status vkv_row_ring_read(const vkv_row_ring *ring, int64_t row_start, int32_t n_rows,
+                             float *dst, void *hip_stream);
+
+/* vkv_encoder_chunk with the final norm's rows stored at the encoder-output
+ * ring's logical rows plan->q_start .. + n_new (build_encoder_steady_graph's
+ * ggml_set_rows, src/voxtral.cpp:2505-2508); x ends holding the last layer's
+ * residual stream.  ring width = model dim, n_new <= capacity. */
+vkv_status vkv_encoder_chunk_ring(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
+                                  int32_t window, const vkv_enc_model *model, float *x,
+                                  vkv_row_ring *enc_out, void *workspace, size_t workspace_bytes,
+                                  void *hip_stream);
+
+/* The adapter over ring groups (build_adapter_ring_graph_reusable,
+ * src/voxtral.cpp:2589-2620, as voxtral_ctx_adapter_commit :5424-5485 runs
+ * it): for each group g in [group_start, group_start + n_groups), its
+ * frames downsample*g .. downsample*g + downsample-1 of the encoder-output ring (one
+ * contiguous row of enc_dim * downsample floats: the ring capacity must be a
+ * multiple of downsample), h = gelu_erf(W0 x), audio-embedding logical row
+ * g = W2 h.  Both products as vkv_matmul computes them (Q8_K input,
+ * integer block sums); Q4_K or Q6_K weights. */
+typedef struct vkv_adapter {
+    const void *w0;       /* adapter.0.weight [dec_dim][enc_dim * downsample] */
+    const void *w2;       /* adapter.2.weight [dec_dim][dec_dim] */
+    int32_t w0_type, w2_type;
+    int32_t enc_dim, dec_dim, downsample;
+} vkv_adapter;
+
+size_t vkv_adapter_workspace(const vkv_adapter *adapter, int32_t n_groups);
+vkv_status vkv_adapter_commit(const vkv_adapter *adapter, const vkv_row_ring *enc_out,
+                              vkv_row_ring *audio_emb, int64_t group_start, int32_t n_groups,
+                              void *workspace, size_t workspace_bytes, void *hip_stream);
 
 /* The decoder step's input row: ggml_get_rows(tok_embeddings, token) +
  * audio embedding (src/voxtral.cpp:3008-3019): row `token` of a Q4_K/Q6_K

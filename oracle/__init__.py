@@ -121,6 +121,11 @@ _protos = {
     "orc_conv1d": (None, [_vp, _i64, _i64, _i32, _i32, _vp, _vp, _i32, _i32, _i32, _i32, _i32,
                           _i32, _vp]),
     "orc_conv_stem": (None, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp]),
+    "orc_gelu_erf": (_f32, [_f32]),
+    "orc_row_ring_write": (_i32, [_vp, _i32, _i32, _i64, _vp, _i32]),
+    "orc_row_ring_read": (_i32, [_vp, _i32, _i32, _i64, _i32, _vp]),
+    "orc_adapter_commit": (_i32, [_vp, _i32, _i32, _i32, _vp, _i32, _i32, _i64, _i32,
+                                  ctypes.c_int, _vp, ctypes.c_int, _vp, ctypes.c_int]),
     "orc_wrow_bytes": (_i64, [ctypes.c_int, _i64]),
     "orc_matvec": (None, [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, ctypes.c_int]),
     "orc_decode_step_mimic_mt": (_f64, [ctypes.c_int, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
@@ -444,3 +449,45 @@ def conv1d(inp, stride_c, stride_t, in_len, n_ch, w, b, stride, pad, t0, n_out, 
     lib.orc_conv1d(_ptr(inp), stride_c, stride_t, in_len, n_ch, _ptr(w), _ptr(b), w.shape[0],
                    stride, pad, t0, n_out, 1 if gelu else 0, _ptr(y))
     return y
+
+
+# ---- the realtime rows rings and the adapter ----
+def gelu_erf(x):
+    """ggml_gelu_erf of f32 values, elementwise"""
+    x = _f32a(x)
+    return np.array([lib.orc_gelu_erf(float(v)) for v in x.ravel()], np.float32).reshape(x.shape)
+
+
+def row_ring_write(ring, row_start, src):
+    """src rows -> logical rows row_start.. of ring [capacity][width] (in place)"""
+    assert ring.dtype == np.float32 and ring.flags.c_contiguous
+    src = _f32a(src).reshape(-1, ring.shape[1])
+    rc = lib.orc_row_ring_write(_ptr(ring), ring.shape[0], ring.shape[1], row_start, _ptr(src),
+                                src.shape[0])
+    if rc != 0:
+        raise ValueError("ring write rejected")
+
+
+def row_ring_read(ring, row_start, n_rows):
+    ring = _f32a(ring)
+    dst = np.empty((n_rows, ring.shape[1]), np.float32)
+    rc = lib.orc_row_ring_read(_ptr(ring), ring.shape[0], ring.shape[1], row_start, n_rows, _ptr(dst))
+    if rc != 0:
+        raise ValueError("ring read rejected")
+    return dst
+
+
+def adapter_commit(enc_ring, aemb_ring, group_start, n_groups, w0_type, w0, w2_type, w2,
+                   down=4, n_threads=8):
+    """the adapter over ring groups; aemb_ring [capacity][dec_dim] updated in place"""
+    enc_ring = _f32a(enc_ring)
+    assert aemb_ring.dtype == np.float32 and aemb_ring.flags.c_contiguous
+    w0, w2 = _u8(w0), _u8(w2)
+    enc_dim, dec_dim = enc_ring.shape[1], aemb_ring.shape[1]
+    assert w0.size >= dec_dim * wrow_bytes(w0_type, enc_dim * down)
+    assert w2.size >= dec_dim * wrow_bytes(w2_type, dec_dim)
+    rc = lib.orc_adapter_commit(_ptr(enc_ring), enc_ring.shape[0], enc_dim, down, _ptr(aemb_ring),
+                                aemb_ring.shape[0], dec_dim, group_start, n_groups, w0_type,
+                                _ptr(w0), w2_type, _ptr(w2), n_threads)
+    if rc != n_groups:
+        raise ValueError("adapter commit rejected")

@@ -34,7 +34,8 @@ void orc_conv_dims(int32_t in_len, int32_t kernel, int32_t stride, int32_t *pad_
     *out_len = (in_len + padding_total + extra - kernel) / stride + 1;
 }
 
-static float gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)); }
+/* ggml_gelu_erf on f32 (ggml_vec_gelu_erf_f32): 0.5 x (1 + erff(x / sqrt 2)) */
+float orc_gelu_erf(float x) { return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f)); }
 
 void orc_conv1d(const float *in, int64_t stride_c, int64_t stride_t, int32_t in_len, int32_t n_ch,
                 const uint16_t *w, const float *b, int32_t n_out_ch, int32_t stride, int32_t pad,
@@ -52,7 +53,7 @@ void orc_conv1d(const float *in, int64_t stride_c, int64_t stride_t, int32_t in_
             float acc = 0.0f;
             for (int32_t j = 0; j < kk; ++j) acc += orc_f16_to_f32(wr[j]) * col[j];
             acc = acc + b[oc];
-            y[(int64_t)t * n_out_ch + oc] = gelu ? gelu_erf(acc) : acc;
+            y[(int64_t)t * n_out_ch + oc] = gelu ? orc_gelu_erf(acc) : acc;
         }
     }
     free(col);

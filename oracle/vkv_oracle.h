@@ -227,6 +227,19 @@ void orc_conv_stem(const float *mel, int32_t n_mel, int32_t conv_len, int32_t sl
                    int32_t n_new, const uint16_t *w0, const float *b0, const uint16_t *w1,
                    const float *b1, int32_t dim, float *x);
 
+/* ggml_gelu_erf of one f32 (conv.c) */
+float orc_gelu_erf(float x);
+
+/* ---- the realtime rows rings and the adapter (adapter.c) ---- */
+int32_t orc_row_ring_write(float *ring, int32_t capacity, int32_t width, int64_t row_start,
+                           const float *src, int32_t n_rows);
+int32_t orc_row_ring_read(const float *ring, int32_t capacity, int32_t width, int64_t row_start,
+                          int32_t n_rows, float *dst);
+int32_t orc_adapter_commit(const float *enc_ring, int32_t enc_cap, int32_t enc_dim, int32_t down,
+                           float *aemb_ring, int32_t aemb_cap, int32_t dec_dim,
+                           int64_t group_start, int32_t n_groups, int w0_type, const uint8_t *w0,
+                           int w2_type, const uint8_t *w2, int n_threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -52,6 +52,8 @@ def test_struct_layout_matches_c():
         "vkv_enc_model": (vkv.EncModel, None),
         "vkv_dec_layer": (vkv.DecLayer, None),
         "vkv_dec_model": (vkv.DecModel, None),
+        "vkv_row_ring": (vkv.RowRing, None),
+        "vkv_adapter": (vkv.Adapter, None),
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "vkv.h"', "int main(void){"]
     for cname, (py, _) in structs.items():
@@ -172,6 +174,35 @@ def test_error_statuses_without_device():
     assert L.vkv_decoder_layer_step(None, 0, None, 0, 0, 1, None, None, None, None, 32, 1.0,
                                     1e6, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_dequantize(vkv.Q4_K, 16, 255, 16, None) == vkv.INVALID_ARGUMENT
+    # the rows rings and the adapter: validation precedes any device work
+    enc = vkv.RowRing(4096, 256, 1280)
+    aemb = vkv.RowRing(4096, 256, 3072)
+    assert L.vkv_row_ring_write(ctypes.byref(enc), 0, 4096, 257, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_row_ring_write(ctypes.byref(enc), -1, 4096, 1, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_row_ring_read(ctypes.byref(enc), 0, 0, 4096, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_row_ring_read(ctypes.byref(vkv.RowRing(4100, 256, 1280)), 0, 1, 4096,
+                               None) == vkv.INVALID_ARGUMENT        # misaligned rows
+    ad = vkv.Adapter(16, 16, vkv.Q4_K, vkv.Q4_K, 1280, 3072, 4)
+    assert L.vkv_adapter_workspace(ctypes.byref(ad), 1) >= 3072 * 4
+    assert L.vkv_adapter_workspace(ctypes.byref(ad), 32) > L.vkv_matmul_workspace(32, 5120)
+    assert L.vkv_adapter_workspace(ctypes.byref(ad), 0) == 0
+    assert L.vkv_adapter_commit(ctypes.byref(ad), ctypes.byref(enc), ctypes.byref(aemb), 0, 1,
+                                4096, 16, None) == vkv.BUFFER_TOO_SMALL
+    assert L.vkv_adapter_commit(ctypes.byref(ad), ctypes.byref(enc), ctypes.byref(aemb), 0, 0,
+                                4096, 1 << 20, None) == vkv.INVALID_ARGUMENT
+    odd = vkv.RowRing(4096, 258, 1280)
+    assert L.vkv_adapter_commit(ctypes.byref(ad), ctypes.byref(odd), ctypes.byref(aemb), 0, 1,
+                                4096, 1 << 20, None) == vkv.INVALID_ARGUMENT
+    assert "multiple of 4" in vkv.last_error()
+    assert L.vkv_adapter_commit(ctypes.byref(ad), ctypes.byref(aemb), ctypes.byref(enc), 0, 1,
+                                4096, 1 << 20, None) == vkv.INVALID_ARGUMENT   # widths swapped
+    bad = vkv.Adapter(16, 16, vkv.Q8_0, vkv.Q4_K, 1280, 3072, 4)
+    assert L.vkv_adapter_workspace(ctypes.byref(bad), 1) == 0
+    assert L.vkv_encoder_chunk_ring(None, 0, None, 750, ctypes.byref(em), None, None, None, 0,
+                                    None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_matvec(x, 3072, None, None, 1e-5,
+                        (vkv.MvOut * 1)(vkv.MvOut(16, vkv.Q4_K, 8, 16, 16)), 1, vkv.MV_GELU,
+                        None) == vkv.INVALID_ARGUMENT           # GELU has no residual
     assert L.vkv_cache_destroy(None) == vkv.OK
     with pytest.raises(vkv.VkvError) as ei:
         vkv.decoder_plan(r, 5, 1)

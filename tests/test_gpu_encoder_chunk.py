@@ -209,3 +209,42 @@ def test_encoder_chunk(q_start, n_new):
     ca.close()
     cb.close()
     del keep, arr
+
+
+@pytest.mark.parametrize("q_start,n_new", [(1276, 16), (4, 4)])
+def test_encoder_chunk_into_the_output_ring(q_start, n_new):
+    """vkv_encoder_chunk_ring stores exactly vkv_encoder_chunk's output rows at
+    the 256-row encoder-output ring's logical rows q_start.. (across the wrap
+    for 1276: rows 252..255, 0..11) and leaves every other row alone"""
+    rng = np.random.default_rng(q_start)
+    n_layers = 1
+    m = make_model(rng, n_layers)
+    model, keep, arr = upload(m)
+    x0 = rng.standard_normal((n_new, DIM)).astype(np.float32)
+    ca, cb = filled_ring(n_layers, q_start), filled_ring(n_layers, q_start)
+    plan = vkv.enc_plan(q_start, n_new, CAP, WIN)
+    xa, xb = to_dev(x0), to_dev(x0)
+    ws_b = vkv.encoder_chunk_workspace(model, n_new)
+    ws = torch.empty(ws_b // 4 + 64, device=dev())
+    wsp = (ws.data_ptr() + 255) & ~255
+    ring_t = torch.full((256, DIM), np.nan, device=dev())
+    ring = vkv.RowRing(ring_t.data_ptr(), 256, DIM)
+    vkv.encoder_chunk(ca, 0, plan, WIN, model, xa.data_ptr(), wsp, ws_b, hip_stream=stream_ptr())
+    vkv.encoder_chunk_ring(cb, 0, plan, WIN, model, xb.data_ptr(), ring, wsp, ws_b,
+                           hip_stream=stream_ptr())
+    got, want = host(ring_t), host(xa)
+    slots = [(q_start + i) % 256 for i in range(n_new)]
+    assert np.array_equal(got[slots], want)
+    rest = np.ones(256, bool)
+    rest[slots] = False
+    assert np.isnan(got[rest]).all()
+    # x keeps the residual stream before the final norm
+    assert rel(np.stack([oracle.norm_act(r, m["out_norm"], eps=EPS, norm_b=m["out_norm_b"])
+                         for r in host(xb)]), want) <= 2e-6
+    with pytest.raises(vkv.VkvError):
+        vkv.encoder_chunk_ring(cb, 0, plan, WIN, model, xb.data_ptr(),
+                               vkv.RowRing(ring_t.data_ptr(), 256, 1024), wsp, ws_b,
+                               hip_stream=stream_ptr())
+    ca.close()
+    cb.close()
+    del keep, arr

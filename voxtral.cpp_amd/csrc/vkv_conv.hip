@@ -41,11 +41,6 @@ __global__ void __launch_bounds__(256) k_im2col_f16(const float *__restrict__ in
     cols[idx] = (_Float16)v;
 }
 
-__device__ __forceinline__ float gelu_erf(float x) {
-    // ggml_gelu_erf: 0.5 x (1 + erf(x / sqrt(2)))
-    return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
-}
-
 __global__ void __launch_bounds__(64 * kConvWaves) k_gemm_f16(const _Float16 *__restrict__ w,
                                                               const _Float16 *__restrict__ cols,
                                                               const float *__restrict__ bias,

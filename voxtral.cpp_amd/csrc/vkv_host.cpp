@@ -1026,9 +1026,9 @@ vkv_status matvec_impl(const float *x, int64_t n_in, const float *norm_w, const 
     if (!outs || n_outs < 1 || n_outs > VKV_MV_MAX_OUTS)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: n_outs=%d outside [1, %d]", n_outs,
                     VKV_MV_MAX_OUTS);
-    if (epilogue != VKV_MV_STORE && epilogue != VKV_MV_SWIGLU)
+    if (epilogue != VKV_MV_STORE && epilogue != VKV_MV_SWIGLU && epilogue != VKV_MV_GELU)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: unknown epilogue %d", epilogue);
-    const bool swiglu = epilogue == VKV_MV_SWIGLU;
+    const bool swiglu = epilogue == VKV_MV_SWIGLU, gelu = epilogue == VKV_MV_GELU;
     if (swiglu && (n_outs != 2 || outs[0].n_rows != outs[1].n_rows ||
                    outs[0].dtype != outs[1].dtype))
         return fail(VKV_STATUS_INVALID_ARGUMENT,
@@ -1044,8 +1044,8 @@ vkv_status matvec_impl(const float *x, int64_t n_in, const float *norm_w, const 
             return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: matrix %d exceeds 4 GiB", k);
         if (reinterpret_cast<uintptr_t>(o.w) & 3u)
             return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: weights must be 4-byte aligned");
-        if (swiglu && o.add)
-            return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: SwiGLU has no residual add");
+        if ((swiglu || gelu) && o.add)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matvec: SwiGLU and GELU have no residual add");
         total += o.n_rows;
     }
     if (swiglu) total = outs[0].n_rows;
@@ -1063,6 +1063,7 @@ vkv_status matvec_impl(const float *x, int64_t n_in, const float *norm_w, const 
     a.n_outs = n_outs;
     a.rows_per_wg = (int32_t)(4 * rpw);
     a.swiglu = swiglu ? 1 : 0;
+    a.gelu = gelu ? 1 : 0;
     int64_t wg = 0;
     for (int32_t k = 0; k < n_outs; ++k) {
         a.out[k] = MvOut{(const uint8_t *)outs[k].w, outs[k].y, outs[k].add, outs[k].dtype,
@@ -1111,6 +1112,17 @@ MmImage mm_image(int32_t n_cols, int64_t n_in, uint8_t *base) {
     im.bytes = off;
     return im;
 }
+
+// Where input / output row p of a product lives: row (row0 + p) % ring of a
+// ring buffer when ring > 0, else row p.
+struct RowMap {
+    int32_t ring = 0, row0 = 0;
+};
+
+vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float *norm_w,
+                       const float *norm_b, const float *ada, float eps, const vkv_mm_out *outs,
+                       int32_t n_outs, int32_t epilogue, void *workspace, size_t workspace_bytes,
+                       void *hip_stream, RowMap in_rows, RowMap out_rows);
 }  // namespace
 
 size_t vkv_matmul_workspace(int32_t n_cols, int64_t n_in) {
@@ -1122,6 +1134,15 @@ vkv_status vkv_matmul(const float *x, int32_t n_cols, int64_t n_in, const float 
                       const float *norm_b, const float *ada, float eps, const vkv_mm_out *outs,
                       int32_t n_outs, int32_t epilogue, void *workspace, size_t workspace_bytes,
                       void *hip_stream) {
+    return matmul_impl(x, n_cols, n_in, norm_w, norm_b, ada, eps, outs, n_outs, epilogue, workspace,
+                       workspace_bytes, hip_stream, RowMap{}, RowMap{});
+}
+
+namespace {
+vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float *norm_w,
+                       const float *norm_b, const float *ada, float eps, const vkv_mm_out *outs,
+                       int32_t n_outs, int32_t epilogue, void *workspace, size_t workspace_bytes,
+                       void *hip_stream, RowMap in_rows, RowMap out_rows) {
     if (vkv_status st = check_mv_input("matmul", x, n_in, norm_w, ada)) return st;
     if (norm_b && !norm_w) return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: norm_b requires norm_w");
     if (vkv_status st = check_aligned("matmul", {norm_b})) return st;
@@ -1130,9 +1151,9 @@ vkv_status vkv_matmul(const float *x, int32_t n_cols, int64_t n_in, const float 
     if (!outs || n_outs < 1 || n_outs > VKV_MV_MAX_OUTS)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: n_outs=%d outside [1, %d]", n_outs,
                     VKV_MV_MAX_OUTS);
-    if (epilogue != VKV_MV_STORE && epilogue != VKV_MV_SWIGLU)
+    if (epilogue != VKV_MV_STORE && epilogue != VKV_MV_SWIGLU && epilogue != VKV_MV_GELU)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: unknown epilogue %d", epilogue);
-    const bool swiglu = epilogue == VKV_MV_SWIGLU;
+    const bool swiglu = epilogue == VKV_MV_SWIGLU, gelu = epilogue == VKV_MV_GELU;
     if (swiglu && (n_outs != 2 || outs[0].n_rows != outs[1].n_rows || outs[0].dtype != outs[1].dtype))
         return fail(VKV_STATUS_INVALID_ARGUMENT,
                     "matmul: SwiGLU takes two matrices of equal rows and dtype");
@@ -1148,7 +1169,8 @@ vkv_status vkv_matmul(const float *x, int32_t n_cols, int64_t n_in, const float 
             return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: matrix %d exceeds 4 GiB", k);
         if (reinterpret_cast<uintptr_t>(o.w) & 3u)
             return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: weights must be 4-byte aligned");
-        if (swiglu && o.add) return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: SwiGLU has no residual add");
+        if ((swiglu || gelu) && o.add)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: SwiGLU and GELU have no residual add");
         a.out[k] = MmOut{(const uint8_t *)o.w, o.y, o.add, o.bias, o.dtype, o.n_rows, (int32_t)tiles};
         if (!swiglu || k == 0) tiles += (o.n_rows + 15) / 16;
     }
@@ -1161,8 +1183,8 @@ vkv_status vkv_matmul(const float *x, int32_t n_cols, int64_t n_in, const float 
     if (workspace_bytes < im.bytes)
         return fail(VKV_STATUS_BUFFER_TOO_SMALL, "matmul: workspace %zu < %zu bytes", workspace_bytes,
                     im.bytes);
-    hipError_t e = launch_q8k_rows(x, n_in, n_cols, (int)n_in, norm_w, norm_b, ada, eps, im.codes,
-                                   im.xd, im.bs32, as_stream(hip_stream));
+    hipError_t e = launch_q8k_rows(x, n_in, in_rows.ring, in_rows.row0, n_cols, (int)n_in, norm_w,
+                                   norm_b, ada, eps, im.codes, im.xd, im.bs32, as_stream(hip_stream));
     if (e != hipSuccess) return hip_fail(e, "matmul input launch");
     a.xq = im.codes;
     a.xd = im.xd;
@@ -1171,10 +1193,14 @@ vkv_status vkv_matmul(const float *x, int32_t n_cols, int64_t n_in, const float 
     a.n_cols = n_cols;
     a.n_outs = n_outs;
     a.swiglu = swiglu ? 1 : 0;
+    a.gelu = gelu ? 1 : 0;
+    a.y_ring = out_rows.ring;
+    a.y_row0 = out_rows.row0;
     e = launch_gemm_kq(a, (int)tiles, (n_cols + 15) / 16, as_stream(hip_stream));
     if (e != hipSuccess) return hip_fail(e, "matmul launch");
     return ok();
 }
+}  // namespace
 
 vkv_status vkv_quantize_q8_k(const float *x, int64_t n, const float *norm_w, const float *ada,
                              float eps, void *blocks, void *hip_stream) {
@@ -1501,9 +1527,21 @@ size_t vkv_encoder_chunk_workspace(const vkv_enc_model *model, int32_t n_new) {
     return enc_buffers(*model, model->n_heads * model->head_dim, n_new, nullptr).bytes;
 }
 
-vkv_status vkv_encoder_chunk(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
-                             int32_t window, const vkv_enc_model *model, float *x,
-                             void *workspace, size_t workspace_bytes, void *hip_stream) {
+namespace {
+vkv_status check_row_ring(const vkv_row_ring *r, const char *what) {
+    if (!r || !r->rows || r->capacity < 1 || r->width < 1)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: null ring or empty shape", what);
+    if ((int64_t)r->capacity * r->width > ((int64_t)1 << 40))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: ring too large", what);
+    return check_aligned(what, {r->rows});
+}
+
+// vkv_encoder_chunk; with out_ring the final norm's rows go to its logical
+// rows q_start.. instead of x
+vkv_status encoder_chunk_impl(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
+                              int32_t window, const vkv_enc_model *model, float *x,
+                              vkv_row_ring *out_ring, void *workspace, size_t workspace_bytes,
+                              void *hip_stream) {
     if (vkv_status st = check_enc_model(model)) return st;
     const vkv_enc_model &m = *model;
     if (vkv_status st = check_cache(cache, "encoder chunk")) return st;
@@ -1564,9 +1602,190 @@ vkv_status vkv_encoder_chunk(vkv_cache *cache, int32_t stream, const vkv_enc_pla
             return s;
     }
     if (vkv_status st = check_aligned("encoder chunk", {m.out_norm, m.out_norm_b})) return st;
-    hipError_t e = launch_rms_norm_rows(x, N, m.dim, m.out_norm, m.out_norm_b, m.norm_eps, x,
-                                        as_stream(hip_stream));
+    hipError_t e = out_ring ? launch_rms_norm_rows(x, N, m.dim, m.out_norm, m.out_norm_b, m.norm_eps,
+                                                   out_ring->rows, out_ring->capacity,
+                                                   (int)(plan->q_start % out_ring->capacity),
+                                                   as_stream(hip_stream))
+                            : launch_rms_norm_rows(x, N, m.dim, m.out_norm, m.out_norm_b, m.norm_eps,
+                                                   x, 0, 0, as_stream(hip_stream));
     if (e != hipSuccess) return hip_fail(e, "encoder chunk: final norm launch");
+    return ok();
+}
+}  // namespace
+
+vkv_status vkv_encoder_chunk(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
+                             int32_t window, const vkv_enc_model *model, float *x,
+                             void *workspace, size_t workspace_bytes, void *hip_stream) {
+    return encoder_chunk_impl(cache, stream, plan, window, model, x, nullptr, workspace,
+                              workspace_bytes, hip_stream);
+}
+
+vkv_status vkv_encoder_chunk_ring(vkv_cache *cache, int32_t stream, const vkv_enc_plan *plan,
+                                  int32_t window, const vkv_enc_model *model, float *x,
+                                  vkv_row_ring *enc_out, void *workspace, size_t workspace_bytes,
+                                  void *hip_stream) {
+    if (vkv_status st = check_row_ring(enc_out, "encoder chunk")) return st;
+    if (model && enc_out->width != model->dim)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "encoder chunk: ring width %d != dim %d",
+                    enc_out->width, model->dim);
+    if (plan && (plan->n_new > enc_out->capacity || plan->q_start < 0))
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "encoder chunk: %d new frames do not fit a ring of %d rows", plan->n_new,
+                    enc_out->capacity);
+    return encoder_chunk_impl(cache, stream, plan, window, model, x, enc_out, workspace,
+                              workspace_bytes, hip_stream);
+}
+
+// ---- the realtime rows rings and the adapter ----
+
+vkv_status vkv_row_ring_write(vkv_row_ring *ring, int64_t row_start, const float *src,
+                              int32_t n_rows, void *hip_stream) {
+    if (vkv_status st = check_row_ring(ring, "ring write")) return st;
+    if (!src || row_start < 0 || n_rows < 0 || n_rows > ring->capacity)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "ring write: rows [%lld, +%d) on a ring of %d",
+                    (long long)row_start, n_rows, ring->capacity);
+    const size_t rb = (size_t)ring->width * sizeof(float);
+    int32_t done = 0;
+    while (done < n_rows) {
+        const int32_t slot = (int32_t)((row_start + done) % ring->capacity);
+        const int32_t seg = std::min(n_rows - done, ring->capacity - slot);
+        hipError_t e = hipMemcpyAsync((uint8_t *)ring->rows + (size_t)slot * rb,
+                                      (const uint8_t *)src + (size_t)done * rb, (size_t)seg * rb,
+                                      hipMemcpyDefault, as_stream(hip_stream));
+        if (e != hipSuccess) return hip_fail(e, "ring write copy");
+        done += seg;
+    }
+    return ok();
+}
+
+vkv_status vkv_row_ring_read(const vkv_row_ring *ring, int64_t row_start, int32_t n_rows,
+                             float *dst, void *hip_stream) {
+    if (vkv_status st = check_row_ring(ring, "ring read")) return st;
+    if (!dst || row_start < 0 || n_rows < 1 || n_rows > ring->capacity)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "ring read: rows [%lld, +%d) on a ring of %d",
+                    (long long)row_start, n_rows, ring->capacity);
+    const size_t rb = (size_t)ring->width * sizeof(float);
+    int32_t done = 0;
+    while (done < n_rows) {
+        const int32_t slot = (int32_t)((row_start + done) % ring->capacity);
+        const int32_t seg = std::min(n_rows - done, ring->capacity - slot);
+        hipError_t e = hipMemcpyAsync((uint8_t *)dst + (size_t)done * rb,
+                                      (const uint8_t *)ring->rows + (size_t)slot * rb,
+                                      (size_t)seg * rb, hipMemcpyDefault, as_stream(hip_stream));
+        if (e != hipSuccess) return hip_fail(e, "ring read copy");
+        done += seg;
+    }
+    hipError_t e = hipStreamSynchronize(as_stream(hip_stream));
+    if (e != hipSuccess) return hip_fail(e, "ring read synchronize");
+    return ok();
+}
+
+namespace {
+// groups per product launch; longer commits run in pieces
+constexpr int32_t kAdapterRun = 256;
+
+struct AdapterBuffers {
+    float *hidden;     // gelu(W0 x) rows [run][dec_dim]
+    uint8_t *image;    // the Q8_K image of either product's input
+    size_t image_bytes, bytes;
+};
+
+AdapterBuffers adapter_buffers(const vkv_adapter &ad, int32_t run, uint8_t *base) {
+    AdapterBuffers t{};
+    size_t off = 0;
+    auto take = [&](size_t b) {
+        uint8_t *p = base ? base + off : nullptr;
+        off += (b + 255) & ~(size_t)255;
+        return p;
+    };
+    t.hidden = (float *)take((size_t)run * ad.dec_dim * 4);
+    t.image_bytes = run > 1 ? std::max(vkv_matmul_workspace(run, (int64_t)ad.enc_dim * ad.downsample),
+                                       vkv_matmul_workspace(run, ad.dec_dim))
+                            : 0;
+    t.image = t.image_bytes ? take(t.image_bytes) : nullptr;
+    t.bytes = off;
+    return t;
+}
+
+vkv_status check_adapter(const vkv_adapter *ad) {
+    if (!ad || !ad->w0 || !ad->w2)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "adapter: null weights");
+    const int64_t n_in = (int64_t)ad->enc_dim * ad->downsample;
+    if (ad->downsample < 1 || ad->enc_dim < 1 || n_in % 256 || n_in > VKV_MV_MAX_IN ||
+        ad->dec_dim < 256 || ad->dec_dim % 256 || ad->dec_dim > VKV_MV_MAX_IN)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "adapter: dimensions");
+    if (!kq_block_bytes(ad->w0_type) || !kq_block_bytes(ad->w2_type))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "adapter: weight dtypes %d / %d", ad->w0_type,
+                    ad->w2_type);
+    return VKV_STATUS_OK;
+}
+}  // namespace
+
+size_t vkv_adapter_workspace(const vkv_adapter *adapter, int32_t n_groups) {
+    if (check_adapter(adapter) || n_groups < 1) return 0;
+    return adapter_buffers(*adapter, std::min(n_groups, kAdapterRun), nullptr).bytes;
+}
+
+vkv_status vkv_adapter_commit(const vkv_adapter *adapter, const vkv_row_ring *enc_out,
+                              vkv_row_ring *audio_emb, int64_t group_start, int32_t n_groups,
+                              void *workspace, size_t workspace_bytes, void *hip_stream) {
+    if (vkv_status st = check_adapter(adapter)) return st;
+    const vkv_adapter &ad = *adapter;
+    if (vkv_status st = check_row_ring(enc_out, "adapter")) return st;
+    if (vkv_status st = check_row_ring(audio_emb, "adapter")) return st;
+    if (enc_out->width != ad.enc_dim || audio_emb->width != ad.dec_dim)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "adapter: ring widths %d / %d, model %d / %d",
+                    enc_out->width, audio_emb->width, ad.enc_dim, ad.dec_dim);
+    if (enc_out->capacity % ad.downsample)
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "adapter: encoder ring capacity %d is not a multiple of %d", enc_out->capacity,
+                    ad.downsample);
+    if (group_start < 0 || n_groups < 1)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "adapter: groups [%lld, +%d)",
+                    (long long)group_start, n_groups);
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "adapter: workspace null or not 256-byte aligned");
+    const int32_t run_max = std::min(n_groups, kAdapterRun);
+    const AdapterBuffers t = adapter_buffers(ad, run_max, (uint8_t *)workspace);
+    if (workspace_bytes < t.bytes)
+        return fail(VKV_STATUS_BUFFER_TOO_SMALL, "adapter: workspace %zu < %zu bytes",
+                    workspace_bytes, t.bytes);
+    // a group's frames are one contiguous row of enc_dim * downsample floats;
+    // the encoder ring holds capacity / downsample of them
+    const int32_t n_in = ad.enc_dim * ad.downsample, g_ring = enc_out->capacity / ad.downsample;
+    int32_t done = 0;
+    while (done < n_groups) {
+        // a run writes distinct rows of the audio ring, so no two of its
+        // groups race for one row (later groups win across runs)
+        const int32_t run = std::min({n_groups - done, kAdapterRun, audio_emb->capacity});
+        const int64_t g0 = group_start + done;
+        const int32_t in_row = (int32_t)(g0 % g_ring), out_row = (int32_t)(g0 % audio_emb->capacity);
+        if (run == 1) {
+            // one group: two single-row products, input quantization fused
+            const vkv_mv_out h[1] = {{ad.w0, ad.w0_type, ad.dec_dim, t.hidden, nullptr}};
+            if (vkv_status s = matvec_impl(enc_out->rows + (size_t)in_row * n_in, n_in, nullptr,
+                                           nullptr, 0.0f, h, 1, VKV_MV_GELU, hip_stream, nullptr,
+                                           nullptr))
+                return s;
+            const vkv_mv_out y[1] = {{ad.w2, ad.w2_type, ad.dec_dim,
+                                      audio_emb->rows + (size_t)out_row * ad.dec_dim, nullptr}};
+            if (vkv_status s = matvec_impl(t.hidden, ad.dec_dim, nullptr, nullptr, 0.0f, y, 1,
+                                           VKV_MV_STORE, hip_stream, nullptr, nullptr))
+                return s;
+        } else {
+            const vkv_mm_out h[1] = {{ad.w0, ad.w0_type, ad.dec_dim, t.hidden, nullptr, nullptr}};
+            if (vkv_status s = matmul_impl(enc_out->rows, run, n_in, nullptr, nullptr, nullptr, 0.0f,
+                                           h, 1, VKV_MV_GELU, t.image, t.image_bytes, hip_stream,
+                                           RowMap{g_ring, in_row}, RowMap{}))
+                return s;
+            const vkv_mm_out y[1] = {{ad.w2, ad.w2_type, ad.dec_dim, audio_emb->rows, nullptr, nullptr}};
+            if (vkv_status s = matmul_impl(t.hidden, run, ad.dec_dim, nullptr, nullptr, nullptr, 0.0f,
+                                           y, 1, VKV_MV_STORE, t.image, t.image_bytes, hip_stream,
+                                           RowMap{}, RowMap{audio_emb->capacity, out_row}))
+                return s;
+        }
+        done += run;
+    }
     return ok();
 }
 

@@ -10,6 +10,11 @@
 
 namespace vkv {
 
+// ggml_gelu_erf as the CPU path computes it: 0.5 x (1 + erf(x / sqrt(2)))
+__device__ __forceinline__ float gelu_erf(float x) {
+    return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
 constexpr int kMaxStreams = VKV_MAX_BATCH_STREAMS;
 
 // Logical window of one stream: logical index i maps to physical slot
@@ -119,6 +124,7 @@ struct MvArgs {
     int32_t n_in, n_outs;
     int32_t rows_per_wg;   // multiple of 4 (one contiguous quarter per wave)
     int32_t swiglu;        // out[0].y = silu(W0 x) * (W1 x), rows paired
+    int32_t gelu;          // every y = gelu_erf(W x) (no residual)
     MvOut out[kMvMaxOuts];
     // Fused argmax of out[0].y (one matrix, no SwiGLU): each work group
     // atomically maxes its best (order key of the value, row) into *amax;
@@ -146,12 +152,18 @@ struct MmArgs {
     const float *xd;       // block scales [n_cols][n_in / 256]
     const int32_t *xbs;    // 32-element sums [n_cols][n_in / 32]
     int32_t n_in, n_cols, n_outs, swiglu;
+    int32_t gelu;          // y = gelu_erf(W h + bias) (no residual)
+    // Input row p's output (and residual) row: (y_row0 + p) % y_ring when
+    // y_ring > 0 (rows of a ring buffer), else p.
+    int32_t y_ring, y_row0;
     MmOut out[kMvMaxOuts];
 };
 
-hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int n_rows, int n, const float *norm_w,
-                           const float *norm_b, const float *ada, float eps, int8_t *codes,
-                           float *xd, int32_t *bs32, hipStream_t st);
+// Input row p is read at x + ((x_row0 + p) % x_ring) * x_stride when
+// x_ring > 0 (rows of a ring buffer), else at x + p * x_stride.
+hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_row0, int n_rows,
+                           int n, const float *norm_w, const float *norm_b, const float *ada,
+                           float eps, int8_t *codes, float *xd, int32_t *bs32, hipStream_t st);
 hipError_t launch_gemm_kq(const MmArgs &a, int n_tiles, int n_col_tiles, hipStream_t st);
 hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const float *ada, float eps,
                             uint8_t *out, hipStream_t st);
@@ -164,8 +176,10 @@ hipError_t launch_im2col_f16(const float *in, int64_t stride_c, int64_t stride_t
                              hipStream_t st);
 hipError_t launch_gemm_f16(const void *w, const void *cols, const float *bias, float *y, int M,
                            int N, int K, bool gelu, hipStream_t st);
+// Row p's output goes to y + ((y_row0 + p) % y_ring) * n when y_ring > 0,
+// else y + p * n.
 hipError_t launch_rms_norm_rows(const float *x, int n_rows, int n, const float *w, const float *b,
-                                float eps, float *y, hipStream_t st);
+                                float eps, float *y, int y_ring, int y_row0, hipStream_t st);
 
 hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st);
 hipError_t launch_gather(const uint8_t *src, int64_t row_bytes, SegPair seg, uint8_t *dst,

@@ -523,7 +523,7 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
                 const float r = wave_sum(acc);
                 acc = 0.0f;
                 if (!swiglu) {
-                    const float yv = o0.add ? o0.add[row] + r : r;
+                    const float yv = a.gelu ? gelu_erf(r) : o0.add ? o0.add[row] + r : r;
                     if (lane == 0) o0.y[row] = yv;
                     if constexpr (AMAX) {
                         const uint32_t b = __builtin_bit_cast(uint32_t, yv);
@@ -625,11 +625,12 @@ __global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__
 __global__ void __launch_bounds__(256) k_rms_norm_rows(const float *__restrict__ x, int n,
                                                        const float *__restrict__ w,
                                                        const float *__restrict__ b, float eps,
-                                                       float *__restrict__ y) {
+                                                       float *y, int y_ring, int y_row0) {
 #pragma clang fp contract(off)
     __shared__ double red[4];
-    const float *xr = x + (int64_t)blockIdx.x * n;
-    float *yr = y + (int64_t)blockIdx.x * n;
+    const int p = blockIdx.x;
+    const float *xr = x + (int64_t)p * n;
+    float *yr = y + (int64_t)(y_ring > 0 ? (y_row0 + p) % y_ring : p) * n;
     double s = 0.0;
     for (int i = threadIdx.x; i < n; i += 256) s += (double)(xr[i] * xr[i]);
     s = wave_sum_d(s);
@@ -709,14 +710,15 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, in
 //                 k window zeroed).
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, int64_t x_stride,
-                                                  int n, const float *nw, const float *nbias,
-                                                  const float *ada, float eps,
+                                                  int x_ring, int x_row0, int n, const float *nw,
+                                                  const float *nbias, const float *ada, float eps,
                                                   int8_t *__restrict__ codes, float *__restrict__ xd,
                                                   int32_t *__restrict__ bs32) {
     __shared__ ActSmem sm;
     const int p = blockIdx.x;
+    const int src = x_ring > 0 ? (x_row0 + p) % x_ring : p;
     ActRegs<kMvMaxIn / 1024, false> r;
-    act_load(r, x + (int64_t)p * x_stride, n, nw, ada);
+    act_load(r, x + (int64_t)src * x_stride, n, nw, ada);
     act_finish(r, n, nw, ada, eps, sm, nullptr, nbias);
     int4 *dst = reinterpret_cast<int4 *>(codes + (int64_t)p * n);
     for (int i = threadIdx.x; i < n / 16; i += 256) dst[i] = reinterpret_cast<const int4 *>(sm.xq)[i];
@@ -965,15 +967,19 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
             float v0 = 0.0f, v1 = 0.0f;
             for (int w = 0; w < kw; ++w) v0 += red[0][w][r][c];
             if (o0.bias) v0 = v0 + o0.bias[orow];
+            const int64_t at =
+                (int64_t)(a.y_ring > 0 ? (a.y_row0 + ocol) % a.y_ring : ocol) * o0.n_rows + orow;
             float y;
             if (swiglu) {
                 for (int w = 0; w < kw; ++w) v1 += red[1][w][r][c];
                 if (o1.bias) v1 = v1 + o1.bias[orow];
                 y = silu(v0) * v1;
+            } else if (a.gelu) {
+                y = gelu_erf(v0);
             } else {
-                y = o0.add ? o0.add[(int64_t)ocol * o0.n_rows + orow] + v0 : v0;
+                y = o0.add ? o0.add[at] + v0 : v0;
             }
-            o0.y[(int64_t)ocol * o0.n_rows + orow] = y;
+            o0.y[at] = y;
         }
     }
 }
@@ -1019,10 +1025,11 @@ hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const flo
     return hipGetLastError();
 }
 
-hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int n_rows, int n, const float *norm_w,
-                           const float *norm_b, const float *ada, float eps, int8_t *codes,
-                           float *xd, int32_t *bs32, hipStream_t st) {
-    k_q8k_rows<<<n_rows, 256, 0, st>>>(x, x_stride, n, norm_w, norm_b, ada, eps, codes, xd, bs32);
+hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_row0, int n_rows,
+                           int n, const float *norm_w, const float *norm_b, const float *ada,
+                           float eps, int8_t *codes, float *xd, int32_t *bs32, hipStream_t st) {
+    k_q8k_rows<<<n_rows, 256, 0, st>>>(x, x_stride, x_ring, x_row0, n, norm_w, norm_b, ada, eps,
+                                       codes, xd, bs32);
     return hipGetLastError();
 }
 
@@ -1033,8 +1040,8 @@ hipError_t launch_gemm_kq(const MmArgs &a, int n_tiles, int n_col_tiles, hipStre
 }
 
 hipError_t launch_rms_norm_rows(const float *x, int n_rows, int n, const float *w, const float *b,
-                                float eps, float *y, hipStream_t st) {
-    k_rms_norm_rows<<<n_rows, 256, 0, st>>>(x, n, w, b, eps, y);
+                                float eps, float *y, int y_ring, int y_row0, hipStream_t st) {
+    k_rms_norm_rows<<<n_rows, 256, 0, st>>>(x, n, w, b, eps, y, y_ring, y_row0);
     return hipGetLastError();
 }
 

@@ -48,7 +48,7 @@ MAX_BATCH_STREAMS = 32
 KQ_BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_K: 292}
 MV_MAX_IN = 12288
 MV_MAX_OUTS = 4
-MV_STORE, MV_SWIGLU = 0, 1
+MV_STORE, MV_SWIGLU, MV_GELU = 0, 1, 2
 
 
 def row_bytes(dtype, n):
@@ -167,6 +167,16 @@ class DecModel(ctypes.Structure):
                 ("out_norm", _vp), ("output", _vp), ("output_type", _i32),
                 ("layers", _P(DecLayer))]
 
+
+class RowRing(ctypes.Structure):
+    _fields_ = [("rows", _vp), ("capacity", _i32), ("width", _i32)]
+
+
+class Adapter(ctypes.Structure):
+    _fields_ = [("w0", _vp), ("w2", _vp), ("w0_type", _i32), ("w2_type", _i32),
+                ("enc_dim", _i32), ("dec_dim", _i32), ("downsample", _i32)]
+
+
 # prototypes: name -> (restype, argtypes); exactly the functions of include/vkv.h
 PROTOTYPES = {
     "vkv_decoder_plan": (_i32, [_P(Ring), _i64, _i32, _P(Plan)]),
@@ -210,6 +220,13 @@ PROTOTYPES = {
                                  ctypes.c_size_t, _vp]),
     "vkv_matmul": (_i32, [_vp, _i32, _i64, _vp, _vp, _vp, _f32, _P(MmOut), _i32, _i32, _vp,
                           ctypes.c_size_t, _vp]),
+    "vkv_encoder_chunk_ring": (_i32, [_vp, _i32, _P(EncPlan), _i32, _P(EncModel), _vp,
+                                      _P(RowRing), _vp, ctypes.c_size_t, _vp]),
+    "vkv_row_ring_write": (_i32, [_P(RowRing), _i64, _vp, _i32, _vp]),
+    "vkv_row_ring_read": (_i32, [_P(RowRing), _i64, _i32, _vp, _vp]),
+    "vkv_adapter_workspace": (ctypes.c_size_t, [_P(Adapter), _i32]),
+    "vkv_adapter_commit": (_i32, [_P(Adapter), _P(RowRing), _P(RowRing), _i64, _i32, _vp,
+                                  ctypes.c_size_t, _vp]),
     "vkv_quantize_q8_k": (_i32, [_vp, _i64, _vp, _vp, _f32, _vp, _vp]),
     "vkv_dequantize": (_i32, [_i32, _vp, _i64, _vp, _vp]),
     "vkv_decoder_layer_step": (_i32, [_vp, _i32, _P(Plan), _i64, _i32, _i32, _vp, _vp, _vp, _vp,
@@ -463,6 +480,32 @@ def encoder_chunk_workspace(model, n_new):
 def encoder_chunk(cache, stream, plan, window, model, x_ptr, ws_ptr, ws_bytes, hip_stream=0):
     check(lib.vkv_encoder_chunk(cache.handle, stream, ctypes.byref(plan), window,
                                 ctypes.byref(model), x_ptr, ws_ptr, ws_bytes, hip_stream))
+
+
+def encoder_chunk_ring(cache, stream, plan, window, model, x_ptr, enc_out, ws_ptr, ws_bytes,
+                       hip_stream=0):
+    check(lib.vkv_encoder_chunk_ring(cache.handle, stream, ctypes.byref(plan), window,
+                                     ctypes.byref(model), x_ptr, ctypes.byref(enc_out), ws_ptr,
+                                     ws_bytes, hip_stream))
+
+
+def row_ring_write(ring, row_start, src_ptr, n_rows, hip_stream=0):
+    check(lib.vkv_row_ring_write(ctypes.byref(ring), row_start, src_ptr, n_rows, hip_stream))
+
+
+def row_ring_read(ring, row_start, n_rows, dst_ptr, hip_stream=0):
+    check(lib.vkv_row_ring_read(ctypes.byref(ring), row_start, n_rows, dst_ptr, hip_stream))
+
+
+def adapter_workspace(adapter, n_groups):
+    return lib.vkv_adapter_workspace(ctypes.byref(adapter), n_groups)
+
+
+def adapter_commit(adapter, enc_out, audio_emb, group_start, n_groups, ws_ptr, ws_bytes,
+                   hip_stream=0):
+    check(lib.vkv_adapter_commit(ctypes.byref(adapter), ctypes.byref(enc_out),
+                                 ctypes.byref(audio_emb), group_start, n_groups, ws_ptr, ws_bytes,
+                                 hip_stream))
 
 
 def matmul_workspace(n_cols, n_in):
