@@ -37,6 +37,13 @@ Other workloads (--workload), reported on the same contract:
                RoPE, ring append + window-750 attention, O + bias + residual,
                RMSNorm + SwiGLU, W2 + bias + residual) + final norm, on Q4_K_M
                weights (539 MB per chunk), steady state; frames/s.
+  adapter_q4km / adapter_group_q4km  the adapter over the rows rings: 32
+               groups (the startup commit) or one group (the steady 80 ms
+               commit); audio embeddings/s.
+  model_load_q4km  a full-size realtime Q4_K_M GGUF file (the reference's
+               tensor names, dims and quantization mix; synthetic bytes)
+               written to $TMPDIR once, then vkv_model_load into one device
+               allocation per step (file in the page cache); GB/s.
   decoder_token_q4km  one whole decoder token through vkv_decoder_token:
                embedding + audio row, 26 x (RMSNorm+QKV, RoPE + K/V append +
                attention over the full 8192-slot F16 ring, O + residual,
@@ -94,6 +101,10 @@ WORKLOADS = {
                                streams=1, pmc="", groups=1,
                                data="synthetic (random valid Q4_K blocks, N(0,1) encoder "
                                     "frames, generated on device)"),
+    "model_load_q4km": dict(dtype=12, dtype_name="bytes (q4_k/q6_k/f16/f32 tensors copied verbatim)",
+                            streams=1, pmc="",
+                            data="synthetic (a full-size realtime Q4_K_M GGUF file of random "
+                                 "bytes, written to local disk before timing)"),
     "decoder_weights_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k (int8 dot)", streams=1,
                                  pmc="matvec_q4km_26l_pmc.json",
                                  data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs, "
@@ -252,6 +263,166 @@ def cpu_adapter_leg(n_groups, target_seconds):
     return {"value": groups / secs, "unit": "audio embeddings/s", "cores": threads, "kind": "port",
             "sample": f"{groups} adapter groups (4 x 1280 -> 3072 -> 3072, Q4_K) of the oracle's "
                       f"restatement of ggml's CPU path, {threads} threads, {secs:.1f} s"}
+
+
+def realtime_tensor_list():
+    """(name, ggml type, ne) of the realtime model in the Q4_K_M mix
+    (src/voxtral.cpp:1193-1265 names, src/voxtral-quantize.cpp:148-159 types)"""
+    q4, q6 = 12, 14
+    T = [("enc.conv0.weight", 1, [3, 128, 1280]), ("enc.conv0.bias", 0, [1280]),
+         ("enc.conv1.weight", 1, [3, 1280, 1280]), ("enc.conv1.bias", 0, [1280])]
+    for i in range(E_LAYERS):
+        p = f"enc.blk.{i}."
+        T += [(p + "attn_norm.weight", 0, [1280]), (p + "attn_q.weight", q4, [1280, 2048]),
+              (p + "attn_q.bias", 0, [2048]), (p + "attn_k.weight", q4, [1280, 2048]),
+              (p + "attn_v.weight", q6, [1280, 2048]), (p + "attn_v.bias", 0, [2048]),
+              (p + "attn_o.weight", q4, [2048, 1280]), (p + "attn_o.bias", 0, [1280]),
+              (p + "ffn_norm.weight", 0, [1280]), (p + "ffn_w1.weight", q4, [1280, 5120]),
+              (p + "ffn_w2.weight", q6, [5120, 1280]), (p + "ffn_w2.bias", 0, [1280]),
+              (p + "ffn_w3.weight", q4, [1280, 5120])]
+    T += [("enc.norm.weight", 0, [1280]), ("adapter.0.weight", q4, [5120, DIM]),
+          ("adapter.2.weight", q4, [DIM, DIM]), ("tok_embeddings.weight", q6, [DIM, VOCAB]),
+          ("norm.weight", 0, [DIM])]
+    for i in range(LAYERS):
+        p = f"dec.blk.{i}."
+        T += [(p + "attn_norm.weight", 0, [DIM]), (p + "attn_q.weight", q4, [DIM, Q_DIM]),
+              (p + "attn_k.weight", q4, [DIM, KV_DIM]), (p + "attn_v.weight", q6, [DIM, KV_DIM]),
+              (p + "attn_o.weight", q4, [Q_DIM, DIM]), (p + "ffn_norm.weight", 0, [DIM]),
+              (p + "ffn_w1.weight", q4, [DIM, HIDDEN]), (p + "ffn_w2.weight", q6, [HIDDEN, DIM]),
+              (p + "ffn_w3.weight", q4, [DIM, HIDDEN]), (p + "ada0.weight", q4, [DIM, 32]),
+              (p + "ada2.weight", 1, [32, DIM])]
+    T.append(("audio.mel_filters", 0, [201, 128]))
+    return T
+
+
+def write_synthetic_gguf(path):
+    """the realtime model's GGUF layout with random bytes, streamed (GGUF v3,
+    32-byte alignment); returns the data-section bytes"""
+    import struct
+
+    import numpy as np
+
+    blk = {0: (1, 4), 1: (1, 2), 12: (256, 144), 14: (256, 210)}
+    T = realtime_tensor_list()
+
+    def sz(t, ne):
+        n = 1
+        for d in ne:
+            n *= d
+        return n // blk[t][0] * blk[t][1]
+
+    def s(b):
+        return struct.pack("<Q", len(b)) + b
+
+    kvs = [(b"general.architecture", 8, s(b"voxtral_realtime")),
+           (b"voxtral.vocab_size", 5, struct.pack("<i", VOCAB))]
+    head = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(T), len(kvs)))
+    for k, t, v in kvs:
+        head += s(k) + struct.pack("<I", t) + v
+    off, offs = 0, []
+    for name, t, ne in T:
+        offs.append(off)
+        off += (sz(t, ne) + 31) // 32 * 32
+    for (name, t, ne), o in zip(T, offs):
+        head += s(name.encode()) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<Q", d) for d in ne)
+        head += struct.pack("<IQ", t, o)
+    head += b"\0" * ((-len(head)) % 32)
+    pool = np.random.default_rng(SEED).integers(0, 256, 64 << 20, dtype=np.uint8).tobytes()
+    with open(path, "wb") as f:
+        f.write(head)
+        written = 0
+        while written < off:
+            n = min(len(pool), off - written)
+            f.write(pool[:n])
+            written += n
+    return off
+
+
+def gpu_model_load(steps, warmup):
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    tmp = os.environ.get("TMPDIR", "/tmp")
+    path = os.path.join(tmp, f"vkv_bench_realtime_q4km_{os.getpid()}.gguf")
+    try:
+        data_bytes = write_synthetic_gguf(path)
+        torch.cuda.synchronize()
+        for _ in range(warmup):
+            vkv.Model(path, hip_stream=st.cuda_stream).close()
+        times = []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            a = time.perf_counter()
+            m = vkv.Model(path, hip_stream=st.cuda_stream)
+            times.append(time.perf_counter() - a)
+            m.close()
+        wall = time.perf_counter() - t0
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+    return sum(times) * 1e3, [t * 1e3 for t in times], wall, data_bytes
+
+
+def cpu_load_leg(target_seconds):
+    """The reference's weight upload on the CPU backend (src/voxtral.cpp:
+    1160-1190): per tensor, seek + read into a staging vector + copy into the
+    weight buffer, on a bounded prefix of the same synthetic file."""
+    import numpy as np
+
+    tmp = os.environ.get("TMPDIR", "/tmp")
+    path = os.path.join(tmp, f"vkv_bench_cpu_load_{os.getpid()}.gguf")
+    try:
+        write_synthetic_gguf(path)
+        import struct
+        T = realtime_tensor_list()
+        blk = {0: (1, 4), 1: (1, 2), 12: (256, 144), 14: (256, 210)}
+        sizes = []
+        for name, t, ne in T:
+            n = 1
+            for d in ne:
+                n *= d
+            sizes.append(n // blk[t][0] * blk[t][1])
+        with open(path, "rb") as f:
+            head = f.read(1 << 20)
+        # data offset: end of the tensor infos, aligned (the writer pads to 32)
+        pos = 24
+        for _ in range(2):
+            n = struct.unpack_from("<Q", head, pos)[0]
+            pos += 8 + n
+            t = struct.unpack_from("<I", head, pos)[0]
+            pos += 4
+            pos += 8 + struct.unpack_from("<Q", head, pos)[0] if t == 8 else 4
+        offs = []
+        for _ in T:
+            n = struct.unpack_from("<Q", head, pos)[0]
+            pos += 8 + n
+            nd = struct.unpack_from("<I", head, pos)[0]
+            pos += 4 + 8 * nd + 4
+            offs.append(struct.unpack_from("<Q", head, pos)[0])
+            pos += 8
+        data0 = (pos + 31) // 32 * 32
+        weights = np.empty(sum(sizes), np.uint8)
+        moved, dst = 0, 0
+        t0 = time.perf_counter()
+        with open(path, "rb", buffering=0) as f:
+            for o, n in zip(offs, sizes):
+                f.seek(data0 + o)
+                tmpv = bytearray(n)
+                f.readinto(tmpv)
+                weights[dst:dst + n] = np.frombuffer(tmpv, np.uint8)
+                dst += n
+                moved += n
+                if time.perf_counter() - t0 > target_seconds:
+                    break
+        secs = time.perf_counter() - t0
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+    return {"value": moved / secs / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{moved / 1e9:.2f} GB of the same file (page cache) read tensor by tensor "
+                      f"into a staging buffer and copied into host weight memory, as the "
+                      f"reference's CPU-backend load does, 1 thread, {secs:.1f} s"}
 
 
 def encoder_chunk_bytes(n_keys):
@@ -773,6 +944,19 @@ def main():
                   "groups_per_commit": ng, "bytes_per_commit": bytes_step}
         kernel = ("k_q8k_rows + k_gemm_kq (GELU) + k_q8k_rows + k_gemm_kq" if ng > 1 else
                   "k_matvec (GELU) + k_matvec")
+    elif args.workload == "model_load_q4km":
+        args.steps, args.warmup = min(args.steps, 5), min(args.warmup, 1)
+        total_ms, step_ms, wall, data_bytes = gpu_model_load(args.steps, args.warmup)
+        bytes_step = data_bytes
+        units_per_step = data_bytes / 1e9
+        res = {"metric": "GGUF model load GB/s (file in the page cache -> one device allocation)",
+               "unit": "GB/s"}
+        config = {"workload": "vkv_model_load of a full-size realtime Q4_K_M GGUF (32 encoder "
+                              "layers, 26 decoder layers, 131072-row Q6_K embeddings, adapter, "
+                              "conv stem, ada weights, mel filters; "
+                              f"{len(realtime_tensor_list())} tensors)",
+                  "bytes_per_load": data_bytes, "staging": "3 x 64 MiB pinned buffers"}
+        kernel = "hipMemcpyAsync host-to-device copies (no kernels)"
     elif args.workload == "decoder_token_q4km":
         total_ms, step_ms, wall = gpu_token(args.steps, args.warmup)
         bytes_step = token_bytes()
@@ -826,6 +1010,9 @@ def main():
                   "head_dim": HD, "streams": ns}
         fmt = "FmtF16" if wl["dtype"] == 1 else "FmtQ8"
         kernel = f"k_decode<{fmt}> (append fused; one pass per (stream, layer, kv head))"
+    # the load is bound by the host link, not HBM: PCIe 5.0 x16, 64 GB/s per direction
+    bound, peak = ("host link (PCIe 5.0 x16)", 64.0) if args.workload == "model_load_q4km" else \
+        ("hbm", HBM_PEAK_GBPS)
     ms_per_step = total_ms / args.steps
     step_avg = sum(step_ms) / len(step_ms)
     achieved = bytes_step / (step_avg * 1e-3) / 1e9
@@ -844,8 +1031,8 @@ def main():
         "config": config,
         "hbm_gbps": round(bytes_step / (ms_per_step * 1e-3) / 1e9, 1),
         "pct_hbm_peak": round(100 * bytes_step / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBPS, 2),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "roofline": {"bound": bound, "achieved": round(achieved, 1), "peak": peak,
+                     "unit": "GB/s", "frac": round(achieved / peak, 4),
                      "traffic": round(traffic) if traffic else None,
                      "kernel": kernel,
                      "bytes_per_launch": bytes_step,
@@ -858,8 +1045,11 @@ def main():
         res["cpu_baseline"] = cpu_token_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload in ("adapter_q4km", "adapter_group_q4km"):
         res["cpu_baseline"] = cpu_adapter_leg(wl["groups"], args.cpu_seconds)
+    elif not args.no_cpu and args.workload == "model_load_q4km":
+        res["cpu_baseline"] = cpu_load_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload not in ("encoder_f16", "encoder_chunk_q4km",
-                                                   "adapter_q4km", "adapter_group_q4km"):
+                                                   "adapter_q4km", "adapter_group_q4km",
+                                                   "model_load_q4km"):
         res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds)
     print(json.dumps(res), flush=True)
 

@@ -47,6 +47,7 @@ typedef enum vkv_status {
     VKV_STATUS_INVALID_ARGUMENT = 1,
     VKV_STATUS_INVALID_STATE = 2,
     VKV_STATUS_OUT_OF_MEMORY = 3,
+    VKV_STATUS_MODEL_ERROR = 8,
     VKV_STATUS_BACKEND_ERROR = 9,
     VKV_STATUS_INTERNAL_ERROR = 10,
     VKV_STATUS_BUFFER_TOO_SMALL = 11
@@ -573,6 +574,122 @@ vkv_status vkv_decoder_token(vkv_cache *cache, int32_t stream, vkv_ring *ring,
                              const vkv_dec_model *model, int32_t token, const float *audio_emb,
                              float *logits, int32_t *token_out, void *workspace,
                              size_t workspace_bytes, vkv_plan *plan_out, void *hip_stream);
+
+/* ---------------------------------------------------------------------------
+ * GGUF model files (voxtral_model_load_from_file, src/voxtral.cpp:1035-1316,
+ * over ggml's gguf reader; the files tools/convert_voxtral_to_gguf.py and
+ * src/voxtral-quantize.cpp write).  GGUF v2/v3: magic "GGUF", version,
+ * tensor and key counts, typed key/value metadata, tensor infos (name, dims
+ * ne[] fastest first, ggml type, offset), then the data section at the
+ * file's alignment (general.alignment, default 32) with every tensor at its
+ * packed, aligned offset.  Files are mapped read-only; strings returned stay
+ * valid until vkv_gguf_close.  Reading metadata needs no GPU.
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_gguf vkv_gguf;
+
+/* GGUF value types (the file's type codes) */
+#define VKV_GGUF_UINT8 0
+#define VKV_GGUF_INT8 1
+#define VKV_GGUF_UINT16 2
+#define VKV_GGUF_INT16 3
+#define VKV_GGUF_UINT32 4
+#define VKV_GGUF_INT32 5
+#define VKV_GGUF_FLOAT32 6
+#define VKV_GGUF_BOOL 7
+#define VKV_GGUF_STRING 8
+#define VKV_GGUF_ARRAY 9
+#define VKV_GGUF_UINT64 10
+#define VKV_GGUF_INT64 11
+#define VKV_GGUF_FLOAT64 12
+
+typedef struct vkv_gguf_tensor {
+    const char *name;
+    int32_t type;          /* ggml_type */
+    int32_t n_dims;
+    int64_t ne[4];         /* elements per dimension, ne[0] fastest; 1 past n_dims */
+    uint64_t offset;       /* from the start of the data section */
+    uint64_t nbytes;
+} vkv_gguf_tensor;
+
+/* MODEL_ERROR for a missing, truncated or malformed file (the message says
+ * what was wrong); *out is NULL then. */
+vkv_status vkv_gguf_open(const char *path, vkv_gguf **out);
+vkv_status vkv_gguf_close(vkv_gguf *gguf);
+uint32_t vkv_gguf_version(const vkv_gguf *gguf);
+uint64_t vkv_gguf_alignment(const vkv_gguf *gguf);
+uint64_t vkv_gguf_data_offset(const vkv_gguf *gguf);   /* file offset of the data section */
+int64_t vkv_gguf_n_kv(const vkv_gguf *gguf);
+int64_t vkv_gguf_find_key(const vkv_gguf *gguf, const char *key);   /* -1 when absent */
+const char *vkv_gguf_key(const vkv_gguf *gguf, int64_t i);         /* NULL out of range */
+int32_t vkv_gguf_kv_type(const vkv_gguf *gguf, int64_t i);         /* -1 out of range */
+/* Scalar values; INVALID_ARGUMENT when the key's type differs (ggml's
+ * gguf_get_val_* assert it).  bool reads as 0/1. */
+vkv_status vkv_gguf_get_i32(const vkv_gguf *gguf, int64_t i, int32_t *out);
+vkv_status vkv_gguf_get_u32(const vkv_gguf *gguf, int64_t i, uint32_t *out);
+vkv_status vkv_gguf_get_i64(const vkv_gguf *gguf, int64_t i, int64_t *out);
+vkv_status vkv_gguf_get_f32(const vkv_gguf *gguf, int64_t i, float *out);
+vkv_status vkv_gguf_get_f64(const vkv_gguf *gguf, int64_t i, double *out);
+vkv_status vkv_gguf_get_bool(const vkv_gguf *gguf, int64_t i, int32_t *out);
+/* any scalar value's bytes (1, 2, 4 or 8 by its type), little-endian */
+vkv_status vkv_gguf_get_scalar(const vkv_gguf *gguf, int64_t i, void *out, uint64_t out_bytes);
+/* NUL-terminated copy of a string value (len excludes the NUL) */
+vkv_status vkv_gguf_get_str(const vkv_gguf *gguf, int64_t i, const char **out, uint64_t *len);
+/* Arrays: element type and count; data points at the elements in the file
+ * (NULL for string arrays, read with vkv_gguf_get_arr_str). */
+vkv_status vkv_gguf_get_arr(const vkv_gguf *gguf, int64_t i, int32_t *elem_type, uint64_t *n,
+                            const void **data);
+vkv_status vkv_gguf_get_arr_str(const vkv_gguf *gguf, int64_t i, uint64_t j, const char **out,
+                                uint64_t *len);
+int64_t vkv_gguf_n_tensors(const vkv_gguf *gguf);
+int64_t vkv_gguf_find_tensor(const vkv_gguf *gguf, const char *name);   /* -1 when absent */
+vkv_status vkv_gguf_tensor_info(const vkv_gguf *gguf, int64_t i, vkv_gguf_tensor *out);
+/* the tensor's bytes in the mapped file */
+const void *vkv_gguf_tensor_data(const vkv_gguf *gguf, int64_t i);
+
+/* The model's hyperparameters as the reference populates them from the
+ * metadata (src/voxtral.cpp:1066-1113): each key overrides the default of
+ * include/voxtral.h when present; is_offline = (general.architecture ==
+ * "voxtral"); encoder causality and ada conditioning default to !is_offline. */
+typedef struct vkv_hparams {
+    int32_t is_offline;
+    int32_t enc_dim, enc_layers, enc_heads, enc_head_dim, enc_hidden, enc_kv_heads, enc_causal;
+    float enc_norm_eps, enc_rope_theta;
+    int32_t dec_dim, dec_layers, dec_heads, dec_head_dim, dec_hidden, dec_kv_heads;
+    float dec_norm_eps, dec_rope_theta;
+    int32_t ada_t_cond, vocab_size, downsample_factor;
+    int32_t tok_bos, tok_eos, tok_audio, tok_begin_audio;
+} vkv_hparams;
+
+vkv_status vkv_gguf_hparams(const vkv_gguf *gguf, vkv_hparams *out);
+
+/* ---------------------------------------------------------------------------
+ * A model in device memory: every tensor of the file at its data-section
+ * offset in one device allocation (the file's bytes unchanged, so Q4_K/Q6_K
+ * rows are what the kernels read), and the description the entry points take,
+ * by the reference's tensor names (src/voxtral.cpp:1193-1265).  Streamed from
+ * the file through pinned staging buffers on the given HIP stream (host
+ * copies on up to 8 threads); the call
+ * returns when the upload is complete.  MODEL_ERROR when a tensor the
+ * realtime model requires is missing or has an unsupported type.
+ * ------------------------------------------------------------------------- */
+typedef struct vkv_model vkv_model;
+
+typedef struct vkv_model_view {
+    vkv_hparams hp;
+    vkv_enc_model enc;             /* layers: the model's own array */
+    vkv_dec_model dec;             /* ada_scale of every layer NULL (session input) */
+    vkv_adapter adapter;
+    const void *conv0_w, *conv1_w; /* f16 [out][in][3] */
+    const float *conv0_b, *conv1_b;
+    const float *mel_filters;      /* audio.mel_filters or NULL */
+    uint64_t device_bytes;         /* the allocation holding every tensor */
+} vkv_model_view;
+
+vkv_status vkv_model_load(const char *path, int32_t device, void *hip_stream, vkv_model **out);
+vkv_status vkv_model_free(vkv_model *model);
+vkv_status vkv_model_get_view(const vkv_model *model, vkv_model_view *out);
+/* device address of a tensor by name, NULL when absent; info may be NULL */
+const void *vkv_model_tensor(const vkv_model *model, const char *name, vkv_gguf_tensor *info);
 
 /* ---------------------------------------------------------------------------
  * Seeded synthetic rows (integer Irwin-Hall N(0,1), bit-identical to the CPU

@@ -1,0 +1,210 @@
+"""GPU side of the GGUF loader (voxtral_model_load_from_file,
+src/voxtral.cpp:1035-1316): vkv_model_load places every tensor's file bytes in
+device memory unchanged, its view maps the reference's tensor names
+(:1193-1265) with their types and shapes, and a realtime step run from the
+loaded model (conv stem, encoder chunk into the output ring, adapter, decoder
+token reading the audio row) equals, bit for bit, the same step run from the
+tensors uploaded one by one outside the loader."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.gguf as og
+import vkv
+from gguf_util import gguf_bytes, realtime_model
+from gpu_util import dev, stream_ptr
+
+pytestmark = pytest.mark.gpu
+
+ENC_L, DEC_L, VOCAB = 1, 2, 1024
+
+
+@pytest.fixture(scope="module")
+def model_file(tmp_path_factory):
+    kvs, tensors = realtime_model(np.random.default_rng(1035), enc_layers=ENC_L, dec_layers=DEC_L,
+                                  vocab=VOCAB)
+    data = gguf_bytes(kvs, tensors)
+    p = tmp_path_factory.mktemp("gguf") / "realtime.gguf"
+    p.write_bytes(data)
+    return str(p), og.read(data)
+
+
+def d2h(ptr, n):
+    torch.cuda.synchronize()
+    out = torch.empty(n, dtype=torch.uint8)
+    hip = ctypes.CDLL("libamdhip64.so")   # the runtime torch has loaded
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip.hipMemcpy(out.data_ptr(), ctypes.c_void_p(ptr), n, 2) == 0
+    return out.numpy().tobytes()
+
+
+def test_device_bytes_are_the_file_bytes(model_file):
+    path, g = model_file
+    m = vkv.Model(path, hip_stream=stream_ptr())
+    base, t0 = m.tensor(g["tensors"][0]["name"])
+    assert t0.offset == 0 and base % 256 == 0
+    last = g["tensors"][-1]
+    n = last["offset"] + last["nbytes"]
+    assert m.view.device_bytes >= n
+    assert d2h(base, n) == g["data"][g["data_offset"]:g["data_offset"] + n]
+    for ti in g["tensors"]:
+        p, info = m.tensor(ti["name"])
+        assert p == base + ti["offset"] and info.nbytes == ti["nbytes"] and info.type == ti["type"]
+    assert m.tensor("absent.weight") == (None, None)
+    m.close()
+
+
+def test_view_maps_the_reference_names(model_file):
+    path, g = model_file
+    m = vkv.Model(path, hip_stream=stream_ptr())
+    v = m.view
+    hp = og.hparams(g)
+    for f, _ in vkv.Hparams._fields_:
+        assert getattr(v.hp, f) == pytest.approx(hp[f], rel=1e-7), f
+
+    def at(name):
+        return m.tensor(name)[0]
+
+    def typ(name):
+        return m.tensor(name)[1].type
+
+    assert (v.conv0_w, v.conv0_b, v.conv1_w, v.conv1_b) == (
+        at("enc.conv0.weight"), at("enc.conv0.bias"), at("enc.conv1.weight"), at("enc.conv1.bias"))
+    assert v.mel_filters == at("audio.mel_filters")
+    e = v.enc
+    assert (e.n_layers, e.dim, e.hidden, e.n_heads, e.head_dim) == (ENC_L, 1280, 5120, 32, 64)
+    assert (e.out_norm, e.out_norm_b) == (at("enc.norm.weight"), None)
+    for i in range(ENC_L):
+        L, p = e.layers[i], f"enc.blk.{i}."
+        for field, name in [("attn_norm", "attn_norm.weight"), ("attn_q", "attn_q.weight"),
+                            ("attn_k", "attn_k.weight"), ("attn_v", "attn_v.weight"),
+                            ("attn_o", "attn_o.weight"), ("attn_q_b", "attn_q.bias"),
+                            ("attn_v_b", "attn_v.bias"), ("attn_o_b", "attn_o.bias"),
+                            ("ffn_norm", "ffn_norm.weight"), ("ffn_w1", "ffn_w1.weight"),
+                            ("ffn_w2", "ffn_w2.weight"), ("ffn_w3", "ffn_w3.weight"),
+                            ("ffn_w2_b", "ffn_w2.bias")]:
+            assert getattr(L, field) == at(p + name), field
+        assert (L.attn_norm_b, L.ffn_norm_b) == (None, None)
+        assert (L.attn_q_type, L.attn_v_type, L.ffn_w2_type) == (typ(p + "attn_q.weight"), 14, 14)
+    a = v.adapter
+    assert (a.w0, a.w2, a.w0_type, a.w2_type, a.enc_dim, a.dec_dim, a.downsample) == (
+        at("adapter.0.weight"), at("adapter.2.weight"), 12, 12, 1280, 3072, 4)
+    d = v.dec
+    assert (d.n_layers, d.dim, d.hidden, d.n_q_heads, d.n_kv_heads, d.head_dim, d.vocab) == (
+        DEC_L, 3072, 9216, 32, 8, 128, VOCAB)
+    # the realtime model's output is tied to the embeddings
+    assert d.tok_embeddings == d.output == at("tok_embeddings.weight")
+    assert d.tok_embeddings_type == d.output_type == 14 and d.out_norm == at("norm.weight")
+    for i in range(DEC_L):
+        L, p = d.layers[i], f"dec.blk.{i}."
+        for field, name in [("attn_norm", "attn_norm.weight"), ("attn_q", "attn_q.weight"),
+                            ("attn_k", "attn_k.weight"), ("attn_v", "attn_v.weight"),
+                            ("attn_o", "attn_o.weight"), ("ffn_norm", "ffn_norm.weight"),
+                            ("ffn_w1", "ffn_w1.weight"), ("ffn_w2", "ffn_w2.weight"),
+                            ("ffn_w3", "ffn_w3.weight")]:
+            assert getattr(L, field) == at(p + name), field
+        assert L.ada_scale is None
+        assert (L.attn_v_type, L.ffn_w2_type, L.ffn_w1_type) == (14, 14, 12)
+    m.close()
+
+
+def independent(g):
+    """the same tensors uploaded one by one (no loader), described by hand"""
+    keep = {}
+    for ti in g["tensors"]:
+        b = np.frombuffer(og.tensor_bytes(g, ti), np.uint8).copy()
+        keep[ti["name"]] = torch.from_numpy(b).to(dev())
+
+    def at(n):
+        return keep[n].data_ptr()
+
+    el = (vkv.EncLayer * ENC_L)()
+    for i in range(ENC_L):
+        p = f"enc.blk.{i}."
+        el[i] = vkv.EncLayer(at(p + "attn_norm.weight"), None, at(p + "attn_q.weight"),
+                             at(p + "attn_k.weight"), at(p + "attn_v.weight"), at(p + "attn_o.weight"),
+                             12, 12, 14, 12, at(p + "attn_q.bias"), at(p + "attn_v.bias"),
+                             at(p + "attn_o.bias"), at(p + "ffn_norm.weight"), None,
+                             at(p + "ffn_w1.weight"), at(p + "ffn_w2.weight"), at(p + "ffn_w3.weight"),
+                             12, 14, 12, at(p + "ffn_w2.bias"))
+    enc = vkv.EncModel(ENC_L, 1280, 5120, 32, 64, 1e-5, 1e6, at("enc.norm.weight"), None, el)
+    dl = (vkv.DecLayer * DEC_L)()
+    for i in range(DEC_L):
+        p = f"dec.blk.{i}."
+        dl[i] = vkv.DecLayer(at(p + "attn_norm.weight"), at(p + "attn_q.weight"), at(p + "attn_k.weight"),
+                             at(p + "attn_v.weight"), at(p + "attn_o.weight"), 12, 12, 14, 12,
+                             at(p + "ffn_norm.weight"), None, at(p + "ffn_w1.weight"),
+                             at(p + "ffn_w2.weight"), at(p + "ffn_w3.weight"), 12, 14, 12)
+    dec = vkv.DecModel(DEC_L, 3072, 9216, 32, 8, 128, VOCAB, 1e-5, 1e6, at("tok_embeddings.weight"), 14,
+                       at("norm.weight"), at("tok_embeddings.weight"), 14, dl)
+    ad = vkv.Adapter(at("adapter.0.weight"), at("adapter.2.weight"), 12, 12, 1280, 3072, 4)
+    conv = (at("enc.conv0.weight"), at("enc.conv0.bias"), at("enc.conv1.weight"), at("enc.conv1.bias"))
+    return dict(enc=enc, dec=dec, adapter=ad, conv=conv, keep=(keep, el, dl))
+
+
+def realtime_step(enc, dec, ad, conv, mel_window, plan):
+    """conv stem -> encoder chunk into the output ring -> adapter groups ->
+    one decoder token per group reading its audio row; returns the logits
+    of every token and the rings"""
+    sp = stream_ptr()
+    n = plan.n_new
+    ecache = vkv.Cache(n_streams=1, n_layers=ENC_L, capacity=878, n_kv_heads=32,
+                       head_dim=64, n_q_heads=32, dtype=vkv.F16)
+    dcache = vkv.Cache(n_streams=1, n_layers=DEC_L, capacity=512, n_kv_heads=8, head_dim=128,
+                       n_q_heads=32, dtype=vkv.F16)
+    ring = vkv.new_ring(512)
+    x = torch.empty(n, 1280, device=dev())
+    cb = vkv.enc_conv_stem_workspace(mel_window.shape[1], 128, 1280, n)
+    cws = torch.empty(cb // 4 + 64, device=dev())
+    vkv.enc_conv_stem(mel_window.data_ptr(), 128, plan, conv[0], conv[1], conv[2], conv[3], 1280,
+                      x.data_ptr(), (cws.data_ptr() + 255) & ~255, cb, hip_stream=sp)
+    enc_out = torch.full((256, 1280), np.nan, device=dev())
+    aemb = torch.full((256, 3072), np.nan, device=dev())
+    er = vkv.RowRing(enc_out.data_ptr(), 256, 1280)
+    ar = vkv.RowRing(aemb.data_ptr(), 256, 3072)
+    wb = vkv.encoder_chunk_workspace(enc, n)
+    ws = torch.empty(wb // 4 + 64, device=dev())
+    vkv.encoder_chunk_ring(ecache, 0, plan, 750, enc, x.data_ptr(), er, (ws.data_ptr() + 255) & ~255,
+                           wb, hip_stream=sp)
+    groups = n // 4
+    ab = vkv.adapter_workspace(ad, groups)
+    aws = torch.empty(ab // 4 + 64, device=dev())
+    vkv.adapter_commit(ad, er, ar, 0, groups, (aws.data_ptr() + 255) & ~255, ab, hip_stream=sp)
+    tb = vkv.decoder_token_workspace(dec)
+    tws = torch.empty(tb // 4 + 64, device=dev())
+    logits = torch.empty(groups, VOCAB, device=dev())
+    tok = torch.zeros(groups + 1, dtype=torch.int32, device=dev())
+    token = 1
+    for p in range(groups):
+        vkv.decoder_token(dcache, 0, ring, dec, token, aemb[p % 256].data_ptr(), logits[p].data_ptr(),
+                          tok[p].data_ptr(), (tws.data_ptr() + 255) & ~255, tb, hip_stream=sp)
+        torch.cuda.synchronize()
+        token = int(tok[p].item())
+    torch.cuda.synchronize()
+    out = (logits.cpu().numpy(), tok.cpu().numpy(), enc_out.cpu().numpy(), aemb.cpu().numpy())
+    ecache.close()
+    dcache.close()
+    return out
+
+
+def test_a_realtime_step_from_the_loaded_model(model_file):
+    path, g = model_file
+    rng = np.random.default_rng(5424)
+    plan = vkv.enc_plan(0, 16, 878, 750)
+    win = plan.conv_mel_end - plan.conv_mel_start
+    mel = torch.from_numpy(rng.uniform(-1.5, 1.5, (128, win)).astype(np.float32)).to(dev())
+    m = vkv.Model(path, hip_stream=stream_ptr())
+    v = m.view
+    got = realtime_step(v.enc, v.dec, v.adapter, (v.conv0_w, v.conv0_b, v.conv1_w, v.conv1_b),
+                        mel, plan)
+    ind = independent(g)
+    want = realtime_step(ind["enc"], ind["dec"], ind["adapter"], ind["conv"], mel, plan)
+    for a, b in zip(got, want):
+        assert np.array_equal(a, b, equal_nan=True)
+    logits, toks, enc_out, aemb = got
+    assert np.isfinite(logits).all() and np.isfinite(enc_out[:16]).all() and np.isfinite(aemb[:4]).all()
+    assert np.isnan(enc_out[16:]).all() and np.isnan(aemb[4:]).all()
+    assert all(0 <= t < VOCAB for t in toks[:4])
+    m.close()

@@ -386,6 +386,12 @@ vkv_status do_window(vkv_cache *c, int32_t stream, int32_t layer0, int32_t n_lay
 
 }  // namespace
 
+namespace vkv {
+vkv_status host_fail(vkv_status st, const char *msg) { return fail(st, "%s", msg); }
+vkv_status host_hip_fail(hipError_t e, const char *what) { return hip_fail(e, what); }
+vkv_status host_ok() { return ok(); }
+}  // namespace vkv
+
 extern "C" {
 
 uint32_t vkv_api_version(void) { return VKV_API_VERSION; }

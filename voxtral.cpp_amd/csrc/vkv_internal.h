@@ -10,6 +10,12 @@
 
 namespace vkv {
 
+// The library's per-thread error state (vkv_last_error), for host sources
+// other than vkv_host.cpp.
+vkv_status host_fail(vkv_status st, const char *msg);
+vkv_status host_hip_fail(hipError_t e, const char *what);
+vkv_status host_ok();
+
 // ggml_gelu_erf as the CPU path computes it: 0.5 x (1 + erf(x / sqrt(2)))
 __device__ __forceinline__ float gelu_erf(float x) {
     return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));

@@ -34,6 +34,7 @@ OK = 0
 INVALID_ARGUMENT = 1
 INVALID_STATE = 2
 OUT_OF_MEMORY = 3
+MODEL_ERROR = 8
 BACKEND_ERROR = 9
 INTERNAL_ERROR = 10
 BUFFER_TOO_SMALL = 11
@@ -177,6 +178,28 @@ class Adapter(ctypes.Structure):
                 ("enc_dim", _i32), ("dec_dim", _i32), ("downsample", _i32)]
 
 
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("type", _i32), ("n_dims", _i32), ("ne", _i64 * 4),
+                ("offset", _u64), ("nbytes", _u64)]
+
+
+class Hparams(ctypes.Structure):
+    _fields_ = [("is_offline", _i32), ("enc_dim", _i32), ("enc_layers", _i32), ("enc_heads", _i32),
+                ("enc_head_dim", _i32), ("enc_hidden", _i32), ("enc_kv_heads", _i32),
+                ("enc_causal", _i32), ("enc_norm_eps", _f32), ("enc_rope_theta", _f32),
+                ("dec_dim", _i32), ("dec_layers", _i32), ("dec_heads", _i32),
+                ("dec_head_dim", _i32), ("dec_hidden", _i32), ("dec_kv_heads", _i32),
+                ("dec_norm_eps", _f32), ("dec_rope_theta", _f32), ("ada_t_cond", _i32),
+                ("vocab_size", _i32), ("downsample_factor", _i32), ("tok_bos", _i32),
+                ("tok_eos", _i32), ("tok_audio", _i32), ("tok_begin_audio", _i32)]
+
+
+class ModelView(ctypes.Structure):
+    _fields_ = [("hp", Hparams), ("enc", EncModel), ("dec", DecModel), ("adapter", Adapter),
+                ("conv0_w", _vp), ("conv1_w", _vp), ("conv0_b", _vp), ("conv1_b", _vp),
+                ("mel_filters", _vp), ("device_bytes", _u64)]
+
+
 # prototypes: name -> (restype, argtypes); exactly the functions of include/vkv.h
 PROTOTYPES = {
     "vkv_decoder_plan": (_i32, [_P(Ring), _i64, _i32, _P(Plan)]),
@@ -236,6 +259,34 @@ PROTOTYPES = {
                                  ctypes.c_size_t, _P(Plan), _vp]),
     "vkv_embed": (_i32, [_i32, _vp, _i32, _i64, _i32, _vp, _vp, _vp]),
     "vkv_argmax": (_i32, [_vp, _i64, _vp, _vp]),
+    "vkv_gguf_open": (_i32, [ctypes.c_char_p, _P(_vp)]),
+    "vkv_gguf_close": (_i32, [_vp]),
+    "vkv_gguf_version": (_u32, [_vp]),
+    "vkv_gguf_alignment": (_u64, [_vp]),
+    "vkv_gguf_data_offset": (_u64, [_vp]),
+    "vkv_gguf_n_kv": (_i64, [_vp]),
+    "vkv_gguf_find_key": (_i64, [_vp, ctypes.c_char_p]),
+    "vkv_gguf_key": (ctypes.c_char_p, [_vp, _i64]),
+    "vkv_gguf_kv_type": (_i32, [_vp, _i64]),
+    "vkv_gguf_get_i32": (_i32, [_vp, _i64, _P(_i32)]),
+    "vkv_gguf_get_u32": (_i32, [_vp, _i64, _P(_u32)]),
+    "vkv_gguf_get_i64": (_i32, [_vp, _i64, _P(_i64)]),
+    "vkv_gguf_get_f32": (_i32, [_vp, _i64, _P(_f32)]),
+    "vkv_gguf_get_f64": (_i32, [_vp, _i64, _P(ctypes.c_double)]),
+    "vkv_gguf_get_bool": (_i32, [_vp, _i64, _P(_i32)]),
+    "vkv_gguf_get_str": (_i32, [_vp, _i64, _P(_vp), _P(_u64)]),
+    "vkv_gguf_get_scalar": (_i32, [_vp, _i64, _vp, _u64]),
+    "vkv_gguf_get_arr": (_i32, [_vp, _i64, _P(_i32), _P(_u64), _P(_vp)]),
+    "vkv_gguf_get_arr_str": (_i32, [_vp, _i64, _u64, _P(_vp), _P(_u64)]),
+    "vkv_gguf_n_tensors": (_i64, [_vp]),
+    "vkv_gguf_find_tensor": (_i64, [_vp, ctypes.c_char_p]),
+    "vkv_gguf_tensor_info": (_i32, [_vp, _i64, _P(GgufTensor)]),
+    "vkv_gguf_tensor_data": (_vp, [_vp, _i64]),
+    "vkv_gguf_hparams": (_i32, [_vp, _P(Hparams)]),
+    "vkv_model_load": (_i32, [ctypes.c_char_p, _i32, _vp, _P(_vp)]),
+    "vkv_model_free": (_i32, [_vp]),
+    "vkv_model_get_view": (_i32, [_vp, _P(ModelView)]),
+    "vkv_model_tensor": (_vp, [_vp, ctypes.c_char_p, _P(GgufTensor)]),
     "vkv_synth_rows": (_i32, [_vp, _i32, _u64, _u32, _i64, _i32, _i64, _i64, _i32, _i64, _i64,
                               _i32, _i64, _vp]),
     "vkv_api_version": (_u32, []),
@@ -573,3 +624,139 @@ def synth_rows(dst_ptr, row_len, seed, tag, s0=0, ns=1, s_stride=0, l0=0, nl=1, 
         s_stride = nl * l_stride
     check(lib.vkv_synth_rows(dst_ptr, row_len, seed, tag, s0, ns, s_stride, l0, nl, l_stride, p0,
                              np_, p_stride, hip_stream))
+
+
+# ---- GGUF files and models ----
+GGUF_UINT8, GGUF_INT8, GGUF_UINT16, GGUF_INT16, GGUF_UINT32, GGUF_INT32 = 0, 1, 2, 3, 4, 5
+GGUF_FLOAT32, GGUF_BOOL, GGUF_STRING, GGUF_ARRAY, GGUF_UINT64, GGUF_INT64 = 6, 7, 8, 9, 10, 11
+GGUF_FLOAT64 = 12
+_GGUF_NP = {GGUF_UINT8: "<u1", GGUF_INT8: "<i1", GGUF_UINT16: "<u2", GGUF_INT16: "<i2",
+            GGUF_UINT32: "<u4", GGUF_INT32: "<i4", GGUF_FLOAT32: "<f4", GGUF_BOOL: "<u1",
+            GGUF_UINT64: "<u8", GGUF_INT64: "<i8", GGUF_FLOAT64: "<f8"}
+
+
+class Gguf:
+    """A GGUF file opened by the library (metadata and tensor infos; the
+    tensor bytes stay in the file mapping)."""
+
+    def __init__(self, path):
+        h = _vp()
+        self.handle = None
+        check(lib.vkv_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self.handle = h
+        self._close = lib.vkv_gguf_close   # still bound at interpreter exit
+
+    def close(self):
+        if self.handle:
+            self._close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def version(self):
+        return lib.vkv_gguf_version(self.handle)
+
+    @property
+    def alignment(self):
+        return lib.vkv_gguf_alignment(self.handle)
+
+    @property
+    def data_offset(self):
+        return lib.vkv_gguf_data_offset(self.handle)
+
+    def keys(self):
+        return [lib.vkv_gguf_key(self.handle, i).decode() for i in range(lib.vkv_gguf_n_kv(self.handle))]
+
+    def find_key(self, key):
+        return lib.vkv_gguf_find_key(self.handle, key.encode())
+
+    def kv_type(self, i):
+        return lib.vkv_gguf_kv_type(self.handle, i)
+
+    def value(self, key):
+        """(type, value): scalars as Python numbers, strings as bytes, arrays
+        as (element type, numpy array or list of bytes)"""
+        import numpy as np
+        i = self.find_key(key)
+        if i < 0:
+            raise KeyError(key)
+        t = self.kv_type(i)
+        if t == GGUF_STRING:
+            p, n = _vp(), _u64()
+            check(lib.vkv_gguf_get_str(self.handle, i, ctypes.byref(p), ctypes.byref(n)))
+            return t, ctypes.string_at(p, n.value)
+        if t == GGUF_ARRAY:
+            et, n, d = _i32(), _u64(), _vp()
+            check(lib.vkv_gguf_get_arr(self.handle, i, ctypes.byref(et), ctypes.byref(n),
+                                       ctypes.byref(d)))
+            if et.value == GGUF_STRING:
+                out = []
+                for j in range(n.value):
+                    p, m = _vp(), _u64()
+                    check(lib.vkv_gguf_get_arr_str(self.handle, i, j, ctypes.byref(p), ctypes.byref(m)))
+                    out.append(ctypes.string_at(p, m.value))
+                return t, (et.value, out)
+            dt = np.dtype(_GGUF_NP[et.value])
+            raw = ctypes.string_at(d, dt.itemsize * n.value) if n.value else b""
+            return t, (et.value, np.frombuffer(raw, dt).copy())
+        getters = {GGUF_INT32: (lib.vkv_gguf_get_i32, _i32), GGUF_UINT32: (lib.vkv_gguf_get_u32, _u32),
+                   GGUF_INT64: (lib.vkv_gguf_get_i64, _i64), GGUF_FLOAT32: (lib.vkv_gguf_get_f32, _f32),
+                   GGUF_FLOAT64: (lib.vkv_gguf_get_f64, ctypes.c_double),
+                   GGUF_BOOL: (lib.vkv_gguf_get_bool, _i32)}
+        if t in getters:
+            fn, ct = getters[t]
+            v = ct()
+            check(fn(self.handle, i, ctypes.byref(v)))
+            return t, v.value
+        dt = np.dtype(_GGUF_NP[t])
+        buf = ctypes.create_string_buffer(8)
+        check(lib.vkv_gguf_get_scalar(self.handle, i, buf, 8))
+        return t, np.frombuffer(buf.raw[:dt.itemsize], dt)[0].item()
+
+    def tensors(self):
+        out = []
+        for i in range(lib.vkv_gguf_n_tensors(self.handle)):
+            ti = GgufTensor()
+            check(lib.vkv_gguf_tensor_info(self.handle, i, ctypes.byref(ti)))
+            out.append(ti)
+        return out
+
+    def tensor_bytes(self, i):
+        ti = GgufTensor()
+        check(lib.vkv_gguf_tensor_info(self.handle, i, ctypes.byref(ti)))
+        return ctypes.string_at(lib.vkv_gguf_tensor_data(self.handle, i), ti.nbytes)
+
+    def hparams(self):
+        hp = Hparams()
+        check(lib.vkv_gguf_hparams(self.handle, ctypes.byref(hp)))
+        return hp
+
+
+class Model:
+    """A GGUF model uploaded into one device allocation."""
+
+    def __init__(self, path, device=0, hip_stream=0):
+        h = _vp()
+        self.handle = None
+        check(lib.vkv_model_load(os.fsencode(path), device, hip_stream, ctypes.byref(h)))
+        self.handle = h
+        self._free = lib.vkv_model_free
+        self.view = ModelView()
+        check(lib.vkv_model_get_view(self.handle, ctypes.byref(self.view)))
+
+    def tensor(self, name):
+        """(device address, GgufTensor) or (None, None)"""
+        ti = GgufTensor()
+        p = lib.vkv_model_tensor(self.handle, name.encode(), ctypes.byref(ti))
+        return (p, ti) if p else (None, None)
+
+    def close(self):
+        if self.handle:
+            self._free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()
+
