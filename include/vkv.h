@@ -523,6 +523,21 @@ vkv_status vkv_adapter_commit(const vkv_adapter *adapter, const vkv_row_ring *en
 vkv_status vkv_embed(int32_t dtype, const void *table, int32_t n_rows, int64_t n_cols,
                      int32_t token, const float *add, float *y, void *hip_stream);
 
+/* The decoder's ada time conditioning, constant for a session
+ * (build_decoder_layer src/voxtral.cpp:2864-2874 on the time embedding of
+ * compute_time_embedding :729-740, evaluated at t = VOXTRAL_N_DELAY_TOKENS,
+ * :1535): scale = W2 gelu_erf(W0 e(t)) with e(t)[i] = cos(t f_i),
+ * e(t)[i + dim/2] = sin(t f_i), f_i = expf(-logf(10000) i / (dim/2)), as the
+ * reference computes it on the host.  W0: Q4_K/Q6_K [ada_dim][dim] (the
+ * product as vkv_matvec computes it); W2: F16 or F32 (dtype 1 / 0)
+ * [dim][ada_dim], its input rounded to f16 for F16 as ggml's vec-dot type
+ * does.  out: [dim] f32 device memory, the vkv_dec_layer.ada_scale of the
+ * layer.  workspace: vkv_ada_scale_workspace bytes of device memory. */
+size_t vkv_ada_scale_workspace(int32_t dim, int32_t ada_dim);
+vkv_status vkv_ada_scale(const void *w0, int32_t w0_type, const void *w2, int32_t w2_type,
+                         int32_t dim, int32_t ada_dim, float t, float *out, void *workspace,
+                         size_t workspace_bytes, void *hip_stream);
+
 /* ggml_argmax of f32 logits (emit_logits_argmax, src/voxtral.cpp:2966-2972):
  * the last index of the maximum (ggml_vec_argmax_f32 keeps updating the index
  * while x[i] equals the running max); NaN input gives an unspecified index.
@@ -690,6 +705,12 @@ vkv_status vkv_model_free(vkv_model *model);
 vkv_status vkv_model_get_view(const vkv_model *model, vkv_model_view *out);
 /* device address of a tensor by name, NULL when absent; info may be NULL */
 const void *vkv_model_tensor(const vkv_model *model, const char *name, vkv_gguf_tensor *info);
+/* Every decoder layer's ada scale (vkv_ada_scale with the layer's
+ * dec.blk.N.ada0 / ada2 weights) at time value t into scales [n_layers][dim]
+ * (caller's device memory, kept by the model's view from then on:
+ * dec.layers[l].ada_scale = scales + l * dim).  A model without ada
+ * conditioning leaves the view alone. */
+vkv_status vkv_model_set_ada(vkv_model *model, float t, float *scales, void *hip_stream);
 
 /* ---------------------------------------------------------------------------
  * Seeded synthetic rows (integer Irwin-Hall N(0,1), bit-identical to the CPU

@@ -122,6 +122,8 @@ _protos = {
                           _i32, _vp]),
     "orc_conv_stem": (None, [_vp, _i32, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _i32, _vp]),
     "orc_gelu_erf": (_f32, [_f32]),
+    "orc_time_embedding": (None, [_f32, _i32, _vp]),
+    "orc_ada_scale": (_i32, [ctypes.c_int, _vp, ctypes.c_int, _vp, _i32, _i32, _f32, _vp]),
     "orc_row_ring_write": (_i32, [_vp, _i32, _i32, _i64, _vp, _i32]),
     "orc_row_ring_read": (_i32, [_vp, _i32, _i32, _i64, _i32, _vp]),
     "orc_adapter_commit": (_i32, [_vp, _i32, _i32, _i32, _vp, _i32, _i32, _i64, _i32,
@@ -491,3 +493,22 @@ def adapter_commit(enc_ring, aemb_ring, group_start, n_groups, w0_type, w0, w2_t
                                 _ptr(w0), w2_type, _ptr(w2), n_threads)
     if rc != n_groups:
         raise ValueError("adapter commit rejected")
+
+
+def time_embedding(t, dim):
+    out = np.empty(dim, np.float32)
+    lib.orc_time_embedding(t, dim, _ptr(out))
+    return out
+
+
+def ada_scale(w0_type, w0, w2, dim, ada_dim, t):
+    """w2: uint16 (f16 bits) or float32 array [dim][ada_dim]"""
+    w0 = _u8(w0)
+    w2 = np.ascontiguousarray(w2)
+    assert w2.dtype in (np.uint16, np.float32) and w2.size == dim * ada_dim
+    out = np.empty(dim, np.float32)
+    rc = lib.orc_ada_scale(w0_type, _ptr(w0), 1 if w2.dtype == np.uint16 else 0, _ptr(w2), dim,
+                           ada_dim, t, _ptr(out))
+    if rc != 0:
+        raise ValueError("ada scale rejected")
+    return out

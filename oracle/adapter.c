@@ -14,14 +14,23 @@
  * stored at audio row g % aemb_cap (ggml_set_rows).  Each product is
  * orc_matvec (the CPU mul_mat: input quantized to Q8_K, integer block dots).
  *
+ * The decoder's ada time conditioning (build_decoder_layer :2864-2874):
+ * scale = W2 gelu(W0 e(t)) with the time embedding of compute_time_embedding
+ * (:729-740) evaluated as the reference does on the host; W0 through
+ * orc_matvec, W2 (f16 [dim][ada_dim]) through ggml's f16 vec-dot: the input
+ * rounded to f16, products summed in double (the generic path).
+ *
  * Pinned by tests/test_adapter.py: the gather against an independent index
  * rule (the 4-frame reshape of a contiguous run of encoder frames), the
  * products against fp64 products of the dequantized weights and the Q8_K
  * images, GELU against math.erf, the rings against a dictionary model of the
- * logical rows.
+ * logical rows; the time embedding against fp64 cos/sin of the stated
+ * frequencies, the ada scale against an fp64 composition of the dequantized
+ * weights.
  */
 #include "vkv_oracle.h"
 
+#include <math.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -86,4 +95,45 @@ int32_t orc_adapter_commit(const float *enc_ring, int32_t enc_cap, int32_t enc_d
     free(x);
     free(h);
     return n_groups;
+}
+
+void orc_time_embedding(float t, int32_t dim, float *out) {
+    const int32_t half = dim / 2;
+    for (int32_t i = 0; i < half; i++) {
+        const float inv_freq = expf(-logf(10000.0f) * (float)i / (float)half);
+        const float angle = t * inv_freq;
+        out[i] = cosf(angle);
+        out[i + half] = sinf(angle);
+    }
+}
+
+int32_t orc_ada_scale(int w0_type, const uint8_t *w0, int w2_f16, const void *w2, int32_t dim,
+                      int32_t ada_dim, float t, float *out) {
+    if (dim < 2 || ada_dim < 1) return -1;
+    float *e = malloc((size_t)dim * sizeof(float));
+    float *h = malloc((size_t)ada_dim * sizeof(float));
+    if (!e || !h) {
+        free(e);
+        free(h);
+        return -1;
+    }
+    orc_time_embedding(t, dim, e);
+    orc_matvec(w0_type, w0, ada_dim, dim, e, h, 1);
+    for (int32_t k = 0; k < ada_dim; k++) h[k] = orc_gelu_erf(h[k]);
+    for (int32_t r = 0; r < dim; r++) {
+        double acc = 0.0;
+        for (int32_t k = 0; k < ada_dim; k++) {
+            if (w2_f16) {
+                const float a = orc_f16_to_f32(((const uint16_t *)w2)[(int64_t)r * ada_dim + k]);
+                const float b = orc_f16_to_f32(orc_f32_to_f16(h[k]));
+                acc += (double)(a * b);
+            } else {
+                acc += (double)(((const float *)w2)[(int64_t)r * ada_dim + k] * h[k]);
+            }
+        }
+        out[r] = (float)acc;
+    }
+    free(e);
+    free(h);
+    return 0;
 }

@@ -135,9 +135,9 @@ def realtime_model(rng, enc_layers=1, dec_layers=2, vocab=1024, enc=1280, dec=30
         mat(p + "ffn_w1.weight", q4, dec_hidden, dec, 0.005)
         mat(p + "ffn_w2.weight", q6, dec, dec_hidden, 0.05)
         mat(p + "ffn_w3.weight", q4, dec_hidden, dec, 0.005)
-        mat(p + "ada0.weight", q4, 32, dec, 0.01)
+        mat(p + "ada0.weight", q4, 32, dec, 0.002)
         T.append((p + "ada2.weight", 1, [32, dec],
-                  (rng.standard_normal((dec, 32)) * 0.05).astype(np.float16).tobytes()))
+                  (rng.standard_normal((dec, 32)) * 0.01).astype(np.float16).tobytes()))
     T.append(("audio.mel_filters", 0, [201, n_mel],
               rng.uniform(0, 0.01, 201 * n_mel).astype(np.float32).tobytes()))
     return kvs, T

@@ -145,3 +145,51 @@ def test_adapter_rejects_a_ring_that_splits_groups(adapter_weights):
     with pytest.raises(ValueError):
         oracle.adapter_commit(enc, np.zeros((4, DEC), np.float32), 0, 1, oracle.Q4_K, w0,
                               oracle.Q6_K, w2)
+
+
+def test_time_embedding_closed_form():
+    """compute_time_embedding (src/voxtral.cpp:729-740): cos of the first half,
+    sin of the second, frequencies exp(-ln(10000) i / half); at t = 6 (the
+    delay tokens, :1535) and a few other times"""
+    for t in (6.0, 0.0, 1.0, 37.5):
+        e = oracle.time_embedding(t, 3072).astype(np.float64)
+        i = np.arange(1536)
+        ang = t * np.exp(-np.log(10000.0) * i / 1536)
+        assert np.allclose(e[:1536], np.cos(ang), rtol=0, atol=3e-6)
+        assert np.allclose(e[1536:], np.sin(ang), rtol=0, atol=3e-6)
+    assert np.all(oracle.time_embedding(0.0, 3072)[:1536] == 1) and \
+        np.all(oracle.time_embedding(0.0, 3072)[1536:] == 0)
+
+
+def ada_w0(rng, ad, dim):
+    """Q4_K rows whose products with e(t) straddle GELU's bend: small
+    scales, and the sign of d flipped on odd rows (a negative fp16 d is a
+    valid block)"""
+    w0 = random_matrix(rng, oracle.Q4_K, ad, dim, 0.004).reshape(ad, dim // 256, 144)
+    w0[1::2, :, 1] |= 0x80
+    return w0.reshape(-1)
+
+
+def test_ada_scale_against_fp64():
+    """build_decoder_layer's ada MLP (:2864-2874): W2 gelu(W0 e(t)), W0 Q4_K
+    [32][3072] through the Q8_K product, W2 f16 [3072][32] with its input
+    rounded to f16"""
+    rng = np.random.default_rng(2864)
+    dim, ad = 3072, 32
+    w0 = ada_w0(rng, ad, dim)
+    w2 = (rng.standard_normal((dim, ad)) * 0.1).astype(np.float16)
+    got = oracle.ada_scale(oracle.Q4_K, w0, w2.view(np.uint16), dim, ad, 6.0).astype(np.float64)
+    e = oracle.time_embedding(6.0, dim)
+    w0d = oracle.dequantize(oracle.Q4_K, w0, ad * dim).reshape(ad, dim).astype(np.float64)
+    eq = q8k_image(e)
+    pre = w0d @ eq
+    h = gelu64(pre)
+    dh = 1.13 * 1e-5 * (np.abs(w0d) @ np.abs(eq)) + 1e-7 * np.abs(h)
+    hf = h.astype(np.float16).astype(np.float64)   # the f16 vec-dot input
+    w2d = w2.astype(np.float64)
+    want = w2d @ hf
+    # a change of h within dh may move its f16 rounding by one ulp
+    bound = np.abs(w2d) @ (dh + np.abs(hf) * 2.0 ** -10) + 1e-6 * np.abs(want)
+    assert np.all(np.abs(got - want) <= bound)
+    # not the unrounded product and not without GELU: both miss by more
+    assert np.abs(w2d @ gelu64(pre) - w2d @ pre).max() > 100 * bound.max()

@@ -176,3 +176,35 @@ def test_adapter_rejects_bad_rings(weights):
         vkv.adapter_commit(ad, ring_of(enc_t), ring_of(aemb_t), 0, 1, ws_t.data_ptr(), 1 << 22,
                            hip_stream=stream_ptr())
     assert "multiple of 4" in vkv.last_error()
+
+
+@pytest.mark.parametrize("f16", [True, False])
+def test_ada_scale(f16):
+    """vkv_ada_scale (build_decoder_layer's ada MLP, src/voxtral.cpp:2864-2874)
+    against the oracle: the hidden rows within the Q4_K product's bound through
+    GELU, the output within the second product's bound plus one f16 ulp of h"""
+    from test_adapter import ada_w0
+    rng = np.random.default_rng(2866 + f16)
+    dim, ad = 3072, 32
+    w0 = ada_w0(rng, ad, dim)
+    w2 = (rng.standard_normal((dim, ad)) * 0.1).astype(np.float16 if f16 else np.float32)
+    w2_arg = w2.view(np.uint16) if f16 else w2
+    want = oracle.ada_scale(oracle.Q4_K, w0, w2_arg, dim, ad, 6.0).astype(np.float64)
+    w0t, w2t = to_dev(w0), to_dev(w2_arg)
+    out = torch.full((dim,), np.nan, device=dev())
+    wb = vkv.ada_scale_workspace(dim, ad)
+    ws_t = torch.empty(wb // 4 + 64, device=dev())
+    ws = (ws_t.data_ptr() + 255) & ~255
+    vkv.ada_scale(w0t.data_ptr(), vkv.Q4_K, w2t.data_ptr(), vkv.F16 if f16 else vkv.F32, dim, ad,
+                  6.0, out.data_ptr(), ws, wb, hip_stream=stream_ptr())
+    got = host(out).astype(np.float64)
+    e = oracle.time_embedding(6.0, dim)
+    w0d = np.abs(oracle.dequantize(oracle.Q4_K, w0, ad * dim).reshape(ad, dim).astype(np.float64))
+    dh = 1.13 * 1e-5 * (w0d @ q8k_abs(e)) + 1e-6
+    # the workspace keeps h after the time embedding (256-byte aligned)
+    h = host(ws_t).view(np.uint8)[ws - ws_t.data_ptr() + dim * 4:][:ad * 4].view(np.float32).astype(np.float64)
+    h_want = oracle.gelu_erf(oracle.matvec(oracle.Q4_K, w0, ad, dim, e)).astype(np.float64)
+    assert np.all(np.abs(h - h_want) <= dh)
+    w2d = np.abs(w2.astype(np.float64))
+    ulp = np.abs(h) * 2.0 ** -10 if f16 else 0.0
+    assert np.all(np.abs(got - want) <= w2d @ (dh + ulp) + 1e-6 * np.abs(want) + 1e-30)

@@ -11,6 +11,7 @@ import numpy as np
 import pytest
 import torch
 
+import oracle
 import oracle.gguf as og
 import vkv
 from gguf_util import gguf_bytes, realtime_model
@@ -189,6 +190,34 @@ def realtime_step(enc, dec, ad, conv, mel_window, plan):
     return out
 
 
+def test_ada_scales_of_the_loaded_model(model_file):
+    """vkv_model_set_ada: every layer's scale equals vkv_ada_scale on that
+    layer's weights (bit for bit) and the oracle's within its bound; the
+    view's layers point at the rows"""
+    path, g = model_file
+    m = vkv.Model(path, hip_stream=stream_ptr())
+    scales = torch.full((DEC_L, 3072), np.nan, device=dev())
+    m.set_ada(6.0, scales.data_ptr(), hip_stream=stream_ptr())
+    got = scales.cpu().numpy()
+    wb = vkv.ada_scale_workspace(3072, 32)
+    ws = torch.empty(wb // 4 + 64, device=dev())
+    one = torch.empty(3072, device=dev())
+    for l in range(DEC_L):
+        assert m.view.dec.layers[l].ada_scale == scales[l].data_ptr()
+        a0, i0 = m.tensor(f"dec.blk.{l}.ada0.weight")
+        a2, i2 = m.tensor(f"dec.blk.{l}.ada2.weight")
+        vkv.ada_scale(a0, i0.type, a2, i2.type, 3072, 32, 6.0, one.data_ptr(),
+                      (ws.data_ptr() + 255) & ~255, wb, hip_stream=stream_ptr())
+        assert np.array_equal(one.cpu().numpy(), got[l])
+        t0 = next(t for t in g["tensors"] if t["name"] == f"dec.blk.{l}.ada0.weight")
+        t2 = next(t for t in g["tensors"] if t["name"] == f"dec.blk.{l}.ada2.weight")
+        w0 = np.frombuffer(og.tensor_bytes(g, t0), np.uint8)
+        w2 = np.frombuffer(og.tensor_bytes(g, t2), np.uint16)
+        want = oracle.ada_scale(oracle.Q4_K, w0, w2, 3072, 32, 6.0)
+        assert np.abs(got[l] - want).max() <= 1e-3 * max(np.abs(want).max(), 1e-3)
+    m.close()
+
+
 def test_a_realtime_step_from_the_loaded_model(model_file):
     path, g = model_file
     rng = np.random.default_rng(5424)
@@ -196,10 +225,22 @@ def test_a_realtime_step_from_the_loaded_model(model_file):
     win = plan.conv_mel_end - plan.conv_mel_start
     mel = torch.from_numpy(rng.uniform(-1.5, 1.5, (128, win)).astype(np.float32)).to(dev())
     m = vkv.Model(path, hip_stream=stream_ptr())
+    scales = torch.empty(DEC_L, 3072, device=dev())
+    m.set_ada(6.0, scales.data_ptr(), hip_stream=stream_ptr())
     v = m.view
     got = realtime_step(v.enc, v.dec, v.adapter, (v.conv0_w, v.conv0_b, v.conv1_w, v.conv1_b),
                         mel, plan)
     ind = independent(g)
+    # the independent side computes its ada scales through vkv_ada_scale
+    ind_scales = torch.empty(DEC_L, 3072, device=dev())
+    wb = vkv.ada_scale_workspace(3072, 32)
+    ws = torch.empty(wb // 4 + 64, device=dev())
+    for l in range(DEC_L):
+        k = ind["keep"][0]
+        vkv.ada_scale(k[f"dec.blk.{l}.ada0.weight"].data_ptr(), 12, k[f"dec.blk.{l}.ada2.weight"].data_ptr(),
+                      1, 3072, 32, 6.0, ind_scales[l].data_ptr(), (ws.data_ptr() + 255) & ~255, wb,
+                      hip_stream=stream_ptr())
+        ind["dec"].layers[l].ada_scale = ind_scales[l].data_ptr()
     want = realtime_step(ind["enc"], ind["dec"], ind["adapter"], ind["conv"], mel, plan)
     for a, b in zip(got, want):
         assert np.array_equal(a, b, equal_nan=True)

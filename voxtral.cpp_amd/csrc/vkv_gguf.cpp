@@ -513,6 +513,7 @@ struct vkv_model {
     vkv_gguf *g = nullptr;
     int device = 0;
     uint8_t *base = nullptr;   // the data section, one allocation
+    uint8_t *ada_ws = nullptr; // vkv_ada_scale's workspace, on first use
     vkv_model_view view{};
     std::vector<vkv_enc_layer> enc_layers;
     std::vector<vkv_dec_layer> dec_layers;
@@ -522,6 +523,7 @@ struct vkv_model {
             (void)hipGetDevice(&prev);
             (void)hipSetDevice(device);
             (void)hipFree(base);
+            if (ada_ws) (void)hipFree(ada_ws);
             if (prev >= 0) (void)hipSetDevice(prev);
         }
         vkv_gguf_close(g);
@@ -795,6 +797,56 @@ vkv_status vkv_model_get_view(const vkv_model *model, vkv_model_view *out) {
     if (!model || !out) return gfail(VKV_STATUS_INVALID_ARGUMENT, "model: null argument");
     *out = model->view;
     return vkv::host_ok();
+}
+
+vkv_status vkv_model_set_ada(vkv_model *model, float t, float *scales, void *hip_stream) {
+    if (!model || !scales) return gfail(VKV_STATUS_INVALID_ARGUMENT, "model: null argument");
+    const vkv_hparams &hp = model->view.hp;
+    if (!hp.ada_t_cond) return vkv::host_ok();
+    int prev = -1;
+    (void)hipGetDevice(&prev);
+    if (hipSetDevice(model->device) != hipSuccess)
+        return gfail(VKV_STATUS_BACKEND_ERROR, "model: cannot select device %d", model->device);
+    vkv_status s = VKV_STATUS_OK;
+    char nm[96];
+    int64_t ada_dim = 0;
+    std::vector<std::pair<const TensorInfo *, const TensorInfo *>> w((size_t)hp.dec_layers);
+    for (int l = 0; l < hp.dec_layers && !s; ++l) {
+        std::snprintf(nm, sizeof(nm), "dec.blk.%d.ada0.weight", l);
+        const int64_t i0 = vkv_gguf_find_tensor(model->g, nm);
+        std::snprintf(nm, sizeof(nm), "dec.blk.%d.ada2.weight", l);
+        const int64_t i2 = vkv_gguf_find_tensor(model->g, nm);
+        if (i0 < 0 || i2 < 0) {
+            s = gfail(VKV_STATUS_MODEL_ERROR, "model: layer %d has no ada weights", l);
+            break;
+        }
+        const TensorInfo &a0 = model->g->tensors[(size_t)i0], &a2 = model->g->tensors[(size_t)i2];
+        if (l == 0) ada_dim = a0.t.ne[1];
+        if (a0.t.n_dims != 2 || a0.t.ne[0] != hp.dec_dim || a0.t.ne[1] != ada_dim ||
+            (a0.t.type != kQ4K && a0.t.type != kQ6K) || a2.t.n_dims != 2 || a2.t.ne[0] != ada_dim ||
+            a2.t.ne[1] != hp.dec_dim || (a2.t.type != kF16 && a2.t.type != kF32))
+            s = gfail(VKV_STATUS_MODEL_ERROR, "model: layer %d ada weights have unexpected shapes or types", l);
+        w[(size_t)l] = {&a0, &a2};
+    }
+    const size_t wsb = s ? 0 : vkv_ada_scale_workspace(hp.dec_dim, (int32_t)ada_dim);
+    if (!s && !wsb) s = gfail(VKV_STATUS_MODEL_ERROR, "model: ada dimension %lld", (long long)ada_dim);
+    if (!s && !model->ada_ws) {
+        hipError_t e = hipMalloc((void **)&model->ada_ws, wsb);
+        if (e != hipSuccess) {
+            model->ada_ws = nullptr;
+            s = vkv::host_hip_fail(e, "model: ada workspace");
+        }
+    }
+    for (int l = 0; l < hp.dec_layers && !s; ++l)
+        s = vkv_ada_scale(model->base + w[(size_t)l].first->t.offset, w[(size_t)l].first->t.type,
+                          model->base + w[(size_t)l].second->t.offset, w[(size_t)l].second->t.type,
+                          hp.dec_dim, (int32_t)ada_dim, t, scales + (size_t)l * hp.dec_dim,
+                          model->ada_ws, wsb, hip_stream);
+    if (!s)
+        for (int l = 0; l < hp.dec_layers; ++l)
+            model->dec_layers[(size_t)l].ada_scale = scales + (size_t)l * hp.dec_dim;
+    if (prev >= 0) (void)hipSetDevice(prev);
+    return s ? s : vkv::host_ok();
 }
 
 const void *vkv_model_tensor(const vkv_model *model, const char *name, vkv_gguf_tensor *info) {

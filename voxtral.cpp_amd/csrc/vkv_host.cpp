@@ -16,6 +16,7 @@
 #include <initializer_list>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "vkv.h"
 #include "vkv_internal.h"
@@ -1207,6 +1208,54 @@ vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float
     return ok();
 }
 }  // namespace
+
+size_t vkv_ada_scale_workspace(int32_t dim, int32_t ada_dim) {
+    if (dim < 256 || dim % 256 || dim > VKV_MV_MAX_IN || ada_dim < 1 || ada_dim > VKV_MV_MAX_IN)
+        return 0;
+    return ((size_t)dim * 4 + 255) / 256 * 256 + ((size_t)ada_dim * 4 + 255) / 256 * 256;
+}
+
+vkv_status vkv_ada_scale(const void *w0, int32_t w0_type, const void *w2, int32_t w2_type,
+                         int32_t dim, int32_t ada_dim, float t, float *out, void *workspace,
+                         size_t workspace_bytes, void *hip_stream) {
+    const size_t need = vkv_ada_scale_workspace(dim, ada_dim);
+    if (!need) return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: dim=%d ada_dim=%d", dim, ada_dim);
+    if (!w0 || !w2 || !out || !workspace)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: null argument");
+    if (!kq_block_bytes(w0_type) || (w2_type != VKV_DTYPE_F16 && w2_type != VKV_DTYPE_F32))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: weight dtypes %d / %d", w0_type, w2_type);
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: workspace not 256-byte aligned");
+    if (workspace_bytes < need)
+        return fail(VKV_STATUS_BUFFER_TOO_SMALL, "ada scale: workspace %zu < %zu bytes", workspace_bytes, need);
+    if ((reinterpret_cast<uintptr_t>(w2) & (w2_type == VKV_DTYPE_F16 ? 1u : 3u)) ||
+        (reinterpret_cast<uintptr_t>(out) & 3u))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: misaligned w2 or out");
+    // the time embedding as the reference computes it on the host
+    // (compute_time_embedding, src/voxtral.cpp:729-740)
+    std::vector<float> emb((size_t)dim);
+    const int32_t half = dim / 2;
+    for (int32_t i = 0; i < half; ++i) {
+        const float inv_freq = expf(-logf(10000.0f) * (float)i / (float)half);
+        const float angle = t * inv_freq;
+        emb[(size_t)i] = cosf(angle);
+        emb[(size_t)(i + half)] = sinf(angle);
+    }
+    float *e_dev = (float *)workspace;
+    float *hidden = (float *)((uint8_t *)workspace + ((size_t)dim * 4 + 255) / 256 * 256);
+    hipStream_t st = as_stream(hip_stream);
+    hipError_t e = hipMemcpyAsync(e_dev, emb.data(), (size_t)dim * 4, hipMemcpyHostToDevice, st);
+    // the host vector must outlive the copy
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "ada scale: time embedding upload");
+    const vkv_mv_out h[1] = {{w0, w0_type, ada_dim, hidden, nullptr}};
+    if (vkv_status s = matvec_impl(e_dev, dim, nullptr, nullptr, 0.0f, h, 1, VKV_MV_GELU, hip_stream,
+                                   nullptr, nullptr))
+        return s;
+    e = launch_rows_small(w2, w2_type == VKV_DTYPE_F16, hidden, ada_dim, dim, out, st);
+    if (e != hipSuccess) return hip_fail(e, "ada scale: second product launch");
+    return ok();
+}
 
 vkv_status vkv_quantize_q8_k(const float *x, int64_t n, const float *norm_w, const float *ada,
                              float eps, void *blocks, void *hip_stream) {

@@ -176,6 +176,8 @@ hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const fl
 hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const float *add, float *y,
                              hipStream_t st, unsigned long long *zero_words = nullptr);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, hipStream_t st);
+hipError_t launch_rows_small(const void *w, bool w_f16, const float *x, int n_in, int n_rows,
+                             float *y, hipStream_t st);
 // The encoder conv stem (vkv_conv.hip)
 hipError_t launch_im2col_f16(const float *in, int64_t stride_c, int64_t stride_t, int in_len,
                              int n_ch, int stride, int pad, int t0, int n_out, void *cols,

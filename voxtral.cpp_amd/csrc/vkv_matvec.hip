@@ -647,6 +647,29 @@ __global__ void __launch_bounds__(256) k_rms_norm_rows(const float *__restrict__
     }
 }
 
+// y[r] = sum_k W[r][k] x[k] for a small f16 or f32 matrix (the ada MLP's
+// second layer, [dim][ada_dim] with ada_dim = 32): the CPU path's vec-dot type
+// for an f16 matrix is f16, so x is rounded to f16 and every product is exact
+// in f32; f32 matrices take x as it is.  One wave per row, lanes over k.
+__global__ void __launch_bounds__(256) k_rows_small(const void *__restrict__ w, int w_f16,
+                                                    const float *__restrict__ x, int n_in,
+                                                    int n_rows, float *__restrict__ y) {
+    const int lane = threadIdx.x & 63;
+    const int row = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n_rows) return;
+    float acc = 0.0f;
+    for (int k = lane; k < n_in; k += 64) {
+        if (w_f16) {
+            const _Float16 a = reinterpret_cast<const _Float16 *>(w)[(int64_t)row * n_in + k];
+            acc += (float)a * (float)(_Float16)x[k];
+        } else {
+            acc += reinterpret_cast<const float *>(w)[(int64_t)row * n_in + k] * x[k];
+        }
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = acc;
+}
+
 // ggml_argmax of f32 (ggml_vec_argmax_f32: the running max MAX(max, x[i]) and
 // idx = i whenever x[i] equals it), i.e. for finite input the last index of
 // the maximum.  One work group; (value, index) pairs reduce by larger value,
@@ -1042,6 +1065,12 @@ hipError_t launch_gemm_kq(const MmArgs &a, int n_tiles, int n_col_tiles, hipStre
 hipError_t launch_rms_norm_rows(const float *x, int n_rows, int n, const float *w, const float *b,
                                 float eps, float *y, int y_ring, int y_row0, hipStream_t st) {
     k_rms_norm_rows<<<n_rows, 256, 0, st>>>(x, n, w, b, eps, y, y_ring, y_row0);
+    return hipGetLastError();
+}
+
+hipError_t launch_rows_small(const void *w, bool w_f16, const float *x, int n_in, int n_rows,
+                             float *y, hipStream_t st) {
+    k_rows_small<<<(unsigned)((n_rows + 3) / 4), 256, 0, st>>>(w, w_f16 ? 1 : 0, x, n_in, n_rows, y);
     return hipGetLastError();
 }
 

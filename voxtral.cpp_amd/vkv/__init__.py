@@ -257,6 +257,9 @@ PROTOTYPES = {
     "vkv_decoder_token_workspace": (ctypes.c_size_t, [_P(DecModel)]),
     "vkv_decoder_token": (_i32, [_vp, _i32, _P(Ring), _P(DecModel), _i32, _vp, _vp, _vp, _vp,
                                  ctypes.c_size_t, _P(Plan), _vp]),
+    "vkv_ada_scale_workspace": (ctypes.c_size_t, [_i32, _i32]),
+    "vkv_ada_scale": (_i32, [_vp, _i32, _vp, _i32, _i32, _i32, _f32, _vp, _vp, ctypes.c_size_t, _vp]),
+    "vkv_model_set_ada": (_i32, [_vp, _f32, _vp, _vp]),
     "vkv_embed": (_i32, [_i32, _vp, _i32, _i64, _i32, _vp, _vp, _vp]),
     "vkv_argmax": (_i32, [_vp, _i64, _vp, _vp]),
     "vkv_gguf_open": (_i32, [ctypes.c_char_p, _P(_vp)]),
@@ -603,6 +606,16 @@ def decoder_token(cache, stream, ring, model, token, audio_ptr, logits_ptr, toke
     return plan
 
 
+def ada_scale_workspace(dim, ada_dim):
+    return lib.vkv_ada_scale_workspace(dim, ada_dim)
+
+
+def ada_scale(w0_ptr, w0_type, w2_ptr, w2_type, dim, ada_dim, t, out_ptr, ws_ptr, ws_bytes,
+              hip_stream=0):
+    check(lib.vkv_ada_scale(w0_ptr, w0_type, w2_ptr, w2_type, dim, ada_dim, t, out_ptr, ws_ptr,
+                            ws_bytes, hip_stream))
+
+
 def argmax(x_ptr, n, out_ptr, hip_stream=0):
     check(lib.vkv_argmax(x_ptr, n, out_ptr, hip_stream))
 
@@ -744,6 +757,12 @@ class Model:
         self.handle = h
         self._free = lib.vkv_model_free
         self.view = ModelView()
+        check(lib.vkv_model_get_view(self.handle, ctypes.byref(self.view)))
+
+    def set_ada(self, t, scales_ptr, hip_stream=0):
+        """every decoder layer's ada scale at time t into scales [layers][dim];
+        the view's layers point at them afterwards"""
+        check(lib.vkv_model_set_ada(self.handle, t, scales_ptr, hip_stream))
         check(lib.vkv_model_get_view(self.handle, ctypes.byref(self.view)))
 
     def tensor(self, name):
