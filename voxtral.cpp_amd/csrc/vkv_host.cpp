@@ -1126,10 +1126,19 @@ struct RowMap {
     int32_t ring = 0, row0 = 0;
 };
 
+// RoPE of the outputs whose bit is set in mask (ggml mode 0, head_dim-wide
+// heads, position pos0 + input row), fused into the products' epilogue
+struct MmRope {
+    uint32_t mask = 0;
+    int32_t head_dim = 0;
+    int64_t pos0 = 0;
+    float theta = 0.0f;
+};
+
 vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float *norm_w,
                        const float *norm_b, const float *ada, float eps, const vkv_mm_out *outs,
                        int32_t n_outs, int32_t epilogue, void *workspace, size_t workspace_bytes,
-                       void *hip_stream, RowMap in_rows, RowMap out_rows);
+                       void *hip_stream, RowMap in_rows, RowMap out_rows, MmRope rope = MmRope{});
 }  // namespace
 
 size_t vkv_matmul_workspace(int32_t n_cols, int64_t n_in) {
@@ -1149,7 +1158,7 @@ namespace {
 vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float *norm_w,
                        const float *norm_b, const float *ada, float eps, const vkv_mm_out *outs,
                        int32_t n_outs, int32_t epilogue, void *workspace, size_t workspace_bytes,
-                       void *hip_stream, RowMap in_rows, RowMap out_rows) {
+                       void *hip_stream, RowMap in_rows, RowMap out_rows, MmRope rope) {
     if (vkv_status st = check_mv_input("matmul", x, n_in, norm_w, ada)) return st;
     if (norm_b && !norm_w) return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: norm_b requires norm_w");
     if (vkv_status st = check_aligned("matmul", {norm_b})) return st;
@@ -1203,6 +1212,19 @@ vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float
     a.gelu = gelu ? 1 : 0;
     a.y_ring = out_rows.ring;
     a.y_row0 = out_rows.row0;
+    if (rope.mask) {
+        if (epilogue != VKV_MV_STORE || rope.head_dim < 2 || rope.head_dim % 2 || rope.head_dim > 16 * 1024)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: RoPE takes plain outputs and an even head_dim");
+        for (int32_t k = 0; k < n_outs; ++k) {
+            if (!(rope.mask >> k & 1u)) continue;
+            if (outs[k].add || outs[k].n_rows % rope.head_dim)
+                return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: RoPE output %d shape", k);
+            a.out[k].rope = 1;
+        }
+        a.rope_ts = rope_theta_scale(rope.theta, rope.head_dim);
+        a.rope_hd = rope.head_dim;
+        a.rope_pos0 = rope.pos0;
+    }
     e = launch_gemm_kq(a, (int)tiles, (n_cols + 15) / 16, as_stream(hip_stream));
     if (e != hipSuccess) return hip_fail(e, "matmul launch");
     return ok();
@@ -1624,21 +1646,17 @@ vkv_status encoder_chunk_impl(vkv_cache *cache, int32_t stream, const vkv_enc_pl
         const vkv_mm_out qkv[3] = {{L.attn_q, L.attn_q_type, qd, q, nullptr, L.attn_q_b},
                                    {L.attn_k, L.attn_k_type, kvd, k, nullptr, nullptr},
                                    {L.attn_v, L.attn_v_type, kvd, t.v, nullptr, L.attn_v_b}};
-        if (vkv_status s = vkv_matmul(x, N, m.dim, L.attn_norm, L.attn_norm_b, nullptr, m.norm_eps,
-                                      qkv, 3, VKV_MV_STORE, t.image, t.image_bytes, hip_stream))
+        // RoPE of the q and k rows at positions q_start + r, in the
+        // products' epilogue (vkv_rope's arithmetic, so the same bits)
+        MmRope rope;
+        rope.mask = 3u;
+        rope.head_dim = m.head_dim;
+        rope.pos0 = plan->q_start;
+        rope.theta = m.rope_theta;
+        if (vkv_status s = matmul_impl(x, N, m.dim, L.attn_norm, L.attn_norm_b, nullptr, m.norm_eps,
+                                       qkv, 3, VKV_MV_STORE, t.image, t.image_bytes, hip_stream,
+                                       RowMap{}, RowMap{}, rope))
             return s;
-        // RoPE of the q and k rows at positions q_start + r (one launch when the
-        // widths agree, as in the MHA encoder)
-        if (qd == kvd) {
-            if (vkv_status s = vkv_rope(t.qk, 2, N, qd, m.head_dim, plan->q_start, m.rope_theta,
-                                        hip_stream))
-                return s;
-        } else {
-            if (vkv_status s = vkv_rope(q, 1, N, qd, m.head_dim, plan->q_start, m.rope_theta, hip_stream))
-                return s;
-            if (vkv_status s = vkv_rope(k, 1, N, kvd, m.head_dim, plan->q_start, m.rope_theta, hip_stream))
-                return s;
-        }
         if (vkv_status s = vkv_enc_step(cache, stream, plan, window, l, 1, q, k, t.v, t.attn,
                                         m.n_heads, scale, hip_stream))
             return s;

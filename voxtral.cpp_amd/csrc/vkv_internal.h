@@ -151,6 +151,7 @@ struct MmOut {
     const float *bias;     // nullable: [n_rows]
     int32_t dtype, n_rows;
     int32_t tile0;         // first 16-row tile of this matrix
+    int32_t rope;          // rows rotated by RoPE (ggml mode 0) after the bias
 };
 
 struct MmArgs {
@@ -162,6 +163,12 @@ struct MmArgs {
     // Input row p's output (and residual) row: (y_row0 + p) % y_ring when
     // y_ring > 0 (rows of a ring buffer), else p.
     int32_t y_ring, y_row0;
+    // RoPE of the outputs with MmOut::rope: pairs (2i, 2i+1) of each
+    // rope_hd-wide head at position rope_pos0 + input row, angle
+    // pos * rope_ts^i (vkv_rope's arithmetic)
+    float rope_ts;
+    int32_t rope_hd;
+    int64_t rope_pos0;
     MmOut out[kMvMaxOuts];
 };
 

@@ -114,6 +114,52 @@ __device__ __forceinline__ int wave_min_i(int x) {
     return min(min(lane_i(x, 0), lane_i(x, 16)), min(lane_i(x, 32), lane_i(x, 48)));
 }
 
+// One Q8_K block held by a wave, lane l with elements 4l..4l+3: the codes
+// packed 4 per lane, the sums of 16 (lanes 4k..4k+3 hold the same) and of 32
+// codes (lanes 8k..8k+7), and d.  ggml quantize_row_q8_K_ref: iscale = -127 /
+// (the first element of largest |h|), code = min(127, rint(iscale * h)),
+// d = 1 / iscale; an all-zero block gives zero codes and d = 0.
+struct QBlock {
+    uint32_t packed;
+    int s16, s32;
+    float d;
+};
+
+__device__ __forceinline__ QBlock q8k_block(const float (&e)[4], int lane) {
+#pragma clang fp contract(off)
+    // first element of largest magnitude (|h| > running max, in order)
+    float am = 0.0f;
+    int ai = 0x7fffffff;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (fabsf(e[k]) > am) {
+            am = fabsf(e[k]);
+            ai = 4 * lane + k;
+        }
+    const uint32_t wm = wave_max_u(__builtin_bit_cast(uint32_t, am));
+    const int wi = wave_min_i((__builtin_bit_cast(uint32_t, am) == wm && wm != 0u) ? ai : 0x7fffffff);
+    int q[4] = {0, 0, 0, 0};
+    QBlock r;
+    r.d = 0.0f;
+    if (wm != 0u) {
+        const int k = wi & 3;
+        const float mine = k == 0 ? e[0] : k == 1 ? e[1] : k == 2 ? e[2] : e[3];
+        const float mx = lane_f(mine, wi >> 2);
+        const float iscale = -127.0f / mx;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[j] = min(127, (int)__builtin_rintf(iscale * e[j]));
+        r.d = 1.0f / iscale;
+    }
+    r.packed = (uint32_t)(q[0] & 255) | (uint32_t)(q[1] & 255) << 8 | (uint32_t)(q[2] & 255) << 16 |
+               (uint32_t)(q[3] & 255) << 24;
+    int s = q[0] + q[1] + q[2] + q[3];
+    s += dppi<0xB1>(s);
+    s += dppi<0x4E>(s);               // sum of 16 (lanes 4k..4k+3)
+    r.s16 = s;
+    r.s32 = s + dppi<0x141>(s);
+    return r;
+}
+
 // Q8_K quantization of rms_norm(x) * norm_w (* (1 + ada)), or of x itself
 // (norm_w == nullptr).  Wave w handles blocks w, w + 4, ...; each lane 4
 // consecutive elements of a block.  Rounding follows the CPU path step by
@@ -210,35 +256,10 @@ __device__ __forceinline__ void act_finish(const ActRegs<NBW, NE> &r, int n,
                 }
             }
         }
-        // first element of largest magnitude (|h| > running max, in order)
-        float am = 0.0f;
-        int ai = 0x7fffffff;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            if (fabsf(e[k]) > am) {
-                am = fabsf(e[k]);
-                ai = 4 * lane + k;
-            }
-        const uint32_t wm = wave_max_u(__builtin_bit_cast(uint32_t, am));
-        const int wi = wave_min_i((__builtin_bit_cast(uint32_t, am) == wm && wm != 0u) ? ai
-                                                                                        : 0x7fffffff);
-        int q[4] = {0, 0, 0, 0};
-        float d = 0.0f;
-        if (wm != 0u) {
-            const int k = wi & 3;
-            const float mine = k == 0 ? e[0] : k == 1 ? e[1] : k == 2 ? e[2] : e[3];
-            const float mx = lane_f(mine, wi >> 2);
-            const float iscale = -127.0f / mx;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) q[j] = min(127, (int)__builtin_rintf(iscale * e[j]));
-            d = 1.0f / iscale;
-        }
-        const uint32_t packed = (uint32_t)(q[0] & 255) | (uint32_t)(q[1] & 255) << 8 |
-                                (uint32_t)(q[2] & 255) << 16 | (uint32_t)(q[3] & 255) << 24;
-        int s = q[0] + q[1] + q[2] + q[3];
-        s += dppi<0xB1>(s);
-        s += dppi<0x4E>(s);               // sum of 16 (lanes 4k..4k+3)
-        const int s32 = s + dppi<0x141>(s);
+        const QBlock qb = q8k_block(e, lane);
+        const uint32_t packed = qb.packed;
+        const int s = qb.s16, s32 = qb.s32;
+        const float d = qb.d;
         const int k16 = lane >> 2;        // 16-group 8n + 2g + h
         if (gout) {
             uint8_t *blk = gout + (size_t)b * 292;
@@ -721,9 +742,11 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, in
 //   k_q8k_rows -- the Q8_K image of every input row (one work group per row,
 //                 same input side as k_matvec), to global memory: codes
 //                 [p][K], block scales [p][K/256], 32-element sums [p][K/32].
-//   k_gemm_kq  -- a work group owns 16 weight rows x 16 input rows; its eight
-//                 waves split the 256-blocks of K (each with the next block's
-//                 loads in flight) and meet in LDS.  One
+//   k_gemm_kq  -- a work group owns 16 weight rows x 16 input rows; its 8
+//                 (or 16) waves split the 256-blocks of K and meet in LDS.
+//                 A wave holds one block's fragments (about 100 VGPRs), so
+//                 two work groups share a CU and hide each other's load
+//                 latency.  One
 //                 v_mfma_i32_16x16x32_i8 per 32 weights: A = 16 rows' codes
 //                 (lane (kg, r): row r, k = 8kg..8kg+7), B = 16 input rows'
 //                 Q8_K codes, C = exact int32 sums, row m = 4kg + i of lane
@@ -927,13 +950,24 @@ __device__ __forceinline__ void gemm_compute(const GFragQ6 &f, const GFragX &x, 
     for (int i = 0; i < 4; ++i) acc[i] += (h2f(hd[i][0]) * x.dx) * (float)isum[i];
 }
 
-constexpr int kGemmWaves = 8;
+// RoPE (ggml mode 0) of one element of a pair in the products' epilogue,
+// with vkv_rope's arithmetic: the angle pos * ts^pair by the running f32
+// product, cos/sin in double rounded to f32, no contraction
+__device__ __forceinline__ float rope_elem(float self, float partner, bool odd, int pair, float pos,
+                                           float ts) {
+#pragma clang fp contract(off)
+    float theta = pos;
+    for (int i = 0; i < pair; ++i) theta *= ts;
+    const float c = (float)cos((double)theta), sn = (float)sin((double)theta);
+    return odd ? partner * sn + self * c : self * c - partner * sn;
+}
 
-template <bool Q4>
+// Waves per work group: 8, or 16 when a call has few 16-row tiles (the
+// 1280-row products of a 16-frame chunk are 80 work groups): more waves split
+// the same K, so each walks a shorter chain of blocks.
+template <bool Q4, int W>
 __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, const MmOut &o1,
-                                          uint32_t (*hdr)[16][6],
-                                          float (*red)[kGemmWaves][16][17]) {
-    constexpr int W = kGemmWaves;
+                                          uint32_t (*hdr)[16][6], float (*red)[W][16][17]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kg = lane >> 4, rr = lane & 15;
     const bool swiglu = a.swiglu != 0;
     const int mats = swiglu ? 2 : 1;
@@ -953,29 +987,13 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
     const __amdgpu_buffer_rsrc_t rs = m ? rs1 : rs0;
     float acc[4] = {0, 0, 0, 0};
     using GF = std::conditional_t<Q4, GFragQ4, GFragQ6>;
-    // two register sets, A and B, alternate between the wave's blocks
-    // b, b + kw, b + 2 kw, ...: the next block's loads are in flight while the
-    // current one is computed, and no set is copied
-    GF wa, wb;
-    GFragX xa, xb;
+    // the wave's blocks b, b + kw, b + 2 kw, ...: one set of fragments
+    // (occupancy, not a second register set, covers the load latency)
     auto boff = [&](int b) { return (uint32_t)row * rbytes + (uint32_t)b * bbytes; };
-    int b = wm;
-    if (b < nb) {
-        wa = gemm_load_w<Q4>(rs, boff(b), kg);
-        xa = gemm_load_x<Q4>(a, col, b, kg);
-    }
-    for (; b < nb; b += 2 * kw) {
-        if (b + kw < nb) {
-            wb = gemm_load_w<Q4>(rs, boff(b + kw), kg);
-            xb = gemm_load_x<Q4>(a, col, b + kw, kg);
-        }
-        gemm_compute(wa, xa, hdr[wave], kg, rr, acc);
-        if (b + kw >= nb) break;
-        if (b + 2 * kw < nb) {
-            wa = gemm_load_w<Q4>(rs, boff(b + 2 * kw), kg);
-            xa = gemm_load_x<Q4>(a, col, b + 2 * kw, kg);
-        }
-        gemm_compute(wb, xb, hdr[wave], kg, rr, acc);
+    for (int b = wm; b < nb; b += kw) {
+        const GF w = gemm_load_w<Q4>(rs, boff(b), kg);
+        const GFragX x = gemm_load_x<Q4>(a, col, b, kg);
+        gemm_compute(w, x, hdr[wave], kg, rr, acc);
     }
     // the waves' partial sums meet in LDS: red[matrix][wave of that matrix][row][input row]
 #pragma unroll
@@ -999,6 +1017,14 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
                 y = silu(v0) * v1;
             } else if (a.gelu) {
                 y = gelu_erf(v0);
+            } else if (o0.rope) {
+                // the pair's other row is in this tile: its sum and bias
+                const int pr = r ^ 1;
+                float vp = 0.0f;
+                for (int w = 0; w < kw; ++w) vp += red[0][w][pr][c];
+                if (o0.bias) vp = vp + o0.bias[row0 + pr];
+                y = rope_elem(v0, vp, (orow & 1) != 0, (orow % a.rope_hd) >> 1,
+                              (float)(a.rope_pos0 + ocol), a.rope_ts);
             } else {
                 y = o0.add ? o0.add[at] + v0 : v0;
             }
@@ -1007,9 +1033,10 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
     }
 }
 
-__global__ void __launch_bounds__(64 * kGemmWaves) k_gemm_kq(MmArgs a) {
-    __shared__ uint32_t hdr[kGemmWaves][16][6];
-    __shared__ float red[2][kGemmWaves][16][17];
+template <int W>
+__global__ void __launch_bounds__(64 * W) k_gemm_kq(MmArgs a) {
+    __shared__ uint32_t hdr[W][16][6];
+    __shared__ float red[2][W][16][17];
     int seg = 0;
 #pragma unroll
     for (int k = 1; k < kMvMaxOuts; ++k)
@@ -1017,8 +1044,8 @@ __global__ void __launch_bounds__(64 * kGemmWaves) k_gemm_kq(MmArgs a) {
     const MmOut o0 = mm_out_at(a, seg);
     const MmOut o1 = a.swiglu ? a.out[1] : o0;
     // one weight dtype per work group (both SwiGLU matrices share it)
-    if (o0.dtype == VKV_DTYPE_Q4_K) gemm_body<true>(a, o0, o1, hdr, red);
-    else gemm_body<false>(a, o0, o1, hdr, red);
+    if (o0.dtype == VKV_DTYPE_Q4_K) gemm_body<true, W>(a, o0, o1, hdr, red);
+    else gemm_body<false, W>(a, o0, o1, hdr, red);
 }
 
 }  // namespace
@@ -1058,7 +1085,8 @@ hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_r
 
 hipError_t launch_gemm_kq(const MmArgs &a, int n_tiles, int n_col_tiles, hipStream_t st) {
     const dim3 grid((unsigned)n_tiles, (unsigned)n_col_tiles);
-    k_gemm_kq<<<grid, 64 * kGemmWaves, 0, st>>>(a);
+    if ((int64_t)n_tiles * n_col_tiles < 128) k_gemm_kq<16><<<grid, 1024, 0, st>>>(a);
+    else k_gemm_kq<8><<<grid, 512, 0, st>>>(a);
     return hipGetLastError();
 }
 
