@@ -656,26 +656,35 @@ def encoder_bytes_per_chunk(n_keys):
     return E_LAYERS * per_layer
 
 
-def timed_loop(step, steps, warmup, st):
+def timed_loop(step, steps, warmup, st, every=8):
+    """W untimed steps, then K timed steps between a synchronize and two
+    events on the launch stream; every `every`-th timed step is also
+    bracketed by its own pair of events (an event costs a few microseconds of
+    GPU time, so bracketing every step would slow the timed region)."""
     import torch
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * steps)]
+    marks = [i for i in range(steps) if i % every == 0]
+    ev = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for i in marks}
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     t_start.record(st)
     for i in range(steps):
-        ev[2 * i].record(st)
-        step(warmup + i)
-        ev[2 * i + 1].record(st)
+        if i in ev:
+            ev[i][0].record(st)
+            step(warmup + i)
+            ev[i][1].record(st)
+        else:
+            step(warmup + i)
     t_end.record(st)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_start.elapsed_time(t_end)
-    step_ms = [ev[2 * i].elapsed_time(ev[2 * i + 1]) for i in range(steps)]
+    step_ms = [ev[i][0].elapsed_time(ev[i][1]) for i in marks]
     return total_ms, step_ms, wall
 
 
@@ -812,9 +821,11 @@ def gpu_encoder(steps, warmup):
     return total_ms, step_ms, wall, n_keys
 
 
-def cpu_leg(dtype, target_seconds):
+def cpu_leg(dtype, target_seconds, layers=LAYERS, n_keys=CAP, streams=1, label=None):
     """The oracle's threaded ggml-CPU restatement of the same step (append +
-    attention over 8192 positions, 26 layers) on a bounded number of tokens."""
+    attention over n_keys positions, `layers` layers) on a bounded number of
+    tokens; with several streams the CPU runs them one after another, so the
+    aggregate rate is the single-stream one."""
     from concurrent.futures import ThreadPoolExecutor
 
     import numpy as np
@@ -823,34 +834,36 @@ def cpu_leg(dtype, target_seconds):
 
     threads = min(os.cpu_count() or 1, 16)
     rb = oracle.row_bytes(dtype, KV_DIM)
-    layer_bytes = rb * CAP
-    kimg = np.empty(LAYERS * layer_bytes, np.uint8)
-    vimg = np.empty(LAYERS * layer_bytes, np.uint8)
+    layer_bytes = rb * n_keys
+    kimg = np.empty(layers * layer_bytes, np.uint8)
+    vimg = np.empty(layers * layer_bytes, np.uint8)
 
     def fill(job):
         img, tag, l = job
         img[l * layer_bytes:(l + 1) * layer_bytes] = oracle.expected_layer(
-            dtype, CAP, CAP, KV_DIM, CAP, SEED, tag, 0, l)
+            dtype, n_keys, n_keys, KV_DIM, n_keys, SEED, tag, 0, l)
 
     with ThreadPoolExecutor(threads) as pool:
         list(pool.map(fill, [(img, tag, l) for img, tag in ((kimg, oracle.TAG_K), (vimg, oracle.TAG_V))
-                             for l in range(LAYERS)]))
+                             for l in range(layers)]))
     scale = 1.0 / (HD ** 0.5)
     secs, n = 0.0, 0
     while n < 1 or (secs < target_seconds and n < 64):
-        pos = CAP + n
-        qs = np.stack([oracle.synth_row(SEED, oracle.TAG_Q, 0, l, pos, Q_DIM) for l in range(LAYERS)])
-        ks = np.stack([oracle.synth_row(SEED, oracle.TAG_K, 0, l, pos, KV_DIM) for l in range(LAYERS)])
-        vs = np.stack([oracle.synth_row(SEED, oracle.TAG_V, 0, l, pos, KV_DIM) for l in range(LAYERS)])
-        dt, _ = oracle.decode_step_mimic_mt(dtype, kimg, vimg, layer_bytes, rb, LAYERS, CAP, qs,
-                                            QH, KVH, HD, scale, threads, ks, vs, pos % CAP)
+        pos = n_keys + n
+        qs = np.stack([oracle.synth_row(SEED, oracle.TAG_Q, 0, l, pos, Q_DIM) for l in range(layers)])
+        ks = np.stack([oracle.synth_row(SEED, oracle.TAG_K, 0, l, pos, KV_DIM) for l in range(layers)])
+        vs = np.stack([oracle.synth_row(SEED, oracle.TAG_V, 0, l, pos, KV_DIM) for l in range(layers)])
+        dt, _ = oracle.decode_step_mimic_mt(dtype, kimg, vimg, layer_bytes, rb, layers, n_keys, qs,
+                                            QH, KVH, HD, scale, threads, ks, vs, pos % n_keys)
         secs += dt
         n += 1
     name = "f16" if dtype == 1 else "q8_0"
+    what = label or f"{layers} layers, {n_keys}-position window, {name} KV"
     return {"value": n / secs, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps (26 layers, 8192-position window, {name} KV, 1 stream) "
-                      f"of the oracle's restatement of ggml's CPU flash-attention step, "
-                      f"{threads} threads, {secs:.1f} s"}
+            "sample": f"{n} decode steps ({what}) of the oracle's restatement of ggml's CPU "
+                      f"flash-attention step, {threads} threads, {secs:.1f} s"
+                      + (f"; the {streams} streams run one after another on the CPU, so the "
+                         f"aggregate rate equals one stream's" if streams > 1 else "")}
 
 
 def load_traffic(name):
@@ -1047,10 +1060,19 @@ def main():
         res["cpu_baseline"] = cpu_adapter_leg(wl["groups"], args.cpu_seconds)
     elif not args.no_cpu and args.workload == "model_load_q4km":
         res["cpu_baseline"] = cpu_load_leg(args.cpu_seconds)
+    elif not args.no_cpu and args.workload == "layer1_f16":
+        res["cpu_baseline"] = cpu_leg(1, args.cpu_seconds, layers=1, n_keys=1025,
+                                      label="1 layer, 1025 positions, f16 KV")
+    elif not args.no_cpu and args.workload == "stream4096_f16":
+        # the CPU step's time is linear in the window: the run's mean window
+        # (steps 0..4095 attend 1..4096 keys) stands for the run
+        res["cpu_baseline"] = cpu_leg(1, args.cpu_seconds, n_keys=2048,
+                                      label="26 layers at the run's mean window of 2048 positions, "
+                                            "f16 KV")
     elif not args.no_cpu and args.workload not in ("encoder_f16", "encoder_chunk_q4km",
                                                    "adapter_q4km", "adapter_group_q4km",
                                                    "model_load_q4km"):
-        res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds)
+        res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds, streams=wl["streams"])
     print(json.dumps(res), flush=True)
 
 
