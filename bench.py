@@ -44,6 +44,11 @@ Other workloads (--workload), reported on the same contract:
                tensor names, dims and quantization mix; synthetic bytes)
                written to $TMPDIR once, then vkv_model_load into one device
                allocation per step (file in the page cache); GB/s.
+  realtime_step_q4km  one 80 ms step of the streaming path: conv stem +
+               encoder over 4 new frames into the encoder-output ring, the
+               adapter over the completed group, one decoder token reading its
+               audio row (full 8192-slot ring); steps/s (x 0.08 = the
+               realtime factor).
   decoder_token_q4km  one whole decoder token through vkv_decoder_token:
                embedding + audio row, 26 x (RMSNorm+QKV, RoPE + K/V append +
                attention over the full 8192-slot F16 ring, O + residual,
@@ -105,6 +110,10 @@ WORKLOADS = {
                             streams=1, pmc="",
                             data="synthetic (a full-size realtime Q4_K_M GGUF file of random "
                                  "bytes, written to local disk before timing)"),
+    "realtime_step_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights, f16 KV, f32 rings",
+                               streams=1, pmc="",
+                               data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) Mel windows "
+                                    "and KV rows, generated on device)"),
     "decoder_weights_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k (int8 dot)", streams=1,
                                  pmc="matvec_q4km_26l_pmc.json",
                                  data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs, "
@@ -425,22 +434,21 @@ def cpu_load_leg(target_seconds):
                       f"reference's CPU-backend load does, 1 thread, {secs:.1f} s"}
 
 
-def encoder_chunk_bytes(n_keys):
+def encoder_chunk_bytes(n_keys, P=E_CHUNK):
     """conv stem weights (f16) + 32 layers' weights + the window attention's
     bytes for one chunk"""
     conv = 2 * 1280 * 3 * (128 + 1280)
     w = E_LAYERS * sum(mat_bytes(dt, r, n) for _, dt, r, n in ENC_MATS)
-    return conv + w + encoder_bytes_per_chunk(n_keys)
+    return conv + w + encoder_bytes_per_chunk(n_keys, P)
 
 
-def gpu_encoder_chunk(steps, warmup):
+def encoder_setup(gen, sp):
+    """Random Q4_K_M encoder weights on the device, their vkv_enc_model, and an
+    encoder cache whose ring holds frames [0, 768) (the steady state); returns
+    (model, cache, keep)."""
     import torch
     import vkv
 
-    st = torch.cuda.current_stream()
-    sp = st.cuda_stream
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(SEED)
     keep = []
     layers = (vkv.EncLayer * E_LAYERS)()
 
@@ -475,6 +483,20 @@ def gpu_encoder_chunk(steps, warmup):
                        np_=E_CHUNK, hip_stream=sp)
         cache.append(0, 0, E_LAYERS, vkv.plan_segs(plan.write_seg, plan.write_nseg), k.data_ptr(),
                      v.data_ptr(), hip_stream=sp)
+    torch.cuda.synchronize()
+    return model, cache, (keep, layers)
+
+
+def gpu_encoder_chunk(steps, warmup):
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED)
+    model, cache, keep = encoder_setup(gen, sp)
+    first = (E_WIN + E_CHUNK - 1) // E_CHUNK + 1
     T = warmup + steps
     plans = [vkv.enc_plan((first + i) * E_CHUNK, E_CHUNK, E_CAP, E_WIN) for i in range(T)]
     # the conv stem's f16 weights and each chunk's Mel window [128][2 * 16 + 4]
@@ -504,6 +526,85 @@ def gpu_encoder_chunk(steps, warmup):
     n_keys = plans[0].win_end - plans[0].win_start
     cache.close()
     del keep
+    return total_ms, step_ms, wall, n_keys
+
+
+R_FRAMES = 4   # encoder frames per realtime step (the steady physical 4-row launch)
+
+
+def gpu_realtime_step(steps, warmup):
+    """One 80 ms realtime step: the conv stem and the encoder over 4 new frames
+    into the encoder-output ring, the adapter over the completed group into
+    the audio-embedding ring, and one decoder token reading that row
+    (26 layers, the full 8192-slot ring)."""
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED)
+    emodel, ecache, ekeep = encoder_setup(gen, sp)
+    dmodel, dkeep = device_model(gen)
+    dcache = vkv.Cache(n_streams=1, n_layers=LAYERS, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
+                       n_q_heads=QH, dtype=vkv.F16)
+    ring = vkv.new_ring(CAP)
+    plan = vkv.decoder_plan(ring, 0, CAP)
+    k0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
+    v0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
+    vkv.synth_rows(k0.data_ptr(), KV_DIM, SEED, vkv.TAG_K, nl=LAYERS, p0=0, np_=CAP, hip_stream=sp)
+    vkv.synth_rows(v0.data_ptr(), KV_DIM, SEED, vkv.TAG_V, nl=LAYERS, p0=0, np_=CAP, hip_stream=sp)
+    dcache.append(0, 0, LAYERS, vkv.plan_segs(plan.write_seg, plan.write_nseg), k0.data_ptr(),
+                  v0.data_ptr(), hip_stream=sp)
+    vkv.decoder_commit(ring, plan)
+    torch.cuda.synchronize()
+    del k0, v0
+    ad_w0 = random_kq_device(12, DIM, 1280 * A_DOWN, gen)
+    ad_w2 = random_kq_device(12, DIM, DIM, gen)
+    ad = vkv.Adapter(ad_w0.data_ptr(), ad_w2.data_ptr(), 12, 12, 1280, DIM, A_DOWN)
+    enc_out = torch.zeros(A_RING, 1280, device="cuda")
+    aemb = torch.zeros(A_RING, DIM, device="cuda")
+    er = vkv.RowRing(enc_out.data_ptr(), A_RING, 1280)
+    ar = vkv.RowRing(aemb.data_ptr(), A_RING, DIM)
+    q0 = ((E_WIN + E_CHUNK - 1) // E_CHUNK + 1) * E_CHUNK   # frames the ring already holds
+    T = warmup + steps
+    plans = [vkv.enc_plan(q0 + R_FRAMES * i, R_FRAMES, E_CAP, E_WIN) for i in range(T)]
+    conv_len = plans[0].conv_mel_end - plans[0].conv_mel_start
+    w0 = (torch.randn(1280, 128, 3, device="cuda", generator=gen) * 0.05).half()
+    w1 = (torch.randn(1280, 1280, 3, device="cuda", generator=gen) * 0.02).half()
+    b0 = torch.randn(1280, device="cuda", generator=gen) * 0.1
+    b1 = torch.randn(1280, device="cuda", generator=gen) * 0.1
+    mel = torch.randn(T, 128, conv_len, device="cuda", generator=gen)
+    x = torch.empty(R_FRAMES, 1280, device="cuda")
+    ewb = vkv.encoder_chunk_workspace(emodel, R_FRAMES)
+    ews = torch.empty(ewb // 4 + 64, device="cuda")
+    cb = vkv.enc_conv_stem_workspace(conv_len, 128, 1280, R_FRAMES)
+    cws = torch.empty(cb // 4 + 64, device="cuda")
+    awb = vkv.adapter_workspace(ad, 1)
+    aws = torch.empty(awb // 4 + 64, device="cuda")
+    twb = vkv.decoder_token_workspace(dmodel)
+    tws = torch.empty(twb // 4 + 64, device="cuda")
+    logits = torch.empty(VOCAB, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    al = lambda t: (t.data_ptr() + 255) & ~255
+
+    def step(i):
+        p = plans[i]
+        vkv.enc_conv_stem(mel[i].data_ptr(), 128, p, w0.data_ptr(), b0.data_ptr(), w1.data_ptr(),
+                          b1.data_ptr(), 1280, x.data_ptr(), al(cws), cb, hip_stream=sp)
+        vkv.encoder_chunk_ring(ecache, 0, p, E_WIN, emodel, x.data_ptr(), er, al(ews), ewb,
+                               hip_stream=sp)
+        g = (p.q_start + R_FRAMES) // A_DOWN - 1          # the group these frames complete
+        vkv.adapter_commit(ad, er, ar, g, 1, al(aws), awb, hip_stream=sp)
+        vkv.decoder_token(dcache, 0, ring, dmodel, 32, aemb[g % A_RING].data_ptr(),
+                          logits.data_ptr(), tok.data_ptr(), al(tws), twb, hip_stream=sp)
+
+    total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
+    assert bool(torch.isfinite(logits).all()) and bool(torch.isfinite(aemb).all())
+    n_keys = plans[0].win_end - plans[0].win_start
+    ecache.close()
+    dcache.close()
+    del ekeep, dkeep
     return total_ms, step_ms, wall, n_keys
 
 
@@ -647,10 +748,9 @@ def decode_bytes_per_stream_token(n_valid, dtype):
     return int(LAYERS * per_layer)
 
 
-def encoder_bytes_per_chunk(n_keys):
+def encoder_bytes_per_chunk(n_keys, P=E_CHUNK):
     """Per layer: K+V read of the window keys, new K/V f32 read, appended rows
     (f16) write, Q read, output write -- times the layer count."""
-    P = E_CHUNK
     per_layer = (n_keys * 2 * E_DIM * 2 + P * E_DIM * 4 * 2 + P * E_DIM * 2 * 2 + P * E_DIM * 4 +
                  P * E_DIM * 4)
     return E_LAYERS * per_layer
@@ -970,6 +1070,19 @@ def main():
                               f"{len(realtime_tensor_list())} tensors)",
                   "bytes_per_load": data_bytes, "staging": "3 x 64 MiB pinned buffers"}
         kernel = "hipMemcpyAsync host-to-device copies (no kernels)"
+    elif args.workload == "realtime_step_q4km":
+        total_ms, step_ms, wall, n_keys = gpu_realtime_step(args.steps, args.warmup)
+        bytes_step = (encoder_chunk_bytes(n_keys, R_FRAMES) + adapter_bytes(1) + token_bytes())
+        units_per_step = 1
+        res = {"metric": "realtime steps/s (one 80 ms audio step: 4 encoder frames, 1 adapter "
+                         "group, 1 decoder token) and HBM GB/s", "unit": "steps/s"}
+        config = {"workload": "one realtime step of the streaming path: conv stem + vkv_encoder_"
+                              "chunk_ring over 4 new frames (32 layers, window 750), "
+                              "vkv_adapter_commit of the completed group, vkv_decoder_token "
+                              "reading its audio row (26 layers, full 8192-slot f16 ring, logits, "
+                              "argmax); Q4_K_M weights",
+                  "audio_ms_per_step": 80, "bytes_per_step": bytes_step}
+        kernel = "whole step (encoder, adapter and decoder launches)"
     elif args.workload == "decoder_token_q4km":
         total_ms, step_ms, wall = gpu_token(args.steps, args.warmup)
         bytes_step = token_bytes()
@@ -1071,7 +1184,7 @@ def main():
                                             "f16 KV")
     elif not args.no_cpu and args.workload not in ("encoder_f16", "encoder_chunk_q4km",
                                                    "adapter_q4km", "adapter_group_q4km",
-                                                   "model_load_q4km"):
+                                                   "model_load_q4km", "realtime_step_q4km"):
         res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds, streams=wl["streams"])
     print(json.dumps(res), flush=True)
 
