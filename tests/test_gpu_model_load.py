@@ -249,3 +249,40 @@ def test_a_realtime_step_from_the_loaded_model(model_file):
     assert np.isnan(enc_out[16:]).all() and np.isnan(aemb[4:]).all()
     assert all(0 <= t < VOCAB for t in toks[:4])
     m.close()
+
+
+def small_file(tmp_path, name, edit=None, arch="voxtral_realtime"):
+    from test_gguf import small_model
+    kvs, tensors = small_model(np.random.default_rng(7))
+    kvs = [(k, t, arch if k == "general.architecture" else v) for k, t, v in kvs]
+    if edit:
+        tensors = edit(tensors)
+    p = tmp_path / name
+    p.write_bytes(gguf_bytes(kvs, tensors))
+    return str(p)
+
+
+def test_model_errors(tmp_path):
+    """the loader's model errors (voxtral_model_load's MODEL_ERROR): the
+    offline architecture, a missing required tensor, a matrix of a type the
+    products do not take, a tensor of the wrong shape; a small realtime file
+    loads"""
+    m = vkv.Model(small_file(tmp_path, "ok.gguf"), hip_stream=stream_ptr())
+    assert m.view.hp.dec_dim == 256 and m.view.dec.layers[1].attn_q is not None
+    m.close()
+    cases = {
+        "offline.gguf": (None, "voxtral", "offline"),
+        "missing.gguf": (lambda T: [t for t in T if t[0] != "dec.blk.1.ffn_w2.weight"], "voxtral_realtime",
+                         "dec.blk.1.ffn_w2.weight"),
+        "f16mat.gguf": (lambda T: [(n, 1, ne, np.zeros(ne[0] * ne[1] * 2, np.uint8).tobytes())
+                                   if n == "enc.blk.0.attn_o.weight" else (n, t, ne, b)
+                                   for n, t, ne, b in T], "voxtral_realtime", "Q4_K and Q6_K"),
+        "shape.gguf": (lambda T: [(n, t, [ne[0] // 2], b[:len(b) // 2]) if n == "norm.weight"
+                                  else (n, t, ne, b) for n, t, ne, b in T], "voxtral_realtime",
+                       "norm.weight"),
+    }
+    for name, (edit, arch, msg) in cases.items():
+        with pytest.raises(vkv.VkvError) as ei:
+            vkv.Model(small_file(tmp_path, name, edit, arch), hip_stream=stream_ptr())
+        assert ei.value.status == vkv.MODEL_ERROR, name
+        assert msg in vkv.last_error(), (name, vkv.last_error())

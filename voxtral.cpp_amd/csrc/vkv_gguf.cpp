@@ -526,7 +526,7 @@ struct vkv_model {
             if (ada_ws) (void)hipFree(ada_ws);
             if (prev >= 0) (void)hipSetDevice(prev);
         }
-        vkv_gguf_close(g);
+        delete g;   // not vkv_gguf_close: a failed load keeps its error message
     }
 };
 
