@@ -54,6 +54,11 @@ Other workloads (--workload), reported on the same contract:
                attention over the full 8192-slot F16 ring, O + residual,
                RMSNorm*(1+ada) + SwiGLU, W2 + residual), final norm, logits,
                argmax; tokens/s.
+  decoder_prompt_q4km  the decoder prefill of a 38-token prompt at the stream
+               start through vkv_decoder_prompt: token + audio rows, 26 x
+               (multi-row Q4_K_M products with RoPE in the epilogue, causal
+               attention + K/V append, O, SwiGLU, W2), final norm, logits of
+               the last token; prompt tokens/s.
 
 Prints one JSON line: throughput, the roofline of the step (algorithmic bytes /
 average step time from HIP events on the launch stream), the HBM traffic from
@@ -114,6 +119,10 @@ WORKLOADS = {
                                streams=1, pmc="",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) Mel windows "
                                     "and KV rows, generated on device)"),
+    "decoder_prompt_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights (MFMA int8), f16 KV",
+                                streams=1, pmc="decoder_prompt_q4km_pmc.json",
+                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) audio rows, "
+                                     "random prompt tokens, generated on device)"),
     "decoder_weights_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k (int8 dot)", streams=1,
                                  pmc="matvec_q4km_26l_pmc.json",
                                  data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs, "
@@ -674,6 +683,103 @@ def gpu_token(steps, warmup):
     return total_ms, step_ms, wall
 
 
+P_TOKENS, P_AUDIO_CAP = 38, 256
+
+
+def gpu_prompt(steps, warmup):
+    """The decoder prefill of a 38-token prompt at the stream start, each
+    token plus its audio row from a 256-row ring; the ring is cleared before
+    every step (host bookkeeping only: the prompt rewrites slots 0..37 before
+    any read)."""
+    import torch
+    import vkv
+
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED)
+    model, keep = device_model(gen)
+    cache = vkv.Cache(n_streams=1, n_layers=LAYERS, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
+                      n_q_heads=QH, dtype=vkv.F16)
+    ring = vkv.new_ring(CAP)
+    aemb = torch.randn(P_AUDIO_CAP, DIM, device="cuda", generator=gen) * 0.1
+    aring = vkv.RowRing(aemb.data_ptr(), P_AUDIO_CAP, DIM)
+    logits = torch.empty(VOCAB, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws_bytes = vkv.decoder_prompt_workspace(model, P_TOKENS)
+    ws = torch.empty(ws_bytes // 4 + 64, device="cuda")
+    ws_ptr = (ws.data_ptr() + 255) & ~255
+    g = torch.Generator().manual_seed(1)
+    prompts = [[int(t) for t in torch.randint(0, VOCAB, (P_TOKENS,), generator=g)]
+               for _ in range(warmup + steps)]
+
+    def step(i):
+        vkv.decoder_clear(ring, CAP)
+        vkv.decoder_prompt(cache, 0, ring, model, prompts[i], aring, logits.data_ptr(),
+                           tok.data_ptr(), ws_ptr, ws_bytes, hip_stream=sp)
+
+    total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
+    assert bool(torch.isfinite(logits).all())
+    assert ring.next_absolute_position == P_TOKENS
+    cache.close()
+    del keep
+    return total_ms, step_ms, wall
+
+
+def prompt_bytes(n=P_TOKENS):
+    """The weights once (26 layers + the logits matrix), the token rows of the
+    Q6_K table and the audio rows read, the K/V rows appended (f16); the
+    activations between launches (n rows of at most 9216 floats) are not
+    counted."""
+    return (weights_bytes_per_token() + n * (DIM // 256 * 210 + DIM * 4) +
+            LAYERS * n * 2 * KV_DIM * 2)
+
+
+def cpu_prompt_leg(target_seconds, n=P_TOKENS):
+    """The oracle's restatement of ggml's CPU mul_mat (one Q8_K vec_dot per
+    (row, column)) on one layer's seven matrices over n input columns, and the
+    logits of the last token; a prompt's time = 26 x layer + logits (the
+    attention over at most 38 keys is left out: under 0.1% of the work)."""
+    import numpy as np
+
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(SEED)
+
+    def mat(dt, r, k):
+        w = rng.integers(0, 256, size=(r * (k // 256), KQ_BLOCK[dt]), dtype=np.uint8)
+        if dt == 12:
+            w[:, 0:2] = rng.uniform(2e-4, 4e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+            w[:, 2:4] = rng.uniform(1e-4, 2e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        else:
+            w[:, 208:210] = rng.uniform(1e-5, 2e-4, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        return w.reshape(-1)
+
+    mats = [(dt, r, k, mat(dt, r, k)) for _, dt, r, k in LAYER_MATS]
+    lw = mat(14, VOCAB, DIM)
+    xs = {k: rng.standard_normal((n, k)).astype(np.float32) for k in (DIM, Q_DIM, HIDDEN)}
+    t_layer = t_logits = 0.0
+    reps = 0
+    t0 = time.perf_counter()
+    while reps < 1 or (time.perf_counter() - t0 < target_seconds and reps < 10):
+        a = time.perf_counter()
+        for dt, r, k, w in mats:
+            for c in range(n):
+                oracle.matvec(dt, w, r, k, xs[k][c], n_threads=threads)
+        b = time.perf_counter()
+        oracle.matvec(14, lw, VOCAB, DIM, xs[DIM][n - 1], n_threads=threads)
+        c_ = time.perf_counter()
+        t_layer += b - a
+        t_logits += c_ - b
+        reps += 1
+    prompt_s = (LAYERS * t_layer + t_logits) / reps
+    return {"value": n / prompt_s, "unit": "prompt tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} x (one layer's 7 projections over {n} columns + the 131072-row "
+                      f"logits of one) of the oracle's restatement of ggml's generic CPU "
+                      f"q4_K/q6_K x q8_K mul_mat, {threads} threads; prompt = 26 x layer + logits"}
+
+
 def token_bytes():
     """Weights + the KV window read (26 layers x 8192 x 2 x 1024 f16) + the
     appended rows and the per-layer activations (small)."""
@@ -1083,6 +1189,20 @@ def main():
                               "argmax); Q4_K_M weights",
                   "audio_ms_per_step": 80, "bytes_per_step": bytes_step}
         kernel = "whole step (encoder, adapter and decoder launches)"
+    elif args.workload == "decoder_prompt_q4km":
+        total_ms, step_ms, wall = gpu_prompt(args.steps, args.warmup)
+        bytes_step = prompt_bytes()
+        units_per_step = P_TOKENS
+        res = {"metric": "decoder prefill prompt tokens/s (38-token prompt + audio rows through "
+                         "26 Q4_K_M layers, causal attention with KV append, logits of the last "
+                         "token) and HBM GB/s", "unit": "prompt tokens/s"}
+        config = {"workload": "vkv_decoder_prompt of a 38-token prompt at the stream start: "
+                              "embedding rows + audio rows, 26 x (RMSNorm + Q/K/V with RoPE, "
+                              "causal attention + K/V append, O + residual, RMSNorm*(1+ada) + "
+                              "SwiGLU, W2 + residual), final norm, 131072-row logits, argmax",
+                  "layers": LAYERS, "dim": DIM, "hidden": HIDDEN, "vocab": VOCAB,
+                  "prompt_tokens": P_TOKENS, "bytes_per_prompt": bytes_step}
+        kernel = "whole prompt (k_gemm_kq, k_q8k_rows, k_window_mfma, k_matvec launches)"
     elif args.workload == "decoder_token_q4km":
         total_ms, step_ms, wall = gpu_token(args.steps, args.warmup)
         bytes_step = token_bytes()
@@ -1167,6 +1287,8 @@ def main():
     })
     if not args.no_cpu and args.workload == "decoder_weights_q4km":
         res["cpu_baseline"] = cpu_weights_leg(args.cpu_seconds)
+    elif not args.no_cpu and args.workload == "decoder_prompt_q4km":
+        res["cpu_baseline"] = cpu_prompt_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload == "decoder_token_q4km":
         res["cpu_baseline"] = cpu_token_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload in ("adapter_q4km", "adapter_group_q4km"):

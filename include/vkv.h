@@ -590,6 +590,27 @@ vkv_status vkv_decoder_token(vkv_cache *cache, int32_t stream, vkv_ring *ring,
                              float *logits, int32_t *token_out, void *workspace,
                              size_t workspace_bytes, vkv_plan *plan_out, void *hip_stream);
 
+/* Device workspace of a prompt of n_tokens (bytes); 0 for a bad model or count. */
+size_t vkv_decoder_prompt_workspace(const vkv_dec_model *model, int32_t n_tokens);
+
+/* The decoder prefill of a prompt (run_decoder_prefill, src/voxtral.cpp:
+ * 5161-5213, graph build_decoder_prefill_graph :2893-2961): n_tokens prompt
+ * tokens at positions ring->next_absolute_position + i, each embedded
+ * (get_rows) plus its audio row, through every layer (the multi-row products
+ * with the RoPE in their epilogue, the causal window attention appending the
+ * K/V rows, SwiGLU, residuals), the final norm of the last token and its
+ * logits with the greedy token; then commits the ring.  tokens: host array,
+ * each in [0, vocab); audio_emb: device ring whose logical row
+ * next_absolute_position + i is token i's audio row (width dim), or NULL.
+ * The post-append window must be one read segment, as for
+ * vkv_decoder_prefill.  The workspace keeps, after the call, the residual
+ * stream of all n_tokens rows ([n_tokens][dim] f32) at offset 0. */
+vkv_status vkv_decoder_prompt(vkv_cache *cache, int32_t stream, vkv_ring *ring,
+                              const vkv_dec_model *model, const int32_t *tokens, int32_t n_tokens,
+                              const vkv_row_ring *audio_emb, float *logits, int32_t *token_out,
+                              void *workspace, size_t workspace_bytes, vkv_plan *plan_out,
+                              void *hip_stream);
+
 /* ---------------------------------------------------------------------------
  * GGUF model files (voxtral_model_load_from_file, src/voxtral.cpp:1035-1316,
  * over ggml's gguf reader; the files tools/convert_voxtral_to_gguf.py and

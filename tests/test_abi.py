@@ -171,6 +171,13 @@ def test_error_statuses_without_device():
     assert L.vkv_decoder_token_workspace(ctypes.byref(m)) == 0
     assert L.vkv_decoder_token(None, 0, None, ctypes.byref(m), 0, None, None, None, None, 0,
                                None, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_decoder_prompt_workspace(ctypes.byref(m), 38) == 0
+    ids = (ctypes.c_int32 * 2)(1, 2)
+    plan = vkv.Plan()
+    plan.n_new = 7
+    assert L.vkv_decoder_prompt(None, 0, None, ctypes.byref(m), ids, 2, None, None, None, None, 0,
+                                ctypes.byref(plan), None) == vkv.INVALID_ARGUMENT
+    assert plan.n_new == 0                                        # out-parameter cleared
     assert L.vkv_decoder_layer_step(None, 0, None, 0, 0, 1, None, None, None, None, 32, 1.0,
                                     1e6, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_dequantize(vkv.Q4_K, 16, 255, 16, None) == vkv.INVALID_ARGUMENT

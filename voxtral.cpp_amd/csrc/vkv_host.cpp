@@ -1360,6 +1360,14 @@ TokenBuffers token_buffers(const vkv_dec_model &m, uint8_t *base) {
     return t;
 }
 
+vkv_status check_row_ring(const vkv_row_ring *r, const char *what) {
+    if (!r || !r->rows || r->capacity < 1 || r->width < 1)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: null ring or empty shape", what);
+    if ((int64_t)r->capacity * r->width > ((int64_t)1 << 40))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: ring too large", what);
+    return check_aligned(what, {r->rows});
+}
+
 vkv_status check_model(const vkv_dec_model *m) {
     if (!m || !m->layers || m->n_layers < 1)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder token: null model or no layers");
@@ -1451,6 +1459,156 @@ vkv_status vkv_decoder_token(vkv_cache *cache, int32_t stream, vkv_ring *ring,
     const vkv_mv_out head[1] = {{m.output, m.output_type, m.vocab, logits, nullptr}};
     if (vkv_status s = matvec_impl(t.x, m.dim, m.out_norm, nullptr, m.norm_eps, head, 1,
                                    VKV_MV_STORE, st, t.amax, token_out))
+        return s;
+    vkv_decoder_commit(ring, &plan);
+    if (plan_out) *plan_out = plan;
+    return ok();
+}
+
+// ---- the decoder prefill of a prompt ----
+
+namespace {
+
+struct PromptBuffers {
+    float *x, *q, *k, *v, *attn, *ffn;
+    unsigned long long *amax;
+    void *image;
+    size_t image_bytes, bytes;
+};
+
+PromptBuffers prompt_buffers(const vkv_dec_model &m, int32_t n, uint8_t *base) {
+    PromptBuffers t{};
+    size_t off = 0;
+    auto take = [&](size_t b) {
+        uint8_t *p = base ? base + off : nullptr;
+        off += align256(b);
+        return p;
+    };
+    const size_t qd = (size_t)m.n_q_heads * m.head_dim, kd = (size_t)m.n_kv_heads * m.head_dim;
+    t.x = (float *)take((size_t)n * m.dim * 4);
+    t.q = (float *)take((size_t)n * qd * 4);
+    t.k = (float *)take((size_t)n * kd * 4);
+    t.v = (float *)take((size_t)n * kd * 4);
+    t.attn = (float *)take((size_t)n * qd * 4);
+    t.ffn = (float *)take((size_t)n * m.hidden * 4);
+    t.amax = (unsigned long long *)take(16);
+    // the products' Q8_K input image, sized for the widest input
+    t.image_bytes = vkv_matmul_workspace(n, std::max<int64_t>(std::max<int64_t>(m.dim, m.hidden), qd));
+    t.image = take(t.image_bytes);
+    t.bytes = off;
+    return t;
+}
+
+}  // namespace
+
+size_t vkv_decoder_prompt_workspace(const vkv_dec_model *model, int32_t n_tokens) {
+    if (check_model(model) || n_tokens < 1 || n_tokens > 65535 * 16) return 0;
+    return prompt_buffers(*model, n_tokens, nullptr).bytes;
+}
+
+vkv_status vkv_decoder_prompt(vkv_cache *cache, int32_t stream, vkv_ring *ring,
+                              const vkv_dec_model *model, const int32_t *tokens, int32_t n_tokens,
+                              const vkv_row_ring *audio_emb, float *logits, int32_t *token_out,
+                              void *workspace, size_t workspace_bytes, vkv_plan *plan_out,
+                              void *hip_stream) {
+    if (plan_out) std::memset(plan_out, 0, sizeof(*plan_out));
+    if (vkv_status st = check_model(model)) return st;
+    const vkv_dec_model &m = *model;
+    if (vkv_status st = check_cache(cache, "decoder prompt")) return st;
+    if (vkv_status st = check_span(cache, stream, 1, 0, m.n_layers, "decoder prompt")) return st;
+    if (m.n_layers != cache->p.n_layers || m.n_kv_heads != cache->p.n_kv_heads ||
+        m.head_dim != cache->p.head_dim || m.n_q_heads > cache->p.n_q_heads)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prompt: model and cache shapes differ");
+    if (vkv_status st = check_heads(cache, m.n_q_heads, "decoder prompt")) return st;
+    if (!ring || !tokens || !logits || !token_out || !workspace)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prompt: null argument");
+    if (n_tokens < 1 || n_tokens > 65535 * 16)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prompt: n_tokens=%d", n_tokens);
+    for (int32_t i = 0; i < n_tokens; ++i)
+        if (tokens[i] < 0 || tokens[i] >= m.vocab)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prompt: token %d (%d) outside [0, %d)",
+                        i, tokens[i], m.vocab);
+    if (audio_emb) {
+        if (vkv_status st = check_row_ring(audio_emb, "decoder prompt")) return st;
+        if (audio_emb->width != m.dim)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prompt: audio rows of width %d, not %d",
+                        audio_emb->width, m.dim);
+    }
+    if (reinterpret_cast<uintptr_t>(workspace) & 255u)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prompt: workspace not 256-byte aligned");
+    const PromptBuffers t = prompt_buffers(m, n_tokens, (uint8_t *)workspace);
+    if (workspace_bytes < t.bytes)
+        return fail(VKV_STATUS_BUFFER_TOO_SMALL, "decoder prompt: workspace %zu < %zu bytes",
+                    workspace_bytes, t.bytes);
+    if (ring->capacity > cache->p.capacity)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prompt: ring capacity exceeds the cache");
+    const int64_t pos0 = ring->next_absolute_position;
+    vkv_plan plan;
+    if (vkv_status st = vkv_decoder_plan(ring, pos0, n_tokens, &plan)) return st;
+    if (plan.read_nseg != 1)
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "decoder prompt: the post-append window must be one segment (got %d)", plan.read_nseg);
+    if (pos0 + n_tokens > (1 << 24))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prompt: rope position beyond 2^24");
+    const int64_t bb = kq_block_bytes(m.tok_embeddings_type);
+    if (!bb) return fail(VKV_STATUS_INVALID_ARGUMENT, "decoder prompt: embedding dtype");
+    const int32_t qd = m.n_q_heads * m.head_dim, kd = m.n_kv_heads * m.head_dim;
+    const float scale = 1.0f / std::sqrt((float)m.head_dim);
+    DeviceGuard guard(cache->p.device);
+    void *hs = hip_stream;
+    hipStream_t st = as_stream(hs);
+    // token rows + audio rows, kEmbedChunk tokens per launch (ids in the
+    // kernel arguments); the first launch also clears the argmax words
+    for (int32_t c0 = 0; c0 < n_tokens; c0 += kEmbedChunk) {
+        const int32_t nc = std::min<int32_t>(kEmbedChunk, n_tokens - c0);
+        EmbedTokens tok{};
+        std::memcpy(tok.id, tokens + c0, (size_t)nc * sizeof(int32_t));
+        const int add_ring = audio_emb ? audio_emb->capacity : 0;
+        const int add_row0 = audio_emb ? (int)((pos0 + c0) % audio_emb->capacity) : 0;
+        hipError_t e = launch_embed_rows(m.tok_embeddings_type, (const uint8_t *)m.tok_embeddings,
+                                         (m.dim / 256) * bb, tok, nc, m.dim,
+                                         audio_emb ? audio_emb->rows : nullptr, add_ring, add_row0,
+                                         t.x + (size_t)c0 * m.dim, st, c0 == 0 ? t.amax : nullptr);
+        if (e != hipSuccess) return hip_fail(e, "decoder prompt: embedding launch");
+    }
+    for (int32_t l = 0; l < m.n_layers; ++l) {
+        const vkv_dec_layer &L = m.layers[l];
+        const vkv_mm_out qkv[3] = {{L.attn_q, L.attn_q_type, qd, t.q, nullptr, nullptr},
+                                   {L.attn_k, L.attn_k_type, kd, t.k, nullptr, nullptr},
+                                   {L.attn_v, L.attn_v_type, kd, t.v, nullptr, nullptr}};
+        MmRope rope;
+        rope.mask = 3u;
+        rope.head_dim = m.head_dim;
+        rope.pos0 = pos0;
+        rope.theta = m.rope_theta;
+        if (vkv_status s = matmul_impl(t.x, n_tokens, m.dim, L.attn_norm, nullptr, nullptr,
+                                       m.norm_eps, qkv, 3, VKV_MV_STORE, t.image, t.image_bytes, hs,
+                                       RowMap{}, RowMap{}, rope))
+            return s;
+        // causal attention over the retained keys, appending this layer's rows
+        if (vkv_status s = do_window(cache, stream, l, 1, plan.read_seg, plan.read_nseg,
+                                     plan.oldest_after, plan.absolute_start, n_tokens, 0, t.q, t.attn,
+                                     m.n_q_heads, scale, st, t.k, t.v, plan.write_seg,
+                                     plan.write_nseg))
+            return s;
+        const vkv_mm_out o[1] = {{L.attn_o, L.attn_o_type, m.dim, t.x, t.x, nullptr}};
+        if (vkv_status s = vkv_matmul(t.attn, n_tokens, qd, nullptr, nullptr, nullptr, m.norm_eps, o,
+                                      1, VKV_MV_STORE, t.image, t.image_bytes, hs))
+            return s;
+        const vkv_mm_out gu[2] = {{L.ffn_w1, L.ffn_w1_type, m.hidden, t.ffn, nullptr, nullptr},
+                                  {L.ffn_w3, L.ffn_w3_type, m.hidden, nullptr, nullptr, nullptr}};
+        if (vkv_status s = vkv_matmul(t.x, n_tokens, m.dim, L.ffn_norm, nullptr, L.ada_scale,
+                                      m.norm_eps, gu, 2, VKV_MV_SWIGLU, t.image, t.image_bytes, hs))
+            return s;
+        const vkv_mm_out down[1] = {{L.ffn_w2, L.ffn_w2_type, m.dim, t.x, t.x, nullptr}};
+        if (vkv_status s = vkv_matmul(t.ffn, n_tokens, m.hidden, nullptr, nullptr, nullptr,
+                                      m.norm_eps, down, 1, VKV_MV_STORE, t.image, t.image_bytes, hs))
+            return s;
+    }
+    // the final norm and the logits of the last token only (:2950-2955)
+    const vkv_mv_out head[1] = {{m.output, m.output_type, m.vocab, logits, nullptr}};
+    if (vkv_status s = matvec_impl(t.x + (size_t)(n_tokens - 1) * m.dim, m.dim, m.out_norm, nullptr,
+                                   m.norm_eps, head, 1, VKV_MV_STORE, hs, t.amax, token_out))
         return s;
     vkv_decoder_commit(ring, &plan);
     if (plan_out) *plan_out = plan;
@@ -1605,13 +1763,6 @@ size_t vkv_encoder_chunk_workspace(const vkv_enc_model *model, int32_t n_new) {
 }
 
 namespace {
-vkv_status check_row_ring(const vkv_row_ring *r, const char *what) {
-    if (!r || !r->rows || r->capacity < 1 || r->width < 1)
-        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: null ring or empty shape", what);
-    if ((int64_t)r->capacity * r->width > ((int64_t)1 << 40))
-        return fail(VKV_STATUS_INVALID_ARGUMENT, "%s: ring too large", what);
-    return check_aligned(what, {r->rows});
-}
 
 // vkv_encoder_chunk; with out_ring the final norm's rows go to its logical
 // rows q_start.. instead of x

@@ -182,6 +182,15 @@ hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const fl
                             uint8_t *out, hipStream_t st);
 hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const float *add, float *y,
                              hipStream_t st, unsigned long long *zero_words = nullptr);
+// token ids of one embedding launch, passed by value in the kernel arguments
+constexpr int kEmbedChunk = 256;
+struct EmbedTokens {
+    int32_t id[kEmbedChunk];
+};
+hipError_t launch_embed_rows(int dtype, const uint8_t *table, int64_t row_bytes,
+                             const EmbedTokens &tok, int n_rows, int64_t n, const float *add,
+                             int add_ring, int add_row0, float *y, hipStream_t st,
+                             unsigned long long *zero_words = nullptr);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, hipStream_t st);
 hipError_t launch_rows_small(const void *w, bool w_f16, const float *x, int n_in, int n_rows,
                              float *y, hipStream_t st);

@@ -587,20 +587,12 @@ __global__ void __launch_bounds__(256) k_q8k_quant(const float *x, int n, const 
     act_finish(r, n, nw, ada, eps, sm, out);
 }
 
-// ggml dequantize_row_q4_K / _q6_K, plus add[i] when add is given (the
-// token embedding + audio embedding sum); one thread per 8 elements.
-__global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__restrict__ src,
-                                                    int64_t n, const float *__restrict__ add,
-                                                    float *__restrict__ y,
-                                                    unsigned long long *zero_words) {
+// ggml dequantize_row_q4_K / _q6_K of elements i8 .. i8 + 7 of a row
+__device__ __forceinline__ void kq_dequant8(int dtype, const uint8_t *__restrict__ src, int64_t i8,
+                                            float out[8]) {
 #pragma clang fp contract(off)
-    const int64_t i8 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
-    // the decoder token's argmax words start each token at zero
-    if (zero_words && blockIdx.x == 0 && threadIdx.x < 2) zero_words[threadIdx.x] = 0ull;
-    if (i8 >= n) return;
     const int64_t b = i8 >> 8;
     const int e0 = (int)(i8 & 255);
-    float out[8];
     if (dtype == VKV_DTYPE_Q4_K) {
         const uint8_t *blk = src + b * kQ4Bytes;
         const float d = h2f(blk[0] | blk[1] << 8), dmin = h2f(blk[2] | blk[3] << 8);
@@ -635,8 +627,51 @@ __global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__
             out[i] = ds * (float)(q - 32);
         }
     }
+}
+
+// ggml dequantize_row_q4_K / _q6_K, plus add[i] when add is given (the
+// token embedding + audio embedding sum); one thread per 8 elements.
+__global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__restrict__ src,
+                                                    int64_t n, const float *__restrict__ add,
+                                                    float *__restrict__ y,
+                                                    unsigned long long *zero_words) {
+#pragma clang fp contract(off)
+    const int64_t i8 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    // the decoder token's argmax words start each token at zero
+    if (zero_words && blockIdx.x == 0 && threadIdx.x < 2) zero_words[threadIdx.x] = 0ull;
+    if (i8 >= n) return;
+    float out[8];
+    kq_dequant8(dtype, src, i8, out);
 #pragma unroll
     for (int i = 0; i < 8; ++i) y[i8 + i] = add ? out[i] + add[i8 + i] : out[i];
+}
+
+// get_rows of up to kEmbedChunk token rows of a Q4_K / Q6_K table, each plus
+// its audio row when add is given (build_decoder_prefill_graph's tok_emb +
+// audio_emb): row p = blockIdx.y is table row tok.id[p] into y row p, the
+// audio row at (add_row0 + p) % add_ring of a ring (add_ring > 0) or row p.
+// The host checked every id against the table's rows.
+__global__ void __launch_bounds__(256) k_embed_rows(int dtype, const uint8_t *__restrict__ table,
+                                                    int64_t row_bytes, EmbedTokens tok, int64_t n,
+                                                    const float *__restrict__ add, int add_ring,
+                                                    int add_row0, float *__restrict__ y,
+                                                    unsigned long long *zero_words) {
+#pragma clang fp contract(off)
+    const int p = blockIdx.y;
+    const int64_t i8 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (zero_words && blockIdx.x == 0 && p == 0 && threadIdx.x < 2) zero_words[threadIdx.x] = 0ull;
+    if (i8 >= n) return;
+    float out[8];
+    kq_dequant8(dtype, table + (int64_t)tok.id[p] * row_bytes, i8, out);
+    float *yr = y + (int64_t)p * n;
+    if (add) {
+        const float *ar = add + (int64_t)(add_ring > 0 ? (add_row0 + p) % add_ring : p) * n;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) yr[i8 + i] = out[i] + ar[i8 + i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) yr[i8 + i] = out[i];
+    }
 }
 
 // rms_norm(x_p) * w (+ b) per row, f32 out (the encoder's final norm,
@@ -742,8 +777,8 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, in
 //   k_q8k_rows -- the Q8_K image of every input row (one work group per row,
 //                 same input side as k_matvec), to global memory: codes
 //                 [p][K], block scales [p][K/256], 32-element sums [p][K/32].
-//   k_gemm_kq  -- a work group owns 16 weight rows x 16 input rows; its 8
-//                 (or 16) waves split the 256-blocks of K and meet in LDS.
+//   k_gemm_kq  -- a work group owns 16 weight rows x 16 (or 32) input rows;
+//                 its 8 (or 16) waves split the 256-blocks of K and meet in LDS.
 //                 A wave holds one block's fragments (about 100 VGPRs), so
 //                 two work groups share a CU and hide each other's load
 //                 latency.  One
@@ -871,23 +906,59 @@ __device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, int col, int b, i
     return x;
 }
 
-__device__ __forceinline__ void gemm_compute(const GFragQ4 &f, const GFragX &x, uint32_t (*hdr)[6],
-                                             int kg, int rr, float (&acc)[4]) {
-    const i32x4_t z = {0, 0, 0, 0};
+// The weight codes through an empty asm: what is derived from them (nibbles,
+// recentred 6-bit codes) is derived again instead of held in registers.
+__device__ __forceinline__ void opaque_codes(GFragQ4 &f) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(f.qs[c]));
+}
+__device__ __forceinline__ void opaque_codes(GFragQ6 &f) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+        asm volatile("" : "+v"(f.ql[n][0]));
+        asm volatile("" : "+v"(f.ql[n][1]));
+        asm volatile("" : "+v"(f.qh[n]));
+    }
+}
+
+// The block headers of the lane's four accumulator rows 4kg + i (d|dmin and
+// the 6-bit scales and mins one per byte for Q4_K; d and the 16 int8 scales
+// for Q6_K), passed between the wave's lanes through LDS: lanes kg = 0 hold
+// row rr's header.  A wave's LDS accesses complete in order, so the rows'
+// headers are in place when read back.
+__device__ __forceinline__ void gemm_hdr(const GFragQ4 &f, uint32_t (*hdr)[6], int kg, int rr,
+                                         uint32_t (&hd)[4][5]) {
     if (kg == 0) {
-        // this lane's row: d|dmin, then the 6-bit scales and mins one per byte
         hdr[rr][0] = f.h.x;
         hdr[rr][1] = f.h.y & 0x3f3f3f3fu;
         hdr[rr][2] = (f.h.w & 0x0f0f0f0fu) | ((f.h.y >> 2) & 0x30303030u);
         hdr[rr][3] = f.h.z & 0x3f3f3f3fu;
         hdr[rr][4] = ((f.h.w >> 4) & 0x0f0f0f0fu) | ((f.h.z >> 2) & 0x30303030u);
     }
-    // (a wave's LDS accesses complete in order: the rows' headers are in place)
-    uint32_t hd[4][5];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int w = 0; w < 5; ++w) hd[i][w] = hdr[4 * kg + i][w];
+}
+
+__device__ __forceinline__ void gemm_hdr(const GFragQ6 &f, uint32_t (*hdr)[6], int kg, int rr,
+                                         uint32_t (&hd)[4][5]) {
+    if (kg == 0) {
+        hdr[rr][0] = f.dh;
+        hdr[rr][1] = (uint32_t)f.s0;
+        hdr[rr][2] = (uint32_t)(f.s0 >> 32);
+        hdr[rr][3] = (uint32_t)f.s1;
+        hdr[rr][4] = (uint32_t)(f.s1 >> 32);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int w = 0; w < 5; ++w) hd[i][w] = hdr[4 * kg + i][w];
+}
+
+__device__ __forceinline__ void gemm_dot(const GFragQ4 &f, const GFragX &x, const uint32_t (&hd)[4][5],
+                                         int kg, float (&acc)[4]) {
+    const i32x4_t z = {0, 0, 0, 0};
     int isum[4] = {0, 0, 0, 0}, imin[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -910,21 +981,9 @@ __device__ __forceinline__ void gemm_compute(const GFragQ4 &f, const GFragX &x, 
     }
 }
 
-__device__ __forceinline__ void gemm_compute(const GFragQ6 &f, const GFragX &x, uint32_t (*hdr)[6],
-                                             int kg, int rr, float (&acc)[4]) {
+__device__ __forceinline__ void gemm_dot(const GFragQ6 &f, const GFragX &x, const uint32_t (&hd)[4][5],
+                                         int kg, float (&acc)[4]) {
     const i32x4_t z = {0, 0, 0, 0};
-    if (kg == 0) {
-        hdr[rr][0] = f.dh;
-        hdr[rr][1] = (uint32_t)f.s0;
-        hdr[rr][2] = (uint32_t)(f.s0 >> 32);
-        hdr[rr][3] = (uint32_t)f.s1;
-        hdr[rr][4] = (uint32_t)(f.s1 >> 32);
-    }
-    uint32_t hd[4][5];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int w = 0; w < 5; ++w) hd[i][w] = hdr[4 * kg + i][w];
     int isum[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int n = 0; n < 2; ++n)
@@ -964,18 +1023,21 @@ __device__ __forceinline__ float rope_elem(float self, float partner, bool odd, 
 
 // Waves per work group: 8, or 16 when a call has few 16-row tiles (the
 // 1280-row products of a 16-frame chunk are 80 work groups): more waves split
-// the same K, so each walks a shorter chain of blocks.
-template <bool Q4, int W>
+// the same K, so each walks a shorter chain of blocks.  CT column tiles (16
+// input rows each) per work group: a wave loads each weight block once and
+// applies it to every column tile, so the weights are read once per 16 CT
+// input rows.
+template <bool Q4, int W, int CT>
 __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, const MmOut &o1,
                                           uint32_t (*hdr)[16][6], float (*red)[W][16][17]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kg = lane >> 4, rr = lane & 15;
     const bool swiglu = a.swiglu != 0;
-    const int mats = swiglu ? 2 : 1;
     const int K = a.n_in, nb = K >> 8;
     const uint32_t bbytes = Q4 ? kQ4Bytes : kQ6Bytes, rbytes = (uint32_t)nb * bbytes;
-    const int row0 = ((int)blockIdx.x - o0.tile0) * 16, col0 = (int)blockIdx.y * 16;
+    const int row0 = ((int)blockIdx.x - o0.tile0) * 16, col0 = (int)blockIdx.y * 16 * CT;
     const int row = min(row0 + rr, o0.n_rows - 1);
-    const int col = min(col0 + rr, a.n_cols - 1);
+    // column tiles holding input rows (uniform over the work group)
+    const int n_ct = min(CT, (a.n_cols - col0 + 15) / 16);
     const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t *>(o0.w), (short)0, (int)(rbytes * (uint32_t)o0.n_rows), 0x00020000);
     const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
@@ -985,34 +1047,57 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
     const int kw = swiglu ? W / 2 : W;
     const int m = swiglu ? wave / kw : 0, wm = wave - m * kw;
     const __amdgpu_buffer_rsrc_t rs = m ? rs1 : rs0;
-    float acc[4] = {0, 0, 0, 0};
+    float acc[CT][4];
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[c][i] = 0.0f;
     using GF = std::conditional_t<Q4, GFragQ4, GFragQ6>;
     // the wave's blocks b, b + kw, b + 2 kw, ...: one set of fragments
     // (occupancy, not a second register set, covers the load latency)
     auto boff = [&](int b) { return (uint32_t)row * rbytes + (uint32_t)b * bbytes; };
     for (int b = wm; b < nb; b += kw) {
-        const GF w = gemm_load_w<Q4>(rs, boff(b), kg);
-        const GFragX x = gemm_load_x<Q4>(a, col, b, kg);
-        gemm_compute(w, x, hdr[wave], kg, rr, acc);
-    }
-    // the waves' partial sums meet in LDS: red[matrix][wave of that matrix][row][input row]
+        GF w = gemm_load_w<Q4>(rs, boff(b), kg);
+        uint32_t hd[4][5];
+        gemm_hdr(w, hdr[wave], kg, rr, hd);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[m][wm][4 * kg + i][rr] = acc[i];
-    (void)mats;
+        for (int c = 0; c < CT; ++c) {
+            if (c < n_ct) {
+                // the header words pass through an empty asm per column tile,
+                // so the scales are extracted again for each tile instead of
+                // being held in registers (occupancy covers the load latency)
+                if (CT > 1) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int v = 0; v < 5; ++v) asm volatile("" : "+v"(hd[i][v]));
+                    opaque_codes(w);
+                }
+                const GFragX x = gemm_load_x<Q4>(a, min(col0 + 16 * c + rr, a.n_cols - 1), b, kg);
+                gemm_dot(w, x, hd, kg, acc[c]);
+            }
+            if (CT > 1) __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    // the waves' partial sums meet in LDS: red[column tile][wave][row][input row]
+    // (SwiGLU: waves m kw .. m kw + kw - 1 hold matrix m)
+#pragma unroll
+    for (int c = 0; c < CT; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[c][wave][4 * kg + i][rr] = acc[c][i];
     __syncthreads();
-    const int t = threadIdx.x;
-    if (t < 256) {
-        const int c = t >> 4, r = t & 15;   // 16 consecutive rows per input row
-        const int orow = row0 + r, ocol = col0 + c;
+    for (int idx = threadIdx.x; idx < 256 * n_ct; idx += 64 * W) {
+        const int ct = idx >> 8, c = (idx >> 4) & 15, r = idx & 15;   // 16 consecutive rows per input row
+        const int orow = row0 + r, ocol = col0 + 16 * ct + c;
         if (orow < o0.n_rows && ocol < a.n_cols) {
             float v0 = 0.0f, v1 = 0.0f;
-            for (int w = 0; w < kw; ++w) v0 += red[0][w][r][c];
+            for (int w = 0; w < kw; ++w) v0 += red[ct][w][r][c];
             if (o0.bias) v0 = v0 + o0.bias[orow];
             const int64_t at =
                 (int64_t)(a.y_ring > 0 ? (a.y_row0 + ocol) % a.y_ring : ocol) * o0.n_rows + orow;
             float y;
             if (swiglu) {
-                for (int w = 0; w < kw; ++w) v1 += red[1][w][r][c];
+                for (int w = 0; w < kw; ++w) v1 += red[ct][kw + w][r][c];
                 if (o1.bias) v1 = v1 + o1.bias[orow];
                 y = silu(v0) * v1;
             } else if (a.gelu) {
@@ -1021,7 +1106,7 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
                 // the pair's other row is in this tile: its sum and bias
                 const int pr = r ^ 1;
                 float vp = 0.0f;
-                for (int w = 0; w < kw; ++w) vp += red[0][w][pr][c];
+                for (int w = 0; w < kw; ++w) vp += red[ct][w][pr][c];
                 if (o0.bias) vp = vp + o0.bias[row0 + pr];
                 y = rope_elem(v0, vp, (orow & 1) != 0, (orow % a.rope_hd) >> 1,
                               (float)(a.rope_pos0 + ocol), a.rope_ts);
@@ -1033,10 +1118,10 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
     }
 }
 
-template <int W>
-__global__ void __launch_bounds__(64 * W) k_gemm_kq(MmArgs a) {
+template <int W, int CT>
+__global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))) k_gemm_kq(MmArgs a) {
     __shared__ uint32_t hdr[W][16][6];
-    __shared__ float red[2][W][16][17];
+    __shared__ float red[CT][W][16][17];
     int seg = 0;
 #pragma unroll
     for (int k = 1; k < kMvMaxOuts; ++k)
@@ -1044,8 +1129,8 @@ __global__ void __launch_bounds__(64 * W) k_gemm_kq(MmArgs a) {
     const MmOut o0 = mm_out_at(a, seg);
     const MmOut o1 = a.swiglu ? a.out[1] : o0;
     // one weight dtype per work group (both SwiGLU matrices share it)
-    if (o0.dtype == VKV_DTYPE_Q4_K) gemm_body<true, W>(a, o0, o1, hdr, red);
-    else gemm_body<false, W>(a, o0, o1, hdr, red);
+    if (o0.dtype == VKV_DTYPE_Q4_K) gemm_body<true, W, CT>(a, o0, o1, hdr, red);
+    else gemm_body<false, W, CT>(a, o0, o1, hdr, red);
 }
 
 }  // namespace
@@ -1075,6 +1160,17 @@ hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const flo
     return hipGetLastError();
 }
 
+hipError_t launch_embed_rows(int dtype, const uint8_t *table, int64_t row_bytes,
+                             const EmbedTokens &tok, int n_rows, int64_t n, const float *add,
+                             int add_ring, int add_row0, float *y, hipStream_t st,
+                             unsigned long long *zero_words) {
+    if (n_rows < 1 || n_rows > kEmbedChunk) return hipErrorInvalidValue;
+    const int64_t threads = n / 8;
+    k_embed_rows<<<dim3((unsigned)((threads + 255) / 256), (unsigned)n_rows), 256, 0, st>>>(
+        dtype, table, row_bytes, tok, n, add, add_ring, add_row0, y, zero_words);
+    return hipGetLastError();
+}
+
 hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_row0, int n_rows,
                            int n, const float *norm_w, const float *norm_b, const float *ada,
                            float eps, int8_t *codes, float *xd, int32_t *bs32, hipStream_t st) {
@@ -1083,10 +1179,23 @@ hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_r
     return hipGetLastError();
 }
 
+namespace {
+template <int CT>
+void launch_gemm_ct(const MmArgs &a, int n_tiles, int n_col_tiles, hipStream_t st) {
+    const int gy = (n_col_tiles + CT - 1) / CT;
+    const dim3 grid((unsigned)n_tiles, (unsigned)gy);
+    // (16 waves only for one column tile: their 128-register budget has no
+    // room for more accumulators)
+    if (CT == 1 && (int64_t)n_tiles * gy < 128) k_gemm_kq<16, 1><<<grid, 1024, 0, st>>>(a);
+    else k_gemm_kq<8, CT><<<grid, 512, 0, st>>>(a);
+}
+}  // namespace
+
 hipError_t launch_gemm_kq(const MmArgs &a, int n_tiles, int n_col_tiles, hipStream_t st) {
-    const dim3 grid((unsigned)n_tiles, (unsigned)n_col_tiles);
-    if ((int64_t)n_tiles * n_col_tiles < 128) k_gemm_kq<16><<<grid, 1024, 0, st>>>(a);
-    else k_gemm_kq<8><<<grid, 512, 0, st>>>(a);
+    // two column tiles (32 input rows) per work group at most: a third
+    // set of accumulators spills at four waves per SIMD, and measured slower
+    if (n_col_tiles == 1) launch_gemm_ct<1>(a, n_tiles, n_col_tiles, st);
+    else launch_gemm_ct<2>(a, n_tiles, n_col_tiles, st);
     return hipGetLastError();
 }
 

@@ -257,6 +257,9 @@ PROTOTYPES = {
     "vkv_decoder_token_workspace": (ctypes.c_size_t, [_P(DecModel)]),
     "vkv_decoder_token": (_i32, [_vp, _i32, _P(Ring), _P(DecModel), _i32, _vp, _vp, _vp, _vp,
                                  ctypes.c_size_t, _P(Plan), _vp]),
+    "vkv_decoder_prompt_workspace": (ctypes.c_size_t, [_P(DecModel), _i32]),
+    "vkv_decoder_prompt": (_i32, [_vp, _i32, _P(Ring), _P(DecModel), _P(ctypes.c_int32), _i32,
+                                  _P(RowRing), _vp, _vp, _vp, ctypes.c_size_t, _P(Plan), _vp]),
     "vkv_ada_scale_workspace": (ctypes.c_size_t, [_i32, _i32]),
     "vkv_ada_scale": (_i32, [_vp, _i32, _vp, _i32, _i32, _i32, _f32, _vp, _vp, ctypes.c_size_t, _vp]),
     "vkv_model_set_ada": (_i32, [_vp, _f32, _vp, _vp]),
@@ -339,6 +342,11 @@ def new_ring(capacity):
     r = Ring()
     check(lib.vkv_decoder_clear(ctypes.byref(r), capacity))
     return r
+
+
+def decoder_clear(ring, capacity):
+    """resets ring in place to an empty ring of the given capacity"""
+    check(lib.vkv_decoder_clear(ctypes.byref(ring), capacity))
 
 
 def enc_plan(q_start, n_new, capacity, window):
@@ -603,6 +611,24 @@ def decoder_token(cache, stream, ring, model, token, audio_ptr, logits_ptr, toke
     check(lib.vkv_decoder_token(cache.handle, stream, ctypes.byref(ring), ctypes.byref(model),
                                 token, audio_ptr, logits_ptr, token_out_ptr, ws_ptr, ws_bytes,
                                 ctypes.byref(plan), hip_stream))
+    return plan
+
+
+def decoder_prompt_workspace(model, n_tokens):
+    return lib.vkv_decoder_prompt_workspace(ctypes.byref(model), n_tokens)
+
+
+def decoder_prompt(cache, stream, ring, model, tokens, audio_ring, logits_ptr, token_out_ptr,
+                   ws_ptr, ws_bytes, hip_stream=0):
+    """The decoder prefill of a prompt (host token ids; audio_ring a RowRing
+    or None) through vkv_decoder_prompt; returns the committed plan."""
+    ids = (ctypes.c_int32 * max(len(tokens), 1))(*[int(t) for t in tokens])
+    plan = Plan()
+    check(lib.vkv_decoder_prompt(cache.handle, stream, ctypes.byref(ring), ctypes.byref(model),
+                                 ids, len(tokens),
+                                 ctypes.byref(audio_ring) if audio_ring is not None else None,
+                                 logits_ptr, token_out_ptr, ws_ptr, ws_bytes, ctypes.byref(plan),
+                                 hip_stream))
     return plan
 
 
