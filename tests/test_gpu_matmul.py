@@ -73,8 +73,11 @@ def test_encoder_qkv_with_norm_bias_and_biases(P):
                ws_ptr, ws_b, norm_w_ptr=nwd.data_ptr(), norm_b_ptr=nbd.data_ptr(), eps=EPS,
                hip_stream=stream_ptr())
     hs = [oracle.norm_act(x[p], nw, eps=EPS, norm_b=nb) for p in range(P)]
-    # the Q8_K image (codes at the workspace start, [P][n_in]) is the oracle's, bit for bit
-    codes = host(t).view(np.uint8)[ws_ptr - t.data_ptr():][:P * n_in].reshape(P, n_in)
+    # the Q8_K image (codes at the workspace start, [P][n_in], each 256-block
+    # in the products' lane order: byte 64 q + 16 kg + 8 h + e holds code
+    # 32 (2q + h) + 8 kg + e) is the oracle's, bit for bit
+    raw = host(t).view(np.uint8)[ws_ptr - t.data_ptr():][:P * n_in]
+    codes = raw.reshape(P, n_in // 256, 4, 4, 2, 8).transpose(0, 1, 2, 4, 3, 5).reshape(P, n_in)
     for p in range(P):
         want = oracle.q8_k_quantize(hs[p]).reshape(-1, 292)[:, 4:260].ravel()
         assert np.array_equal(codes[p], want)

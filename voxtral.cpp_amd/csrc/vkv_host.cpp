@@ -1187,11 +1187,9 @@ vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float
             return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: weights must be 4-byte aligned");
         if ((swiglu || gelu) && o.add)
             return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: SwiGLU and GELU have no residual add");
-        a.out[k] = MmOut{(const uint8_t *)o.w, o.y, o.add, o.bias, o.dtype, o.n_rows, (int32_t)tiles};
+        a.out[k] = MmOut{(const uint8_t *)o.w, o.y, o.add, o.bias, o.dtype, o.n_rows, 0};
         if (!swiglu || k == 0) tiles += (o.n_rows + 15) / 16;
     }
-    if (swiglu) a.out[1].tile0 = 0x7fffffff;
-    for (int32_t k = n_outs; k < VKV_MV_MAX_OUTS; ++k) a.out[k].tile0 = 0x7fffffff;
     if (tiles > 0x7fffffff) return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: grid too large");
     if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u))
         return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: workspace null or not 256-byte aligned");
@@ -1225,7 +1223,7 @@ vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float
         a.rope_hd = rope.head_dim;
         a.rope_pos0 = rope.pos0;
     }
-    e = launch_gemm_kq(a, (int)tiles, (n_cols + 15) / 16, as_stream(hip_stream));
+    e = launch_gemm_kq(a, (n_cols + 15) / 16, as_stream(hip_stream));
     if (e != hipSuccess) return hip_fail(e, "matmul launch");
     return ok();
 }

@@ -150,7 +150,7 @@ struct MmOut {
     const float *add;      // nullable: y = add + (W h + bias), same layout as y
     const float *bias;     // nullable: [n_rows]
     int32_t dtype, n_rows;
-    int32_t tile0;         // first 16-row tile of this matrix
+    int32_t tile0;         // first work group of this matrix (set by launch_gemm_kq)
     int32_t rope;          // rows rotated by RoPE (ggml mode 0) after the bias
 };
 
@@ -177,7 +177,7 @@ struct MmArgs {
 hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_row0, int n_rows,
                            int n, const float *norm_w, const float *norm_b, const float *ada,
                            float eps, int8_t *codes, float *xd, int32_t *bs32, hipStream_t st);
-hipError_t launch_gemm_kq(const MmArgs &a, int n_tiles, int n_col_tiles, hipStream_t st);
+hipError_t launch_gemm_kq(MmArgs a, int n_col_tiles, hipStream_t st);
 hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const float *ada, float eps,
                             uint8_t *out, hipStream_t st);
 hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const float *add, float *y,

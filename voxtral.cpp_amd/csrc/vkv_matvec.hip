@@ -801,8 +801,18 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, i
     ActRegs<kMvMaxIn / 1024, false> r;
     act_load(r, x + (int64_t)src * x_stride, n, nw, ada);
     act_finish(r, n, nw, ada, eps, sm, nullptr, nbias);
+    // codes in the products' lane order: within each 256-block, the 16 bytes
+    // at 64 q + 16 kg hold the codes k = 32 j + 8 kg + e of j = 2q, 2q + 1
+    // (e = 0..7): lane group kg's MFMA B operands, and one 16-byte load per q
+    // reads 64 contiguous bytes of each input row
     int4 *dst = reinterpret_cast<int4 *>(codes + (int64_t)p * n);
-    for (int i = threadIdx.x; i < n / 16; i += 256) dst[i] = reinterpret_cast<const int4 *>(sm.xq)[i];
+    const uint64_t *src8 = reinterpret_cast<const uint64_t *>(sm.xq);
+    for (int i = threadIdx.x; i < n / 16; i += 256) {
+        const int base = (i >> 4) * 32, kg = i & 3, j0 = 2 * ((i >> 2) & 3);
+        const uint64_t lo = src8[base + 4 * j0 + kg], hi = src8[base + 4 * (j0 + 1) + kg];
+        dst[i] = make_int4((int)(uint32_t)lo, (int)(uint32_t)(lo >> 32), (int)(uint32_t)hi,
+                           (int)(uint32_t)(hi >> 32));
+    }
     for (int i = threadIdx.x; i < n / 256; i += 256) xd[(int64_t)p * (n / 256) + i] = sm.dx[i];
     for (int i = threadIdx.x; i < n / 32; i += 256) bs32[(int64_t)p * (n / 32) + i] = sm.bs32[i];
 }
@@ -890,9 +900,14 @@ template <bool Q4>
 __device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, int col, int b, int kg) {
     GFragX x;
     const int K = a.n_in;
-    const int8_t *xc = a.xq + (int64_t)col * K + 256 * b + 8 * kg;
+    // the image's lane order: 16 bytes per lane group at 64 q + 16 kg
+    const int4 *xc = reinterpret_cast<const int4 *>(a.xq + (int64_t)col * K + 256 * b + 16 * kg);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x.xb[j] = *reinterpret_cast<const uint64_t *>(xc + 32 * j);
+    for (int q = 0; q < 4; ++q) {
+        const int4 v = xc[4 * q];
+        x.xb[2 * q] = ((uint64_t)(uint32_t)v.y << 32) | (uint32_t)v.x;
+        x.xb[2 * q + 1] = ((uint64_t)(uint32_t)v.w << 32) | (uint32_t)v.z;
+    }
     if constexpr (Q4) {
         const int4 *bs = reinterpret_cast<const int4 *>(a.xbs + (int64_t)col * (K / 32) + 8 * b);
         const int4 s0 = bs[0], s1 = bs[1];
@@ -1032,7 +1047,7 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
                                           uint32_t (*hdr)[16][6], float (*red)[W][16][17]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kg = lane >> 4, rr = lane & 15;
     const bool swiglu = a.swiglu != 0;
-    const int K = a.n_in, nb = K >> 8;
+    const int nb = a.n_in >> 8;
     const uint32_t bbytes = Q4 ? kQ4Bytes : kQ6Bytes, rbytes = (uint32_t)nb * bbytes;
     const int row0 = ((int)blockIdx.x - o0.tile0) * 16, col0 = (int)blockIdx.y * 16 * CT;
     const int row = min(row0 + rr, o0.n_rows - 1);
@@ -1053,27 +1068,21 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[c][i] = 0.0f;
     using GF = std::conditional_t<Q4, GFragQ4, GFragQ6>;
-    // the wave's blocks b, b + kw, b + 2 kw, ...: one set of fragments
-    // (occupancy, not a second register set, covers the load latency)
-    auto boff = [&](int b) { return (uint32_t)row * rbytes + (uint32_t)b * bbytes; };
+    // the wave's blocks b, b + kw, b + 2 kw, ...: one block's fragments at a
+    // time (occupancy, not a second register set, covers the load latency)
     for (int b = wm; b < nb; b += kw) {
-        GF w = gemm_load_w<Q4>(rs, boff(b), kg);
-        uint32_t hd[4][5];
-        gemm_hdr(w, hdr[wave], kg, rr, hd);
+        GF w = gemm_load_w<Q4>(rs, (uint32_t)row * rbytes + (uint32_t)b * bbytes, kg);
 #pragma unroll
         for (int c = 0; c < CT; ++c) {
             if (c < n_ct) {
-                // the header words pass through an empty asm per column tile,
-                // so the scales are extracted again for each tile instead of
-                // being held in registers (occupancy covers the load latency)
-                if (CT > 1) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int v = 0; v < 5; ++v) asm volatile("" : "+v"(hd[i][v]));
-                    opaque_codes(w);
-                }
                 const GFragX x = gemm_load_x<Q4>(a, min(col0 + 16 * c + rr, a.n_cols - 1), b, kg);
+                // with several column tiles the codes pass through an empty
+                // asm before each use, so what is derived from them (nibbles,
+                // recentred codes, scales) is derived again instead of held
+                // in registers
+                if (CT > 1) opaque_codes(w);
+                uint32_t hd[4][5];
+                gemm_hdr(w, hdr[wave], kg, rr, hd);
                 gemm_dot(w, x, hd, kg, acc[c]);
             }
             if (CT > 1) __builtin_amdgcn_sched_barrier(0);
@@ -1086,8 +1095,9 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
 #pragma unroll
         for (int i = 0; i < 4; ++i) red[c][wave][4 * kg + i][rr] = acc[c][i];
     __syncthreads();
+    // outputs: 16 consecutive rows per input row
     for (int idx = threadIdx.x; idx < 256 * n_ct; idx += 64 * W) {
-        const int ct = idx >> 8, c = (idx >> 4) & 15, r = idx & 15;   // 16 consecutive rows per input row
+        const int ct = idx >> 8, c = (idx >> 4) & 15, r = idx & 15;
         const int orow = row0 + r, ocol = col0 + 16 * ct + c;
         if (orow < o0.n_rows && ocol < a.n_cols) {
             float v0 = 0.0f, v1 = 0.0f;
@@ -1118,6 +1128,9 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
     }
 }
 
+// (the body is in the kernel itself: a reference to the by-value kernel
+// argument passed through one more inlined function made the compiler copy
+// the argument to scratch memory)
 template <int W, int CT>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))) k_gemm_kq(MmArgs a) {
     __shared__ uint32_t hdr[W][16][6];
@@ -1191,11 +1204,22 @@ void launch_gemm_ct(const MmArgs &a, int n_tiles, int n_col_tiles, hipStream_t s
 }
 }  // namespace
 
-hipError_t launch_gemm_kq(const MmArgs &a, int n_tiles, int n_col_tiles, hipStream_t st) {
+hipError_t launch_gemm_kq(MmArgs a, int n_col_tiles, hipStream_t st) {
+    // the 16-row tiles of each matrix are consecutive work groups
+    int tiles = 0;
+    for (int k = 0; k < a.n_outs; ++k) {
+        if (a.swiglu && k == 1) {
+            a.out[1].tile0 = 0x7fffffff;   // W3 rides with W1's tiles
+            continue;
+        }
+        a.out[k].tile0 = tiles;
+        tiles += (a.out[k].n_rows + 15) / 16;
+    }
+    for (int k = a.n_outs; k < kMvMaxOuts; ++k) a.out[k].tile0 = 0x7fffffff;
     // two column tiles (32 input rows) per work group at most: a third
     // set of accumulators spills at four waves per SIMD, and measured slower
-    if (n_col_tiles == 1) launch_gemm_ct<1>(a, n_tiles, n_col_tiles, st);
-    else launch_gemm_ct<2>(a, n_tiles, n_col_tiles, st);
+    if (n_col_tiles == 1) launch_gemm_ct<1>(a, tiles, n_col_tiles, st);
+    else launch_gemm_ct<2>(a, tiles, n_col_tiles, st);
     return hipGetLastError();
 }
 
