@@ -283,6 +283,80 @@ def cpu_adapter_leg(n_groups, target_seconds):
                       f"restatement of ggml's CPU path, {threads} threads, {secs:.1f} s"}
 
 
+def cpu_encoder_leg(P, target_seconds):
+    """The oracle on one encoder execution of P new frames: the conv stem
+    (C, one thread) over the frames' Mel window, then per layer the seven
+    products (ggml's generic CPU q4_K/q6_K x q8_K mul_mat restated, threaded
+    over rows) and the window attention of the P queries over the 750-frame
+    window (the oracle's fp64 window attention, one thread); a chunk's time =
+    conv + 32 x layer (sampled on one layer)."""
+    import numpy as np
+
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    rng = np.random.default_rng(SEED)
+
+    def mat(dt, r, k):
+        w = rng.integers(0, 256, size=(r * (k // 256), KQ_BLOCK[dt]), dtype=np.uint8)
+        if dt == 12:
+            w[:, 0:2] = rng.uniform(2e-4, 4e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+            w[:, 2:4] = rng.uniform(1e-4, 2e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        else:
+            w[:, 208:210] = rng.uniform(1e-5, 2e-4, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        return w.reshape(-1)
+
+    mats = [(dt, r, k, mat(dt, r, k)) for _, dt, r, k in ENC_MATS]
+    xs = {k: rng.standard_normal((P, k)).astype(np.float32) for k in (1280, E_DIM, E_HID)}
+    conv_len = 2 * P + 4
+    mel = rng.standard_normal((128, conv_len)).astype(np.float32)
+    w0 = (rng.standard_normal((1280, 128, 3)) * 0.05).astype(np.float16).view(np.uint16)
+    w1 = (rng.standard_normal((1280, 1280, 3)) * 0.02).astype(np.float16).view(np.uint16)
+    b0 = np.zeros(1280, np.float32)
+    row_b = E_DIM * 2
+    kimg = (rng.standard_normal(E_CAP * E_DIM) * 0.5).astype(np.float16).view(np.uint8)
+    vimg = (rng.standard_normal(E_CAP * E_DIM) * 0.5).astype(np.float16).view(np.uint8)
+    q0 = 768
+    key_pos = np.arange(q0 + P - E_WIN, q0 + P)
+    q = rng.standard_normal((P, E_HEADS, E_HD)).astype(np.float32)
+    t_conv = t_proj = t_attn = 0.0
+    reps = 0
+    t0 = time.perf_counter()
+    while reps < 1 or (time.perf_counter() - t0 < target_seconds and reps < 10):
+        a = time.perf_counter()
+        oracle.conv_stem(mel, 2, P, w0, b0, w1, b0)
+        b = time.perf_counter()
+        for dt, r, k, w in mats:
+            for c in range(P):
+                oracle.matvec(dt, w, r, k, xs[k][c], n_threads=threads)
+        c_ = time.perf_counter()
+        oracle.window_attn_f64(1, kimg, vimg, row_b, (key_pos % E_CAP).astype(np.int32), key_pos, q,
+                               np.arange(q0, q0 + P), E_HEADS, E_HEADS, E_HD, E_WIN, 0.125)
+        d = time.perf_counter()
+        t_conv += b - a
+        t_proj += c_ - b
+        t_attn += d - c_
+        reps += 1
+    chunk_s = (t_conv + E_LAYERS * (t_proj + t_attn)) / reps
+    return {"value": P / chunk_s, "unit": "frames/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} x (conv stem over {P} frames + one layer's 7 projections over {P} "
+                      f"rows + its window-750 attention of {P} queries) of the oracle, projections "
+                      f"on {threads} threads; chunk = conv + 32 x layer"}
+
+
+def cpu_realtime_leg(target_seconds):
+    """One realtime step on the oracle: the encoder over 4 frames, one adapter
+    group and one decoder token, each sampled as in its own workload; a step's
+    time is their sum."""
+    enc = cpu_encoder_leg(R_FRAMES, target_seconds / 3)
+    ad = cpu_adapter_leg(1, target_seconds / 6)
+    tok = cpu_token_leg(target_seconds / 2)
+    step_s = R_FRAMES / enc["value"] + 1.0 / ad["value"] + 1.0 / tok["value"]
+    return {"value": 1.0 / step_s, "unit": "steps/s", "cores": tok["cores"], "kind": "port",
+            "sample": f"encoder: {enc['sample']}; adapter: {ad['sample']}; decoder token: "
+                      f"{tok['sample']}; step = sum"}
+
+
 def realtime_tensor_list():
     """(name, ggml type, ne) of the realtime model in the Q4_K_M mix
     (src/voxtral.cpp:1193-1265 names, src/voxtral-quantize.cpp:148-159 types)"""
@@ -1287,6 +1361,10 @@ def main():
     })
     if not args.no_cpu and args.workload == "decoder_weights_q4km":
         res["cpu_baseline"] = cpu_weights_leg(args.cpu_seconds)
+    elif not args.no_cpu and args.workload == "encoder_chunk_q4km":
+        res["cpu_baseline"] = cpu_encoder_leg(E_CHUNK, args.cpu_seconds)
+    elif not args.no_cpu and args.workload == "realtime_step_q4km":
+        res["cpu_baseline"] = cpu_realtime_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload == "decoder_prompt_q4km":
         res["cpu_baseline"] = cpu_prompt_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload == "decoder_token_q4km":
