@@ -1102,7 +1102,7 @@ namespace {
 struct MmImage {
     int8_t *codes;
     float *xd;
-    int32_t *bs32;
+    int16_t *bs16;
     size_t bytes;
 };
 MmImage mm_image(int32_t n_cols, int64_t n_in, uint8_t *base) {
@@ -1115,7 +1115,7 @@ MmImage mm_image(int32_t n_cols, int64_t n_in, uint8_t *base) {
     };
     im.codes = (int8_t *)take((size_t)n_cols * n_in);
     im.xd = (float *)take((size_t)n_cols * (n_in / 256) * 4);
-    im.bs32 = (int32_t *)take((size_t)n_cols * (n_in / 32) * 4);
+    im.bs16 = (int16_t *)take((size_t)n_cols * (n_in / 32) * 2);
     im.bytes = off;
     return im;
 }
@@ -1198,11 +1198,11 @@ vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float
         return fail(VKV_STATUS_BUFFER_TOO_SMALL, "matmul: workspace %zu < %zu bytes", workspace_bytes,
                     im.bytes);
     hipError_t e = launch_q8k_rows(x, n_in, in_rows.ring, in_rows.row0, n_cols, (int)n_in, norm_w,
-                                   norm_b, ada, eps, im.codes, im.xd, im.bs32, as_stream(hip_stream));
+                                   norm_b, ada, eps, im.codes, im.xd, im.bs16, as_stream(hip_stream));
     if (e != hipSuccess) return hip_fail(e, "matmul input launch");
     a.xq = im.codes;
     a.xd = im.xd;
-    a.xbs = im.bs32;
+    a.xbs = im.bs16;
     a.n_in = (int32_t)n_in;
     a.n_cols = n_cols;
     a.n_outs = n_outs;

@@ -157,7 +157,7 @@ struct MmOut {
 struct MmArgs {
     const int8_t *xq;      // Q8_K image: codes [n_cols][n_in]
     const float *xd;       // block scales [n_cols][n_in / 256]
-    const int32_t *xbs;    // 32-element sums [n_cols][n_in / 32]
+    const int16_t *xbs;    // 32-element sums [n_cols][n_in / 32]
     int32_t n_in, n_cols, n_outs, swiglu;
     int32_t gelu;          // y = gelu_erf(W h + bias) (no residual)
     // Input row p's output (and residual) row: (y_row0 + p) % y_ring when
@@ -176,7 +176,7 @@ struct MmArgs {
 // x_ring > 0 (rows of a ring buffer), else at x + p * x_stride.
 hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_row0, int n_rows,
                            int n, const float *norm_w, const float *norm_b, const float *ada,
-                           float eps, int8_t *codes, float *xd, int32_t *bs32, hipStream_t st);
+                           float eps, int8_t *codes, float *xd, int16_t *bs16, hipStream_t st);
 hipError_t launch_gemm_kq(MmArgs a, int n_col_tiles, hipStream_t st);
 hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const float *ada, float eps,
                             uint8_t *out, hipStream_t st);

@@ -776,7 +776,7 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, in
 //
 //   k_q8k_rows -- the Q8_K image of every input row (one work group per row,
 //                 same input side as k_matvec), to global memory: codes
-//                 [p][K], block scales [p][K/256], 32-element sums [p][K/32].
+//                 [p][K], block scales [p][K/256], 32-element sums [p][K/32] (int16).
 //   k_gemm_kq  -- a work group owns 16 weight rows x 16 (or 32) input rows;
 //                 its 8 (or 16) waves split the 256-blocks of K and meet in LDS.
 //                 A wave holds one block's fragments (about 100 VGPRs), so
@@ -794,7 +794,7 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, i
                                                   int x_ring, int x_row0, int n, const float *nw,
                                                   const float *nbias, const float *ada, float eps,
                                                   int8_t *__restrict__ codes, float *__restrict__ xd,
-                                                  int32_t *__restrict__ bs32) {
+                                                  int16_t *__restrict__ bs16) {
     __shared__ ActSmem sm;
     const int p = blockIdx.x;
     const int src = x_ring > 0 ? (x_row0 + p) % x_ring : p;
@@ -814,7 +814,8 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, i
                            (int)(uint32_t)(hi >> 32));
     }
     for (int i = threadIdx.x; i < n / 256; i += 256) xd[(int64_t)p * (n / 256) + i] = sm.dx[i];
-    for (int i = threadIdx.x; i < n / 32; i += 256) bs32[(int64_t)p * (n / 32) + i] = sm.bs32[i];
+    // (a sum of 32 codes fits in 16 bits: |s| <= 32 * 127)
+    for (int i = threadIdx.x; i < n / 32; i += 256) bs16[(int64_t)p * (n / 32) + i] = (int16_t)sm.bs32[i];
 }
 
 // 8 bytes at an even byte offset of a buffer (Q6_K blocks are 2-byte
@@ -909,10 +910,14 @@ __device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, int col, int b, i
         x.xb[2 * q + 1] = ((uint64_t)(uint32_t)v.w << 32) | (uint32_t)v.z;
     }
     if constexpr (Q4) {
-        const int4 *bs = reinterpret_cast<const int4 *>(a.xbs + (int64_t)col * (K / 32) + 8 * b);
-        const int4 s0 = bs[0], s1 = bs[1];
-        x.bsx[0] = s0.x; x.bsx[1] = s0.y; x.bsx[2] = s0.z; x.bsx[3] = s0.w;
-        x.bsx[4] = s1.x; x.bsx[5] = s1.y; x.bsx[6] = s1.z; x.bsx[7] = s1.w;
+        // the block's eight 16-bit sums in one 16-byte load
+        const int4 v = *reinterpret_cast<const int4 *>(a.xbs + (int64_t)col * (K / 32) + 8 * b);
+        const int w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x.bsx[2 * i] = (int)(int16_t)(w4[i] & 0xffff);
+            x.bsx[2 * i + 1] = w4[i] >> 16;
+        }
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) x.bsx[j] = 0;
@@ -1186,9 +1191,9 @@ hipError_t launch_embed_rows(int dtype, const uint8_t *table, int64_t row_bytes,
 
 hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_row0, int n_rows,
                            int n, const float *norm_w, const float *norm_b, const float *ada,
-                           float eps, int8_t *codes, float *xd, int32_t *bs32, hipStream_t st) {
+                           float eps, int8_t *codes, float *xd, int16_t *bs16, hipStream_t st) {
     k_q8k_rows<<<n_rows, 256, 0, st>>>(x, x_stride, x_ring, x_row0, n, norm_w, norm_b, ada, eps,
-                                       codes, xd, bs32);
+                                       codes, xd, bs16);
     return hipGetLastError();
 }
 
