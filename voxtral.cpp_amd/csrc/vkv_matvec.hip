@@ -880,7 +880,9 @@ __device__ __forceinline__ auto gemm_load_w(__amdgpu_buffer_rsrc_t rs, uint32_t 
                 u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs, boff + 16 + 32 * c + 8 * kg, 0, 0));
             f.qs[c] = ((uint64_t)v.y << 32) | v.x;
         }
-        f.h = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, boff, 0, 0));
+        // the header is only read by the lanes that pass it on (kg = 0)
+        f.h = u32x4_t{0, 0, 0, 0};
+        if (kg == 0) f.h = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, boff, 0, 0));
         return f;
     } else {
         GFragQ6 f;
@@ -890,9 +892,14 @@ __device__ __forceinline__ auto gemm_load_w(__amdgpu_buffer_rsrc_t rs, uint32_t 
             f.ql[n][1] = ld8_even(rs, boff + 64 * n + 32 + 8 * kg);
             f.qh[n] = ld8_even(rs, boff + 128 + 32 * n + 8 * kg);
         }
-        f.s0 = ld8_even(rs, boff + 192);
-        f.s1 = ld8_even(rs, boff + 200);
-        f.dh = __builtin_amdgcn_raw_buffer_load_b16(rs, boff + 208, 0, 0);
+        // scales and d are only read by the lanes that pass them on (kg = 0)
+        f.s0 = f.s1 = 0;
+        f.dh = 0;
+        if (kg == 0) {
+            f.s0 = ld8_even(rs, boff + 192);
+            f.s1 = ld8_even(rs, boff + 200);
+            f.dh = __builtin_amdgcn_raw_buffer_load_b16(rs, boff + 208, 0, 0);
+        }
         return f;
     }
 }
