@@ -337,3 +337,50 @@ def test_prompt_errors_leave_the_ring():
     torch.cuda.synchronize()
     cache.close()
     del keep, arr, at
+
+
+def test_prompt_on_a_q8_0_cache_then_tokens():
+    """A q8_0 cache (quantize-on-append in the prefill attention), then three
+    decoder tokens continuing from the prompt's ring: the entry points and the
+    composed sequence agree bit for bit at every step."""
+    rng = np.random.default_rng(808)
+    n_layers, vocab, cap, N = 1, 1024, 256, 38
+    m = tok.make_model(rng, n_layers, vocab)
+    model, keep, arr = tok.upload_model(m)
+    tokens = [int(t) for t in rng.integers(0, vocab, N)]
+    aring, at, _ = audio_ring(rng, 64, 0, N + 3)
+    sp = stream_ptr()
+    caches = []
+    for _ in range(2):
+        c = vkv.Cache(n_streams=1, n_layers=n_layers, capacity=cap, n_kv_heads=KVH, head_dim=HD,
+                      n_q_heads=QH, dtype=vkv.Q8_0)
+        caches.append((c, vkv.new_ring(cap)))
+    torch.cuda.synchronize()
+    (ca, ra), (cb, rb) = caches
+    ws, wp, wb = workspace_for(model, N)
+    la, lb = torch.empty(vocab, device=dev()), torch.empty(vocab, device=dev())
+    ta = torch.zeros(1, dtype=torch.int32, device=dev())
+    tb = torch.zeros(1, dtype=torch.int32, device=dev())
+    vkv.decoder_prompt(ca, 0, ra, model, tokens, aring, la.data_ptr(), ta.data_ptr(), wp, wb,
+                       hip_stream=sp)
+    composed_prompt(cb, rb, model, tokens, aring, lb, tb, sp)
+    assert np.array_equal(host(la).view(np.uint32), host(lb).view(np.uint32))
+    assert int(host(ta)[0]) == int(host(tb)[0])
+    tws_b = vkv.decoder_token_workspace(model)
+    tws = torch.empty(tws_b // 4 + 64, device=dev())
+    tws_p = (tws.data_ptr() + 255) & ~255
+    for step in range(3):
+        nxt = int(host(ta)[0])
+        a_ptr = aring.rows + ((N + step) % aring.capacity) * DIM * 4
+        vkv.decoder_token(ca, 0, ra, model, nxt, a_ptr, la.data_ptr(), ta.data_ptr(), tws_p, tws_b,
+                          hip_stream=sp)
+        tok.composed_token(cb, rb, model, nxt, a_ptr, lb, tb, sp)
+        assert np.array_equal(host(la).view(np.uint32), host(lb).view(np.uint32)), step
+        assert int(host(ta)[0]) == int(host(tb)[0])
+        assert ring_tuple(ra) == ring_tuple(rb) and ra.next_absolute_position == N + step + 1
+    for which in (0, 1):
+        assert np.array_equal(layer_image(ca, which, 0, 0), layer_image(cb, which, 0, 0))
+    assert np.isfinite(host(la)).all()
+    ca.close()
+    cb.close()
+    del keep, arr, at
