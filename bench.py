@@ -938,16 +938,19 @@ def encoder_bytes_per_chunk(n_keys, P=E_CHUNK):
 
 def timed_loop(step, steps, warmup, st, every=8):
     """W untimed steps, then K timed steps between a synchronize and two
-    events on the launch stream; every `every`-th timed step is also
-    bracketed by its own pair of events (an event costs a few microseconds of
-    GPU time, so bracketing every step would slow the timed region)."""
+    events on the launch stream.  Each run of `every` consecutive timed steps
+    is also bracketed by its own pair of events, and its duration / `every`
+    is one sample of the step's GPU time: an event record costs the GPU a few
+    microseconds, so bracketing single steps would add that to every sample
+    (and events around every step would slow the timed region)."""
     import torch
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
-    marks = [i for i in range(steps) if i % every == 0]
-    ev = {i: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for i in marks}
+    every = max(1, min(every, steps))
+    groups = [g for g in range(0, steps - every + 1, every)]
+    ev = {g: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for g in groups}
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -956,15 +959,14 @@ def timed_loop(step, steps, warmup, st, every=8):
     for i in range(steps):
         if i in ev:
             ev[i][0].record(st)
-            step(warmup + i)
-            ev[i][1].record(st)
-        else:
-            step(warmup + i)
+        step(warmup + i)
+        if i - every + 1 in ev:
+            ev[i - every + 1][1].record(st)
     t_end.record(st)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_start.elapsed_time(t_end)
-    step_ms = [ev[i][0].elapsed_time(ev[i][1]) for i in marks]
+    step_ms = [ev[g][0].elapsed_time(ev[g][1]) / every for g in groups]
     return total_ms, step_ms, wall
 
 
