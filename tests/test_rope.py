@@ -5,8 +5,11 @@ sin(p w_i), x'_{2i+1} = x_{2i} sin(p w_i) + x_{2i+1} cos(p w_i) with
 w_i = theta^(-2i/d) at small positions (a swapped pair, a wrong sign or a
 wrong frequency index fails it), norm preservation of every pair, and the
 relative-position property q(p1).k(p2) = q(p1+s).k(p2+s).  ggml's f32 running
-product for theta_i is followed as recalled from its public source; how far it
-matches ggml bit for bit is parity unpinned (ggml is not vendored)."""
+product for theta_i is followed as recalled from its public source (ggml is
+not vendored), and the cos/sin of every angle the decoder and encoder use are
+checked against the C library's cosf/sinf, which ggml's CPU rope calls: within
+one ulp everywhere, equal for ~99% (the C library's are not correctly rounded,
+so bit-equality with a ggml build depends on its libm)."""
 import numpy as np
 
 import oracle
@@ -75,3 +78,41 @@ def test_rows_take_consecutive_positions():
     whole = oracle.rope(x, D, 1000, THETA)
     for r in range(6):
         assert np.array_equal(whole[r], oracle.rope(x[r:r + 1], D, 1000 + r, THETA)[0])
+
+
+def test_cos_sin_against_the_c_library():
+    """ggml's CPU rope evaluates cosf/sinf of each f32 angle (the C
+    library's, glibc here).  Rotating (1, 0) pairs makes the oracle return its
+    cos and sin of every angle; against glibc's cosf/sinf of the same angles
+    (ggml's f32 running product restated in numpy) they agree to within one
+    ulp at every angle of positions 0..8191 for the decoder's and the
+    encoder's head widths, and are equal for all but ~1% (glibc's cosf/sinf
+    are accurate to < 1 ulp, not correctly rounded, while the oracle rounds
+    the double result).  A wrong angle (frequency index, running product, a
+    swapped cos/sin) would miss by far more than one ulp."""
+    import ctypes
+
+    libm = ctypes.CDLL("libm.so.6")
+    for fn in (libm.cosf, libm.sinf):
+        fn.restype, fn.argtypes = ctypes.c_float, [ctypes.c_float]
+    libm.powf.restype, libm.powf.argtypes = ctypes.c_float, [ctypes.c_float, ctypes.c_float]
+    cosf = np.frompyfunc(lambda v: libm.cosf(float(v)), 1, 1)
+    sinf = np.frompyfunc(lambda v: libm.sinf(float(v)), 1, 1)
+    npos = 8192
+    for d in (128, 64):
+        ts = np.float32(libm.powf(THETA, np.float32(-2.0) / np.float32(d)))
+        ang = np.empty((npos, d // 2), np.float32)
+        ang[:, 0] = np.arange(npos, dtype=np.float32)
+        for i in range(1, d // 2):
+            ang[:, i] = ang[:, i - 1] * ts
+        unit = np.tile(np.array([1.0, 0.0], np.float32), d // 2)[None, :].repeat(npos, 0)
+        got = oracle.rope(unit, d, 0, THETA)
+        got_c, got_s = got[:, 0::2], got[:, 1::2]
+        want_c = cosf(ang).astype(np.float32)
+        want_s = sinf(ang).astype(np.float32)
+        for g, w in ((got_c, want_c), (got_s, want_s)):
+            ulp = np.abs(g.view(np.int32).astype(np.int64) - w.view(np.int32).astype(np.int64))
+            same_sign = np.sign(g) == np.sign(w)
+            assert np.all(same_sign | (g == 0) | (w == 0))
+            assert ulp.max() <= 1, d
+            assert np.mean(ulp != 0) < 0.02, d
