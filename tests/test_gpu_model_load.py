@@ -147,8 +147,9 @@ def independent(g):
 
 def realtime_step(enc, dec, ad, conv, mel_window, plan):
     """conv stem -> encoder chunk into the output ring -> adapter groups ->
-    one decoder token per group reading its audio row; returns the logits
-    of every token and the rings"""
+    a two-token decoder prompt over the first audio rows, then one decoder
+    token per remaining group reading its audio row; returns the logits of
+    the prompt's last token and of every token, and the rings"""
     sp = stream_ptr()
     n = plan.n_new
     ecache = vkv.Cache(n_streams=1, n_layers=ENC_L, capacity=878, n_kv_heads=32,
@@ -173,16 +174,25 @@ def realtime_step(enc, dec, ad, conv, mel_window, plan):
     ab = vkv.adapter_workspace(ad, groups)
     aws = torch.empty(ab // 4 + 64, device=dev())
     vkv.adapter_commit(ad, er, ar, 0, groups, (aws.data_ptr() + 255) & ~255, ab, hip_stream=sp)
+    # the decoder: a two-token prompt at positions 0, 1 (audio rows 0, 1),
+    # then one token per remaining group, as the stream decoder runs them
+    logits = torch.zeros(groups, VOCAB, device=dev())
+    tok = torch.zeros(groups + 1, dtype=torch.int32, device=dev())
+    n_prompt = 2
+    pb = vkv.decoder_prompt_workspace(dec, n_prompt)
+    pws = torch.empty(pb // 4 + 64, device=dev())
+    vkv.decoder_prompt(dcache, 0, ring, dec, [1, 5], ar, logits[n_prompt - 1].data_ptr(),
+                       tok[n_prompt - 1].data_ptr(), (pws.data_ptr() + 255) & ~255, pb, hip_stream=sp)
+    torch.cuda.synchronize()
+    token = int(tok[n_prompt - 1].item())
     tb = vkv.decoder_token_workspace(dec)
     tws = torch.empty(tb // 4 + 64, device=dev())
-    logits = torch.empty(groups, VOCAB, device=dev())
-    tok = torch.zeros(groups + 1, dtype=torch.int32, device=dev())
-    token = 1
-    for p in range(groups):
+    for p in range(n_prompt, groups):
         vkv.decoder_token(dcache, 0, ring, dec, token, aemb[p % 256].data_ptr(), logits[p].data_ptr(),
                           tok[p].data_ptr(), (tws.data_ptr() + 255) & ~255, tb, hip_stream=sp)
         torch.cuda.synchronize()
         token = int(tok[p].item())
+    assert ring.next_absolute_position == groups
     torch.cuda.synchronize()
     out = (logits.cpu().numpy(), tok.cpu().numpy(), enc_out.cpu().numpy(), aemb.cpu().numpy())
     ecache.close()
@@ -248,6 +258,7 @@ def test_a_realtime_step_from_the_loaded_model(model_file):
     assert np.isfinite(logits).all() and np.isfinite(enc_out[:16]).all() and np.isfinite(aemb[:4]).all()
     assert np.isnan(enc_out[16:]).all() and np.isnan(aemb[4:]).all()
     assert all(0 <= t < VOCAB for t in toks[:4])
+    assert np.abs(logits[1:4]).max() > 0     # the prompt's and both tokens' logits were written
     m.close()
 
 
