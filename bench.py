@@ -6,10 +6,11 @@ layers, an 8192-slot sliding ring that is full and wrapping (every step evicts
 the oldest position), F16 KV, 32 query / 8 KV heads x 128, one stream.  One
 step = one token = for every layer, append the token's K/V row (f32 -> f16) at
 pos % 8192 and run the single-query GQA attention over all 8192 retained
-positions, through the vkv_decoder_step C entry point: one k_decode launch per
-step (append fused in its prologue; one work group per (layer, kv head) owns
-the whole window, so there are no split partials to merge).  Inputs (Q, K, V
-for every timed step) are generated on the device before timing.
+positions, through the vkv_decoder_step C entry point: one k_decode_rows launch
+(append fused in its prologue; a work group per (layer, 1024-slot chunk) reads
+whole 2 KiB rows for all 8 kv heads) and one k_combine launch merging the 8
+chunks per head.  Inputs (Q, K, V for every timed step) are generated on the
+device before timing.
 
 Other workloads (--workload), reported on the same contract:
   longform_rope_f16  the default workload through vkv_decoder_step_rope: Q and
@@ -1330,8 +1331,11 @@ def main():
                               f"{'s' if ns > 1 else ''}, append + 1-query attention per layer",
                   "layers": LAYERS, "window": CAP, "kv_heads": KVH, "q_heads": QH,
                   "head_dim": HD, "streams": ns}
-        fmt = "FmtF16" if wl["dtype"] == 1 else "FmtQ8"
-        kernel = f"k_decode<{fmt}> (append fused; one pass per (stream, layer, kv head))"
+        if wl["dtype"] == 1 and ns == 1:
+            kernel = ("k_decode_rows + k_combine (append fused; a work group per (layer, 1024-slot "
+                      "chunk) reading whole rows, then the merge of the 8 chunks)")
+        else:
+            kernel = "k_decode_q8mfma + k_combine (append fused; split chunks)"
     # the load is bound by the host link, not HBM: PCIe 5.0 x16, 64 GB/s per direction
     bound, peak = ("host link (PCIe 5.0 x16)", 64.0) if args.workload == "model_load_q4km" else \
         ("hbm", HBM_PEAK_GBPS)

@@ -348,6 +348,7 @@ def test_decoder_token_two_layers():
         scale = np.abs(want).max()
         err = np.abs(got - want).max()
         corr = np.corrcoef(got, want)[0, 1]
+        print(f"{attn_fn.__name__}: max err {err:.4g} of scale {scale:.4g}, corr {corr:.6f}", flush=True)
         assert err <= max_rel * scale and corr > min_corr, (attn_fn.__name__, err, scale, corr)
         top2 = np.sort(want)[-2:]
         if top2[1] - top2[0] > 2 * err:

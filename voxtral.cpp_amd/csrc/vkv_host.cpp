@@ -312,6 +312,40 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     const int64_t units = (int64_t)n_streams * n_layers * G;
     a.chunk = pick_chunk(c, units, n_kv_max, gqa, &a.n_chunks);
     a.out = out;
+    // F16 by whole rows (k_decode_rows): a work group per (stream, layer,
+    // 1024-slot chunk) reads 2 KiB rows, which stream faster than one head's
+    // 256-byte segments (measured on MI355X at 26 layers x 8192 slots: 135.4
+    // against 140.0 us per step with the merge launch included).  Used when
+    // its grid holds between 3/4 of the CUs and the CUs, as the one-pass
+    // k_decode; VKV_DECODE_ROWS=0 / 1 overrides.
+    {
+        const int32_t rows_chunk = 1024;
+        const int32_t nc = std::max(1, (n_kv_max + rows_chunk - 1) / rows_chunk);
+        const int64_t groups = (int64_t)n_streams * n_layers * nc;
+        const bool shape_ok = c->p.dtype == VKV_DTYPE_F16 && G == 8 && n_q_heads == 32 &&
+                              (nc == 1 || units * nc * gqa <= c->part_heads_budget);
+        const char *force = std::getenv("VKV_DECODE_ROWS");
+        const bool want = force ? env_int("VKV_DECODE_ROWS") == 1
+                                : 4 * groups >= 3 * (int64_t)c->n_cus && groups <= c->n_cus;
+        if (shape_ok && want) {
+            a.chunk = rows_chunk;
+            a.n_chunks = nc;
+            hipError_t e = launch_decode_rows(k_new != nullptr, n_streams, a, st);
+            if (e != hipSuccess) return hip_fail(e, "decode launch");
+            if (a.n_chunks == 1) return VKV_STATUS_OK;
+            CombineArgs cb{};
+            cb.part_o = c->part_o;
+            cb.part_ml = c->part_ml;
+            cb.out = out;
+            cb.n_chunks = a.n_chunks;
+            cb.n_q_heads = n_q_heads;
+            cb.n_layers = n_layers;
+            cb.head_dim = D;
+            e = launch_combine(cb, n_streams, st);
+            if (e != hipSuccess) return hip_fail(e, "combine launch");
+            return VKV_STATUS_OK;
+        }
+    }
     // XCD-grouped order: q8_0 head segments (136 B) share cache lines with
     // their neighbours.  VKV_XCD_SWIZZLE=0/1 overrides.
     const int64_t n_wg = units * a.n_chunks;

@@ -211,6 +211,7 @@ hipError_t launch_gather(const uint8_t *src, int64_t row_bytes, SegPair seg, uin
 // mfma: the q8_0 decode on the matrix cores (4 waves)
 hipError_t launch_decode(int dtype, int gqa, int waves, int stages, bool mfma, bool fuse_append,
                          int n_streams, const DecodeArgs &a, hipStream_t st);
+hipError_t launch_decode_rows(bool fuse_append, int n_streams, const DecodeArgs &a, hipStream_t st);
 hipError_t launch_combine(const CombineArgs &a, int n_streams, hipStream_t st);
 hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st);
 hipError_t launch_q8_0_pack(const float *x, uint8_t *blocks, int64_t n, hipStream_t st);

@@ -822,6 +822,191 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention by whole rows (F16, 8 kv heads x 128, 4 query heads each).
+// Work group = 8 waves on (stream, layer, chunk of `chunk` logical slots);
+// wave w reads half h = w & 1 of each row (kv heads 4h..4h+3, 1 KiB, one
+// load instruction of 16 B per lane) for the slots of sub-stream sw = w >> 1:
+// per round the 4 sub-streams take 16 consecutive slots, 4 each, and both
+// halves read the same slots, so the work group consumes whole rows.  Lane
+// (grp, c) holds dims [8c, 8c+8) of kv head 4h + grp; the 16 lanes of a group
+// are that head's, so the score transposition, the running max and sum and
+// the P.V accumulation are k_decode's with one head per lane group.  The 4
+// sub-streams of each head meet in LDS; one chunk writes the output, several
+// write partials for k_combine.
+// ---------------------------------------------------------------------------
+template <bool FUSE, int NS>
+__global__ void __launch_bounds__(512) k_decode_rows(DecodeArgs a) {
+    using F = FmtF16;
+    constexpr int D = 128, GQA = 4, NH = 32;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int h = wave & 1, sw = wave >> 1;
+    const int grp = lane >> 4, c = lane & 15;
+    const int g = 4 * h + grp;
+    const int chunk = blockIdx.x, layer = blockIdx.y, s = blockIdx.z;
+    const SegPair sp = a.seg[s];
+    const int n_kv = sp.n0 + sp.n1;
+    const int64_t base = (int64_t)s * a.stream_bytes + (int64_t)layer * a.layer_bytes;
+    const uint8_t *kl = a.k + base;
+    const uint8_t *vl = a.v + base;
+    const int e = g * D + c * 8;
+    const uint32_t row_bytes24 = (uint32_t)a.row_bytes;
+    const int i_begin = chunk * a.chunk;
+    const int i_end = min(i_begin + a.chunk, n_kv);
+    auto load_batch = [&](int b, F::Frag (&kf)[4], F::Frag (&vf)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            // past the chunk end: reload the last valid slot (masked later)
+            const int ix = min(b + u, i_end - 1);
+            const uint32_t off = __umul24((uint32_t)slot_of(sp, ix), row_bytes24);
+            kf[u] = F::load<true>(kl + off, e);
+            vf[u] = F::load<true>(vl + off, e);
+        }
+    };
+    F::Frag kf[NS][4], vf[NS][4];
+    constexpr int kStep = 16;   // slots per round of the 4 sub-streams
+    int b0 = i_begin + 4 * sw;
+    const bool early = !FUSE || i_begin + (NS - 1) * kStep <= n_kv - 1;
+    if (early && i_begin < i_end) {
+#pragma unroll
+        for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
+    }
+    __shared__ float2 sm_rope[64];
+    if (a.rope) {
+        rope_table(sm_rope, a.rope_pos[s], a.rope_theta_scale);
+        __syncthreads();
+    }
+    F::QFrag qf[GQA];
+    {
+        const float *qp = a.q + (int64_t)s * a.q_sstride + (int64_t)layer * a.q_lstride +
+                          (int64_t)(g * GQA) * D + c * 8;
+#pragma unroll
+        for (int j = 0; j < GQA; ++j) {
+            const float4 q0 = reinterpret_cast<const float4 *>(qp + j * D)[0];
+            const float4 q1 = reinterpret_cast<const float4 *>(qp + j * D)[1];
+            float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+            if (a.rope) rope8_tab(qv, 4 * c, sm_rope);
+            qf[j] = F::make_q(qv);
+        }
+    }
+    const int hj = c & 3;
+    const int hu = c >> 2;
+    float m = -INFINITY, l = 0.0f;
+    float acc[GQA][8];
+#pragma unroll
+    for (int j = 0; j < GQA; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[j][i] = 0.0f;
+    __shared__ float4 sm_p[8][16];   // per wave: p[slot u * 4 + group][head]
+
+    auto process = [&](F::Frag (&kf)[4], F::Frag (&vf)[4], const int b) __attribute__((always_inline)) {
+        float part[16];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int j = 0; j < GQA; ++j) part[u * 4 + j] = F::dot(kf[u], qf[j]);
+        float sc = transpose_sum16(part, c) * a.scale_log2;   // (slot u = hu, head j = hj)
+        if (b + hu >= i_end) sc = -INFINITY;
+        // batch max of head j over the group's 4 slots (lanes j, j+4, j+8, j+12)
+        float bm = fmaxf(sc, dpp<0x124>(sc));
+        bm = fmaxf(bm, dpp<0x128>(bm));
+        if (__any(bm > m + 8.0f)) {
+            const float mn = fmaxf(m, bm);
+            const float alpha = mn == -INFINITY ? 1.0f : fast_exp2(m - mn);
+            l *= alpha;
+            float al[GQA];
+            al[0] = dpp<0x00>(alpha);
+            al[1] = dpp<0x55>(alpha);
+            al[2] = dpp<0xAA>(alpha);
+            al[3] = dpp<0xFF>(alpha);
+#pragma unroll
+            for (int j = 0; j < GQA; ++j)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[j][i] *= al[j];
+            m = mn;
+        }
+        const float p = sc == -INFINITY ? 0.0f : fast_exp2(sc - m);
+        l += p;
+        reinterpret_cast<float *>(&sm_p[wave][hu * 4 + grp])[hj] = p;
+        __builtin_amdgcn_wave_barrier();
+        float4 pw[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pw[u] = sm_p[wave][u * 4 + grp];
+        __builtin_amdgcn_wave_barrier();
+        pv_accumulate<F>(acc, vf, pw);
+    };
+    if (FUSE) {
+        // the step's new row (the newest logical index): the two sub-stream-0
+        // waves of the work group that holds it write both halves
+        if (n_kv >= 1 && n_kv - 1 >= i_begin && n_kv - 1 < i_end && sw == 0) {
+            const int slot = slot_of(sp, n_kv - 1);
+            const float *kn = a.k_new + (int64_t)s * a.new_sstride + (int64_t)layer * a.new_lstride + e;
+            const float *vn = a.v_new + (int64_t)s * a.new_sstride + (int64_t)layer * a.new_lstride + e;
+            float xk[8], xv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { xk[i] = kn[i]; xv[i] = vn[i]; }
+            if (a.rope) rope8_tab(xk, (e & 127) >> 1, sm_rope);
+            store_new<F>(a.k_w + base + (int64_t)slot * a.row_bytes, e, xk, true);
+            store_new<F>(a.v_w + base + (int64_t)slot * a.row_bytes, e, xv, true);
+        }
+        __syncthreads();
+    }
+    if (!early && i_begin < i_end) {
+#pragma unroll
+        for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
+    }
+    for (; b0 < i_end; b0 += NS * kStep) {
+#pragma unroll
+        for (int p = 0; p < NS; ++p) {
+            load_batch(b0 + (p + NS - 1) * kStep, kf[(p + NS - 1) % NS], vf[(p + NS - 1) % NS]);
+            process(kf[p], vf[p], b0 + p * kStep);
+        }
+    }
+    // the head's sum over its 4 slot lanes (the max is shared already)
+    l += dpp<0x124>(l);
+    l += dpp<0x128>(l);
+
+    // the 4 sub-streams of each head meet in LDS
+    __shared__ float sm_m[4][NH], sm_l[4][NH];
+    __shared__ float sm_o[4][NH][D];
+    if (c < GQA) {
+        sm_m[sw][g * GQA + c] = m;   // lane c < 4: head j = c (slot 0's lanes)
+        sm_l[sw][g * GQA + c] = l;
+    }
+#pragma unroll
+    for (int j = 0; j < GQA; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) sm_o[sw][g * GQA + j][c * 8 + i] = acc[j][i];
+    __syncthreads();
+    const int64_t head0 = ((int64_t)s * a.n_layers + layer) * a.n_q_heads;
+    for (int t = threadIdx.x; t < NH * D; t += 512) {
+        const int hh = t / D, d = t % D;
+        float M = sm_m[0][hh];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) M = fmaxf(M, sm_m[w][hh]);
+        float O = 0.0f, L = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float sc_w = fast_exp2(sm_m[w][hh] - M);
+                O = fmaf(sm_o[w][hh][d], sc_w, O);
+                L = fmaf(sm_l[w][hh], sc_w, L);
+            }
+        }
+        if (a.n_chunks == 1) {
+            a.out[(head0 + hh) * D + d] = L > 0.0f ? O / L : 0.0f;
+        } else {
+            const int64_t pidx = (head0 + hh) * a.n_chunks + chunk;
+            a.part_o[pidx * D + d] = O;
+            if (d == 0) {
+                a.part_ml[pidx * 2] = M;
+                a.part_ml[pidx * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Decode attention over a q8_0 cache on the matrix cores, in ggml's q8_0
 // arithmetic for QK: Q is quantized per 32-element block with the cache's own
 // quantizer and each v_mfma_i32_16x16x32_i8 contracts exactly one block, so
@@ -1652,6 +1837,15 @@ hipError_t launch_decode(int dtype, int gqa, int waves, int stages, bool mfma, b
     default: break;
     }
     if (!ok) return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_rows(bool fuse_append, int n_streams, const DecodeArgs &a, hipStream_t st) {
+    if (a.n_kv_heads != 8 || a.n_q_heads != 32) return hipErrorInvalidValue;
+    dim3 grid((unsigned)a.n_chunks, (unsigned)a.n_layers, (unsigned)n_streams);
+    // two batches in flight per wave (three or four measured 1-2% slower)
+    if (fuse_append) hipLaunchKernelGGL((k_decode_rows<true, 2>), grid, dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((k_decode_rows<false, 2>), grid, dim3(512), 0, st, a);
     return hipGetLastError();
 }
 
