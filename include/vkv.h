@@ -190,7 +190,7 @@ vkv_status vkv_enc_drive_next(int64_t emitted, int64_t target, int32_t final,
 typedef struct vkv_cache vkv_cache;
 
 typedef struct vkv_cache_params {
-    uint32_t struct_size;  /* sizeof(vkv_cache_params) */
+    uint32_t struct_size;  /* sizeof(vkv_cache_params), or offsetof(.., kernel_flags) */
     int32_t n_streams;     /* independent rings sharing the allocation (>=1) */
     int32_t n_layers;      /* decoder 26, encoder 32 */
     int32_t capacity;      /* backing slots per (stream, layer): 8192 / 878 */
@@ -199,7 +199,24 @@ typedef struct vkv_cache_params {
     int32_t n_q_heads;     /* attention heads (multiple of n_kv_heads): 32 */
     int32_t dtype;         /* vkv_dtype */
     int32_t device;        /* HIP device ordinal */
+    /* Kernel selection, for cross-checks and A/B measurement only; all zero
+     * (or a struct_size that ends at `device`) = the automatic choice, which
+     * is what production callers use.  Fixed for the cache's lifetime: no
+     * process environment is consulted. */
+    int32_t kernel_flags;  /* VKV_KERNEL_* bits */
+    int32_t decode_chunk;  /* slots per split decode work group (multiple of 64); 0 = automatic */
+    int32_t decode_waves;  /* waves per per-head decode work group (4 or 8); 0 = automatic */
+    int32_t decode_stages; /* K/V batches in flight per decode wave (2..4); 0 = automatic */
 } vkv_cache_params;
+
+/* vkv_cache_params.kernel_flags */
+#define VKV_KERNEL_DECODE_HEADS 0x1    /* F16 decode: per-kv-head kernel where whole rows would run */
+#define VKV_KERNEL_DECODE_ROWS 0x2     /* F16 decode: whole-row kernel whenever the shape allows */
+#define VKV_KERNEL_DECODE_VALU 0x4     /* q8_0 decode: vector-ALU kernel, not the matrix cores */
+#define VKV_KERNEL_WINDOW_VALU 0x8     /* window attention: vector-ALU kernel, not the matrix cores */
+#define VKV_KERNEL_XCD_SWIZZLE 0x10    /* XCD-grouped decode work-group order for every dtype */
+#define VKV_KERNEL_NO_XCD_SWIZZLE 0x20 /* no XCD-grouped order (q8_0's default is on) */
+#define VKV_KERNEL_FLAGS_ALL 0x3f
 
 typedef struct vkv_cache_layout {
     uint64_t row_bytes;    /* bytes per (slot) row = kv_dim elements */

@@ -113,6 +113,22 @@ def test_error_statuses_without_device():
     assert L.vkv_cache_create(ctypes.byref(odd), ctypes.byref(h)) == vkv.INVALID_ARGUMENT
     badtype = vkv.CacheParams(ctypes.sizeof(vkv.CacheParams), 1, 1, 8, 8, 128, 32, 2, 0)
     assert L.vkv_cache_create(ctypes.byref(badtype), ctypes.byref(h)) == vkv.INVALID_ARGUMENT
+    # kernel selection fields: contradictory or unknown flags and out-of-range
+    # tuning values are rejected before any device call
+    full = ctypes.sizeof(vkv.CacheParams)
+    for extra, what in (((vkv.KERNEL_DECODE_HEADS | vkv.KERNEL_DECODE_ROWS, 0, 0, 0), "kernel_flags"),
+                        ((vkv.KERNEL_XCD_SWIZZLE | vkv.KERNEL_NO_XCD_SWIZZLE, 0, 0, 0), "kernel_flags"),
+                        ((0x40, 0, 0, 0), "kernel_flags"),
+                        ((0, 100, 0, 0), "decode_chunk"), ((0, 0, 6, 0), "decode_chunk"),
+                        ((0, 0, 0, 5), "decode_chunk")):
+        p = vkv.CacheParams(full, 1, 1, 8, 8, 128, 32, vkv.F16, 0, *extra)
+        assert L.vkv_cache_create(ctypes.byref(p), ctypes.byref(h)) == vkv.INVALID_ARGUMENT
+        assert what in vkv.last_error() and not h.value
+    # a parameter block that ends at `device` is accepted (its shape is then checked)
+    base = vkv.CacheParams(vkv.CacheParams.kernel_flags.offset, 1, 1, 8, 8, 100, 32, vkv.Q8_0, 0,
+                           0x40, 0, 0, 0)
+    assert L.vkv_cache_create(ctypes.byref(base), ctypes.byref(h)) == vkv.INVALID_ARGUMENT
+    assert "invalid shape" in vkv.last_error()
     # hot-path calls on a null cache
     segs = (vkv.Seg * 2)()
     assert L.vkv_append(None, 0, 0, 1, segs, 1, None, None, 0, None) == vkv.INVALID_ARGUMENT

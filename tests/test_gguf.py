@@ -256,3 +256,15 @@ def test_model_load_rejects_bad_files_before_touching_a_device(tmp_path):
         vkv.Model(p)
     assert ei.value.status == vkv.MODEL_ERROR
     assert not os.path.exists(str(tmp_path / "missing.gguf"))
+
+
+def test_huge_tensor_sizes_do_not_wrap(tmp_path):
+    """An F32 tensor claiming 2^62 - 1 elements over no data bytes: its byte
+    count (2^64 - 4) and its padded size would wrap a 64-bit sum; both
+    readers reject the file instead of exposing the tensor."""
+    for ne0 in (2 ** 62 - 1, 2 ** 62 - 8, 2 ** 61 + 3):
+        h = b"GGUF" + le(3, 4) + le(1, 8) + le(0, 8)
+        h += le(1, 8) + b"h" + le(1, 4) + le(ne0, 8) + le(0, 4) + le(0, 8)
+        data = h + b"\0" * ((-len(h)) % 32) + b"\0" * 64
+        msg = rejected(tmp_path, data, f"huge{ne0 % 97}.gguf")
+        assert "too large" in msg or "past the end" in msg

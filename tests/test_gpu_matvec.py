@@ -145,11 +145,8 @@ def test_logits_matvec_full_vocab():
     check_rows(host(y), want, magnitude(vkv.Q6_K, w, n_rows, n_in, h))
 
 
-@pytest.mark.parametrize("rows_per_wave", [None, 1, 3, 64])
-def test_qkv_in_one_call_with_norm(monkeypatch, rows_per_wave):
-    if rows_per_wave:
-        monkeypatch.setenv("VKV_MV_ROWS", str(rows_per_wave))
-    rng = np.random.default_rng(6144 + (rows_per_wave or 0))
+def test_qkv_in_one_call_with_norm():
+    rng = np.random.default_rng(6144)
     n_in = 3072
     mats = [(vkv.Q4_K, 4096), (vkv.Q4_K, 1024), (vkv.Q6_K, 1024)]
     ws = [random_matrix(rng, dt, n, n_in) for dt, n in mats]

@@ -75,11 +75,13 @@ def test_encoder_window_chunks(dtype, frames):
 @pytest.mark.parametrize("dtype", [vkv.F16, vkv.Q8_0])
 def test_decoder_prefill_then_steps(dtype):
     """38-token causal prefill at positions 0..37 (the stream prompt), a second
-    10-token prefill, then single decode steps over the same cache."""
+    10-token prefill, then a 300-token one (75 query tiles per kv head: its
+    rows are appended in a launch of their own instead of the fused write),
+    each against the oracle's ring image and fp64 causal attention."""
     L = 4
     with vkv.Cache(n_streams=1, n_layers=L, capacity=8192, dtype=dtype) as c:
         ring = vkv.new_ring(8192)
-        for n in (38, 10):
+        for n in (38, 10, 300):
             start = ring.next_absolute_position
             q = synth(None, 4096, vkv.TAG_Q, nl=L, p0=start, np_=n)
             k = synth(None, 1024, vkv.TAG_K, nl=L, p0=start, np_=n)

@@ -148,3 +148,140 @@ def test_window_f64_matches_masked_sdpa(dtype):
     mask = torch.tril(torch.ones(n, n, dtype=torch.bool))
     want = sdpa_ref(q, kst, vst, np.arange(n), H, G, D, 1 / np.sqrt(D), mask=mask.unsqueeze(0))
     assert np.max(np.abs(got - want)) < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# Closed forms that pin the roundings which separate ggml's CPU flash
+# attention (the mimic) from the exact result: the f16 V accumulator, Q
+# rounded to f16 against an F16 K, and Q quantized to q8_0 blocks against a
+# q8_0 K (integer block sums).  Each case is built so that the plausible
+# alternative (f32 accumulator, unrounded Q, f16 Q against q8_0 K) lands
+# many ulp away from the closed form.
+# ---------------------------------------------------------------------------
+
+def _ulps(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    return np.abs(a.view(np.int32).astype(np.int64) - b.view(np.int32).astype(np.int64))
+
+
+def _f32(x):
+    return np.float32(x)
+
+
+def test_mimic_f16_accumulator_stalls_at_2048():
+    """4096 keys with equal scores (K = 0) and V = 1.0 everywhere: ggml adds
+    each weight 1.0 into an f16 accumulator, which stops growing at 2048
+    (2049 is a tie that rounds to even, 2048), while the weight sum S reaches
+    4096 in f32; the output is exactly 0.5.  An f32 accumulator would give
+    exactly 1.0, the exact attention 1.0."""
+    n = 4096
+    kimg, _ = make_layer(oracle.F16, np.zeros((n, KV), np.float32))
+    vimg, _ = make_layer(oracle.F16, np.ones((n, KV), np.float32))
+    q = np.random.default_rng(3).standard_normal((H, D)).astype(np.float32)
+    rb = oracle.row_bytes(oracle.F16, KV)
+    slots = np.arange(n, dtype=np.int32)
+    mi = oracle.decode_attn_mimic(oracle.F16, kimg, vimg, rb, slots, q, G, D, 1 / np.sqrt(D))
+    assert np.all(mi == np.float32(0.5))
+    ex = oracle.decode_attn_f64(oracle.F16, kimg, vimg, rb, slots, q, G, D, 1 / np.sqrt(D))
+    assert np.all(ex == 1.0)
+    # below the stall every partial sum is an exact f16 integer
+    mi = oracle.decode_attn_mimic(oracle.F16, kimg, vimg, rb, slots[:2048], q, G, D, 0.1)
+    assert np.all(mi == np.float32(1.0))
+
+
+# q values at f16 midpoints (ties) and just off them: RNE decides each
+MIDPOINTS = [1 + 2 ** -11,          # tie -> 1.0 (even)
+             1 + 3 * 2 ** -11,      # tie -> 1 + 2^-9 (even mantissa 2)
+             2049.0 / 2048,         # 1 + 2^-11 again, written differently
+             1.5 + 2 ** -11,        # tie -> 1.5 (mantissa 512, even)
+             0.75 + 2 ** -12,       # tie below 1 -> 0.75
+             0.75 + 3 * 2 ** -12,   # tie -> 0.75 + 2^-10
+             1 + 2 ** -11 + 2 ** -20,  # just above a tie -> rounds up
+             1.25 - 2 ** -12]       # tie -> 1.25 (mantissa 256, even)
+
+
+def test_mimic_rounds_q_to_f16_against_f16_k():
+    """Two keys: key 0 has K = 1.0 in dimension 0 of every kv head and V = 1.0
+    in dimension 0; key 1 has K = 0 and V = 1.0 in dimension 1.  Query head h
+    holds a value q_h at or near an f16 midpoint in dimension 0 and zeros
+    elsewhere.  ggml's CPU path converts Q to f16 (RNE) for the F16 K dot,
+    so with s = scale * f16(q_h), w = expf(-s), S = 1 + w:
+        out[h][0] = 1 / S,   out[h][1] = f16(w) / S   (f16 V accumulator)."""
+    scale = 1.0
+    krows = np.zeros((2, KV), np.float32)
+    vrows = np.zeros((2, KV), np.float32)
+    for g in range(G):
+        krows[0, g * D] = 1.0
+        vrows[0, g * D] = 1.0
+        vrows[1, g * D + 1] = 1.0
+    kimg, _ = make_layer(oracle.F16, krows)
+    vimg, _ = make_layer(oracle.F16, vrows)
+    q = np.zeros((H, D), np.float32)
+    for h in range(H):
+        q[h, 0] = MIDPOINTS[h % len(MIDPOINTS)] * (1 + h // len(MIDPOINTS))
+    rb = oracle.row_bytes(oracle.F16, KV)
+    mi = oracle.decode_attn_mimic(oracle.F16, kimg, vimg, rb, np.arange(2, dtype=np.int32), q, G, D,
+                                  scale)
+    for h in range(H):
+        qh = oracle.f16_bits_to_f32(oracle.f32_to_f16_bits(q[h, :1]))[0]
+        assert qh == np.float16(q[h, 0]).astype(np.float32)         # numpy's RNE agrees
+        s = _f32(_f32(qh) * _f32(scale))
+        w = _f32(np.exp(-np.float64(s)))
+        S = _f32(_f32(1.0) + w)
+        inv = _f32(_f32(1.0) / S)
+        want0 = inv
+        want1 = _f32(np.float32(np.float16(w)) * inv)
+        assert _ulps(mi[h, 0], want0) <= 2, h
+        assert _ulps(mi[h, 1], want1) <= 2, h
+        assert np.all(mi[h, 2:] == 0)
+        # unrounded Q would move out[h][0] far beyond those 2 ulp when the
+        # midpoint actually rounds
+        if np.float32(q[h, 0]) != qh:
+            s_alt = _f32(q[h, 0] * scale)
+            alt = _f32(_f32(1.0) / _f32(_f32(1.0) + _f32(np.exp(-np.float64(s_alt)))))
+            assert _ulps(alt, want0) >= 50, h
+        # an f32 accumulator would keep w unrounded in out[h][1]
+        assert _ulps(_f32(w * inv), want1) >= 50, h
+
+
+def test_mimic_quantizes_q_to_q8_0_against_q8_0_k():
+    """Two keys over a q8_0 cache.  Key 0: block 0 of every kv head holds 1.0
+    in all 32 places (codes 127, d_k = f16(1/127)); V has 1.0 in dimension 0.
+    Key 1: K = 0, V = 1.0 in dimension 1.  Query block 0 is
+    (127 c, c/2, ..., c/2) with c = 2^-6: its q8_0 form has d_q = c and codes
+    (127, 1, ..., 1) (0.5 rounds half away from zero), so the score is the
+    integer block sum 127*127 + 31*127 = 20066 times d_k*d_q, not the f16 dot
+    product (which would weigh the 31 halves at 0.5)."""
+    scale = 0.5
+    krows = np.zeros((2, KV), np.float32)
+    vrows = np.zeros((2, KV), np.float32)
+    for g in range(G):
+        krows[0, g * D:g * D + 32] = 1.0
+        vrows[0, g * D] = 1.0
+        vrows[1, g * D + 1] = 1.0
+    kimg, _ = make_layer(oracle.Q8_0, krows)
+    vimg, vst = make_layer(oracle.Q8_0, vrows)
+    c = 2.0 ** -6
+    q = np.zeros((H, D), np.float32)
+    q[:, 0] = 127 * c
+    q[:, 1:32] = c / 2
+    blk = oracle.q8_0_quantize(q[0, :32])
+    assert blk[2] == 127 and all(int(np.int8(b)) == 1 for b in blk[3:34])
+    dk = oracle.f16_bits_to_f32(np.frombuffer(kimg[0:2].tobytes(), np.uint16))[0]
+    assert dk == np.float32(np.float16(np.float32(1.0) / np.float32(127.0)))
+    rb = oracle.row_bytes(oracle.Q8_0, KV)
+    mi = oracle.decode_attn_mimic(oracle.Q8_0, kimg, vimg, rb, np.arange(2, dtype=np.int32), q, G, D,
+                                  scale)
+    v0 = np.float32(vst[0, 0])
+    s = _f32(_f32(_f32(20066) * _f32(dk * _f32(c))) * _f32(scale))
+    w = _f32(np.exp(-np.float64(s)))
+    inv = _f32(_f32(1.0) / _f32(_f32(1.0) + w))
+    want0 = _f32(v0 * inv)
+    assert np.all(_ulps(mi[:, 0], want0) <= 2)
+    # the f16 dot product of the unquantized Q would give a different score
+    kdq = np.float32(127) * dk
+    s_alt = _f32(_f32(np.float32(np.float16(127 * c)) * kdq + 31 * np.float32(np.float16(c / 2)) * kdq)
+                 * _f32(scale))
+    alt = _f32(v0 * _f32(_f32(1.0) / _f32(_f32(1.0) + _f32(np.exp(-np.float64(s_alt))))))
+    assert _ulps(alt, want0) >= 1000

@@ -245,7 +245,13 @@ vkv_status parse(vkv_gguf &g) {
                          ti.name.c_str(), (long long)ti.t.ne[0], (long long)ts.blck);
         ti.t.type = (int32_t)type;
         ti.t.offset = off;
-        ti.t.nbytes = (uint64_t)(elems / ts.blck) * (uint64_t)ts.bytes;
+        // sizes checked before every product and sum, so a tensor claiming
+        // ~2^62 elements cannot wrap its byte count, its padding or the end
+        // check below
+        const uint64_t nblocks = (uint64_t)(elems / ts.blck);
+        if (nblocks > (UINT64_MAX - g.alignment) / (uint64_t)ts.bytes)
+            return gfail(VKV_STATUS_MODEL_ERROR, "gguf: tensor %s too large", ti.name.c_str());
+        ti.t.nbytes = nblocks * (uint64_t)ts.bytes;
         if (off != packed)
             return gfail(VKV_STATUS_MODEL_ERROR, "gguf: tensor %s has offset %llu, expected %llu",
                          ti.name.c_str(), (unsigned long long)off, (unsigned long long)packed);
@@ -261,7 +267,8 @@ vkv_status parse(vkv_gguf &g) {
     g.data_size = packed;
     // every tensor's bytes inside the file (the last one may end unpadded)
     for (const auto &ti : g.tensors)
-        if (g.data_offset > g.size || ti.t.offset + ti.t.nbytes > g.size - g.data_offset)
+        if (g.data_offset > g.size || ti.t.offset > g.size - g.data_offset ||
+            ti.t.nbytes > g.size - g.data_offset - ti.t.offset)
             return gfail(VKV_STATUS_MODEL_ERROR, "gguf: tensor %s extends past the end of the file",
                          ti.name.c_str());
     return VKV_STATUS_OK;

@@ -11,6 +11,7 @@
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
+#include <cstddef>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -186,39 +187,7 @@ vkv_status do_append(vkv_cache *c, int32_t stream, int32_t layer0, int32_t n_lay
     return VKV_STATUS_OK;
 }
 
-// VKV_DECODE_CHUNK: fixed slots per decode work group (multiple of 64);
-// unset = automatic.  VKV_DECODE_WAVES: waves per decode work group (4, 8 or
-// 16); unset = automatic.
-int32_t env_int(const char *name) {
-    const char *e = std::getenv(name);
-    return e ? (int32_t)std::strtol(e, nullptr, 10) : 0;
-}
-
-int32_t forced_chunk() {
-    static const int32_t v = [] {
-        const int32_t c = env_int("VKV_DECODE_CHUNK");
-        return (c >= 64 && c % 64 == 0) ? c : 0;
-    }();
-    return v;
-}
-
-int32_t forced_waves() {
-    static const int32_t v = [] {
-        const int32_t w = env_int("VKV_DECODE_WAVES");
-        return (w == 4 || w == 8) ? w : 0;
-    }();
-    return v;
-}
-
-// VKV_DECODE_STAGES: K/V batches in flight per wave (2..4 with 4 waves, 2..3
-// with 8); unset = automatic.
-int32_t forced_stages() {
-    static const int32_t v = [] {
-        const int32_t n = env_int("VKV_DECODE_STAGES");
-        return (n >= 2 && n <= 4) ? n : 0;
-    }();
-    return v;
-}
+bool has_flag(const vkv_cache *c, int32_t flag) { return (c->p.kernel_flags & flag) != 0; }
 
 // Chunk size (logical slots per work group) for decode attention.
 //
@@ -237,7 +206,8 @@ int32_t forced_stages() {
 // over more batches) and 4096 by 8% (too few work groups per CU).
 int32_t pick_chunk(const vkv_cache *c, int64_t units, int32_t n_kv_max, int32_t gqa,
                    int32_t *n_chunks_out) {
-    if (!forced_chunk() && 4 * units >= 3 * (int64_t)c->n_cus && units <= c->n_cus) {
+    const int32_t forced_chunk = c->p.decode_chunk;
+    if (!forced_chunk && 4 * units >= 3 * (int64_t)c->n_cus && units <= c->n_cus) {
         *n_chunks_out = 1;
         return std::max(n_kv_max, 1);
     }
@@ -246,7 +216,7 @@ int32_t pick_chunk(const vkv_cache *c, int64_t units, int32_t n_kv_max, int32_t 
     // leave less to merge
     int32_t chunk = 2048;
     while (chunk > 64 && units * ((n_kv_max + chunk - 1) / chunk) < c->n_cus) chunk /= 2;
-    if (forced_chunk()) chunk = forced_chunk();
+    if (forced_chunk) chunk = forced_chunk;
     for (;;) {
         const int32_t nc = std::max(1, (n_kv_max + chunk - 1) / chunk);
         if (units * nc * gqa <= c->part_heads_budget || chunk >= (1 << 30)) {
@@ -317,16 +287,16 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     // 256-byte segments (measured on MI355X at 26 layers x 8192 slots: 135.4
     // against 140.0 us per step with the merge launch included).  Used when
     // its grid holds between 3/4 of the CUs and the CUs, as the one-pass
-    // k_decode; VKV_DECODE_ROWS=0 / 1 overrides.
+    // k_decode; the cache's VKV_KERNEL_DECODE_HEADS / _ROWS flags override.
     {
         const int32_t rows_chunk = 1024;
         const int32_t nc = std::max(1, (n_kv_max + rows_chunk - 1) / rows_chunk);
         const int64_t groups = (int64_t)n_streams * n_layers * nc;
         const bool shape_ok = c->p.dtype == VKV_DTYPE_F16 && G == 8 && n_q_heads == 32 &&
                               (nc == 1 || units * nc * gqa <= c->part_heads_budget);
-        const char *force = std::getenv("VKV_DECODE_ROWS");
-        const bool want = force ? env_int("VKV_DECODE_ROWS") == 1
-                                : 4 * groups >= 3 * (int64_t)c->n_cus && groups <= c->n_cus;
+        const bool want = has_flag(c, VKV_KERNEL_DECODE_ROWS) ||
+                          (!has_flag(c, VKV_KERNEL_DECODE_HEADS) &&
+                           4 * groups >= 3 * (int64_t)c->n_cus && groups <= c->n_cus);
         if (shape_ok && want) {
             a.chunk = rows_chunk;
             a.n_chunks = nc;
@@ -347,16 +317,15 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
         }
     }
     // XCD-grouped order: q8_0 head segments (136 B) share cache lines with
-    // their neighbours.  VKV_XCD_SWIZZLE=0/1 overrides.
+    // their neighbours.  The cache's XCD flags override.
     const int64_t n_wg = units * a.n_chunks;
-    const int32_t sw_env = env_int("VKV_XCD_SWIZZLE");
-    const bool sw_want = std::getenv("VKV_XCD_SWIZZLE") ? sw_env == 1
-                                                         : c->p.dtype == VKV_DTYPE_Q8_0;
+    const bool sw_want = has_flag(c, VKV_KERNEL_XCD_SWIZZLE) ||
+                         (!has_flag(c, VKV_KERNEL_NO_XCD_SWIZZLE) && c->p.dtype == VKV_DTYPE_Q8_0);
     a.xcd_swizzle = (sw_want && G == 8 && n_wg % 64 == 0) ? 1 : 0;
-    const int32_t waves = forced_waves() ? forced_waves() : 4;
-    const int32_t stages = std::min(forced_stages() ? forced_stages() : 2, waves == 8 ? 3 : 4);
-    // q8_0: the matrix-core kernel unless VKV_DECODE_MFMA=0
-    const bool mfma = !(std::getenv("VKV_DECODE_MFMA") && env_int("VKV_DECODE_MFMA") == 0);
+    const int32_t waves = c->p.decode_waves ? c->p.decode_waves : 4;
+    const int32_t stages = std::min(c->p.decode_stages ? c->p.decode_stages : 2, waves == 8 ? 3 : 4);
+    // q8_0: the matrix-core kernel unless the cache asks for the VALU one
+    const bool mfma = !has_flag(c, VKV_KERNEL_DECODE_VALU);
     hipError_t e = launch_decode(c->p.dtype, gqa, waves, stages, mfma, k_new != nullptr,
                                  n_streams, a, st);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
@@ -415,7 +384,7 @@ vkv_status do_window(vkv_cache *c, int32_t stream, int32_t layer0, int32_t n_lay
         a.n_new = n_q;
         a.wseg = seg_pair(wsegs, wnseg);
     }
-    hipError_t e = launch_window(c->p.dtype, a, st);
+    hipError_t e = launch_window(c->p.dtype, has_flag(c, VKV_KERNEL_WINDOW_VALU), a, st);
     if (e != hipSuccess) return hip_fail(e, "window attention launch");
     return VKV_STATUS_OK;
 }
@@ -603,9 +572,25 @@ vkv_status vkv_enc_plan_build(int64_t q_start, int32_t n_new, int32_t capacity, 
 vkv_status vkv_cache_create(const vkv_cache_params *params, vkv_cache **out) {
     if (!out) return fail(VKV_STATUS_INVALID_ARGUMENT, "cache create: null out");
     *out = nullptr;
-    if (!params || params->struct_size < sizeof(vkv_cache_params))
+    // Callers built against the parameter block that ends at `device` get the
+    // automatic kernel selection (the later fields read as zero).
+    constexpr size_t kBaseSize = offsetof(vkv_cache_params, kernel_flags);
+    if (!params || params->struct_size < kBaseSize)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "cache create: params missing or struct_size too small");
-    const vkv_cache_params &p = *params;
+    vkv_cache_params p{};
+    std::memcpy(&p, params, std::min<size_t>(params->struct_size, sizeof(vkv_cache_params)));
+    p.struct_size = sizeof(vkv_cache_params);
+    if ((p.kernel_flags & ~VKV_KERNEL_FLAGS_ALL) != 0 ||
+        ((p.kernel_flags & VKV_KERNEL_DECODE_HEADS) && (p.kernel_flags & VKV_KERNEL_DECODE_ROWS)) ||
+        ((p.kernel_flags & VKV_KERNEL_XCD_SWIZZLE) && (p.kernel_flags & VKV_KERNEL_NO_XCD_SWIZZLE)))
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "cache create: kernel_flags 0x%x invalid",
+                    (unsigned)p.kernel_flags);
+    if ((p.decode_chunk != 0 && (p.decode_chunk < 64 || p.decode_chunk % 64 != 0)) ||
+        (p.decode_waves != 0 && p.decode_waves != 4 && p.decode_waves != 8) ||
+        (p.decode_stages != 0 && (p.decode_stages < 2 || p.decode_stages > 4)))
+        return fail(VKV_STATUS_INVALID_ARGUMENT,
+                    "cache create: decode_chunk %d / waves %d / stages %d out of range",
+                    p.decode_chunk, p.decode_waves, p.decode_stages);
     if (p.n_streams < 1 || p.n_layers < 1 || p.capacity < 1 || p.n_kv_heads < 1 ||
         p.head_dim < 8 || p.head_dim % 8 != 0 || p.n_q_heads < p.n_kv_heads ||
         p.n_q_heads % p.n_kv_heads != 0)
@@ -1094,8 +1079,6 @@ vkv_status matvec_impl(const float *x, int64_t n_in, const float *norm_w, const 
     if (swiglu) total = outs[0].n_rows;
     const int cus = device_cus();
     int64_t rpw = (total + 8LL * cus - 1) / (8LL * cus);
-    const int32_t forced = env_int("VKV_MV_ROWS");
-    if (forced > 0) rpw = forced;
     rpw = std::max<int64_t>(1, std::min<int64_t>(rpw, 1 << 20));
     MvArgs a{};
     a.x = x;

@@ -213,7 +213,7 @@ hipError_t launch_decode(int dtype, int gqa, int waves, int stages, bool mfma, b
                          int n_streams, const DecodeArgs &a, hipStream_t st);
 hipError_t launch_decode_rows(bool fuse_append, int n_streams, const DecodeArgs &a, hipStream_t st);
 hipError_t launch_combine(const CombineArgs &a, int n_streams, hipStream_t st);
-hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st);
+hipError_t launch_window(int dtype, bool valu, const WindowArgs &a, hipStream_t st);
 hipError_t launch_q8_0_pack(const float *x, uint8_t *blocks, int64_t n, hipStream_t st);
 hipError_t launch_q8_0_unpack(const uint8_t *blocks, float *y, int64_t n, hipStream_t st);
 hipError_t launch_fill_zero(void *dst, int64_t bytes, hipStream_t st);

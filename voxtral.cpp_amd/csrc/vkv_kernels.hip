@@ -1753,16 +1753,6 @@ inline unsigned grid_for(int64_t work, int64_t per_block, int64_t cap = 1 << 20)
 // ---------------------------------------------------------------------------
 // Launchers.
 // ---------------------------------------------------------------------------
-// VKV_WINDOW_VALU=1 routes F16 window attention to the scalar-ALU kernel
-// instead of the matrix-core tile (cross-check and A/B measurement).
-static bool window_valu_forced() {
-    static const bool v = [] {
-        const char *e = getenv("VKV_WINDOW_VALU");
-        return e && e[0] == '1';
-    }();
-    return v;
-}
-
 hipError_t launch_append(int dtype, const AppendArgs &a, int n_layers, hipStream_t st) {
     const int64_t threads = ((int64_t)a.n_rows * a.kv_dim + 7) / 8;
     dim3 grid(grid_for(threads, 256, INT32_MAX), (unsigned)n_layers, 2);
@@ -1855,10 +1845,18 @@ hipError_t launch_combine(const CombineArgs &a, int n_streams, hipStream_t st) {
     return hipGetLastError();
 }
 
-hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st) {
-    const bool mfma =
-        dtype == VKV_DTYPE_F16 && !window_valu_forced() && (a.head_dim == 64 || a.head_dim == 128);
-    if (a.k_new && !mfma) {
+// valu: the scalar-ALU kernel instead of the matrix-core tile (cross-check and
+// A/B measurement)
+hipError_t launch_window(int dtype, bool valu, const WindowArgs &a_in, hipStream_t st) {
+    const bool mfma = dtype == VKV_DTYPE_F16 && !valu && (a_in.head_dim == 64 || a_in.head_dim == 128);
+    WindowArgs a = a_in;
+    // Every query tile of a kv head stores that head's new rows in the fused
+    // write, so its bytes grow with tiles x rows: keep it for calls with few
+    // tiles per head (the encoder's 16-frame chunk is one tile, a 38-token
+    // prompt ten) and append in a launch of its own above that.
+    constexpr int kMaxFusedTiles = 16;
+    const int tiles_per_head = (a.n_q * (a.n_q_heads / a.n_kv_heads) + 15) / 16;
+    if (a.k_new && (!mfma || tiles_per_head > kMaxFusedTiles)) {
         // the scalar-ALU kernel has no fused write: append first
         AppendArgs ap{};
         ap.k = a.k_w;
@@ -1873,6 +1871,9 @@ hipError_t launch_window(int dtype, const WindowArgs &a, hipStream_t st) {
         ap.seg = a.wseg;
         hipError_t e = launch_append(dtype, ap, a.n_layers, st);
         if (e != hipSuccess) return e;
+        a.k_new = nullptr;
+        a.v_new = nullptr;
+        a.n_new = 0;
     }
     if (mfma) {
         const int gqa = a.n_q_heads / a.n_kv_heads;

@@ -111,7 +111,18 @@ class CacheParams(ctypes.Structure):
                 ("n_layers", ctypes.c_int32), ("capacity", ctypes.c_int32),
                 ("n_kv_heads", ctypes.c_int32), ("head_dim", ctypes.c_int32),
                 ("n_q_heads", ctypes.c_int32), ("dtype", ctypes.c_int32),
-                ("device", ctypes.c_int32)]
+                ("device", ctypes.c_int32), ("kernel_flags", ctypes.c_int32),
+                ("decode_chunk", ctypes.c_int32), ("decode_waves", ctypes.c_int32),
+                ("decode_stages", ctypes.c_int32)]
+
+
+# vkv_cache_params.kernel_flags (cross-checks and A/B measurement only)
+KERNEL_DECODE_HEADS = 0x1
+KERNEL_DECODE_ROWS = 0x2
+KERNEL_DECODE_VALU = 0x4
+KERNEL_WINDOW_VALU = 0x8
+KERNEL_XCD_SWIZZLE = 0x10
+KERNEL_NO_XCD_SWIZZLE = 0x20
 
 
 class CacheLayout(ctypes.Structure):
@@ -390,9 +401,11 @@ class Cache:
     """Owns one vkv_cache handle (K and V storage on the device)."""
 
     def __init__(self, n_streams=1, n_layers=26, capacity=8192, n_kv_heads=8, head_dim=128,
-                 n_q_heads=32, dtype=F16, device=0):
+                 n_q_heads=32, dtype=F16, device=0, kernel_flags=0, decode_chunk=0,
+                 decode_waves=0, decode_stages=0):
         p = CacheParams(ctypes.sizeof(CacheParams), n_streams, n_layers, capacity, n_kv_heads,
-                        head_dim, n_q_heads, dtype, device)
+                        head_dim, n_q_heads, dtype, device, kernel_flags, decode_chunk,
+                        decode_waves, decode_stages)
         h = _vp()
         check(lib.vkv_cache_create(ctypes.byref(p), ctypes.byref(h)))
         self.handle = h
