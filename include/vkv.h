@@ -607,6 +607,23 @@ vkv_status vkv_decoder_token(vkv_cache *cache, int32_t stream, vkv_ring *ring,
                              float *logits, int32_t *token_out, void *workspace,
                              size_t workspace_bytes, vkv_plan *plan_out, void *hip_stream);
 
+/* vkv_decoder_token without the workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  No counterpart in the reference (its
+ * step graph allocates its work buffers once per context).  The workspace is
+ * a fixed device array of VKV_TOKEN_SCRATCH_BYTES inside the library, one
+ * copy per GPU held until the process ends; the call allocates nothing.
+ * BUFFER_TOO_SMALL when vkv_decoder_token_workspace(model) exceeds it (the
+ * realtime decoder needs ~90 KB).  Every call on one GPU shares that GPU's
+ * copy: calls that overlap on a GPU (other HIP streams, other threads) race,
+ * so serialize them.  Otherwise identical to vkv_decoder_token (the final
+ * residual stream stays in the library's array, not visible to the caller). */
+#define VKV_TOKEN_SCRATCH_BYTES (1u << 20)
+vkv_status vkv_decoder_token_noalloc(vkv_cache *cache, int32_t stream, vkv_ring *ring,
+                                     const vkv_dec_model *model, int32_t token,
+                                     const float *audio_emb, float *logits, int32_t *token_out,
+                                     vkv_plan *plan_out, void *hip_stream);
+
 /* Device workspace of a prompt of n_tokens (bytes); 0 for a bad model or count. */
 size_t vkv_decoder_prompt_workspace(const vkv_dec_model *model, int32_t n_tokens);
 

@@ -11,7 +11,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "vkv", "libvkv.so")
-SOURCES = ["vkv_kernels.hip", "vkv_matvec.hip", "vkv_conv.hip", "vkv_host.cpp", "vkv_gguf.cpp"]
+SOURCES = ["vkv_kernels.hip", "vkv_matvec.hip", "vkv_conv.hip", "vkv_static.hip", "vkv_host.cpp",
+           "vkv_gguf.cpp"]
 ARCH = os.environ.get("VKV_OFFLOAD_ARCH", "gfx950")
 
 

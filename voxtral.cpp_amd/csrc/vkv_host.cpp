@@ -395,6 +395,7 @@ namespace vkv {
 vkv_status host_fail(vkv_status st, const char *msg) { return fail(st, "%s", msg); }
 vkv_status host_hip_fail(hipError_t e, const char *what) { return hip_fail(e, what); }
 vkv_status host_ok() { return ok(); }
+int cache_device(const vkv_cache *c) { return c->p.device; }
 }  // namespace vkv
 
 extern "C" {

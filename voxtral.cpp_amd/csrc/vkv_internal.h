@@ -15,6 +15,8 @@ namespace vkv {
 vkv_status host_fail(vkv_status st, const char *msg);
 vkv_status host_hip_fail(hipError_t e, const char *what);
 vkv_status host_ok();
+// HIP device ordinal of a cache (non-null)
+int cache_device(const vkv_cache *c);
 
 // ggml_gelu_erf as the CPU path computes it: 0.5 x (1 + erf(x / sqrt(2)))
 __device__ __forceinline__ float gelu_erf(float x) {

@@ -268,6 +268,8 @@ PROTOTYPES = {
     "vkv_decoder_token_workspace": (ctypes.c_size_t, [_P(DecModel)]),
     "vkv_decoder_token": (_i32, [_vp, _i32, _P(Ring), _P(DecModel), _i32, _vp, _vp, _vp, _vp,
                                  ctypes.c_size_t, _P(Plan), _vp]),
+    "vkv_decoder_token_noalloc": (_i32, [_vp, _i32, _P(Ring), _P(DecModel), _i32, _vp, _vp, _vp,
+                                         _P(Plan), _vp]),
     "vkv_decoder_prompt_workspace": (ctypes.c_size_t, [_P(DecModel), _i32]),
     "vkv_decoder_prompt": (_i32, [_vp, _i32, _P(Ring), _P(DecModel), _P(ctypes.c_int32), _i32,
                                   _P(RowRing), _vp, _vp, _vp, ctypes.c_size_t, _P(Plan), _vp]),
@@ -624,6 +626,20 @@ def decoder_token(cache, stream, ring, model, token, audio_ptr, logits_ptr, toke
     check(lib.vkv_decoder_token(cache.handle, stream, ctypes.byref(ring), ctypes.byref(model),
                                 token, audio_ptr, logits_ptr, token_out_ptr, ws_ptr, ws_bytes,
                                 ctypes.byref(plan), hip_stream))
+    return plan
+
+
+TOKEN_SCRATCH_BYTES = 1 << 20   # VKV_TOKEN_SCRATCH_BYTES
+
+
+def decoder_token_noalloc(cache, stream, ring, model, token, audio_ptr, logits_ptr, token_out_ptr,
+                          hip_stream=0):
+    """vkv_decoder_token with the library's static per-GPU scratch as its
+    workspace (nothing allocated); returns the committed plan."""
+    plan = Plan()
+    check(lib.vkv_decoder_token_noalloc(cache.handle, stream, ctypes.byref(ring),
+                                        ctypes.byref(model), token, audio_ptr, logits_ptr,
+                                        token_out_ptr, ctypes.byref(plan), hip_stream))
     return plan
 
 
