@@ -408,9 +408,9 @@ ROWS_CASES = {
 }
 
 
-def _rows_case_run(fills, flags, rope):
+def _rows_case_run(fills, flags, rope, dtype=vkv.F16):
     ns = len(fills)
-    with vkv.Cache(n_streams=ns, n_layers=26, capacity=8192, dtype=vkv.F16,
+    with vkv.Cache(n_streams=ns, n_layers=26, capacity=8192, dtype=dtype,
                    kernel_flags=flags) as c:
         rings = (vkv.Ring * ns)(*[vkv.new_ring(8192) for _ in range(ns)])
         for s, n in enumerate(fills):
@@ -468,3 +468,30 @@ def test_whole_row_kernel_streams_and_partial_chunks(case, rope):
         worst = np.maximum(worst, errs)
     print(f"whole rows {case} rope={rope} ok: |rows-heads| {d_kernels:.2e}, |rows-fp64| "
           f"{worst[0]:.2e}, |mimic-fp64| {worst[1]:.2e}, |rows-mimic| {worst[2]:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("case", sorted(ROWS_CASES))
+def test_q8_0_whole_row_kernel_streams_and_partial_chunks(case, rope):
+    """The q8_0 whole-row decode (VKV_KERNEL_DECODE_ROWS: rows streamed flat
+    into LDS, re-packed, the matrix-core arithmetic of the per-head kernel)
+    on the same cases, against the oracle (mimic 1e-2, exact 3e-2) and
+    against the default per-head matrix-core kernel on identical caches:
+    identical cache bytes (the fused append quantizes the new row the same
+    way), outputs within 5e-3 (the two round p * d_v to f16 against
+    different running maxima)."""
+    fills = ROWS_CASES[case]
+    out_r, img_r, checks = _rows_case_run(fills, vkv.KERNEL_DECODE_ROWS, rope, vkv.Q8_0)
+    out_h, img_h, _ = _rows_case_run(fills, vkv.KERNEL_DECODE_HEADS, rope, vkv.Q8_0)
+    for a, b in zip(img_r, img_h):
+        assert np.array_equal(a, b)
+    d_kernels = float(np.max(np.abs(out_r - out_h)))
+    assert np.isfinite(out_r).all() and d_kernels <= 5e-3
+    worst = np.zeros(2)
+    for s, layer, got, exact, mimic in checks:
+        e_mimic = float(np.max(np.abs(got - mimic)))
+        e_exact = float(np.max(np.abs(got - exact)))
+        assert e_mimic <= TOL[vkv.Q8_0] and e_exact <= EXACT_TOL[vkv.Q8_0], (s, layer, e_mimic, e_exact)
+        worst = np.maximum(worst, (e_mimic, e_exact))
+    print(f"q8_0 whole rows {case} rope={rope} ok: |rows-heads| {d_kernels:.2e}, "
+          f"|rows-mimic| {worst[0]:.2e}, |rows-fp64| {worst[1]:.2e}", flush=True)

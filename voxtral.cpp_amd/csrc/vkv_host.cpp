@@ -233,6 +233,32 @@ float rope_theta_scale(float theta, int32_t head_dim) {
     return std::pow(theta, -2.0f / (float)head_dim);
 }
 
+// The 64 (cos, sin) pairs of ggml's RoPE angles at one position, as the
+// kernels' rope_table forms them: theta_i by the f32 running product (i
+// multiplications by theta_scale, no contraction), cos/sin in double rounded
+// to f32.  Kept per thread for the last position, so the layers of one
+// token evaluate them once.
+void host_rope_table(float pos, float theta_scale, float2 *tab) {
+    struct Cached {
+        bool valid = false;
+        float pos = 0.0f, ts = 0.0f;
+        float2 tab[64];
+    };
+    thread_local Cached cached;
+    if (!cached.valid || cached.pos != pos || cached.ts != theta_scale) {
+        volatile float theta = pos;   // one f32 rounding per step, as on the device
+        for (int i = 0; i < 64; ++i) {
+            const double t = (double)theta;
+            cached.tab[i] = make_float2((float)std::cos(t), (float)std::sin(t));
+            theta = theta * theta_scale;
+        }
+        cached.valid = true;
+        cached.pos = pos;
+        cached.ts = theta_scale;
+    }
+    std::memcpy(tab, cached.tab, sizeof(cached.tab));
+}
+
 vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t layer0,
                      int32_t n_layers, const SegPair *segs, const float *q, float *out,
                      int32_t n_q_heads, float scale, const float *k_new, const float *v_new,
@@ -278,6 +304,10 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
         a.rope = 1;
         a.rope_theta_scale = rope_theta_scale(*rope_theta, D);
         for (int32_t s = 0; s < n_streams; ++s) a.rope_pos[s] = (float)rope_pos[s];
+        if (n_streams == 1) {
+            host_rope_table(a.rope_pos[0], a.rope_theta_scale, a.rope_tab);
+            a.rope_host = 1;
+        }
     }
     const int64_t units = (int64_t)n_streams * n_layers * G;
     a.chunk = pick_chunk(c, units, n_kv_max, gqa, &a.n_chunks);
@@ -315,6 +345,43 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
             if (e != hipSuccess) return hip_fail(e, "combine launch");
             return VKV_STATUS_OK;
         }
+    }
+    // q8_0 by whole rows (k_decode_q8rows, with VKV_KERNEL_DECODE_ROWS):
+    // 1088-byte rows read as flat 16-byte streams, re-packed in LDS.  Its HBM
+    // reads are 1.015x the algorithmic bytes against 1.20x for the per-head
+    // kernel, but at 8 streams x 26 layers x 8192 slots it measured 766 us
+    // against 749 us (one 8-wave work group per CU, LDS-bound re-pack), so
+    // the per-head kernel stays the default.  Chunk: the largest of 1024..64
+    // slots (a multiple of the 16-slot stage) that gives every CU a work
+    // group, within the partials workspace.
+    if (c->p.dtype == VKV_DTYPE_Q8_0 && G == 8 && n_q_heads == 32 && c->row_bytes == 1088 &&
+        has_flag(c, VKV_KERNEL_DECODE_ROWS)) {
+        const int64_t row_units = (int64_t)n_streams * n_layers;
+        int32_t chunk = 1024;
+        while (chunk > 64 && row_units * ((n_kv_max + chunk - 1) / chunk) < (int64_t)c->n_cus)
+            chunk /= 2;
+        if (c->p.decode_chunk) chunk = c->p.decode_chunk;
+        int32_t nc = std::max(1, (n_kv_max + chunk - 1) / chunk);
+        while (nc > 1 && units * nc * gqa > c->part_heads_budget) {
+            chunk *= 2;
+            nc = std::max(1, (n_kv_max + chunk - 1) / chunk);
+        }
+        a.chunk = chunk;
+        a.n_chunks = nc;
+        hipError_t e = launch_decode_q8rows(k_new != nullptr, n_streams, a, st);
+        if (e != hipSuccess) return hip_fail(e, "decode launch");
+        if (a.n_chunks == 1) return VKV_STATUS_OK;
+        CombineArgs cb{};
+        cb.part_o = c->part_o;
+        cb.part_ml = c->part_ml;
+        cb.out = out;
+        cb.n_chunks = a.n_chunks;
+        cb.n_q_heads = n_q_heads;
+        cb.n_layers = n_layers;
+        cb.head_dim = D;
+        e = launch_combine(cb, n_streams, st);
+        if (e != hipSuccess) return hip_fail(e, "combine launch");
+        return VKV_STATUS_OK;
     }
     // XCD-grouped order: q8_0 head segments (136 B) share cache lines with
     // their neighbours.  The cache's XCD flags override.

@@ -70,6 +70,10 @@ struct DecodeArgs {
     float rope_theta_scale;
     float rope_pos[kMaxStreams];
     SegPair seg[kMaxStreams];
+    // rope_host != 0 (one stream): the position's 64 (cos, sin) pairs of
+    // ggml's angles, evaluated on the host, so no work group evaluates them
+    int32_t rope_host;
+    float2 rope_tab[64];
 };
 
 struct CombineArgs {
@@ -214,6 +218,9 @@ hipError_t launch_gather(const uint8_t *src, int64_t row_bytes, SegPair seg, uin
 hipError_t launch_decode(int dtype, int gqa, int waves, int stages, bool mfma, bool fuse_append,
                          int n_streams, const DecodeArgs &a, hipStream_t st);
 hipError_t launch_decode_rows(bool fuse_append, int n_streams, const DecodeArgs &a, hipStream_t st);
+// q8_0 by whole rows (8 kv heads x 128, 4 query heads each, chunk % 16 == 0)
+hipError_t launch_decode_q8rows(bool fuse_append, int n_streams, const DecodeArgs &a,
+                               hipStream_t st);
 hipError_t launch_combine(const CombineArgs &a, int n_streams, hipStream_t st);
 hipError_t launch_window(int dtype, bool valu, const WindowArgs &a, hipStream_t st);
 hipError_t launch_q8_0_pack(const float *x, uint8_t *blocks, int64_t n, hipStream_t st);

@@ -486,14 +486,23 @@ __device__ __forceinline__ void rope8(float (&x)[8], int pair0, float pos, float
 }
 
 // The same angles once per work group: lane i of wave 0 computes pair i's
-// (cos, sin) with i steps of the running product (64 pairs = head_dim 128);
-// the caller synchronises before reading tab.
+// (cos, sin) with i steps of the running product (64 pairs = head_dim 128),
+// or copies them from the host's table (rope_host, one stream); the caller
+// synchronises before reading tab.
 __device__ __forceinline__ void rope_table(float2 *tab, float pos, float theta_scale) {
 #pragma clang fp contract(off)
     if (threadIdx.x < 64) {
         float theta = pos;
         for (int i = 0; i < (int)threadIdx.x; ++i) theta *= theta_scale;
         tab[threadIdx.x] = make_float2((float)cos((double)theta), (float)sin((double)theta));
+    }
+}
+
+__device__ __forceinline__ void decode_rope_table(float2 *tab, const DecodeArgs &a, int s) {
+    if (a.rope_host) {
+        if (threadIdx.x < 64) tab[threadIdx.x] = a.rope_tab[threadIdx.x];
+    } else {
+        rope_table(tab, a.rope_pos[s], a.rope_theta_scale);
     }
 }
 
@@ -697,7 +706,7 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
     }
     __shared__ float2 sm_rope[64];
     if (a.rope) {
-        rope_table(sm_rope, a.rope_pos[s], a.rope_theta_scale);
+        decode_rope_table(sm_rope, a, s);
         __syncthreads();
     }
 
@@ -873,7 +882,7 @@ __global__ void __launch_bounds__(512) k_decode_rows(DecodeArgs a) {
     }
     __shared__ float2 sm_rope[64];
     if (a.rope) {
-        rope_table(sm_rope, a.rope_pos[s], a.rope_theta_scale);
+        decode_rope_table(sm_rope, a, s);
         __syncthreads();
     }
     F::QFrag qf[GQA];
@@ -1123,7 +1132,7 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
     }
     __shared__ float2 sm_rope[64];
     if (a.rope) {
-        rope_table(sm_rope, a.rope_pos[s], a.rope_theta_scale);
+        decode_rope_table(sm_rope, a, s);
         __syncthreads();
     }
 
@@ -1305,11 +1314,327 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
     decode_merge_finish<W, GQA>(a, it, msm);
 }
 
+// ---------------------------------------------------------------------------
+// q8_0 decode by whole rows (8 kv heads x 128, 4 query heads each).  Work
+// group = 8 waves on (stream, layer, chunk of `chunk` logical slots); wave w
+// owns kv head w over the whole chunk, so no merge between waves.  Per stage
+// of 16 slots:
+//   - the K and V rows (2 x 16 x 1088 contiguous bytes per ring segment) are
+//     read as a flat stream of 16-byte streaming loads, three stages ahead in
+//     registers, and stored raw to LDS: whole rows per load instruction, the
+//     pattern that streams fastest (the per-head 12-byte fragments of
+//     k_decode_q8mfma, 4 slots x 136 bytes per instruction, stream at about
+//     half the rate);
+//   - each wave re-packs its head's part of the raw rows into
+//     k_decode_q8mfma's tiles: per (K|V, slot) the head's 128 quants
+//     contiguous (block t at 32t, row stride QS) and its 4 block scales as a
+//     float4;
+//   - each wave runs k_decode_q8mfma's arithmetic on its head's tiles: QK on
+//     v_mfma_i32_16x16x32_i8 (Q quantized per block as the cache is, one
+//     MFMA per block, score = sum_t sumi_t d_k[t] d_q[t]), P.V on
+//     v_mfma_f32_16x16x16f16 with V^T from ds_read_b64_tr_b8.
+// ---------------------------------------------------------------------------
+// Work-group barrier that orders LDS accesses only: global loads in flight
+// stay in flight (__syncthreads' release would wait for them too).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+template <bool FUSE>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+k_decode_q8rows(DecodeArgs a) {
+    constexpr int D = 128, GQA = 4, NH = 8, SL = 16;
+    constexpr int RB = 1088;                  // q8_0 row: 32 blocks x 34 bytes
+    constexpr int QS = D + 8;                 // tile row stride (bytes)
+    constexpr int UNITS = SL * RB / 16;       // 16-byte units per stage of K (or V): 1088
+    constexpr int NU = (2 * UNITS + 511) / 512;   // units per thread per stage: 5
+    constexpr int NR = 3;                     // stages in flight
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int g = __builtin_amdgcn_readfirstlane(tid >> 6);   // this wave's kv head
+    const int kg = lane >> 4;
+    const int r = lane & 15;
+    const int chunk = blockIdx.x, layer = blockIdx.y, s = blockIdx.z;
+    const SegPair sp = a.seg[s];
+    const int n_kv = sp.n0 + sp.n1;
+    const int64_t base = (int64_t)s * a.stream_bytes + (int64_t)layer * a.layer_bytes;
+    const uint8_t *kl = a.k + base;
+    const uint8_t *vl = a.v + base;
+    const int i_begin = chunk * a.chunk;
+    const int i_end = min(i_begin + a.chunk, n_kv);
+    const bool score_lane = r < GQA;
+
+    // Raw rows at a stride of RB + 16 = 1104 bytes (276 dwords): the re-pack
+    // reads the same block of 16 rows at once, and a stride of 272 dwords
+    // put 8 of them on one LDS bank.
+    constexpr int RS = RB + 16;
+    constexpr int RAW = 16 * (512 * NU) + 16 * (512 * NU / 68 + 1);   // K rows, V rows, tail
+    __shared__ __align__(16) uint8_t sm_raw[2][RAW];
+    __shared__ __align__(16) uint8_t sm_q[2][NH][SL * QS];         // [K|V][head][slot][quants]
+    __shared__ float4 sm_d[2][NH][SL];                             // [K|V][head][slot] block scales
+    __shared__ float2 sm_rope[64];
+
+    // Stage loads: unit u < UNITS is bytes [16 (u % 68), +16) of K row u / 68
+    // of the stage, u >= UNITS the same of V; thread tid takes units tid +
+    // 512 k.  Three stages are in flight in registers.  Every load and store
+    // is issued, with no branch around it, so the compiler's wait counts
+    // stay exact: slots past the chunk end reload its last valid one (slot 0
+    // for an empty window), masked in the scores; the fifth unit of threads
+    // past the stage's 2176 repeats the last unit and is stored into the raw
+    // buffer's tail.
+    typedef uint4 Stage[NU];
+    auto load_stage = [&](int b, Stage &dst) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < NU; ++k) {
+            const int u = min(tid + 512 * k, 2 * UNITS - 1);
+            const bool v = u >= UNITS;
+            const int uu = v ? u - UNITS : u;
+            const int j = uu / 68;
+            const int ix = max(min(b + j, i_end - 1), 0);
+            dst[k] = ld16<true>((v ? vl : kl) + (int64_t)slot_of(sp, ix) * RB + (uu - j * 68) * 16);
+        }
+    };
+    auto store_stage = [&](const Stage &src, uint8_t *raw) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < NU; ++k) {
+            const int u = tid + 512 * k;
+            *reinterpret_cast<uint4 *>(raw + 16 * u + 16 * (u / 68)) = src[k];   // row u / 68
+        }
+    };
+    // Re-pack of this wave's head: lane L takes block t = L & 3 of slot
+    // j = L >> 2 of K, then of V; raw bytes [34 b, 34 b + 34) of the row
+    // (b = 4 g + t): scale, 32 quants.
+    auto repack = [&](const uint8_t *raw) __attribute__((always_inline)) {
+        const int j = lane >> 2, t = lane & 3, b = 4 * g + t;
+#pragma unroll
+        for (int kv = 0; kv < 2; ++kv) {
+            const int o = (kv * SL + j) * RS + 34 * b;        // even; o % 4 == 2 * (b & 1)
+            uint32_t w[9];
+            uint32_t dbits;
+            if ((t & 1) == 0) {
+                // o % 4 == 0: dword 0 = (scale, q0, q1), quants at byte 2
+#pragma unroll
+                for (int i = 0; i < 9; ++i) w[i] = *reinterpret_cast<const uint32_t *>(raw + o + 4 * i);
+                dbits = w[0] & 0xffffu;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) w[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+            } else {
+                // o % 4 == 2: the scale is the upper half of the dword at o - 2,
+                // the quants start dword-aligned at o + 2
+                dbits = *reinterpret_cast<const uint32_t *>(raw + o - 2) >> 16;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) w[i] = *reinterpret_cast<const uint32_t *>(raw + o + 2 + 4 * i);
+            }
+            uint8_t *dst = &sm_q[kv][g][j * QS + 32 * t];    // 8-byte aligned
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<uint2 *>(dst + 8 * i) = make_uint2(w[2 * i], w[2 * i + 1]);
+            reinterpret_cast<float *>(&sm_d[kv][g][j])[t] =
+                (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
+        }
+    };
+
+    if (a.rope) {
+        decode_rope_table(sm_rope, a, s);
+        lds_barrier();
+    }
+    // Q of head r (score lanes), dims 32 t + 8 kg + [0, 8): requested before
+    // the stage loads, so that its first use waits for these loads alone
+    // (loads complete in issue order)
+    float qx[4][8];
+    {
+        const float *qp = a.q + (int64_t)s * a.q_sstride + (int64_t)layer * a.q_lstride +
+                          (int64_t)(g * GQA + (score_lane ? r : 0)) * D + kg * 8;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const float4 q0 = score_lane ? reinterpret_cast<const float4 *>(qp + 32 * t)[0]
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 q1 = score_lane ? reinterpret_cast<const float4 *>(qp + 32 * t)[1]
+                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+            qx[t][0] = q0.x; qx[t][1] = q0.y; qx[t][2] = q0.z; qx[t][3] = q0.w;
+            qx[t][4] = q1.x; qx[t][5] = q1.y; qx[t][6] = q1.z; qx[t][7] = q1.w;
+        }
+    }
+    // The work group whose chunk holds the step's new row (the newest logical
+    // index n_kv - 1) stores it first: lanes (kg = 0, r) of wave g quantize
+    // quants [8r, 8r + 8) of head g (quads = blocks) with the block scales;
+    // the barrier's release orders those global stores before the loads.
+    if (FUSE && n_kv >= 1 && n_kv - 1 >= i_begin && n_kv - 1 < i_end) {
+        if (kg == 0) {
+            const int slot = slot_of(sp, n_kv - 1);
+            const int e = g * D + r * 8;
+            const float *kn = a.k_new + (int64_t)s * a.new_sstride + (int64_t)layer * a.new_lstride + e;
+            const float *vn = a.v_new + (int64_t)s * a.new_sstride + (int64_t)layer * a.new_lstride + e;
+            float xk[8], xv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) { xk[i] = kn[i]; xv[i] = vn[i]; }
+            if (a.rope) rope8_tab(xk, (e & 127) >> 1, sm_rope);
+            store_new<FmtQ8>(a.k_w + base + (int64_t)slot * a.row_bytes, e, xk, true);
+            store_new<FmtQ8>(a.v_w + base + (int64_t)slot * a.row_bytes, e, xv, true);
+        }
+        __syncthreads();
+    }
+    Stage stg[NR];
+#pragma unroll
+    for (int p = 0; p < NR; ++p) load_stage(i_begin + p * SL, stg[p]);
+
+    // Q quantized as the cache is (d = amax / 127, round half away from
+    // zero, d kept in f16), the block's amax across the 4 lane groups
+    int64_t qb[4];
+    float dq[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma clang fp contract(off)
+        float x[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = qx[t][i];
+        if (a.rope) rope8_tab(x, 16 * t + 4 * kg, sm_rope);
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
+        amax = fmaxf(amax, __shfl_xor(amax, 16));
+        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint64_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            w |= (uint64_t)((uint32_t)((int)round_half_away(x[i] * id)) & 0xffu) << (8 * i);
+        qb[t] = (int64_t)w;
+        dq[t] = (float)(_Float16)d;
+    }
+
+    float m = -INFINITY, l = 0.0f;
+    float4v_t o[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[t] = float4v_t{0.0f, 0.0f, 0.0f, 0.0f};
+    const uint8_t *tk = sm_q[0][g];
+    const uint8_t *tv = sm_q[1][g];
+
+    auto stage = [&](const int b) __attribute__((always_inline)) {
+        // QK: one MFMA per block t
+        int4v_t ci[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint2 ka = *reinterpret_cast<const uint2 *>(tk + r * QS + 32 * t + 8 * kg);
+            ci[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                (int64_t)(((uint64_t)ka.y << 32) | ka.x), qb[t], int4v_t{0, 0, 0, 0}, 0, 0, 0);
+        }
+        // V^T operands, block P: lane 2k+h of a group reads quants
+        // [32P + 16(k>>2) + 8h, +8) of slot 4kg + (k&3)
+        int2v_t vt8[4];
+        {
+            const int k = r >> 1, h = r & 1;
+            const int src = (4 * kg + (k & 3)) * QS + 16 * (k >> 2) + 8 * h;
+#pragma unroll
+            for (int P = 0; P < 4; ++P)
+                vt8[P] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                    (__attribute__((address_space(3))) int2v_t *)(tv + src + 32 * P));
+        }
+        float sc[4];
+        float bm = -INFINITY;
+        float4 dvs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 dk = sm_d[0][g][4 * kg + i];
+            dvs[i] = sm_d[1][g][4 * kg + i];
+            float x = 0.0f;
+            x = fmaf((float)ci[0][i], dk.x * dq[0], x);
+            x = fmaf((float)ci[1][i], dk.y * dq[1], x);
+            x = fmaf((float)ci[2][i], dk.z * dq[2], x);
+            x = fmaf((float)ci[3][i], dk.w * dq[3], x);
+            const bool ok = score_lane && b + 4 * kg + i < i_end;
+            sc[i] = ok ? x * a.scale_log2 : -INFINITY;
+            bm = fmaxf(bm, sc[i]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        // lazy rescale: the reference max moves only when a head's batch max
+        // exceeds it by more than 2^8 (p <= 256)
+        if (__any(bm > m + 8.0f)) {
+            const float mn = fmaxf(m, bm);
+            const float alpha = mn == -INFINITY ? 1.0f : fast_exp2(m - mn);
+            l *= alpha;
+            m = mn;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) o[t] *= alpha;
+        }
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            p[i] = sc[i] == -INFINITY ? 0.0f : fast_exp2(sc[i] - m);
+            l += p[i];
+        }
+        // P.V per block P: B = p * d_v[.][P] (f16), two 16-dim tiles
+#pragma unroll
+        for (int P = 0; P < 4; ++P) {
+            const half4v_t pb = {(_Float16)(p[0] * reinterpret_cast<const float *>(&dvs[0])[P]),
+                                 (_Float16)(p[1] * reinterpret_cast<const float *>(&dvs[1])[P]),
+                                 (_Float16)(p[2] * reinterpret_cast<const float *>(&dvs[2])[P]),
+                                 (_Float16)(p[3] * reinterpret_cast<const float *>(&dvs[3])[P])};
+            o[2 * P] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4((uint32_t)vt8[P].x), pb,
+                                                             o[2 * P], 0, 0, 0);
+            o[2 * P + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4((uint32_t)vt8[P].y), pb,
+                                                                 o[2 * P + 1], 0, 0, 0);
+        }
+    };
+    // One barrier per stage: stage n's raw rows go to buffer n & 1, which
+    // every wave last read (re-packing stage n - 2) before it reached stage
+    // n - 1's barrier; the tiles are per wave.
+    for (int b0 = i_begin, n = 0; b0 < i_end; b0 += NR * SL, n += NR) {
+#pragma unroll
+        for (int p = 0; p < NR; ++p) {
+            const int b = b0 + p * SL;
+            uint8_t *raw = sm_raw[(n + p) & 1];
+            store_stage(stg[p], raw);                // waits for this stage's loads only
+            load_stage(b + NR * SL, stg[p]);
+            lds_barrier();                           // raw rows complete
+            if (b < i_end) {
+                repack(raw);
+                __builtin_amdgcn_wave_barrier();
+                stage(b);
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+    }
+
+    // l over the 4 lane groups; score lane r holds query head 4g + r: dims
+    // 16 T + 4 kg + i of o[T][i]
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (score_lane) {
+        const int64_t head = ((int64_t)s * a.n_layers + layer) * a.n_q_heads + g * GQA + r;
+        if (a.n_chunks == 1) {
+            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+            float *op = a.out + head * D;
+#pragma unroll
+            for (int T = 0; T < 8; ++T)
+                *reinterpret_cast<float4 *>(op + 16 * T + 4 * kg) =
+                    make_float4(o[T][0] * inv, o[T][1] * inv, o[T][2] * inv, o[T][3] * inv);
+        } else {
+            const int64_t pidx = head * a.n_chunks + chunk;
+            float *pp = a.part_o + pidx * D;
+#pragma unroll
+            for (int T = 0; T < 8; ++T)
+                *reinterpret_cast<float4 *>(pp + 16 * T + 4 * kg) =
+                    make_float4(o[T][0], o[T][1], o[T][2], o[T][3]);
+            if (kg == 0) {
+                a.part_ml[pidx * 2] = m;
+                a.part_ml[pidx * 2 + 1] = l;
+            }
+        }
+    }
+}
+
 // One work group of head_dim (128) threads per (stream, layer, query head):
 // the chunk maxima, weights exp2(m_c - M) and the weighted sum of l_c are
 // reduced once for the group; each thread then accumulates its dimension over
 // the chunks with the partial loads batched (they do not depend on each
 // other), 128 chunk weights at a time through LDS.
+constexpr int kCombineRegs = 32;   // chunks merged from registers in one round trip
+
 __global__ void __launch_bounds__(128) k_combine(CombineArgs a) {
     __shared__ float sw[128];
     __shared__ float red[2][2];
@@ -1320,6 +1645,38 @@ __global__ void __launch_bounds__(128) k_combine(CombineArgs a) {
     const float *ml = a.part_ml + p0 * 2;
     const float *po = a.part_o + p0 * a.head_dim + t;
     const int n = a.n_chunks;
+    if (n <= kCombineRegs) {
+        // One round trip: every partial of this thread's dimension is
+        // requested together with the chunk maxima and sums (they do not
+        // depend on each other), then weighted once the maximum is known.
+        float v[kCombineRegs];
+#pragma unroll
+        for (int c = 0; c < kCombineRegs; ++c) v[c] = c < n ? po[(int64_t)c * a.head_dim] : 0.0f;
+        const float mc = t < n ? ml[2 * t] : -INFINITY;
+        const float lc = t < n ? ml[2 * t + 1] : 0.0f;
+        float m = mc;
+        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        if (lane == 0) red[0][wave] = m;
+        __syncthreads();
+        const float M = fmaxf(red[0][0], red[0][1]);
+        if (M == -INFINITY) {
+            a.out[head * a.head_dim + t] = 0.0f;
+            return;
+        }
+        const float w = t < n ? fast_exp2(mc - M) : 0.0f;
+        float l = lc * w;
+        sw[t] = w;
+        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
+        if (lane == 0) red[1][wave] = l;
+        __syncthreads();
+        float O = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kCombineRegs; ++c)
+            if (c < n) O = fmaf(v[c], sw[c], O);
+        const float L = red[1][0] + red[1][1];
+        a.out[head * a.head_dim + t] = L > 0.0f ? O / L : 0.0f;
+        return;
+    }
     float m = -INFINITY;
     for (int c = t; c < n; c += 128) m = fmaxf(m, ml[2 * c]);
     for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
@@ -1836,6 +2193,16 @@ hipError_t launch_decode_rows(bool fuse_append, int n_streams, const DecodeArgs 
     // two batches in flight per wave (three or four measured 1-2% slower)
     if (fuse_append) hipLaunchKernelGGL((k_decode_rows<true, 2>), grid, dim3(512), 0, st, a);
     else hipLaunchKernelGGL((k_decode_rows<false, 2>), grid, dim3(512), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_q8rows(bool fuse_append, int n_streams, const DecodeArgs &a,
+                               hipStream_t st) {
+    if (a.n_kv_heads != 8 || a.n_q_heads != 32 || a.row_bytes != 1088 || a.chunk % 16 != 0)
+        return hipErrorInvalidValue;
+    dim3 grid((unsigned)a.n_chunks, (unsigned)a.n_layers, (unsigned)n_streams);
+    if (fuse_append) hipLaunchKernelGGL(k_decode_q8rows<true>, grid, dim3(512), 0, st, a);
+    else hipLaunchKernelGGL(k_decode_q8rows<false>, grid, dim3(512), 0, st, a);
     return hipGetLastError();
 }
 
