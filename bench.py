@@ -27,6 +27,8 @@ Other workloads (--workload), reported on the same contract:
   encoder_f16  the encoder's streaming window: 32 layers, 32 heads x 64, an
                878-slot ring, window 750, 16 new frames per chunk appended and
                attended as a 16-query block (MFMA tile); frames/s.
+  encoder_f32  the same with the reference's default F32 encoder ring (f32
+               MFMA tile, 460 MB ring); frames/s.
   decoder_weights_q4km  the decoder step's projections on Q4_K_M weights
                (random valid blocks): per layer RMSNorm+Q/K/V (one call), O +
                residual, RMSNorm*(1+ada)+SwiGLU W1/W3, W2 + residual; then the
@@ -96,6 +98,8 @@ WORKLOADS = {
                         pmc="decode_q8_0_8x26x8192_pmc.json"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
                         pmc="encoder_f16_32x750_pmc.json"),
+    "encoder_f32": dict(dtype=0, dtype_name="f32", streams=1,
+                        pmc="encoder_f32_32x750_pmc.json"),
     "encoder_chunk_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights (MFMA int8), f16 KV",
                                streams=1, pmc="encoder_chunk_q4km_pmc.json",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) frames and "
@@ -929,10 +933,11 @@ def decode_bytes_per_stream_token(n_valid, dtype):
     return int(LAYERS * per_layer)
 
 
-def encoder_bytes_per_chunk(n_keys, P=E_CHUNK):
+def encoder_bytes_per_chunk(n_keys, P=E_CHUNK, e=2):
     """Per layer: K+V read of the window keys, new K/V f32 read, appended rows
-    (f16) write, Q read, output write -- times the layer count."""
-    per_layer = (n_keys * 2 * E_DIM * 2 + P * E_DIM * 4 * 2 + P * E_DIM * 2 * 2 + P * E_DIM * 4 +
+    write (e bytes per element: f16 2, f32 4), Q read, output write -- times
+    the layer count."""
+    per_layer = (n_keys * 2 * E_DIM * e + P * E_DIM * 4 * 2 + P * E_DIM * e * 2 + P * E_DIM * 4 +
                  P * E_DIM * 4)
     return E_LAYERS * per_layer
 
@@ -1067,14 +1072,14 @@ def gpu_stream_from_empty(n_steps, layers, prefill):
     return total_ms, step_ms, wall
 
 
-def gpu_encoder(steps, warmup):
+def gpu_encoder(steps, warmup, dtype=1):
     import torch
     import vkv
 
     st = torch.cuda.current_stream()
     sp = st.cuda_stream
     cache = vkv.Cache(n_streams=1, n_layers=E_LAYERS, capacity=E_CAP, n_kv_heads=E_HEADS,
-                      head_dim=E_HD, n_q_heads=E_HEADS, dtype=vkv.F16)
+                      head_dim=E_HD, n_q_heads=E_HEADS, dtype=dtype)
     # chunks from frame 0; the window is full (765 keys) from frame 752 on
     first = (E_WIN + E_CHUNK - 1) // E_CHUNK + 1
     T = first + warmup + steps
@@ -1307,18 +1312,20 @@ def main():
                   "layers": LAYERS, "dim": DIM, "hidden": HIDDEN, "vocab": VOCAB,
                   "weight_bytes_per_token": bytes_step, "calls_per_token": 4 * LAYERS + 1}
         kernel = "k_matvec (105 launches per token)"
-    elif args.workload == "encoder_f16":
-        total_ms, step_ms, wall, n_keys = gpu_encoder(args.steps, args.warmup)
-        bytes_step = encoder_bytes_per_chunk(n_keys)
+    elif args.workload in ("encoder_f16", "encoder_f32"):
+        total_ms, step_ms, wall, n_keys = gpu_encoder(args.steps, args.warmup, wl["dtype"])
+        e = 2 if wl["dtype"] == 1 else 4
+        bytes_step = encoder_bytes_per_chunk(n_keys, e=e)
         units_per_step = E_CHUNK
         res = {"metric": "encoder sliding-window attention + ring append frames/s at window 750",
                "unit": "frames/s"}
-        config = {"workload": "encoder streaming window: 32 layers, 32 heads x 64, 878-slot ring "
-                              "(f16), window 750, 16 new frames appended and attended per chunk "
-                              "as a 16-query block",
+        config = {"workload": f"encoder streaming window: 32 layers, 32 heads x 64, 878-slot ring "
+                              f"({wl['dtype_name']}), window 750, 16 new frames appended and "
+                              f"attended per chunk as a 16-query block",
                   "layers": E_LAYERS, "window": E_WIN, "heads": E_HEADS, "head_dim": E_HD,
                   "ring": E_CAP, "frames_per_chunk": E_CHUNK, "keys_per_query_block": n_keys}
-        kernel = "k_window_mfma<64> + k_append<FmtF16> (one chunk)"
+        kernel = ("k_window_mfma<64>" if e == 2 else "k_window_mfma_f32<64>") + \
+            " (ring append fused; one launch per chunk)"
     else:
         ns = wl["streams"]
         rope = 1.0e6 if args.workload == "longform_rope_f16" else None
@@ -1388,7 +1395,7 @@ def main():
         res["cpu_baseline"] = cpu_leg(1, args.cpu_seconds, n_keys=2048,
                                       label="26 layers at the run's mean window of 2048 positions, "
                                             "f16 KV")
-    elif not args.no_cpu and args.workload not in ("encoder_f16", "encoder_chunk_q4km",
+    elif not args.no_cpu and args.workload not in ("encoder_f16", "encoder_f32", "encoder_chunk_q4km",
                                                    "adapter_q4km", "adapter_group_q4km",
                                                    "model_load_q4km", "realtime_step_q4km"):
         res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds, streams=wl["streams"])

@@ -17,7 +17,9 @@ pytestmark = pytest.mark.gpu
 
 POOL = ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 4))
 EH, ED, ECAP, EWIN, EL = 32, 64, 878, 750, 32
-TOL = {vkv.F16: 2e-3, vkv.F32: 2e-3, vkv.Q8_0: 1e-2}
+# F32: the reference's gate for the F32 encoder ring (encoder KV against the
+# global batch within 1e-5, tests/node/baseline/encoder-kv.test.js:27)
+TOL = {vkv.F16: 2e-3, vkv.F32: 1e-5, vkv.Q8_0: 1e-2}
 
 
 def enc_inputs(layers, q_start, n):
@@ -38,7 +40,7 @@ def oracle_window(c, layer, key_pos, q_rows, q_pos, n_q_heads, n_kv_heads, head_
                                   window, scale)
 
 
-@pytest.mark.parametrize("dtype,frames", [(vkv.F16, 6000), (vkv.F32, 1200), (vkv.Q8_0, 1200)])
+@pytest.mark.parametrize("dtype,frames", [(vkv.F16, 6000), (vkv.F32, 6000), (vkv.Q8_0, 1200)])
 def test_encoder_window_chunks(dtype, frames):
     """16 new frames per chunk as a 16-query block against the window."""
     P = 16
@@ -72,7 +74,7 @@ def test_encoder_window_chunks(dtype, frames):
             print(f"encoder chunk {ch} ok", flush=True)
 
 
-@pytest.mark.parametrize("dtype", [vkv.F16, vkv.Q8_0])
+@pytest.mark.parametrize("dtype", [vkv.F16, vkv.F32, vkv.Q8_0])
 def test_decoder_prefill_then_steps(dtype):
     """38-token causal prefill at positions 0..37 (the stream prompt), a second
     10-token prefill, then a 300-token one (75 query tiles per kv head: its
@@ -178,3 +180,34 @@ def test_encoder_stream_driven_by_the_schedule(sched, batch_terminal):
         run_until_stop(target, True)
         assert emitted == target
         print(f"encoder stream: {runs_done} runs, {emitted} frames", flush=True)
+
+
+@pytest.mark.parametrize("head_dim,n_kv_heads,n_q_heads", [(64, 32, 32), (128, 8, 32)])
+def test_f32_matrix_core_tile_against_scalar_kernel(head_dim, n_kv_heads, n_q_heads):
+    """The F32 window tile on v_mfma_f32_16x16x4_f32 against the scalar-ALU
+    kernel (VKV_KERNEL_WINDOW_VALU) over the same wrapped ring and queries:
+    both f32 throughout, within 2e-6; ring bytes identical (the fused copy
+    and the separate append store the same f32 rows)."""
+    cap, layers, n_q = 878, 2, 16
+    kv_dim = n_kv_heads * head_dim
+    outs, imgs = [], []
+    for flags in (0, vkv.KERNEL_WINDOW_VALU):
+        with vkv.Cache(n_streams=1, n_layers=layers, capacity=cap, n_kv_heads=n_kv_heads,
+                       head_dim=head_dim, n_q_heads=n_q_heads, dtype=vkv.F32, kernel_flags=flags) as c:
+            for ch in range(70):                     # 1120 frames: the ring wraps
+                q_start = ch * n_q
+                plan = vkv.enc_plan(q_start, n_q, cap, EWIN)
+                q = synth(None, n_q_heads * head_dim, vkv.TAG_EQ, nl=layers, p0=q_start, np_=n_q)
+                k = synth(None, kv_dim, vkv.TAG_EK, nl=layers, p0=q_start, np_=n_q)
+                v = synth(None, kv_dim, vkv.TAG_EV, nl=layers, p0=q_start, np_=n_q)
+                out = empty_f32(layers, n_q, n_q_heads * head_dim)
+                c.enc_step(0, plan, EWIN, 0, layers, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                           out.data_ptr(), 1 / np.sqrt(head_dim), hip_stream=stream_ptr())
+            torch.cuda.synchronize()
+            outs.append(out.cpu().numpy())
+            imgs.append([layer_image(c, w, 0, l).copy() for l in range(layers) for w in (0, 1)])
+    for a, b in zip(*imgs):
+        assert np.array_equal(a, b)
+    d = float(np.max(np.abs(outs[0] - outs[1])))
+    assert np.isfinite(outs[0]).all() and d <= 2e-6, d
+    print(f"f32 tile head_dim {head_dim}: |mfma - valu| {d:.2e}", flush=True)

@@ -1899,11 +1899,11 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
 
     // Software pipeline over two register sets: the next key block's K/V
     // loads are in flight while the current one is reduced; indices clamp
-    // to the last key (blocks past the end are fully masked).
+    // into [j_lo, j_hi) (keys outside it are masked).
     auto load_kv = [&](int jb, uint4 (&kr)[DL / 8], uint4 (&vr)[DL / 8])
                        __attribute__((always_inline)) {
         // K and V of key jb+lr, dims [DL*lg, +DL): one contiguous run per lane
-        const int jk = min(jb + lr, j_hi - 1);
+        const int jk = max(min(jb + lr, j_hi - 1), j_lo);
         const uint32_t off = (uint32_t)slot_of(a.seg, jk) * (uint32_t)a.row_bytes +
                              (uint32_t)(g * D + DL * lg) * 2u;
 #pragma unroll
@@ -1938,19 +1938,21 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
         for (int i = 0; i < 4; ++i) {
             const int j = jb + 4 * lg + i;
             const int64_t kabs = a.key_pos0 + j;
-            const bool ok = row_ok && j < j_hi && kabs <= q_abs && kabs >= my_lo;
+            const bool ok = row_ok && j >= j_lo && j < j_hi && kabs <= q_abs && kabs >= my_lo;
             sc[i] = ok ? st[i] * a.scale_log2 : -INFINITY;
             bm = fmaxf(bm, sc[i]);
         }
         bm = fmaxf(bm, __shfl_xor(bm, 16));
         bm = fmaxf(bm, __shfl_xor(bm, 32));
-        if (__any(bm > m + 8.0f)) {
-            const float mn = fmaxf(m, bm);
-            const float alpha = mn == -INFINITY ? 1.0f : fast_exp2(m - mn);
+        // lazy rescale, per row: a row's running max moves only when its own
+        // block max passes it by 2^8 (rows that do not move scale by 1)
+        const bool grow = bm > m + 8.0f;
+        if (__any(grow)) {
+            const float alpha = grow && m != -INFINITY ? fast_exp2(m - bm) : 1.0f;
             l *= alpha;
 #pragma unroll
             for (int t = 0; t < KB; ++t) o[t] *= alpha;
-            m = mn;
+            m = grow ? bm : m;
         }
         half4_t pb;
 #pragma unroll
@@ -1978,11 +1980,16 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
         __builtin_amdgcn_wave_barrier();
         };
     uint4 ka_[DL / 8], va_[DL / 8], kb_[DL / 8], vb_[DL / 8];
-    int jb0 = j_lo + wave * 16;
-    if (j_lo < j_hi) load_kv(jb0, ka_, va_);   // j_hi >= 1: clamped keys are valid
+    // The block grid is absolute: wave w takes the 16-key blocks starting at
+    // key positions = 16 w (mod 64), whatever the run's first query, so a
+    // row meets its keys in the same blocks, waves and order under every
+    // chunking of the stream (schedule-invariant results, bit for bit).
+    int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & 63) + wave * 16;
+    if (j_lo < j_hi) load_kv(jb0, ka_, va_);   // j_lo < j_hi: clamped keys are valid
     for (; jb0 < j_hi; jb0 += 128) {
         load_kv(jb0 + 64, kb_, vb_);
         process(ka_, va_, jb0);
+        if (jb0 + 64 >= j_hi) break;
         load_kv(jb0 + 128, ka_, va_);
         process(kb_, vb_, jb0 + 64);
     }
@@ -2020,6 +2027,222 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
                     ((int64_t)tk * a.n_q_heads + g * gqa + rr % gqa) * D + d;
         *op = L > 0.0f ? O / L : 0.0f;
     }
+}
+
+// ---------------------------------------------------------------------------
+// Window attention on the matrix cores over an F32 cache (the reference's
+// default encoder ring, src/voxtral.cpp:100-105, :3955-3984), in f32
+// throughout with v_mfma_f32_16x16x4_f32.  Same decomposition as
+// k_window_mfma: work group = 4 waves on (layer, kv head g, 16 query rows),
+// the waves split the window's 16-key blocks.  Per key block:
+//   S^T[key][row] = K . Q^T   A lane (lg, r) = K[key r][DL lg + s] (16..32
+//                   contiguous dims per lane, one float per MFMA step s),
+//                   B lane (lg, c) = Q[row c][DL lg + s] (registers);
+//   O^T[d][row]  += V^T[d][key] P^T[key][row] with step s contracting keys
+//                   4 lg + s, so B = the lane's own softmax weight of key
+//                   4 lg + s, and A = V^T from a padded LDS tile (V rows
+//                   written transposed, stride 17 floats).
+// The fused ring write copies the new rows (F32 cache: no conversion).
+// ---------------------------------------------------------------------------
+template <int D>
+__device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
+    constexpr int DL = D / 4;           // contiguous head dims per lane
+    constexpr int NT = D / 16;          // 16-dim tiles of P.V
+    constexpr int VS = 17;              // LDS stride of the V^T tile (floats)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lg = lane >> 4;
+    const int lr = lane & 15;
+    const int gqa = a.n_q_heads / a.n_kv_heads;
+    const int g = blockIdx.x % a.n_kv_heads;
+    const int tile = blockIdx.x / a.n_kv_heads;
+    const int layer = blockIdx.y;
+    const int n_rows = a.n_q * gqa;
+    const int n_keys = a.seg.n0 + a.seg.n1;
+    const uint8_t *kl = a.k + (int64_t)layer * a.layer_bytes;
+    const uint8_t *vl = a.v + (int64_t)layer * a.layer_bytes;
+
+    __shared__ float sm_vt[4][D * VS];   // per wave: V^T[d][key]
+    __shared__ float sm_o[4][16][D + 1];
+    __shared__ float sm_m[4][16], sm_l[4][16];
+
+    // Fused ring write of kv head g's part of the n_new new rows.
+    if (a.k_new) {
+        const int kv_dim = a.n_kv_heads * D;
+        const int64_t src0 = (int64_t)layer * a.n_new * kv_dim;
+        uint8_t *kw = a.k_w + (int64_t)layer * a.layer_bytes;
+        uint8_t *vw = a.v_w + (int64_t)layer * a.layer_bytes;
+        for (int t = threadIdx.x; t < a.n_new * (D / 4); t += 256) {
+            const int row = t / (D / 4);
+            const int col = g * D + (t % (D / 4)) * 4;
+            const int64_t so = src0 + (int64_t)row * kv_dim + col;
+            const int64_t dst = (int64_t)slot_of(a.wseg, row) * a.row_bytes + (int64_t)col * 4;
+            *reinterpret_cast<float4 *>(kw + dst) = *reinterpret_cast<const float4 *>(a.k_new + so);
+            *reinterpret_cast<float4 *>(vw + dst) = *reinterpret_cast<const float4 *>(a.v_new + so);
+        }
+        __syncthreads();
+    }
+
+    // ---- Q^T operand: lane holds row lr, dims [DL lg, DL lg + DL) ----
+    const int row = tile * 16 + lr;
+    const bool row_ok = row < n_rows;
+    const int tok = row_ok ? row / gqa : 0;
+    const int64_t q_abs = a.q_pos0 + tok;
+    float qf[DL];
+    {
+        const float *qp = a.q + (int64_t)layer * a.q_lstride +
+                          ((int64_t)tok * a.n_q_heads + g * gqa + (row_ok ? row % gqa : 0)) * D + DL * lg;
+#pragma unroll
+        for (int t = 0; t < DL / 4; ++t) {
+            const float4 v4 = row_ok ? reinterpret_cast<const float4 *>(qp)[t] : make_float4(0, 0, 0, 0);
+            qf[4 * t] = v4.x; qf[4 * t + 1] = v4.y; qf[4 * t + 2] = v4.z; qf[4 * t + 3] = v4.w;
+        }
+    }
+
+    // ---- the key range any row of this tile may attend ----
+    const int row0 = tile * 16;
+    const int row1 = min(row0 + 16, n_rows) - 1;
+    const int64_t qa_lo = a.q_pos0 + row0 / gqa;
+    const int64_t qa_hi = a.q_pos0 + row1 / gqa;
+    const int64_t lo = a.window > 0 ? qa_lo - (a.window - 1) : -((int64_t)1 << 62);
+    const int j_lo = (int)max<int64_t>(0, lo - a.key_pos0);
+    const int j_hi = (int)min<int64_t>(n_keys, qa_hi - a.key_pos0 + 1);
+    const int64_t my_lo = a.window > 0 ? q_abs - (a.window - 1) : -((int64_t)1 << 62);
+
+    float m = -INFINITY, l = 0.0f;
+    float4_t o[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) o[t] = float4_t{0, 0, 0, 0};
+    float *vt = sm_vt[wave];
+
+    // K and V of key jb + lr, dims [DL lg, +DL): one contiguous run per lane;
+    // indices clamp into [j_lo, j_hi) (keys outside it are masked)
+    auto load_kv = [&](int jb, float4 (&kr)[DL / 4], float4 (&vr)[DL / 4]) __attribute__((always_inline)) {
+        const int jk = max(min(jb + lr, j_hi - 1), j_lo);
+        const uint32_t off = (uint32_t)slot_of(a.seg, jk) * (uint32_t)a.row_bytes +
+                             (uint32_t)(g * D + DL * lg) * 4u;
+#pragma unroll
+        for (int t = 0; t < DL / 4; ++t) {
+            kr[t] = reinterpret_cast<const float4 *>(kl + off)[t];
+            vr[t] = reinterpret_cast<const float4 *>(vl + off)[t];
+        }
+    };
+    auto process = [&](const float4 (&kr)[DL / 4], const float4 (&vr)[DL / 4], int jb) __attribute__((always_inline)) {
+        // V^T tile: this lane's key lr, dims DL lg + x
+#pragma unroll
+        for (int t = 0; t < DL / 4; ++t) {
+            vt[(DL * lg + 4 * t + 0) * VS + lr] = vr[t].x;
+            vt[(DL * lg + 4 * t + 1) * VS + lr] = vr[t].y;
+            vt[(DL * lg + 4 * t + 2) * VS + lr] = vr[t].z;
+            vt[(DL * lg + 4 * t + 3) * VS + lr] = vr[t].w;
+        }
+        // S^T = K Q^T, one MFMA per dim step s
+        float4_t st = float4_t{0, 0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < DL / 4; ++t) {
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].x, qf[4 * t], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].y, qf[4 * t + 1], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].z, qf[4 * t + 2], st, 0, 0, 0);
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].w, qf[4 * t + 3], st, 0, 0, 0);
+        }
+        // lane holds keys jb + 4 lg + i (i = 0..3) for row lr
+        float sc[4];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = jb + 4 * lg + i;
+            const int64_t kabs = a.key_pos0 + j;
+            const bool ok = row_ok && j >= j_lo && j < j_hi && kabs <= q_abs && kabs >= my_lo;
+            sc[i] = ok ? st[i] * a.scale_log2 : -INFINITY;
+            bm = fmaxf(bm, sc[i]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 16));
+        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        // lazy rescale, per row: a row's running max moves only when its own
+        // block max passes it by 2^8 (rows that do not move scale by 1)
+        const bool grow = bm > m + 8.0f;
+        if (__any(grow)) {
+            const float alpha = grow && m != -INFINITY ? fast_exp2(m - bm) : 1.0f;
+            l *= alpha;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) o[t] *= alpha;
+            m = grow ? bm : m;
+        }
+        float p[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            p[i] = sc[i] == -INFINITY ? 0.0f : fast_exp2(sc[i] - m);
+            l += p[i];
+        }
+        __builtin_amdgcn_wave_barrier();
+        // O^T tile T += V^T[16 T + lr][key 4 lg + s] p_s
+#pragma unroll
+        for (int T = 0; T < NT; ++T)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                o[T] = __builtin_amdgcn_mfma_f32_16x16x4f32(vt[(16 * T + lr) * VS + 4 * lg + s], p[s],
+                                                             o[T], 0, 0, 0);
+        __builtin_amdgcn_wave_barrier();
+    };
+    float4 ka_[DL / 4], va_[DL / 4], kb_[DL / 4], vb_[DL / 4];
+    // The block grid is absolute: wave w takes the 16-key blocks starting at
+    // key positions = 16 w (mod 64), whatever the run's first query, so a
+    // row meets its keys in the same blocks, waves and order under every
+    // chunking of the stream (schedule-invariant results, bit for bit).
+    int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & 63) + wave * 16;
+    if (j_lo < j_hi) load_kv(jb0, ka_, va_);   // j_lo < j_hi: clamped keys are valid
+    for (; jb0 < j_hi; jb0 += 128) {
+        load_kv(jb0 + 64, kb_, vb_);
+        process(ka_, va_, jb0);
+        if (jb0 + 64 >= j_hi) break;
+        load_kv(jb0 + 128, ka_, va_);
+        process(kb_, vb_, jb0 + 64);
+    }
+
+    // row sums over the 4 lane groups (they share m)
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    // O^T tile T: lane holds d = 16 T + 4 lg + i of row lr
+#pragma unroll
+    for (int T = 0; T < NT; ++T)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sm_o[wave][lr][16 * T + 4 * lg + i] = o[T][i];
+    if (lg == 0) {
+        sm_m[wave][lr] = m;
+        sm_l[wave][lr] = l;
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < 16 * D; t += 256) {
+        const int r = t / D;
+        const int d = t % D;
+        const int rr = tile * 16 + r;
+        if (rr >= n_rows) continue;
+        const float M = fmaxf(fmaxf(sm_m[0][r], sm_m[1][r]), fmaxf(sm_m[2][r], sm_m[3][r]));
+        float O = 0.0f, L = 0.0f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float f = fast_exp2(sm_m[w][r] - M);
+                O = fmaf(sm_o[w][r][d], f, O);
+                L = fmaf(sm_l[w][r], f, L);
+            }
+        }
+        const int tk = rr / gqa;
+        float *op = a.out + (int64_t)layer * a.q_lstride +
+                    ((int64_t)tk * a.n_q_heads + g * gqa + rr % gqa) * D + d;
+        *op = L > 0.0f ? O / L : 0.0f;
+    }
+}
+
+// head_dim 64 (the encoder): at most 128 VGPRs, so four 4-wave work groups
+// share a CU and the 32 heads x 32 layers of a chunk fit in one round of the
+// 256 CUs (at 139 VGPRs, three per CU, a third of them ran in a second round)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
+k_window_mfma_f32_64(WindowArgs a) {
+    window_mfma_f32<64>(a);
+}
+__global__ void __launch_bounds__(256) k_window_mfma_f32_128(WindowArgs a) {
+    window_mfma_f32<128>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -2215,7 +2438,8 @@ hipError_t launch_combine(const CombineArgs &a, int n_streams, hipStream_t st) {
 // valu: the scalar-ALU kernel instead of the matrix-core tile (cross-check and
 // A/B measurement)
 hipError_t launch_window(int dtype, bool valu, const WindowArgs &a_in, hipStream_t st) {
-    const bool mfma = dtype == VKV_DTYPE_F16 && !valu && (a_in.head_dim == 64 || a_in.head_dim == 128);
+    const bool mfma = (dtype == VKV_DTYPE_F16 || dtype == VKV_DTYPE_F32) && !valu &&
+                      (a_in.head_dim == 64 || a_in.head_dim == 128);
     WindowArgs a = a_in;
     // Every query tile of a kv head stores that head's new rows in the fused
     // write, so its bytes grow with tiles x rows: keep it for calls with few
@@ -2246,8 +2470,13 @@ hipError_t launch_window(int dtype, bool valu, const WindowArgs &a_in, hipStream
         const int gqa = a.n_q_heads / a.n_kv_heads;
         const int tiles = (a.n_q * gqa + 15) / 16;
         dim3 g2((unsigned)(tiles * a.n_kv_heads), (unsigned)a.n_layers);
-        if (a.head_dim == 64) hipLaunchKernelGGL(k_window_mfma<64>, g2, dim3(256), 0, st, a);
-        else hipLaunchKernelGGL(k_window_mfma<128>, g2, dim3(256), 0, st, a);
+        if (dtype == VKV_DTYPE_F32) {
+            if (a.head_dim == 64) hipLaunchKernelGGL(k_window_mfma_f32_64, g2, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL(k_window_mfma_f32_128, g2, dim3(256), 0, st, a);
+        } else {
+            if (a.head_dim == 64) hipLaunchKernelGGL(k_window_mfma<64>, g2, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL(k_window_mfma<128>, g2, dim3(256), 0, st, a);
+        }
         return hipGetLastError();
     }
     dim3 grid((unsigned)(a.n_q * a.n_q_heads), (unsigned)a.n_layers);

@@ -1049,8 +1049,8 @@ __device__ __forceinline__ float rope_elem(float self, float partner, bool odd, 
 }
 
 // Waves per work group: 8, or 16 when a call has few 16-row tiles (the
-// 1280-row products of a 16-frame chunk are 80 work groups): more waves split
-// the same K, so each walks a shorter chain of blocks.  CT column tiles (16
+// 1280-row products of the encoder are 80 tiles): more waves split the same
+// K, so each walks a shorter chain of blocks.  CT column tiles (16
 // input rows each) per work group: a wave loads each weight block once and
 // applies it to every column tile, so the weights are read once per 16 CT
 // input rows.
@@ -1204,18 +1204,6 @@ hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_r
     return hipGetLastError();
 }
 
-namespace {
-template <int CT>
-void launch_gemm_ct(const MmArgs &a, int n_tiles, int n_col_tiles, hipStream_t st) {
-    const int gy = (n_col_tiles + CT - 1) / CT;
-    const dim3 grid((unsigned)n_tiles, (unsigned)gy);
-    // (16 waves only for one column tile: their 128-register budget has no
-    // room for more accumulators)
-    if (CT == 1 && (int64_t)n_tiles * gy < 128) k_gemm_kq<16, 1><<<grid, 1024, 0, st>>>(a);
-    else k_gemm_kq<8, CT><<<grid, 512, 0, st>>>(a);
-}
-}  // namespace
-
 hipError_t launch_gemm_kq(MmArgs a, int n_col_tiles, hipStream_t st) {
     // the 16-row tiles of each matrix are consecutive work groups
     int tiles = 0;
@@ -1228,10 +1216,21 @@ hipError_t launch_gemm_kq(MmArgs a, int n_col_tiles, hipStream_t st) {
         tiles += (a.out[k].n_rows + 15) / 16;
     }
     for (int k = a.n_outs; k < kMvMaxOuts; ++k) a.out[k].tile0 = 0x7fffffff;
-    // two column tiles (32 input rows) per work group at most: a third
-    // set of accumulators spills at four waves per SIMD, and measured slower
-    if (n_col_tiles == 1) launch_gemm_ct<1>(a, tiles, n_col_tiles, st);
-    else launch_gemm_ct<2>(a, tiles, n_col_tiles, st);
+    // The waves per work group follow from the call's matrices alone, never
+    // from its number of input rows: an output's reduction order (the K split
+    // over the waves and their sum) then is the same whether its input row
+    // comes in a run of 4 or of 128, so a streamed encoder matches its batch
+    // run bit for bit.  16 waves (one column tile per work group: their
+    // 128-register budget has no room for a second set of accumulators) when
+    // the call has fewer than 128 row tiles; else 8 waves with two column
+    // tiles (32 input rows) per work group at most: a third set of
+    // accumulators spills at four waves per SIMD, and measured slower.
+    if (tiles < 128)
+        k_gemm_kq<16, 1><<<dim3((unsigned)tiles, (unsigned)n_col_tiles), 1024, 0, st>>>(a);
+    else if (n_col_tiles == 1)
+        k_gemm_kq<8, 1><<<dim3((unsigned)tiles, 1u), 512, 0, st>>>(a);
+    else
+        k_gemm_kq<8, 2><<<dim3((unsigned)tiles, (unsigned)((n_col_tiles + 1) / 2)), 512, 0, st>>>(a);
     return hipGetLastError();
 }
 
