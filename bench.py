@@ -90,16 +90,16 @@ METRIC = "decode attn+KV-append tokens/s and achieved HBM GB/s (% of peak) at 81
 # F16 = 1, Q8_0 = 8 (ggml_type numbering, as in include/vkv.h)
 WORKLOADS = {
     "longform_f16": dict(dtype=1, dtype_name="f16", streams=1,
-                         pmc="decode_f16_26x8192_pmc.json"),
+                         pmc="decode_f16_26x8192_pmc.json", kern="k_decode_rows"),
     "longform_rope_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "stream4096_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "layer1_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "q8_0_batch8": dict(dtype=8, dtype_name="q8_0", streams=8,
-                        pmc="decode_q8_0_8x26x8192_pmc.json"),
+                        pmc="decode_q8_0_8x26x8192_pmc.json", kern="k_decode_q8mfma"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
-                        pmc="encoder_f16_32x750_pmc.json"),
+                        pmc="encoder_f16_32x750_pmc.json", kern="k_window_mfma<64>"),
     "encoder_f32": dict(dtype=0, dtype_name="f32", streams=1,
-                        pmc="encoder_f32_32x750_pmc.json"),
+                        pmc="encoder_f32_32x750_pmc.json", kern="k_window_mfma_f32_64"),
     "encoder_chunk_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights (MFMA int8), f16 KV",
                                streams=1, pmc="encoder_chunk_q4km_pmc.json",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) frames and "
@@ -756,7 +756,7 @@ def gpu_token(steps, warmup):
 
     total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
     assert bool(torch.isfinite(logits).all())
-    assert ring.next_absolute_position == CAP + warmup + steps
+    assert ring.next_absolute_position == CAP + warmup + len(REP_MS) * steps
     cache.close()
     del keep
     return total_ms, step_ms, wall
@@ -942,38 +942,50 @@ def encoder_bytes_per_chunk(n_keys, P=E_CHUNK, e=2):
     return E_LAYERS * per_layer
 
 
-def timed_loop(step, steps, warmup, st, every=8):
-    """W untimed steps, then K timed steps between a synchronize and two
-    events on the launch stream.  Each run of `every` consecutive timed steps
-    is also bracketed by its own pair of events, and its duration / `every`
-    is one sample of the step's GPU time: an event record costs the GPU a few
-    microseconds, so bracketing single steps would add that to every sample
-    (and events around every step would slow the timed region)."""
+REPS = 5            # timed repetitions of the K steps; the median is reported
+REP_MS = []         # the last timed_loop's per-repetition totals (ms)
+
+
+def timed_loop(step, steps, warmup, st, every=8, reps=None):
+    """W untimed steps, then `reps` repetitions of K timed steps, each between
+    a synchronize and two events on the launch stream; returns the median
+    repetition's total (ms), the per-group samples of every repetition and
+    the wall time of all repetitions.  Each run of `every` consecutive timed
+    steps is also bracketed by its own pair of events, and its duration /
+    `every` is one sample of the step's GPU time: an event record costs the
+    GPU a few microseconds, so bracketing single steps would add that to
+    every sample (and events around every step would slow the timed region).
+    A repetition replays the same step indices (their inputs); the state the
+    steps advance (ring positions) keeps advancing."""
     import torch
+    reps = REPS if reps is None else reps
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     every = max(1, min(every, steps))
     groups = [g for g in range(0, steps - every + 1, every)]
-    ev = {g: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for g in groups}
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
+    totals, step_ms = [], []
     wall0 = time.perf_counter()
-    t_start.record(st)
-    for i in range(steps):
-        if i in ev:
-            ev[i][0].record(st)
-        step(warmup + i)
-        if i - every + 1 in ev:
-            ev[i - every + 1][1].record(st)
-    t_end.record(st)
-    torch.cuda.synchronize()
+    for _ in range(reps):
+        ev = {g: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for g in groups}
+        t_start = torch.cuda.Event(enable_timing=True)
+        t_end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t_start.record(st)
+        for i in range(steps):
+            if i in ev:
+                ev[i][0].record(st)
+            step(warmup + i)
+            if i - every + 1 in ev:
+                ev[i - every + 1][1].record(st)
+        t_end.record(st)
+        torch.cuda.synchronize()
+        totals.append(t_start.elapsed_time(t_end))
+        step_ms += [ev[g][0].elapsed_time(ev[g][1]) / every for g in groups]
     wall = time.perf_counter() - wall0
-    total_ms = t_start.elapsed_time(t_end)
-    step_ms = [ev[g][0].elapsed_time(ev[g][1]) / every for g in groups]
-    return total_ms, step_ms, wall
+    REP_MS[:] = totals
+    return sorted(totals)[len(totals) // 2], step_ms, wall
 
 
 def gpu_decode(dtype, ns, steps, warmup, rope_theta=None):
@@ -1024,7 +1036,8 @@ def gpu_decode(dtype, ns, steps, warmup, rope_theta=None):
 
     total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
     for s in range(ns):
-        assert rings[s].used == CAP and rings[s].next_absolute_position == CAP + T
+        assert rings[s].used == CAP and rings[s].next_absolute_position == CAP + warmup + \
+            len(REP_MS) * steps
     assert bool(torch.isfinite(out).all())
     cache.close()
     return total_ms, step_ms, wall
@@ -1065,7 +1078,7 @@ def gpu_stream_from_empty(n_steps, layers, prefill):
         cache.decoder_step(0, rings, [prefill + i], 0, layers, q[i].data_ptr(), k[i].data_ptr(),
                            v[i].data_ptr(), out[i].data_ptr(), scale, hip_stream=sp)
 
-    total_ms, step_ms, wall = timed_loop(step, n_steps, 0, st)
+    total_ms, step_ms, wall = timed_loop(step, n_steps, 0, st, reps=1)
     assert rings[0].next_absolute_position == prefill + n_steps
     assert bool(torch.isfinite(out).all())
     cache.close()
@@ -1109,18 +1122,42 @@ def gpu_encoder(steps, warmup, dtype=1):
     return total_ms, step_ms, wall, n_keys
 
 
+def host_cpu():
+    """The host's processor as the CPU legs see it: nproc, the CPUs this
+    process may run on, the model name (lscpu's "Model name" line)."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"nproc": os.cpu_count(), "usable_cpus": usable, "model": model}
+
+
 def cpu_leg(dtype, target_seconds, layers=LAYERS, n_keys=CAP, streams=1, label=None):
-    """The oracle's threaded ggml-CPU restatement of the same step (append +
-    attention over n_keys positions, `layers` layers) on a bounded number of
-    tokens; with several streams the CPU runs them one after another, so the
-    aggregate rate is the single-stream one."""
+    """The oracle's threaded restatement of ggml's CPU flash-attention step
+    (append + attention over n_keys positions, `layers` layers) on a bounded
+    number of tokens, in four legs: the vector leg (AVX2/FMA/F16C lanes, the
+    mimic's roundings; its threaded rate is the baseline's value) and the
+    scalar mimic, each on min(usable CPUs, 16) threads and on one thread.  The
+    scalar one-thread leg times a 2-layer sample and scales it to `layers`
+    (the step's time is linear in the layers).  With several streams the CPU
+    runs them one after another, so the aggregate rate is one stream's."""
     from concurrent.futures import ThreadPoolExecutor
 
     import numpy as np
 
     import oracle
 
-    threads = min(os.cpu_count() or 1, 16)
+    host = host_cpu()
+    threads = max(1, min(host["usable_cpus"] or 1, 16))
     rb = oracle.row_bytes(dtype, KV_DIM)
     layer_bytes = rb * n_keys
     kimg = np.empty(layers * layer_bytes, np.uint8)
@@ -1135,34 +1172,188 @@ def cpu_leg(dtype, target_seconds, layers=LAYERS, n_keys=CAP, streams=1, label=N
         list(pool.map(fill, [(img, tag, l) for img, tag in ((kimg, oracle.TAG_K), (vimg, oracle.TAG_V))
                              for l in range(layers)]))
     scale = 1.0 / (HD ** 0.5)
-    secs, n = 0.0, 0
-    while n < 1 or (secs < target_seconds and n < 64):
-        pos = n_keys + n
-        qs = np.stack([oracle.synth_row(SEED, oracle.TAG_Q, 0, l, pos, Q_DIM) for l in range(layers)])
-        ks = np.stack([oracle.synth_row(SEED, oracle.TAG_K, 0, l, pos, KV_DIM) for l in range(layers)])
-        vs = np.stack([oracle.synth_row(SEED, oracle.TAG_V, 0, l, pos, KV_DIM) for l in range(layers)])
-        dt, _ = oracle.decode_step_mimic_mt(dtype, kimg, vimg, layer_bytes, rb, layers, n_keys, qs,
-                                            QH, KVH, HD, scale, threads, ks, vs, pos % n_keys)
-        secs += dt
-        n += 1
-    name = "f16" if dtype == 1 else "q8_0"
-    what = label or f"{layers} layers, {n_keys}-position window, {name} KV"
-    return {"value": n / secs, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps ({what}) of the oracle's restatement of ggml's CPU "
-                      f"flash-attention step, {threads} threads, {secs:.1f} s"
+
+    def leg(simd, n_threads, n_layers, budget):
+        secs, n = 0.0, 0
+        while n < 1 or (secs < budget and n < 64):
+            pos = n_keys + n
+            qs = np.stack([oracle.synth_row(SEED, oracle.TAG_Q, 0, l, pos, Q_DIM) for l in range(n_layers)])
+            ks = np.stack([oracle.synth_row(SEED, oracle.TAG_K, 0, l, pos, KV_DIM) for l in range(n_layers)])
+            vs = np.stack([oracle.synth_row(SEED, oracle.TAG_V, 0, l, pos, KV_DIM) for l in range(n_layers)])
+            dt, _ = oracle.decode_step_mimic_mt(dtype, kimg, vimg, layer_bytes, rb, n_layers, n_keys,
+                                                qs, QH, KVH, HD, scale, n_threads, ks, vs,
+                                                pos % n_keys, simd=simd)
+            secs += dt
+            n += 1
+        return n, secs, n * n_layers / (secs * layers)   # tokens/s of the full `layers`
+
+    simd_ok = oracle.simd_available()
+    legs = []
+    plan = ([("vector avx2/fma/f16c", True, threads, layers, 0.3),
+             ("vector avx2/fma/f16c", True, 1, layers, 0.2)] if simd_ok else []) + \
+        [("scalar mimic", False, threads, layers, 0.3),
+         ("scalar mimic", False, 1, min(layers, 2), 0.2)]
+    for name, simd, nt, nl, share in plan:
+        n, secs, rate = leg(simd, nt, nl, target_seconds * share)
+        legs.append({"leg": name, "threads": nt, "value": round(rate, 4), "steps": n,
+                     "layers_timed": nl, "seconds": round(secs, 2)})
+    main = legs[0]
+    dname = "f16" if dtype == 1 else "q8_0"
+    what = label or f"{layers} layers, {n_keys}-position window, {dname} KV"
+    return {"value": main["value"], "unit": "tokens/s", "cores": main["threads"], "kind": "port",
+            "sample": f"{main['steps']} decode steps ({what}) of the oracle's {main['leg']} "
+                      f"restatement of ggml's CPU flash-attention step, {main['threads']} threads, "
+                      f"{main['seconds']:.1f} s; the other legs (one thread; the scalar mimic) "
+                      f"are listed under legs"
                       + (f"; the {streams} streams run one after another on the CPU, so the "
-                         f"aggregate rate equals one stream's" if streams > 1 else "")}
+                         f"aggregate rate equals one stream's" if streams > 1 else "")
+                      + ("" if simd_ok else "; this host lacks AVX2/FMA/F16C: scalar legs only"),
+            "host": host, "legs": legs}
+
+
+RDREQ = ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_128B_sum", "TCC_EA0_RDREQ_64B_sum",
+         "TCC_EA0_RDREQ_32B_sum")
+
+
+def summarize_profiles(workload, d):
+    """profiles/<name>_kernel_trace.md, _pmc.md and _pmc.json from the runs
+    of one session under directory d:
+      tr_<w>/ and tr_<w>.log      rocprofv3 --kernel-trace --stats of the bench
+                                  (its last line: the bench's JSON);
+      pmc_<w>_FETCH_SIZE/, pmc_<w>_WRITE_SIZE/, pmc_<w>_RDREQ/
+                                  --pmc runs of the bench (RDREQ: the four
+                                  TCC_EA0_RDREQ counters of RDREQ);
+      calib_FETCH_SIZE/, calib_WRITE_SIZE/, calib_RDREQ/
+                                  the same counters over --copy-calibration 512.
+    Read bytes two ways: FETCH_SIZE scaled by the copy's bytes / its
+    FETCH_SIZE, and the request counts by size (128, 64, 32 bytes), which
+    read the copy at 1.00x.  On gfx950 FETCH_SIZE's formula counts a
+    128-byte request as 64 bytes (its TCC_BUBBLE term reads 0), so the copy
+    scale is 2 and a kernel that also issues 64-byte requests is over-read by
+    the scaled figure; the per-size figure is the traffic reported."""
+    import csv
+    import glob
+
+    wl = WORKLOADS[workload]
+    kern, prefix = wl["kern"], wl["pmc"][:-len("_pmc.json")]
+
+    def rows(sub):
+        f = glob.glob(os.path.join(d, sub, "**", "*counter_collection.csv"), recursive=True)
+        if not f:
+            raise SystemExit(f"no counter_collection.csv under {os.path.join(d, sub)}")
+        with open(f[0]) as fh:
+            return list(csv.DictReader(fh))
+
+    def per_dispatch(rs, name_sub):
+        """counter -> (mean per dispatch, dispatches) over kernels matching
+        name_sub (None: the kernel with the largest counter total)"""
+        if name_sub is None:
+            tot = {}
+            for r in rs:
+                tot[r["Kernel_Name"]] = tot.get(r["Kernel_Name"], 0.0) + float(r["Counter_Value"])
+            name_sub = max(tot, key=tot.get)
+        acc = {}
+        for r in rs:
+            if name_sub in r["Kernel_Name"]:
+                acc.setdefault(r["Counter_Name"], {})[r["Dispatch_Id"]] = float(r["Counter_Value"])
+        return {c: (sum(v.values()) / len(v), len(v)) for c, v in acc.items()}
+
+    with open(os.path.join(d, f"tr_{workload}.log")) as fh:
+        line = [x for x in fh.read().splitlines() if x.startswith("{")][-1]
+    bl = json.loads(line)
+    algo = bl["roofline"]["bytes_per_launch"]
+    sf = glob.glob(os.path.join(d, f"tr_{workload}", "**", "*kernel_stats.csv"), recursive=True)
+    with open(sf[0]) as fh:
+        stats = list(csv.DictReader(fh))
+    dom = next(r for r in stats if kern in r["Name"])
+    avg_us = float(dom["AverageNs"]) / 1e3
+
+    kf = per_dispatch(rows(f"pmc_{workload}_FETCH_SIZE"), kern)["FETCH_SIZE"]
+    kw = per_dispatch(rows(f"pmc_{workload}_WRITE_SIZE"), kern)["WRITE_SIZE"]
+    kr = per_dispatch(rows(f"pmc_{workload}_RDREQ"), kern)
+    cf = per_dispatch(rows("calib_FETCH_SIZE"), None)["FETCH_SIZE"][0]
+    cw = per_dispatch(rows("calib_WRITE_SIZE"), None)["WRITE_SIZE"][0]
+    cr = per_dispatch(rows("calib_RDREQ"), None)
+    calib = 512 * (1 << 20)
+
+    def req_bytes(c):
+        return 128 * c[RDREQ[1]][0] + 64 * c[RDREQ[2]][0] + 32 * c[RDREQ[3]][0]
+
+    f_scale, w_scale = calib / (cf * 1024), calib / (cw * 1024)
+    rd_fetch = kf[0] * 1024 * f_scale
+    rd_req = req_bytes(kr)
+    wr = kw[0] * 1024 * w_scale
+    j = {"workload": bl["config"]["workload"], "kernel": kern, "dispatches": kf[1],
+         "avg_launch_us_trace": avg_us, "algorithmic_bytes_per_launch": algo,
+         "fetch_size_kib_per_launch": kf[0], "write_size_kib_per_launch": kw[0],
+         "rdreq_per_launch": {c: kr[c][0] for c in RDREQ},
+         "copy_calibration": {"bytes": calib, "fetch_size_kib": cf, "write_size_kib": cw,
+                              "fetch_scale": f_scale, "write_scale": w_scale,
+                              "rdreq_bytes": req_bytes(cr), "rdreq_scale": calib / req_bytes(cr)},
+         "hbm_read_bytes_per_launch": rd_req, "hbm_read_bytes_per_launch_fetch_size": rd_fetch,
+         "hbm_write_bytes_per_launch": wr, "traffic_bytes_per_launch": rd_req + wr,
+         "traffic_bytes_per_launch_fetch_size": rd_fetch + wr}
+    with open(os.path.join(ROOT, "profiles", f"{prefix}_pmc.json"), "w") as fh:
+        json.dump(j, fh, indent=1)
+    run = "python3 $R/bench.py --steps 20 --warmup 5 --no-cpu --workload " + workload
+    cal = "python3 $R/bench.py --copy-calibration 512"
+    cmds = [f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/pmc_{workload}_FETCH_SIZE -o p -- {run}",
+            f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/pmc_{workload}_WRITE_SIZE -o p -- {run}",
+            f"rocprofv3 --pmc {' '.join(RDREQ)} --output-format csv -d $OUT/pmc_{workload}_RDREQ -o p -- {run}",
+            f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/calib_FETCH_SIZE -o c -- {cal}",
+            f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/calib_WRITE_SIZE -o c -- {cal}",
+            f"rocprofv3 --pmc {' '.join(RDREQ)} --output-format csv -d $OUT/calib_RDREQ -o c -- {cal}",
+            f"python3 $R/bench.py --summarize {workload} --prof-dir $OUT"]
+    title = bl["config"]["workload"]
+    md = [f"# {title}: HBM traffic counters", "",
+          "Commands, one session (run from /tmp with TMPDIR=/tmp; repo at $R, output under $OUT):",
+          "", "```", *cmds, "```", "", "| quantity | value |", "|---|---|",
+          f"| `{kern}` dispatches counted | {kf[1]} |",
+          f"| FETCH_SIZE / WRITE_SIZE per dispatch | {kf[0]:.1f} / {kw[0]:.1f} KiB |",
+          "| read requests per dispatch: all / 128 B / 64 B / 32 B | " +
+          " / ".join(f"{kr[c][0]:,.0f}" for c in RDREQ) + " |",
+          f"| copy calibration (512 MiB): FETCH_SIZE / WRITE_SIZE | {cf:.1f} / {cw:.1f} KiB |",
+          f"| copy calibration: read bytes from request sizes | {req_bytes(cr):,.0f} "
+          f"({req_bytes(cr) / calib:.4f}x the copy) |",
+          f"| scale factors fetch, write (copy bytes / counter bytes) | {f_scale:.4f}, {w_scale:.4f} |",
+          f"| HBM read bytes per launch, from request sizes | {rd_req:,.0f} |",
+          f"| HBM read bytes per launch, scaled FETCH_SIZE | {rd_fetch:,.0f} |",
+          f"| HBM write bytes per launch (scaled WRITE_SIZE) | {wr:,.0f} |",
+          f"| algorithmic bytes per launch | {algo:,} |",
+          f"| traffic / algorithmic (request sizes; scaled FETCH_SIZE) | "
+          f"{(rd_req + wr) / algo:.4f}; {(rd_fetch + wr) / algo:.4f} |"]
+    with open(os.path.join(ROOT, "profiles", f"{prefix}_pmc.md"), "w") as fh:
+        fh.write("\n".join(md) + "\n")
+    tr = [f"# {title}: kernel trace", "",
+          "Command (run from /tmp with TMPDIR=/tmp; repo at $R, output under $OUT):", "", "```",
+          f"rocprofv3 --kernel-trace --stats --output-format csv -d $OUT/tr_{workload} -o trace -- "
+          f"python3 $R/bench.py --steps 200 --warmup 20 --no-cpu --workload {workload}",
+          "```", "", "| kernel | calls | avg us | min us | max us | % |", "|---|---|---|---|---|---|"]
+    for r in stats:
+        name = r["Name"].replace("vkv::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
+        tr.append(f"| {name[:80]} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                  f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                  f"{float(r['Percentage']):.2f} |")
+    tr += ["", f"Dominant kernel `{kern}`: {algo:,} algorithmic bytes / {avg_us:.2f} us = "
+               f"{algo / avg_us / 1e3:.1f} GB/s = {100 * algo / avg_us / 1e3 / HBM_PEAK_GBPS:.1f}% of "
+               f"8 TB/s (the bench's own events over the same run: "
+               f"{bl['roofline']['avg_launch_ms'] * 1e3:.2f} us per launch, frac "
+               f"{bl['roofline']['frac']})."]
+    with open(os.path.join(ROOT, "profiles", f"{prefix}_kernel_trace.md"), "w") as fh:
+        fh.write("\n".join(tr) + "\n")
+    print("\n".join(tr[-1:] + md[-9:]))
 
 
 def load_traffic(name):
+    """(traffic, traffic from scaled FETCH_SIZE) in HBM bytes per launch of
+    the dominant kernel, from the committed rocprofv3 counter runs of this
+    same workload (summarize_profiles)"""
     pmc = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(pmc):
-        return None
-    # HBM bytes per launch of the dominant kernel from the committed rocprofv3
-    # FETCH_SIZE / WRITE_SIZE runs of this same workload (scaled by a
-    # plain-copy calibration)
+        return None, None
     with open(pmc) as f:
-        return json.load(f).get("traffic_bytes_per_launch")
+        j = json.load(f)
+    return j.get("traffic_bytes_per_launch"), j.get("traffic_bytes_per_launch_fetch_size")
 
 
 def main():
@@ -1173,10 +1364,17 @@ def main():
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="longform_f16")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--summarize", choices=sorted(w for w in WORKLOADS if "kern" in WORKLOADS[w]),
+                    help="only write the workload's profiles/ summaries from the rocprofv3 runs "
+                         "under --prof-dir")
+    ap.add_argument("--prof-dir", default=".")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 20 times (scales rocprof "
                          "FETCH_SIZE/WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
+    if args.summarize:
+        summarize_profiles(args.summarize, args.prof_dir)
+        return
     if args.copy_calibration:
         import torch
         n = args.copy_calibration * (1 << 20) // 4
@@ -1193,7 +1391,7 @@ def main():
         sys.exit(2)
 
     wl = WORKLOADS[args.workload]
-    traffic = load_traffic(wl["pmc"]) if wl["pmc"] else None
+    traffic, traffic_fetch = load_traffic(wl["pmc"]) if wl["pmc"] else (None, None)
     if args.workload in ("stream4096_f16", "layer1_f16"):
         layers, prefill = (LAYERS, 0) if args.workload == "stream4096_f16" else (1, 1024)
         n_steps = 4096 if args.workload == "stream4096_f16" else args.steps
@@ -1355,6 +1553,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
+        "reps": len(REP_MS),
+        "rep_ms_per_step": [round(t / args.steps, 5) for t in REP_MS],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -1367,6 +1567,7 @@ def main():
         "roofline": {"bound": bound, "achieved": round(achieved, 1), "peak": peak,
                      "unit": "GB/s", "frac": round(achieved / peak, 4),
                      "traffic": round(traffic) if traffic else None,
+                     "traffic_scaled_fetch_size": round(traffic_fetch) if traffic_fetch else None,
                      "kernel": kernel,
                      "bytes_per_launch": bytes_step,
                      "avg_launch_ms": round(step_avg, 5)},
@@ -1399,6 +1600,8 @@ def main():
                                                    "adapter_q4km", "adapter_group_q4km",
                                                    "model_load_q4km", "realtime_step_q4km"):
         res["cpu_baseline"] = cpu_leg(wl["dtype"], args.cpu_seconds, streams=wl["streams"])
+    if "cpu_baseline" in res:
+        res["cpu_baseline"].setdefault("host", host_cpu())
     print(json.dumps(res), flush=True)
 
 

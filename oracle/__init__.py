@@ -132,6 +132,9 @@ _protos = {
     "orc_matvec": (None, [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, ctypes.c_int]),
     "orc_decode_step_mimic_mt": (_f64, [ctypes.c_int, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
                                         _i32, _i32, _i32, _f32, _vp, _vp, _vp, _i32, _i32]),
+    "orc_decode_step_simd_mt": (_f64, [ctypes.c_int, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
+                                       _i32, _i32, _i32, _f32, _vp, _vp, _vp, _i32, _i32]),
+    "orc_simd_available": (ctypes.c_int, []),
 }
 for _n, (_r, _a) in _protos.items():
     _f = getattr(lib, _n)
@@ -338,18 +341,30 @@ def window_attn_f64(dtype, k_img, v_img, row_b, k_slot, k_pos, q, q_pos, n_q_hea
     return out.reshape(n_q, n_q_heads, head_dim)
 
 
+def simd_available():
+    """whether this host runs the vector leg (AVX2, FMA and F16C)"""
+    return bool(lib.orc_simd_available())
+
+
 def decode_step_mimic_mt(dtype, k_cache, v_cache, layer_bytes, row_b, n_layers, n_valid, q,
                          n_q_heads, n_kv_heads, head_dim, scale, n_threads, k_new=None,
-                         v_new=None, new_slot=0):
+                         v_new=None, new_slot=0, simd=False):
+    """One threaded decode step (append, then attention over slots [0, n_valid)
+    of every layer) -> (wall seconds, out [n_layers][n_q_heads][head_dim]);
+    simd: each head on AVX2/FMA/F16C lanes (orc_decode_step_simd_mt)."""
+    if simd and not lib.orc_simd_available():
+        raise RuntimeError("this host lacks AVX2, FMA or F16C")
     q = np.ascontiguousarray(q, dtype=np.float32)
     out = np.empty(n_layers * n_q_heads * head_dim, dtype=np.float32)
     kn_arr = np.ascontiguousarray(k_new, dtype=np.float32) if k_new is not None else None
     vn_arr = np.ascontiguousarray(v_new, dtype=np.float32) if v_new is not None else None
     kn = _ptr(kn_arr) if kn_arr is not None else None
     vn = _ptr(vn_arr) if vn_arr is not None else None
-    secs = lib.orc_decode_step_mimic_mt(dtype, _ptr(k_cache), _ptr(v_cache), layer_bytes, row_b,
-                                        n_layers, n_valid, _ptr(q), n_q_heads, n_kv_heads,
-                                        head_dim, scale, _ptr(out), kn, vn, new_slot, n_threads)
+    fn = lib.orc_decode_step_simd_mt if simd else lib.orc_decode_step_mimic_mt
+    secs = fn(dtype, _ptr(k_cache), _ptr(v_cache), layer_bytes, row_b, n_layers, n_valid, _ptr(q),
+              n_q_heads, n_kv_heads, head_dim, scale, _ptr(out), kn, vn, new_slot, n_threads)
+    if secs < 0:
+        raise ValueError(f"vector step: head_dim {head_dim} is not a multiple of 32 up to 512")
     return secs, out.reshape(n_layers, n_q_heads, head_dim)
 
 

@@ -24,6 +24,8 @@
  *                          (append of the new K/V row, then attention over
  *                          slots [0, n_valid)) threaded over query heads within
  *                          a layer, as ggml's CPU backend splits rows.
+ * orc_decode_step_simd_mt  -- the same step with orc_simd_head (attention_simd.c:
+ *                          AVX2/FMA/F16C lanes, the mimic's roundings).
  */
 #include "vkv_oracle.h"
 
@@ -226,6 +228,7 @@ typedef struct orc_step_job {
     int32_t new_slot;
     pthread_barrier_t *barrier;
     int32_t ith;
+    int simd;
 } orc_step_job;
 
 static void *orc_step_worker(void *arg) {
@@ -251,21 +254,27 @@ static void *orc_step_worker(void *arg) {
             }
             pthread_barrier_wait(j->barrier);
         }
-        for (int32_t h = h0; h < h1; ++h)
-            orc_mimic_head(j->dtype, kl, vl, j->row_bytes, NULL, j->n_valid, 0,
-                           ql + (int64_t)h * j->head_dim, h / group, j->head_dim, j->scale,
-                           ol + (int64_t)h * j->head_dim);
+        for (int32_t h = h0; h < h1; ++h) {
+            if (j->simd)
+                orc_simd_head(j->dtype, kl, vl, j->row_bytes, j->n_valid,
+                              ql + (int64_t)h * j->head_dim, h / group, j->head_dim, j->scale,
+                              ol + (int64_t)h * j->head_dim);
+            else
+                orc_mimic_head(j->dtype, kl, vl, j->row_bytes, NULL, j->n_valid, 0,
+                               ql + (int64_t)h * j->head_dim, h / group, j->head_dim, j->scale,
+                               ol + (int64_t)h * j->head_dim);
+        }
         pthread_barrier_wait(j->barrier);   /* one graph node per layer */
     }
     return NULL;
 }
 
-double orc_decode_step_mimic_mt(int dtype, const uint8_t *k_cache, const uint8_t *v_cache,
-                                int64_t layer_bytes, int64_t row_bytes, int32_t n_layers,
-                                int32_t n_valid, const float *q, int32_t n_q_heads,
-                                int32_t n_kv_heads, int32_t head_dim, float scale,
-                                float *out, const float *k_new, const float *v_new,
-                                int32_t new_slot, int32_t n_threads) {
+static double orc_decode_step_mt(int simd, int dtype, const uint8_t *k_cache,
+                                 const uint8_t *v_cache, int64_t layer_bytes, int64_t row_bytes,
+                                 int32_t n_layers, int32_t n_valid, const float *q,
+                                 int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
+                                 float scale, float *out, const float *k_new, const float *v_new,
+                                 int32_t new_slot, int32_t n_threads) {
     if (n_threads < 1) n_threads = 1;
     if (n_threads > 64) n_threads = 64;
     pthread_t tid[64];
@@ -277,7 +286,7 @@ double orc_decode_step_mimic_mt(int dtype, const uint8_t *k_cache, const uint8_t
     for (int32_t t = 0; t < n_threads; ++t) {
         orc_step_job jb = {dtype, k_cache, v_cache, layer_bytes, row_bytes, n_layers, n_valid,
                            n_q_heads, n_kv_heads, head_dim, n_threads, q, scale, out, k_new, v_new,
-                           new_slot, &barrier, t};
+                           new_slot, &barrier, t, simd};
         jobs[t] = jb;
         if (t > 0) pthread_create(&tid[t], NULL, orc_step_worker, &jobs[t]);
     }
@@ -286,4 +295,27 @@ double orc_decode_step_mimic_mt(int dtype, const uint8_t *k_cache, const uint8_t
     clock_gettime(CLOCK_MONOTONIC, &t1);
     pthread_barrier_destroy(&barrier);
     return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
+}
+
+double orc_decode_step_mimic_mt(int dtype, const uint8_t *k_cache, const uint8_t *v_cache,
+                                int64_t layer_bytes, int64_t row_bytes, int32_t n_layers,
+                                int32_t n_valid, const float *q, int32_t n_q_heads,
+                                int32_t n_kv_heads, int32_t head_dim, float scale,
+                                float *out, const float *k_new, const float *v_new,
+                                int32_t new_slot, int32_t n_threads) {
+    return orc_decode_step_mt(0, dtype, k_cache, v_cache, layer_bytes, row_bytes, n_layers,
+                              n_valid, q, n_q_heads, n_kv_heads, head_dim, scale, out, k_new,
+                              v_new, new_slot, n_threads);
+}
+
+double orc_decode_step_simd_mt(int dtype, const uint8_t *k_cache, const uint8_t *v_cache,
+                               int64_t layer_bytes, int64_t row_bytes, int32_t n_layers,
+                               int32_t n_valid, const float *q, int32_t n_q_heads,
+                               int32_t n_kv_heads, int32_t head_dim, float scale,
+                               float *out, const float *k_new, const float *v_new,
+                               int32_t new_slot, int32_t n_threads) {
+    if (!orc_simd_available() || head_dim % 32 || head_dim > 512) return -1.0;
+    return orc_decode_step_mt(1, dtype, k_cache, v_cache, layer_bytes, row_bytes, n_layers,
+                              n_valid, q, n_q_heads, n_kv_heads, head_dim, scale, out, k_new,
+                              v_new, new_slot, n_threads);
 }

@@ -194,6 +194,21 @@ double orc_decode_step_mimic_mt(int dtype, const uint8_t *k_cache, const uint8_t
                                 int32_t n_kv_heads, int32_t head_dim, float scale,
                                 float *out, const float *k_new, const float *v_new,
                                 int32_t new_slot, int32_t n_threads);
+/* orc_decode_step_mimic_mt with each head on AVX2 + FMA + F16C lanes
+ * (attention_simd.c): -1.0 where the host lacks them or head_dim is not a
+ * multiple of 32 up to 512. */
+double orc_decode_step_simd_mt(int dtype, const uint8_t *k_cache, const uint8_t *v_cache,
+                               int64_t layer_bytes, int64_t row_bytes, int32_t n_layers,
+                               int32_t n_valid, const float *q, int32_t n_q_heads,
+                               int32_t n_kv_heads, int32_t head_dim, float scale,
+                               float *out, const float *k_new, const float *v_new,
+                               int32_t new_slot, int32_t n_threads);
+/* internal to the oracle: one head of the vector leg, and whether the host
+ * has AVX2, FMA and F16C */
+void orc_simd_head(int dtype, const uint8_t *k_layer, const uint8_t *v_layer, int64_t row_bytes,
+                   int32_t n_slots, const float *qh, int32_t g, int32_t head_dim, float scale,
+                   float *oh);
+int orc_simd_available(void);
 
 /* ---- decoder weights (kquants.c): ggml Q4_K (144 B / 256), Q6_K (210 B),
  * Q8_K activations (292 B: f32 d, i8 qs[256], i16 bsums[16]) ---- */

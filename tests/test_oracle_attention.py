@@ -3,7 +3,9 @@ vendored): exact fp64 attention against torch's scaled_dot_product_attention in
 float64 on the CPU, closed forms (all-equal scores -> mean of V, one key -> its
 value), permutation equivariance (why attending over the physical ring after a
 wrap equals the logical order, src/voxtral.cpp:2801-2807), the GQA head map,
-and the ggml-mimic reduction order against the exact result.  CPU only."""
+and the ggml-mimic reduction order against the exact result; the mimic's
+closed-form pins hold for its scalar form and for the baseline's vector leg
+(AVX2/FMA/F16C) alike.  CPU only."""
 import numpy as np
 import pytest
 import torch
@@ -169,7 +171,23 @@ def _f32(x):
     return np.float32(x)
 
 
-def test_mimic_f16_accumulator_stalls_at_2048():
+LEGS = ["scalar", pytest.param("vector", marks=pytest.mark.skipif(
+    not oracle.simd_available(), reason="host lacks AVX2/FMA/F16C"))]
+
+
+def mimic(leg, dtype, kimg, vimg, rb, n, q, scale):
+    """the mimic over slots [0, n): the scalar restatement, or the CPU
+    baseline's vector leg (one layer of the threaded step, no append)"""
+    if leg == "scalar":
+        return oracle.decode_attn_mimic(dtype, kimg, vimg, rb, np.arange(n, dtype=np.int32), q, G,
+                                        D, scale)
+    _, out = oracle.decode_step_mimic_mt(dtype, kimg, vimg, len(kimg), rb, 1, n, q.reshape(1, -1),
+                                         H, G, D, scale, 4, simd=True)
+    return out[0]
+
+
+@pytest.mark.parametrize("leg", LEGS)
+def test_mimic_f16_accumulator_stalls_at_2048(leg):
     """4096 keys with equal scores (K = 0) and V = 1.0 everywhere: ggml adds
     each weight 1.0 into an f16 accumulator, which stops growing at 2048
     (2049 is a tie that rounds to even, 2048), while the weight sum S reaches
@@ -181,12 +199,12 @@ def test_mimic_f16_accumulator_stalls_at_2048():
     q = np.random.default_rng(3).standard_normal((H, D)).astype(np.float32)
     rb = oracle.row_bytes(oracle.F16, KV)
     slots = np.arange(n, dtype=np.int32)
-    mi = oracle.decode_attn_mimic(oracle.F16, kimg, vimg, rb, slots, q, G, D, 1 / np.sqrt(D))
+    mi = mimic(leg, oracle.F16, kimg, vimg, rb, n, q, 1 / np.sqrt(D))
     assert np.all(mi == np.float32(0.5))
     ex = oracle.decode_attn_f64(oracle.F16, kimg, vimg, rb, slots, q, G, D, 1 / np.sqrt(D))
     assert np.all(ex == 1.0)
     # below the stall every partial sum is an exact f16 integer
-    mi = oracle.decode_attn_mimic(oracle.F16, kimg, vimg, rb, slots[:2048], q, G, D, 0.1)
+    mi = mimic(leg, oracle.F16, kimg, vimg, rb, 2048, q, 0.1)
     assert np.all(mi == np.float32(1.0))
 
 
@@ -201,7 +219,8 @@ MIDPOINTS = [1 + 2 ** -11,          # tie -> 1.0 (even)
              1.25 - 2 ** -12]       # tie -> 1.25 (mantissa 256, even)
 
 
-def test_mimic_rounds_q_to_f16_against_f16_k():
+@pytest.mark.parametrize("leg", LEGS)
+def test_mimic_rounds_q_to_f16_against_f16_k(leg):
     """Two keys: key 0 has K = 1.0 in dimension 0 of every kv head and V = 1.0
     in dimension 0; key 1 has K = 0 and V = 1.0 in dimension 1.  Query head h
     holds a value q_h at or near an f16 midpoint in dimension 0 and zeros
@@ -221,8 +240,7 @@ def test_mimic_rounds_q_to_f16_against_f16_k():
     for h in range(H):
         q[h, 0] = MIDPOINTS[h % len(MIDPOINTS)] * (1 + h // len(MIDPOINTS))
     rb = oracle.row_bytes(oracle.F16, KV)
-    mi = oracle.decode_attn_mimic(oracle.F16, kimg, vimg, rb, np.arange(2, dtype=np.int32), q, G, D,
-                                  scale)
+    mi = mimic(leg, oracle.F16, kimg, vimg, rb, 2, q, scale)
     for h in range(H):
         qh = oracle.f16_bits_to_f32(oracle.f32_to_f16_bits(q[h, :1]))[0]
         assert qh == np.float16(q[h, 0]).astype(np.float32)         # numpy's RNE agrees
@@ -245,7 +263,8 @@ def test_mimic_rounds_q_to_f16_against_f16_k():
         assert _ulps(_f32(w * inv), want1) >= 50, h
 
 
-def test_mimic_quantizes_q_to_q8_0_against_q8_0_k():
+@pytest.mark.parametrize("leg", LEGS)
+def test_mimic_quantizes_q_to_q8_0_against_q8_0_k(leg):
     """Two keys over a q8_0 cache.  Key 0: block 0 of every kv head holds 1.0
     in all 32 places (codes 127, d_k = f16(1/127)); V has 1.0 in dimension 0.
     Key 1: K = 0, V = 1.0 in dimension 1.  Query block 0 is
@@ -271,8 +290,7 @@ def test_mimic_quantizes_q_to_q8_0_against_q8_0_k():
     dk = oracle.f16_bits_to_f32(np.frombuffer(kimg[0:2].tobytes(), np.uint16))[0]
     assert dk == np.float32(np.float16(np.float32(1.0) / np.float32(127.0)))
     rb = oracle.row_bytes(oracle.Q8_0, KV)
-    mi = oracle.decode_attn_mimic(oracle.Q8_0, kimg, vimg, rb, np.arange(2, dtype=np.int32), q, G, D,
-                                  scale)
+    mi = mimic(leg, oracle.Q8_0, kimg, vimg, rb, 2, q, scale)
     v0 = np.float32(vst[0, 0])
     s = _f32(_f32(_f32(20066) * _f32(dk * _f32(c))) * _f32(scale))
     w = _f32(np.exp(-np.float64(s)))
@@ -285,3 +303,28 @@ def test_mimic_quantizes_q_to_q8_0_against_q8_0_k():
                  * _f32(scale))
     alt = _f32(v0 * _f32(_f32(1.0) / _f32(_f32(1.0) + _f32(np.exp(-np.float64(s_alt))))))
     assert _ulps(alt, want0) >= 1000
+
+
+@pytest.mark.skipif(not oracle.simd_available(), reason="host lacks AVX2/FMA/F16C")
+@pytest.mark.parametrize("dtype,tol", [(oracle.F32, 1e-6), (oracle.F16, 2e-4), (oracle.Q8_0, 1e-6)])
+def test_vector_leg_against_scalar_mimic(dtype, tol):
+    """The baseline's vector leg computes the mimic's function: two layers of
+    1025 seeded keys, with the step's append of a new row at slot 700 first,
+    within tol of the scalar step (only the K-row sum order differs: 8 lanes x
+    4 f32 accumulators against one double sum; for F16 the per-key f16 V
+    accumulator turns those differences into f16 ulps of the partial sums)."""
+    L, n = 2, 1025
+    rb = oracle.row_bytes(dtype, KV)
+    imgs = [np.concatenate([oracle.expected_layer(dtype, n, n, KV, n, 11, tag, 0, l)
+                            for l in range(L)]) for tag in (oracle.TAG_K, oracle.TAG_V)]
+    rng = np.random.default_rng(int(dtype) + 5)
+    q = rng.standard_normal((L, H * D)).astype(np.float32)
+    kn = rng.standard_normal((L, KV)).astype(np.float32)
+    vn = rng.standard_normal((L, KV)).astype(np.float32)
+    outs = []
+    for simd in (False, True):
+        k, v = imgs[0].copy(), imgs[1].copy()
+        _, o = oracle.decode_step_mimic_mt(dtype, k, v, rb * n, rb, L, n, q, H, G, D, 1 / np.sqrt(D),
+                                           3, k_new=kn, v_new=vn, new_slot=700, simd=simd)
+        outs.append(o)
+    assert np.max(np.abs(outs[0] - outs[1])) <= tol
