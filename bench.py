@@ -101,15 +101,15 @@ WORKLOADS = {
     "encoder_f32": dict(dtype=0, dtype_name="f32", streams=1,
                         pmc="encoder_f32_32x750_pmc.json", kern="k_window_mfma_f32_64"),
     "encoder_chunk_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights (MFMA int8), f16 KV",
-                               streams=1, pmc="encoder_chunk_q4km_pmc.json",
+                               streams=1, pmc="encoder_chunk_q4km_pmc.json", kern="",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) frames and "
                                     "KV rows, generated on device)"),
     "decoder_token_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights, f16 KV",
-                               streams=1, pmc="decoder_token_q4km_pmc.json",
+                               streams=1, pmc="decoder_token_q4km_pmc.json", kern="",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs and "
                                     "KV rows, generated on device)"),
     "adapter_q4km": dict(dtype=12, dtype_name="q4_k x q8_k weights (MFMA int8), f32 rings",
-                         streams=1, pmc="adapter_q4km_pmc.json", groups=32,
+                         streams=1, pmc="adapter_q4km_pmc.json", kern="", groups=32,
                          data="synthetic (random valid Q4_K blocks, N(0,1) encoder frames, "
                               "generated on device)"),
     "adapter_group_q4km": dict(dtype=12, dtype_name="q4_k x q8_k weights (int8 dot), f32 rings",
@@ -125,11 +125,11 @@ WORKLOADS = {
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) Mel windows "
                                     "and KV rows, generated on device)"),
     "decoder_prompt_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights (MFMA int8), f16 KV",
-                                streams=1, pmc="decoder_prompt_q4km_pmc.json",
+                                streams=1, pmc="decoder_prompt_q4km_pmc.json", kern="",
                                 data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) audio rows, "
                                      "random prompt tokens, generated on device)"),
     "decoder_weights_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k (int8 dot)", streams=1,
-                                 pmc="matvec_q4km_26l_pmc.json",
+                                 pmc="matvec_q4km_26l_pmc.json", kern="",
                                  data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs, "
                                       "generated on device)"),
 }
@@ -943,6 +943,7 @@ def encoder_bytes_per_chunk(n_keys, P=E_CHUNK, e=2):
 
 
 REPS = 5            # timed repetitions of the K steps; the median is reported
+REPS_SET = [REPS]   # the run's repetitions (--reps)
 REP_MS = []         # the last timed_loop's per-repetition totals (ms)
 
 
@@ -958,7 +959,7 @@ def timed_loop(step, steps, warmup, st, every=8, reps=None):
     A repetition replays the same step indices (their inputs); the state the
     steps advance (ring positions) keeps advancing."""
     import torch
-    reps = REPS if reps is None else reps
+    reps = REPS_SET[0] if reps is None else reps
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -1215,16 +1216,20 @@ RDREQ = ("TCC_EA0_RDREQ_sum", "TCC_EA0_RDREQ_128B_sum", "TCC_EA0_RDREQ_64B_sum",
          "TCC_EA0_RDREQ_32B_sum")
 
 
-def summarize_profiles(workload, d):
+def summarize_profiles(workload, d, out_dir):
     """profiles/<name>_kernel_trace.md, _pmc.md and _pmc.json from the runs
     of one session under directory d:
       tr_<w>/ and tr_<w>.log      rocprofv3 --kernel-trace --stats of the bench
                                   (its last line: the bench's JSON);
-      pmc_<w>_FETCH_SIZE/, pmc_<w>_WRITE_SIZE/, pmc_<w>_RDREQ/
+      pmc_<w>_FETCH_SIZE/, pmc_<w>_WRITE_SIZE/, pmc_<w>_RDREQ/ (+ .log)
                                   --pmc runs of the bench (RDREQ: the four
                                   TCC_EA0_RDREQ counters of RDREQ);
       calib_FETCH_SIZE/, calib_WRITE_SIZE/, calib_RDREQ/
                                   the same counters over --copy-calibration 512.
+    A workload with a dominant kernel is summarized per launch of it; one
+    whose step is many launches (kern "") per step, the step's kernels being
+    the library's kernels dispatched a whole number of times per executed
+    step (warmup + reps x steps).
     Read bytes two ways: FETCH_SIZE scaled by the copy's bytes / its
     FETCH_SIZE, and the request counts by size (128, 64, 32 bytes), which
     read the copy at 1.00x.  On gfx950 FETCH_SIZE's formula counts a
@@ -1236,110 +1241,180 @@ def summarize_profiles(workload, d):
 
     wl = WORKLOADS[workload]
     kern, prefix = wl["kern"], wl["pmc"][:-len("_pmc.json")]
+    step_mode = not kern
 
-    def rows(sub):
-        f = glob.glob(os.path.join(d, sub, "**", "*counter_collection.csv"), recursive=True)
+    def csv_rows(sub, pattern):
+        f = glob.glob(os.path.join(d, sub, "**", pattern), recursive=True)
         if not f:
-            raise SystemExit(f"no counter_collection.csv under {os.path.join(d, sub)}")
+            raise SystemExit(f"no {pattern} under {os.path.join(d, sub)}")
         with open(f[0]) as fh:
             return list(csv.DictReader(fh))
 
-    def per_dispatch(rs, name_sub):
-        """counter -> (mean per dispatch, dispatches) over kernels matching
-        name_sub (None: the kernel with the largest counter total)"""
-        if name_sub is None:
-            tot = {}
-            for r in rs:
-                tot[r["Kernel_Name"]] = tot.get(r["Kernel_Name"], 0.0) + float(r["Counter_Value"])
-            name_sub = max(tot, key=tot.get)
+    def bench_line(log):
+        with open(os.path.join(d, log)) as fh:
+            return json.loads([x for x in fh.read().splitlines() if x.startswith("{")][-1])
+
+    def executed(b):
+        return b["warmup"] + b.get("reps", 1) * b["steps"]
+
+    bl = bench_line(f"tr_{workload}.log")
+    algo = bl["roofline"]["bytes_per_launch"]
+    trace = csv_rows(f"tr_{workload}", "*kernel_trace.csv")
+    stats = csv_rows(f"tr_{workload}", "*kernel_stats.csv")
+    n_tr = executed(bl)
+    calls = {}
+    for r in trace:
+        calls[r["Kernel_Name"]] = calls.get(r["Kernel_Name"], 0) + 1
+    if step_mode:
+        # the library's kernels dispatched a whole number of times per step
+        # (setup kernels -- weight generation, fills -- run a count unrelated
+        # to the steps)
+        names = {k for k, v in calls.items() if "vkv::" in k and v >= n_tr and v % n_tr == 0}
+    else:
+        names = {k for k in calls if kern in k}
+
+    def matches(name):
+        return name in names
+
+    # the step's time: kernel durations, and the span with the gaps between
+    # consecutive step kernels (gaps over 200 us are the host's syncs and
+    # the setup, not the step's)
+    disp = sorted((int(r["Start_Timestamp"]), int(r["End_Timestamp"])) for r in trace
+                  if matches(r["Kernel_Name"]))
+    busy = sum(e - b for b, e in disp)
+    gaps = sum(max(0, b2 - e1) for (_, e1), (b2, _) in zip(disp, disp[1:]) if b2 - e1 < 200_000)
+    per = n_tr if step_mode else len(disp)
+    kernel_us, span_us = busy / per / 1e3, (busy + gaps) / per / 1e3
+    avg_us = kernel_us
+
+    def pmc(c):
+        b = bench_line(f"pmc_{workload}_{c}.log")
+        rs = csv_rows(f"pmc_{workload}_{c}", "*counter_collection.csv")
+        acc, seen = {}, set()
+        for r in rs:
+            if matches(r["Kernel_Name"]):
+                acc[r["Counter_Name"]] = acc.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+                seen.add(r["Dispatch_Id"])
+        n = executed(b) if step_mode else len(seen)
+        return {k: v / n for k, v in acc.items()}, len(seen)
+
+    def calib(c):
+        rs = csv_rows(f"calib_{c}", "*counter_collection.csv")
+        tot = {}
+        for r in rs:
+            tot[r["Kernel_Name"]] = tot.get(r["Kernel_Name"], 0.0) + float(r["Counter_Value"])
+        big = max(tot, key=tot.get)
         acc = {}
         for r in rs:
-            if name_sub in r["Kernel_Name"]:
+            if r["Kernel_Name"] == big:
                 acc.setdefault(r["Counter_Name"], {})[r["Dispatch_Id"]] = float(r["Counter_Value"])
-        return {c: (sum(v.values()) / len(v), len(v)) for c, v in acc.items()}
+        return {k: sum(v.values()) / len(v) for k, v in acc.items()}
 
-    with open(os.path.join(d, f"tr_{workload}.log")) as fh:
-        line = [x for x in fh.read().splitlines() if x.startswith("{")][-1]
-    bl = json.loads(line)
-    algo = bl["roofline"]["bytes_per_launch"]
-    sf = glob.glob(os.path.join(d, f"tr_{workload}", "**", "*kernel_stats.csv"), recursive=True)
-    with open(sf[0]) as fh:
-        stats = list(csv.DictReader(fh))
-    dom = next(r for r in stats if kern in r["Name"])
-    avg_us = float(dom["AverageNs"]) / 1e3
-
-    kf = per_dispatch(rows(f"pmc_{workload}_FETCH_SIZE"), kern)["FETCH_SIZE"]
-    kw = per_dispatch(rows(f"pmc_{workload}_WRITE_SIZE"), kern)["WRITE_SIZE"]
-    kr = per_dispatch(rows(f"pmc_{workload}_RDREQ"), kern)
-    cf = per_dispatch(rows("calib_FETCH_SIZE"), None)["FETCH_SIZE"][0]
-    cw = per_dispatch(rows("calib_WRITE_SIZE"), None)["WRITE_SIZE"][0]
-    cr = per_dispatch(rows("calib_RDREQ"), None)
-    calib = 512 * (1 << 20)
+    kf, nd = pmc("FETCH_SIZE")
+    kf = kf["FETCH_SIZE"]
+    kw = pmc("WRITE_SIZE")[0]["WRITE_SIZE"]
+    kr = pmc("RDREQ")[0]
+    cf, cw, cr = calib("FETCH_SIZE")["FETCH_SIZE"], calib("WRITE_SIZE")["WRITE_SIZE"], calib("RDREQ")
+    cal_bytes = 512 * (1 << 20)
 
     def req_bytes(c):
-        return 128 * c[RDREQ[1]][0] + 64 * c[RDREQ[2]][0] + 32 * c[RDREQ[3]][0]
+        return 128 * c[RDREQ[1]] + 64 * c[RDREQ[2]] + 32 * c[RDREQ[3]]
 
-    f_scale, w_scale = calib / (cf * 1024), calib / (cw * 1024)
-    rd_fetch = kf[0] * 1024 * f_scale
+    f_scale, w_scale = cal_bytes / (cf * 1024), cal_bytes / (cw * 1024)
+    rd_fetch = kf * 1024 * f_scale
     rd_req = req_bytes(kr)
-    wr = kw[0] * 1024 * w_scale
-    j = {"workload": bl["config"]["workload"], "kernel": kern, "dispatches": kf[1],
-         "avg_launch_us_trace": avg_us, "algorithmic_bytes_per_launch": algo,
-         "fetch_size_kib_per_launch": kf[0], "write_size_kib_per_launch": kw[0],
-         "rdreq_per_launch": {c: kr[c][0] for c in RDREQ},
-         "copy_calibration": {"bytes": calib, "fetch_size_kib": cf, "write_size_kib": cw,
+    wr = kw * 1024 * w_scale
+    unit = "step" if step_mode else "launch"
+    j = {"workload": bl["config"]["workload"], "kernel": kern or "the step's kernels",
+         "unit": unit, "dispatches_counted": nd, "algorithmic_bytes_per_launch": algo,
+         "kernel_us_per_launch": kernel_us, "span_us_per_launch": span_us,
+         "fetch_size_kib_per_launch": kf, "write_size_kib_per_launch": kw,
+         "rdreq_per_launch": {c: kr[c] for c in RDREQ},
+         "copy_calibration": {"bytes": cal_bytes, "fetch_size_kib": cf, "write_size_kib": cw,
                               "fetch_scale": f_scale, "write_scale": w_scale,
-                              "rdreq_bytes": req_bytes(cr), "rdreq_scale": calib / req_bytes(cr)},
+                              "rdreq_bytes": req_bytes(cr), "rdreq_scale": cal_bytes / req_bytes(cr)},
          "hbm_read_bytes_per_launch": rd_req, "hbm_read_bytes_per_launch_fetch_size": rd_fetch,
          "hbm_write_bytes_per_launch": wr, "traffic_bytes_per_launch": rd_req + wr,
          "traffic_bytes_per_launch_fetch_size": rd_fetch + wr}
-    with open(os.path.join(ROOT, "profiles", f"{prefix}_pmc.json"), "w") as fh:
+    if step_mode:
+        j["dispatches_per_step"] = len(disp) / n_tr
+    with open(os.path.join(out_dir, f"{prefix}_pmc.json"), "w") as fh:
         json.dump(j, fh, indent=1)
-    run = "python3 $R/bench.py --steps 20 --warmup 5 --no-cpu --workload " + workload
+    pb = bench_line(f"pmc_{workload}_FETCH_SIZE.log")
+
+    def args_of(b):
+        return f"--steps {b['steps']} --warmup {b['warmup']} --reps {b.get('reps', 1)}"
+
+    run = f"python3 $R/bench.py {args_of(pb)} --no-cpu --workload {workload}"
     cal = "python3 $R/bench.py --copy-calibration 512"
-    cmds = [f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/pmc_{workload}_FETCH_SIZE -o p -- {run}",
-            f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/pmc_{workload}_WRITE_SIZE -o p -- {run}",
-            f"rocprofv3 --pmc {' '.join(RDREQ)} --output-format csv -d $OUT/pmc_{workload}_RDREQ -o p -- {run}",
+    cmds = [f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/pmc_{workload}_FETCH_SIZE -o p -- {run} > $OUT/pmc_{workload}_FETCH_SIZE.log",
+            f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/pmc_{workload}_WRITE_SIZE -o p -- {run} > $OUT/pmc_{workload}_WRITE_SIZE.log",
+            f"rocprofv3 --pmc {' '.join(RDREQ)} --output-format csv -d $OUT/pmc_{workload}_RDREQ -o p -- {run} > $OUT/pmc_{workload}_RDREQ.log",
             f"rocprofv3 --pmc FETCH_SIZE --output-format csv -d $OUT/calib_FETCH_SIZE -o c -- {cal}",
             f"rocprofv3 --pmc WRITE_SIZE --output-format csv -d $OUT/calib_WRITE_SIZE -o c -- {cal}",
             f"rocprofv3 --pmc {' '.join(RDREQ)} --output-format csv -d $OUT/calib_RDREQ -o c -- {cal}",
-            f"python3 $R/bench.py --summarize {workload} --prof-dir $OUT"]
+            f"python3 $R/bench.py --summarize {workload} --prof-dir $OUT --summary-dir $R/profiles"]
     title = bl["config"]["workload"]
+    what = "step" if step_mode else f"dispatch of `{kern}`"
     md = [f"# {title}: HBM traffic counters", "",
           "Commands, one session (run from /tmp with TMPDIR=/tmp; repo at $R, output under $OUT):",
-          "", "```", *cmds, "```", "", "| quantity | value |", "|---|---|",
-          f"| `{kern}` dispatches counted | {kf[1]} |",
-          f"| FETCH_SIZE / WRITE_SIZE per dispatch | {kf[0]:.1f} / {kw[0]:.1f} KiB |",
-          "| read requests per dispatch: all / 128 B / 64 B / 32 B | " +
-          " / ".join(f"{kr[c][0]:,.0f}" for c in RDREQ) + " |",
+          "", "```", *cmds, "```", "", f"Per {what}:", "", "| quantity | value |", "|---|---|",
+          f"| dispatches counted | {nd} |",
+          f"| FETCH_SIZE / WRITE_SIZE | {kf:.1f} / {kw:.1f} KiB |",
+          "| read requests: all / 128 B / 64 B / 32 B | " +
+          " / ".join(f"{kr[c]:,.0f}" for c in RDREQ) + " |",
           f"| copy calibration (512 MiB): FETCH_SIZE / WRITE_SIZE | {cf:.1f} / {cw:.1f} KiB |",
           f"| copy calibration: read bytes from request sizes | {req_bytes(cr):,.0f} "
-          f"({req_bytes(cr) / calib:.4f}x the copy) |",
+          f"({req_bytes(cr) / cal_bytes:.4f}x the copy) |",
           f"| scale factors fetch, write (copy bytes / counter bytes) | {f_scale:.4f}, {w_scale:.4f} |",
-          f"| HBM read bytes per launch, from request sizes | {rd_req:,.0f} |",
-          f"| HBM read bytes per launch, scaled FETCH_SIZE | {rd_fetch:,.0f} |",
-          f"| HBM write bytes per launch (scaled WRITE_SIZE) | {wr:,.0f} |",
-          f"| algorithmic bytes per launch | {algo:,} |",
+          f"| HBM read bytes, from request sizes | {rd_req:,.0f} |",
+          f"| HBM read bytes, scaled FETCH_SIZE | {rd_fetch:,.0f} |",
+          f"| HBM write bytes (scaled WRITE_SIZE) | {wr:,.0f} |",
+          f"| algorithmic bytes | {algo:,} |",
           f"| traffic / algorithmic (request sizes; scaled FETCH_SIZE) | "
           f"{(rd_req + wr) / algo:.4f}; {(rd_fetch + wr) / algo:.4f} |"]
-    with open(os.path.join(ROOT, "profiles", f"{prefix}_pmc.md"), "w") as fh:
+    with open(os.path.join(out_dir, f"{prefix}_pmc.md"), "w") as fh:
         fh.write("\n".join(md) + "\n")
     tr = [f"# {title}: kernel trace", "",
           "Command (run from /tmp with TMPDIR=/tmp; repo at $R, output under $OUT):", "", "```",
           f"rocprofv3 --kernel-trace --stats --output-format csv -d $OUT/tr_{workload} -o trace -- "
-          f"python3 $R/bench.py --steps 200 --warmup 20 --no-cpu --workload {workload}",
-          "```", "", "| kernel | calls | avg us | min us | max us | % |", "|---|---|---|---|---|---|"]
-    for r in stats:
-        name = r["Name"].replace("vkv::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
-        tr.append(f"| {name[:80]} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
-                  f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
-                  f"{float(r['Percentage']):.2f} |")
-    tr += ["", f"Dominant kernel `{kern}`: {algo:,} algorithmic bytes / {avg_us:.2f} us = "
-               f"{algo / avg_us / 1e3:.1f} GB/s = {100 * algo / avg_us / 1e3 / HBM_PEAK_GBPS:.1f}% of "
-               f"8 TB/s (the bench's own events over the same run: "
-               f"{bl['roofline']['avg_launch_ms'] * 1e3:.2f} us per launch, frac "
-               f"{bl['roofline']['frac']})."]
-    with open(os.path.join(ROOT, "profiles", f"{prefix}_kernel_trace.md"), "w") as fh:
+          f"python3 $R/bench.py {args_of(bl)} --no-cpu --workload {workload} > $OUT/tr_{workload}.log",
+          "```", ""]
+    short = lambda n: n.replace("vkv::(anonymous namespace)::", "").replace("(anonymous namespace)::", "")
+    if step_mode:
+        tr += [f"{n_tr} executed steps; the step's kernels by grid (one row per matrix or "
+               f"launch shape):", "",
+               "| kernel | grid (threads) | per step | avg us | us per step |", "|---|---|---|---|---|"]
+        per_name = {}
+        for r in trace:
+            if matches(r["Kernel_Name"]):
+                key = (r["Kernel_Name"], f"{r['Grid_Size_X']}x{r['Grid_Size_Y']}")
+                a = per_name.setdefault(key, [0, 0])
+                a[0] += 1
+                a[1] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        for (n, g), (c, t) in sorted(per_name.items(), key=lambda kv: -kv[1][1]):
+            tr.append(f"| {short(n)[:70]} | {g} | {c / n_tr:.2f} | {t / c / 1e3:.2f} | "
+                      f"{t / n_tr / 1e3:.1f} |")
+        tr += ["", f"Per step: {len(disp) / n_tr:.1f} dispatches, {kernel_us:.1f} us of kernels, "
+                   f"{span_us:.1f} us from the first kernel's start to the last one's end "
+                   f"(gaps {span_us - kernel_us:.1f} us); {algo:,} algorithmic bytes / {kernel_us:.1f} us "
+                   f"of kernels = {algo / kernel_us / 1e3:.1f} GB/s ({100 * algo / kernel_us / 1e3 / HBM_PEAK_GBPS:.1f}% "
+                   f"of 8 TB/s); the bench's own events over the same run: "
+                   f"{bl['roofline']['avg_launch_ms'] * 1e3:.1f} us per step."]
+    else:
+        tr += ["| kernel | calls | avg us | min us | max us | % |", "|---|---|---|---|---|---|"]
+        for r in stats:
+            tr.append(f"| {short(r['Name'])[:80]} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                      f"{float(r['MinNs']) / 1e3:.2f} | {float(r['MaxNs']) / 1e3:.2f} | "
+                      f"{float(r['Percentage']):.2f} |")
+        dom = next(r for r in stats if kern in r["Name"])
+        avg_us = float(dom["AverageNs"]) / 1e3
+        tr += ["", f"Dominant kernel `{kern}`: {algo:,} algorithmic bytes / {avg_us:.2f} us = "
+                   f"{algo / avg_us / 1e3:.1f} GB/s = {100 * algo / avg_us / 1e3 / HBM_PEAK_GBPS:.1f}% of "
+                   f"8 TB/s (the bench's own events over the same run: "
+                   f"{bl['roofline']['avg_launch_ms'] * 1e3:.2f} us per launch, frac "
+                   f"{bl['roofline']['frac']})."]
+    with open(os.path.join(out_dir, f"{prefix}_kernel_trace.md"), "w") as fh:
         fh.write("\n".join(tr) + "\n")
     print("\n".join(tr[-1:] + md[-9:]))
 
@@ -1368,13 +1443,20 @@ def main():
                     help="only write the workload's profiles/ summaries from the rocprofv3 runs "
                          "under --prof-dir")
     ap.add_argument("--prof-dir", default=".")
+    ap.add_argument("--summary-dir", default=os.path.join(ROOT, "profiles"),
+                    help="where --summarize writes its three files")
+    ap.add_argument("--reps", type=int, default=REPS,
+                    help="timed repetitions of the K steps (the median is reported)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 20 times (scales rocprof "
                          "FETCH_SIZE/WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     if args.summarize:
-        summarize_profiles(args.summarize, args.prof_dir)
+        summarize_profiles(args.summarize, args.prof_dir, args.summary_dir)
         return
+    if args.reps < 1:
+        ap.error("--reps must be at least 1")
+    REPS_SET[0] = args.reps
     if args.copy_calibration:
         import torch
         n = args.copy_calibration * (1 << 20) // 4
