@@ -450,7 +450,8 @@ def test_whole_row_kernel_streams_and_partial_chunks(case, rope):
     whose shorter window leaves chunks empty (their -inf partials in the
     merge), and one stream whose last chunk is partial.  Against the oracle
     (exact and mimic) and against the per-head kernel on identical caches:
-    identical cache bytes, outputs within 2e-4."""
+    identical cache bytes, outputs within 1e-3 (each kernel rounds the
+    softmax weights to f16 against its own running maxima)."""
     fills = ROWS_CASES[case]
     out_r, img_r, checks = _rows_case_run(fills, vkv.KERNEL_DECODE_ROWS, rope)
     out_h, img_h, _ = _rows_case_run(fills, vkv.KERNEL_DECODE_HEADS, rope)
