@@ -19,6 +19,10 @@ Other workloads (--workload), reported on the same contract:
   stream4096_f16  the decoder from an empty ring: steps 0..4095 (append at
                pos, attend pos+1 keys; no wrap), every step timed; tokens/s
                over the whole run, bytes summed over the growing windows.
+  layerwise_f16  the default workload in the decoder's own call shape: per
+               token 26 vkv_decoder_layer_step calls, one layer each (layer
+               l+1's Q depends on layer l's output), RoPE fused (theta 1e6),
+               then the ring commit; tokens/s and the mean time per layer.
   layer1_f16   one decoder layer, 1024 positions prefilled, then one step per
                token (append + attention over 1025 positions): a latency case.
   q8_0_batch8  the same decoder shape with q8_0 K/V (quantize-on-append,
@@ -70,6 +74,7 @@ threaded restatement of ggml's CPU flash-attention step, timed on a bounded
 sample on this host; decode workloads only).
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -94,6 +99,7 @@ WORKLOADS = {
     "longform_rope_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "stream4096_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "layer1_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
+    "layerwise_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "q8_0_batch8": dict(dtype=8, dtype_name="q8_0", streams=8,
                         pmc="decode_q8_0_8x26x8192_pmc.json", kern="k_decode_q8mfma"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
@@ -989,14 +995,17 @@ def timed_loop(step, steps, warmup, st, every=8, reps=None):
     return sorted(totals)[len(totals) // 2], step_ms, wall
 
 
-def gpu_decode(dtype, ns, steps, warmup, rope_theta=None):
+CACHE_KW = {}   # cache parameters from the command line (kernel selection for A/B runs)
+
+
+def gpu_decode(dtype, ns, steps, warmup, rope_theta=None, layerwise=False):
     import torch
     import vkv
 
     st = torch.cuda.current_stream()
     sp = st.cuda_stream
     cache = vkv.Cache(n_streams=ns, n_layers=LAYERS, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
-                      n_q_heads=QH, dtype=dtype)
+                      n_q_heads=QH, dtype=dtype, **CACHE_KW)
     rings = (vkv.Ring * ns)(*[vkv.new_ring(CAP) for _ in range(ns)])
     # fill every ring: positions [0, 8192) through the planned append path
     k0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
@@ -1024,7 +1033,30 @@ def gpu_decode(dtype, ns, steps, warmup, rope_theta=None):
     scale = 1.0 / (HD ** 0.5)
     pos = [CAP]
 
+    # the decoder's call shape: one plan per token, one C call per layer
+    # (arguments prepared outside the loop, so the host keeps ahead of the GPU)
+    layer_step = vkv.lib.vkv_decoder_layer_step
+    ptrs = [t.data_ptr() for t in (q, k, v, out)]
+    strides = [LAYERS * Q_DIM * 4, LAYERS * KV_DIM * 4, LAYERS * KV_DIM * 4, LAYERS * Q_DIM * 4]
+    lstr = [Q_DIM * 4, KV_DIM * 4, KV_DIM * 4, Q_DIM * 4]
+
+    def step_layers(i):
+        plan = vkv.decoder_plan(rings[0], pos[0], 1)
+        pref = ctypes.byref(plan)
+        b = [p + i * st_ for p, st_ in zip(ptrs, strides)]
+        for layer in range(LAYERS):
+            rc = layer_step(cache.handle, 0, pref, pos[0], layer, 1, b[0] + layer * lstr[0],
+                            b[1] + layer * lstr[1], b[2] + layer * lstr[2], b[3] + layer * lstr[3],
+                            QH, scale, rope_theta, sp)
+            if rc:
+                vkv.check(rc)
+        vkv.decoder_commit(rings[0], plan)
+        pos[0] += 1
+
     def step(i):
+        if layerwise:
+            step_layers(i)
+            return
         if rope_theta is None:
             cache.decoder_step(0, rings, [pos[0]] * ns, 0, LAYERS, q[i].data_ptr(),
                                k[i].data_ptr(), v[i].data_ptr(), out[i].data_ptr(), scale,
@@ -1447,6 +1479,12 @@ def main():
                     help="where --summarize writes its three files")
     ap.add_argument("--reps", type=int, default=REPS,
                     help="timed repetitions of the K steps (the median is reported)")
+    ap.add_argument("--kernel-flags", type=lambda x: int(x, 0), default=0,
+                    help="vkv_cache_params.kernel_flags of the decode workloads' cache "
+                         "(VKV_KERNEL_* bits; kernel selection for A/B runs)")
+    ap.add_argument("--decode-chunk", type=int, default=0)
+    ap.add_argument("--decode-waves", type=int, default=0)
+    ap.add_argument("--decode-stages", type=int, default=0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB 20 times (scales rocprof "
                          "FETCH_SIZE/WRITE_SIZE counters to bytes)")
@@ -1457,6 +1495,8 @@ def main():
     if args.reps < 1:
         ap.error("--reps must be at least 1")
     REPS_SET[0] = args.reps
+    CACHE_KW.update(kernel_flags=args.kernel_flags, decode_chunk=args.decode_chunk,
+                    decode_waves=args.decode_waves, decode_stages=args.decode_stages)
     if args.copy_calibration:
         import torch
         n = args.copy_calibration * (1 << 20) // 4
@@ -1608,8 +1648,10 @@ def main():
             " (ring append fused; one launch per chunk)"
     else:
         ns = wl["streams"]
-        rope = 1.0e6 if args.workload == "longform_rope_f16" else None
-        total_ms, step_ms, wall = gpu_decode(wl["dtype"], ns, args.steps, args.warmup, rope)
+        layerwise = args.workload == "layerwise_f16"
+        rope = 1.0e6 if args.workload in ("longform_rope_f16", "layerwise_f16") else None
+        total_ms, step_ms, wall = gpu_decode(wl["dtype"], ns, args.steps, args.warmup, rope,
+                                             layerwise)
         bytes_step = ns * decode_bytes_per_stream_token(CAP, wl["dtype"])
         units_per_step = ns
         res = {"metric": METRIC, "unit": "tokens/s"}
@@ -1618,7 +1660,13 @@ def main():
                               f"{'s' if ns > 1 else ''}, append + 1-query attention per layer",
                   "layers": LAYERS, "window": CAP, "kv_heads": KVH, "q_heads": QH,
                   "head_dim": HD, "streams": ns}
-        if wl["dtype"] == 1 and ns == 1:
+        if layerwise:
+            config["workload"] = ("decoder KV step in the decoder's call shape: 26 "
+                                  "vkv_decoder_layer_step calls per token (one layer each, RoPE "
+                                  "fused), 8192-slot ring full and wrapping, f16 KV, 32 q / 8 kv "
+                                  "heads x 128, 1 stream")
+            kernel = "26 x (k_decode + k_combine) (RoPE and append fused; 256-slot chunks, then the merge)"
+        elif wl["dtype"] == 1 and ns == 1:
             kernel = ("k_decode_rows + k_combine (append fused; a work group per (layer, 1024-slot "
                       "chunk) reading whole rows, then the merge of the 8 chunks)")
         else:

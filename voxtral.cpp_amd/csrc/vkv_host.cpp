@@ -259,6 +259,23 @@ void host_rope_table(float pos, float theta_scale, float2 *tab) {
     std::memcpy(tab, cached.tab, sizeof(cached.tab));
 }
 
+// The merge of a split decode's chunk partials (k_combine), launched after it.
+vkv_status merge_launch(const vkv_cache *c, const DecodeArgs &a, int32_t n_streams,
+                        hipStream_t st) {
+    if (a.n_chunks == 1) return VKV_STATUS_OK;
+    CombineArgs cb{};
+    cb.part_o = c->part_o;
+    cb.part_ml = c->part_ml;
+    cb.out = a.out;
+    cb.n_chunks = a.n_chunks;
+    cb.n_q_heads = a.n_q_heads;
+    cb.n_layers = a.n_layers;
+    cb.head_dim = c->p.head_dim;
+    hipError_t e = launch_combine(cb, n_streams, st);
+    if (e != hipSuccess) return hip_fail(e, "combine launch");
+    return VKV_STATUS_OK;
+}
+
 vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t layer0,
                      int32_t n_layers, const SegPair *segs, const float *q, float *out,
                      int32_t n_q_heads, float scale, const float *k_new, const float *v_new,
@@ -319,7 +336,7 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     // its grid holds between 3/4 of the CUs and the CUs, as the one-pass
     // k_decode; the cache's VKV_KERNEL_DECODE_HEADS / _ROWS flags override.
     {
-        const int32_t rows_chunk = 1024;
+        const int32_t rows_chunk = c->p.decode_chunk ? c->p.decode_chunk : 1024;
         const int32_t nc = std::max(1, (n_kv_max + rows_chunk - 1) / rows_chunk);
         const int64_t groups = (int64_t)n_streams * n_layers * nc;
         const bool shape_ok = c->p.dtype == VKV_DTYPE_F16 && G == 8 && n_q_heads == 32 &&
@@ -332,18 +349,7 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
             a.n_chunks = nc;
             hipError_t e = launch_decode_rows(k_new != nullptr, n_streams, a, st);
             if (e != hipSuccess) return hip_fail(e, "decode launch");
-            if (a.n_chunks == 1) return VKV_STATUS_OK;
-            CombineArgs cb{};
-            cb.part_o = c->part_o;
-            cb.part_ml = c->part_ml;
-            cb.out = out;
-            cb.n_chunks = a.n_chunks;
-            cb.n_q_heads = n_q_heads;
-            cb.n_layers = n_layers;
-            cb.head_dim = D;
-            e = launch_combine(cb, n_streams, st);
-            if (e != hipSuccess) return hip_fail(e, "combine launch");
-            return VKV_STATUS_OK;
+            return merge_launch(c, a, n_streams, st);
         }
     }
     // q8_0 by whole rows (k_decode_q8rows, with VKV_KERNEL_DECODE_ROWS):
@@ -370,18 +376,7 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
         a.n_chunks = nc;
         hipError_t e = launch_decode_q8rows(k_new != nullptr, n_streams, a, st);
         if (e != hipSuccess) return hip_fail(e, "decode launch");
-        if (a.n_chunks == 1) return VKV_STATUS_OK;
-        CombineArgs cb{};
-        cb.part_o = c->part_o;
-        cb.part_ml = c->part_ml;
-        cb.out = out;
-        cb.n_chunks = a.n_chunks;
-        cb.n_q_heads = n_q_heads;
-        cb.n_layers = n_layers;
-        cb.head_dim = D;
-        e = launch_combine(cb, n_streams, st);
-        if (e != hipSuccess) return hip_fail(e, "combine launch");
-        return VKV_STATUS_OK;
+        return merge_launch(c, a, n_streams, st);
     }
     // XCD-grouped order: q8_0 head segments (136 B) share cache lines with
     // their neighbours.  The cache's XCD flags override.
@@ -396,18 +391,7 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     hipError_t e = launch_decode(c->p.dtype, gqa, waves, stages, mfma, k_new != nullptr,
                                  n_streams, a, st);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
-    if (a.n_chunks == 1) return VKV_STATUS_OK;
-    CombineArgs cb{};
-    cb.part_o = c->part_o;
-    cb.part_ml = c->part_ml;
-    cb.out = out;
-    cb.n_chunks = a.n_chunks;
-    cb.n_q_heads = n_q_heads;
-    cb.n_layers = n_layers;
-    cb.head_dim = D;
-    e = launch_combine(cb, n_streams, st);
-    if (e != hipSuccess) return hip_fail(e, "combine launch");
-    return VKV_STATUS_OK;
+    return merge_launch(c, a, n_streams, st);
 }
 
 // Window attention of n_q queries; with k_new, the n_q new rows are first

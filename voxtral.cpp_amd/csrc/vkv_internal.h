@@ -52,7 +52,7 @@ struct DecodeArgs {
     int64_t q_sstride, q_lstride;
     float *part_o;         // [stream][layer][n_q_heads][n_chunks][head_dim]
     float *part_ml;        // [stream][layer][n_q_heads][n_chunks][2]
-    float *out;            // [stream][layer][n_q_heads][head_dim] (n_chunks == 1)
+    float *out;            // [stream][layer][n_q_heads][head_dim]
     int32_t n_chunks, chunk;
     int32_t xcd_swizzle;   // 1: XCD-grouped work-group order (8 kv heads, grid % 64 == 0)
     int32_t n_layers, n_kv_heads, n_q_heads;
@@ -73,7 +73,7 @@ struct DecodeArgs {
     // rope_host != 0 (one stream): the position's 64 (cos, sin) pairs of
     // ggml's angles, evaluated on the host, so no work group evaluates them
     int32_t rope_host;
-    float2 rope_tab[64];
+    alignas(16) float2 rope_tab[64];
 };
 
 struct CombineArgs {

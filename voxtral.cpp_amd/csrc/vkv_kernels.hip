@@ -59,6 +59,34 @@ __device__ __forceinline__ float quad_max(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Sum / max over lanes l and l ^ 16, and over lanes l and l ^ 32, with the
+// gfx950 row-swap permutes (VALU, no LDS round trip).  permlane16_swap
+// exchanges the odd 16-lane rows of its first operand with the even rows of
+// its second, permlane32_swap the upper half of the first with the lower
+// half of the second; with both operands the same value, the two results
+// hold the lane's own value and its partner's, which every lane combines in
+// the same order (v[lo] op v[hi]).
+__device__ __forceinline__ float xor16_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // Round half away from zero.  Contraction stays off: the quantizer rounds the
 // product x*id first, exactly like the CPU quantizer.
 __device__ __forceinline__ float round_half_away(float v) {
@@ -518,6 +546,32 @@ __device__ __forceinline__ void rope8_tab(float (&x)[8], int pair0, const float2
     }
 }
 
+// A lane's 4 (cos, sin) pairs [pair0, pair0 + 4) of the host-evaluated table
+// (rope_host): two 16-byte loads, straight into registers.
+struct RopePairs {
+    float2 cs[4];
+};
+__device__ __forceinline__ RopePairs rope_pairs_host(const DecodeArgs &a, int pair0) {
+    const float4 *t = reinterpret_cast<const float4 *>(a.rope_tab + pair0);
+    const float4 x = t[0], y = t[1];
+    return RopePairs{{make_float2(x.x, x.y), make_float2(x.z, x.w), make_float2(y.x, y.y),
+                      make_float2(y.z, y.w)}};
+}
+__device__ __forceinline__ RopePairs rope_pairs_lds(const float2 *tab, int pair0) {
+    return RopePairs{{tab[pair0], tab[pair0 + 1], tab[pair0 + 2], tab[pair0 + 3]}};
+}
+// rope8_tab's rotation with the pairs in registers
+__device__ __forceinline__ void rope8_pairs(float (&x)[8], const RopePairs &r) {
+#pragma clang fp contract(off)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float2 cs = r.cs[j];
+        const float x0 = x[2 * j], x1 = x[2 * j + 1];
+        x[2 * j] = x0 * cs.x - x1 * cs.y;
+        x[2 * j + 1] = x0 * cs.y + x1 * cs.x;
+    }
+}
+
 __global__ void __launch_bounds__(256) k_rope(float *x, int64_t n_outer, int64_t n_rows,
                                               int32_t row_len, int32_t head_dim, int64_t pos0,
                                               float theta_scale) {
@@ -571,7 +625,7 @@ __device__ __forceinline__ DecodeItem decode_item(const DecodeArgs &a) {
 template <class F>
 __device__ __forceinline__ void fused_append(const DecodeArgs &a, const SegPair &sp, int s,
                                              int layer, int64_t base, int e, int i_begin,
-                                             int i_end, bool leader, const float2 *rope_tab) {
+                                             int i_end, bool leader, const RopePairs &rp) {
     const int n_kv = sp.n0 + sp.n1;
     if (n_kv >= 1 && n_kv - 1 >= i_begin && n_kv - 1 < i_end && leader) {
         const int slot = slot_of(sp, n_kv - 1);
@@ -580,7 +634,7 @@ __device__ __forceinline__ void fused_append(const DecodeArgs &a, const SegPair 
         float xk[8], xv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) { xk[i] = kn[i]; xv[i] = vn[i]; }
-        if (a.rope) rope8_tab(xk, (e & 127) >> 1, rope_tab);
+        if (a.rope) rope8_pairs(xk, rp);   // pairs (e & 127) / 2 = 4c
         store_new<F>(a.k_w + base + (int64_t)slot * a.row_bytes, e, xk, true);
         store_new<F>(a.v_w + base + (int64_t)slot * a.row_bytes, e, xv, true);
     }
@@ -657,7 +711,9 @@ __device__ __forceinline__ void decode_merge(const DecodeArgs &a, const DecodeIt
 // of the GQA group share every K/V load.  With one chunk per (stream, layer,
 // kv head) the work group owns the whole window and writes the normalised
 // output itself; otherwise it writes a (max, sum, unnormalised output)
-// partial for k_combine.
+// partial for k_combine.  Q (and the host's RoPE pairs) are requested before
+// any K/V batch: the vector-memory counter retires loads in order, so waiting
+// for Q never waits for K/V.
 // ---------------------------------------------------------------------------
 template <class F, int GQA, bool FUSE, int W, int NS>
 __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
@@ -678,8 +734,6 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
     const uint32_t row_bytes24 = (uint32_t)a.row_bytes;
     const int i_begin = chunk * a.chunk;
     const int i_end = min(i_begin + a.chunk, n_kv);
-    // Software pipeline: the next batch's K/V loads are in flight while the
-    // current batch is reduced.
     auto load_batch = [&](int b, typename F::Frag (&kf)[4], typename F::Frag (&vf)[4])
                           __attribute__((always_inline)) {
 #pragma unroll
@@ -696,6 +750,22 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
     typename F::Frag kf[NS][4], vf[NS][4];
     constexpr int kStep = W * 16;   // slots covered by one batch of all waves
     int b0 = i_begin + wave * 16;
+
+    // Q first, then the host's RoPE pairs of this lane (pairs [4c, 4c+4):
+    // the same for its Q elements and its new-K elements)
+    float4 qraw[GQA][2];
+    {
+        const float *qp = a.q + (int64_t)s * a.q_sstride + (int64_t)layer * a.q_lstride +
+                          (int64_t)(g * GQA) * D + c * 8;
+#pragma unroll
+        for (int j = 0; j < GQA; ++j) {
+            qraw[j][0] = reinterpret_cast<const float4 *>(qp + j * D)[0];
+            qraw[j][1] = reinterpret_cast<const float4 *>(qp + j * D)[1];
+        }
+    }
+    RopePairs rp{};
+    if (a.rope && a.rope_host) rp = rope_pairs_host(a, 4 * c);
+
     // The first batches are requested before the prologue (RoPE table, Q,
     // fused append) whenever none of them can hold the step's new row, the
     // newest logical index n_kv-1; clamped indices then stay below it too.
@@ -705,23 +775,19 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
         for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
     }
     __shared__ float2 sm_rope[64];
-    if (a.rope) {
+    if (a.rope && !a.rope_host) {
         decode_rope_table(sm_rope, a, s);
         __syncthreads();
+        rp = rope_pairs_lds(sm_rope, 4 * c);
     }
 
     typename F::QFrag qf[GQA];
-    {
-        const float *qp = a.q + (int64_t)s * a.q_sstride + (int64_t)layer * a.q_lstride +
-                          (int64_t)(g * GQA) * D + c * 8;
 #pragma unroll
-        for (int j = 0; j < GQA; ++j) {
-            const float4 q0 = reinterpret_cast<const float4 *>(qp + j * D)[0];
-            const float4 q1 = reinterpret_cast<const float4 *>(qp + j * D)[1];
-            float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-            if (a.rope) rope8_tab(qv, 4 * c, sm_rope);
-            qf[j] = F::make_q(qv);
-        }
+    for (int j = 0; j < GQA; ++j) {
+        float qv[8] = {qraw[j][0].x, qraw[j][0].y, qraw[j][0].z, qraw[j][0].w,
+                       qraw[j][1].x, qraw[j][1].y, qraw[j][1].z, qraw[j][1].w};
+        if (a.rope) rope8_pairs(qv, rp);
+        qf[j] = F::make_q(qv);
     }
 
     static_assert(GQA == 4, "the score transposition maps 4 slots x 4 heads onto 16 lanes");
@@ -759,8 +825,8 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
         // batch max of head j: lanes {j, j+4, j+8, j+12} of the row, then groups
         float bm = fmaxf(sc, dpp<0x124>(sc));
         bm = fmaxf(bm, dpp<0x128>(bm));
-        bm = fmaxf(bm, __shfl_xor(bm, 16));
-        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        bm = xor16_max(bm);
+        bm = xor32_max(bm);
         // Lazy rescale: the reference max only moves when a head's batch max
         // exceeds it by more than 2^8, so p <= 256 and rescaling is rare.
         if (__any(bm > m + 8.0f)) {
@@ -789,11 +855,11 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
         __builtin_amdgcn_wave_barrier();
         pv_accumulate<F>(acc, vf, pw);
     };
+
     if (FUSE) {
-        fused_append<F>(a, sp, s, layer, base, e, i_begin, i_end, wave == 0 && grp == 0, sm_rope);
+        fused_append<F>(a, sp, s, layer, base, e, i_begin, i_end, wave == 0 && grp == 0, rp);
         __syncthreads();
     }
-
     // Software pipeline over NS register sets (no copies, so the wave never
     // waits on a batch it has just requested): while batch p is reduced, the
     // loads of the next NS-1 batches are in flight.  The loop body always
@@ -816,15 +882,12 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
     // over its row and the groups; acc over the groups.
     l += dpp<0x124>(l);
     l += dpp<0x128>(l);
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = xor16_sum(l);
+    l = xor32_sum(l);
 #pragma unroll
     for (int j = 0; j < GQA; ++j) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            acc[j][i] += __shfl_xor(acc[j][i], 16);
-            acc[j][i] += __shfl_xor(acc[j][i], 32);
-        }
+        for (int i = 0; i < 8; ++i) acc[j][i] = xor32_sum(xor16_sum(acc[j][i]));
     }
 
     decode_merge<W, GQA>(a, it, wave, lane, m, l, acc);
@@ -1280,7 +1343,7 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
     };
     if (FUSE) {
         fused_append<FmtQ8>(a, sp, s, layer, base, e, i_begin, i_end, wave == 0 && kg == 0,
-                            sm_rope);
+                            a.rope ? rope_pairs_lds(sm_rope, (e & 127) >> 1) : RopePairs{});
         __syncthreads();
     }
 
