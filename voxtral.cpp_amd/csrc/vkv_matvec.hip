@@ -96,73 +96,73 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
-__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+// Max over the 16 lanes of a DPP row (every lane of the row receives it).
+__device__ __forceinline__ uint32_t row_max_u(uint32_t v) {
     int x = (int)v;
     x = (int)max((uint32_t)x, (uint32_t)dppi<0xB1>(x));
     x = (int)max((uint32_t)x, (uint32_t)dppi<0x4E>(x));
     x = (int)max((uint32_t)x, (uint32_t)dppi<0x141>(x));
     x = (int)max((uint32_t)x, (uint32_t)dppi<0x140>(x));
-    return max(max((uint32_t)lane_i(x, 0), (uint32_t)lane_i(x, 16)),
-               max((uint32_t)lane_i(x, 32), (uint32_t)lane_i(x, 48)));
+    return (uint32_t)x;
 }
 
-__device__ __forceinline__ int wave_min_i(int x) {
-    x = min(x, dppi<0xB1>(x));
-    x = min(x, dppi<0x4E>(x));
-    x = min(x, dppi<0x141>(x));
-    x = min(x, dppi<0x140>(x));
-    return min(min(lane_i(x, 0), lane_i(x, 16)), min(lane_i(x, 32), lane_i(x, 48)));
-}
-
-// One Q8_K block held by a wave, lane l with elements 4l..4l+3: the codes
-// packed 4 per lane, the sums of 16 (lanes 4k..4k+3 hold the same) and of 32
-// codes (lanes 8k..8k+7), and d.  ggml quantize_row_q8_K_ref: iscale = -127 /
-// (the first element of largest |h|), code = min(127, rint(iscale * h)),
-// d = 1 / iscale; an all-zero block gives zero codes and d = 0.
-struct QBlock {
-    uint32_t packed;
+// One Q8_K block held by a 16-lane row, lane l with elements 16l..16l+15:
+// the codes packed 4 per dword, the sum of the lane's 16 codes, of 32 codes
+// (lanes 2k, 2k+1 hold the same) and d.  The same arithmetic as q8k_block
+// (ggml quantize_row_q8_K_ref); the first element of largest |h| is found as
+// the row maximum of |h|, then the row maximum of a key that orders its
+// holders by smallest index and carries the element's sign.
+struct QBlock16 {
+    uint32_t packed[4];
     int s16, s32;
     float d;
 };
-
-__device__ __forceinline__ QBlock q8k_block(const float (&e)[4], int lane) {
+__device__ __forceinline__ QBlock16 q8k_block16(const float (&e)[16], int l) {
 #pragma clang fp contract(off)
-    // first element of largest magnitude (|h| > running max, in order)
     float am = 0.0f;
-    int ai = 0x7fffffff;
+    int ai = 0;
+    uint32_t neg = 0;
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < 16; ++k)
         if (fabsf(e[k]) > am) {
             am = fabsf(e[k]);
-            ai = 4 * lane + k;
+            ai = k;
+            neg = __builtin_bit_cast(uint32_t, e[k]) >> 31;
         }
-    const uint32_t wm = wave_max_u(__builtin_bit_cast(uint32_t, am));
-    const int wi = wave_min_i((__builtin_bit_cast(uint32_t, am) == wm && wm != 0u) ? ai : 0x7fffffff);
-    int q[4] = {0, 0, 0, 0};
-    QBlock r;
+    const uint32_t amb = __builtin_bit_cast(uint32_t, am);
+    const uint32_t mxa = row_max_u(amb);
+    const uint32_t key = (amb == mxa && mxa != 0u) ? ((uint32_t)(255 - (16 * l + ai)) << 1) | neg : 0u;
+    const uint32_t kmax = row_max_u(key);
+    int q[16];
+    QBlock16 r;
     r.d = 0.0f;
-    if (wm != 0u) {
-        const int k = wi & 3;
-        const float mine = k == 0 ? e[0] : k == 1 ? e[1] : k == 2 ? e[2] : e[3];
-        const float mx = lane_f(mine, wi >> 2);
+    if (mxa != 0u) {
+        const float mx = __builtin_bit_cast(float, mxa | (kmax & 1u) << 31);
         const float iscale = -127.0f / mx;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) q[j] = min(127, (int)__builtin_rintf(iscale * e[j]));
+        for (int k = 0; k < 16; ++k) q[k] = min(127, (int)__builtin_rintf(iscale * e[k]));
         r.d = 1.0f / iscale;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) q[k] = 0;
     }
-    r.packed = (uint32_t)(q[0] & 255) | (uint32_t)(q[1] & 255) << 8 | (uint32_t)(q[2] & 255) << 16 |
-               (uint32_t)(q[3] & 255) << 24;
-    int s = q[0] + q[1] + q[2] + q[3];
-    s += dppi<0xB1>(s);
-    s += dppi<0x4E>(s);               // sum of 16 (lanes 4k..4k+3)
-    r.s16 = s;
-    r.s32 = s + dppi<0x141>(s);
+    int sum = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        r.packed[w] = (uint32_t)(q[4 * w] & 255) | (uint32_t)(q[4 * w + 1] & 255) << 8 |
+                      (uint32_t)(q[4 * w + 2] & 255) << 16 | (uint32_t)(q[4 * w + 3] & 255) << 24;
+        sum += (q[4 * w] + q[4 * w + 1]) + (q[4 * w + 2] + q[4 * w + 3]);
+    }
+    r.s16 = sum;
+    r.s32 = sum + dppi<0xB1>(sum);
     return r;
 }
 
 // Q8_K quantization of rms_norm(x) * norm_w (* (1 + ada)), or of x itself
-// (norm_w == nullptr).  Wave w handles blocks w, w + 4, ...; each lane 4
-// consecutive elements of a block.  Rounding follows the CPU path step by
+// (norm_w == nullptr).  In round k a wave holds 4 blocks, one per 16-lane
+// row: lane (row r, l) has elements [16 l, 16 l + 16) of block 16 k + 4 w +
+// r, so every reduction over a block stays inside a DPP row and the wave's
+// blocks are quantized side by side.  Rounding follows the CPU path step by
 // step: the squares are f32 products summed in double, mean = f32(sum / n),
 // scale = 1 / sqrtf(mean + eps), h = (x * scale) * w, then h + h * ada;
 // iscale = -127 / (first element of largest |h|), code = min(127,
@@ -170,8 +170,8 @@ __device__ __forceinline__ QBlock q8k_block(const float (&e)[4], int lane) {
 //
 // Split in two so that a caller can issue its own loads between them: the
 // input loads of act_load retire first (vmcnt counts in issue order), and
-// act_finish then waits for them alone.  NBW = most blocks per wave; with
-// NORM_EARLY the norm weights are loaded up front too.
+// act_finish then waits for them alone.  NBW = 4 x rounds (float4 per lane);
+// with NORM_EARLY the norm weights are loaded up front too.
 template <int NBW, bool NORM_EARLY>
 struct ActRegs {
     float4 x[NBW];
@@ -187,8 +187,9 @@ __device__ __forceinline__ void act_load(ActRegs<NBW, NE> &r, const float *__res
     const float *wp = nw ? nw : x, *ap = ada ? ada : x;
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
-        const int b = wave + 4 * i < nb ? wave + 4 * i : 0;
-        const int e0 = 256 * b + 4 * lane;
+        const int bb = 16 * (i >> 2) + 4 * wave + (lane >> 4);
+        const int b = bb < nb ? bb : 0;   // rows past the last block read block 0, unused
+        const int e0 = 256 * b + 16 * (lane & 15) + 4 * (i & 3);
         r.x[i] = *reinterpret_cast<const float4 *>(x + e0);
         if (NE) {
             r.w[i] = *reinterpret_cast<const float4 *>(wp + e0);
@@ -205,12 +206,13 @@ __device__ __forceinline__ void act_finish(const ActRegs<NBW, NE> &r, int n,
                                            const float *__restrict__ nbias = nullptr) {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nb = n >> 8;
+    const int l = lane & 15;
     float scale = 1.0f;
     if (nw) {
         double s = 0.0;
 #pragma unroll
         for (int i = 0; i < NBW; ++i)
-            if (wave + 4 * i < nb) {
+            if (16 * (i >> 2) + 4 * wave + (lane >> 4) < nb) {
                 const float4 v = r.x[i];
                 s += (double)(v.x * v.x);
                 s += (double)(v.y * v.y);
@@ -225,53 +227,67 @@ __device__ __forceinline__ void act_finish(const ActRegs<NBW, NE> &r, int n,
         scale = 1.0f / sqrtf(mean + eps);
     }
 #pragma unroll
-    for (int i = 0; i < NBW; ++i) {
-        const int b = wave + 4 * i;
-        if (b >= nb) break;
-        const int e0 = 256 * b + 4 * lane;
-        float e[4] = {r.x[i].x, r.x[i].y, r.x[i].z, r.x[i].w};
+    for (int k = 0; k < NBW / 4; ++k) {
+        if (16 * k + 4 * wave >= nb) break;   // no block of this wave in this round
+        const int bb = 16 * k + 4 * wave + (lane >> 4);
+        const bool valid = bb < nb;           // rows past the last block compute, store nothing
+        const int b = valid ? bb : 0;
+        float e[16];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 v = r.x[4 * k + j];
+            e[4 * j] = v.x;
+            e[4 * j + 1] = v.y;
+            e[4 * j + 2] = v.z;
+            e[4 * j + 3] = v.w;
+        }
         if (nw) {
-            const float4 w4 = NE ? r.w[i] : *reinterpret_cast<const float4 *>(nw + e0);
-            const float w[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                e[k] = e[k] * scale;
-                e[k] = e[k] * w[k];
-            }
-            if (nbias) {
-                // + the norm's bias (the encoder's norms, src/voxtral.cpp:1855-1861)
-                const float4 b4 = *reinterpret_cast<const float4 *>(nbias + e0);
-                e[0] = e[0] + b4.x;
-                e[1] = e[1] + b4.y;
-                e[2] = e[2] + b4.z;
-                e[3] = e[3] + b4.w;
-            }
-            if (ada) {
-                const float4 a4 = NE ? r.a[i] : *reinterpret_cast<const float4 *>(ada + e0);
-                const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+            for (int j = 0; j < 4; ++j) {
+                const int e0 = 256 * b + 16 * l + 4 * j;
+                const float4 w4 = NE ? r.w[4 * k + j] : *reinterpret_cast<const float4 *>(nw + e0);
+                const float w[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const float t = e[k] * av[k];
-                    e[k] = e[k] + t;
+                for (int t = 0; t < 4; ++t) {
+                    e[4 * j + t] = e[4 * j + t] * scale;
+                    e[4 * j + t] = e[4 * j + t] * w[t];
+                }
+                if (nbias) {
+                    // + the norm's bias (the encoder's norms, src/voxtral.cpp:1855-1861)
+                    const float4 b4 = *reinterpret_cast<const float4 *>(nbias + e0);
+                    e[4 * j] = e[4 * j] + b4.x;
+                    e[4 * j + 1] = e[4 * j + 1] + b4.y;
+                    e[4 * j + 2] = e[4 * j + 2] + b4.z;
+                    e[4 * j + 3] = e[4 * j + 3] + b4.w;
+                }
+                if (ada) {
+                    const float4 a4 =
+                        NE ? r.a[4 * k + j] : *reinterpret_cast<const float4 *>(ada + e0);
+                    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const float tt = e[4 * j + t] * av[t];
+                        e[4 * j + t] = e[4 * j + t] + tt;
+                    }
                 }
             }
         }
-        const QBlock qb = q8k_block(e, lane);
-        const uint32_t packed = qb.packed;
-        const int s = qb.s16, s32 = qb.s32;
-        const float d = qb.d;
-        const int k16 = lane >> 2;        // 16-group 8n + 2g + h
+        const QBlock16 qb = q8k_block16(e, l);
+        if (!valid) continue;
         if (gout) {
             uint8_t *blk = gout + (size_t)b * 292;
-            *reinterpret_cast<uint32_t *>(blk + 4 + 4 * lane) = packed;
-            if ((lane & 3) == 0) *reinterpret_cast<int16_t *>(blk + 260 + 2 * k16) = (int16_t)s;
-            if (lane == 0) *reinterpret_cast<float *>(blk) = d;
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                *reinterpret_cast<uint32_t *>(blk + 4 + 16 * l + 4 * w) = qb.packed[w];
+            *reinterpret_cast<int16_t *>(blk + 260 + 2 * l) = (int16_t)qb.s16;
+            if (l == 0) *reinterpret_cast<float *>(blk) = qb.d;
         } else {
-            *reinterpret_cast<uint32_t *>(&sm.xq[e0]) = packed;
-            if ((lane & 3) == 0)
-                sm.bs16[16 * b + 8 * (k16 >> 3) + 4 * (k16 & 1) + ((k16 >> 1) & 3)] = s;
-            if ((lane & 7) == 0) sm.bs32[8 * b + (lane >> 3)] = s32;
-            if (lane == 0) sm.dx[b] = d;
+            *reinterpret_cast<u32x4_t *>(&sm.xq[256 * b + 16 * l]) =
+                u32x4_t{qb.packed[0], qb.packed[1], qb.packed[2], qb.packed[3]};
+            // 16-group l of the block, in the Q6_K order [b][n][h][g]
+            sm.bs16[16 * b + 8 * (l >> 3) + 4 * (l & 1) + ((l >> 1) & 3)] = qb.s16;
+            if ((l & 1) == 0) sm.bs32[8 * b + (l >> 1)] = qb.s32;
+            if (l == 0) sm.dx[b] = qb.d;
         }
     }
     __syncthreads();
@@ -492,7 +508,7 @@ __device__ __forceinline__ void argmax_publish(const MvArgs &a, unsigned long lo
 // Q4 (the work group's weight dtype) is a template parameter so that every
 // load writes its final registers (a load feeding a merge of two paths would
 // be copied, and the copy waits for the load).
-template <int S, int D0, bool Q4, bool AMAX>
+template <int S, int D0, bool Q4, bool AMAX, bool NE>
 __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, const MvOut &ob,
                                             int row0, int nrow, ActSmem &sm) {
     const int lane = threadIdx.x & 63;
@@ -507,7 +523,7 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
 
     constexpr int D = Q4 ? D0 : 2;            // units in flight (Q6_K fragments are larger)
     constexpr int NBW = S == 1 ? 4 : 4 * S;   // n_in <= 4096 / 12288
-    ActRegs<NBW, false> ar;
+    ActRegs<NBW, NE> ar;
     act_load(ar, a.x, a.n_in, a.norm_w, a.ada);
     using Frag = std::conditional_t<Q4, FragQ4, FragQ6>;
     Frag f[D];
@@ -575,8 +591,15 @@ __global__ void __launch_bounds__(256) k_matvec(MvArgs a) {
     const MvOut ob = a.swiglu ? a.out[1] : o0;
     const int row0 = ((int)blockIdx.x - o0.wg0) * a.rows_per_wg + wave * (a.rows_per_wg >> 2);
     const int nrow = max(0, min(a.rows_per_wg >> 2, o0.n_rows - row0));
-    if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D, true, AMAX>(a, o0, ob, row0, nrow, sm);
-    else matvec_body<S, D, false, AMAX>(a, o0, ob, row0, nrow, sm);
+    // With a norm (S == 1: the inputs of up to 4096), its weights (and the ada
+    // row) are requested together with x, so the norm costs one round trip.
+    if (S == 1 && a.norm_w) {
+        if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D, true, AMAX, true>(a, o0, ob, row0, nrow, sm);
+        else matvec_body<S, D, false, AMAX, true>(a, o0, ob, row0, nrow, sm);
+    } else {
+        if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D, true, AMAX, false>(a, o0, ob, row0, nrow, sm);
+        else matvec_body<S, D, false, AMAX, false>(a, o0, ob, row0, nrow, sm);
+    }
 }
 
 __global__ void __launch_bounds__(256) k_q8k_quant(const float *x, int n, const float *nw,
