@@ -164,6 +164,16 @@ struct MmArgs {
     const int8_t *xq;      // Q8_K image: codes [n_cols][n_in]
     const float *xd;       // block scales [n_cols][n_in / 256]
     const int16_t *xbs;    // 32-element sums [n_cols][n_in / 32]
+    // Fused input (x != nullptr): each work group quantizes its own input
+    // rows into LDS (k_q8k_rows' arithmetic) instead of reading the image:
+    // input row p at x + ((x_row0 + p) % x_ring) * x_stride (x_ring > 0) or
+    // x + p * x_stride; rms_norm(x) * norm_w (+ norm_b) (* (1 + ada)) when
+    // norm_w is given.
+    const float *x;
+    int64_t x_stride;
+    int32_t x_ring, x_row0;
+    const float *norm_w, *norm_b, *ada;
+    float eps;
     int32_t n_in, n_cols, n_outs, swiglu;
     int32_t gelu;          // y = gelu_erf(W h + bias) (no residual)
     // Input row p's output (and residual) row: (y_row0 + p) % y_ring when
@@ -184,6 +194,11 @@ hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_r
                            int n, const float *norm_w, const float *norm_b, const float *ada,
                            float eps, int8_t *codes, float *xd, int16_t *bs16, hipStream_t st);
 hipError_t launch_gemm_kq(MmArgs a, int n_col_tiles, hipStream_t st);
+// input rows one work group of launch_gemm_kq covers for this call
+int gemm_cols_per_wg(const MmArgs &a, int n_col_tiles);
+// whether launch_gemm_kq may quantize this call's input inside its work
+// groups (MmArgs::x): few (row, block) tasks per work group, LDS to spare
+bool gemm_fused_ok(const MmArgs &a, int n_col_tiles);
 hipError_t launch_q8k_quant(const float *x, int n, const float *norm_w, const float *ada, float eps,
                             uint8_t *out, hipStream_t st);
 hipError_t launch_kq_dequant(int dtype, const uint8_t *src, int64_t n, const float *add, float *y,

@@ -22,6 +22,7 @@
 //   k_argmax     -- ggml_argmax of the logits (src/voxtral.cpp:2970).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <type_traits>
@@ -927,12 +928,23 @@ __device__ __forceinline__ auto gemm_load_w(__amdgpu_buffer_rsrc_t rs, uint32_t 
     }
 }
 
+// The input image: a.xq / a.xd / a.xbs in global memory, or (fused input)
+// the work group's own columns in LDS, column col - col0 of the same layout.
+struct XImage {
+    const int8_t *xq;
+    const float *xd;
+    const int16_t *xbs;
+    int col0;
+};
+
 template <bool Q4>
-__device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, int col, int b, int kg) {
+__device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, const XImage &im, int col, int b,
+                                              int kg) {
     GFragX x;
     const int K = a.n_in;
+    col -= im.col0;
     // the image's lane order: 16 bytes per lane group at 64 q + 16 kg
-    const int4 *xc = reinterpret_cast<const int4 *>(a.xq + (int64_t)col * K + 256 * b + 16 * kg);
+    const int4 *xc = reinterpret_cast<const int4 *>(im.xq + (int64_t)col * K + 256 * b + 16 * kg);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int4 v = xc[4 * q];
@@ -941,7 +953,7 @@ __device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, int col, int b, i
     }
     if constexpr (Q4) {
         // the block's eight 16-bit sums in one 16-byte load
-        const int4 v = *reinterpret_cast<const int4 *>(a.xbs + (int64_t)col * (K / 32) + 8 * b);
+        const int4 v = *reinterpret_cast<const int4 *>(im.xbs + (int64_t)col * (K / 32) + 8 * b);
         const int w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -952,8 +964,114 @@ __device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, int col, int b, i
 #pragma unroll
         for (int j = 0; j < 8; ++j) x.bsx[j] = 0;
     }
-    x.dx = a.xd[(int64_t)col * (K >> 8) + b];
+    x.dx = im.xd[(int64_t)col * (K >> 8) + b];
     return x;
+}
+
+// Fused input: the Q8_K image of input rows [col0, col0 + ncol) in LDS, in
+// the products' layout (codes of row c at c n_in, lane order within each
+// 256-block; block scales; 32-element sums as int16), by the same arithmetic
+// as k_q8k_rows (ggml's rms_norm then quantize_row_q8_K_ref): task (row c,
+// block b) is one 16-lane DPP row, lane l holding elements [16 l, 16 l +
+// 16) of the block, and a group takes at most kFqRounds tasks, all loaded up
+// front (the host routes larger calls to k_q8k_rows).  With a norm, each
+// task's sum of squares (f32 products summed in double, the row's 16 lanes
+// by DPP) goes to LDS and a row's scale is taken from its block sums in block
+// order, so a row's codes do not depend on the work group or the number of
+// rows in the call.
+constexpr int kFqRounds = 2;
+
+template <int W>
+__device__ void gemm_quant_cols(const MmArgs &a, int col0, int ncol, int8_t *cq, float *cd,
+                                int16_t *cs, double *ss) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l = lane & 15;
+    const int K = a.n_in, nb = K >> 8, tasks = ncol * nb;
+    const int gi = 4 * wave + (lane >> 4);   // this 16-lane group
+    float e[kFqRounds][16];
+#pragma unroll
+    for (int r = 0; r < kFqRounds; ++r) {
+        const int t = min(gi + 4 * W * r, tasks - 1);   // past the last task: reload it, unused
+        const int c = t / nb, b = t % nb;
+        const int p = col0 + c;
+        const int src = a.x_ring > 0 ? (a.x_row0 + p) % a.x_ring : p;
+        const float4 *xp =
+            reinterpret_cast<const float4 *>(a.x + (int64_t)src * a.x_stride + 256 * b + 16 * l);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 v = xp[j];
+            e[r][4 * j] = v.x;
+            e[r][4 * j + 1] = v.y;
+            e[r][4 * j + 2] = v.z;
+            e[r][4 * j + 3] = v.w;
+        }
+    }
+    if (a.norm_w) {
+#pragma unroll
+        for (int r = 0; r < kFqRounds; ++r) {
+            const int t = gi + 4 * W * r;
+            double s = 0.0;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) s += (double)(e[r][k] * e[r][k]);
+            s += dppd<0xB1>(s);
+            s += dppd<0x4E>(s);
+            s += dppd<0x141>(s);
+            s += dppd<0x140>(s);
+            if (t < tasks && l == 0) ss[t] = s;
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < kFqRounds; ++r) {
+        const int t = gi + 4 * W * r;
+        if (t >= tasks) break;
+        const int c = t / nb, b = t % nb;
+        if (a.norm_w) {
+            double tot = 0.0;
+            for (int k = 0; k < nb; ++k) tot += ss[c * nb + k];
+            const float mean = (float)(tot / (double)K);
+            const float scale = 1.0f / sqrtf(mean + a.eps);
+            const int e0 = 256 * b + 16 * l;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 w4 = *reinterpret_cast<const float4 *>(a.norm_w + e0 + 4 * j);
+                const float w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    e[r][4 * j + u] = e[r][4 * j + u] * scale;
+                    e[r][4 * j + u] = e[r][4 * j + u] * w[u];
+                }
+                if (a.norm_b) {
+                    const float4 b4 = *reinterpret_cast<const float4 *>(a.norm_b + e0 + 4 * j);
+                    e[r][4 * j] = e[r][4 * j] + b4.x;
+                    e[r][4 * j + 1] = e[r][4 * j + 1] + b4.y;
+                    e[r][4 * j + 2] = e[r][4 * j + 2] + b4.z;
+                    e[r][4 * j + 3] = e[r][4 * j + 3] + b4.w;
+                }
+                if (a.ada) {
+                    const float4 a4 = *reinterpret_cast<const float4 *>(a.ada + e0 + 4 * j);
+                    const float av[4] = {a4.x, a4.y, a4.z, a4.w};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const float tt = e[r][4 * j + u] * av[u];
+                        e[r][4 * j + u] = e[r][4 * j + u] + tt;
+                    }
+                }
+            }
+        }
+        const QBlock16 q = q8k_block16(e[r], l);
+        // codes 32 j + 8 kg + e at byte 64 q + 16 kg + 8 (j & 1) + e of the
+        // block (q = j / 2): lane l holds j = l / 2, kg = 2 (l & 1) + h
+        int8_t *blk = cq + (int64_t)c * K + 256 * b;
+        const int jj = (l >> 1) & 1, qq = l >> 2;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            *reinterpret_cast<uint2 *>(blk + 64 * qq + 16 * (2 * (l & 1) + h) + 8 * jj) =
+                make_uint2(q.packed[2 * h], q.packed[2 * h + 1]);
+        if ((l & 1) == 0) cs[(int64_t)c * (K / 32) + 8 * b + (l >> 1)] = (int16_t)q.s32;
+        if (l == 0) cd[(int64_t)c * nb + b] = q.d;
+    }
+    __syncthreads();
 }
 
 // The weight codes through an empty asm: what is derived from them (nibbles,
@@ -1079,7 +1197,8 @@ __device__ __forceinline__ float rope_elem(float self, float partner, bool odd, 
 // input rows.
 template <bool Q4, int W, int CT>
 __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, const MmOut &o1,
-                                          uint32_t (*hdr)[16][6], float (*red)[W][16][17]) {
+                                          uint32_t (*hdr)[16][6], float (*red)[W][16][17],
+                                          const XImage &im) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kg = lane >> 4, rr = lane & 15;
     const bool swiglu = a.swiglu != 0;
     const int nb = a.n_in >> 8;
@@ -1110,7 +1229,8 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
 #pragma unroll
         for (int c = 0; c < CT; ++c) {
             if (c < n_ct) {
-                const GFragX x = gemm_load_x<Q4>(a, min(col0 + 16 * c + rr, a.n_cols - 1), b, kg);
+                const GFragX x =
+                    gemm_load_x<Q4>(a, im, min(col0 + 16 * c + rr, a.n_cols - 1), b, kg);
                 // with several column tiles the codes pass through an empty
                 // asm before each use, so what is derived from them (nibbles,
                 // recentred codes, scales) is derived again instead of held
@@ -1166,7 +1286,15 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
 // (the body is in the kernel itself: a reference to the by-value kernel
 // argument passed through one more inlined function made the compiler copy
 // the argument to scratch memory)
-template <int W, int CT>
+// Fused input image in dynamic LDS: codes, block scales, 32-element sums,
+// per-task sums of squares (the norm's first pass).
+__host__ __device__ constexpr size_t al16(size_t b) { return (b + 15) & ~(size_t)15; }
+__host__ __device__ constexpr size_t fused_lds_bytes(int cols, int n_in) {
+    return al16((size_t)cols * n_in) + al16((size_t)cols * (n_in / 256) * 4) +
+           al16((size_t)cols * (n_in / 32) * 2) + al16((size_t)cols * (n_in / 256) * 8);
+}
+
+template <int W, int CT, bool FQ>
 __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))) k_gemm_kq(MmArgs a) {
     __shared__ uint32_t hdr[W][16][6];
     __shared__ float red[CT][W][16][17];
@@ -1176,9 +1304,36 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         if (k < a.n_outs && (int)blockIdx.x >= a.out[k].tile0) seg = k;
     const MmOut o0 = mm_out_at(a, seg);
     const MmOut o1 = a.swiglu ? a.out[1] : o0;
+    XImage im{a.xq, a.xd, a.xbs, 0};
+    if constexpr (FQ) {
+        extern __shared__ __align__(16) uint8_t fq_lds[];
+        const int col0 = (int)blockIdx.y * 16 * CT;
+        const int ncol = min(16 * CT, a.n_cols - col0);
+        const int K = a.n_in, nb = K >> 8, cols = 16 * CT;
+        int8_t *cq = reinterpret_cast<int8_t *>(fq_lds);
+        float *cd = reinterpret_cast<float *>(fq_lds + al16((size_t)cols * K));
+        int16_t *cs = reinterpret_cast<int16_t *>(reinterpret_cast<uint8_t *>(cd) +
+                                                  al16((size_t)cols * nb * 4));
+        double *ss = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(cs) +
+                                                al16((size_t)cols * (K / 32) * 2));
+        gemm_quant_cols<W>(a, col0, ncol, cq, cd, cs, ss);
+        im = XImage{cq, cd, cs, col0};
+        if (blockIdx.x == 0 && a.xq) {
+            // the first row tile's work groups leave their rows' image in the
+            // caller's workspace too (the separate quantization's output),
+            // read by nothing in the call
+            const int4 *src = reinterpret_cast<const int4 *>(cq);
+            int4 *dst = reinterpret_cast<int4 *>(const_cast<int8_t *>(a.xq) + (int64_t)col0 * K);
+            for (int i = threadIdx.x; i < ncol * K / 16; i += 64 * W) dst[i] = src[i];
+            float *xd = const_cast<float *>(a.xd) + (int64_t)col0 * nb;
+            for (int i = threadIdx.x; i < ncol * nb; i += 64 * W) xd[i] = cd[i];
+            int16_t *xb = const_cast<int16_t *>(a.xbs) + (int64_t)col0 * (K / 32);
+            for (int i = threadIdx.x; i < ncol * (K / 32); i += 64 * W) xb[i] = cs[i];
+        }
+    }
     // one weight dtype per work group (both SwiGLU matrices share it)
-    if (o0.dtype == VKV_DTYPE_Q4_K) gemm_body<true, W, CT>(a, o0, o1, hdr, red);
-    else gemm_body<false, W, CT>(a, o0, o1, hdr, red);
+    if (o0.dtype == VKV_DTYPE_Q4_K) gemm_body<true, W, CT>(a, o0, o1, hdr, red, im);
+    else gemm_body<false, W, CT>(a, o0, o1, hdr, red, im);
 }
 
 }  // namespace
@@ -1248,13 +1403,49 @@ hipError_t launch_gemm_kq(MmArgs a, int n_col_tiles, hipStream_t st) {
     // the call has fewer than 128 row tiles; else 8 waves with two column
     // tiles (32 input rows) per work group at most: a third set of
     // accumulators spills at four waves per SIMD, and measured slower.
-    if (tiles < 128)
-        k_gemm_kq<16, 1><<<dim3((unsigned)tiles, (unsigned)n_col_tiles), 1024, 0, st>>>(a);
-    else if (n_col_tiles == 1)
-        k_gemm_kq<8, 1><<<dim3((unsigned)tiles, 1u), 512, 0, st>>>(a);
-    else
-        k_gemm_kq<8, 2><<<dim3((unsigned)tiles, (unsigned)((n_col_tiles + 1) / 2)), 512, 0, st>>>(a);
+    // A fused-input call (a.x) quantizes each work group's input rows into
+    // dynamic LDS (the caller checked gemm_fused_lds).
+    const bool fq = a.x != nullptr;
+    const int cols = gemm_cols_per_wg(a, n_col_tiles);
+    const size_t lds = fq ? fused_lds_bytes(cols, a.n_in) : 0;
+    if (tiles < 128) {
+        const dim3 g((unsigned)tiles, (unsigned)n_col_tiles);
+        if (fq) k_gemm_kq<16, 1, true><<<g, 1024, lds, st>>>(a);
+        else k_gemm_kq<16, 1, false><<<g, 1024, 0, st>>>(a);
+    } else if (n_col_tiles == 1) {
+        const dim3 g((unsigned)tiles, 1u);
+        if (fq) k_gemm_kq<8, 1, true><<<g, 512, lds, st>>>(a);
+        else k_gemm_kq<8, 1, false><<<g, 512, 0, st>>>(a);
+    } else {
+        const dim3 g((unsigned)tiles, (unsigned)((n_col_tiles + 1) / 2));
+        if (fq) k_gemm_kq<8, 2, true><<<g, 512, lds, st>>>(a);
+        else k_gemm_kq<8, 2, false><<<g, 512, 0, st>>>(a);
+    }
     return hipGetLastError();
+}
+
+int gemm_cols_per_wg(const MmArgs &a, int n_col_tiles) {
+    int tiles = 0;
+    for (int k = 0; k < a.n_outs; ++k)
+        if (!(a.swiglu && k == 1)) tiles += (a.out[k].n_rows + 15) / 16;
+    return (tiles < 128 || n_col_tiles == 1) ? 16 : 32;
+}
+
+// Whether the call's input image is quantized inside its work groups: every
+// 16-lane group then has at most kFqRounds (row, block) tasks (the realtime
+// encoder's 4-frame chunks, single adapter groups), and the image fits in LDS
+// beside the product's own.  Measured on MI355X: 16-frame encoder chunks
+// and 38-row prompts, with 3 to 12 tasks per group, run slower fused than
+// with the separate k_q8k_rows launch (2.68 vs 2.23 ms, 6.65 vs 3.40 ms).
+bool gemm_fused_ok(const MmArgs &a, int n_col_tiles) {
+    int tiles = 0;
+    for (int k = 0; k < a.n_outs; ++k)
+        if (!(a.swiglu && k == 1)) tiles += (a.out[k].n_rows + 15) / 16;
+    const int waves = tiles < 128 ? 16 : 8;
+    const int cols = gemm_cols_per_wg(a, n_col_tiles);
+    const int rows = std::min(cols, a.n_cols);
+    return rows * (a.n_in / 256) <= kFqRounds * 4 * waves &&
+           fused_lds_bytes(cols, a.n_in) <= 128 * 1024;
 }
 
 hipError_t launch_rms_norm_rows(const float *x, int n_rows, int n, const float *w, const float *b,
