@@ -148,3 +148,43 @@ def test_matches_the_single_row_kernel():
                ws_ptr, ws_b, hip_stream=stream_ptr())
     _, mag = rows_ref(vkv.Q4_K, w, n_rows, n_in, [x])
     check(host(y2), host(y1), 2 * mag[0])
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_fused_and_separate_input_images_agree(norm):
+    """A call with few input rows quantizes them inside the products' work
+    groups (at most two 16-lane tasks per group); a call with many rows takes
+    the separate quantization launch.  The same rows must get the same Q8_K
+    image bit for bit, and the same outputs, whatever the call's size: the
+    encoder's outputs must not depend on how a stream is cut into chunks.
+    Rows span a dynamic range of e^+-6 (the norm's double sums of f32
+    squares), the Q/K/V shape of the encoder (three matrices over 1280)."""
+    rng = np.random.default_rng(4242 + norm)
+    n_in, P_big, P_small = 1280, 64, 4
+    mats = [(vkv.Q4_K, 1280), (vkv.Q4_K, 1280), (vkv.Q6_K, 1280)]
+    ws = [to_dev(random_matrix(rng, dt, n, n_in, 0.05)) for dt, n in mats]
+    x = (rng.standard_normal((P_big, n_in)) *
+         np.exp(rng.uniform(-6, 6, (P_big, 1)))).astype(np.float32)
+    nw = to_dev(rng.uniform(0.5, 1.5, n_in).astype(np.float32)) if norm else None
+    nb = to_dev(rng.uniform(-0.3, 0.3, n_in).astype(np.float32)) if norm else None
+    xd = to_dev(x)
+    runs = []
+    for P in (P_small, P_big):
+        ys = [torch.full((P, n), np.nan, device=dev()) for _, n in mats]
+        t, ws_ptr, ws_b = workspace(P, n_in)
+        vkv.matmul(xd.data_ptr(), P, n_in,
+                   [(w.data_ptr(), dt, n, y.data_ptr()) for w, (dt, n), y in zip(ws, mats, ys)],
+                   ws_ptr, ws_b, norm_w_ptr=nw.data_ptr() if norm else None,
+                   norm_b_ptr=nb.data_ptr() if norm else None, eps=EPS, hip_stream=stream_ptr())
+        raw = host(t).view(np.uint8)[ws_ptr - t.data_ptr():][:P * n_in].reshape(P, n_in)
+        runs.append((raw.copy(), [host(y) for y in ys]))
+    (img_s, out_s), (img_b, out_b) = runs
+    assert np.array_equal(img_s, img_b[:P_small])
+    for a, b in zip(out_s, out_b):
+        assert np.array_equal(a.view(np.uint32), b[:P_small].view(np.uint32))
+    # and the image is the oracle's
+    for p in range(P_small):
+        h = oracle.norm_act(x[p], host(nw), eps=EPS, norm_b=host(nb)) if norm else x[p]
+        want = oracle.q8_k_quantize(h).reshape(-1, 292)[:, 4:260].ravel()
+        codes = img_s[p].reshape(n_in // 256, 4, 4, 2, 8).transpose(0, 1, 3, 2, 4).reshape(n_in)
+        assert np.array_equal(codes, want)

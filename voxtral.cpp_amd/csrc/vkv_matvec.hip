@@ -47,7 +47,7 @@ struct ActSmem {
     int32_t bs32[kMvMaxIn / 32];         // sums of 32 codes (Q4_K sub-blocks)
     int32_t bs16[kMvMaxIn / 16];         // sums of 16 codes, order [b][n][h][g] (Q6_K)
     float dx[kMvMaxIn / 256];            // block scales
-    double red[4];
+    double ss[kMvMaxIn / 256];           // per-block sums of squares (the norm)
 };
 
 __device__ __forceinline__ float h2f(uint32_t bits16) {
@@ -210,20 +210,32 @@ __device__ __forceinline__ void act_finish(const ActRegs<NBW, NE> &r, int n,
     const int l = lane & 15;
     float scale = 1.0f;
     if (nw) {
-        double s = 0.0;
+        // Sum of squares per block (the 16 lanes' f32 products summed in
+        // double, the lanes by DPP, lane 0's sum kept), then over the blocks
+        // in block order: the fused-input products' order, so both images of
+        // a row are equal bit for bit.
 #pragma unroll
-        for (int i = 0; i < NBW; ++i)
-            if (16 * (i >> 2) + 4 * wave + (lane >> 4) < nb) {
-                const float4 v = r.x[i];
+        for (int k = 0; k < NBW / 4; ++k) {
+            if (16 * k + 4 * wave >= nb) break;
+            const int bb = 16 * k + 4 * wave + (lane >> 4);
+            double s = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = r.x[4 * k + j];
                 s += (double)(v.x * v.x);
                 s += (double)(v.y * v.y);
                 s += (double)(v.z * v.z);
                 s += (double)(v.w * v.w);
             }
-        s = wave_sum_d(s);
-        if (lane == 0) sm.red[wave] = s;
+            s += dppd<0xB1>(s);
+            s += dppd<0x4E>(s);
+            s += dppd<0x141>(s);
+            s += dppd<0x140>(s);
+            if (bb < nb && l == 0) sm.ss[bb] = s;
+        }
         __syncthreads();
-        const double tot = (sm.red[0] + sm.red[1]) + (sm.red[2] + sm.red[3]);
+        double tot = 0.0;
+        for (int b = 0; b < nb; ++b) tot += sm.ss[b];
         const float mean = (float)(tot / (double)n);
         scale = 1.0f / sqrtf(mean + eps);
     }
