@@ -99,7 +99,8 @@ WORKLOADS = {
     "longform_rope_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "stream4096_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "layer1_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
-    "layerwise_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
+    "layerwise_f16": dict(dtype=1, dtype_name="f16", streams=1,
+                          pmc="decode_f16_26x8192_layerwise_pmc.json", kern=""),
     "q8_0_batch8": dict(dtype=8, dtype_name="q8_0", streams=8,
                         pmc="decode_q8_0_8x26x8192_pmc.json", kern="k_decode_q8mfma"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
@@ -127,7 +128,7 @@ WORKLOADS = {
                             data="synthetic (a full-size realtime Q4_K_M GGUF file of random "
                                  "bytes, written to local disk before timing)"),
     "realtime_step_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights, f16 KV, f32 rings",
-                               streams=1, pmc="",
+                               streams=1, pmc="realtime_step_q4km_pmc.json", kern="",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) Mel windows "
                                     "and KV rows, generated on device)"),
     "decoder_prompt_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights (MFMA int8), f16 KV",
