@@ -7,9 +7,9 @@ the oldest position), F16 KV, 32 query / 8 KV heads x 128, one stream.  One
 step = one token = for every layer, append the token's K/V row (f32 -> f16) at
 pos % 8192 and run the single-query GQA attention over all 8192 retained
 positions, through the vkv_decoder_step C entry point: one k_decode_rows launch
-(append fused in its prologue; a work group per (layer, 1024-slot chunk) reads
-whole 2 KiB rows for all 8 kv heads) and one k_combine launch merging the 8
-chunks per head.  Inputs (Q, K, V for every timed step) are generated on the
+(append fused in its prologue; a work group per (layer, 912-slot chunk) reads
+whole 2 KiB rows for all 8 kv heads: 234 work groups, one per CU) and one
+k_combine launch merging the 9 chunks per head.  Inputs (Q, K, V for every timed step) are generated on the
 device before timing.
 
 Other workloads (--workload), reported on the same contract:
@@ -1668,8 +1668,8 @@ def main():
                                   "heads x 128, 1 stream")
             kernel = "26 x (k_decode + k_combine) (RoPE and append fused; 256-slot chunks, then the merge)"
         elif wl["dtype"] == 1 and ns == 1:
-            kernel = ("k_decode_rows + k_combine (append fused; a work group per (layer, 1024-slot "
-                      "chunk) reading whole rows, then the merge of the 8 chunks)")
+            kernel = ("k_decode_rows + k_combine (append fused; a work group per (layer, 912-slot "
+                      "chunk) reading whole rows, then the merge of the 9 chunks)")
         else:
             kernel = "k_decode_q8mfma + k_combine (append fused; split chunks)"
     # the load is bound by the host link, not HBM: PCIe 5.0 x16, 64 GB/s per direction

@@ -204,7 +204,7 @@ typedef struct vkv_cache_params {
      * is what production callers use.  Fixed for the cache's lifetime: no
      * process environment is consulted. */
     int32_t kernel_flags;  /* VKV_KERNEL_* bits */
-    int32_t decode_chunk;  /* slots per split decode work group (multiple of 64); 0 = automatic */
+    int32_t decode_chunk;  /* slots per split decode work group (multiple of 16); 0 = automatic */
     int32_t decode_waves;  /* waves per per-head decode work group (4 or 8); 0 = automatic */
     int32_t decode_stages; /* K/V batches in flight per decode wave (2..4); 0 = automatic */
 } vkv_cache_params;

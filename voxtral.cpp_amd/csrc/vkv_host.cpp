@@ -330,11 +330,12 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     a.chunk = pick_chunk(c, units, n_kv_max, gqa, &a.n_chunks);
     a.out = out;
     // F16 by whole rows (k_decode_rows): a work group per (stream, layer,
-    // 1024-slot chunk) reads 2 KiB rows, which stream faster than one head's
-    // 256-byte segments (measured on MI355X at 26 layers x 8192 slots: 135.4
-    // against 140.0 us per step with the merge launch included).  Used when
-    // its grid holds between 3/4 of the CUs and the CUs, as the one-pass
-    // k_decode; the cache's VKV_KERNEL_DECODE_HEADS / _ROWS flags override.
+    // chunk of at most 1024 slots) reads 2 KiB rows, which stream faster than
+    // one head's 256-byte segments (measured on MI355X at 26 layers x 8192
+    // slots: 135.4 against 140.0 us per step with the merge launch included).
+    // Used when its grid at 1024-slot chunks holds between 3/4 of the CUs and
+    // the CUs, as the one-pass k_decode; the cache's VKV_KERNEL_DECODE_HEADS
+    // / _ROWS flags override.
     {
         const int32_t rows_chunk = c->p.decode_chunk ? c->p.decode_chunk : 1024;
         const int32_t nc = std::max(1, (n_kv_max + rows_chunk - 1) / rows_chunk);
@@ -345,8 +346,23 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
                           (!has_flag(c, VKV_KERNEL_DECODE_HEADS) &&
                            4 * groups >= 3 * (int64_t)c->n_cus && groups <= c->n_cus);
         if (shape_ok && want) {
-            a.chunk = rows_chunk;
-            a.n_chunks = nc;
+            // As many chunks per (stream, layer) as leave every work group a
+            // CU of its own: each reads less of the window.  Measured on
+            // MI355X at 26 layers x 8192 slots: 9 chunks of 912 slots (234
+            // work groups) 135.7 us per step against 8 of 1024 (208) 139.8;
+            // 10 chunks (260 work groups, 4 of them doubled up) 158 us.
+            int32_t chunk = rows_chunk;
+            if (!c->p.decode_chunk && nc > 1) {
+                const int64_t row_units = (int64_t)n_streams * n_layers;
+                const int32_t cpl = (int32_t)std::max<int64_t>(1, c->n_cus / row_units);
+                chunk = std::min(rows_chunk, ((n_kv_max + cpl - 1) / cpl + 15) / 16 * 16);
+            }
+            a.chunk = chunk;
+            a.n_chunks = std::max(1, (n_kv_max + chunk - 1) / chunk);
+            if (units * a.n_chunks * gqa > c->part_heads_budget) {
+                a.chunk = rows_chunk;
+                a.n_chunks = nc;
+            }
             hipError_t e = launch_decode_rows(k_new != nullptr, n_streams, a, st);
             if (e != hipSuccess) return hip_fail(e, "decode launch");
             return merge_launch(c, a, n_streams, st);
@@ -637,7 +653,7 @@ vkv_status vkv_cache_create(const vkv_cache_params *params, vkv_cache **out) {
         ((p.kernel_flags & VKV_KERNEL_XCD_SWIZZLE) && (p.kernel_flags & VKV_KERNEL_NO_XCD_SWIZZLE)))
         return fail(VKV_STATUS_INVALID_ARGUMENT, "cache create: kernel_flags 0x%x invalid",
                     (unsigned)p.kernel_flags);
-    if ((p.decode_chunk != 0 && (p.decode_chunk < 64 || p.decode_chunk % 64 != 0)) ||
+    if ((p.decode_chunk != 0 && (p.decode_chunk < 16 || p.decode_chunk % 16 != 0)) ||
         (p.decode_waves != 0 && p.decode_waves != 4 && p.decode_waves != 8) ||
         (p.decode_stages != 0 && (p.decode_stages < 2 || p.decode_stages > 4)))
         return fail(VKV_STATUS_INVALID_ARGUMENT,
