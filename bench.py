@@ -1618,8 +1618,9 @@ def main():
                               "8192-slot f16 ring, O + residual, RMSNorm*(1+ada) + SwiGLU, W2 + "
                               "residual), final norm, 131072-row logits, argmax",
                   "layers": LAYERS, "dim": DIM, "hidden": HIDDEN, "vocab": VOCAB, "window": CAP,
-                  "bytes_per_token": bytes_step, "launches_per_token": 5 * LAYERS + 3}
-        kernel = "k_matvec + k_decode (133 launches per token)"
+                  "bytes_per_token": bytes_step, "launches_per_token": 6 * LAYERS + 2}
+        kernel = ("k_kq_dequant + 26 x (4 k_matvec + k_decode + k_combine) + k_matvec "
+                  "(158 launches per token)")
     elif args.workload == "decoder_weights_q4km":
         total_ms, step_ms, wall = gpu_weights(args.steps, args.warmup)
         bytes_step = weights_bytes_per_token()
