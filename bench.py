@@ -954,6 +954,9 @@ REPS_SET = [REPS]   # the run's repetitions (--reps)
 REP_MS = []         # the last timed_loop's per-repetition totals (ms)
 
 
+SPIN_CYCLES = 500_000   # GPU clock cycles of the pre-repetition spin (~0.2 ms)
+
+
 def timed_loop(step, steps, warmup, st, every=8, reps=None):
     """W untimed steps, then `reps` repetitions of K timed steps, each between
     a synchronize and two events on the launch stream; returns the median
@@ -964,7 +967,11 @@ def timed_loop(step, steps, warmup, st, every=8, reps=None):
     GPU a few microseconds, so bracketing single steps would add that to
     every sample (and events around every step would slow the timed region).
     A repetition replays the same step indices (their inputs); the state the
-    steps advance (ring positions) keeps advancing."""
+    steps advance (ring positions) keeps advancing.  Before each repetition's
+    start event the stream gets a short spin (~0.2 ms, untimed) so the host
+    has queued the first steps when the start event runs: the timed region
+    then holds the K steps, not the host's latency in launching the first
+    one after the synchronize (~1% of a 20-step region)."""
     import torch
     reps = REPS_SET[0] if reps is None else reps
     for i in range(warmup):
@@ -980,6 +987,8 @@ def timed_loop(step, steps, warmup, st, every=8, reps=None):
         t_start = torch.cuda.Event(enable_timing=True)
         t_end = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        with torch.cuda.stream(st):
+            torch.cuda._sleep(SPIN_CYCLES)
         t_start.record(st)
         for i in range(steps):
             if i in ev:
