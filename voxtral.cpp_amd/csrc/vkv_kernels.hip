@@ -1986,14 +1986,16 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
             dst[1] = make_uint2(vr[t].z, vr[t].w);
         }
 
-        // S^T = K Q^T
-        float4_t st = float4_t{0, 0, 0, 0};
+        // S^T = K Q^T, even and odd 16-dim steps in two accumulators (a
+        // shorter chain of dependent MFMAs; summed at the end)
+        float4_t s2[2] = {float4_t{0, 0, 0, 0}, float4_t{0, 0, 0, 0}};
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
             const uint32_t w0 = (&kr[0].x)[2 * kb], w1 = (&kr[0].x)[2 * kb + 1];
             const half4_t ka = __builtin_bit_cast(half4_t, (uint64_t)w0 | ((uint64_t)w1 << 32));
-            st = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qb[kb], st, 0, 0, 0);
+            s2[kb & 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(ka, qb[kb], s2[kb & 1], 0, 0, 0);
         }
+        const float4_t st = s2[0] + s2[1];
         // lane holds keys jb + 4*lg + i (i = 0..3) for row lr
         float sc[4];
         float bm = -INFINITY;
@@ -2199,15 +2201,19 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
             vt[(DL * lg + 4 * t + 2) * VS + lr] = vr[t].z;
             vt[(DL * lg + 4 * t + 3) * VS + lr] = vr[t].w;
         }
-        // S^T = K Q^T, one MFMA per dim step s
-        float4_t st = float4_t{0, 0, 0, 0};
+        // S^T = K Q^T, one MFMA per dim step, into four independent
+        // accumulators (dims = 0, 1, 2, 3 mod 4) summed at the end: one
+        // chain of DL dependent MFMAs per block cost 5% of the launch
+        float4_t sa[4] = {float4_t{0, 0, 0, 0}, float4_t{0, 0, 0, 0}, float4_t{0, 0, 0, 0},
+                          float4_t{0, 0, 0, 0}};
 #pragma unroll
         for (int t = 0; t < DL / 4; ++t) {
-            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].x, qf[4 * t], st, 0, 0, 0);
-            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].y, qf[4 * t + 1], st, 0, 0, 0);
-            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].z, qf[4 * t + 2], st, 0, 0, 0);
-            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].w, qf[4 * t + 3], st, 0, 0, 0);
+            sa[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].x, qf[4 * t], sa[0], 0, 0, 0);
+            sa[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].y, qf[4 * t + 1], sa[1], 0, 0, 0);
+            sa[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].z, qf[4 * t + 2], sa[2], 0, 0, 0);
+            sa[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(kr[t].w, qf[4 * t + 3], sa[3], 0, 0, 0);
         }
+        const float4_t st = (sa[0] + sa[1]) + (sa[2] + sa[3]);
         // lane holds keys jb + 4 lg + i (i = 0..3) for row lr
         float sc[4];
         float bm = -INFINITY;
