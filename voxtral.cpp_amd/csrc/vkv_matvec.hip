@@ -858,13 +858,11 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, i
 // aligned): one 8-byte load when the offset is 4-aligned, else 12 bytes from
 // 2 below, realigned -- never past off + 10
 __device__ __forceinline__ uint64_t ld8_even(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
-    if ((off & 3u) == 0) {
-        const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
-        return ((uint64_t)v.y << 32) | v.x;
-    }
-    const u32x3_t w = __builtin_amdgcn_raw_buffer_load_b96(rs, off - 2u, 0, 0);
-    const uint32_t lo = __builtin_amdgcn_alignbyte(w.y, w.x, 2u);
-    const uint32_t hi = __builtin_amdgcn_alignbyte(w.z, w.y, 2u);
+    // one load path for both alignments (a value merged from two loads is
+    // copied, and the copy waits for its load)
+    const u32x3_t w = __builtin_amdgcn_raw_buffer_load_b96(rs, off & ~3u, 0, 0);
+    const uint32_t lo = __builtin_amdgcn_alignbyte(w.y, w.x, off & 3u);
+    const uint32_t hi = __builtin_amdgcn_alignbyte(w.z, w.y, off & 3u);
     return ((uint64_t)hi << 32) | lo;
 }
 
@@ -992,10 +990,18 @@ __device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, const XImage &im,
 // order, so a row's codes do not depend on the work group or the number of
 // rows in the call.
 constexpr int kFqRounds = 2;
+// The norm's vectors (weight, bias, ada) reach the fused quantizer through
+// LDS, each thread loading at most kFqNormPer elements of each (the host
+// fuses a normed call only when n_in <= kFqNormPer * 64 * waves).
+constexpr int kFqNormPer = 4;
 
-template <int W>
-__device__ void gemm_quant_cols(const MmArgs &a, int col0, int ncol, int8_t *cq, float *cd,
-                                int16_t *cs, double *ss) {
+// pre() is called once the input rows (and the norm's vectors) have been
+// requested and before anything waits for them: the caller requests its
+// first weights there, so their round trip overlaps the input's.
+template <int W, class Pre>
+__device__ __forceinline__ void gemm_quant_cols(const MmArgs &a, int col0, int ncol, int8_t *cq,
+                                                float *cd, int16_t *cs, double *ss, float *nv,
+                                                Pre &&pre) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l = lane & 15;
     const int K = a.n_in, nb = K >> 8, tasks = ncol * nb;
@@ -1018,7 +1024,27 @@ __device__ void gemm_quant_cols(const MmArgs &a, int col0, int ncol, int8_t *cq,
             e[r][4 * j + 3] = v.w;
         }
     }
+    float nvr[3][kFqNormPer];
     if (a.norm_w) {
+#pragma unroll
+        for (int k = 0; k < kFqNormPer; ++k) {
+            const int i = (int)threadIdx.x + 64 * W * k;
+            nvr[0][k] = i < K ? a.norm_w[i] : 0.0f;
+            nvr[1][k] = a.norm_b && i < K ? a.norm_b[i] : 0.0f;
+            nvr[2][k] = a.ada && i < K ? a.ada[i] : 0.0f;
+        }
+    }
+    pre();
+    if (a.norm_w) {
+#pragma unroll
+        for (int k = 0; k < kFqNormPer; ++k) {
+            const int i = (int)threadIdx.x + 64 * W * k;
+            if (i < K) {
+                nv[i] = nvr[0][k];
+                nv[K + i] = nvr[1][k];
+                nv[2 * K + i] = nvr[2][k];
+            }
+        }
 #pragma unroll
         for (int r = 0; r < kFqRounds; ++r) {
             const int t = gi + 4 * W * r;
@@ -1046,7 +1072,7 @@ __device__ void gemm_quant_cols(const MmArgs &a, int col0, int ncol, int8_t *cq,
             const int e0 = 256 * b + 16 * l;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float4 w4 = *reinterpret_cast<const float4 *>(a.norm_w + e0 + 4 * j);
+                const float4 w4 = *reinterpret_cast<const float4 *>(nv + e0 + 4 * j);
                 const float w[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
                 for (int u = 0; u < 4; ++u) {
@@ -1054,14 +1080,14 @@ __device__ void gemm_quant_cols(const MmArgs &a, int col0, int ncol, int8_t *cq,
                     e[r][4 * j + u] = e[r][4 * j + u] * w[u];
                 }
                 if (a.norm_b) {
-                    const float4 b4 = *reinterpret_cast<const float4 *>(a.norm_b + e0 + 4 * j);
+                    const float4 b4 = *reinterpret_cast<const float4 *>(nv + K + e0 + 4 * j);
                     e[r][4 * j] = e[r][4 * j] + b4.x;
                     e[r][4 * j + 1] = e[r][4 * j + 1] + b4.y;
                     e[r][4 * j + 2] = e[r][4 * j + 2] + b4.z;
                     e[r][4 * j + 3] = e[r][4 * j + 3] + b4.w;
                 }
                 if (a.ada) {
-                    const float4 a4 = *reinterpret_cast<const float4 *>(a.ada + e0 + 4 * j);
+                    const float4 a4 = *reinterpret_cast<const float4 *>(nv + 2 * K + e0 + 4 * j);
                     const float av[4] = {a4.x, a4.y, a4.z, a4.w};
 #pragma unroll
                     for (int u = 0; u < 4; ++u) {
@@ -1207,11 +1233,15 @@ __device__ __forceinline__ float rope_elem(float self, float partner, bool odd, 
 // input rows each) per work group: a wave loads each weight block once and
 // applies it to every column tile, so the weights are read once per 16 CT
 // input rows.
-template <bool Q4, int W, int CT>
+template <bool Q4, int W, int CT, class GF>
 __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, const MmOut &o1,
                                           uint32_t (*hdr)[16][6], float (*red)[W][16][17],
-                                          const XImage &im) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kg = lane >> 4, rr = lane & 15;
+                                          const XImage &im, const GF &w_first) {
+    // the wave index through readfirstlane: the per-wave descriptor select
+    // below is then scalar (a per-lane one puts every load in a loop over
+    // the descriptor's values)
+    const int lane = threadIdx.x & 63, kg = lane >> 4, rr = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool swiglu = a.swiglu != 0;
     const int nb = a.n_in >> 8;
     const uint32_t bbytes = Q4 ? kQ4Bytes : kQ6Bytes, rbytes = (uint32_t)nb * bbytes;
@@ -1233,11 +1263,10 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
     for (int c = 0; c < CT; ++c)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[c][i] = 0.0f;
-    using GF = std::conditional_t<Q4, GFragQ4, GFragQ6>;
     // the wave's blocks b, b + kw, b + 2 kw, ...: one block's fragments at a
-    // time (occupancy, not a second register set, covers the load latency)
-    for (int b = wm; b < nb; b += kw) {
-        GF w = gemm_load_w<Q4>(rs, (uint32_t)row * rbytes + (uint32_t)b * bbytes, kg);
+    // time (occupancy, not a second register set, covers the load latency);
+    // the first block's (w_first) were requested by the caller
+    auto block = [&](GF w, int b) __attribute__((always_inline)) {
 #pragma unroll
         for (int c = 0; c < CT; ++c) {
             if (c < n_ct) {
@@ -1254,7 +1283,10 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
             }
             if (CT > 1) __builtin_amdgcn_sched_barrier(0);
         }
-    }
+    };
+    if (wm < nb) block(w_first, wm);
+    for (int b = wm + kw; b < nb; b += kw)
+        block(gemm_load_w<Q4>(rs, (uint32_t)row * rbytes + (uint32_t)b * bbytes, kg), b);
     // the waves' partial sums meet in LDS: red[column tile][wave][row][input row]
     // (SwiGLU: waves m kw .. m kw + kw - 1 hold matrix m)
 #pragma unroll
@@ -1301,9 +1333,10 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
 // Fused input image in dynamic LDS: codes, block scales, 32-element sums,
 // per-task sums of squares (the norm's first pass).
 __host__ __device__ constexpr size_t al16(size_t b) { return (b + 15) & ~(size_t)15; }
-__host__ __device__ constexpr size_t fused_lds_bytes(int cols, int n_in) {
+__host__ __device__ constexpr size_t fused_lds_bytes(int cols, int n_in, bool norm) {
     return al16((size_t)cols * n_in) + al16((size_t)cols * (n_in / 256) * 4) +
-           al16((size_t)cols * (n_in / 32) * 2) + al16((size_t)cols * (n_in / 256) * 8);
+           al16((size_t)cols * (n_in / 32) * 2) + al16((size_t)cols * (n_in / 256) * 8) +
+           (norm ? (size_t)3 * n_in * 4 : 0);
 }
 
 template <int W, int CT, bool FQ>
@@ -1316,36 +1349,65 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         if (k < a.n_outs && (int)blockIdx.x >= a.out[k].tile0) seg = k;
     const MmOut o0 = mm_out_at(a, seg);
     const MmOut o1 = a.swiglu ? a.out[1] : o0;
-    XImage im{a.xq, a.xd, a.xbs, 0};
-    if constexpr (FQ) {
-        extern __shared__ __align__(16) uint8_t fq_lds[];
-        const int col0 = (int)blockIdx.y * 16 * CT;
-        const int ncol = min(16 * CT, a.n_cols - col0);
-        const int K = a.n_in, nb = K >> 8, cols = 16 * CT;
-        int8_t *cq = reinterpret_cast<int8_t *>(fq_lds);
-        float *cd = reinterpret_cast<float *>(fq_lds + al16((size_t)cols * K));
-        int16_t *cs = reinterpret_cast<int16_t *>(reinterpret_cast<uint8_t *>(cd) +
-                                                  al16((size_t)cols * nb * 4));
-        double *ss = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(cs) +
-                                                al16((size_t)cols * (K / 32) * 2));
-        gemm_quant_cols<W>(a, col0, ncol, cq, cd, cs, ss);
-        im = XImage{cq, cd, cs, col0};
-        if (blockIdx.x == 0 && a.xq) {
-            // the first row tile's work groups leave their rows' image in the
-            // caller's workspace too (the separate quantization's output),
-            // read by nothing in the call
-            const int4 *src = reinterpret_cast<const int4 *>(cq);
-            int4 *dst = reinterpret_cast<int4 *>(const_cast<int8_t *>(a.xq) + (int64_t)col0 * K);
-            for (int i = threadIdx.x; i < ncol * K / 16; i += 64 * W) dst[i] = src[i];
-            float *xd = const_cast<float *>(a.xd) + (int64_t)col0 * nb;
-            for (int i = threadIdx.x; i < ncol * nb; i += 64 * W) xd[i] = cd[i];
-            int16_t *xb = const_cast<int16_t *>(a.xbs) + (int64_t)col0 * (K / 32);
-            for (int i = threadIdx.x; i < ncol * (K / 32); i += 64 * W) xb[i] = cs[i];
-        }
-    }
     // one weight dtype per work group (both SwiGLU matrices share it)
-    if (o0.dtype == VKV_DTYPE_Q4_K) gemm_body<true, W, CT>(a, o0, o1, hdr, red, im);
-    else gemm_body<false, W, CT>(a, o0, o1, hdr, red, im);
+    auto run = [&](auto q4) __attribute__((always_inline)) {
+        constexpr bool Q4 = decltype(q4)::value;
+        // the wave's first weight block (gemm_body's decomposition), requested
+        // before the fused input quantization waits for anything; the block
+        // index is clamped so the request is unconditional (a wave without a
+        // block does not use it)
+        const int lane = threadIdx.x & 63, kg = lane >> 4, rr = lane & 15;
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int nb = a.n_in >> 8;
+        const uint32_t bbytes = Q4 ? kQ4Bytes : kQ6Bytes, rbytes = (uint32_t)nb * bbytes;
+        const int row = min(((int)blockIdx.x - o0.tile0) * 16 + rr, o0.n_rows - 1);
+        const int kw = a.swiglu ? W / 2 : W;
+        const int m = a.swiglu ? wave / kw : 0, wm = wave - m * kw;
+        const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(o0.w), (short)0, (int)(rbytes * (uint32_t)o0.n_rows), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t *>(o1.w), (short)0, (int)(rbytes * (uint32_t)o1.n_rows), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rs = m ? rs1 : rs0;
+        using GF = std::conditional_t<Q4, GFragQ4, GFragQ6>;
+        GF wf;
+        auto pre = [&]() __attribute__((always_inline)) {
+            wf = gemm_load_w<Q4>(rs, (uint32_t)row * rbytes + (uint32_t)min(wm, nb - 1) * bbytes, kg);
+        };
+        XImage im{a.xq, a.xd, a.xbs, 0};
+        if constexpr (FQ) {
+            extern __shared__ __align__(16) uint8_t fq_lds[];
+            const int col0 = (int)blockIdx.y * 16 * CT;
+            const int ncol = min(16 * CT, a.n_cols - col0);
+            const int K = a.n_in, cols = 16 * CT;
+            int8_t *cq = reinterpret_cast<int8_t *>(fq_lds);
+            float *cd = reinterpret_cast<float *>(fq_lds + al16((size_t)cols * K));
+            int16_t *cs = reinterpret_cast<int16_t *>(reinterpret_cast<uint8_t *>(cd) +
+                                                      al16((size_t)cols * nb * 4));
+            double *ss = reinterpret_cast<double *>(reinterpret_cast<uint8_t *>(cs) +
+                                                    al16((size_t)cols * (K / 32) * 2));
+            float *nv = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ss) +
+                                                  al16((size_t)cols * nb * 8));
+            gemm_quant_cols<W>(a, col0, ncol, cq, cd, cs, ss, nv, pre);
+            im = XImage{cq, cd, cs, col0};
+            if (blockIdx.x == 0 && a.xq) {
+                // the first row tile's work groups leave their rows' image in
+                // the caller's workspace too (the separate quantization's
+                // output), read by nothing in the call
+                const int4 *src = reinterpret_cast<const int4 *>(cq);
+                int4 *dst = reinterpret_cast<int4 *>(const_cast<int8_t *>(a.xq) + (int64_t)col0 * K);
+                for (int i = threadIdx.x; i < ncol * K / 16; i += 64 * W) dst[i] = src[i];
+                float *xd = const_cast<float *>(a.xd) + (int64_t)col0 * nb;
+                for (int i = threadIdx.x; i < ncol * nb; i += 64 * W) xd[i] = cd[i];
+                int16_t *xb = const_cast<int16_t *>(a.xbs) + (int64_t)col0 * (K / 32);
+                for (int i = threadIdx.x; i < ncol * (K / 32); i += 64 * W) xb[i] = cs[i];
+            }
+        } else {
+            pre();
+        }
+        gemm_body<Q4, W, CT>(a, o0, o1, hdr, red, im, wf);
+    };
+    if (o0.dtype == VKV_DTYPE_Q4_K) run(std::true_type{});
+    else run(std::false_type{});
 }
 
 }  // namespace
@@ -1419,7 +1481,7 @@ hipError_t launch_gemm_kq(MmArgs a, int n_col_tiles, hipStream_t st) {
     // dynamic LDS (the caller checked gemm_fused_lds).
     const bool fq = a.x != nullptr;
     const int cols = gemm_cols_per_wg(a, n_col_tiles);
-    const size_t lds = fq ? fused_lds_bytes(cols, a.n_in) : 0;
+    const size_t lds = fq ? fused_lds_bytes(cols, a.n_in, a.norm_w != nullptr) : 0;
     if (tiles < 128) {
         const dim3 g((unsigned)tiles, (unsigned)n_col_tiles);
         if (fq) k_gemm_kq<16, 1, true><<<g, 1024, lds, st>>>(a);
@@ -1457,7 +1519,8 @@ bool gemm_fused_ok(const MmArgs &a, int n_col_tiles) {
     const int cols = gemm_cols_per_wg(a, n_col_tiles);
     const int rows = std::min(cols, a.n_cols);
     return rows * (a.n_in / 256) <= kFqRounds * 4 * waves &&
-           fused_lds_bytes(cols, a.n_in) <= 128 * 1024;
+           (!a.norm_w || a.n_in <= kFqNormPer * 64 * waves) &&
+           fused_lds_bytes(cols, a.n_in, a.norm_w != nullptr) <= 128 * 1024;
 }
 
 hipError_t launch_rms_norm_rows(const float *x, int n_rows, int n, const float *w, const float *b,
