@@ -904,7 +904,12 @@ struct GFragX {
     float dx;
 };
 
-template <bool Q4>
+// ALLH: every lane loads the block header (scales, d); otherwise only the
+// lanes that pass it on (kg = 0) do, and the others' zeros merge with the
+// loaded value, which waits for the load there.  The fused-input kernels
+// request a block before the input quantization and must not wait for it;
+// the others issue fewer loads without it.
+template <bool Q4, bool ALLH>
 __device__ __forceinline__ auto gemm_load_w(__amdgpu_buffer_rsrc_t rs, uint32_t boff, int kg) {
     if constexpr (Q4) {
         GFragQ4 f;
@@ -915,8 +920,12 @@ __device__ __forceinline__ auto gemm_load_w(__amdgpu_buffer_rsrc_t rs, uint32_t 
             f.qs[c] = ((uint64_t)v.y << 32) | v.x;
         }
         // the header is only read by the lanes that pass it on (kg = 0)
-        f.h = u32x4_t{0, 0, 0, 0};
-        if (kg == 0) f.h = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, boff, 0, 0));
+        if (ALLH) {
+            f.h = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, boff, 0, 0));
+        } else {
+            f.h = u32x4_t{0, 0, 0, 0};
+            if (kg == 0) f.h = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, boff, 0, 0));
+        }
         return f;
     } else {
         GFragQ6 f;
@@ -927,12 +936,18 @@ __device__ __forceinline__ auto gemm_load_w(__amdgpu_buffer_rsrc_t rs, uint32_t 
             f.qh[n] = ld8_even(rs, boff + 128 + 32 * n + 8 * kg);
         }
         // scales and d are only read by the lanes that pass them on (kg = 0)
-        f.s0 = f.s1 = 0;
-        f.dh = 0;
-        if (kg == 0) {
+        if (ALLH) {
             f.s0 = ld8_even(rs, boff + 192);
             f.s1 = ld8_even(rs, boff + 200);
             f.dh = __builtin_amdgcn_raw_buffer_load_b16(rs, boff + 208, 0, 0);
+        } else {
+            f.s0 = f.s1 = 0;
+            f.dh = 0;
+            if (kg == 0) {
+                f.s0 = ld8_even(rs, boff + 192);
+                f.s1 = ld8_even(rs, boff + 200);
+                f.dh = __builtin_amdgcn_raw_buffer_load_b16(rs, boff + 208, 0, 0);
+            }
         }
         return f;
     }
@@ -1233,7 +1248,7 @@ __device__ __forceinline__ float rope_elem(float self, float partner, bool odd, 
 // input rows each) per work group: a wave loads each weight block once and
 // applies it to every column tile, so the weights are read once per 16 CT
 // input rows.
-template <bool Q4, int W, int CT, class GF>
+template <bool Q4, int W, int CT, bool ALLH, class GF>
 __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, const MmOut &o1,
                                           uint32_t (*hdr)[16][6], float (*red)[W][16][17],
                                           const XImage &im, const GF &w_first) {
@@ -1286,7 +1301,7 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
     };
     if (wm < nb) block(w_first, wm);
     for (int b = wm + kw; b < nb; b += kw)
-        block(gemm_load_w<Q4>(rs, (uint32_t)row * rbytes + (uint32_t)b * bbytes, kg), b);
+        block(gemm_load_w<Q4, ALLH>(rs, (uint32_t)row * rbytes + (uint32_t)b * bbytes, kg), b);
     // the waves' partial sums meet in LDS: red[column tile][wave][row][input row]
     // (SwiGLU: waves m kw .. m kw + kw - 1 hold matrix m)
 #pragma unroll
@@ -1371,7 +1386,8 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         using GF = std::conditional_t<Q4, GFragQ4, GFragQ6>;
         GF wf;
         auto pre = [&]() __attribute__((always_inline)) {
-            wf = gemm_load_w<Q4>(rs, (uint32_t)row * rbytes + (uint32_t)min(wm, nb - 1) * bbytes, kg);
+            wf = gemm_load_w<Q4, FQ>(rs, (uint32_t)row * rbytes + (uint32_t)min(wm, nb - 1) * bbytes,
+                                     kg);
         };
         XImage im{a.xq, a.xd, a.xbs, 0};
         if constexpr (FQ) {
@@ -1404,7 +1420,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         } else {
             pre();
         }
-        gemm_body<Q4, W, CT>(a, o0, o1, hdr, red, im, wf);
+        gemm_body<Q4, W, CT, FQ>(a, o0, o1, hdr, red, im, wf);
     };
     if (o0.dtype == VKV_DTYPE_Q4_K) run(std::true_type{});
     else run(std::false_type{});
