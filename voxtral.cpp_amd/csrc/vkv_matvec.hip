@@ -172,20 +172,24 @@ __device__ __forceinline__ QBlock16 q8k_block16(const float (&e)[16], int l) {
 // Split in two so that a caller can issue its own loads between them: the
 // input loads of act_load retire first (vmcnt counts in issue order), and
 // act_finish then waits for them alone.  NBW = 4 x rounds (float4 per lane);
-// with NORM_EARLY the norm weights are loaded up front too.
-template <int NBW, bool NORM_EARLY>
+// with NORM_EARLY the norm weights (and the ada row) are loaded up front too,
+// with BIAS_EARLY the norm's bias as well (absent vectors read x instead:
+// one load path, unused).
+template <int NBW, bool NORM_EARLY, bool BIAS_EARLY = false>
 struct ActRegs {
     float4 x[NBW];
     float4 w[NORM_EARLY ? NBW : 1];
     float4 a[NORM_EARLY ? NBW : 1];
+    float4 b[BIAS_EARLY ? NBW : 1];
 };
 
-template <int NBW, bool NE>
-__device__ __forceinline__ void act_load(ActRegs<NBW, NE> &r, const float *__restrict__ x, int n,
-                                         const float *__restrict__ nw,
-                                         const float *__restrict__ ada) {
+template <int NBW, bool NE, bool NB>
+__device__ __forceinline__ void act_load(ActRegs<NBW, NE, NB> &r, const float *__restrict__ x,
+                                         int n, const float *__restrict__ nw,
+                                         const float *__restrict__ ada,
+                                         const float *__restrict__ nbias = nullptr) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nb = n >> 8;
-    const float *wp = nw ? nw : x, *ap = ada ? ada : x;
+    const float *wp = nw ? nw : x, *ap = ada ? ada : x, *bp = nbias ? nbias : x;
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
         const int bb = 16 * (i >> 2) + 4 * wave + (lane >> 4);
@@ -196,11 +200,12 @@ __device__ __forceinline__ void act_load(ActRegs<NBW, NE> &r, const float *__res
             r.w[i] = *reinterpret_cast<const float4 *>(wp + e0);
             r.a[i] = *reinterpret_cast<const float4 *>(ap + e0);
         }
+        if (NB) r.b[i] = *reinterpret_cast<const float4 *>(bp + e0);
     }
 }
 
-template <int NBW, bool NE>
-__device__ __forceinline__ void act_finish(const ActRegs<NBW, NE> &r, int n,
+template <int NBW, bool NE, bool NB>
+__device__ __forceinline__ void act_finish(const ActRegs<NBW, NE, NB> &r, int n,
                                            const float *__restrict__ nw,
                                            const float *__restrict__ ada, float eps, ActSmem &sm,
                                            uint8_t *__restrict__ gout,
@@ -267,7 +272,7 @@ __device__ __forceinline__ void act_finish(const ActRegs<NBW, NE> &r, int n,
                 }
                 if (nbias) {
                     // + the norm's bias (the encoder's norms, src/voxtral.cpp:1855-1861)
-                    const float4 b4 = *reinterpret_cast<const float4 *>(nbias + e0);
+                    const float4 b4 = NB ? r.b[4 * k + j] : *reinterpret_cast<const float4 *>(nbias + e0);
                     e[4 * j] = e[4 * j] + b4.x;
                     e[4 * j + 1] = e[4 * j + 1] + b4.y;
                     e[4 * j + 2] = e[4 * j + 2] + b4.z;
@@ -826,6 +831,9 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, in
 //                 one MFMA per 16-element scale group (the other half of the
 //                 k window zeroed).
 // ---------------------------------------------------------------------------
+// NE: inputs of up to 4096 (one round of 16-lane rows), with the norm's
+// weight, ada and bias requested together with the input (one round trip)
+template <int NBW, bool NE>
 __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, int64_t x_stride,
                                                   int x_ring, int x_row0, int n, const float *nw,
                                                   const float *nbias, const float *ada, float eps,
@@ -834,8 +842,8 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, i
     __shared__ ActSmem sm;
     const int p = blockIdx.x;
     const int src = x_ring > 0 ? (x_row0 + p) % x_ring : p;
-    ActRegs<kMvMaxIn / 1024, false> r;
-    act_load(r, x + (int64_t)src * x_stride, n, nw, ada);
+    ActRegs<NBW, NE, NE> r;
+    act_load(r, x + (int64_t)src * x_stride, n, nw, ada, nbias);
     act_finish(r, n, nw, ada, eps, sm, nullptr, nbias);
     // codes in the products' lane order: within each 256-block, the 16 bytes
     // at 64 q + 16 kg hold the codes k = 32 j + 8 kg + e of j = 2q, 2q + 1
@@ -1467,8 +1475,13 @@ hipError_t launch_embed_rows(int dtype, const uint8_t *table, int64_t row_bytes,
 hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_row0, int n_rows,
                            int n, const float *norm_w, const float *norm_b, const float *ada,
                            float eps, int8_t *codes, float *xd, int16_t *bs16, hipStream_t st) {
-    k_q8k_rows<<<n_rows, 256, 0, st>>>(x, x_stride, x_ring, x_row0, n, norm_w, norm_b, ada, eps,
-                                       codes, xd, bs16);
+    if (n <= 4096)
+        k_q8k_rows<4, true><<<n_rows, 256, 0, st>>>(x, x_stride, x_ring, x_row0, n, norm_w, norm_b,
+                                                     ada, eps, codes, xd, bs16);
+    else
+        k_q8k_rows<kMvMaxIn / 1024, false><<<n_rows, 256, 0, st>>>(x, x_stride, x_ring, x_row0, n,
+                                                                    norm_w, norm_b, ada, eps,
+                                                                    codes, xd, bs16);
     return hipGetLastError();
 }
 
