@@ -188,7 +188,8 @@ __device__ __forceinline__ void act_load(ActRegs<NBW, NE, NB> &r, const float *_
                                          int n, const float *__restrict__ nw,
                                          const float *__restrict__ ada,
                                          const float *__restrict__ nbias = nullptr) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nb = n >> 8;
+    const int lane = threadIdx.x & 63, nb = n >> 8;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const float *wp = nw ? nw : x, *ap = ada ? ada : x, *bp = nbias ? nbias : x;
 #pragma unroll
     for (int i = 0; i < NBW; ++i) {
@@ -211,7 +212,8 @@ __device__ __forceinline__ void act_finish(const ActRegs<NBW, NE, NB> &r, int n,
                                            uint8_t *__restrict__ gout,
                                            const float *__restrict__ nbias = nullptr) {
 #pragma clang fp contract(off)
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nb = n >> 8;
+    const int tid = threadIdx.x, lane = tid & 63, nb = n >> 8;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l = lane & 15;
     float scale = 1.0f;
     if (nw) {
@@ -600,7 +602,9 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
 template <int S, int D, bool AMAX>
 __global__ void __launch_bounds__(256) k_matvec(MvArgs a) {
     __shared__ ActSmem sm;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform (readfirstlane): the row range and the unit loop follow
+    // from it, and a per-lane wave makes the loop divergent
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     int seg = 0;
 #pragma unroll
     for (int k = 1; k < kMvMaxOuts; ++k)
