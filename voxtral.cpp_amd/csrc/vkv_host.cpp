@@ -1153,7 +1153,8 @@ vkv_status matvec_impl(const float *x, int64_t n_in, const float *norm_w, const 
     const int cus = device_cus();
     const int64_t per_cu = total > 32768 ? 8 : 16;
     int64_t rpw = (total + per_cu * cus - 1) / (per_cu * cus);
-    rpw = std::max<int64_t>(1, std::min<int64_t>(rpw, 1 << 20));
+    // at most 64 rows per wave: a lane holds each row's residual
+    rpw = std::max<int64_t>(1, std::min<int64_t>(rpw, 64));
     MvArgs a{};
     a.x = x;
     a.norm_w = norm_w;

@@ -110,9 +110,11 @@ __device__ __forceinline__ uint32_t row_max_u(uint32_t v) {
 // One Q8_K block held by a 16-lane row, lane l with elements 16l..16l+15:
 // the codes packed 4 per dword, the sum of the lane's 16 codes, of 32 codes
 // (lanes 2k, 2k+1 hold the same) and d.  The same arithmetic as q8k_block
-// (ggml quantize_row_q8_K_ref); the first element of largest |h| is found as
-// the row maximum of |h|, then the row maximum of a key that orders its
-// holders by smallest index and carries the element's sign.
+// (ggml quantize_row_q8_K_ref).  The first element of largest |h|: each lane
+// keeps its own first one (strict >, in element order), the row maximum of
+// |h| picks the value, and the row maximum of a key that orders the lanes
+// holding it by smallest lane (lane l holds elements before lane l + 1's)
+// carries the element's sign.
 struct QBlock16 {
     uint32_t packed[4];
     int s16, s32;
@@ -120,19 +122,14 @@ struct QBlock16 {
 };
 __device__ __forceinline__ QBlock16 q8k_block16(const float (&e)[16], int l) {
 #pragma clang fp contract(off)
-    float am = 0.0f;
-    int ai = 0;
-    uint32_t neg = 0;
+    float mv = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k)
-        if (fabsf(e[k]) > am) {
-            am = fabsf(e[k]);
-            ai = k;
-            neg = __builtin_bit_cast(uint32_t, e[k]) >> 31;
-        }
-    const uint32_t amb = __builtin_bit_cast(uint32_t, am);
+    for (int k = 0; k < 16; ++k) mv = fabsf(e[k]) > fabsf(mv) ? e[k] : mv;
+    const uint32_t amb = __builtin_bit_cast(uint32_t, fabsf(mv));
     const uint32_t mxa = row_max_u(amb);
-    const uint32_t key = (amb == mxa && mxa != 0u) ? ((uint32_t)(255 - (16 * l + ai)) << 1) | neg : 0u;
+    const uint32_t key = (amb == mxa && mxa != 0u)
+                             ? ((uint32_t)(16 - l) << 1) | (__builtin_bit_cast(uint32_t, mv) >> 31)
+                             : 0u;
     const uint32_t kmax = row_max_u(key);
     int q[16];
     QBlock16 r;
@@ -457,13 +454,14 @@ __device__ __forceinline__ XFrag xfrag(const ActSmem &sm, bool q4, int t) {
 
 // Where unit u of a wave reads its weights.  The buffer descriptor is built
 // per load from a uniform pointer and size (a select between two descriptors
-// is lowered through scratch memory).
+// is lowered through scratch memory).  Units past the wave's last one read
+// zeros (an offset past the buffer), so every load is unconditional.
 struct UnitMap {
     const uint8_t *w0, *w1;
     uint32_t n0, n1;
     int row0;
     uint32_t rbytes, bbytes;
-    int tasks, lane, mats;
+    int tasks, lane, mats, units;
     bool swiglu;
 
     template <int S, bool Q4>
@@ -472,7 +470,8 @@ struct UnitMap {
         const bool second = swiglu && ((u / S) & 1);
         const int row = row0 + u / (S * mats);
         const int t = 64 * step + lane;
-        const uint32_t off = t < tasks ? (uint32_t)row * rbytes + (uint32_t)(t >> 2) * bbytes : kOob;
+        const uint32_t off =
+            t < tasks && u < units ? (uint32_t)row * rbytes + (uint32_t)(t >> 2) * bbytes : kOob;
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t *>(second ? w1 : w0), (short)0, (int)(second ? n1 : n0), 0x00020000);
         if constexpr (Q4) return load_q4(rs, off, t & 3);
@@ -528,7 +527,7 @@ __device__ __forceinline__ void argmax_publish(const MvArgs &a, unsigned long lo
 // Q4 (the work group's weight dtype) is a template parameter so that every
 // load writes its final registers (a load feeding a merge of two paths would
 // be copied, and the copy waits for the load).
-template <int S, int D0, bool Q4, bool AMAX, bool NE>
+template <int S, int D4, int D6, bool ONE, bool Q4, bool AMAX, bool NE>
 __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, const MvOut &ob,
                                             int row0, int nrow, ActSmem &sm) {
     const int lane = threadIdx.x & 63;
@@ -539,67 +538,100 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
     const uint32_t bbytes = Q4 ? kQ4Bytes : kQ6Bytes;
     const uint32_t rbytes = (uint32_t)nb * bbytes;
     const UnitMap um{o0.w, ob.w, rbytes * (uint32_t)o0.n_rows, rbytes * (uint32_t)ob.n_rows, row0,
-                     rbytes, bbytes, tasks, lane, mats, swiglu};
+                     rbytes, bbytes, tasks, lane, mats, units, swiglu};
 
-    constexpr int D = Q4 ? D0 : 2;            // units in flight (Q6_K fragments are larger)
+    constexpr int D = Q4 ? D4 : D6;           // units in flight per dtype
     constexpr int NBW = S == 1 ? 4 : 4 * S;   // n_in <= 4096 / 12288
     ActRegs<NBW, NE> ar;
     act_load(ar, a.x, a.n_in, a.norm_w, a.ada);
     using Frag = std::conditional_t<Q4, FragQ4, FragQ6>;
+    // Every weight load is unconditional (units past the end read zeros):
+    // a load issued on one path only makes the compiler's wait counts assume
+    // it absent, and the input quantization then waited for all of them.
+    // The loads stay in unit order (scheduling barriers): the unit loop's
+    // waits hold for its first pass too, and a unit requested last there
+    // made every pass wait for all of them.
     Frag f[D];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int k = 0; k < D; ++k)
-        if (k < units) f[k] = um.load<S, Q4>(k);
+    for (int k = 0; k < D; ++k) {
+        f[k] = um.load<S, Q4>(k);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // The residual of the wave's rows (lane l: row row0 + l; a wave has at
+    // most 64 rows), requested up front: loaded at a row's end it waited for
+    // every weight load in flight.  Without a residual it reads y, unused.
+    const float *ap = o0.add ? o0.add : o0.y;
+    const float addv = ap[min(row0 + min(lane, max(nrow - 1, 0)), o0.n_rows - 1)];
+    __builtin_amdgcn_sched_barrier(0);
     act_finish(ar, a.n_in, a.norm_w, a.ada, a.eps, sm, nullptr);
 
     const XFrag xr = xfrag(sm, Q4, min(lane, tasks - 1));   // the only step when S == 1
 
     float acc = 0.0f, first = 0.0f;
     unsigned long long best = 0;   // argmax key: order key of the value << 32 | row
-    for (int u0 = 0; u0 < units; u0 += D) {
-#pragma unroll
-        for (int k = 0; k < D; ++k) {
-            const int u = u0 + k;
-            if (u >= units) break;
-            const Frag cur = f[k];
-            if (u + D < units) f[k] = um.load<S, Q4>(u + D);
-            const int step = u % S, m = swiglu ? (u / S) & 1 : 0;
-            const int row = row0 + u / (S * mats);
-            const int t = 64 * step + lane;
-            const XFrag xf = S == 1 ? xr : xfrag(sm, Q4, min(t, tasks - 1));
-            float c;
-            if constexpr (Q4) {
-                c = compute_q4(cur, xf, t & 3);
-            } else {
-                // Q6_K block (row, b) starts at 210 (row nb + b): 2 mod 4 when odd
-                const uint32_t mis = 2u * (uint32_t)((row * nb + (t >> 2)) & 1);
-                c = compute_q6(cur, xf, mis, t & 1);
-            }
-            acc += t < tasks ? c : 0.0f;
-            if (step == S - 1) {
-                const float r = wave_sum(acc);
-                acc = 0.0f;
-                if (!swiglu) {
-                    const float yv = a.gelu ? gelu_erf(r) : o0.add ? o0.add[row] + r : r;
-                    if (lane == 0) o0.y[row] = yv;
-                    if constexpr (AMAX) {
-                        const uint32_t b = __builtin_bit_cast(uint32_t, yv);
-                        const uint32_t ok = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-                        const unsigned long long key = ((unsigned long long)ok << 32) | (uint32_t)row;
-                        best = key > best ? key : best;
-                    }
-                } else if (m == 0) {
-                    first = r;
-                } else if (lane == 0) {
-                    o0.y[row] = silu(first) * r;
+    // unit u (fragment fr): its share of the row's sum, and the row's end
+    auto unit = [&](const Frag &fr, int u) __attribute__((always_inline)) {
+        const int step = u % S, m = swiglu ? (u / S) & 1 : 0;
+        const int row = row0 + u / (S * mats);
+        const int t = 64 * step + lane;
+        const XFrag xf = S == 1 ? xr : xfrag(sm, Q4, min(t, tasks - 1));
+        float c;
+        if constexpr (Q4) {
+            c = compute_q4(fr, xf, t & 3);
+        } else {
+            // Q6_K block (row, b) starts at 210 (row nb + b): 2 mod 4 when odd
+            const uint32_t mis = 2u * (uint32_t)((row * nb + (t >> 2)) & 1);
+            c = compute_q6(fr, xf, mis, t & 1);
+        }
+        acc += t < tasks ? c : 0.0f;
+        if (step == S - 1 && u < units) {
+            const float r = wave_sum(acc);
+            acc = 0.0f;
+            if (!swiglu) {
+                const float res = __builtin_bit_cast(
+                    float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, addv), u / (S * mats)));
+                const float yv = a.gelu ? gelu_erf(r) : o0.add ? res + r : r;
+                if (lane == 0) o0.y[row] = yv;
+                if constexpr (AMAX) {
+                    const uint32_t b = __builtin_bit_cast(uint32_t, yv);
+                    const uint32_t ok = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+                    const unsigned long long key = ((unsigned long long)ok << 32) | (uint32_t)row;
+                    best = key > best ? key : best;
                 }
+            } else if (m == 0) {
+                first = r;
+            } else if (lane == 0) {
+                o0.y[row] = silu(first) * r;
+            }
+        }
+    };
+    if constexpr (ONE) {
+        // every unit was requested above (the launch checked units <= D):
+        // no refills, and each unit waits for its own loads only
+#pragma unroll
+        for (int k = 0; k < D; ++k)
+            if (k < units) unit(f[k], k);
+    } else {
+        for (int u0 = 0; u0 < units; u0 += D) {
+#pragma unroll
+            for (int k = 0; k < D; ++k) {
+                unit(f[k], u0 + k);
+                // the next load into this slot once its fragment is consumed,
+                // so it can write the slot's own registers (a load into other
+                // registers is copied back at the loop's end, and the copy
+                // waits for it)
+                f[k] = um.load<S, Q4>(u0 + k + D);
             }
         }
     }
     if constexpr (AMAX) argmax_publish(a, best);
 }
 
-template <int S, int D, bool AMAX>
+// D4 / D6: a wave's units in flight for Q4_K / Q6_K rows; ONE: every wave's
+// units fit (the launch picks it from the units per wave, so that a decoder
+// product's wave requests all its weights at once and streams nothing).
+template <int S, int D4, int D6, bool ONE, bool AMAX>
 __global__ void __launch_bounds__(256) k_matvec(MvArgs a) {
     __shared__ ActSmem sm;
     // wave-uniform (readfirstlane): the row range and the unit loop follow
@@ -616,11 +648,11 @@ __global__ void __launch_bounds__(256) k_matvec(MvArgs a) {
     // With a norm (S == 1: the inputs of up to 4096), its weights (and the ada
     // row) are requested together with x, so the norm costs one round trip.
     if (S == 1 && a.norm_w) {
-        if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D, true, AMAX, true>(a, o0, ob, row0, nrow, sm);
-        else matvec_body<S, D, false, AMAX, true>(a, o0, ob, row0, nrow, sm);
+        if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D4, D6, ONE, true, AMAX, true>(a, o0, ob, row0, nrow, sm);
+        else matvec_body<S, D4, D6, ONE, false, AMAX, true>(a, o0, ob, row0, nrow, sm);
     } else {
-        if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D, true, AMAX, false>(a, o0, ob, row0, nrow, sm);
-        else matvec_body<S, D, false, AMAX, false>(a, o0, ob, row0, nrow, sm);
+        if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D4, D6, ONE, true, AMAX, false>(a, o0, ob, row0, nrow, sm);
+        else matvec_body<S, D4, D6, ONE, false, AMAX, false>(a, o0, ob, row0, nrow, sm);
     }
 }
 
@@ -1444,10 +1476,24 @@ hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st) {
     const int S = (a.n_in / 256 * 4 + 63) / 64;
     // the fused argmax only serves the logits (one step per row)
     if (a.amax && S != 1) return hipErrorInvalidValue;
-    if (a.amax) k_matvec<1, 3, true><<<n_wg, 256, 0, st>>>(a);
-    else if (S == 1) k_matvec<1, 3, false><<<n_wg, 256, 0, st>>>(a);
-    else if (S == 2) k_matvec<2, 2, false><<<n_wg, 256, 0, st>>>(a);
-    else k_matvec<3, 2, false><<<n_wg, 256, 0, st>>>(a);
+    // A wave's units: its rows x steps x (2 under SwiGLU).  When they fit in
+    // one request for every dtype of the call (6 Q4_K or 3 Q6_K units: the
+    // decoder's products), the wave requests them all up front; otherwise 3
+    // Q4_K / 2 Q6_K units stream.
+    const int units = (a.rows_per_wg >> 2) * S * (a.swiglu ? 2 : 1);
+    bool q4 = false, q6 = false;
+    for (int k = 0; k < a.n_outs; ++k) (a.out[k].dtype == VKV_DTYPE_Q4_K ? q4 : q6) = true;
+    auto fits = [&](int d4, int d6) { return (!q4 || units <= d4) && (!q6 || units <= d6); };
+    const bool one = fits(6, 3);
+    if (a.amax) k_matvec<1, 3, 2, false, true><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 1 && fits(3, 2)) k_matvec<1, 3, 2, true, false><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 1 && one) k_matvec<1, 6, 3, true, false><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 1) k_matvec<1, 3, 2, false, false><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 2 && fits(2, 2)) k_matvec<2, 2, 2, true, false><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 2 && one) k_matvec<2, 6, 3, true, false><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 2) k_matvec<2, 2, 2, false, false><<<n_wg, 256, 0, st>>>(a);
+    else if (one) k_matvec<3, 6, 3, true, false><<<n_wg, 256, 0, st>>>(a);
+    else k_matvec<3, 2, 2, false, false><<<n_wg, 256, 0, st>>>(a);
     return hipGetLastError();
 }
 
