@@ -1322,6 +1322,25 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
     for (int c = 0; c < CT; ++c)
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[c][i] = 0.0f;
+    // The epilogue's inputs (residual, biases), requested before the blocks:
+    // loaded at the end they waited for a memory round trip of their own.
+    // A thread has at most one output (ot = its index: column tile, input
+    // row, row); indices clamp into the matrix and absent vectors read y
+    // (unused), so the loads are unconditional.
+    static_assert(64 * W >= 256 * CT, "one output per thread");
+    const int ot = threadIdx.x;
+    const int ot_r = ot & 15, ot_row = min(row0 + ot_r, o0.n_rows - 1);
+    const int ot_col = min(col0 + 16 * (ot >> 8) + ((ot >> 4) & 15), a.n_cols - 1);
+    const int64_t ot_at =
+        (int64_t)(a.y_ring > 0 ? (a.y_row0 + ot_col) % a.y_ring : ot_col) * o0.n_rows + ot_row;
+    const float e_b0 = (o0.bias ? o0.bias : o0.y)[ot_row];
+    // the second input: W3's bias (SwiGLU), the pair row's bias (RoPE) or
+    // the residual
+    const float *e2p = swiglu ? (o1.bias ? o1.bias : o0.y)
+                       : o0.rope ? (o0.bias ? o0.bias : o0.y)
+                                 : (o0.add ? o0.add : o0.y);
+    const int64_t e2i = swiglu ? ot_row : o0.rope ? min(row0 + (ot_r ^ 1), o0.n_rows - 1) : ot_at;
+    const float e_2 = e2p[e2i];
     // the wave's blocks b, b + kw, b + 2 kw, ...: one block's fragments at a
     // time (occupancy, not a second register set, covers the load latency);
     // the first block's (w_first) were requested by the caller
@@ -1353,20 +1372,18 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
 #pragma unroll
         for (int i = 0; i < 4; ++i) red[c][wave][4 * kg + i][rr] = acc[c][i];
     __syncthreads();
-    // outputs: 16 consecutive rows per input row
-    for (int idx = threadIdx.x; idx < 256 * n_ct; idx += 64 * W) {
-        const int ct = idx >> 8, c = (idx >> 4) & 15, r = idx & 15;
+    // outputs: 16 consecutive rows per input row, one per thread
+    if (ot < 256 * n_ct) {
+        const int ct = ot >> 8, c = (ot >> 4) & 15, r = ot & 15;
         const int orow = row0 + r, ocol = col0 + 16 * ct + c;
         if (orow < o0.n_rows && ocol < a.n_cols) {
             float v0 = 0.0f, v1 = 0.0f;
             for (int w = 0; w < kw; ++w) v0 += red[ct][w][r][c];
-            if (o0.bias) v0 = v0 + o0.bias[orow];
-            const int64_t at =
-                (int64_t)(a.y_ring > 0 ? (a.y_row0 + ocol) % a.y_ring : ocol) * o0.n_rows + orow;
+            if (o0.bias) v0 = v0 + e_b0;
             float y;
             if (swiglu) {
                 for (int w = 0; w < kw; ++w) v1 += red[ct][kw + w][r][c];
-                if (o1.bias) v1 = v1 + o1.bias[orow];
+                if (o1.bias) v1 = v1 + e_2;
                 y = silu(v0) * v1;
             } else if (a.gelu) {
                 y = gelu_erf(v0);
@@ -1375,13 +1392,13 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
                 const int pr = r ^ 1;
                 float vp = 0.0f;
                 for (int w = 0; w < kw; ++w) vp += red[ct][w][pr][c];
-                if (o0.bias) vp = vp + o0.bias[row0 + pr];
+                if (o0.bias) vp = vp + e_2;
                 y = rope_elem(v0, vp, (orow & 1) != 0, (orow % a.rope_hd) >> 1,
                               (float)(a.rope_pos0 + ocol), a.rope_ts);
             } else {
-                y = o0.add ? o0.add[at] + v0 : v0;
+                y = o0.add ? e_2 + v0 : v0;
             }
-            o0.y[at] = y;
+            o0.y[ot_at] = y;
         }
     }
 }
