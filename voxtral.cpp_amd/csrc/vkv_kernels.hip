@@ -738,9 +738,10 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
                           __attribute__((always_inline)) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            // past the chunk end: reload the last valid slot (masked later)
+            // past the chunk end: reload the last valid slot (masked later);
+            // an empty chunk reads slot 0 (unused)
             const int ix = min(b + u * 4 + grp, i_end - 1);
-            const int slot = slot_of(sp, ix);
+            const int slot = i_begin < i_end ? slot_of(sp, ix) : 0;
             // slot < 2^24 and row_bytes < 2^24 (host-checked): 24-bit multiply
             const uint32_t off = __umul24((uint32_t)slot, row_bytes24);
             kf[u] = F::template load<true>(kl + off, e);
@@ -767,13 +768,15 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
     if (a.rope && a.rope_host) rp = rope_pairs_host(a, 4 * c);
 
     // The first batches are requested before the prologue (RoPE table, Q,
-    // fused append) whenever none of them can hold the step's new row, the
-    // newest logical index n_kv-1; clamped indices then stay below it too.
+    // fused append), unconditionally: a load issued on one path only makes
+    // the compiler's wait counts assume it absent, and Q's RoPE then waited
+    // for the whole first batch, so the second was requested only after it
+    // had arrived.  A work group whose first batches can hold the step's new
+    // row (the newest logical index n_kv-1, not yet appended) requests them
+    // again after the append.
     const bool early = !FUSE || i_begin + (NS - 1) * kStep <= n_kv - 1;
-    if (early && i_begin < i_end) {   // i_end >= 1: every clamped index is a valid slot
 #pragma unroll
-        for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
-    }
+    for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
     __shared__ float2 sm_rope[64];
     if (a.rope && !a.rope_host) {
         decode_rope_table(sm_rope, a, s);
@@ -866,7 +869,7 @@ __global__ void __launch_bounds__(W * 64) k_decode(DecodeArgs a) {
     // handles NS batches and the prefetches are unconditional (indices clamp
     // to the last valid slot, an L2 hit; batches past the end are fully
     // masked), so the wait counts stay exact.
-    if (!early && i_begin < i_end) {
+    if (!early && i_begin < i_end) {   // the first batches again, after the append
 #pragma unroll
         for (int p = 0; p < NS - 1; ++p) load_batch(b0 + p * kStep, kf[p], vf[p]);
     }
