@@ -1902,51 +1902,24 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
     __shared__ float sm_o[4][16][D + 1];
     __shared__ float sm_m[4][16], sm_l[4][16];
 
-    // Fused ring write (the encoder step's and the prefill's append): this
-    // work group converts kv head g's part of the n_new new rows (F16 RNE)
-    // and stores them through the write segments; the barrier makes them
-    // visible to its waves, which attend them like any other key.  Several
-    // tiles of one head (GQA prefill) store identical bytes.
-    if (a.k_new) {
-        const int kv_dim = a.n_kv_heads * D;
-        const int64_t src0 = (int64_t)layer * a.n_new * kv_dim;
-        uint8_t *kw = a.k_w + (int64_t)layer * a.layer_bytes;
-        uint8_t *vw = a.v_w + (int64_t)layer * a.layer_bytes;
-        for (int t = threadIdx.x; t < a.n_new * (D / 8); t += 256) {
-            const int row = t / (D / 8);
-            const int col = g * D + (t % (D / 8)) * 8;
-            const int64_t so = src0 + (int64_t)row * kv_dim + col;
-            const int64_t dst = (int64_t)slot_of(a.wseg, row) * a.row_bytes;
-            float xk[8], xv[8];
-            const float4 k0 = reinterpret_cast<const float4 *>(a.k_new + so)[0];
-            const float4 k1 = reinterpret_cast<const float4 *>(a.k_new + so)[1];
-            const float4 v0 = reinterpret_cast<const float4 *>(a.v_new + so)[0];
-            const float4 v1 = reinterpret_cast<const float4 *>(a.v_new + so)[1];
-            xk[0] = k0.x; xk[1] = k0.y; xk[2] = k0.z; xk[3] = k0.w;
-            xk[4] = k1.x; xk[5] = k1.y; xk[6] = k1.z; xk[7] = k1.w;
-            xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
-            xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
-            FmtF16::store(kw + dst, col, FmtF16::from_f32(xk));
-            FmtF16::store(vw + dst, col, FmtF16::from_f32(xv));
-        }
-        __syncthreads();
-    }
-
     // ---- Q^T operand: lane holds row lr, dims [DL*lg, DL*lg + DL) as f16 ----
     const int row = tile * 16 + lr;
     const bool row_ok = row < n_rows;
     const int tok = row_ok ? row / gqa : 0;
     const int64_t q_abs = a.q_pos0 + tok;
-    half4_t qb[KB];
+    // Q first (rows past the tile's last read a valid row, unused), then the
+    // wave's first key block, then the fused ring write: every request is
+    // unconditional and in the order it is waited for, so the three first
+    // touches of the launch are in flight together (one after another they
+    // were three round trips before the first product).
+    float4 qraw[KB];
     {
         const float *qp = a.q + (int64_t)layer * a.q_lstride +
                           ((int64_t)tok * a.n_q_heads + g * gqa + (row_ok ? row % gqa : 0)) * D + DL * lg;
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-            const float4 v4 = row_ok ? reinterpret_cast<const float4 *>(qp)[kb] : make_float4(0, 0, 0, 0);
-            qb[kb] = half4_t{(_Float16)v4.x, (_Float16)v4.y, (_Float16)v4.z, (_Float16)v4.w};
-        }
+        for (int kb = 0; kb < KB; ++kb) qraw[kb] = reinterpret_cast<const float4 *>(qp)[kb];
     }
+    half4_t qb[KB];   // Q as f16, formed after the ring write
 
     // ---- the key range any row of this tile may attend ----
     const int row0 = tile * 16;
@@ -1970,7 +1943,8 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
                        __attribute__((always_inline)) {
         // K and V of key jb+lr, dims [DL*lg, +DL): one contiguous run per lane
         const int jk = max(min(jb + lr, j_hi - 1), j_lo);
-        const uint32_t off = (uint32_t)slot_of(a.seg, jk) * (uint32_t)a.row_bytes +
+        // an empty key range reads slot 0 (unused)
+        const uint32_t off = (uint32_t)(j_lo < j_hi ? slot_of(a.seg, jk) : 0) * (uint32_t)a.row_bytes +
                              (uint32_t)(g * D + DL * lg) * 2u;
 #pragma unroll
         for (int t = 0; t < DL / 8; ++t) {
@@ -2053,7 +2027,46 @@ __global__ void __launch_bounds__(256) k_window_mfma(WindowArgs a) {
     // row meets its keys in the same blocks, waves and order under every
     // chunking of the stream (schedule-invariant results, bit for bit).
     int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & 63) + wave * 16;
-    if (j_lo < j_hi) load_kv(jb0, ka_, va_);   // j_lo < j_hi: clamped keys are valid
+    load_kv(jb0, ka_, va_);
+    // Fused ring write (the encoder step's and the prefill's append): this
+    // work group converts kv head g's part of the n_new new rows (F16 RNE)
+    // and stores them through the write segments; the barrier makes them
+    // visible to its waves, which attend them like any other key.  Several
+    // tiles of one head (GQA prefill) store identical bytes.  A wave whose
+    // first block holds a new row (the newest n_new keys) requests it again
+    // after the barrier.
+    if (a.k_new) {
+        const int kv_dim = a.n_kv_heads * D;
+        const int64_t src0 = (int64_t)layer * a.n_new * kv_dim;
+        uint8_t *kw = a.k_w + (int64_t)layer * a.layer_bytes;
+        uint8_t *vw = a.v_w + (int64_t)layer * a.layer_bytes;
+        for (int t = threadIdx.x; t < a.n_new * (D / 8); t += 256) {
+            const int row = t / (D / 8);
+            const int col = g * D + (t % (D / 8)) * 8;
+            const int64_t so = src0 + (int64_t)row * kv_dim + col;
+            const int64_t dst = (int64_t)slot_of(a.wseg, row) * a.row_bytes;
+            float xk[8], xv[8];
+            const float4 k0 = reinterpret_cast<const float4 *>(a.k_new + so)[0];
+            const float4 k1 = reinterpret_cast<const float4 *>(a.k_new + so)[1];
+            const float4 v0 = reinterpret_cast<const float4 *>(a.v_new + so)[0];
+            const float4 v1 = reinterpret_cast<const float4 *>(a.v_new + so)[1];
+            xk[0] = k0.x; xk[1] = k0.y; xk[2] = k0.z; xk[3] = k0.w;
+            xk[4] = k1.x; xk[5] = k1.y; xk[6] = k1.z; xk[7] = k1.w;
+            xv[0] = v0.x; xv[1] = v0.y; xv[2] = v0.z; xv[3] = v0.w;
+            xv[4] = v1.x; xv[5] = v1.y; xv[6] = v1.z; xv[7] = v1.w;
+            FmtF16::store(kw + dst, col, FmtF16::from_f32(xk));
+            FmtF16::store(vw + dst, col, FmtF16::from_f32(xv));
+        }
+        __syncthreads();
+    }
+
+    // (its largest index read: clamped into [j_lo, j_hi))
+    if (a.k_new && max(j_lo, min(jb0 + 15, j_hi - 1)) >= n_keys - a.n_new) load_kv(jb0, ka_, va_);
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+        const float4 v4 = row_ok ? qraw[kb] : make_float4(0, 0, 0, 0);
+        qb[kb] = half4_t{(_Float16)v4.x, (_Float16)v4.y, (_Float16)v4.z, (_Float16)v4.w};
+    }
     for (; jb0 < j_hi; jb0 += 128) {
         load_kv(jb0 + 64, kb_, vb_);
         process(ka_, va_, jb0);
@@ -2134,38 +2147,23 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
     __shared__ float sm_o[4][16][D + 1];
     __shared__ float sm_m[4][16], sm_l[4][16];
 
-    // Fused ring write of kv head g's part of the n_new new rows.
-    if (a.k_new) {
-        const int kv_dim = a.n_kv_heads * D;
-        const int64_t src0 = (int64_t)layer * a.n_new * kv_dim;
-        uint8_t *kw = a.k_w + (int64_t)layer * a.layer_bytes;
-        uint8_t *vw = a.v_w + (int64_t)layer * a.layer_bytes;
-        for (int t = threadIdx.x; t < a.n_new * (D / 4); t += 256) {
-            const int row = t / (D / 4);
-            const int col = g * D + (t % (D / 4)) * 4;
-            const int64_t so = src0 + (int64_t)row * kv_dim + col;
-            const int64_t dst = (int64_t)slot_of(a.wseg, row) * a.row_bytes + (int64_t)col * 4;
-            *reinterpret_cast<float4 *>(kw + dst) = *reinterpret_cast<const float4 *>(a.k_new + so);
-            *reinterpret_cast<float4 *>(vw + dst) = *reinterpret_cast<const float4 *>(a.v_new + so);
-        }
-        __syncthreads();
-    }
-
     // ---- Q^T operand: lane holds row lr, dims [DL lg, DL lg + DL) ----
     const int row = tile * 16 + lr;
     const bool row_ok = row < n_rows;
     const int tok = row_ok ? row / gqa : 0;
     const int64_t q_abs = a.q_pos0 + tok;
-    float qf[DL];
+    // Q first (rows past the tile's last read a valid row, unused), then the
+    // wave's first key block, then the fused ring write: every request is
+    // unconditional and in the order it is waited for, so the three first
+    // touches of the launch are in flight together.
+    float4 qraw[DL / 4];
     {
         const float *qp = a.q + (int64_t)layer * a.q_lstride +
                           ((int64_t)tok * a.n_q_heads + g * gqa + (row_ok ? row % gqa : 0)) * D + DL * lg;
 #pragma unroll
-        for (int t = 0; t < DL / 4; ++t) {
-            const float4 v4 = row_ok ? reinterpret_cast<const float4 *>(qp)[t] : make_float4(0, 0, 0, 0);
-            qf[4 * t] = v4.x; qf[4 * t + 1] = v4.y; qf[4 * t + 2] = v4.z; qf[4 * t + 3] = v4.w;
-        }
+        for (int t = 0; t < DL / 4; ++t) qraw[t] = reinterpret_cast<const float4 *>(qp)[t];
     }
+    float qf[DL];   // formed after the ring write
 
     // ---- the key range any row of this tile may attend ----
     const int row0 = tile * 16;
@@ -2187,7 +2185,8 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
     // indices clamp into [j_lo, j_hi) (keys outside it are masked)
     auto load_kv = [&](int jb, float4 (&kr)[DL / 4], float4 (&vr)[DL / 4]) __attribute__((always_inline)) {
         const int jk = max(min(jb + lr, j_hi - 1), j_lo);
-        const uint32_t off = (uint32_t)slot_of(a.seg, jk) * (uint32_t)a.row_bytes +
+        // an empty key range reads slot 0 (unused)
+        const uint32_t off = (uint32_t)(j_lo < j_hi ? slot_of(a.seg, jk) : 0) * (uint32_t)a.row_bytes +
                              (uint32_t)(g * D + DL * lg) * 4u;
 #pragma unroll
         for (int t = 0; t < DL / 4; ++t) {
@@ -2262,7 +2261,32 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
     // row meets its keys in the same blocks, waves and order under every
     // chunking of the stream (schedule-invariant results, bit for bit).
     int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & 63) + wave * 16;
-    if (j_lo < j_hi) load_kv(jb0, ka_, va_);   // j_lo < j_hi: clamped keys are valid
+    load_kv(jb0, ka_, va_);
+    // Fused ring write of kv head g's part of the n_new new rows.  A wave
+    // whose first block holds a new row (the newest n_new keys; its largest
+    // index read, clamped into [j_lo, j_hi)) requests it again after it.
+    if (a.k_new) {
+        const int kv_dim = a.n_kv_heads * D;
+        const int64_t src0 = (int64_t)layer * a.n_new * kv_dim;
+        uint8_t *kw = a.k_w + (int64_t)layer * a.layer_bytes;
+        uint8_t *vw = a.v_w + (int64_t)layer * a.layer_bytes;
+        for (int t = threadIdx.x; t < a.n_new * (D / 4); t += 256) {
+            const int row = t / (D / 4);
+            const int col = g * D + (t % (D / 4)) * 4;
+            const int64_t so = src0 + (int64_t)row * kv_dim + col;
+            const int64_t dst = (int64_t)slot_of(a.wseg, row) * a.row_bytes + (int64_t)col * 4;
+            *reinterpret_cast<float4 *>(kw + dst) = *reinterpret_cast<const float4 *>(a.k_new + so);
+            *reinterpret_cast<float4 *>(vw + dst) = *reinterpret_cast<const float4 *>(a.v_new + so);
+        }
+        __syncthreads();
+    }
+
+    if (a.k_new && max(j_lo, min(jb0 + 15, j_hi - 1)) >= n_keys - a.n_new) load_kv(jb0, ka_, va_);
+#pragma unroll
+    for (int t = 0; t < DL / 4; ++t) {
+        const float4 v4 = row_ok ? qraw[t] : make_float4(0, 0, 0, 0);
+        qf[4 * t] = v4.x; qf[4 * t + 1] = v4.y; qf[4 * t + 2] = v4.z; qf[4 * t + 3] = v4.w;
+    }
     for (; jb0 < j_hi; jb0 += 128) {
         load_kv(jb0 + 64, kb_, vb_);
         process(ka_, va_, jb0);
