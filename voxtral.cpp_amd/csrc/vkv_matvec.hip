@@ -1496,16 +1496,17 @@ hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st) {
     // A wave's units: its rows x steps x (2 under SwiGLU).  When they fit in
     // one request for every dtype of the call (6 Q4_K or 3 Q6_K units: the
     // decoder's products), the wave requests them all up front; otherwise 3
-    // Q4_K / 2 Q6_K units stream.
+    // Q4_K / 2 Q6_K units stream, single-step rows (the 131072-row logits)
+    // 3 / 4 (Q6_K 2, 3, 5, 6: 0.2-1.2% slower per token).
     const int units = (a.rows_per_wg >> 2) * S * (a.swiglu ? 2 : 1);
     bool q4 = false, q6 = false;
     for (int k = 0; k < a.n_outs; ++k) (a.out[k].dtype == VKV_DTYPE_Q4_K ? q4 : q6) = true;
     auto fits = [&](int d4, int d6) { return (!q4 || units <= d4) && (!q6 || units <= d6); };
     const bool one = fits(6, 3);
-    if (a.amax) k_matvec<1, 3, 2, false, true><<<n_wg, 256, 0, st>>>(a);
+    if (a.amax) k_matvec<1, 3, 4, false, true><<<n_wg, 256, 0, st>>>(a);
     else if (S == 1 && fits(3, 2)) k_matvec<1, 3, 2, true, false><<<n_wg, 256, 0, st>>>(a);
     else if (S == 1 && one) k_matvec<1, 6, 3, true, false><<<n_wg, 256, 0, st>>>(a);
-    else if (S == 1) k_matvec<1, 3, 2, false, false><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 1) k_matvec<1, 3, 4, false, false><<<n_wg, 256, 0, st>>>(a);
     else if (S == 2 && fits(2, 2)) k_matvec<2, 2, 2, true, false><<<n_wg, 256, 0, st>>>(a);
     else if (S == 2 && one) k_matvec<2, 6, 3, true, false><<<n_wg, 256, 0, st>>>(a);
     else if (S == 2) k_matvec<2, 2, 2, false, false><<<n_wg, 256, 0, st>>>(a);
