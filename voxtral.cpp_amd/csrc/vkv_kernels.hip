@@ -1712,14 +1712,17 @@ __global__ void __launch_bounds__(128) k_combine(CombineArgs a) {
     const float *po = a.part_o + p0 * a.head_dim + t;
     const int n = a.n_chunks;
     if (n <= kCombineRegs) {
-        // One round trip: every partial of this thread's dimension is
-        // requested together with the chunk maxima and sums (they do not
-        // depend on each other), then weighted once the maximum is known.
+        // One round trip: the chunk maxima and sums are requested first,
+        // then every partial of this thread's dimension, all unconditionally
+        // (indices clamp to the last chunk; a load merged with a value of
+        // another path is waited for at once), so the two reductions run
+        // while the partials are in flight.
+        const float mc0 = ml[2 * min(t, n - 1)], lc0 = ml[2 * min(t, n - 1) + 1];
         float v[kCombineRegs];
 #pragma unroll
-        for (int c = 0; c < kCombineRegs; ++c) v[c] = c < n ? po[(int64_t)c * a.head_dim] : 0.0f;
-        const float mc = t < n ? ml[2 * t] : -INFINITY;
-        const float lc = t < n ? ml[2 * t + 1] : 0.0f;
+        for (int c = 0; c < kCombineRegs; ++c) v[c] = po[(int64_t)min(c, n - 1) * a.head_dim];
+        const float mc = t < n ? mc0 : -INFINITY;
+        const float lc = t < n ? lc0 : 0.0f;
         float m = mc;
         for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
         if (lane == 0) red[0][wave] = m;
