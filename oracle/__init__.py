@@ -104,8 +104,12 @@ _protos = {
                                    _i32, _f64, _vp]),
     "orc_decode_attn_mimic": (None, [ctypes.c_int, _vp, _vp, _i64, _vp, _i32, _vp, _i32, _i32,
                                      _i32, _f32, _vp]),
+    "orc_decode_attn_mimic_acc32": (None, [ctypes.c_int, _vp, _vp, _i64, _vp, _i32, _vp, _i32,
+                                           _i32, _i32, _f32, _vp]),
     "orc_window_attn_f64": (None, [ctypes.c_int, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp, _i32,
                                    _i32, _i32, _i32, _i32, _f64, _vp]),
+    "orc_window_attn_mimic": (_i32, [ctypes.c_int, _vp, _vp, _i64, _vp, _vp, _i32, _i32, _vp, _vp,
+                                     _i32, _i32, _i32, _i32, _i32, _f32, ctypes.c_int, _vp]),
     "orc_q4_k_dequantize": (None, [_vp, _vp, _i64]),
     "orc_q6_k_dequantize": (None, [_vp, _vp, _i64]),
     "orc_q8_k_quantize": (None, [_vp, _vp, _i64]),
@@ -325,6 +329,44 @@ def decode_attn_mimic(dtype, k_img, v_img, row_b, slots, q, n_kv_heads, head_dim
     lib.orc_decode_attn_mimic(dtype, _ptr(k_img), _ptr(v_img), row_b, _ptr(slots), slots.size,
                               _ptr(q), n_q_heads, n_kv_heads, head_dim, scale, _ptr(out))
     return out.reshape(n_q_heads, head_dim)
+
+
+def decode_attn_mimic_acc32(dtype, k_img, v_img, row_b, slots, q, n_kv_heads, head_dim, scale):
+    """the mimic with an f32 V accumulator: every other rounding of ggml's CPU
+    flash attention kept"""
+    slots = np.ascontiguousarray(slots, dtype=np.int32)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n_q_heads = q.size // head_dim
+    out = np.empty(n_q_heads * head_dim, dtype=np.float32)
+    lib.orc_decode_attn_mimic_acc32(dtype, _ptr(k_img), _ptr(v_img), row_b, _ptr(slots),
+                                    slots.size, _ptr(q), n_q_heads, n_kv_heads, head_dim, scale,
+                                    _ptr(out))
+    return out.reshape(n_q_heads, head_dim)
+
+
+def window_attn_mimic(dtype, k_img, v_img, row_b, k_slot, k_pos, q, q_pos, n_q_heads,
+                      n_kv_heads, head_dim, window, scale, new_start=None, flash=None):
+    """orc_window_attn_f64's function in the reference encoder's ggml CPU
+    arithmetic (segmented below 32 query rows, flash from 32 unless `flash`
+    says otherwise); keys in logical order, the block's new rows from key
+    index new_start (default: the first key at or past the first query)"""
+    k_slot = np.ascontiguousarray(k_slot, dtype=np.int32)
+    k_pos = np.ascontiguousarray(k_pos, dtype=np.int64)
+    q_pos = np.ascontiguousarray(q_pos, dtype=np.int64)
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    n_q = q_pos.size
+    if new_start is None:
+        new_start = int(np.searchsorted(k_pos, q_pos.min())) if n_q else k_slot.size
+    if flash is None:
+        flash = n_q >= 32
+    out = np.empty(n_q * n_q_heads * head_dim, dtype=np.float32)
+    st = lib.orc_window_attn_mimic(dtype, _ptr(k_img), _ptr(v_img), row_b, _ptr(k_slot),
+                                   _ptr(k_pos), k_slot.size, new_start, _ptr(q), _ptr(q_pos), n_q,
+                                   n_q_heads, n_kv_heads, head_dim, window, scale, int(flash),
+                                   _ptr(out))
+    if st != 0:
+        raise ValueError("window_attn_mimic: F16 and F32 rings only")
+    return out.reshape(n_q, n_q_heads, head_dim)
 
 
 def window_attn_f64(dtype, k_img, v_img, row_b, k_slot, k_pos, q, q_pos, n_q_heads, n_kv_heads,

@@ -16,10 +16,26 @@
  *                          online softmax, and an F16 V is accumulated in f16.
  *                          ggml is not vendored (CMakeLists.txt:81-95), so this
  *                          reduction order is restated, not imported.
+ * orc_decode_attn_mimic_acc32 -- orc_decode_attn_mimic with an f32 V
+ *                          accumulator: ggml's reduction with every rounding
+ *                          but the f16 accumulator (the one ggml applies to an
+ *                          F32 V, ggml_vec_mad_f32 into VKQ32).
  * orc_window_attn_f64   -- multi-query attention with the causal sliding-window
  *                          predicate of voxtral_enc_kv_mask_allows
  *                          (src/voxtral.cpp:3636-3638, mask build :4259-4279)
  *                          or the causal prefill mask (src/voxtral.cpp:3316-3323).
+ * orc_window_attn_mimic -- the same function in the arithmetic of the
+ *                          reference's encoder graph on ggml's CPU backend:
+ *                          below 32 query rows the segmented manual path
+ *                          (src/voxtral.cpp:2201-2284: ggml_mul_mat of each
+ *                          K segment with the query, which ggml converts to
+ *                          f16 for an F16 K; ggml_soft_max_ext in f32 at the
+ *                          scale with the -inf mask; ggml_mul_mat of each V^T
+ *                          segment with its slice of the weights, converted
+ *                          to f16 for an F16 V; the segments' f32 sums added
+ *                          in order), from 32 rows the flash path with the
+ *                          window gathered (:2285-2350), i.e. the decode
+ *                          mimic over each query's allowed keys.
  * orc_decode_step_mimic_mt -- the CPU baseline: one decode step of every layer
  *                          (append of the new K/V row, then attention over
  *                          slots [0, n_valid)) threaded over query heads within
@@ -108,7 +124,7 @@ static float orc_dot_q8_0(const uint8_t *kb, const uint8_t *qb, int32_t n) {
 static void orc_mimic_head(int dtype, const uint8_t *k_layer, const uint8_t *v_layer,
                            int64_t row_bytes, const int32_t *slots, int32_t n_slots,
                            int32_t first_slot, const float *qh, int32_t g, int32_t head_dim,
-                           float scale, float *oh) {
+                           float scale, int acc16, float *oh) {
     uint16_t qf16[512];
     uint8_t qq8[16 * 34];
     uint16_t vkq16[512];
@@ -138,7 +154,7 @@ static void orc_mimic_head(int dtype, const uint8_t *k_layer, const uint8_t *v_l
         if (s > M) {
             M = s;
             ms = expf(Mold - M);
-            if (dtype == ORC_F16) {
+            if (acc16) {
                 for (int32_t d = 0; d < head_dim; ++d)
                     vkq16[d] = orc_f32_to_f16(orc_f16_to_f32(vkq16[d]) * ms);
             } else {
@@ -147,7 +163,7 @@ static void orc_mimic_head(int dtype, const uint8_t *k_layer, const uint8_t *v_l
         } else {
             vs = expf(s - M);
         }
-        if (dtype == ORC_F16) {
+        if (acc16) {
             const uint16_t *vh = (const uint16_t *)vrow_p + (int64_t)g * head_dim;
             for (int32_t d = 0; d < head_dim; ++d)
                 vkq16[d] = orc_f32_to_f16(fmaf(orc_f16_to_f32(vh[d]), vs, orc_f16_to_f32(vkq16[d])));
@@ -157,7 +173,7 @@ static void orc_mimic_head(int dtype, const uint8_t *k_layer, const uint8_t *v_l
         }
         S = S * ms + vs;
     }
-    if (dtype == ORC_F16)
+    if (acc16)
         for (int32_t d = 0; d < head_dim; ++d) vkq32[d] = orc_f16_to_f32(vkq16[d]);
     float S_inv = S == 0.0f ? 0.0f : 1.0f / S;
     for (int32_t d = 0; d < head_dim; ++d) oh[d] = vkq32[d] * S_inv;
@@ -171,6 +187,17 @@ void orc_decode_attn_mimic(int dtype, const uint8_t *k_layer, const uint8_t *v_l
     for (int32_t h = 0; h < n_q_heads; ++h)
         orc_mimic_head(dtype, k_layer, v_layer, row_bytes, slots, n_slots, 0,
                        q + (int64_t)h * head_dim, h / group, head_dim, scale,
+                       dtype == ORC_F16, out + (int64_t)h * head_dim);
+}
+
+void orc_decode_attn_mimic_acc32(int dtype, const uint8_t *k_layer, const uint8_t *v_layer,
+                                 int64_t row_bytes, const int32_t *slots, int32_t n_slots,
+                                 const float *q, int32_t n_q_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, float scale, float *out) {
+    int32_t group = n_q_heads / n_kv_heads;
+    for (int32_t h = 0; h < n_q_heads; ++h)
+        orc_mimic_head(dtype, k_layer, v_layer, row_bytes, slots, n_slots, 0,
+                       q + (int64_t)h * head_dim, h / group, head_dim, scale, 0,
                        out + (int64_t)h * head_dim);
 }
 
@@ -212,6 +239,103 @@ void orc_window_attn_f64(int dtype, const uint8_t *k_layer, const uint8_t *v_lay
     }
     free(kr);
     free(s);
+}
+
+static int orc_key_allowed(int64_t kp, int64_t qp, int32_t window) {
+    return kp <= qp && (window <= 0 || kp >= qp - (int64_t)(window - 1));
+}
+
+int orc_window_attn_mimic(int dtype, const uint8_t *k_layer, const uint8_t *v_layer,
+                          int64_t row_bytes, const int32_t *k_slot, const int64_t *k_pos,
+                          int32_t n_keys, int32_t new_start, const float *q,
+                          const int64_t *q_pos, int32_t n_q, int32_t n_q_heads,
+                          int32_t n_kv_heads, int32_t head_dim, int32_t window, float scale,
+                          int flash, float *out) {
+    /* The reference's encoder ring is F16 or F32 (src/voxtral.cpp:82-92). */
+    if ((dtype != ORC_F16 && dtype != ORC_F32) || head_dim > 512 || n_keys < 0) return -1;
+    int32_t group = n_q_heads / n_kv_heads;
+    size_t nk = (size_t)(n_keys > 0 ? n_keys : 1);
+    float *w = (float *)malloc(sizeof(float) * nk);
+    int32_t *allowed = (int32_t *)malloc(sizeof(int32_t) * nk);
+    for (int32_t i = 0; i < n_q; ++i) {
+        for (int32_t h = 0; h < n_q_heads; ++h) {
+            int32_t g = h / group;
+            const float *qh = q + ((int64_t)i * n_q_heads + h) * head_dim;
+            float *oh = out + ((int64_t)i * n_q_heads + h) * head_dim;
+            if (flash) {
+                /* :2347-2349: ggml_flash_attn_ext over the gathered window;
+                 * masked keys (-inf) are skipped (ggml's CPU loop continues
+                 * past them), so it is the decode mimic over the allowed keys
+                 * in logical order. */
+                int32_t na = 0;
+                for (int32_t j = 0; j < n_keys; ++j)
+                    if (orc_key_allowed(k_pos[j], q_pos[i], window)) allowed[na++] = k_slot[j];
+                orc_mimic_head(dtype, k_layer, v_layer, row_bytes, allowed, na, 0, qh, g,
+                               head_dim, scale, dtype == ORC_F16, oh);
+                continue;
+            }
+            /* :2259-2266: scores = concat_s mul_mat(K_s, q).  ggml's CPU
+             * mul_mat converts the f32 query to the weights' dot type (f16
+             * for an F16 ring); products of two f16 values are exact in f32. */
+            uint16_t q16[512];
+            if (dtype == ORC_F16) orc_f32_to_f16_n(qh, q16, head_dim);
+            /* :2268 soft_max_ext: w = s*scale + mask (0 or -inf), max, expf,
+             * the sum in double, then every weight times the f32 of its
+             * reciprocal. */
+            float mx = -INFINITY;
+            for (int32_t j = 0; j < n_keys; ++j) {
+                if (!orc_key_allowed(k_pos[j], q_pos[i], window)) { w[j] = -INFINITY; continue; }
+                const uint8_t *krow = k_layer + (int64_t)k_slot[j] * row_bytes;
+                double acc = 0.0;
+                if (dtype == ORC_F16) {
+                    const uint16_t *kh = (const uint16_t *)krow + (int64_t)g * head_dim;
+                    for (int32_t d = 0; d < head_dim; ++d)
+                        acc += (double)(orc_f16_to_f32(kh[d]) * orc_f16_to_f32(q16[d]));
+                } else {
+                    const float *kf = (const float *)krow + (int64_t)g * head_dim;
+                    for (int32_t d = 0; d < head_dim; ++d) acc += (double)(kf[d] * qh[d]);
+                }
+                w[j] = (float)acc * scale;
+                if (w[j] > mx) mx = w[j];
+            }
+            double sum = 0.0;
+            for (int32_t j = 0; j < n_keys; ++j) {
+                float e = w[j] == -INFINITY ? 0.0f : expf(w[j] - mx);
+                w[j] = e;
+                sum += (double)e;
+            }
+            float inv = sum > 0.0 ? (float)(1.0 / sum) : 0.0f;
+            for (int32_t j = 0; j < n_keys; ++j) w[j] *= inv;
+            /* :2270-2281: per segment (maximal runs of consecutive ring
+             * slots, and the new rows), mul_mat(V_s^T, weights_s): the
+             * weights converted to f16 for an F16 V; the segments' f32
+             * results added in order. */
+            for (int32_t d = 0; d < head_dim; ++d) oh[d] = 0.0f;
+            int32_t j0 = 0;
+            while (j0 < n_keys) {
+                int32_t j1 = j0 + 1;
+                while (j1 < n_keys && j1 != new_start && k_slot[j1] == k_slot[j1 - 1] + 1) ++j1;
+                for (int32_t d = 0; d < head_dim; ++d) {
+                    double acc = 0.0;
+                    for (int32_t j = j0; j < j1; ++j) {
+                        const uint8_t *vrow = v_layer + (int64_t)k_slot[j] * row_bytes;
+                        if (dtype == ORC_F16) {
+                            float pw = orc_f16_to_f32(orc_f32_to_f16(w[j]));
+                            float vv = orc_f16_to_f32(((const uint16_t *)vrow)[(int64_t)g * head_dim + d]);
+                            acc += (double)(pw * vv);
+                        } else {
+                            acc += (double)(w[j] * ((const float *)vrow)[(int64_t)g * head_dim + d]);
+                        }
+                    }
+                    oh[d] += (float)acc;
+                }
+                j0 = j1;
+            }
+        }
+    }
+    free(allowed);
+    free(w);
+    return 0;
 }
 
 /* ---- threaded CPU baseline ---- */
@@ -262,7 +386,7 @@ static void *orc_step_worker(void *arg) {
             else
                 orc_mimic_head(j->dtype, kl, vl, j->row_bytes, NULL, j->n_valid, 0,
                                ql + (int64_t)h * j->head_dim, h / group, j->head_dim, j->scale,
-                               ol + (int64_t)h * j->head_dim);
+                               j->dtype == ORC_F16, ol + (int64_t)h * j->head_dim);
         }
         pthread_barrier_wait(j->barrier);   /* one graph node per layer */
     }

@@ -172,6 +172,12 @@ void orc_decode_attn_mimic(int dtype, const uint8_t *k_layer, const uint8_t *v_l
                            int64_t row_bytes, const int32_t *slots, int32_t n_slots,
                            const float *q, int32_t n_q_heads, int32_t n_kv_heads,
                            int32_t head_dim, float scale, float *out);
+/* orc_decode_attn_mimic with an f32 V accumulator (every other rounding of
+ * ggml's CPU flash attention kept). */
+void orc_decode_attn_mimic_acc32(int dtype, const uint8_t *k_layer, const uint8_t *v_layer,
+                                 int64_t row_bytes, const int32_t *slots, int32_t n_slots,
+                                 const float *q, int32_t n_q_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, float scale, float *out);
 /* Multi-query window attention (encoder sliding window / decoder prefill).
  * Query i has absolute position q_pos[i]; key j has absolute position
  * k_pos[j] at physical slot k_slot[j]; key allowed iff k_pos<=q_pos and
@@ -182,6 +188,21 @@ void orc_window_attn_f64(int dtype, const uint8_t *k_layer, const uint8_t *v_lay
                          int32_t n_keys, const float *q, const int64_t *q_pos, int32_t n_q,
                          int32_t n_q_heads, int32_t n_kv_heads, int32_t head_dim,
                          int32_t window, double scale, double *out);
+
+/* orc_window_attn_f64's function in the reference encoder's ggml CPU
+ * arithmetic: flash == 0 is the segmented path of fewer than 32 query rows
+ * (f16 query against an F16 K, f32 softmax, f16 weights against an F16 V,
+ * f32 sums per segment added in order), flash == 1 the flash path of 32 and
+ * more (the decode mimic over each query's allowed keys).  Keys are listed in
+ * logical order; segments break where slots stop being consecutive and at key
+ * index new_start (the block's new rows).  F16 and F32 only (returns -1
+ * otherwise).  out: [n_q][n_q_heads][head_dim] f32. */
+int orc_window_attn_mimic(int dtype, const uint8_t *k_layer, const uint8_t *v_layer,
+                          int64_t row_bytes, const int32_t *k_slot, const int64_t *k_pos,
+                          int32_t n_keys, int32_t new_start, const float *q,
+                          const int64_t *q_pos, int32_t n_q, int32_t n_q_heads,
+                          int32_t n_kv_heads, int32_t head_dim, int32_t window, float scale,
+                          int flash, float *out);
 
 /* ---- CPU baseline: threaded ggml-mimic decode step ---- */
 /* For each of n_layers layers: if k_new != NULL append k_new[layer]/v_new[layer]

@@ -64,11 +64,14 @@ def sha(b):
     return hashlib.sha256(np.ascontiguousarray(b).tobytes()).hexdigest()
 
 
-def oracle_decode(cache, stream, layer, slots, q_row, mimic=False):
+def oracle_decode(cache, stream, layer, slots, q_row, mimic=False, acc32=False):
+    """exact fp64 attention, the ggml mimic, or (acc32) the mimic with an f32
+    V accumulator"""
     kimg = layer_image(cache, 0, stream, layer)
     vimg = layer_image(cache, 1, stream, layer)
     scale = 1.0 / np.sqrt(cache.head_dim)
-    fn = oracle.decode_attn_mimic if mimic else oracle.decode_attn_f64
+    fn = (oracle.decode_attn_mimic_acc32 if acc32 else
+          oracle.decode_attn_mimic if mimic else oracle.decode_attn_f64)
     return fn(cache.dtype, kimg, vimg, int(cache.row_bytes), np.asarray(slots, np.int32), q_row,
               cache.n_kv_heads, cache.head_dim, scale)
 

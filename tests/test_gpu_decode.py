@@ -27,17 +27,32 @@ TOL = {vkv.F16: 2e-3, vkv.F32: 1e-4, vkv.Q8_0: 1e-2}
 F16_FULL_EXACT = 1e-4
 
 
-def check_full_window_f16(got, exact, mimic, where, bound=F16_FULL_EXACT):
-    """the F16 relation: |gpu - fp64| <= bound and |gpu - mimic| <=
-    |mimic - fp64| + bound (max-abs over the layer); bound 1e-4 at the full
-    window, the 2e-3 tolerance on short ones (one f16 rounding of each
-    softmax weight is not averaged away there)"""
+# ggml's reduction with only its f16 V accumulator replaced by an f32 one
+# (Q rounded to f16, f32 scores, the per-key online softmax) sits within this
+# of the GPU at windows of 2048 keys and more (measured 1.3e-5 .. 3.4e-5 at
+# 2048 .. 8192 keys, against 2e-5 .. 5.6e-5 from the exact attention): the
+# GPU's remaining differences are the f16 rounding of its (lazily rescaled)
+# softmax weights and the summation order.
+F16_ACC32_TOL = 5e-5
+
+
+def check_full_window_f16(got, exact, mimic, where, bound=F16_FULL_EXACT, acc32=None):
+    """the F16 checks at windows where ggml's f16 V accumulator drifts: the
+    GPU within `bound` of the exact attention, and within F16_ACC32_TOL of
+    ggml's arithmetic with an f32 accumulator (`acc32`), which pins the
+    query's f16 rounding and the softmax to the reference's path.  The full
+    mimic's distance from the GPU is returned, not asserted: at these windows
+    it is the f16 accumulator's drift from the exact result (~2.07e-3 at
+    8192 keys), which the oracle's closed forms pin."""
     e_gpu = float(np.max(np.abs(got - exact)))
     e_mimic = float(np.max(np.abs(mimic - exact)))
     d = float(np.max(np.abs(got - mimic)))
+    d32 = float("nan")
     assert e_gpu <= bound, (where, e_gpu)
-    assert d <= e_mimic + bound, (where, d, e_mimic)
-    return e_gpu, e_mimic, d
+    if acc32 is not None:
+        d32 = float(np.max(np.abs(got - acc32)))
+        assert d32 <= F16_ACC32_TOL, (where, d32)
+    return e_gpu, e_mimic, d, d32
 # Distance to the exact attention: for q8_0 the quantization of Q to q8_0
 # blocks (ggml's q8_0 dot product) moves the output by up to ~1.5e-2 on
 # windows of a few keys.
@@ -137,9 +152,20 @@ def test_decoder_stream_4096_steps_no_wrap():
                 check_cache_state(c, [0], range(26), 8192, {0: pos + 1})
             if pos in (0, 1, 2047, 4095):
                 for layer in (0, 13, 25):
-                    want = oracle_decode(c, 0, layer, plan_slots(plans[0]), q[0, layer].cpu().numpy())
+                    slots, q_row = plan_slots(plans[0]), q[0, layer].cpu().numpy()
                     got = out[0, layer].cpu().numpy().reshape(32, 128)
-                    assert np.max(np.abs(got - want)) <= 2e-3, (pos, layer)
+                    exact = oracle_decode(c, 0, layer, slots, q_row)
+                    mimic = oracle_decode(c, 0, layer, slots, q_row, mimic=True)
+                    if pos < 1024:
+                        # short windows: the literal bar against the ggml mimic
+                        assert np.max(np.abs(got - mimic)) <= TOL[vkv.F16], (pos, layer)
+                        assert np.max(np.abs(got - exact)) <= EXACT_TOL[vkv.F16], (pos, layer)
+                        continue
+                    acc32 = oracle_decode(c, 0, layer, slots, q_row, acc32=True)
+                    errs = check_full_window_f16(got, exact, mimic, (pos, layer), acc32=acc32)
+                    print(f"stream step {pos} layer {layer}: |gpu-fp64| {errs[0]:.2e}, "
+                          f"|mimic-fp64| {errs[1]:.2e}, |gpu-mimic| {errs[2]:.2e}, "
+                          f"|gpu-acc32| {errs[3]:.2e}", flush=True)
         assert rings[0].wraps == 0 and rings[0].used == 4096
 
 
@@ -167,9 +193,11 @@ def test_longform_ring_32768_steps():
                     got = out[0, layer].cpu().numpy().reshape(32, 128)
                     exact = oracle_decode(c, 0, layer, slots, q_row)
                     mimic = oracle_decode(c, 0, layer, slots, q_row, mimic=True)
-                    errs = check_full_window_f16(got, exact, mimic, (pos, layer))
+                    acc32 = oracle_decode(c, 0, layer, slots, q_row, acc32=True)
+                    errs = check_full_window_f16(got, exact, mimic, (pos, layer), acc32=acc32)
                     print(f"longform step {pos} layer {layer}: |gpu-fp64| {errs[0]:.2e}, "
-                          f"|mimic-fp64| {errs[1]:.2e}, |gpu-mimic| {errs[2]:.2e}", flush=True)
+                          f"|mimic-fp64| {errs[1]:.2e}, |gpu-mimic| {errs[2]:.2e}, "
+                          f"|gpu-acc32| {errs[3]:.2e}", flush=True)
                 print(f"longform step {pos} ok", flush=True)
 
 
@@ -291,7 +319,8 @@ def test_one_pass_full_ring(dtype):
                 mimic = oracle_decode(c, 0, layer, slots, q_row, mimic=True)
                 exact = oracle_decode(c, 0, layer, slots, q_row)
                 if dtype == vkv.F16:
-                    check_full_window_f16(got, exact, mimic, (pos, layer))
+                    check_full_window_f16(got, exact, mimic, (pos, layer),
+                                          acc32=oracle_decode(c, 0, layer, slots, q_row, acc32=True))
                     continue
                 assert np.max(np.abs(got - mimic)) <= TOL[dtype], (pos, layer)
                 assert np.max(np.abs(got - exact)) <= EXACT_TOL[dtype], (pos, layer)
@@ -466,7 +495,7 @@ def test_whole_row_kernel_streams_and_partial_chunks(case, rope):
     for s, layer, got, exact, mimic in checks:
         bound = F16_FULL_EXACT if fills[s] + 1 > 1024 else TOL[vkv.F16]
         errs = check_full_window_f16(got, exact, mimic, (case, s, layer), bound)
-        worst = np.maximum(worst, errs)
+        worst = np.maximum(worst, errs[:3])
     print(f"whole rows {case} rope={rope} ok: |rows-heads| {d_kernels:.2e}, |rows-fp64| "
           f"{worst[0]:.2e}, |mimic-fp64| {worst[1]:.2e}, |rows-mimic| {worst[2]:.2e}", flush=True)
 

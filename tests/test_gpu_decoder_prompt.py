@@ -158,8 +158,9 @@ def composed_prompt(cache, ring, model, tokens, aring, logits, tok_out, sp, m=No
 
 
 def oracle_prompt(m, k_imgs, v_imgs, row_b, capacity, pos0, tokens, audio):
-    """ggml's CPU path for the whole prompt (oracle restatements throughout):
-    the last token's logits and greedy token"""
+    """ggml's CPU path for the whole prompt (oracle restatements throughout,
+    the attention in ggml's flash-attention arithmetic): the last token's
+    logits and greedy token"""
     n = len(tokens)
     rb = DIM // 256 * 210
     x = np.stack([oracle.dequantize(oracle.Q6_K, m["table"][t * rb:(t + 1) * rb], DIM)
@@ -178,9 +179,13 @@ def oracle_prompt(m, k_imgs, v_imgs, row_b, capacity, pos0, tokens, audio):
             s = (pos0 + i) % capacity
             ki[s * row_b:(s + 1) * row_b] = np.frombuffer(oracle.rows_from_f32(oracle.F16, k[i]), np.uint8)
             vi[s * row_b:(s + 1) * row_b] = np.frombuffer(oracle.rows_from_f32(oracle.F16, v[i]), np.uint8)
-        attn = oracle.window_attn_f64(oracle.F16, ki, vi, row_b,
-                                      (key_pos % capacity).astype(np.int32), key_pos,
-                                      q.reshape(n, QH, HD), q_pos, QH, KVH, HD, 0, SCALE)
+        # the prefill's attention as ggml's CPU flash attention computes it
+        # (src/voxtral.cpp:2763-2773: the query rounded to f16 against the F16
+        # cache, per-key online softmax, f16 V accumulator over the causal keys)
+        attn = oracle.window_attn_mimic(oracle.F16, ki, vi, row_b,
+                                        (key_pos % capacity).astype(np.int32), key_pos,
+                                        q.reshape(n, QH, HD), q_pos, QH, KVH, HD, 0, SCALE,
+                                        flash=True)
         attn = attn.reshape(n, QD).astype(np.float32)
         x = x + rows_matvec(oracle.Q4_K, L["attn_o"], DIM, QD, attn)
         hs = [oracle.norm_act(x[p], L["ffn_norm"], L["ada"], EPS) for p in range(n)]
@@ -208,7 +213,10 @@ def workspace_for(model, n):
 
 # (cache capacity, positions already in the ring, prompt tokens, audio ring capacity or None)
 CASES = [(512, 0, 38, 64),          # the stream prompt at positions 0..37
-         (512, 986, 38, 48)]        # after a wrap: evictions, the audio ring wraps too
+         (512, 986, 38, 48),        # after a wrap: evictions, the audio ring wraps too
+         (512, 0, 1, 64),           # prompts of a few tokens: the normed products at the
+         (512, 40, 3, 64),          # decoder's width 3072 take the separate input
+         (512, 509, 5, 48)]         # quantization (across the ring's wrap here)
 
 
 @pytest.mark.parametrize("cap,P,N,acap", CASES)

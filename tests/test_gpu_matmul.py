@@ -188,3 +188,48 @@ def test_fused_and_separate_input_images_agree(norm):
         want = oracle.q8_k_quantize(h).reshape(-1, 292)[:, 4:260].ravel()
         codes = img_s[p].reshape(n_in // 256, 4, 4, 2, 8).transpose(0, 1, 3, 2, 4).reshape(n_in)
         assert np.array_equal(codes, want)
+
+
+@pytest.mark.parametrize("n_in,ada", [(3072, False), (3072, True), (2048, True)])
+def test_normed_input_wider_than_the_fused_norm(n_in, ada):
+    """A normed call at the decoder's width (the Q/K/V and W1/W3 products of a
+    prompt of a few tokens, RMSNorm x weight x (1 + ada)): each work group of
+    a fused-input call stages the norm's vectors in LDS, 4 elements per
+    thread, so a width above 4 x 64 x waves must take the separate
+    quantization.  A run of 4 rows and a run of 64 rows give the same Q8_K
+    image and the same outputs bit for bit, and both are the oracle's.  (2048
+    fits the 8-wave fused norm exactly: the fused path is exercised at its
+    limit.)"""
+    rng = np.random.default_rng(3072 + n_in + ada)
+    P_big, P_small = 64, 4
+    mats = [(vkv.Q4_K, 4096), (vkv.Q4_K, 1024), (vkv.Q6_K, 1024)]
+    ws_np = [random_matrix(rng, dt, n, n_in, 0.05) for dt, n in mats]
+    ws = [to_dev(w) for w in ws_np]
+    x = (rng.standard_normal((P_big, n_in)) *
+         np.exp(rng.uniform(-3, 3, (P_big, 1)))).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, n_in).astype(np.float32)
+    ad = rng.uniform(-0.5, 0.5, n_in).astype(np.float32) if ada else None
+    xd, nwd = to_dev(x), to_dev(nw)
+    add = to_dev(ad) if ada else None
+    runs = []
+    for P in (P_small, P_big):
+        ys = [torch.full((P, n), np.nan, device=dev()) for _, n in mats]
+        t, ws_ptr, ws_b = workspace(P, n_in)
+        vkv.matmul(xd.data_ptr(), P, n_in,
+                   [(w.data_ptr(), dt, n, y.data_ptr()) for w, (dt, n), y in zip(ws, mats, ys)],
+                   ws_ptr, ws_b, norm_w_ptr=nwd.data_ptr(),
+                   ada_ptr=add.data_ptr() if ada else None, eps=EPS, hip_stream=stream_ptr())
+        raw = host(t).view(np.uint8)[ws_ptr - t.data_ptr():][:P * n_in].reshape(P, n_in)
+        runs.append((raw.copy(), [host(y) for y in ys]))
+    (img_s, out_s), (img_b, out_b) = runs
+    assert np.array_equal(img_s, img_b[:P_small])
+    for a, b in zip(out_s, out_b):
+        assert np.array_equal(a.view(np.uint32), b[:P_small].view(np.uint32))
+    hs = [oracle.norm_act(x[p], nw, ad, EPS) for p in range(P_small)]
+    for p in range(P_small):
+        want = oracle.q8_k_quantize(hs[p]).reshape(-1, 292)[:, 4:260].ravel()
+        codes = img_s[p].reshape(n_in // 256, 4, 4, 2, 8).transpose(0, 1, 3, 2, 4).reshape(n_in)
+        assert np.array_equal(codes, want)
+    for w, (dt, n), y in zip(ws_np, mats, out_s):
+        want, mag = rows_ref(dt, w, n, n_in, hs)
+        check(y, want, mag)

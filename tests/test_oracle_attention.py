@@ -328,3 +328,163 @@ def test_vector_leg_against_scalar_mimic(dtype, tol):
                                            3, k_new=kn, v_new=vn, new_slot=700, simd=simd)
         outs.append(o)
     assert np.max(np.abs(outs[0] - outs[1])) <= tol
+
+
+# ---------------------------------------------------------------------------
+# The encoder's window attention in the reference's ggml CPU arithmetic
+# (src/voxtral.cpp:2259-2281, fewer than 32 query rows): mul_mat of each K
+# segment with the query (converted to f16 against an F16 ring), soft_max_ext
+# in f32, mul_mat of each V^T segment with the weights (converted to f16
+# against an F16 ring).  The closed forms below fail when either conversion
+# is dropped; an F32 ring converts nothing.
+# ---------------------------------------------------------------------------
+
+EH, ED = 2, 64
+
+
+def _enc_layer(dtype, krows, vrows):
+    kimg, _ = make_layer(dtype, krows)
+    vimg, _ = make_layer(dtype, vrows)
+    return kimg, vimg, oracle.row_bytes(dtype, EH * ED)
+
+
+def _two_key_closed_form(dtype, q, krows, vrows, scale):
+    """ggml's manual softmax over keys 0 and 1 for one head: (out0, out1) where
+    V0 = e_0 and V1 = e_1, so out_d = conv(p_d)"""
+    f16 = lambda x: np.float32(np.float16(np.float32(x)))  # noqa: E731  (RNE, as numpy rounds)
+    qc = np.array([f16(x) for x in q], np.float32) if dtype == oracle.F16 else q
+    s = [np.float32(np.dot(krows[j, :ED].astype(np.float64), qc.astype(np.float64)))
+         for j in range(2)]
+    w = [_f32(sj * _f32(scale)) for sj in s]
+    m = max(w)
+    e = [_f32(np.exp(np.float64(_f32(wj - m)))) for wj in w]
+    inv = _f32(1.0 / (np.float64(e[0]) + np.float64(e[1])))
+    p = [_f32(ej * inv) for ej in e]
+    return [f16(pj) if dtype == oracle.F16 else pj for pj in p], p, s
+
+
+@pytest.mark.parametrize("dtype", [oracle.F16, oracle.F32])
+def test_window_mimic_rounds_weights_to_f16(dtype):
+    """Two keys, K0 = a e_0, K1 = 0, V0 = e_0, V1 = e_1, queries e_0 (exact in
+    f16): the softmax weights p0 = 1/(1+exp(-a/8)), p1 = 1 - p0 are not f16
+    values, and an F16 ring's output is f16(p0), f16(p1) exactly, where the
+    unrounded weights sit many ulp away; an F32 ring returns p0 and p1."""
+    n_q = 12
+    krows = np.zeros((2, EH * ED), np.float32)
+    vrows = np.zeros((2, EH * ED), np.float32)
+    for g in range(EH):
+        vrows[0, g * ED] = 1.0
+        vrows[1, g * ED + 1] = 1.0
+    outs = []
+    for i in range(n_q):
+        a = 0.37 + 0.53 * i
+        for g in range(EH):
+            krows[0, g * ED] = a
+        kimg, vimg, rb = _enc_layer(dtype, krows, vrows)
+        a16 = np.float32(oracle.rows_to_f32(dtype, kimg, EH * ED)[0, 0])
+        q = np.zeros((1, EH, ED), np.float32)
+        q[0, :, 0] = 1.0
+        got = oracle.window_attn_mimic(dtype, kimg, vimg, rb, np.array([0, 1]), np.array([0, 1]),
+                                       q, np.array([1]), EH, EH, ED, 750, 0.125)
+        kr = np.zeros((2, EH * ED), np.float32)
+        kr[0, 0] = a16
+        want, unrounded, _ = _two_key_closed_form(dtype, q[0, 0], kr, vrows, 0.125)
+        for h in range(EH):
+            assert _ulps(got[0, h, 0], want[0]) <= 1 and _ulps(got[0, h, 1], want[1]) <= 1, (i, h)
+            assert np.all(got[0, h, 2:] == 0)
+        if dtype == oracle.F16:
+            outs.append(max(_ulps(unrounded[0], want[0]), _ulps(unrounded[1], want[1])))
+    if dtype == oracle.F16:
+        assert min(outs) >= 20      # the f32 weights are never f16 values here
+
+
+@pytest.mark.parametrize("dtype", [oracle.F16, oracle.F32])
+def test_window_mimic_rounds_q_to_f16(dtype):
+    """K0 = e_0, K1 = e_1, V0 = e_0, V1 = e_1, query (q0, 300, 0, ...) with q0
+    near 300 off the f16 grid (ulp 0.25 there): against an F16 ring the
+    scores are f16(q0) and 300, so q0 = 300.1 scores a tie and both outputs
+    are exactly 0.5; unrounded, p0 = sigmoid(0.0125) = 0.5031, whose f16 is
+    0.50293.  An F32 ring keeps q0."""
+    krows = np.zeros((2, EH * ED), np.float32)
+    vrows = np.zeros((2, EH * ED), np.float32)
+    for g in range(EH):
+        krows[0, g * ED] = 1.0
+        krows[1, g * ED + 1] = 1.0
+        vrows[0, g * ED] = 1.0
+        vrows[1, g * ED + 1] = 1.0
+    kimg, vimg, rb = _enc_layer(dtype, krows, vrows)
+    q0s = [300.1, 300.2, 299.9, 300.05, 299.8, 300.37]
+    q = np.zeros((len(q0s), EH, ED), np.float32)
+    for i, q0 in enumerate(q0s):
+        q[i, :, 0] = q0
+        q[i, :, 1] = 300.0
+    q_pos = np.arange(1, 1 + len(q0s))
+    got = oracle.window_attn_mimic(dtype, kimg, vimg, rb, np.array([0, 1]), np.array([0, 1]), q,
+                                   q_pos, EH, EH, ED, 750, 0.125)
+    moved = 0
+    for i in range(len(q0s)):
+        want, _, _ = _two_key_closed_form(dtype, q[i, 0], krows, vrows, 0.125)
+        # the same with the query left in f32
+        alt, _, _ = _two_key_closed_form(oracle.F32, q[i, 0], krows, vrows, 0.125)
+        alt = [np.float32(np.float16(x)) for x in alt] if dtype == oracle.F16 else alt
+        for h in range(EH):
+            assert _ulps(got[i, h, 0], want[0]) <= 1 and _ulps(got[i, h, 1], want[1]) <= 1, (i, h)
+        if dtype == oracle.F16:
+            moved += int(_ulps(alt[0], want[0]) >= 1000)
+    if dtype == oracle.F16:
+        assert got[0, 0, 0] == np.float32(0.5) and got[0, 0, 1] == np.float32(0.5)
+        assert moved == len(q0s)      # every q0 here leaves the f16 grid by >= 0.05
+    else:
+        assert abs(float(got[0, 0, 0]) - 1 / (1 + np.exp(-0.0125))) < 1e-6
+
+
+@pytest.mark.parametrize("dtype,tol", [(oracle.F16, 2e-3), (oracle.F32, 1e-5)])
+def test_window_mimic_within_tolerance_of_exact(dtype, tol):
+    """At the encoder's shape (32 heads x 64, window 750, a 16-frame block at
+    q_start 2000 over a wrapped 878-slot ring) the reference's CPU arithmetic
+    stays within the acceptance tolerance of exact attention; its distance is
+    what the GPU tile is compared against."""
+    rng = np.random.default_rng(2259 + dtype)
+    H_, D_, cap, win, P, q_start = 32, 64, 878, 750, 16, 2000
+    kimg, _ = make_layer(dtype, rng.standard_normal((cap, H_ * D_)).astype(np.float32))
+    vimg, _ = make_layer(dtype, rng.standard_normal((cap, H_ * D_)).astype(np.float32))
+    k_pos = np.arange(q_start - (win - 1), q_start + P, dtype=np.int64)
+    k_slot = (k_pos % cap).astype(np.int32)
+    q_pos = np.arange(q_start, q_start + P, dtype=np.int64)
+    q = rng.standard_normal((P, H_, D_)).astype(np.float32)
+    rb = oracle.row_bytes(dtype, H_ * D_)
+    ex = oracle.window_attn_f64(dtype, kimg, vimg, rb, k_slot, k_pos, q, q_pos, H_, H_, D_, win, 0.125)
+    mi = oracle.window_attn_mimic(dtype, kimg, vimg, rb, k_slot, k_pos, q, q_pos, H_, H_, D_, win,
+                                  0.125)
+    d = float(np.max(np.abs(mi - ex)))
+    assert d < tol
+    if dtype == oracle.F16:
+        assert d > 1e-5       # the two f16 conversions are visible at this size
+    # the flash form (32+ rows) is the decode mimic over each query's keys
+    fl = oracle.window_attn_mimic(dtype, kimg, vimg, rb, k_slot, k_pos, q[:2], q_pos[:2], H_, H_,
+                                  D_, win, 0.125, flash=True)
+    for i in range(2):
+        sl = k_slot[(k_pos <= q_pos[i]) & (k_pos >= q_pos[i] - (win - 1))]
+        want = oracle.decode_attn_mimic(dtype, kimg, vimg, rb, sl, q[i].reshape(-1), H_, D_, 0.125)
+        assert np.array_equal(fl[i], want)
+
+
+def test_decode_mimic_acc32_differs_only_by_the_accumulator():
+    """The f32-accumulator mimic keeps every other rounding: at the stall case
+    (4096 equal weights of V = 1) it gives exactly 1.0 where the mimic gives
+    0.5, and for an F32 cache (no f16 accumulator) both are the same bits."""
+    n = 4096
+    kimg, _ = make_layer(oracle.F16, np.zeros((n, KV), np.float32))
+    vimg, _ = make_layer(oracle.F16, np.ones((n, KV), np.float32))
+    q = np.random.default_rng(3).standard_normal((H, D)).astype(np.float32)
+    rb = oracle.row_bytes(oracle.F16, KV)
+    slots = np.arange(n, dtype=np.int32)
+    a32 = oracle.decode_attn_mimic_acc32(oracle.F16, kimg, vimg, rb, slots, q, G, D, 1 / np.sqrt(D))
+    assert np.all(a32 == np.float32(1.0))
+    rng = np.random.default_rng(8)
+    kimg, _ = make_layer(oracle.F32, rng.standard_normal((300, KV)).astype(np.float32))
+    vimg, _ = make_layer(oracle.F32, rng.standard_normal((300, KV)).astype(np.float32))
+    rb = oracle.row_bytes(oracle.F32, KV)
+    sl = np.arange(300, dtype=np.int32)
+    assert np.array_equal(oracle.decode_attn_mimic(oracle.F32, kimg, vimg, rb, sl, q, G, D, 0.09),
+                          oracle.decode_attn_mimic_acc32(oracle.F32, kimg, vimg, rb, sl, q, G, D, 0.09))

@@ -1314,19 +1314,22 @@ vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float
                 lo + (uintptr_t)(out_rows.ring > 0 ? out_rows.ring : n_cols) * outs[k].n_rows * 4;
             in_place = in_place || (lo < x_hi && x_lo < hi);
         }
+    // The norm's vectors are set before the fused check: its guard on the
+    // input width and its LDS size both depend on whether a norm is applied.
+    a.norm_w = norm_w;
+    a.norm_b = norm_b;
+    a.ada = ada;
     if (!in_place && gemm_fused_ok(a, n_col_tiles)) {
         a.x = x;
         a.x_stride = n_in;
         a.x_ring = in_rows.ring;
         a.x_row0 = in_rows.row0;
-        a.norm_w = norm_w;
-        a.norm_b = norm_b;
-        a.ada = ada;
         a.eps = eps;
         a.xq = im.codes;   // (the image is also left in the workspace)
         a.xd = im.xd;
         a.xbs = im.bs16;
     } else {
+        a.norm_w = a.norm_b = a.ada = nullptr;   // applied by the separate quantization
         e = launch_q8k_rows(x, n_in, in_rows.ring, in_rows.row0, n_cols, (int)n_in, norm_w, norm_b,
                             ada, eps, im.codes, im.xd, im.bs16, as_stream(hip_stream));
         if (e != hipSuccess) return hip_fail(e, "matmul input launch");
