@@ -642,7 +642,7 @@ def gpu_realtime_step(steps, warmup):
     emodel, ecache, ekeep = encoder_setup(gen, sp)
     dmodel, dkeep = device_model(gen)
     dcache = vkv.Cache(n_streams=1, n_layers=LAYERS, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
-                       n_q_heads=QH, dtype=vkv.F16)
+                       n_q_heads=QH, dtype=vkv.F16, **CACHE_KW)
     ring = vkv.new_ring(CAP)
     plan = vkv.decoder_plan(ring, 0, CAP)
     k0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
@@ -737,7 +737,7 @@ def gpu_token(steps, warmup):
     gen.manual_seed(SEED)
     model, keep = device_model(gen)
     cache = vkv.Cache(n_streams=1, n_layers=LAYERS, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
-                      n_q_heads=QH, dtype=vkv.F16)
+                      n_q_heads=QH, dtype=vkv.F16, **CACHE_KW)
     ring = vkv.new_ring(CAP)
     plan = vkv.decoder_plan(ring, 0, CAP)
     k0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
@@ -786,7 +786,7 @@ def gpu_prompt(steps, warmup):
     gen.manual_seed(SEED)
     model, keep = device_model(gen)
     cache = vkv.Cache(n_streams=1, n_layers=LAYERS, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
-                      n_q_heads=QH, dtype=vkv.F16)
+                      n_q_heads=QH, dtype=vkv.F16, **CACHE_KW)
     ring = vkv.new_ring(CAP)
     aemb = torch.randn(P_AUDIO_CAP, DIM, device="cuda", generator=gen) * 0.1
     aring = vkv.RowRing(aemb.data_ptr(), P_AUDIO_CAP, DIM)

@@ -87,6 +87,25 @@ __device__ __forceinline__ float xor32_max(float v) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Max / sum over the 64 lanes of a wave, every lane receiving the result: a
+// DPP butterfly inside each 16-lane row, then the two row-swap permutes.
+// The sum's association is fixed, so every caller summing the same lane
+// values gets the same bits in every lane.  Its input is made opaque first:
+// with contraction on, the compiler otherwise fuses a caller's product into
+// the first butterfly add (fma(a, b, partner's rounded product)), and the
+// two lanes of a pair then round differently.
+__device__ __forceinline__ float wave_max64(float x) {
+    x = fmaxf(x, dpp<0xB1>(x));
+    x = fmaxf(x, dpp<0x4E>(x));
+    x = fmaxf(x, dpp<0x141>(x));
+    x = fmaxf(x, dpp<0x140>(x));
+    return xor32_max(xor16_max(x));
+}
+__device__ __forceinline__ float wave_sum64(float x) {
+    asm volatile("" : "+v"(x));
+    return xor32_sum(xor16_sum(row_sum16(x)));
+}
+
 // Round half away from zero.  Contraction stays off: the quantizer rounds the
 // product x*id first, exactly like the CPU quantizer.
 __device__ __forceinline__ float round_half_away(float v) {
@@ -1723,8 +1742,7 @@ __global__ void __launch_bounds__(128) k_combine(CombineArgs a) {
         for (int c = 0; c < kCombineRegs; ++c) v[c] = po[(int64_t)min(c, n - 1) * a.head_dim];
         const float mc = t < n ? mc0 : -INFINITY;
         const float lc = t < n ? lc0 : 0.0f;
-        float m = mc;
-        for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float m = wave_max64(mc);
         if (lane == 0) red[0][wave] = m;
         __syncthreads();
         const float M = fmaxf(red[0][0], red[0][1]);
@@ -1733,15 +1751,16 @@ __global__ void __launch_bounds__(128) k_combine(CombineArgs a) {
             return;
         }
         const float w = t < n ? fast_exp2(mc - M) : 0.0f;
-        float l = lc * w;
+        const float l = wave_sum64(lc * w);
         sw[t] = w;
-        for (int o = 32; o >= 1; o >>= 1) l += __shfl_xor(l, o);
         if (lane == 0) red[1][wave] = l;
         __syncthreads();
+        // all kCombineRegs slots, unconditionally, so no partial load is held
+        // back behind a condition on n: past the last chunk the weight is 0
+        // (sw[t] = 0 for t >= n) on a clamped, finite partial
         float O = 0.0f;
 #pragma unroll
-        for (int c = 0; c < kCombineRegs; ++c)
-            if (c < n) O = fmaf(v[c], sw[c], O);
+        for (int c = 0; c < kCombineRegs; ++c) O = fmaf(v[c], sw[c], O);
         const float L = red[1][0] + red[1][1];
         a.out[head * a.head_dim + t] = L > 0.0f ? O / L : 0.0f;
         return;
