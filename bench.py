@@ -61,6 +61,11 @@ Other workloads (--workload), reported on the same contract:
                attention over the full 8192-slot F16 ring, O + residual,
                RMSNorm*(1+ada) + SwiGLU, W2 + residual), final norm, logits,
                argmax; tokens/s.
+  decoder_loop_q4km  the production token loop (run_decoder_step): per token
+               vkv_decoder_token, the 4-byte token copied to pinned host
+               memory, one stream synchronize, the token fed to the next
+               step; tokens/s and per-token latency p50/p90/p99 (host wall
+               clock; --steps tokens, 1000 by default for this workload).
   decoder_prompt_q4km  the decoder prefill of a 38-token prompt at the stream
                start through vkv_decoder_prompt: token + audio rows, 26 x
                (multi-row Q4_K_M products with RoPE in the epilogue, causal
@@ -115,6 +120,10 @@ WORKLOADS = {
                                streams=1, pmc="decoder_token_q4km_pmc.json", kern="",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs and "
                                     "KV rows, generated on device)"),
+    "decoder_loop_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights, f16 KV",
+                              streams=1, pmc="",
+                              data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) audio rows "
+                                   "and KV rows, generated on device; tokens fed back greedily)"),
     "adapter_q4km": dict(dtype=12, dtype_name="q4_k x q8_k weights (MFMA int8), f32 rings",
                          streams=1, pmc="adapter_q4km_pmc.json", kern="", groups=32,
                          data="synthetic (random valid Q4_K blocks, N(0,1) encoder frames, "
@@ -767,6 +776,86 @@ def gpu_token(steps, warmup):
     cache.close()
     del keep
     return total_ms, step_ms, wall
+
+
+LOOP_LAT_MS = []   # per-token latencies of the last gpu_token_loop run (ms)
+
+
+def gpu_token_loop(steps, warmup):
+    """The production token loop of run_decoder_step (src/voxtral.cpp:5219-5360:
+    compute :5271, one synchronize :5273, the 4-byte token readback :5341):
+    per token vkv_decoder_token on the stream, the token's 4 bytes copied to
+    pinned host memory on the same stream, one hipStreamSynchronize, and the
+    token fed to the next step (the greedy loop).  Every token's latency is
+    the host's wall clock from the call to the synchronize's return; the
+    repetitions are the K timed tokens, run once."""
+    import ctypes
+
+    import torch
+    import vkv
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+    hip.hipHostFree.argtypes = [ctypes.c_void_p]
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                   ctypes.c_void_p]
+    hip.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+    st = torch.cuda.current_stream()
+    sp = st.cuda_stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED)
+    model, keep = device_model(gen)
+    cache = vkv.Cache(n_streams=1, n_layers=LAYERS, capacity=CAP, n_kv_heads=KVH, head_dim=HD,
+                      n_q_heads=QH, dtype=vkv.F16, **CACHE_KW)
+    ring = vkv.new_ring(CAP)
+    plan = vkv.decoder_plan(ring, 0, CAP)
+    k0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
+    v0 = torch.empty(LAYERS, CAP, KV_DIM, device="cuda")
+    vkv.synth_rows(k0.data_ptr(), KV_DIM, SEED, vkv.TAG_K, nl=LAYERS, p0=0, np_=CAP, hip_stream=sp)
+    vkv.synth_rows(v0.data_ptr(), KV_DIM, SEED, vkv.TAG_V, nl=LAYERS, p0=0, np_=CAP, hip_stream=sp)
+    cache.append(0, 0, LAYERS, vkv.plan_segs(plan.write_seg, plan.write_nseg), k0.data_ptr(),
+                 v0.data_ptr(), hip_stream=sp)
+    vkv.decoder_commit(ring, plan)
+    torch.cuda.synchronize()
+    del k0, v0
+    audio = torch.randn(warmup + steps, DIM, device="cuda", generator=gen) * 0.1
+    logits = torch.empty(VOCAB, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws_bytes = vkv.decoder_token_workspace(model)
+    ws = torch.empty(ws_bytes // 4 + 64, device="cuda")
+    ws_ptr = (ws.data_ptr() + 255) & ~255
+    host = ctypes.c_void_p()
+    if hip.hipHostMalloc(ctypes.byref(host), 64, 0) != 0:
+        raise RuntimeError("hipHostMalloc failed")
+    host_tok = ctypes.cast(host, ctypes.POINTER(ctypes.c_int32))
+
+    def token(i, t):
+        vkv.decoder_token(cache, 0, ring, model, t, audio[i].data_ptr(), logits.data_ptr(),
+                          tok.data_ptr(), ws_ptr, ws_bytes, hip_stream=sp)
+        if hip.hipMemcpyAsync(host, tok.data_ptr(), 4, 2, sp) != 0:   # device to host
+            raise RuntimeError("hipMemcpyAsync failed")
+        if hip.hipStreamSynchronize(sp) != 0:
+            raise RuntimeError("hipStreamSynchronize failed")
+        return int(host_tok[0])
+
+    t = 1
+    for i in range(warmup):
+        t = token(i, t)
+    lat = []
+    wall0 = time.perf_counter()
+    for i in range(steps):
+        t0 = time.perf_counter()
+        t = token(warmup + i, t)
+        lat.append((time.perf_counter() - t0) * 1e3)
+    wall = time.perf_counter() - wall0
+    assert 0 <= t < VOCAB and bool(torch.isfinite(logits).all())
+    assert ring.next_absolute_position == CAP + warmup + steps
+    hip.hipHostFree(host)
+    cache.close()
+    del keep
+    LOOP_LAT_MS[:] = lat
+    REP_MS[:] = [sum(lat)]
+    return sum(lat), lat, wall
 
 
 P_TOKENS, P_AUDIO_CAP = 38, 256
@@ -1630,6 +1719,27 @@ def main():
                   "bytes_per_token": bytes_step, "launches_per_token": 6 * LAYERS + 2}
         kernel = ("k_kq_dequant + 26 x (4 k_matvec + k_decode + k_combine) + k_matvec "
                   "(158 launches per token)")
+    elif args.workload == "decoder_loop_q4km":
+        if not any(a == "--steps" or a.startswith("--steps=") for a in sys.argv[1:]):
+            args.steps = 1000   # enough tokens for a p99
+        total_ms, step_ms, wall = gpu_token_loop(args.steps, args.warmup)
+        bytes_step = token_bytes()
+        units_per_step = 1
+        res = {"metric": "decoder tokens/s in the production loop (vkv_decoder_token + 4-byte "
+                         "token readback + one synchronize per token) and per-token latency",
+               "unit": "tokens/s"}
+        config = {"workload": "the greedy token loop: per token vkv_decoder_token (26 layers, "
+                              "Q4_K_M weights, f16 KV attention over the full 8192-slot ring, "
+                              "logits, argmax), the token copied to pinned host memory, one "
+                              "stream synchronize, the token fed to the next step",
+                  "layers": LAYERS, "dim": DIM, "hidden": HIDDEN, "vocab": VOCAB, "window": CAP,
+                  "bytes_per_token": bytes_step, "syncs_per_token": 1}
+        kernel = "one decoder token (158 launches) + a 4-byte copy, then a synchronize"
+        lat = sorted(LOOP_LAT_MS)
+        pick = lambda q: lat[min(len(lat) - 1, int(round(q * (len(lat) - 1))))]  # noqa: E731
+        res["latency_ms"] = {"p50": round(pick(0.50), 4), "p90": round(pick(0.90), 4),
+                             "p99": round(pick(0.99), 4), "max": round(lat[-1], 4),
+                             "mean": round(sum(lat) / len(lat), 4), "tokens": len(lat)}
     elif args.workload == "decoder_weights_q4km":
         total_ms, step_ms, wall = gpu_weights(args.steps, args.warmup)
         bytes_step = weights_bytes_per_token()
@@ -1722,7 +1832,7 @@ def main():
         res["cpu_baseline"] = cpu_realtime_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload == "decoder_prompt_q4km":
         res["cpu_baseline"] = cpu_prompt_leg(args.cpu_seconds)
-    elif not args.no_cpu and args.workload == "decoder_token_q4km":
+    elif not args.no_cpu and args.workload in ("decoder_token_q4km", "decoder_loop_q4km"):
         res["cpu_baseline"] = cpu_token_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload in ("adapter_q4km", "adapter_group_q4km"):
         res["cpu_baseline"] = cpu_adapter_leg(wl["groups"], args.cpu_seconds)
