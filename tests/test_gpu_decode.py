@@ -297,6 +297,42 @@ def test_q8_0_eight_streams_full_window():
             print(f"q8_0 8-stream step {target} ok", flush=True)
 
 
+def test_q8_0_eight_streams_step_by_step_across_wraps():
+    """Config 5 as a stream: q8_0 KV, 8 independent streams, 26 layers, 8192
+    window, 512 consecutive fused steps (quantize-on-append + attention, every
+    layer, every stream) across the first wrap (positions 7936 .. 8447) and 512
+    across the second (16128 .. 16639), the rings fast-forwarded by planned
+    appends in between.  After each run the whole cache of two streams (every
+    layer, K and V) is bit-exact against the oracle's quantizer; attention of
+    one stream's last layer within 1e-2 of the mimic every 64 steps."""
+    ns, L, cap = 8, 26, 8192
+    with vkv.Cache(n_streams=ns, n_layers=L, capacity=cap, dtype=vkv.Q8_0) as c:
+        rings = (vkv.Ring * ns)(*[vkv.new_ring(cap) for _ in range(ns)])
+        out = empty_f32(ns, L, 4096)
+        pos = 0
+        for first in (cap - 256, 2 * cap - 256):
+            while pos < first:
+                m = min(cap, first - pos)
+                for s in range(ns):
+                    prefill_by_append(c, rings[s], s, m, L)
+                pos += m
+            for step in range(512):
+                q, k, v = step_inputs(c, [pos] * ns)
+                plans = c.decoder_step(0, rings, [pos] * ns, 0, L, q.data_ptr(), k.data_ptr(),
+                                       v.data_ptr(), out.data_ptr(), SCALE, hip_stream=stream_ptr())
+                pos += 1
+                if step % 64 == 63:
+                    slots, q_row = plan_slots(plans[3]), q[3, L - 1].cpu().numpy()
+                    got = out[3, L - 1].cpu().numpy().reshape(32, 128)
+                    mimic = oracle_decode(c, 3, L - 1, slots, q_row, mimic=True)
+                    assert np.max(np.abs(got - mimic)) <= TOL[vkv.Q8_0], (pos, step)
+            assert all(rings[s].next_absolute_position == pos for s in range(ns))
+            assert rings[0].wraps == pos // cap
+            check_cache_state(c, [0, ns - 1], range(L), cap, {0: pos, ns - 1: pos})
+            print(f"q8_0 8 streams: 512 steps up to position {pos - 1} ok (cache bit-exact, "
+                  f"{rings[0].wraps} wraps)", flush=True)
+
+
 @pytest.mark.parametrize("dtype", [vkv.F16, vkv.F32, vkv.Q8_0])
 def test_one_pass_full_ring(dtype):
     """26 layers x 8192 slots, one stream: F16 takes the whole-row kernel (a
