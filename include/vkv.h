@@ -58,8 +58,8 @@ typedef enum vkv_status {
 typedef enum vkv_dtype {
     VKV_DTYPE_F32 = 0,
     VKV_DTYPE_F16 = 1,
-    VKV_DTYPE_Q8_0 = 8,
-    /* decoder weights (ggml block formats, 256 elements per block) */
+    VKV_DTYPE_Q8_0 = 8,    /* 34 B per 32: fp16 d, int8 codes (KV rows; also weights) */
+    /* model weights (ggml block formats, 256 elements per block) */
     VKV_DTYPE_Q4_K = 12,   /* 144 B: fp16 d, fp16 dmin, 6-bit scales/mins, 4-bit codes */
     VKV_DTYPE_Q6_K = 14,   /* 210 B: 4+2-bit codes, int8 scales per 16, fp16 d */
     VKV_DTYPE_Q8_K = 15    /* 292 B: f32 d, int8 codes, int16 sums per 16 (activations) */
@@ -359,7 +359,7 @@ vkv_status vkv_q8_0_pack(const float *x, void *blocks, int64_t n, void *hip_stre
 vkv_status vkv_q8_0_unpack(const void *blocks, float *y, int64_t n, void *hip_stream);
 
 /* ---------------------------------------------------------------------------
- * Decoder projections on ggml Q4_K / Q6_K weights: ggml_mul_mat(W, x) for one
+ * Decoder projections on ggml Q4_K / Q6_K / Q8_0 weights: ggml_mul_mat(W, x) for one
  * token (src/voxtral.cpp:2656-2659 Q/K/V, :2857 O, :2878-2882 SwiGLU FFN),
  * with the RMSNorm that precedes them (:2653-2654, :2861-2862) and the ada
  * time conditioning (:2864-2874) fused into the input side.
@@ -369,15 +369,19 @@ vkv_status vkv_q8_0_unpack(const void *blocks, float *y, int64_t n, void *hip_st
  * then h + h * ada; or h = x when norm_w is NULL.  h is quantized to Q8_K
  * (ggml quantize_row_q8_K_ref) and every row is an integer dot product per
  * 256-block, scaled by fp16(d) * d_x (Q4_K: minus fp16(dmin) * d_x * the
- * mins against 32-element sums).  Rows are W's rows in ggml's row-major block
- * layout, i.e. a GGUF tensor's bytes unchanged.
+ * mins against 32-element sums).  For Q8_0 rows (a Q8_0 file,
+ * src/voxtral-quantize.cpp:95-96) h is quantized to q8_0 instead, as ggml's
+ * x86 quantize_row_q8_0 does (d = fp16(amax/127), codes rint(h * 127/amax),
+ * half to even), and each 32-block's integer dot is scaled by fp16(d_w) * d_x.
+ * Rows are W's rows in ggml's row-major block layout, i.e. a GGUF tensor's
+ * bytes unchanged; matrices of one call may mix the three formats.
  * ------------------------------------------------------------------------- */
 #define VKV_MV_MAX_IN 12288      /* n_in limit (multiple of 256) */
 #define VKV_MV_MAX_OUTS 4        /* matrices per call */
 
 typedef struct vkv_mv_out {
-    const void *w;        /* [n_rows][n_in/256] Q4_K or Q6_K blocks, device memory */
-    int32_t dtype;        /* VKV_DTYPE_Q4_K or VKV_DTYPE_Q6_K */
+    const void *w;        /* [n_rows] rows of Q4_K / Q6_K / Q8_0 blocks, device memory, 4-byte aligned */
+    int32_t dtype;        /* VKV_DTYPE_Q4_K, VKV_DTYPE_Q6_K or VKV_DTYPE_Q8_0 */
     int32_t n_rows;
     float *y;             /* [n_rows] */
     const float *add;     /* NULL, or the residual: y = add + W h (may alias y) */
@@ -399,7 +403,7 @@ vkv_status vkv_matvec(const float *x, int64_t n_in, const float *norm_w, const f
 vkv_status vkv_quantize_q8_k(const float *x, int64_t n, const float *norm_w, const float *ada,
                              float eps, void *blocks, void *hip_stream);
 
-/* ggml dequantize_row_q4_K / _q6_K of n elements (n % 256 == 0) to f32: the
+/* ggml dequantize_row_q4_K / _q6_K / _q8_0 of n elements (n % 256 == 0) to f32: the
  * token-embedding lookup (ggml_get_rows on tok_embeddings, src/voxtral.cpp:
  * 3008) for one row of the table. */
 vkv_status vkv_dequantize(int32_t dtype, const void *blocks, int64_t n, float *y,
@@ -535,7 +539,7 @@ vkv_status vkv_adapter_commit(const vkv_adapter *adapter, const vkv_row_ring *en
                               void *workspace, size_t workspace_bytes, void *hip_stream);
 
 /* The decoder step's input row: ggml_get_rows(tok_embeddings, token) +
- * audio embedding (src/voxtral.cpp:3008-3019): row `token` of a Q4_K/Q6_K
+ * audio embedding (src/voxtral.cpp:3008-3019): row `token` of a Q4_K/Q6_K/Q8_0
  * table [n_rows][n_cols], dequantized, plus add[] when add is not NULL. */
 vkv_status vkv_embed(int32_t dtype, const void *table, int32_t n_rows, int64_t n_cols,
                      int32_t token, const float *add, float *y, void *hip_stream);

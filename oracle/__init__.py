@@ -132,6 +132,8 @@ _protos = {
     "orc_row_ring_read": (_i32, [_vp, _i32, _i32, _i64, _i32, _vp]),
     "orc_adapter_commit": (_i32, [_vp, _i32, _i32, _i32, _vp, _i32, _i32, _i64, _i32,
                                   ctypes.c_int, _vp, ctypes.c_int, _vp, ctypes.c_int]),
+    "orc_q8_0_quantize_x86": (None, [_vp, _vp, _i64]),
+    "orc_vec_dot_q8_0_q8_0": (_f32, [_i64, _vp, _vp]),
     "orc_wrow_bytes": (_i64, [ctypes.c_int, _i64]),
     "orc_matvec": (None, [ctypes.c_int, _vp, _i64, _i64, _vp, _vp, ctypes.c_int]),
     "orc_decode_step_mimic_mt": (_f64, [ctypes.c_int, _vp, _vp, _i64, _i64, _i32, _i32, _vp,
@@ -420,11 +422,11 @@ def _f32a(a):
 
 
 def dequantize(dtype, blocks, n):
-    """ggml dequantize_row_q4_K / _q6_K / _q8_K of n elements -> f32."""
+    """ggml dequantize_row_q4_K / _q6_K / _q8_K / _q8_0 of n elements -> f32."""
     blocks = _u8(blocks)
     y = np.empty(n, dtype=np.float32)
     fn = {Q4_K: lib.orc_q4_k_dequantize, Q6_K: lib.orc_q6_k_dequantize,
-          Q8_K: lib.orc_q8_k_dequantize}[dtype]
+          Q8_K: lib.orc_q8_k_dequantize, Q8_0: lib.orc_q8_0_dequantize}[dtype]
     fn(_ptr(blocks), _ptr(y), n)
     return y
 
@@ -436,9 +438,20 @@ def q8_k_quantize(x):
     return out
 
 
+def q8_0_quantize_x86(x):
+    """q8_0 activation blocks (ggml's x86 quantize_row_q8_0: the input side of
+    a product on Q8_0 weights)."""
+    x = _f32a(x).ravel()
+    out = np.empty(x.size // 32 * 34, dtype=np.uint8)
+    lib.orc_q8_0_quantize_x86(_ptr(x), _ptr(out), x.size)
+    return out
+
+
 def vec_dot(dtype, w_row, xq, n):
+    """one row's dot: Q4_K / Q6_K against Q8_K blocks, Q8_0 against q8_0"""
     w_row, xq = _u8(w_row), _u8(xq)
-    fn = lib.orc_vec_dot_q4_k_q8_k if dtype == Q4_K else lib.orc_vec_dot_q6_k_q8_k
+    fn = {Q4_K: lib.orc_vec_dot_q4_k_q8_k, Q6_K: lib.orc_vec_dot_q6_k_q8_k,
+          Q8_0: lib.orc_vec_dot_q8_0_q8_0}[dtype]
     return fn(n, _ptr(w_row), _ptr(xq))
 
 
@@ -464,12 +477,13 @@ def argmax(x):
 
 
 def wrow_bytes(dtype, n_in):
-    return n_in // 256 * BLOCK_BYTES[dtype]
+    return n_in // 32 * 34 if dtype == Q8_0 else n_in // 256 * BLOCK_BYTES[dtype]
 
 
 def matvec(dtype, w, n_rows, n_in, x, n_threads=1):
     """ggml_mul_mat(W, x) as the CPU path computes it: x (already normalised)
-    quantized to Q8_K, one vec_dot per row."""
+    quantized to Q8_K (Q4_K / Q6_K weights) or q8_0 (Q8_0 weights), one
+    vec_dot per row."""
     w, x = _u8(w), _f32a(x)
     assert w.size >= n_rows * wrow_bytes(dtype, n_in) and x.size == n_in
     y = np.empty(n_rows, dtype=np.float32)

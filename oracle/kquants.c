@@ -37,12 +37,28 @@
  *   ggml rms_norm (f32): the sum of x*x (f32 products) accumulated in double,
  *       mean = (float)(sum / n), scale = 1/sqrtf(mean + eps), y = x * scale.
  *
+ *   block_q8_0 (34 B): fp16 d, i8 qs[32].  Value = d * q.  A Q8_0 file
+ *       (src/voxtral-quantize.cpp:95-96) stores every matrix so; its
+ *       products take a q8_0 activation (Q8_0's vec_dot_type), quantized by
+ *       quantize_row_q8_0 as the x86 CPU backend compiles it (the AVX/AVX2
+ *       branch: amax = max |x| of the 32 elements, d = amax / 127 stored as
+ *       fp16 with F16C's round to nearest even, id = amax ? 127 / amax : 0,
+ *       q = round half to even (x * id)); the portable
+ *       quantize_row_q8_0_ref, which the q8_0 KV rows follow, takes
+ *       id = 1 / d and rounds half away from zero instead.
+ *   ggml_vec_dot_q8_0_q8_0 (x86 AVX2 branch): per block, d = fp16(d_w) *
+ *       fp16(d_x) in f32; eight f32 lanes, lane k holding the exact integer
+ *       sum of the products of elements 4k .. 4k+3, accumulate
+ *       acc[k] = fma(d, sum_k, acc[k]) over the row's blocks; the row's value
+ *       is ((acc0 + acc4) + (acc2 + acc6)) + ((acc1 + acc5) + (acc3 + acc7)).
+ *
  * Pinned by tests/test_kquants.py: pack/unpack round trips of constructed
  * blocks against the formulas above, the integer dot products against fp64
- * dots of the dequantized operands, and closed forms of the Q8_K quantizer
- * (extreme element to -127, tie to the first occurrence, error <= d/2).  No
- * ggml output is available offline, so bitwise agreement with ggml's own
- * binaries is parity unpinned.
+ * dots of the dequantized operands, and closed forms of the Q8_K and q8_0
+ * activation quantizers (extreme element to -127 / +-127, tie to the first
+ * occurrence, half-way codes to even, error <= d/2).  No ggml output is
+ * available offline, so bitwise agreement with ggml's own binaries (the f32
+ * order of the per-block sums) is parity unpinned.
  */
 #include "vkv_oracle.h"
 
@@ -213,6 +229,38 @@ float orc_vec_dot_q6_k_q8_k(int64_t n, const uint8_t *w, const uint8_t *x) {
     return sumf;
 }
 
+void orc_q8_0_quantize_x86(const float *x, uint8_t *blocks, int64_t n) {
+    for (int64_t b = 0; b < n / 32; ++b) {
+        const float *xb = x + b * 32;
+        uint8_t *blk = blocks + b * 34;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(xb[j]));
+        const float d = amax / 127.0f;
+        const uint16_t dh = orc_f32_to_f16(d);
+        memcpy(blk, &dh, 2);
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const int8_t q = (int8_t)nearest_int(xb[j] * id);
+            memcpy(blk + 2 + j, &q, 1);
+        }
+    }
+}
+
+float orc_vec_dot_q8_0_q8_0(int64_t n, const uint8_t *w, const uint8_t *x) {
+    float acc[8] = {0};
+    for (int64_t b = 0; b < n / 32; ++b) {
+        const uint8_t *wb = w + b * 34, *xb = x + b * 34;
+        const float d = h2f(wb) * h2f(xb);
+        const int8_t *qw = (const int8_t *)(wb + 2), *qx = (const int8_t *)(xb + 2);
+        for (int k = 0; k < 8; ++k) {
+            int s = 0;
+            for (int e = 4 * k; e < 4 * k + 4; ++e) s += qw[e] * qx[e];
+            acc[k] = fmaf(d, (float)s, acc[k]);
+        }
+    }
+    return ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+}
+
 void orc_rms_norm(const float *x, float *y, int64_t n, float eps) {
     double sum = 0.0;
     for (int64_t i = 0; i < n; ++i) sum += (double)(x[i] * x[i]);
@@ -258,6 +306,7 @@ int32_t orc_argmax(const float *x, int64_t n) {
 }
 
 int64_t orc_wrow_bytes(int dtype, int64_t n_in) {
+    if (dtype == ORC_Q8_0) return (n_in / 32) * 34;
     return (n_in / QK) * (dtype == ORC_Q4_K ? 144 : dtype == ORC_Q6_K ? 210 : 292);
 }
 
@@ -273,17 +322,20 @@ static void *mv_worker(void *p) {
     const mv_job *j = (const mv_job *)p;
     const int64_t rb = orc_wrow_bytes(j->dtype, j->n_in);
     for (int64_t r = j->r0; r < j->r1; ++r)
-        j->y[r] = j->dtype == ORC_Q4_K ? orc_vec_dot_q4_k_q8_k(j->n_in, j->w + r * rb, j->xq)
-                                       : orc_vec_dot_q6_k_q8_k(j->n_in, j->w + r * rb, j->xq);
+        j->y[r] = j->dtype == ORC_Q4_K   ? orc_vec_dot_q4_k_q8_k(j->n_in, j->w + r * rb, j->xq)
+                  : j->dtype == ORC_Q8_0 ? orc_vec_dot_q8_0_q8_0(j->n_in, j->w + r * rb, j->xq)
+                                         : orc_vec_dot_q6_k_q8_k(j->n_in, j->w + r * rb, j->xq);
     return NULL;
 }
 
-/* ggml_mul_mat(W, x) on the CPU path: x quantized once to Q8_K, then one
- * vec_dot per row of W; rows are split over n_threads */
+/* ggml_mul_mat(W, x) on the CPU path: x quantized once to the weight type's
+ * vec_dot_type (Q8_K for Q4_K / Q6_K, q8_0 for Q8_0), then one vec_dot per
+ * row of W; rows are split over n_threads */
 void orc_matvec(int dtype, const uint8_t *w, int64_t n_rows, int64_t n_in, const float *x,
                 float *y, int n_threads) {
     uint8_t *xq = (uint8_t *)malloc((size_t)(n_in / QK) * 292);
-    orc_q8_k_quantize(x, xq, n_in);
+    if (dtype == ORC_Q8_0) orc_q8_0_quantize_x86(x, xq, n_in);
+    else orc_q8_k_quantize(x, xq, n_in);
     if (n_threads < 1) n_threads = 1;
     if (n_threads > 64) n_threads = 64;
     pthread_t th[64];

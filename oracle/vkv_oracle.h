@@ -239,6 +239,10 @@ void orc_q8_k_quantize(const float *x, uint8_t *blocks, int64_t n);
 void orc_q8_k_dequantize(const uint8_t *blocks, float *y, int64_t n);
 float orc_vec_dot_q4_k_q8_k(int64_t n, const uint8_t *w, const uint8_t *x);
 float orc_vec_dot_q6_k_q8_k(int64_t n, const uint8_t *w, const uint8_t *x);
+/* q8_0 activation blocks as ggml's x86 quantize_row_q8_0 writes them
+ * (id = 127/amax, round half to even), and the Q8_0 x q8_0 row dot */
+void orc_q8_0_quantize_x86(const float *x, uint8_t *blocks, int64_t n);
+float orc_vec_dot_q8_0_q8_0(int64_t n, const uint8_t *w, const uint8_t *x);
 void orc_rms_norm(const float *x, float *y, int64_t n, float eps);
 /* rms_norm(x) * norm_w, then h + h * ada when ada is given; a copy of x when
  * norm_w is NULL */

@@ -159,7 +159,7 @@ def test_error_statuses_without_device():
     assert L.vkv_matvec(x, 3072, None, None, 1e-5, outs, 2, 7, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_matvec(x, 3072, None, None, 1e-5, outs, 2, vkv.MV_SWIGLU,
                         None) == vkv.INVALID_ARGUMENT          # SwiGLU needs equal dtypes
-    wrong = (vkv.MvOut * 1)(vkv.MvOut(16, vkv.Q8_0, 8, 16, None))
+    wrong = (vkv.MvOut * 1)(vkv.MvOut(16, 2, 8, 16, None))       # ggml Q4_0: not taken
     assert L.vkv_matvec(x, 3072, None, None, 1e-5, wrong, 1, 0, None) == vkv.INVALID_ARGUMENT
     huge = (vkv.MvOut * 1)(vkv.MvOut(16, vkv.Q6_K, 1 << 30, 16, None))
     assert L.vkv_matvec(x, 3072, None, None, 1e-5, huge, 1, 0, None) == vkv.INVALID_ARGUMENT
@@ -174,7 +174,7 @@ def test_error_statuses_without_device():
                         None) == vkv.INVALID_ARGUMENT                 # norm_b without norm_w
     assert L.vkv_matmul(x, 16, 1280, None, None, None, 1e-5, mo, 1, 0, 4096, 16,
                         None) == vkv.BUFFER_TOO_SMALL
-    assert L.vkv_dequantize(vkv.Q8_0, 16, 256, 16, None) == vkv.INVALID_ARGUMENT
+    assert L.vkv_dequantize(vkv.F16, 16, 256, 16, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_embed(vkv.Q6_K, 16, 10, 3072, 10, None, 16, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_embed(vkv.Q6_K, 16, 10, 3072, -1, None, 16, None) == vkv.INVALID_ARGUMENT
     assert L.vkv_argmax(x, 0, 16, None) == vkv.INVALID_ARGUMENT
@@ -219,7 +219,7 @@ def test_error_statuses_without_device():
     assert "multiple of 4" in vkv.last_error()
     assert L.vkv_adapter_commit(ctypes.byref(ad), ctypes.byref(aemb), ctypes.byref(enc), 0, 1,
                                 4096, 1 << 20, None) == vkv.INVALID_ARGUMENT   # widths swapped
-    bad = vkv.Adapter(16, 16, vkv.Q8_0, vkv.Q4_K, 1280, 3072, 4)
+    bad = vkv.Adapter(16, 16, 2, vkv.Q4_K, 1280, 3072, 4)
     assert L.vkv_adapter_workspace(ctypes.byref(bad), 1) == 0
     assert L.vkv_encoder_chunk_ring(None, 0, None, 750, ctypes.byref(em), None, None, None, 0,
                                     None) == vkv.INVALID_ARGUMENT

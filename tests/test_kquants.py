@@ -189,6 +189,114 @@ def test_vec_dot_against_fp64(dtype, n):
     assert abs(got - terms.sum()) <= 4e-6 * np.abs(terms).sum()
 
 
+def pack_q8_0(d, q):
+    """One block_q8_0 from d (f16-representable) and codes q[32] (int8)."""
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.frombuffer(f16_bits(d).tobytes(), np.uint8)
+    blk[2:] = np.asarray(q, np.int8).view(np.uint8)
+    return blk
+
+
+def q8_0_fields(blocks):
+    b = blocks.reshape(-1, 34)
+    d = b[:, 0:2].copy().view(np.float16).ravel().astype(np.float32)
+    return d, b[:, 2:].copy().view(np.int8)
+
+
+def random_q8_0(rng, n_blocks):
+    """Q8_0 weight blocks (codes in [-127, 127], the quantizer's range) and the
+    exact (fp64) weight values."""
+    d = rng.uniform(1e-3, 3e-2, n_blocks).astype(np.float16)
+    q = rng.integers(-127, 128, (n_blocks, 32))
+    blocks = np.concatenate([pack_q8_0(d[i], q[i]) for i in range(n_blocks)])
+    return blocks, (d.astype(np.float64)[:, None] * q).ravel()
+
+
+def test_q8_0_weights_dequantize_to_d_times_q():
+    rng = np.random.default_rng(95)
+    blocks, exact = random_q8_0(rng, 40)
+    got = oracle.dequantize(oracle.Q8_0, blocks, exact.size)
+    np.testing.assert_array_equal(got, exact.astype(np.float32))   # d * q is exact in f32
+
+
+def test_q8_0_activation_closed_forms():
+    rng = np.random.default_rng(96)
+    x = (rng.standard_normal(32 * 64) * rng.uniform(0.01, 50, 64).repeat(32)).astype(np.float32)
+    d, qs = q8_0_fields(oracle.q8_0_quantize_x86(x))
+    xb = x.reshape(-1, 32)
+    for i in range(xb.shape[0]):
+        j = int(np.argmax(np.abs(xb[i])))
+        amax = np.abs(xb[i, j])
+        assert qs[i, j] == (127 if xb[i, j] > 0 else -127)
+        assert np.all(np.abs(qs[i].astype(int)) <= 127)
+        # d: amax / 127 in f32, stored as f16 (numpy's conversion rounds to nearest even)
+        assert d[i] == np.float32(np.float16(amax / np.float32(127)))
+        # the codes come from 127 / amax, not from the stored d: |q d' - x| <= d' / 2
+        # with d' = amax / 127, and the f16 rounding of d adds at most 127 d 2^-11
+        err = np.abs(float(d[i]) * qs[i] - xb[i].astype(np.float64))
+        assert np.all(err <= float(amax) / 127 * (0.5 + 1e-5) + 127 * abs(float(d[i])) * 2.0 ** -11)
+
+
+def test_q8_0_activation_ties_scale_source_and_zero():
+    x = np.zeros(32 * 4, np.float32)
+    # block 0: amax = 127 gives id = 1 and d = 1: half-way values round to even
+    # (the portable _ref quantizer would give 3, 4, -3, -4, 1, -1, 2, 127)
+    x[0:9] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5, -0.5, 1.5, 126.5]
+    # block 1: the largest magnitude negative
+    x[32], x[33] = -127.0, 64.0
+    # block 2: amax = 100: 50 * f32(127 / 100) = 63.5 exactly, a tie, -> 64;
+    # a quantizer taking id from the stored f16 d (0.787598) would give 63
+    x[64], x[65] = 100.0, 50.0
+    # block 3: all zero
+    d, qs = q8_0_fields(oracle.q8_0_quantize_x86(x))
+    assert d[0] == 1.0
+    assert list(qs[0, :9]) == [127, 2, 4, -2, -4, 0, 0, 2, 126]
+    assert (qs[1, 0], qs[1, 1]) == (-127, 64)
+    assert d[2] == np.float32(np.float16(np.float32(100) / np.float32(127)))
+    assert (qs[2, 0], qs[2, 1]) == (127, 64)
+    assert d[3] == 0.0 and not qs[3].any()
+
+
+@pytest.mark.parametrize("n", [32, 256, 3072, 9216])
+def test_vec_dot_q8_0_against_fp64(n):
+    rng = np.random.default_rng(n + 8)
+    w, wv = random_q8_0(rng, n // 32)
+    x = rng.standard_normal(n).astype(np.float32)
+    xq = oracle.q8_0_quantize_x86(x)
+    got = oracle.vec_dot(oracle.Q8_0, w, xq, n)
+    xv = oracle.dequantize(oracle.Q8_0, xq, n).astype(np.float64)
+    terms = wv * xv
+    assert abs(got - terms.sum()) <= 4e-6 * np.abs(terms).sum()
+
+
+def test_vec_dot_q8_0_every_element_counts():
+    # unit weights (d = 1, codes 1) against integer activations with amax 127
+    # (d = 1, codes = values): the dot is the plain sum of the values
+    n = 96
+    w = np.concatenate([pack_q8_0(1.0, np.ones(32, int)) for _ in range(n // 32)])
+    x = np.arange(-47, 49, dtype=np.float32)
+    x[[0, 40, 80]] = [-127.0, 127.0, -127.0]
+    for e in (0, 1, 3, 4, 31, 32, 35, 63, 64, 95):
+        xe = x.copy()
+        xe[e] += 0.0 if abs(xe[e]) == 127 else 1.0
+        got = oracle.vec_dot(oracle.Q8_0, w, oracle.q8_0_quantize_x86(xe), n)
+        assert got == float(xe.sum())
+
+
+def test_matvec_q8_0_rows_and_threads():
+    rng = np.random.default_rng(10)
+    n_rows, n = 48, 3072
+    w, _ = random_q8_0(rng, n_rows * n // 32)
+    x = rng.standard_normal(n).astype(np.float32)
+    y1 = oracle.matvec(oracle.Q8_0, w, n_rows, n, x, 1)
+    np.testing.assert_array_equal(y1, oracle.matvec(oracle.Q8_0, w, n_rows, n, x, 4))
+    xq = oracle.q8_0_quantize_x86(x)
+    rb = oracle.wrow_bytes(oracle.Q8_0, n)
+    assert rb == n // 32 * 34
+    for r in (0, 17, 47):
+        assert y1[r] == oracle.vec_dot(oracle.Q8_0, w[r * rb:(r + 1) * rb], xq, n)
+
+
 def test_rms_norm_and_ada():
     rng = np.random.default_rng(7)
     for n in (256, 3072, 9216):

@@ -1096,8 +1096,9 @@ int device_cus() {
     return cus;
 }
 
+// bytes of 256 weights of a product's weight format (Q8_0: 8 blocks of 34)
 int64_t kq_block_bytes(int32_t dtype) {
-    return dtype == VKV_DTYPE_Q4_K ? 144 : dtype == VKV_DTYPE_Q6_K ? 210 : 0;
+    return dtype == VKV_DTYPE_Q4_K ? 144 : dtype == VKV_DTYPE_Q6_K ? 210 : dtype == VKV_DTYPE_Q8_0 ? 272 : 0;
 }
 
 vkv_status check_mv_input(const char *what, const float *x, int64_t n_in, const float *norm_w,
@@ -1272,7 +1273,8 @@ vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float
     for (int32_t k = 0; k < n_outs; ++k) {
         const vkv_mm_out &o = outs[k];
         const int64_t bb = kq_block_bytes(o.dtype);
-        if (!bb) return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: weight dtype %d", o.dtype);
+        if (!bb || o.dtype == VKV_DTYPE_Q8_0)
+            return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: weight dtype %d", o.dtype);
         if (!o.w || (!o.y && !(swiglu && k == 1)) || o.n_rows < 1)
             return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: matrix %d: null pointer or no rows", k);
         if ((int64_t)o.n_rows * (n_in / 256) * bb > (int64_t)0xFFFFFE00)

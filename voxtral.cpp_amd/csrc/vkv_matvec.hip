@@ -5,7 +5,11 @@
 // (src/voxtral-quantize.cpp:148-159), computed the way ggml's CPU path does:
 // x is quantized to Q8_K (f32 scale per 256, int8 codes, 16-element sums) and
 // each row is an integer dot product per block, scaled by fp16(d) * d_x (and
-// for Q4_K minus fp16(dmin) * d_x * sum of mins x 32-element sums).
+// for Q4_K minus fp16(dmin) * d_x * sum of mins x 32-element sums).  Q8_0
+// rows (the files src/voxtral-quantize.cpp:95-96 writes) take a q8_0 image of
+// x instead (ggml's x86 quantize_row_q8_0: fp16 d per 32 elements, codes
+// rint(x * 127 / amax)), and each 32-weight block contributes its integer
+// dot times fp16(d_w) * d_x.
 //
 //   k_matvec     -- one launch for up to four matrices that read the same x:
 //                   prologue = optional RMSNorm x weight (x (1 + ada)) and the
@@ -16,7 +20,7 @@
 //                   store, residual add, or silu(W0 x) * (W1 x).
 //   k_q8k_quant  -- the same prologue alone, to global memory in ggml's
 //                   block_q8_K layout.
-//   k_kq_dequant -- ggml dequantize_row_q4_K / _q6_K (get_rows on the token
+//   k_kq_dequant -- ggml dequantize_row_q4_K / _q6_K / _q8_0 (get_rows on the token
 //                   embedding table, src/voxtral.cpp:3008, + the audio
 //                   embedding, :3019).
 //   k_argmax     -- ggml_argmax of the logits (src/voxtral.cpp:2970).
@@ -39,9 +43,15 @@ typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
 
 constexpr int kQ4Bytes = 144;
 constexpr int kQ6Bytes = 210;
+constexpr int kQ8Bytes = 34;                   // one block_q8_0: fp16 d, 32 int8
+constexpr int kQ8Per256 = 8 * kQ8Bytes;        // bytes of 256 Q8_0 weights
+
+// the weight format a work group streams (one per work group)
+enum WKind { kWQ4 = 0, kWQ6 = 1, kWQ8 = 2 };
 constexpr uint32_t kOob = 0xFFFFFF00u;   // buffer offset past every resource: loads read 0
 
-// Q8_K image of the input vector, per work group.
+// Q8_K image of the input vector, per work group (q8_0 image for Q8_0 rows:
+// xq and, in bs32, the f32 value of each 32-element block's fp16 d).
 struct ActSmem {
     int8_t xq[kMvMaxIn];                 // codes
     int32_t bs32[kMvMaxIn / 32];         // sums of 32 codes (Q4_K sub-blocks)
@@ -156,6 +166,34 @@ __device__ __forceinline__ QBlock16 q8k_block16(const float (&e)[16], int l) {
     return r;
 }
 
+// One ggml block_q8_0 of the input held by lanes 2k, 2k + 1 of a 16-lane
+// row, 16 elements each: quantize_row_q8_0 as ggml's x86 CPU backend computes
+// it -- amax over the 32 elements, d = amax / 127 rounded to fp16 (nearest
+// even), codes rint(x * (127 / amax)) (one f32 product, half to even).
+struct QBlock0 {
+    uint32_t packed[4];
+    float d;   // f32 value of the fp16 d
+};
+__device__ __forceinline__ QBlock0 q8_0_block16(const float (&e)[16]) {
+#pragma clang fp contract(off)
+    float am = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) am = fmaxf(am, fabsf(e[k]));
+    am = fmaxf(am, dppf<0xB1>(am));   // the partner lane's half
+    const float id = am != 0.0f ? 127.0f / am : 0.0f;
+    QBlock0 r;
+    r.d = (float)(_Float16)(am / 127.0f);
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        int q[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) q[t] = (int)__builtin_rintf(e[4 * w + t] * id);
+        r.packed[w] = (uint32_t)(q[0] & 255) | (uint32_t)(q[1] & 255) << 8 |
+                      (uint32_t)(q[2] & 255) << 16 | (uint32_t)(q[3] & 255) << 24;
+    }
+    return r;
+}
+
 // Q8_K quantization of rms_norm(x) * norm_w (* (1 + ada)), or of x itself
 // (norm_w == nullptr).  In round k a wave holds 4 blocks, one per 16-lane
 // row: lane (row r, l) has elements [16 l, 16 l + 16) of block 16 k + 4 w +
@@ -171,7 +209,8 @@ __device__ __forceinline__ QBlock16 q8k_block16(const float (&e)[16], int l) {
 // act_finish then waits for them alone.  NBW = 4 x rounds (float4 per lane);
 // with NORM_EARLY the norm weights (and the ada row) are loaded up front too,
 // with BIAS_EARLY the norm's bias as well (absent vectors read x instead:
-// one load path, unused).
+// one load path, unused).  Q80: the q8_0 image instead of Q8_K (codes in xq,
+// the blocks' d in bs32; the same rounding of the normed input).
 template <int NBW, bool NORM_EARLY, bool BIAS_EARLY = false>
 struct ActRegs {
     float4 x[NBW];
@@ -202,7 +241,7 @@ __device__ __forceinline__ void act_load(ActRegs<NBW, NE, NB> &r, const float *_
     }
 }
 
-template <int NBW, bool NE, bool NB>
+template <int NBW, bool NE, bool NB, bool Q80 = false>
 __device__ __forceinline__ void act_finish(const ActRegs<NBW, NE, NB> &r, int n,
                                            const float *__restrict__ nw,
                                            const float *__restrict__ ada, float eps, ActSmem &sm,
@@ -289,6 +328,14 @@ __device__ __forceinline__ void act_finish(const ActRegs<NBW, NE, NB> &r, int n,
                 }
             }
         }
+        if constexpr (Q80) {
+            const QBlock0 qb = q8_0_block16(e);
+            if (!valid) continue;
+            *reinterpret_cast<u32x4_t *>(&sm.xq[256 * b + 16 * l]) =
+                u32x4_t{qb.packed[0], qb.packed[1], qb.packed[2], qb.packed[3]};
+            if ((l & 1) == 0) sm.bs32[8 * b + (l >> 1)] = __builtin_bit_cast(int32_t, qb.d);
+            continue;
+        }
         const QBlock16 qb = q8k_block16(e, l);
         if (!valid) continue;
         if (gout) {
@@ -350,6 +397,23 @@ __device__ __forceinline__ FragQ6 load_q6(__amdgpu_buffer_rsrc_t rs, uint32_t of
     return f;
 }
 
+// Q8_0: a lane task is two consecutive 34-byte blocks (64 weights) at byte
+// 68 t of the row, 4-byte aligned (rows are multiples of 272 bytes): 17 dwords.
+struct FragQ8 {
+    u32x4_t a, b, c, e;
+    uint32_t x;
+};
+
+__device__ __forceinline__ FragQ8 load_q8(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    FragQ8 f;
+    f.a = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    f.b = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16, 0, 0));
+    f.c = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 32, 0, 0));
+    f.e = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, off + 48, 0, 0));
+    f.x = __builtin_amdgcn_raw_buffer_load_b32(rs, off + 64, 0, 0);
+    return f;
+}
+
 // The activation side of one lane's task for a step (same for every row).
 struct XFrag {
     i32x4_t x[4];     // 64 codes
@@ -383,6 +447,20 @@ __device__ __forceinline__ XFrag x_q6(const ActSmem &sm, int t) {
     f.bs[2] = s.z;
     f.bs[3] = s.w;
     f.dx = sm.dx[b];
+    return f;
+}
+
+// q8_0 image: the task's 64 codes and its two blocks' d (f32 bits in bs[0..1])
+__device__ __forceinline__ XFrag x_q8(const ActSmem &sm, int t) {
+    XFrag f;
+    const i32x4_t *p = reinterpret_cast<const i32x4_t *>(&sm.xq[64 * t]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.x[i] = p[i];
+    const u32x2_t s = *reinterpret_cast<const u32x2_t *>(&sm.bs32[2 * t]);
+    f.bs[0] = (int32_t)s.x;
+    f.bs[1] = (int32_t)s.y;
+    f.bs[2] = f.bs[3] = 0;
+    f.dx = 0.0f;
     return f;
 }
 
@@ -446,10 +524,31 @@ __device__ __forceinline__ float compute_q6(const FragQ6 &f, const XFrag &x, uin
     for (int g = 0; g < 4; ++g) isum += sc[g] * (dot16(q[g], x.x[g], 0) - 32 * x.bs[g]);
     return (h2f(f.dh) * x.dx) * (float)isum;
 }
+// Two Q8_0 blocks: block 2t's d is the first half of dword 0 and its codes
+// bytes 2..33 (realigned by 2), block 2t + 1's d the second half of dword 8
+// and its codes dwords 9..16; each block's integer dot times fp16(d_w) * d_x
+// (ggml_vec_dot_q8_0_q8_0's per-block term).
+__device__ __forceinline__ float compute_q8(const FragQ8 &f, const XFrag &x) {
+    const uint32_t w[17] = {f.a.x, f.a.y, f.a.z, f.a.w, f.b.x, f.b.y, f.b.z, f.b.w, f.c.x,
+                            f.c.y, f.c.z, f.c.w, f.e.x, f.e.y, f.e.z, f.e.w, f.x};
+    uint32_t q0[2][4], q1[2][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        q0[i >> 2][i & 3] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+        q1[i >> 2][i & 3] = w[9 + i];
+    }
+    const int s0 = dot16(q0[1], x.x[1], dot16(q0[0], x.x[0], 0));
+    const int s1 = dot16(q1[1], x.x[3], dot16(q1[0], x.x[2], 0));
+    const float d0 = h2f(w[0] & 0xffffu) * __builtin_bit_cast(float, x.bs[0]);
+    const float d1 = h2f(w[8] >> 16) * __builtin_bit_cast(float, x.bs[1]);
+    return (float)s0 * d0 + (float)s1 * d1;
+}
 
-
-__device__ __forceinline__ XFrag xfrag(const ActSmem &sm, bool q4, int t) {
-    return q4 ? x_q4(sm, t) : x_q6(sm, t);
+template <int WK>
+__device__ __forceinline__ XFrag xfrag(const ActSmem &sm, int t) {
+    if constexpr (WK == kWQ4) return x_q4(sm, t);
+    else if constexpr (WK == kWQ8) return x_q8(sm, t);
+    else return x_q6(sm, t);
 }
 
 // Where unit u of a wave reads its weights.  The buffer descriptor is built
@@ -464,17 +563,19 @@ struct UnitMap {
     int tasks, lane, mats, units;
     bool swiglu;
 
-    template <int S, bool Q4>
+    template <int S, int WK>
     __device__ __forceinline__ auto load(int u) const {
         const int step = u % S;
         const bool second = swiglu && ((u / S) & 1);
         const int row = row0 + u / (S * mats);
         const int t = 64 * step + lane;
-        const uint32_t off =
-            t < tasks && u < units ? (uint32_t)row * rbytes + (uint32_t)(t >> 2) * bbytes : kOob;
+        // a Q8_0 task's two blocks are 68 bytes from the previous task's
+        const uint32_t toff = WK == kWQ8 ? (uint32_t)t * (2 * kQ8Bytes) : (uint32_t)(t >> 2) * bbytes;
+        const uint32_t off = t < tasks && u < units ? (uint32_t)row * rbytes + toff : kOob;
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t *>(second ? w1 : w0), (short)0, (int)(second ? n1 : n0), 0x00020000);
-        if constexpr (Q4) return load_q4(rs, off, t & 3);
+        if constexpr (WK == kWQ4) return load_q4(rs, off, t & 3);
+        else if constexpr (WK == kWQ8) return load_q8(rs, off);
         else return load_q6(rs, off, (t >> 1) & 1, t & 1);
     }
 };
@@ -524,10 +625,11 @@ __device__ __forceinline__ void argmax_publish(const MvArgs &a, unsigned long lo
 // Unit u of a wave = (row, step): step s of a row covers lane tasks
 // [64 s, 64 s + 64) of the row's 4 * nb quarter blocks.  With SWIGLU the rows
 // alternate between the two matrices: u -> (pair u / 2S, matrix (u / S) & 1).
-// Q4 (the work group's weight dtype) is a template parameter so that every
+// WK (the work group's weight format) is a template parameter so that every
 // load writes its final registers (a load feeding a merge of two paths would
-// be copied, and the copy waits for the load).
-template <int S, int D4, int D6, bool ONE, bool Q4, bool AMAX, bool NE>
+// be copied, and the copy waits for the load).  Q8_0 rows keep D6 units in
+// flight (17 dwords a task against Q6_K's 19).
+template <int S, int D4, int D6, bool ONE, int WK, bool AMAX, bool NE>
 __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, const MvOut &ob,
                                             int row0, int nrow, ActSmem &sm) {
     const int lane = threadIdx.x & 63;
@@ -535,16 +637,16 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
     const int mats = swiglu ? 2 : 1;
     const int units = nrow * S * mats;
     const int nb = a.n_in >> 8, tasks = 4 * nb;
-    const uint32_t bbytes = Q4 ? kQ4Bytes : kQ6Bytes;
+    const uint32_t bbytes = WK == kWQ4 ? kQ4Bytes : WK == kWQ8 ? kQ8Per256 : kQ6Bytes;
     const uint32_t rbytes = (uint32_t)nb * bbytes;
     const UnitMap um{o0.w, ob.w, rbytes * (uint32_t)o0.n_rows, rbytes * (uint32_t)ob.n_rows, row0,
                      rbytes, bbytes, tasks, lane, mats, units, swiglu};
 
-    constexpr int D = Q4 ? D4 : D6;           // units in flight per dtype
+    constexpr int D = WK == kWQ4 ? D4 : D6;   // units in flight per dtype
     constexpr int NBW = S == 1 ? 4 : 4 * S;   // n_in <= 4096 / 12288
     ActRegs<NBW, NE> ar;
     act_load(ar, a.x, a.n_in, a.norm_w, a.ada);
-    using Frag = std::conditional_t<Q4, FragQ4, FragQ6>;
+    using Frag = std::conditional_t<WK == kWQ4, FragQ4, std::conditional_t<WK == kWQ8, FragQ8, FragQ6>>;
     // Every weight load is unconditional (units past the end read zeros):
     // a load issued on one path only makes the compiler's wait counts assume
     // it absent, and the input quantization then waited for all of them.
@@ -555,7 +657,7 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < D; ++k) {
-        f[k] = um.load<S, Q4>(k);
+        f[k] = um.load<S, WK>(k);
         __builtin_amdgcn_sched_barrier(0);
     }
     // The residual of the wave's rows (lane l: row row0 + l; a wave has at
@@ -564,9 +666,9 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
     const float *ap = o0.add ? o0.add : o0.y;
     const float addv = ap[min(row0 + min(lane, max(nrow - 1, 0)), o0.n_rows - 1)];
     __builtin_amdgcn_sched_barrier(0);
-    act_finish(ar, a.n_in, a.norm_w, a.ada, a.eps, sm, nullptr);
+    act_finish<NBW, NE, false, WK == kWQ8>(ar, a.n_in, a.norm_w, a.ada, a.eps, sm, nullptr);
 
-    const XFrag xr = xfrag(sm, Q4, min(lane, tasks - 1));   // the only step when S == 1
+    const XFrag xr = xfrag<WK>(sm, min(lane, tasks - 1));   // the only step when S == 1
 
     float acc = 0.0f, first = 0.0f;
     unsigned long long best = 0;   // argmax key: order key of the value << 32 | row
@@ -575,10 +677,12 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
         const int step = u % S, m = swiglu ? (u / S) & 1 : 0;
         const int row = row0 + u / (S * mats);
         const int t = 64 * step + lane;
-        const XFrag xf = S == 1 ? xr : xfrag(sm, Q4, min(t, tasks - 1));
+        const XFrag xf = S == 1 ? xr : xfrag<WK>(sm, min(t, tasks - 1));
         float c;
-        if constexpr (Q4) {
+        if constexpr (WK == kWQ4) {
             c = compute_q4(fr, xf, t & 3);
+        } else if constexpr (WK == kWQ8) {
+            c = compute_q8(fr, xf);
         } else {
             // Q6_K block (row, b) starts at 210 (row nb + b): 2 mod 4 when odd
             const uint32_t mis = 2u * (uint32_t)((row * nb + (t >> 2)) & 1);
@@ -621,14 +725,14 @@ __device__ __forceinline__ void matvec_body(const MvArgs &a, const MvOut &o0, co
                 // so it can write the slot's own registers (a load into other
                 // registers is copied back at the loop's end, and the copy
                 // waits for it)
-                f[k] = um.load<S, Q4>(u0 + k + D);
+                f[k] = um.load<S, WK>(u0 + k + D);
             }
         }
     }
     if constexpr (AMAX) argmax_publish(a, best);
 }
 
-// D4 / D6: a wave's units in flight for Q4_K / Q6_K rows; ONE: every wave's
+// D4 / D6: a wave's units in flight for Q4_K / Q6_K (and Q8_0) rows; ONE: every wave's
 // units fit (the launch picks it from the units per wave, so that a decoder
 // product's wave requests all its weights at once and streams nothing).
 template <int S, int D4, int D6, bool ONE, bool AMAX>
@@ -648,11 +752,13 @@ __global__ void __launch_bounds__(256) k_matvec(MvArgs a) {
     // With a norm (S == 1: the inputs of up to 4096), its weights (and the ada
     // row) are requested together with x, so the norm costs one round trip.
     if (S == 1 && a.norm_w) {
-        if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D4, D6, ONE, true, AMAX, true>(a, o0, ob, row0, nrow, sm);
-        else matvec_body<S, D4, D6, ONE, false, AMAX, true>(a, o0, ob, row0, nrow, sm);
+        if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D4, D6, ONE, kWQ4, AMAX, true>(a, o0, ob, row0, nrow, sm);
+        else if (o0.dtype == VKV_DTYPE_Q8_0) matvec_body<S, D4, D6, ONE, kWQ8, AMAX, true>(a, o0, ob, row0, nrow, sm);
+        else matvec_body<S, D4, D6, ONE, kWQ6, AMAX, true>(a, o0, ob, row0, nrow, sm);
     } else {
-        if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D4, D6, ONE, true, AMAX, false>(a, o0, ob, row0, nrow, sm);
-        else matvec_body<S, D4, D6, ONE, false, AMAX, false>(a, o0, ob, row0, nrow, sm);
+        if (o0.dtype == VKV_DTYPE_Q4_K) matvec_body<S, D4, D6, ONE, kWQ4, AMAX, false>(a, o0, ob, row0, nrow, sm);
+        else if (o0.dtype == VKV_DTYPE_Q8_0) matvec_body<S, D4, D6, ONE, kWQ8, AMAX, false>(a, o0, ob, row0, nrow, sm);
+        else matvec_body<S, D4, D6, ONE, kWQ6, AMAX, false>(a, o0, ob, row0, nrow, sm);
     }
 }
 
@@ -664,7 +770,7 @@ __global__ void __launch_bounds__(256) k_q8k_quant(const float *x, int n, const 
     act_finish(r, n, nw, ada, eps, sm, out);
 }
 
-// ggml dequantize_row_q4_K / _q6_K of elements i8 .. i8 + 7 of a row
+// ggml dequantize_row_q4_K / _q6_K / _q8_0 of elements i8 .. i8 + 7 of a row
 __device__ __forceinline__ void kq_dequant8(int dtype, const uint8_t *__restrict__ src, int64_t i8,
                                             float out[8]) {
 #pragma clang fp contract(off)
@@ -690,6 +796,13 @@ __device__ __forceinline__ void kq_dequant8(int dtype, const uint8_t *__restrict
             const int q = (j & 1) ? (qs[i] >> 4) : (qs[i] & 15);
             out[i] = d1 * (float)q - m1;
         }
+    } else if (dtype == VKV_DTYPE_Q8_0) {
+        // dequantize_row_q8_0: code * f32(d), a block per 32 elements
+        const uint8_t *blk = src + (i8 >> 5) * kQ8Bytes;
+        const float d = h2f(blk[0] | blk[1] << 8);
+        const int8_t *qs = reinterpret_cast<const int8_t *>(blk + 2 + (i8 & 31));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[i] = (float)qs[i] * d;
     } else {
         const uint8_t *blk = src + b * kQ6Bytes;
         const float d = h2f(blk[208] | blk[209] << 8);
@@ -706,7 +819,7 @@ __device__ __forceinline__ void kq_dequant8(int dtype, const uint8_t *__restrict
     }
 }
 
-// ggml dequantize_row_q4_K / _q6_K, plus add[i] when add is given (the
+// ggml dequantize_row_q4_K / _q6_K / _q8_0, plus add[i] when add is given (the
 // token embedding + audio embedding sum); one thread per 8 elements.
 __global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__restrict__ src,
                                                     int64_t n, const float *__restrict__ add,
@@ -723,7 +836,7 @@ __global__ void __launch_bounds__(256) k_kq_dequant(int dtype, const uint8_t *__
     for (int i = 0; i < 8; ++i) y[i8 + i] = add ? out[i] + add[i8 + i] : out[i];
 }
 
-// get_rows of up to kEmbedChunk token rows of a Q4_K / Q6_K table, each plus
+// get_rows of up to kEmbedChunk token rows of a Q4_K / Q6_K / Q8_0 table, each plus
 // its audio row when add is given (build_decoder_prefill_graph's tok_emb +
 // audio_emb): row p = blockIdx.y is table row tok.id[p] into y row p, the
 // audio row at (add_row0 + p) % add_ring of a ring (add_ring > 0) or row p.
@@ -1500,6 +1613,7 @@ hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st) {
     // 3 / 4 (Q6_K 2, 3, 5, 6: 0.2-1.2% slower per token).
     const int units = (a.rows_per_wg >> 2) * S * (a.swiglu ? 2 : 1);
     bool q4 = false, q6 = false;
+    // (Q8_0 rows take the Q6_K counts)
     for (int k = 0; k < a.n_outs; ++k) (a.out[k].dtype == VKV_DTYPE_Q4_K ? q4 : q6) = true;
     auto fits = [&](int d4, int d6) { return (!q4 || units <= d4) && (!q6 || units <= d6); };
     const bool one = fits(6, 3);

@@ -46,7 +46,7 @@ Q4_K = 12
 Q6_K = 14
 Q8_K = 15
 MAX_BATCH_STREAMS = 32
-KQ_BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_K: 292}
+KQ_BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q8_K: 292, Q8_0: 272}   # bytes per 256 elements
 MV_MAX_IN = 12288
 MV_MAX_OUTS = 4
 MV_STORE, MV_SWIGLU, MV_GELU = 0, 1, 2
