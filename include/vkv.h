@@ -418,10 +418,12 @@ vkv_status vkv_dequantize(int32_t dtype, const void *blocks, int64_t n, float *y
  * y: [n_cols][n_rows] per matrix, plus bias[r], plus add (same layout) when
  * given.  SwiGLU pairs the rows of two matrices as vkv_matvec does.  The Q8_K
  * image of x lives in the caller's workspace (vkv_matmul_workspace bytes,
- * 256-byte aligned); matrices of one call may mix Q4_K and Q6_K.
+ * 256-byte aligned); matrices of one call may mix Q4_K and Q6_K.  Q8_0
+ * matrices take the q8_0 image of x (as vkv_matvec forms it) and share a
+ * call only with other Q8_0 matrices.
  * ------------------------------------------------------------------------- */
 typedef struct vkv_mm_out {
-    const void *w;        /* [n_rows][n_in/256] Q4_K or Q6_K blocks */
+    const void *w;        /* [n_rows] rows of Q4_K / Q6_K / Q8_0 blocks, 4-byte aligned */
     int32_t dtype;
     int32_t n_rows;
     float *y;             /* [n_cols][n_rows] */

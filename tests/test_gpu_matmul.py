@@ -38,11 +38,18 @@ def workspace(n_cols, n_in):
     return t, (t.data_ptr() + 255) & ~255, b
 
 
+def x_image(dtype, h, n_in):
+    """the dequantized input image a product on dtype rows multiplies"""
+    if dtype == vkv.Q8_0:
+        return oracle.dequantize(oracle.Q8_0, oracle.q8_0_quantize_x86(h), n_in)
+    return oracle.dequantize(oracle.Q8_K, oracle.q8_k_quantize(h), n_in)
+
+
 def rows_ref(dtype, w, n_rows, n_in, hs):
     """oracle outputs [n_cols][n_rows] and magnitudes sum |w||x| (x = Q8_K image)"""
     out = np.stack([oracle.matvec(dtype, w, n_rows, n_in, h, n_threads=8) for h in hs])
     wd = np.abs(oracle.dequantize(dtype, w, n_rows * n_in).reshape(n_rows, n_in))
-    ax = np.stack([np.abs(oracle.dequantize(oracle.Q8_K, oracle.q8_k_quantize(h), n_in)) for h in hs])
+    ax = np.stack([np.abs(x_image(dtype, h, n_in)) for h in hs])
     return out, ax @ wd.T
 
 
@@ -233,3 +240,111 @@ def test_normed_input_wider_than_the_fused_norm(n_in, ada):
     for w, (dt, n), y in zip(ws_np, mats, out_s):
         want, mag = rows_ref(dt, w, n, n_in, hs)
         check(y, want, mag)
+
+
+def image_parts(t, ws_ptr, P, n_in):
+    """codes [P][n_in] in natural order and the 16-bit words [P][n_in / 32]
+    (Q8_K sums, or the fp16 d of a q8_0 image) from a call's workspace"""
+    raw = host(t).view(np.uint8)[ws_ptr - t.data_ptr():]
+    codes = raw[:P * n_in].reshape(P, n_in // 256, 4, 4, 2, 8).transpose(0, 1, 2, 4, 3, 5)
+    off = -(-P * n_in // 256) * 256
+    off += -(-P * (n_in // 256) * 4 // 256) * 256
+    words = raw[off:off + P * (n_in // 32) * 2].copy().view(np.uint16).reshape(P, n_in // 32)
+    return codes.reshape(P, n_in).copy(), words
+
+
+@pytest.mark.parametrize("P", [1, 4, 16, 38, 64])
+def test_q8_0_products_with_norm_bias_and_biases(P):
+    """A Q8_0 file's encoder Q/K/V (all three Q8_0, src/voxtral-quantize.cpp:
+    95-96): the q8_0 image of every row (codes in the products' lane order,
+    the fp16 d of every 32-element block in the sums' place) is ggml's x86
+    quantize_row_q8_0 of the normed row bit for bit, through the fused (P <= 4)
+    and the separate quantization alike; the outputs are within the bound."""
+    rng = np.random.default_rng(8000 + P)
+    n_in = 1280
+    mats = [(vkv.Q8_0, 1280, True), (vkv.Q8_0, 1280, False), (vkv.Q8_0, 1280, True)]
+    ws = [random_matrix(rng, dt, n, n_in, 0.05) for dt, n, _ in mats]
+    bs = [rng.standard_normal(n).astype(np.float32) if hb else None for _, n, hb in mats]
+    x = (rng.standard_normal((P, n_in)) * np.exp(rng.uniform(-4, 4, (P, 1)))).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, n_in).astype(np.float32)
+    nb = rng.uniform(-0.3, 0.3, n_in).astype(np.float32)
+    xd, nwd, nbd = to_dev(x), to_dev(nw), to_dev(nb)
+    wds = [to_dev(w) for w in ws]
+    bds = [to_dev(b) if b is not None else None for b in bs]
+    ys = [torch.full((P, n), np.nan, device=dev()) for _, n, _ in mats]
+    t, ws_ptr, ws_b = workspace(P, n_in)
+    vkv.matmul(xd.data_ptr(), P, n_in,
+               [(wd.data_ptr(), dt, n, y.data_ptr(), None, bd.data_ptr() if bd is not None else None)
+                for wd, (dt, n, _), y, bd in zip(wds, mats, ys, bds)],
+               ws_ptr, ws_b, norm_w_ptr=nwd.data_ptr(), norm_b_ptr=nbd.data_ptr(), eps=EPS,
+               hip_stream=stream_ptr())
+    hs = [oracle.norm_act(x[p], nw, eps=EPS, norm_b=nb) for p in range(P)]
+    codes, words = image_parts(t, ws_ptr, P, n_in)
+    for p in range(P):
+        blk = oracle.q8_0_quantize_x86(hs[p]).reshape(-1, 34)
+        assert np.array_equal(codes[p], blk[:, 2:].view(np.int8).ravel().view(np.uint8))
+        assert np.array_equal(words[p], blk[:, 0:2].copy().view(np.uint16).ravel())
+    for w, (dt, n, _), y, b in zip(ws, mats, ys, bs):
+        want, mag = rows_ref(dt, w, n, n_in, hs)
+        if b is not None:
+            want = want + b[None, :]
+        check(host(y), want, mag, extra=6e-8 * np.abs(want))
+
+
+@pytest.mark.parametrize("P", [3, 16])
+def test_q8_0_swiglu_and_w2_residual(P):
+    """the encoder FFN of a Q8_0 file: SwiGLU over 5120 rows, then W2 + bias +
+    residual in place over a 5120-wide input (two passes of 256-blocks per wave)"""
+    rng = np.random.default_rng(8362 + P)
+    n_in, hid = 1280, 5120
+    w1 = random_matrix(rng, vkv.Q8_0, hid, n_in, 0.02)
+    w3 = random_matrix(rng, vkv.Q8_0, hid, n_in, 0.02)
+    x = rng.standard_normal((P, n_in)).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, n_in).astype(np.float32)
+    xd, nwd, w1d, w3d = to_dev(x), to_dev(nw), to_dev(w1), to_dev(w3)
+    y = torch.full((P, hid), np.nan, device=dev())
+    t, ws_ptr, ws_b = workspace(P, n_in)
+    vkv.matmul(xd.data_ptr(), P, n_in, [(w1d.data_ptr(), vkv.Q8_0, hid, y.data_ptr()),
+                                        (w3d.data_ptr(), vkv.Q8_0, hid, None)],
+               ws_ptr, ws_b, norm_w_ptr=nwd.data_ptr(), eps=EPS, epilogue=vkv.MV_SWIGLU,
+               hip_stream=stream_ptr())
+    hs = [oracle.norm_act(x[p], nw, eps=EPS) for p in range(P)]
+    g, m1 = rows_ref(vkv.Q8_0, w1, hid, n_in, hs)
+    u, m3 = rows_ref(vkv.Q8_0, w3, hid, n_in, hs)
+    g, u = g.astype(np.float64), u.astype(np.float64)
+    sg = g / (1 + np.exp(-g))
+    want = sg * u
+    bound = REL * (1.1 * m1 * np.abs(u) + np.abs(sg) * m3) + 1e-6 * np.abs(want)
+    f = host(y)
+    assert np.all(np.abs(f - want) <= bound + 1e-30)
+    w2 = random_matrix(rng, vkv.Q8_0, n_in, hid, 0.05)
+    b2 = rng.standard_normal(n_in).astype(np.float32)
+    res = rng.standard_normal((P, n_in)).astype(np.float32)
+    fd, w2d, b2d, r = to_dev(f), to_dev(w2), to_dev(b2), to_dev(res)
+    t2, ws2, wsb2 = workspace(P, hid)
+    vkv.matmul(fd.data_ptr(), P, hid, [(w2d.data_ptr(), vkv.Q8_0, n_in, r.data_ptr(), r.data_ptr(),
+                                         b2d.data_ptr())], ws2, wsb2, hip_stream=stream_ptr())
+    proj, mag = rows_ref(vkv.Q8_0, w2, n_in, hid, list(f))
+    want2 = res + (proj + b2[None, :])
+    check(host(r), want2, mag, extra=1.2e-7 * (np.abs(res) + np.abs(proj) + np.abs(b2)[None, :]))
+
+
+def test_q8_0_matches_the_single_row_kernel_and_rejects_mixing():
+    rng = np.random.default_rng(80)
+    n_rows, n_in = 3072, 4096
+    w = random_matrix(rng, vkv.Q8_0, n_rows, n_in)
+    x = rng.standard_normal(n_in).astype(np.float32)
+    xd, wd = to_dev(x), to_dev(w)
+    y1 = torch.empty(n_rows, device=dev())
+    y2 = torch.empty(n_rows, device=dev())
+    vkv.matvec(xd.data_ptr(), n_in, [(wd.data_ptr(), vkv.Q8_0, n_rows, y1.data_ptr())],
+               hip_stream=stream_ptr())
+    t, ws_ptr, ws_b = workspace(1, n_in)
+    vkv.matmul(xd.data_ptr(), 1, n_in, [(wd.data_ptr(), vkv.Q8_0, n_rows, y2.data_ptr())],
+               ws_ptr, ws_b, hip_stream=stream_ptr())
+    _, mag = rows_ref(vkv.Q8_0, w, n_rows, n_in, [x])
+    check(host(y2), host(y1), 2 * mag[0])
+    with pytest.raises(vkv.VkvError):
+        vkv.matmul(xd.data_ptr(), 1, n_in, [(wd.data_ptr(), vkv.Q8_0, n_rows, y2.data_ptr()),
+                                            (wd.data_ptr(), vkv.Q4_K, 16, y1.data_ptr())],
+                   ws_ptr, ws_b, hip_stream=stream_ptr())

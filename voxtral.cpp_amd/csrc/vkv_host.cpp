@@ -1273,8 +1273,11 @@ vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float
     for (int32_t k = 0; k < n_outs; ++k) {
         const vkv_mm_out &o = outs[k];
         const int64_t bb = kq_block_bytes(o.dtype);
-        if (!bb || o.dtype == VKV_DTYPE_Q8_0)
-            return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: weight dtype %d", o.dtype);
+        if (!bb) return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: weight dtype %d", o.dtype);
+        // one input image per call: q8_0 for Q8_0 rows, Q8_K for the k-quants
+        if ((o.dtype == VKV_DTYPE_Q8_0) != (outs[0].dtype == VKV_DTYPE_Q8_0))
+            return fail(VKV_STATUS_INVALID_ARGUMENT,
+                        "matmul: Q8_0 matrices cannot share a call with Q4_K / Q6_K ones");
         if (!o.w || (!o.y && !(swiglu && k == 1)) || o.n_rows < 1)
             return fail(VKV_STATUS_INVALID_ARGUMENT, "matmul: matrix %d: null pointer or no rows", k);
         if ((int64_t)o.n_rows * (n_in / 256) * bb > (int64_t)0xFFFFFE00)
@@ -1333,7 +1336,8 @@ vkv_status matmul_impl(const float *x, int32_t n_cols, int64_t n_in, const float
     } else {
         a.norm_w = a.norm_b = a.ada = nullptr;   // applied by the separate quantization
         e = launch_q8k_rows(x, n_in, in_rows.ring, in_rows.row0, n_cols, (int)n_in, norm_w, norm_b,
-                            ada, eps, im.codes, im.xd, im.bs16, as_stream(hip_stream));
+                            ada, eps, im.codes, im.xd, im.bs16, outs[0].dtype == VKV_DTYPE_Q8_0,
+                            as_stream(hip_stream));
         if (e != hipSuccess) return hip_fail(e, "matmul input launch");
         a.xq = im.codes;
         a.xd = im.xd;

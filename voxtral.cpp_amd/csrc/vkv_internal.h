@@ -163,7 +163,7 @@ struct MmOut {
 struct MmArgs {
     const int8_t *xq;      // Q8_K image: codes [n_cols][n_in]
     const float *xd;       // block scales [n_cols][n_in / 256]
-    const int16_t *xbs;    // 32-element sums [n_cols][n_in / 32]
+    const int16_t *xbs;    // 32-element sums [n_cols][n_in / 32] (q8_0 image: fp16 d)
     // Fused input (x != nullptr): each work group quantizes its own input
     // rows into LDS (k_q8k_rows' arithmetic) instead of reading the image:
     // input row p at x + ((x_row0 + p) % x_ring) * x_stride (x_ring > 0) or
@@ -190,9 +190,12 @@ struct MmArgs {
 
 // Input row p is read at x + ((x_row0 + p) % x_ring) * x_stride when
 // x_ring > 0 (rows of a ring buffer), else at x + p * x_stride.
+// q80: the q8_0 image (Q8_0 weights): codes, and the fp16 d of every
+// 32-element block in bs16 (xd unused)
 hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_row0, int n_rows,
                            int n, const float *norm_w, const float *norm_b, const float *ada,
-                           float eps, int8_t *codes, float *xd, int16_t *bs16, hipStream_t st);
+                           float eps, int8_t *codes, float *xd, int16_t *bs16, bool q80,
+                           hipStream_t st);
 hipError_t launch_gemm_kq(MmArgs a, int n_col_tiles, hipStream_t st);
 // input rows one work group of launch_gemm_kq covers for this call
 int gemm_cols_per_wg(const MmArgs &a, int n_col_tiles);

@@ -966,7 +966,9 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, in
 //
 //   k_q8k_rows -- the Q8_K image of every input row (one work group per row,
 //                 same input side as k_matvec), to global memory: codes
-//                 [p][K], block scales [p][K/256], 32-element sums [p][K/32] (int16).
+//                 [p][K], block scales [p][K/256], 32-element sums [p][K/32] (int16);
+//                 for Q8_0 weights the q8_0 image: codes and the fp16 d of
+//                 each 32-element block in the sums' place.
 //   k_gemm_kq  -- a work group owns 16 weight rows x 16 (or 32) input rows;
 //                 its 8 (or 16) waves split the 256-blocks of K and meet in LDS.
 //                 A wave holds one block's fragments (about 100 VGPRs), so
@@ -978,11 +980,12 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, in
 //                 (kg, n) for input n.  Q4_K: one MFMA per sub-block, then its
 //                 6-bit scale and min; Q6_K: codes recentred to int8 (q - 32),
 //                 one MFMA per 16-element scale group (the other half of the
-//                 k window zeroed).
+//                 k window zeroed); Q8_0: one MFMA per 34-byte block against
+//                 the q8_0 image, times fp16(d_w) * fp16(d_x).
 // ---------------------------------------------------------------------------
 // NE: inputs of up to 4096 (one round of 16-lane rows), with the norm's
 // weight, ada and bias requested together with the input (one round trip)
-template <int NBW, bool NE>
+template <int NBW, bool NE, bool Q80>
 __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, int64_t x_stride,
                                                   int x_ring, int x_row0, int n, const float *nw,
                                                   const float *nbias, const float *ada, float eps,
@@ -993,7 +996,7 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, i
     const int src = x_ring > 0 ? (x_row0 + p) % x_ring : p;
     ActRegs<NBW, NE, NE> r;
     act_load(r, x + (int64_t)src * x_stride, n, nw, ada, nbias);
-    act_finish(r, n, nw, ada, eps, sm, nullptr, nbias);
+    act_finish<NBW, NE, NE, Q80>(r, n, nw, ada, eps, sm, nullptr, nbias);
     // codes in the products' lane order: within each 256-block, the 16 bytes
     // at 64 q + 16 kg hold the codes k = 32 j + 8 kg + e of j = 2q, 2q + 1
     // (e = 0..7): lane group kg's MFMA B operands, and one 16-byte load per q
@@ -1006,9 +1009,16 @@ __global__ void __launch_bounds__(256) k_q8k_rows(const float *__restrict__ x, i
         dst[i] = make_int4((int)(uint32_t)lo, (int)(uint32_t)(lo >> 32), (int)(uint32_t)hi,
                            (int)(uint32_t)(hi >> 32));
     }
-    for (int i = threadIdx.x; i < n / 256; i += 256) xd[(int64_t)p * (n / 256) + i] = sm.dx[i];
-    // (a sum of 32 codes fits in 16 bits: |s| <= 32 * 127)
-    for (int i = threadIdx.x; i < n / 32; i += 256) bs16[(int64_t)p * (n / 32) + i] = (int16_t)sm.bs32[i];
+    if constexpr (Q80) {
+        // the fp16 d of each 32-element block (held as its f32 value)
+        for (int i = threadIdx.x; i < n / 32; i += 256)
+            bs16[(int64_t)p * (n / 32) + i] = __builtin_bit_cast(
+                int16_t, (_Float16)__builtin_bit_cast(float, sm.bs32[i]));
+    } else {
+        for (int i = threadIdx.x; i < n / 256; i += 256) xd[(int64_t)p * (n / 256) + i] = sm.dx[i];
+        // (a sum of 32 codes fits in 16 bits: |s| <= 32 * 127)
+        for (int i = threadIdx.x; i < n / 32; i += 256) bs16[(int64_t)p * (n / 32) + i] = (int16_t)sm.bs32[i];
+    }
 }
 
 // 8 bytes at an even byte offset of a buffer (Q6_K blocks are 2-byte
@@ -1055,9 +1065,13 @@ struct GFragQ6 {
     uint64_t s0, s1;            // the row's 16 int8 scales
     uint32_t dh;                // fp16 d
 };
+struct GFragQ8 {
+    uint64_t qs[8];   // codes of the 256-block's Q8_0 blocks j = 0..7, k = 8kg..8kg+7
+    uint32_t dh[4];   // fp16 d of blocks 2i (low half) and 2i + 1 (high half)
+};
 struct GFragX {
     uint64_t xb[8];   // Q8_K codes of input row n, k window 32j + 8kg
-    int32_t bsx[8];   // their 32-element sums (Q4_K mins)
+    int32_t bsx[8];   // their 32-element sums (Q4_K mins); q8_0 image: fp16 d of block j
     float dx;
 };
 
@@ -1066,9 +1080,33 @@ struct GFragX {
 // loaded value, which waits for the load there.  The fused-input kernels
 // request a block before the input quantization and must not wait for it;
 // the others issue fewer loads without it.
-template <bool Q4, bool ALLH>
+template <int WK, bool ALLH>
 __device__ __forceinline__ auto gemm_load_w(__amdgpu_buffer_rsrc_t rs, uint32_t boff, int kg) {
-    if constexpr (Q4) {
+    if constexpr (WK == kWQ8) {
+        // block j's codes 8kg..8kg+7 start 2 mod 4 (j even) or 0 mod 4 (j odd)
+        // bytes into the row (boff is a multiple of 272); for kg = 0 and j
+        // even the realigning load starts at the block, so its first half
+        // word is d; odd blocks' d take a load of their own
+        GFragQ8 f;
+        uint32_t de[4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t off = boff + kQ8Bytes * j + 2 + 8 * kg;
+            const u32x3_t w = __builtin_amdgcn_raw_buffer_load_b96(rs, off & ~3u, 0, 0);
+            const uint32_t lo = __builtin_amdgcn_alignbyte(w.y, w.x, off & 3u);
+            const uint32_t hi = __builtin_amdgcn_alignbyte(w.z, w.y, off & 3u);
+            f.qs[j] = ((uint64_t)hi << 32) | lo;
+            if ((j & 1) == 0) de[j >> 1] = w.x & 0xffffu;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t dodd = 0;
+            if (ALLH || kg == 0)
+                dodd = __builtin_amdgcn_raw_buffer_load_b16(rs, boff + kQ8Bytes * (2 * i + 1), 0, 0);
+            f.dh[i] = de[i] | dodd << 16;
+        }
+        return f;
+    } else if constexpr (WK == kWQ4) {
         GFragQ4 f;
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -1119,7 +1157,7 @@ struct XImage {
     int col0;
 };
 
-template <bool Q4>
+template <int WK>
 __device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, const XImage &im, int col, int b,
                                               int kg) {
     GFragX x;
@@ -1133,20 +1171,25 @@ __device__ __forceinline__ GFragX gemm_load_x(const MmArgs &a, const XImage &im,
         x.xb[2 * q] = ((uint64_t)(uint32_t)v.y << 32) | (uint32_t)v.x;
         x.xb[2 * q + 1] = ((uint64_t)(uint32_t)v.w << 32) | (uint32_t)v.z;
     }
-    if constexpr (Q4) {
-        // the block's eight 16-bit sums in one 16-byte load
+    if constexpr (WK == kWQ4 || WK == kWQ8) {
+        // the block's eight 16-bit sums (q8_0: fp16 d) in one 16-byte load
         const int4 v = *reinterpret_cast<const int4 *>(im.xbs + (int64_t)col * (K / 32) + 8 * b);
         const int w4[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            x.bsx[2 * i] = (int)(int16_t)(w4[i] & 0xffff);
-            x.bsx[2 * i + 1] = w4[i] >> 16;
+            if constexpr (WK == kWQ4) {
+                x.bsx[2 * i] = (int)(int16_t)(w4[i] & 0xffff);
+                x.bsx[2 * i + 1] = w4[i] >> 16;
+            } else {
+                x.bsx[2 * i] = w4[i] & 0xffff;
+                x.bsx[2 * i + 1] = (int)((uint32_t)w4[i] >> 16);
+            }
         }
     } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) x.bsx[j] = 0;
     }
-    x.dx = im.xd[(int64_t)col * (K >> 8) + b];
+    x.dx = WK == kWQ8 ? 0.0f : im.xd[(int64_t)col * (K >> 8) + b];
     return x;
 }
 
@@ -1170,7 +1213,7 @@ constexpr int kFqNormPer = 4;
 // pre() is called once the input rows (and the norm's vectors) have been
 // requested and before anything waits for them: the caller requests its
 // first weights there, so their round trip overlaps the input's.
-template <int W, class Pre>
+template <int W, bool Q80, class Pre>
 __device__ __forceinline__ void gemm_quant_cols(const MmArgs &a, int col0, int ncol, int8_t *cq,
                                                 float *cd, int16_t *cs, double *ss, float *nv,
                                                 Pre &&pre) {
@@ -1269,7 +1312,22 @@ __device__ __forceinline__ void gemm_quant_cols(const MmArgs &a, int col0, int n
                 }
             }
         }
-        const QBlock16 q = q8k_block16(e[r], l);
+        uint32_t packed[4];
+        int16_t s32 = 0;
+        float dq = 0.0f;
+        if constexpr (Q80) {
+            // the q8_0 image: the 32-element block's fp16 d in the sums' place
+            const QBlock0 q = q8_0_block16(e[r]);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) packed[w] = q.packed[w];
+            s32 = __builtin_bit_cast(int16_t, (_Float16)q.d);
+        } else {
+            const QBlock16 q = q8k_block16(e[r], l);
+#pragma unroll
+            for (int w = 0; w < 4; ++w) packed[w] = q.packed[w];
+            s32 = (int16_t)q.s32;
+            dq = q.d;
+        }
         // codes 32 j + 8 kg + e at byte 64 q + 16 kg + 8 (j & 1) + e of the
         // block (q = j / 2): lane l holds j = l / 2, kg = 2 (l & 1) + h
         int8_t *blk = cq + (int64_t)c * K + 256 * b;
@@ -1277,9 +1335,9 @@ __device__ __forceinline__ void gemm_quant_cols(const MmArgs &a, int col0, int n
 #pragma unroll
         for (int h = 0; h < 2; ++h)
             *reinterpret_cast<uint2 *>(blk + 64 * qq + 16 * (2 * (l & 1) + h) + 8 * jj) =
-                make_uint2(q.packed[2 * h], q.packed[2 * h + 1]);
-        if ((l & 1) == 0) cs[(int64_t)c * (K / 32) + 8 * b + (l >> 1)] = (int16_t)q.s32;
-        if (l == 0) cd[(int64_t)c * nb + b] = q.d;
+                make_uint2(packed[2 * h], packed[2 * h + 1]);
+        if ((l & 1) == 0) cs[(int64_t)c * (K / 32) + 8 * b + (l >> 1)] = s32;
+        if (l == 0) cd[(int64_t)c * nb + b] = dq;
     }
     __syncthreads();
 }
@@ -1289,6 +1347,10 @@ __device__ __forceinline__ void gemm_quant_cols(const MmArgs &a, int col0, int n
 __device__ __forceinline__ void opaque_codes(GFragQ4 &f) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) asm volatile("" : "+v"(f.qs[c]));
+}
+__device__ __forceinline__ void opaque_codes(GFragQ8 &f) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(f.qs[j]));
 }
 __device__ __forceinline__ void opaque_codes(GFragQ6 &f) {
 #pragma unroll
@@ -1332,6 +1394,37 @@ __device__ __forceinline__ void gemm_hdr(const GFragQ6 &f, uint32_t (*hdr)[6], i
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int w = 0; w < 5; ++w) hd[i][w] = hdr[4 * kg + i][w];
+}
+
+__device__ __forceinline__ void gemm_hdr(const GFragQ8 &f, uint32_t (*hdr)[6], int kg, int rr,
+                                         uint32_t (&hd)[4][5]) {
+    if (kg == 0) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) hdr[rr][w] = f.dh[w];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) hd[i][w] = hdr[4 * kg + i][w];
+        hd[i][4] = 0;
+    }
+}
+
+// Q8_0: block j's exact integer sums, times fp16(d_w) * fp16(d_x) (ggml's
+// per-block term of vec_dot_q8_0_q8_0)
+__device__ __forceinline__ void gemm_dot(const GFragQ8 &f, const GFragX &x, const uint32_t (&hd)[4][5],
+                                         int kg, float (&acc)[4]) {
+    const i32x4_t z = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const i32x4_t c = mfma_i8(f.qs[j], x.xb[j], z);
+        const float dx = h2f((uint32_t)x.bsx[j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float dw = h2f((hd[i][j >> 1] >> (16 * (j & 1))) & 0xffffu);
+            acc[i] = fmaf((float)c[i], dw * dx, acc[i]);
+        }
+    }
 }
 
 __device__ __forceinline__ void gemm_dot(const GFragQ4 &f, const GFragX &x, const uint32_t (&hd)[4][5],
@@ -1405,7 +1498,7 @@ __device__ __forceinline__ float rope_elem(float self, float partner, bool odd, 
 // input rows each) per work group: a wave loads each weight block once and
 // applies it to every column tile, so the weights are read once per 16 CT
 // input rows.
-template <bool Q4, int W, int CT, bool ALLH, class GF>
+template <int WK, int W, int CT, bool ALLH, class GF>
 __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, const MmOut &o1,
                                           uint32_t (*hdr)[16][6], float (*red)[W][16][17],
                                           const XImage &im, const GF &w_first) {
@@ -1416,7 +1509,8 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const bool swiglu = a.swiglu != 0;
     const int nb = a.n_in >> 8;
-    const uint32_t bbytes = Q4 ? kQ4Bytes : kQ6Bytes, rbytes = (uint32_t)nb * bbytes;
+    const uint32_t bbytes = WK == kWQ4 ? kQ4Bytes : WK == kWQ8 ? kQ8Per256 : kQ6Bytes;
+    const uint32_t rbytes = (uint32_t)nb * bbytes;
     const int row0 = ((int)blockIdx.x - o0.tile0) * 16, col0 = (int)blockIdx.y * 16 * CT;
     const int row = min(row0 + rr, o0.n_rows - 1);
     // column tiles holding input rows (uniform over the work group)
@@ -1462,7 +1556,7 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
         for (int c = 0; c < CT; ++c) {
             if (c < n_ct) {
                 const GFragX x =
-                    gemm_load_x<Q4>(a, im, min(col0 + 16 * c + rr, a.n_cols - 1), b, kg);
+                    gemm_load_x<WK>(a, im, min(col0 + 16 * c + rr, a.n_cols - 1), b, kg);
                 // with several column tiles the codes pass through an empty
                 // asm before each use, so what is derived from them (nibbles,
                 // recentred codes, scales) is derived again instead of held
@@ -1477,7 +1571,7 @@ __device__ __forceinline__ void gemm_body(const MmArgs &a, const MmOut &o0, cons
     };
     if (wm < nb) block(w_first, wm);
     for (int b = wm + kw; b < nb; b += kw)
-        block(gemm_load_w<Q4, ALLH>(rs, (uint32_t)row * rbytes + (uint32_t)b * bbytes, kg), b);
+        block(gemm_load_w<WK, ALLH>(rs, (uint32_t)row * rbytes + (uint32_t)b * bbytes, kg), b);
     // the waves' partial sums meet in LDS: red[column tile][wave][row][input row]
     // (SwiGLU: waves m kw .. m kw + kw - 1 hold matrix m)
 #pragma unroll
@@ -1539,8 +1633,8 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
     const MmOut o0 = mm_out_at(a, seg);
     const MmOut o1 = a.swiglu ? a.out[1] : o0;
     // one weight dtype per work group (both SwiGLU matrices share it)
-    auto run = [&](auto q4) __attribute__((always_inline)) {
-        constexpr bool Q4 = decltype(q4)::value;
+    auto run = [&](auto wk) __attribute__((always_inline)) {
+        constexpr int WK = decltype(wk)::value;
         // the wave's first weight block (gemm_body's decomposition), requested
         // before the fused input quantization waits for anything; the block
         // index is clamped so the request is unconditional (a wave without a
@@ -1548,7 +1642,8 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         const int lane = threadIdx.x & 63, kg = lane >> 4, rr = lane & 15;
         const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int nb = a.n_in >> 8;
-        const uint32_t bbytes = Q4 ? kQ4Bytes : kQ6Bytes, rbytes = (uint32_t)nb * bbytes;
+        const uint32_t bbytes = WK == kWQ4 ? kQ4Bytes : WK == kWQ8 ? kQ8Per256 : kQ6Bytes;
+        const uint32_t rbytes = (uint32_t)nb * bbytes;
         const int row = min(((int)blockIdx.x - o0.tile0) * 16 + rr, o0.n_rows - 1);
         const int kw = a.swiglu ? W / 2 : W;
         const int m = a.swiglu ? wave / kw : 0, wm = wave - m * kw;
@@ -1557,10 +1652,11 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint8_t *>(o1.w), (short)0, (int)(rbytes * (uint32_t)o1.n_rows), 0x00020000);
         const __amdgpu_buffer_rsrc_t rs = m ? rs1 : rs0;
-        using GF = std::conditional_t<Q4, GFragQ4, GFragQ6>;
+        using GF = std::conditional_t<WK == kWQ4, GFragQ4,
+                                      std::conditional_t<WK == kWQ8, GFragQ8, GFragQ6>>;
         GF wf;
         auto pre = [&]() __attribute__((always_inline)) {
-            wf = gemm_load_w<Q4, FQ>(rs, (uint32_t)row * rbytes + (uint32_t)min(wm, nb - 1) * bbytes,
+            wf = gemm_load_w<WK, FQ>(rs, (uint32_t)row * rbytes + (uint32_t)min(wm, nb - 1) * bbytes,
                                      kg);
         };
         XImage im{a.xq, a.xd, a.xbs, 0};
@@ -1577,7 +1673,7 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
                                                     al16((size_t)cols * (K / 32) * 2));
             float *nv = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(ss) +
                                                   al16((size_t)cols * nb * 8));
-            gemm_quant_cols<W>(a, col0, ncol, cq, cd, cs, ss, nv, pre);
+            gemm_quant_cols<W, WK == kWQ8>(a, col0, ncol, cq, cd, cs, ss, nv, pre);
             im = XImage{cq, cd, cs, col0};
             if (blockIdx.x == 0 && a.xq) {
                 // the first row tile's work groups leave their rows' image in
@@ -1594,10 +1690,11 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         } else {
             pre();
         }
-        gemm_body<Q4, W, CT, FQ>(a, o0, o1, hdr, red, im, wf);
+        gemm_body<WK, W, CT, FQ>(a, o0, o1, hdr, red, im, wf);
     };
-    if (o0.dtype == VKV_DTYPE_Q4_K) run(std::true_type{});
-    else run(std::false_type{});
+    if (o0.dtype == VKV_DTYPE_Q4_K) run(std::integral_constant<int, kWQ4>{});
+    else if (o0.dtype == VKV_DTYPE_Q8_0) run(std::integral_constant<int, kWQ8>{});
+    else run(std::integral_constant<int, kWQ6>{});
 }
 
 }  // namespace
@@ -1656,14 +1753,19 @@ hipError_t launch_embed_rows(int dtype, const uint8_t *table, int64_t row_bytes,
 
 hipError_t launch_q8k_rows(const float *x, int64_t x_stride, int x_ring, int x_row0, int n_rows,
                            int n, const float *norm_w, const float *norm_b, const float *ada,
-                           float eps, int8_t *codes, float *xd, int16_t *bs16, hipStream_t st) {
-    if (n <= 4096)
-        k_q8k_rows<4, true><<<n_rows, 256, 0, st>>>(x, x_stride, x_ring, x_row0, n, norm_w, norm_b,
-                                                     ada, eps, codes, xd, bs16);
-    else
-        k_q8k_rows<kMvMaxIn / 1024, false><<<n_rows, 256, 0, st>>>(x, x_stride, x_ring, x_row0, n,
-                                                                    norm_w, norm_b, ada, eps,
-                                                                    codes, xd, bs16);
+                           float eps, int8_t *codes, float *xd, int16_t *bs16, bool q80,
+                           hipStream_t st) {
+    auto go = [&](auto kq) {
+        constexpr bool Q80 = decltype(kq)::value;
+        if (n <= 4096)
+            k_q8k_rows<4, true, Q80><<<n_rows, 256, 0, st>>>(x, x_stride, x_ring, x_row0, n, norm_w,
+                                                              norm_b, ada, eps, codes, xd, bs16);
+        else
+            k_q8k_rows<kMvMaxIn / 1024, false, Q80><<<n_rows, 256, 0, st>>>(
+                x, x_stride, x_ring, x_row0, n, norm_w, norm_b, ada, eps, codes, xd, bs16);
+    };
+    if (q80) go(std::true_type{});
+    else go(std::false_type{});
     return hipGetLastError();
 }
 
