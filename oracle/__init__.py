@@ -573,13 +573,18 @@ def time_embedding(t, dim):
 
 
 def ada_scale(w0_type, w0, w2, dim, ada_dim, t):
-    """w2: uint16 (f16 bits) or float32 array [dim][ada_dim]"""
+    """w2: uint16 (f16 bits) or float32 array [dim][ada_dim], or uint8 Q8_0
+    blocks ([dim] rows of ada_dim / 32 blocks)"""
     w0 = _u8(w0)
     w2 = np.ascontiguousarray(w2)
-    assert w2.dtype in (np.uint16, np.float32) and w2.size == dim * ada_dim
+    if w2.dtype == np.uint8:
+        assert w2.size == dim * (ada_dim // 32) * 34
+        w2_type = Q8_0
+    else:
+        assert w2.dtype in (np.uint16, np.float32) and w2.size == dim * ada_dim
+        w2_type = F16 if w2.dtype == np.uint16 else F32
     out = np.empty(dim, np.float32)
-    rc = lib.orc_ada_scale(w0_type, _ptr(w0), 1 if w2.dtype == np.uint16 else 0, _ptr(w2), dim,
-                           ada_dim, t, _ptr(out))
+    rc = lib.orc_ada_scale(w0_type, _ptr(w0), w2_type, _ptr(w2), dim, ada_dim, t, _ptr(out))
     if rc != 0:
         raise ValueError("ada scale rejected")
     return out

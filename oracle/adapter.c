@@ -18,7 +18,9 @@
  * scale = W2 gelu(W0 e(t)) with the time embedding of compute_time_embedding
  * (:729-740) evaluated as the reference does on the host; W0 through
  * orc_matvec, W2 (f16 [dim][ada_dim]) through ggml's f16 vec-dot: the input
- * rounded to f16, products summed in double (the generic path).
+ * rounded to f16, products summed in double (the generic path).  In a Q8_0
+ * file W2 is Q8_0 too (its 32-wide rows are row-compatible with Q8_0,
+ * src/voxtral-quantize.cpp:161-164, :410): then it is an orc_matvec as well.
  *
  * Pinned by tests/test_adapter.py: the gather against an independent index
  * rule (the 4-frame reshape of a contiguous run of encoder frames), the
@@ -107,9 +109,11 @@ void orc_time_embedding(float t, int32_t dim, float *out) {
     }
 }
 
-int32_t orc_ada_scale(int w0_type, const uint8_t *w0, int w2_f16, const void *w2, int32_t dim,
+int32_t orc_ada_scale(int w0_type, const uint8_t *w0, int w2_type, const void *w2, int32_t dim,
                       int32_t ada_dim, float t, float *out) {
     if (dim < 2 || ada_dim < 1) return -1;
+    if (w2_type == ORC_Q8_0 && ada_dim % 32) return -1;
+    const int w2_f16 = w2_type == ORC_F16;
     float *e = malloc((size_t)dim * sizeof(float));
     float *h = malloc((size_t)ada_dim * sizeof(float));
     if (!e || !h) {
@@ -120,7 +124,8 @@ int32_t orc_ada_scale(int w0_type, const uint8_t *w0, int w2_f16, const void *w2
     orc_time_embedding(t, dim, e);
     orc_matvec(w0_type, w0, ada_dim, dim, e, h, 1);
     for (int32_t k = 0; k < ada_dim; k++) h[k] = orc_gelu_erf(h[k]);
-    for (int32_t r = 0; r < dim; r++) {
+    if (w2_type == ORC_Q8_0) orc_matvec(ORC_Q8_0, (const uint8_t *)w2, dim, ada_dim, h, out, 1);
+    for (int32_t r = 0; r < dim && w2_type != ORC_Q8_0; r++) {
         double acc = 0.0;
         for (int32_t k = 0; k < ada_dim; k++) {
             if (w2_f16) {

@@ -333,7 +333,8 @@ static void *mv_worker(void *p) {
  * row of W; rows are split over n_threads */
 void orc_matvec(int dtype, const uint8_t *w, int64_t n_rows, int64_t n_in, const float *x,
                 float *y, int n_threads) {
-    uint8_t *xq = (uint8_t *)malloc((size_t)(n_in / QK) * 292);
+    uint8_t *xq = (uint8_t *)malloc(dtype == ORC_Q8_0 ? (size_t)(n_in / 32) * 34
+                                                      : (size_t)(n_in / QK) * 292);
     if (dtype == ORC_Q8_0) orc_q8_0_quantize_x86(x, xq, n_in);
     else orc_q8_k_quantize(x, xq, n_in);
     if (n_threads < 1) n_threads = 1;

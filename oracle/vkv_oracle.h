@@ -280,7 +280,8 @@ int32_t orc_adapter_commit(const float *enc_ring, int32_t enc_cap, int32_t enc_d
                            int64_t group_start, int32_t n_groups, int w0_type, const uint8_t *w0,
                            int w2_type, const uint8_t *w2, int n_threads);
 void orc_time_embedding(float t, int32_t dim, float *out);
-int32_t orc_ada_scale(int w0_type, const uint8_t *w0, int w2_f16, const void *w2, int32_t dim,
+/* w2_type: ORC_F32, ORC_F16 or ORC_Q8_0 (ada_dim % 32 == 0) */
+int32_t orc_ada_scale(int w0_type, const uint8_t *w0, int w2_type, const void *w2, int32_t dim,
                       int32_t ada_dim, float t, float *out);
 
 #ifdef __cplusplus

@@ -67,7 +67,9 @@ def realtime_model(rng, enc_layers=1, dec_layers=2, vocab=1024, enc=1280, dec=30
     """kvs and tensors of a realtime model in the Q4_K_M mix
     (src/voxtral-quantize.cpp:148-159: attn_v, ffn_w2, tok_embeddings Q6_K;
     other matrices Q4_K), random valid blocks at sizes that keep the
-    activations finite"""
+    activations finite.  q4 = q6 = 8 gives a Q8_0 file (:95-96): every
+    matrix Q8_0, ada2 included (its 32-wide rows are whole Q8_0 blocks,
+    :161-164, :410)."""
     kvs = [("general.architecture", STR, "voxtral_realtime"),
            ("general.name", STR, "Voxtral-Mini-4B-Realtime-2602"),
            ("general.file_type", U32, 1),
@@ -136,8 +138,11 @@ def realtime_model(rng, enc_layers=1, dec_layers=2, vocab=1024, enc=1280, dec=30
         mat(p + "ffn_w2.weight", q6, dec, dec_hidden, 0.05)
         mat(p + "ffn_w3.weight", q4, dec_hidden, dec, 0.005)
         mat(p + "ada0.weight", q4, 32, dec, 0.002)
-        T.append((p + "ada2.weight", 1, [32, dec],
-                  (rng.standard_normal((dec, 32)) * 0.01).astype(np.float16).tobytes()))
+        if q4 == 8:
+            mat(p + "ada2.weight", 8, dec, 32, 0.02)
+        else:
+            T.append((p + "ada2.weight", 1, [32, dec],
+                      (rng.standard_normal((dec, 32)) * 0.01).astype(np.float16).tobytes()))
     T.append(("audio.mel_filters", 0, [201, n_mel],
               rng.uniform(0, 0.01, 201 * n_mel).astype(np.float32).tobytes()))
     return kvs, T

@@ -88,8 +88,8 @@ def composed_prompt(cache, ring, model, tokens, aring, logits, tok_out, sp, m=No
         a_ptr = None
         if aring is not None:
             a_ptr = aring.rows + ((pos0 + i) % aring.capacity) * DIM * 4
-        vkv.embed(vkv.Q6_K, model.tok_embeddings, model.vocab, DIM, t, x[i].data_ptr(), a_ptr,
-                  hip_stream=sp)
+        vkv.embed(model.tok_embeddings_type, model.tok_embeddings, model.vocab, DIM, t,
+                  x[i].data_ptr(), a_ptr, hip_stream=sp)
     xp = x.data_ptr()
     for layer in range(model.n_layers):
         L = model.layers[layer]
@@ -102,9 +102,9 @@ def composed_prompt(cache, ring, model, tokens, aring, logits, tok_out, sp, m=No
             M = m["layers"][layer]
             hs = [oracle.norm_act(x_in[p], M["attn_norm"], None, EPS) for p in range(n)]
             q_in, k_in, v_in = host(q), host(k), host(v)
-            assert rel(q_in, rows_matvec(oracle.Q4_K, M["attn_q"], QD, DIM, hs)) < 2e-6
-            assert rel(k_in, rows_matvec(oracle.Q4_K, M["attn_k"], KD, DIM, hs)) < 2e-6
-            assert rel(v_in, rows_matvec(oracle.Q6_K, M["attn_v"], KD, DIM, hs)) < 2e-6
+            assert rel(q_in, rows_matvec(L.attn_q_type, M["attn_q"], QD, DIM, hs)) < 2e-6
+            assert rel(k_in, rows_matvec(L.attn_k_type, M["attn_k"], KD, DIM, hs)) < 2e-6
+            assert rel(v_in, rows_matvec(L.attn_v_type, M["attn_v"], KD, DIM, hs)) < 2e-6
         vkv.rope(q.data_ptr(), 1, n, QD, HD, pos0, THETA, hip_stream=sp)
         vkv.rope(k.data_ptr(), 1, n, KD, HD, pos0, THETA, hip_stream=sp)
         # every layer plans from the same ring state; the commit comes last
@@ -134,21 +134,21 @@ def composed_prompt(cache, ring, model, tokens, aring, logits, tok_out, sp, m=No
                    hip_stream=sp)
         if m:
             x_o = host(x)
-            assert rel(x_o, x_mid + rows_matvec(oracle.Q4_K, M["attn_o"], DIM, QD, a_got)) < 2e-6
+            assert rel(x_o, x_mid + rows_matvec(L.attn_o_type, M["attn_o"], DIM, QD, a_got)) < 2e-6
         vkv.matmul(xp, n, DIM, [(L.ffn_w1, L.ffn_w1_type, HID, ffn.data_ptr()),
                                 (L.ffn_w3, L.ffn_w3_type, HID, None)],
                    wp, ws_b, norm_w_ptr=L.ffn_norm, ada_ptr=L.ada_scale, eps=EPS,
                    epilogue=vkv.MV_SWIGLU, hip_stream=sp)
         if m:
             h2 = [oracle.norm_act(x_o[p], M["ffn_norm"], M["ada"], EPS) for p in range(n)]
-            g = rows_matvec(oracle.Q4_K, M["ffn_w1"], HID, DIM, h2)
-            u = rows_matvec(oracle.Q4_K, M["ffn_w3"], HID, DIM, h2)
+            g = rows_matvec(L.ffn_w1_type, M["ffn_w1"], HID, DIM, h2)
+            u = rows_matvec(L.ffn_w3_type, M["ffn_w3"], HID, DIM, h2)
             f_got = host(ffn)
             assert rel(f_got, oracle.silu(g).reshape(g.shape) * u) < 2e-6
         vkv.matmul(ffn.data_ptr(), n, HID, [(L.ffn_w2, L.ffn_w2_type, DIM, xp, xp)], wp, ws_b,
                    hip_stream=sp)
         if m:
-            assert rel(host(x), x_o + rows_matvec(oracle.Q6_K, M["ffn_w2"], DIM, HID, f_got)) < 2e-6
+            assert rel(host(x), x_o + rows_matvec(L.ffn_w2_type, M["ffn_w2"], DIM, HID, f_got)) < 2e-6
     vkv.matvec(x[n - 1].data_ptr(), DIM, [(model.output, model.output_type, model.vocab,
                                            logits.data_ptr())],
                norm_w_ptr=model.out_norm, eps=EPS, hip_stream=sp)
@@ -162,8 +162,9 @@ def oracle_prompt(m, k_imgs, v_imgs, row_b, capacity, pos0, tokens, audio, exact
     the attention in ggml's flash-attention arithmetic, or exact with
     `exact`): the last token's logits and greedy token"""
     n = len(tokens)
-    rb = DIM // 256 * 210
-    x = np.stack([oracle.dequantize(oracle.Q6_K, m["table"][t * rb:(t + 1) * rb], DIM)
+    T = m["types"]
+    rb = oracle.wrow_bytes(T["table"], DIM)
+    x = np.stack([oracle.dequantize(T["table"], m["table"][t * rb:(t + 1) * rb], DIM)
                   for t in tokens])
     if audio is not None:
         x = x + audio
@@ -171,9 +172,9 @@ def oracle_prompt(m, k_imgs, v_imgs, row_b, capacity, pos0, tokens, audio, exact
     key_pos = np.arange(max(0, pos0 + n - capacity), pos0 + n)
     for layer, L in enumerate(m["layers"]):
         hs = [oracle.norm_act(x[p], L["attn_norm"], None, EPS) for p in range(n)]
-        q = oracle.rope(rows_matvec(oracle.Q4_K, L["attn_q"], QD, DIM, hs), HD, pos0, THETA)
-        k = oracle.rope(rows_matvec(oracle.Q4_K, L["attn_k"], KD, DIM, hs), HD, pos0, THETA)
-        v = rows_matvec(oracle.Q6_K, L["attn_v"], KD, DIM, hs)
+        q = oracle.rope(rows_matvec(T["attn_q"], L["attn_q"], QD, DIM, hs), HD, pos0, THETA)
+        k = oracle.rope(rows_matvec(T["attn_k"], L["attn_k"], KD, DIM, hs), HD, pos0, THETA)
+        v = rows_matvec(T["attn_v"], L["attn_v"], KD, DIM, hs)
         ki, vi = k_imgs[layer].copy(), v_imgs[layer].copy()
         for i in range(n):
             s = (pos0 + i) % capacity
@@ -187,14 +188,14 @@ def oracle_prompt(m, k_imgs, v_imgs, row_b, capacity, pos0, tokens, audio, exact
         attn = attn_fn(oracle.F16, ki, vi, row_b, (key_pos % capacity).astype(np.int32), key_pos,
                        q.reshape(n, QH, HD), q_pos, QH, KVH, HD, 0, SCALE, **kw)
         attn = attn.reshape(n, QD).astype(np.float32)
-        x = x + rows_matvec(oracle.Q4_K, L["attn_o"], DIM, QD, attn)
+        x = x + rows_matvec(T["attn_o"], L["attn_o"], DIM, QD, attn)
         hs = [oracle.norm_act(x[p], L["ffn_norm"], L["ada"], EPS) for p in range(n)]
-        g = rows_matvec(oracle.Q4_K, L["ffn_w1"], HID, DIM, hs)
-        u = rows_matvec(oracle.Q4_K, L["ffn_w3"], HID, DIM, hs)
+        g = rows_matvec(T["ffn_w1"], L["ffn_w1"], HID, DIM, hs)
+        u = rows_matvec(T["ffn_w3"], L["ffn_w3"], HID, DIM, hs)
         f = (oracle.silu(g).reshape(g.shape) * u).astype(np.float32)
-        x = x + rows_matvec(oracle.Q6_K, L["ffn_w2"], DIM, HID, f)
+        x = x + rows_matvec(T["ffn_w2"], L["ffn_w2"], DIM, HID, f)
     xn = oracle.norm_act(x[-1], m["out_norm"], None, EPS)
-    logits = oracle.matvec(oracle.Q6_K, m["table"], m["vocab"], DIM, xn, 8)
+    logits = oracle.matvec(T["table"], m["table"], m["vocab"], DIM, xn, 8)
     return logits, oracle.argmax(logits)
 
 
@@ -211,19 +212,22 @@ def workspace_for(model, n):
     return ws, (ws.data_ptr() + 255) & ~255, b
 
 
-# (cache capacity, positions already in the ring, prompt tokens, audio ring capacity or None)
-CASES = [(512, 0, 38, 64),          # the stream prompt at positions 0..37
-         (512, 986, 38, 48),        # after a wrap: evictions, the audio ring wraps too
-         (512, 0, 1, 64),           # prompts of a few tokens: the normed products at the
-         (512, 40, 3, 64),          # decoder's width 3072 take the separate input
-         (512, 300, 5, 48)]         # quantization (a prompt's window is one segment)
+# (cache capacity, positions already in the ring, prompt tokens, audio ring
+# capacity or None, weight file kind)
+CASES = [(512, 0, 38, 64, "q4km"),          # the stream prompt at positions 0..37
+         (512, 986, 38, 48, "q4km"),        # after a wrap: evictions, the audio ring wraps too
+         (512, 0, 1, 64, "q4km"),           # prompts of a few tokens: the normed products at the
+         (512, 40, 3, 64, "q4km"),          # decoder's width 3072 take the separate input
+         (512, 300, 5, 48, "q4km"),         # quantization (a prompt's window is one segment)
+         (512, 0, 38, 64, "q8_0"),          # a Q8_0 file: every product on q8_0 images
+         (512, 40, 3, 64, "q8_0")]
 
 
-@pytest.mark.parametrize("cap,P,N,acap", CASES)
-def test_prompt_two_layers(cap, P, N, acap):
+@pytest.mark.parametrize("cap,P,N,acap,kind", CASES)
+def test_prompt_two_layers(cap, P, N, acap, kind):
     rng = np.random.default_rng(7100 + P)
     n_layers, vocab = 2, 4096
-    m = tok.make_model(rng, n_layers, vocab)
+    m = tok.make_model(rng, n_layers, vocab, kind)
     model, keep, arr = tok.upload_model(m)
     tokens = [int(t) for t in rng.integers(0, vocab, N)]
     tokens[0], tokens[-1] = 0, vocab - 1
@@ -248,7 +252,7 @@ def test_prompt_two_layers(cap, P, N, acap):
     lb = torch.empty(vocab, device=dev())
     tb = torch.zeros(1, dtype=torch.int32, device=dev())
     plan_b, xb = composed_prompt(cb, rb, model, tokens, aring, lb, tb, sp, m)
-    print(f"prompt cap={cap} P={P} N={N}: composed stages ok", flush=True)
+    print(f"prompt cap={cap} P={P} N={N} {kind}: composed stages ok", flush=True)
 
     assert np.array_equal(host(la).view(np.uint32), host(lb).view(np.uint32))
     assert int(host(ta)[0]) == int(host(tb)[0])
@@ -273,7 +277,7 @@ def test_prompt_two_layers(cap, P, N, acap):
     spread = np.abs(want.astype(np.float64) - want_x).max()
     err = np.abs(got - want).max()
     corr = np.corrcoef(got, want)[0, 1]
-    print(f"prompt cap={cap} P={P} N={N}: end to end {err:.3f}, mimic-exact spread {spread:.3f}, "
+    print(f"prompt cap={cap} P={P} N={N} {kind}: end to end {err:.3f}, mimic-exact spread {spread:.3f}, "
           f"range {scale:.2f}", flush=True)
     assert err <= 1e-2 * scale + spread and corr > 0.9999, (err, scale, spread, corr)
     top2 = np.sort(want)[-2:]

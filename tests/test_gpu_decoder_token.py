@@ -146,23 +146,43 @@ def test_argmax_matches_ggml_rule():
 
 # ---- one full decoder token ----
 
-def make_model(rng, n_layers, vocab):
-    """Random Q4_K_M decoder weights (numpy) with moderate magnitudes."""
+# weight types of the two file kinds: the Q4_K_M mix (src/voxtral-quantize.cpp:
+# 148-159) and a Q8_0 file (:95-96, every matrix Q8_0)
+MIX = {"q4km": dict(attn_q=vkv.Q4_K, attn_k=vkv.Q4_K, attn_v=vkv.Q6_K, attn_o=vkv.Q4_K,
+                    ffn_w1=vkv.Q4_K, ffn_w3=vkv.Q4_K, ffn_w2=vkv.Q6_K, table=vkv.Q6_K),
+       "q8_0": dict(attn_q=vkv.Q8_0, attn_k=vkv.Q8_0, attn_v=vkv.Q8_0, attn_o=vkv.Q8_0,
+                    ffn_w1=vkv.Q8_0, ffn_w3=vkv.Q8_0, ffn_w2=vkv.Q8_0, table=vkv.Q8_0)}
+
+
+def wscale(dtype, slot):
+    """random_matrix's scale factor for a Q8_0 matrix in a slot the Q4_K_M mix
+    fills with Q4_K (typical |w| ~0.4 x scale) or Q6_K (~0.1 x scale): Q8_0
+    blocks are ~1 x scale, so the activations keep the magnitudes the bounds
+    below were set for"""
+    if dtype != vkv.Q8_0:
+        return 1.0
+    return 0.11 if MIX["q4km"][slot] == vkv.Q6_K else 0.4
+
+
+def make_model(rng, n_layers, vocab, kind="q4km"):
+    """Random decoder weights (numpy) of one file kind, moderate magnitudes."""
+    T = MIX[kind]
     layers = []
     for layer in range(n_layers):
         layers.append(dict(
             attn_norm=rng.uniform(0.5, 1.5, DIM).astype(np.float32),
-            attn_q=random_matrix(rng, vkv.Q4_K, QD, DIM, 0.005),
-            attn_k=random_matrix(rng, vkv.Q4_K, KD, DIM, 0.005),
-            attn_v=random_matrix(rng, vkv.Q6_K, KD, DIM, 0.1),
-            attn_o=random_matrix(rng, vkv.Q4_K, DIM, QD, 0.005),
+            attn_q=random_matrix(rng, T["attn_q"], QD, DIM, 0.005 * wscale(T["attn_q"], "attn_q")),
+            attn_k=random_matrix(rng, T["attn_k"], KD, DIM, 0.005 * wscale(T["attn_k"], "attn_k")),
+            attn_v=random_matrix(rng, T["attn_v"], KD, DIM, 0.1 * wscale(T["attn_v"], "attn_v")),
+            attn_o=random_matrix(rng, T["attn_o"], DIM, QD, 0.005 * wscale(T["attn_o"], "attn_o")),
             ffn_norm=rng.uniform(0.5, 1.5, DIM).astype(np.float32),
             ada=rng.uniform(-0.3, 0.3, DIM).astype(np.float32) if layer == 0 else None,
-            ffn_w1=random_matrix(rng, vkv.Q4_K, HID, DIM, 0.003),
-            ffn_w3=random_matrix(rng, vkv.Q4_K, HID, DIM, 0.003),
-            ffn_w2=random_matrix(rng, vkv.Q6_K, DIM, HID, 0.05)))
-    return dict(layers=layers, table=random_matrix(rng, vkv.Q6_K, vocab, DIM, 0.5),
-                out_norm=rng.uniform(0.5, 1.5, DIM).astype(np.float32), vocab=vocab)
+            ffn_w1=random_matrix(rng, T["ffn_w1"], HID, DIM, 0.003 * wscale(T["ffn_w1"], "ffn_w1")),
+            ffn_w3=random_matrix(rng, T["ffn_w3"], HID, DIM, 0.003 * wscale(T["ffn_w3"], "ffn_w3")),
+            ffn_w2=random_matrix(rng, T["ffn_w2"], DIM, HID, 0.05 * wscale(T["ffn_w2"], "ffn_w2"))))
+    return dict(layers=layers, table=random_matrix(rng, T["table"], vocab, DIM,
+                                                   0.5 * wscale(T["table"], "table")),
+                out_norm=rng.uniform(0.5, 1.5, DIM).astype(np.float32), vocab=vocab, types=T)
 
 
 def upload_model(m):
@@ -177,15 +197,16 @@ def upload_model(m):
         return t.data_ptr()
 
     n = len(m["layers"])
+    T = m["types"]
     arr = (vkv.DecLayer * n)()
     for i, L in enumerate(m["layers"]):
         arr[i] = vkv.DecLayer(d(L["attn_norm"]), d(L["attn_q"]), d(L["attn_k"]), d(L["attn_v"]),
-                              d(L["attn_o"]), vkv.Q4_K, vkv.Q4_K, vkv.Q6_K, vkv.Q4_K,
+                              d(L["attn_o"]), T["attn_q"], T["attn_k"], T["attn_v"], T["attn_o"],
                               d(L["ffn_norm"]), d(L["ada"]), d(L["ffn_w1"]), d(L["ffn_w2"]),
-                              d(L["ffn_w3"]), vkv.Q4_K, vkv.Q6_K, vkv.Q4_K)
+                              d(L["ffn_w3"]), T["ffn_w1"], T["ffn_w2"], T["ffn_w3"])
     table = d(m["table"])
-    model = vkv.DecModel(n, DIM, HID, QH, KVH, HD, m["vocab"], EPS, THETA, table, vkv.Q6_K,
-                         d(m["out_norm"]), table, vkv.Q6_K, arr)
+    model = vkv.DecModel(n, DIM, HID, QH, KVH, HD, m["vocab"], EPS, THETA, table, T["table"],
+                         d(m["out_norm"]), table, T["table"], arr)
     return model, keep, arr
 
 
@@ -210,8 +231,8 @@ def composed_token(cache, ring, model, token, audio_ptr, logits, tok_out, hip_st
         want = np.asarray(want, np.float64)
         return np.abs(np.asarray(got, np.float64) - want).max() / max(np.abs(want).max(), 1e-30)
 
-    vkv.embed(vkv.Q6_K, model.tok_embeddings, model.vocab, DIM, token, x.data_ptr(), audio_ptr,
-              hip_stream=hip_stream)
+    vkv.embed(model.tok_embeddings_type, model.tok_embeddings, model.vocab, DIM, token, x.data_ptr(),
+              audio_ptr, hip_stream=hip_stream)
     xp = x.data_ptr()
     for layer in range(model.n_layers):
         L = model.layers[layer]
@@ -224,9 +245,9 @@ def composed_token(cache, ring, model, token, audio_ptr, logits, tok_out, hip_st
             M = m["layers"][layer]
             h = oracle.norm_act(x_in, M["attn_norm"], None, EPS)
             q_in, k_in, v_in = host(q), host(k), host(v)
-            assert rel(q_in, oracle.matvec(oracle.Q4_K, M["attn_q"], QD, DIM, h, 8)) < 2e-6
-            assert rel(k_in, oracle.matvec(oracle.Q4_K, M["attn_k"], KD, DIM, h, 8)) < 2e-6
-            assert rel(v_in, oracle.matvec(oracle.Q6_K, M["attn_v"], KD, DIM, h, 8)) < 2e-6
+            assert rel(q_in, oracle.matvec(L.attn_q_type, M["attn_q"], QD, DIM, h, 8)) < 2e-6
+            assert rel(k_in, oracle.matvec(L.attn_k_type, M["attn_k"], KD, DIM, h, 8)) < 2e-6
+            assert rel(v_in, oracle.matvec(L.attn_v_type, M["attn_v"], KD, DIM, h, 8)) < 2e-6
         cache.decoder_layer_step(0, plan, pos, layer, 1, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                                  attn.data_ptr(), SCALE, THETA, hip_stream=hip_stream)
         if m:
@@ -258,21 +279,21 @@ def composed_token(cache, ring, model, token, audio_ptr, logits, tok_out, hip_st
                    hip_stream=hip_stream)
         if m:
             x_o = host(x)
-            assert rel(x_o, x_mid + oracle.matvec(oracle.Q4_K, M["attn_o"], DIM, QD, a_got, 8)) < 2e-6
+            assert rel(x_o, x_mid + oracle.matvec(L.attn_o_type, M["attn_o"], DIM, QD, a_got, 8)) < 2e-6
         vkv.matvec(xp, DIM, [(L.ffn_w1, L.ffn_w1_type, HID, ffn.data_ptr()),
                              (L.ffn_w3, L.ffn_w3_type, HID, None)],
                    norm_w_ptr=L.ffn_norm, ada_ptr=L.ada_scale, eps=EPS,
                    epilogue=vkv.MV_SWIGLU, hip_stream=hip_stream)
         if m:
             h2 = oracle.norm_act(x_o, M["ffn_norm"], M["ada"], EPS)
-            g = oracle.matvec(oracle.Q4_K, M["ffn_w1"], HID, DIM, h2, 8)
-            u = oracle.matvec(oracle.Q4_K, M["ffn_w3"], HID, DIM, h2, 8)
+            g = oracle.matvec(L.ffn_w1_type, M["ffn_w1"], HID, DIM, h2, 8)
+            u = oracle.matvec(L.ffn_w3_type, M["ffn_w3"], HID, DIM, h2, 8)
             f_got = host(ffn)
             assert rel(f_got, oracle.silu(g) * u) < 2e-6
         vkv.matvec(ffn.data_ptr(), HID, [(L.ffn_w2, L.ffn_w2_type, DIM, xp, xp)],
                    hip_stream=hip_stream)
         if m:
-            assert rel(host(x), x_o + oracle.matvec(oracle.Q6_K, M["ffn_w2"], DIM, HID, f_got, 8)) < 2e-6
+            assert rel(host(x), x_o + oracle.matvec(L.ffn_w2_type, M["ffn_w2"], DIM, HID, f_got, 8)) < 2e-6
     x_fin = host(x) if m else None
     vkv.matvec(xp, DIM, [(model.output, model.output_type, model.vocab, logits.data_ptr())],
                norm_w_ptr=model.out_norm, eps=EPS, hip_stream=hip_stream)
@@ -280,7 +301,7 @@ def composed_token(cache, ring, model, token, audio_ptr, logits, tok_out, hip_st
     if m:
         lg = host(logits)
         xn = oracle.norm_act(x_fin, m["out_norm"], None, EPS)
-        assert rel(lg, oracle.matvec(oracle.Q6_K, m["table"], model.vocab, DIM, xn, 8)) < 2e-6
+        assert rel(lg, oracle.matvec(model.output_type, m["table"], model.vocab, DIM, xn, 8)) < 2e-6
         assert int(host(tok_out)[0]) == oracle.argmax(lg)
     vkv.decoder_commit(ring, plan)
     return plan, x
@@ -289,36 +310,38 @@ def composed_token(cache, ring, model, token, audio_ptr, logits, tok_out, hip_st
 def oracle_token(m, k_imgs, v_imgs, row_b, plan, pos, token, audio, attn_fn):
     """ggml's CPU path for the same token (oracle restatements throughout);
     attn_fn: the oracle's fp64 attention or its ggml flash-attention mimic."""
-    rb = DIM // 256 * 210
-    x = oracle.dequantize(oracle.Q6_K, m["table"][token * rb:(token + 1) * rb], DIM) + audio
+    T = m["types"]
+    rb = oracle.wrow_bytes(T["table"], DIM)
+    x = oracle.dequantize(T["table"], m["table"][token * rb:(token + 1) * rb], DIM) + audio
     slot = plan.write_seg[0].slot
     slots = plan_slots(plan)
     for layer, L in enumerate(m["layers"]):
         h = oracle.norm_act(x, L["attn_norm"], None, EPS)
-        q = oracle.matvec(oracle.Q4_K, L["attn_q"], QD, DIM, h, 8)
-        k = oracle.matvec(oracle.Q4_K, L["attn_k"], KD, DIM, h, 8)
-        v = oracle.matvec(oracle.Q6_K, L["attn_v"], KD, DIM, h, 8)
+        q = oracle.matvec(T["attn_q"], L["attn_q"], QD, DIM, h, 8)
+        k = oracle.matvec(T["attn_k"], L["attn_k"], KD, DIM, h, 8)
+        v = oracle.matvec(T["attn_v"], L["attn_v"], KD, DIM, h, 8)
         q = oracle.rope(q.reshape(1, QD), HD, pos, THETA).ravel()
         k = oracle.rope(k.reshape(1, KD), HD, pos, THETA).ravel()
         ki, vi = k_imgs[layer].copy(), v_imgs[layer].copy()
         ki[slot * row_b:(slot + 1) * row_b] = np.frombuffer(oracle.rows_from_f32(oracle.F16, k), np.uint8)
         vi[slot * row_b:(slot + 1) * row_b] = np.frombuffer(oracle.rows_from_f32(oracle.F16, v), np.uint8)
         attn = attn_fn(oracle.F16, ki, vi, row_b, slots, q, KVH, HD, SCALE).ravel()
-        x = x + oracle.matvec(oracle.Q4_K, L["attn_o"], DIM, QD, attn, 8)
+        x = x + oracle.matvec(T["attn_o"], L["attn_o"], DIM, QD, attn, 8)
         h = oracle.norm_act(x, L["ffn_norm"], L["ada"], EPS)
-        g = oracle.matvec(oracle.Q4_K, L["ffn_w1"], HID, DIM, h, 8)
-        u = oracle.matvec(oracle.Q4_K, L["ffn_w3"], HID, DIM, h, 8)
+        g = oracle.matvec(T["ffn_w1"], L["ffn_w1"], HID, DIM, h, 8)
+        u = oracle.matvec(T["ffn_w3"], L["ffn_w3"], HID, DIM, h, 8)
         f = (oracle.silu(g) * u).astype(np.float32)
-        x = x + oracle.matvec(oracle.Q6_K, L["ffn_w2"], DIM, HID, f, 8)
+        x = x + oracle.matvec(T["ffn_w2"], L["ffn_w2"], DIM, HID, f, 8)
     xn = oracle.norm_act(x, m["out_norm"], None, EPS)
-    logits = oracle.matvec(oracle.Q6_K, m["table"], m["vocab"], DIM, xn, 8)
+    logits = oracle.matvec(T["table"], m["table"], m["vocab"], DIM, xn, 8)
     return logits, oracle.argmax(logits)
 
 
-def test_decoder_token_two_layers():
+@pytest.mark.parametrize("kind", ["q4km", "q8_0"])
+def test_decoder_token_two_layers(kind):
     rng = np.random.default_rng(5219)
     n_layers, vocab, CAP, P, token = 2, 4096, 512, 700, 1234
-    m = make_model(rng, n_layers, vocab)
+    m = make_model(rng, n_layers, vocab, kind)
     model, keep, arr = upload_model(m)
     audio = (rng.standard_normal(DIM) * 0.1).astype(np.float32)
     ad = to_dev(audio)

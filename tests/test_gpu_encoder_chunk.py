@@ -34,27 +34,44 @@ def host(t):
     return t.cpu().numpy()
 
 
-def make_model(rng, n_layers):
+# weight types of the two file kinds: the Q4_K_M mix (src/voxtral-quantize.cpp:
+# 148-159) and a Q8_0 file (:95-96)
+MIX = {"q4km": dict(attn_q=vkv.Q4_K, attn_k=vkv.Q4_K, attn_v=vkv.Q6_K, attn_o=vkv.Q4_K,
+                    ffn_w1=vkv.Q4_K, ffn_w3=vkv.Q4_K, ffn_w2=vkv.Q6_K),
+       "q8_0": dict(attn_q=vkv.Q8_0, attn_k=vkv.Q8_0, attn_v=vkv.Q8_0, attn_o=vkv.Q8_0,
+                    ffn_w1=vkv.Q8_0, ffn_w3=vkv.Q8_0, ffn_w2=vkv.Q8_0)}
+
+
+def wscale(dtype, slot):
+    """a Q8_0 matrix's scale factor for the magnitudes of the slot's k-quant
+    (Q4_K ~0.4 x scale, Q6_K ~0.1 x scale, Q8_0 ~1 x scale)"""
+    if dtype != vkv.Q8_0:
+        return 1.0
+    return 0.11 if MIX["q4km"][slot] == vkv.Q6_K else 0.4
+
+
+def make_model(rng, n_layers, kind="q4km"):
+    T = MIX[kind]
     layers = []
     for _ in range(n_layers):
         layers.append(dict(
             attn_norm=rng.uniform(0.5, 1.5, DIM).astype(np.float32),
             attn_norm_b=rng.uniform(-0.1, 0.1, DIM).astype(np.float32),
-            attn_q=random_matrix(rng, vkv.Q4_K, QD, DIM, 0.01),
-            attn_k=random_matrix(rng, vkv.Q4_K, QD, DIM, 0.01),
-            attn_v=random_matrix(rng, vkv.Q6_K, QD, DIM, 0.1),
-            attn_o=random_matrix(rng, vkv.Q4_K, DIM, QD, 0.01),
+            attn_q=random_matrix(rng, T["attn_q"], QD, DIM, 0.01 * wscale(T["attn_q"], "attn_q")),
+            attn_k=random_matrix(rng, T["attn_k"], QD, DIM, 0.01 * wscale(T["attn_k"], "attn_k")),
+            attn_v=random_matrix(rng, T["attn_v"], QD, DIM, 0.1 * wscale(T["attn_v"], "attn_v")),
+            attn_o=random_matrix(rng, T["attn_o"], DIM, QD, 0.01 * wscale(T["attn_o"], "attn_o")),
             attn_q_b=rng.uniform(-0.1, 0.1, QD).astype(np.float32),
             attn_v_b=rng.uniform(-0.1, 0.1, QD).astype(np.float32),
             attn_o_b=rng.uniform(-0.1, 0.1, DIM).astype(np.float32),
             ffn_norm=rng.uniform(0.5, 1.5, DIM).astype(np.float32),
             ffn_norm_b=rng.uniform(-0.1, 0.1, DIM).astype(np.float32),
-            ffn_w1=random_matrix(rng, vkv.Q4_K, HID, DIM, 0.005),
-            ffn_w3=random_matrix(rng, vkv.Q4_K, HID, DIM, 0.005),
-            ffn_w2=random_matrix(rng, vkv.Q6_K, DIM, HID, 0.05),
+            ffn_w1=random_matrix(rng, T["ffn_w1"], HID, DIM, 0.005 * wscale(T["ffn_w1"], "ffn_w1")),
+            ffn_w3=random_matrix(rng, T["ffn_w3"], HID, DIM, 0.005 * wscale(T["ffn_w3"], "ffn_w3")),
+            ffn_w2=random_matrix(rng, T["ffn_w2"], DIM, HID, 0.05 * wscale(T["ffn_w2"], "ffn_w2")),
             ffn_w2_b=rng.uniform(-0.1, 0.1, DIM).astype(np.float32)))
     return dict(layers=layers, out_norm=rng.uniform(0.5, 1.5, DIM).astype(np.float32),
-                out_norm_b=rng.uniform(-0.1, 0.1, DIM).astype(np.float32))
+                out_norm_b=rng.uniform(-0.1, 0.1, DIM).astype(np.float32), types=T)
 
 
 def upload(m):
@@ -66,13 +83,14 @@ def upload(m):
         return t.data_ptr()
 
     n = len(m["layers"])
+    T = m["types"]
     arr = (vkv.EncLayer * n)()
     for i, L in enumerate(m["layers"]):
         arr[i] = vkv.EncLayer(d(L["attn_norm"]), d(L["attn_norm_b"]), d(L["attn_q"]), d(L["attn_k"]),
-                              d(L["attn_v"]), d(L["attn_o"]), vkv.Q4_K, vkv.Q4_K, vkv.Q6_K, vkv.Q4_K,
-                              d(L["attn_q_b"]), d(L["attn_v_b"]), d(L["attn_o_b"]), d(L["ffn_norm"]),
-                              d(L["ffn_norm_b"]), d(L["ffn_w1"]), d(L["ffn_w2"]), d(L["ffn_w3"]),
-                              vkv.Q4_K, vkv.Q6_K, vkv.Q4_K, d(L["ffn_w2_b"]))
+                              d(L["attn_v"]), d(L["attn_o"]), T["attn_q"], T["attn_k"], T["attn_v"],
+                              T["attn_o"], d(L["attn_q_b"]), d(L["attn_v_b"]), d(L["attn_o_b"]),
+                              d(L["ffn_norm"]), d(L["ffn_norm_b"]), d(L["ffn_w1"]), d(L["ffn_w2"]),
+                              d(L["ffn_w3"]), T["ffn_w1"], T["ffn_w2"], T["ffn_w3"], d(L["ffn_w2_b"]))
     model = vkv.EncModel(n, DIM, HID, H, HD, EPS, THETA, d(m["out_norm"]), d(m["out_norm_b"]), arr)
     return model, keep, arr
 
@@ -122,9 +140,9 @@ def composed(c, plan, model, m, x, check):
         if check:
             hs = [oracle.norm_act(x_in[p], M["attn_norm"], eps=EPS, norm_b=M["attn_norm_b"]) for p in range(N)]
             q_in, k_in, v_in = host(qk[0]), host(qk[1]), host(v)
-            for got, w, dt, b in ((q_in, M["attn_q"], vkv.Q4_K, M["attn_q_b"]),
-                                  (k_in, M["attn_k"], vkv.Q4_K, None),
-                                  (v_in, M["attn_v"], vkv.Q6_K, M["attn_v_b"])):
+            for got, w, dt, b in ((q_in, M["attn_q"], L.attn_q_type, M["attn_q_b"]),
+                                  (k_in, M["attn_k"], L.attn_k_type, None),
+                                  (v_in, M["attn_v"], L.attn_v_type, M["attn_v_b"])):
                 want, mag = rows_ref(dt, w, QD, DIM, hs)
                 if b is not None:
                     want = want + b[None, :]
@@ -155,7 +173,7 @@ def composed(c, plan, model, m, x, check):
                    ws, ws_b, hip_stream=sp)
         if check:
             x_o = host(x)
-            proj, mag = rows_ref(vkv.Q4_K, M["attn_o"], DIM, QD, list(a_got))
+            proj, mag = rows_ref(L.attn_o_type, M["attn_o"], DIM, QD, list(a_got))
             want = x_mid + (proj + M["attn_o_b"][None, :])
             assert np.all(np.abs(x_o - want) <= 1e-5 * mag + 2e-7 * np.abs(want) + 1e-30)
         vkv.matmul(xp, N, DIM, [(L.ffn_w1, L.ffn_w1_type, HID, ffn.data_ptr()),
@@ -164,8 +182,8 @@ def composed(c, plan, model, m, x, check):
                    epilogue=vkv.MV_SWIGLU, hip_stream=sp)
         if check:
             hs = [oracle.norm_act(x_o[p], M["ffn_norm"], eps=EPS, norm_b=M["ffn_norm_b"]) for p in range(N)]
-            g, m1 = rows_ref(vkv.Q4_K, M["ffn_w1"], HID, DIM, hs)
-            u, m3 = rows_ref(vkv.Q4_K, M["ffn_w3"], HID, DIM, hs)
+            g, m1 = rows_ref(L.ffn_w1_type, M["ffn_w1"], HID, DIM, hs)
+            u, m3 = rows_ref(L.ffn_w3_type, M["ffn_w3"], HID, DIM, hs)
             g64, u64 = g.astype(np.float64), u.astype(np.float64)
             sg = g64 / (1 + np.exp(-g64))
             f_got = host(ffn)
@@ -174,17 +192,19 @@ def composed(c, plan, model, m, x, check):
         vkv.matmul(ffn.data_ptr(), N, HID, [(L.ffn_w2, L.ffn_w2_type, DIM, xp, xp, L.ffn_w2_b)],
                    ws, ws_b, hip_stream=sp)
         if check:
-            proj, mag = rows_ref(vkv.Q6_K, M["ffn_w2"], DIM, HID, list(f_got))
+            proj, mag = rows_ref(L.ffn_w2_type, M["ffn_w2"], DIM, HID, list(f_got))
             want = x_o + (proj + M["ffn_w2_b"][None, :])
             assert np.all(np.abs(host(x) - want) <= 1e-5 * mag + 2e-7 * np.abs(want) + 1e-30)
     return ws_t
 
 
-@pytest.mark.parametrize("q_start,n_new", [(800, 16), (1296, 4), (64, 16)])
-def test_encoder_chunk(q_start, n_new):
+@pytest.mark.parametrize("q_start,n_new,kind", [(800, 16, "q4km"), (1296, 4, "q4km"),
+                                                (64, 16, "q4km"), (800, 16, "q8_0"),
+                                                (1296, 4, "q8_0")])
+def test_encoder_chunk(q_start, n_new, kind):
     rng = np.random.default_rng(q_start + n_new)
     n_layers = 2
-    m = make_model(rng, n_layers)
+    m = make_model(rng, n_layers, kind)
     model, keep, arr = upload(m)
     x0 = rng.standard_normal((n_new, DIM)).astype(np.float32)
     ca, cb = filled_ring(n_layers, q_start), filled_ring(n_layers, q_start)

@@ -42,7 +42,7 @@ def encoder():
     rng = np.random.default_rng(2136)
     sets = [make_model(rng, 1) for _ in range(4)]
     m = dict(layers=[sets[i % 4]["layers"][0] for i in range(LAYERS)],
-             out_norm=sets[0]["out_norm"], out_norm_b=sets[0]["out_norm_b"])
+             out_norm=sets[0]["out_norm"], out_norm_b=sets[0]["out_norm_b"], types=sets[0]["types"])
     model, keep, arr = upload(m)
     w0, b0, w1, b1 = conv_weights(rng)
     conv = [torch.from_numpy(np.ascontiguousarray(a)).to(dev()) for a in (w0, b0, w1, b1)]

@@ -32,6 +32,17 @@ def model_file(tmp_path_factory):
     return str(p), og.read(data)
 
 
+@pytest.fixture(scope="module")
+def q8_0_file(tmp_path_factory):
+    """a Q8_0 file (src/voxtral-quantize.cpp:95-96): every matrix Q8_0"""
+    kvs, tensors = realtime_model(np.random.default_rng(95), enc_layers=ENC_L, dec_layers=DEC_L,
+                                  vocab=VOCAB, q4=8, q6=8)
+    data = gguf_bytes(kvs, tensors)
+    p = tmp_path_factory.mktemp("gguf") / "realtime_q8_0.gguf"
+    p.write_bytes(data)
+    return str(p), og.read(data)
+
+
 def d2h(ptr, n):
     torch.cuda.synchronize()
     out = torch.empty(n, dtype=torch.uint8)
@@ -112,8 +123,10 @@ def test_view_maps_the_reference_names(model_file):
 
 
 def independent(g):
-    """the same tensors uploaded one by one (no loader), described by hand"""
+    """the same tensors uploaded one by one (no loader), described by hand
+    (types as the file records them)"""
     keep = {}
+    types = {ti["name"]: ti["type"] for ti in g["tensors"]}
     for ti in g["tensors"]:
         b = np.frombuffer(og.tensor_bytes(g, ti), np.uint8).copy()
         keep[ti["name"]] = torch.from_numpy(b).to(dev())
@@ -121,26 +134,34 @@ def independent(g):
     def at(n):
         return keep[n].data_ptr()
 
+    def ty(p, *names):
+        return [types[p + n + ".weight"] for n in names]
+
     el = (vkv.EncLayer * ENC_L)()
     for i in range(ENC_L):
         p = f"enc.blk.{i}."
         el[i] = vkv.EncLayer(at(p + "attn_norm.weight"), None, at(p + "attn_q.weight"),
                              at(p + "attn_k.weight"), at(p + "attn_v.weight"), at(p + "attn_o.weight"),
-                             12, 12, 14, 12, at(p + "attn_q.bias"), at(p + "attn_v.bias"),
-                             at(p + "attn_o.bias"), at(p + "ffn_norm.weight"), None,
-                             at(p + "ffn_w1.weight"), at(p + "ffn_w2.weight"), at(p + "ffn_w3.weight"),
-                             12, 14, 12, at(p + "ffn_w2.bias"))
+                             *ty(p, "attn_q", "attn_k", "attn_v", "attn_o"), at(p + "attn_q.bias"),
+                             at(p + "attn_v.bias"), at(p + "attn_o.bias"), at(p + "ffn_norm.weight"),
+                             None, at(p + "ffn_w1.weight"), at(p + "ffn_w2.weight"),
+                             at(p + "ffn_w3.weight"), *ty(p, "ffn_w1", "ffn_w2", "ffn_w3"),
+                             at(p + "ffn_w2.bias"))
     enc = vkv.EncModel(ENC_L, 1280, 5120, 32, 64, 1e-5, 1e6, at("enc.norm.weight"), None, el)
     dl = (vkv.DecLayer * DEC_L)()
     for i in range(DEC_L):
         p = f"dec.blk.{i}."
         dl[i] = vkv.DecLayer(at(p + "attn_norm.weight"), at(p + "attn_q.weight"), at(p + "attn_k.weight"),
-                             at(p + "attn_v.weight"), at(p + "attn_o.weight"), 12, 12, 14, 12,
+                             at(p + "attn_v.weight"), at(p + "attn_o.weight"),
+                             *ty(p, "attn_q", "attn_k", "attn_v", "attn_o"),
                              at(p + "ffn_norm.weight"), None, at(p + "ffn_w1.weight"),
-                             at(p + "ffn_w2.weight"), at(p + "ffn_w3.weight"), 12, 14, 12)
-    dec = vkv.DecModel(DEC_L, 3072, 9216, 32, 8, 128, VOCAB, 1e-5, 1e6, at("tok_embeddings.weight"), 14,
-                       at("norm.weight"), at("tok_embeddings.weight"), 14, dl)
-    ad = vkv.Adapter(at("adapter.0.weight"), at("adapter.2.weight"), 12, 12, 1280, 3072, 4)
+                             at(p + "ffn_w2.weight"), at(p + "ffn_w3.weight"),
+                             *ty(p, "ffn_w1", "ffn_w2", "ffn_w3"))
+    tt = types["tok_embeddings.weight"]
+    dec = vkv.DecModel(DEC_L, 3072, 9216, 32, 8, 128, VOCAB, 1e-5, 1e6, at("tok_embeddings.weight"), tt,
+                       at("norm.weight"), at("tok_embeddings.weight"), tt, dl)
+    ad = vkv.Adapter(at("adapter.0.weight"), at("adapter.2.weight"), types["adapter.0.weight"],
+                     types["adapter.2.weight"], 1280, 3072, 4)
     conv = (at("enc.conv0.weight"), at("enc.conv0.bias"), at("enc.conv1.weight"), at("enc.conv1.bias"))
     return dict(enc=enc, dec=dec, adapter=ad, conv=conv, keep=(keep, el, dl))
 
@@ -228,8 +249,9 @@ def test_ada_scales_of_the_loaded_model(model_file):
     m.close()
 
 
-def test_a_realtime_step_from_the_loaded_model(model_file):
-    path, g = model_file
+@pytest.mark.parametrize("kind", ["q4km", "q8_0"])
+def test_a_realtime_step_from_the_loaded_model(kind, request):
+    path, g = request.getfixturevalue("model_file" if kind == "q4km" else "q8_0_file")
     rng = np.random.default_rng(5424)
     plan = vkv.enc_plan(0, 16, 878, 750)
     win = plan.conv_mel_end - plan.conv_mel_start
@@ -245,10 +267,12 @@ def test_a_realtime_step_from_the_loaded_model(model_file):
     ind_scales = torch.empty(DEC_L, 3072, device=dev())
     wb = vkv.ada_scale_workspace(3072, 32)
     ws = torch.empty(wb // 4 + 64, device=dev())
+    types = {ti["name"]: ti["type"] for ti in g["tensors"]}
     for l in range(DEC_L):
         k = ind["keep"][0]
-        vkv.ada_scale(k[f"dec.blk.{l}.ada0.weight"].data_ptr(), 12, k[f"dec.blk.{l}.ada2.weight"].data_ptr(),
-                      1, 3072, 32, 6.0, ind_scales[l].data_ptr(), (ws.data_ptr() + 255) & ~255, wb,
+        a0, a2 = f"dec.blk.{l}.ada0.weight", f"dec.blk.{l}.ada2.weight"
+        vkv.ada_scale(k[a0].data_ptr(), types[a0], k[a2].data_ptr(), types[a2], 3072, 32, 6.0,
+                      ind_scales[l].data_ptr(), (ws.data_ptr() + 255) & ~255, wb,
                       hip_stream=stream_ptr())
         ind["dec"].layers[l].ada_scale = ind_scales[l].data_ptr()
     want = realtime_step(ind["enc"], ind["dec"], ind["adapter"], ind["conv"], mel, plan)
@@ -276,8 +300,8 @@ def small_file(tmp_path, name, edit=None, arch="voxtral_realtime"):
 def test_model_errors(tmp_path):
     """the loader's model errors (voxtral_model_load's MODEL_ERROR): the
     offline architecture, a missing required tensor, a matrix of a type the
-    products do not take, a tensor of the wrong shape; a small realtime file
-    loads"""
+    products do not take, Q/K/V mixing Q8_0 with k-quants, a tensor of the
+    wrong shape; a small realtime file loads"""
     m = vkv.Model(small_file(tmp_path, "ok.gguf"), hip_stream=stream_ptr())
     assert m.view.hp.dec_dim == 256 and m.view.dec.layers[1].attn_q is not None
     m.close()
@@ -287,7 +311,11 @@ def test_model_errors(tmp_path):
                          "dec.blk.1.ffn_w2.weight"),
         "f16mat.gguf": (lambda T: [(n, 1, ne, np.zeros(ne[0] * ne[1] * 2, np.uint8).tobytes())
                                    if n == "enc.blk.0.attn_o.weight" else (n, t, ne, b)
-                                   for n, t, ne, b in T], "voxtral_realtime", "Q4_K and Q6_K"),
+                                   for n, t, ne, b in T], "voxtral_realtime", "Q6_K and Q8_0"),
+        # one product call reads one input image: Q/K/V cannot mix Q8_0 and k-quants
+        "mixed.gguf": (lambda T: [(n, 8, ne, np.zeros(ne[1] * (ne[0] // 32) * 34, np.uint8).tobytes())
+                                  if n == "enc.blk.0.attn_v.weight" else (n, t, ne, b)
+                                  for n, t, ne, b in T], "voxtral_realtime", "mixes Q8_0"),
         "shape.gguf": (lambda T: [(n, t, [ne[0] // 2], b[:len(b) // 2]) if n == "norm.weight"
                                   else (n, t, ne, b) for n, t, ne, b in T], "voxtral_realtime",
                        "norm.weight"),
@@ -297,3 +325,33 @@ def test_model_errors(tmp_path):
             vkv.Model(small_file(tmp_path, name, edit, arch), hip_stream=stream_ptr())
         assert ei.value.status == vkv.MODEL_ERROR, name
         assert msg in vkv.last_error(), (name, vkv.last_error())
+
+
+def test_a_q8_0_file_maps_and_conditions(q8_0_file):
+    """the view of a Q8_0 file carries Q8_0 for every matrix, and its ada
+    scales (ada0 and ada2 both Q8_0) are vkv_ada_scale's and within the
+    oracle's bound (ggml's product on q8_0 activations for both layers)"""
+    path, g = q8_0_file
+    m = vkv.Model(path, hip_stream=stream_ptr())
+    v = m.view
+    L = v.enc.layers[0]
+    assert {L.attn_q_type, L.attn_k_type, L.attn_v_type, L.attn_o_type, L.ffn_w1_type,
+            L.ffn_w2_type, L.ffn_w3_type} == {vkv.Q8_0}
+    assert (v.adapter.w0_type, v.adapter.w2_type) == (vkv.Q8_0, vkv.Q8_0)
+    assert v.dec.tok_embeddings_type == v.dec.output_type == vkv.Q8_0
+    for l in range(DEC_L):
+        D = v.dec.layers[l]
+        assert {D.attn_q_type, D.attn_v_type, D.ffn_w1_type, D.ffn_w2_type} == {vkv.Q8_0}
+    scales = torch.full((DEC_L, 3072), np.nan, device=dev())
+    m.set_ada(6.0, scales.data_ptr(), hip_stream=stream_ptr())
+    got = scales.cpu().numpy()
+    for l in range(DEC_L):
+        t0 = next(t for t in g["tensors"] if t["name"] == f"dec.blk.{l}.ada0.weight")
+        t2 = next(t for t in g["tensors"] if t["name"] == f"dec.blk.{l}.ada2.weight")
+        assert t0["type"] == t2["type"] == vkv.Q8_0
+        w0 = np.frombuffer(og.tensor_bytes(g, t0), np.uint8)
+        w2 = np.frombuffer(og.tensor_bytes(g, t2), np.uint8)
+        want = oracle.ada_scale(oracle.Q8_0, w0, w2, 3072, 32, 6.0)
+        assert np.abs(want).max() > 1e-3
+        assert np.abs(got[l] - want).max() <= 1e-3 * np.abs(want).max()
+    m.close()

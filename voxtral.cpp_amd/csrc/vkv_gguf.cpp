@@ -539,7 +539,7 @@ struct vkv_model {
 
 namespace {
 
-constexpr int32_t kF32 = 0, kF16 = 1, kQ4K = 12, kQ6K = 14;
+constexpr int32_t kF32 = 0, kF16 = 1, kQ8_0 = 8, kQ4K = 12, kQ6K = 14;
 
 // Resolves the reference's tensor names against the file; the first problem
 // is kept as the load's error.
@@ -567,16 +567,17 @@ struct Mapper {
         }
         return (const float *)dev(ti);
     }
-    // a Q4_K / Q6_K matrix [rows][n_in]
+    // a Q4_K / Q6_K / Q8_0 matrix [rows][n_in] (the Q4_K_M mix, or a Q8_0
+    // file: src/voxtral-quantize.cpp:95-96)
     const void *mat(const std::string &name, int64_t rows, int64_t n_in, int32_t *type) {
         const TensorInfo *ti = info(name);
         if (!ti) {
             miss("tensor '" + name + "' not found");
             return nullptr;
         }
-        if (ti->t.type != kQ4K && ti->t.type != kQ6K) {
+        if (ti->t.type != kQ4K && ti->t.type != kQ6K && ti->t.type != kQ8_0) {
             miss("tensor '" + name + "' has ggml type " + std::to_string(ti->t.type) +
-                 "; the device products take Q4_K and Q6_K");
+                 "; the device products take Q4_K, Q6_K and Q8_0");
             return nullptr;
         }
         if (ti->t.n_dims != 2 || ti->t.ne[0] != n_in || ti->t.ne[1] != rows) {
@@ -684,6 +685,22 @@ vkv_status map_model(vkv_model &m) {
                           tok_type, mp.vec("norm.weight", dd), out, out_type, m.dec_layers.data()};
     const TensorInfo *mf = mp.info("audio.mel_filters");
     v.mel_filters = mf && mf->t.type == kF32 ? (const float *)mp.dev(mf) : nullptr;
+    // Matrices that share one product call read one input image (q8_0 for
+    // Q8_0 rows, Q8_K for the k-quants): a layer's Q/K/V are one call, and
+    // a SwiGLU pair takes one dtype.
+    auto q8 = [](int32_t t) { return t == kQ8_0; };
+    for (int l = 0; l < hp.enc_layers && mp.err.empty(); ++l) {
+        const vkv_enc_layer &L = m.enc_layers[(size_t)l];
+        if (q8(L.attn_q_type) != q8(L.attn_k_type) || q8(L.attn_q_type) != q8(L.attn_v_type) ||
+            L.ffn_w1_type != L.ffn_w3_type)
+            mp.miss(name("encoder layer %d mixes Q8_0 and k-quant matrices within one product", l));
+    }
+    for (int l = 0; l < hp.dec_layers && mp.err.empty(); ++l) {
+        const vkv_dec_layer &L = m.dec_layers[(size_t)l];
+        if (q8(L.attn_q_type) != q8(L.attn_k_type) || q8(L.attn_q_type) != q8(L.attn_v_type) ||
+            L.ffn_w1_type != L.ffn_w3_type)
+            mp.miss(name("decoder layer %d mixes Q8_0 and k-quant matrices within one product", l));
+    }
     if (!mp.err.empty()) return gfail(VKV_STATUS_MODEL_ERROR, "model: %s", mp.err.c_str());
     return VKV_STATUS_OK;
 }
@@ -830,8 +847,9 @@ vkv_status vkv_model_set_ada(vkv_model *model, float t, float *scales, void *hip
         const TensorInfo &a0 = model->g->tensors[(size_t)i0], &a2 = model->g->tensors[(size_t)i2];
         if (l == 0) ada_dim = a0.t.ne[1];
         if (a0.t.n_dims != 2 || a0.t.ne[0] != hp.dec_dim || a0.t.ne[1] != ada_dim ||
-            (a0.t.type != kQ4K && a0.t.type != kQ6K) || a2.t.n_dims != 2 || a2.t.ne[0] != ada_dim ||
-            a2.t.ne[1] != hp.dec_dim || (a2.t.type != kF16 && a2.t.type != kF32))
+            (a0.t.type != kQ4K && a0.t.type != kQ6K && a0.t.type != kQ8_0) || a2.t.n_dims != 2 ||
+            a2.t.ne[0] != ada_dim || a2.t.ne[1] != hp.dec_dim ||
+            (a2.t.type != kF16 && a2.t.type != kF32 && a2.t.type != kQ8_0))
             s = gfail(VKV_STATUS_MODEL_ERROR, "model: layer %d ada weights have unexpected shapes or types", l);
         w[(size_t)l] = {&a0, &a2};
     }

@@ -1378,13 +1378,16 @@ vkv_status vkv_ada_scale(const void *w0, int32_t w0_type, const void *w2, int32_
     if (!need) return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: dim=%d ada_dim=%d", dim, ada_dim);
     if (!w0 || !w2 || !out || !workspace)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: null argument");
-    if (!kq_block_bytes(w0_type) || (w2_type != VKV_DTYPE_F16 && w2_type != VKV_DTYPE_F32))
+    if (!kq_block_bytes(w0_type) ||
+        (w2_type != VKV_DTYPE_F16 && w2_type != VKV_DTYPE_F32 && w2_type != VKV_DTYPE_Q8_0))
         return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: weight dtypes %d / %d", w0_type, w2_type);
+    if (w2_type == VKV_DTYPE_Q8_0 && ada_dim % 32)
+        return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: Q8_0 W2 needs ada_dim %% 32 == 0");
     if (reinterpret_cast<uintptr_t>(workspace) & 255u)
         return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: workspace not 256-byte aligned");
     if (workspace_bytes < need)
         return fail(VKV_STATUS_BUFFER_TOO_SMALL, "ada scale: workspace %zu < %zu bytes", workspace_bytes, need);
-    if ((reinterpret_cast<uintptr_t>(w2) & (w2_type == VKV_DTYPE_F16 ? 1u : 3u)) ||
+    if ((reinterpret_cast<uintptr_t>(w2) & (w2_type == VKV_DTYPE_F32 ? 3u : 1u)) ||
         (reinterpret_cast<uintptr_t>(out) & 3u))
         return fail(VKV_STATUS_INVALID_ARGUMENT, "ada scale: misaligned w2 or out");
     // the time embedding as the reference computes it on the host
@@ -1408,7 +1411,7 @@ vkv_status vkv_ada_scale(const void *w0, int32_t w0_type, const void *w2, int32_
     if (vkv_status s = matvec_impl(e_dev, dim, nullptr, nullptr, 0.0f, h, 1, VKV_MV_GELU, hip_stream,
                                    nullptr, nullptr))
         return s;
-    e = launch_rows_small(w2, w2_type == VKV_DTYPE_F16, hidden, ada_dim, dim, out, st);
+    e = launch_rows_small(w2, w2_type, hidden, ada_dim, dim, out, st);
     if (e != hipSuccess) return hip_fail(e, "ada scale: second product launch");
     return ok();
 }

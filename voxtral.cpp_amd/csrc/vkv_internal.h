@@ -216,7 +216,8 @@ hipError_t launch_embed_rows(int dtype, const uint8_t *table, int64_t row_bytes,
                              int add_ring, int add_row0, float *y, hipStream_t st,
                              unsigned long long *zero_words = nullptr);
 hipError_t launch_argmax(const float *x, int n, int32_t *out, hipStream_t st);
-hipError_t launch_rows_small(const void *w, bool w_f16, const float *x, int n_in, int n_rows,
+// w_type: VKV_DTYPE_F32, _F16 or _Q8_0 (n_in % 32 == 0)
+hipError_t launch_rows_small(const void *w, int w_type, const float *x, int n_in, int n_rows,
                              float *y, hipStream_t st);
 // The encoder conv stem (vkv_conv.hip)
 hipError_t launch_im2col_f16(const float *in, int64_t stride_c, int64_t stride_t, int in_len,

@@ -492,7 +492,9 @@ __device__ __forceinline__ float compute_q4(const FragQ4 &f, const XFrag &x, int
     const int isum = sc_a * dot_a + sc_b * dot_b;
     const int imin = m_a * x.bs[0] + m_b * x.bs[1];
     const float d = h2f(f.c.x & 0xffffu) * x.dx, dmin = h2f(f.c.x >> 16) * x.dx;
-    return d * (float)isum - dmin * (float)imin;
+    // one explicit fma (not left to contraction, which may fuse either
+    // product depending on the kernel instantiation)
+    return fmaf(d, (float)isum, -(dmin * (float)imin));
 }
 
 __device__ __forceinline__ float compute_q6(const FragQ6 &f, const XFrag &x, uint32_t mis, int h) {
@@ -527,8 +529,12 @@ __device__ __forceinline__ float compute_q6(const FragQ6 &f, const XFrag &x, uin
 // Two Q8_0 blocks: block 2t's d is the first half of dword 0 and its codes
 // bytes 2..33 (realigned by 2), block 2t + 1's d the second half of dword 8
 // and its codes dwords 9..16; each block's integer dot times fp16(d_w) * d_x
-// (ggml_vec_dot_q8_0_q8_0's per-block term).
+// (ggml_vec_dot_q8_0_q8_0's per-block term).  The two terms meet in one
+// explicit fma: left to contraction, which product fuses depended on the
+// kernel instantiation, and the fused-argmax logits differed from the plain
+// ones in the last bit.
 __device__ __forceinline__ float compute_q8(const FragQ8 &f, const XFrag &x) {
+#pragma clang fp contract(off)
     const uint32_t w[17] = {f.a.x, f.a.y, f.a.z, f.a.w, f.b.x, f.b.y, f.b.z, f.b.w, f.c.x,
                             f.c.y, f.c.z, f.c.w, f.e.x, f.e.y, f.e.z, f.e.w, f.x};
     uint32_t q0[2][4], q1[2][4];
@@ -541,7 +547,7 @@ __device__ __forceinline__ float compute_q8(const FragQ8 &f, const XFrag &x) {
     const int s1 = dot16(q1[1], x.x[3], dot16(q1[0], x.x[2], 0));
     const float d0 = h2f(w[0] & 0xffffu) * __builtin_bit_cast(float, x.bs[0]);
     const float d1 = h2f(w[8] >> 16) * __builtin_bit_cast(float, x.bs[1]);
-    return (float)s0 * d0 + (float)s1 * d1;
+    return fmaf((float)s1, d1, (float)s0 * d0);
 }
 
 template <int WK>
@@ -893,16 +899,40 @@ __global__ void __launch_bounds__(256) k_rms_norm_rows(const float *__restrict__
     }
 }
 
-// y[r] = sum_k W[r][k] x[k] for a small f16 or f32 matrix (the ada MLP's
-// second layer, [dim][ada_dim] with ada_dim = 32): the CPU path's vec-dot type
-// for an f16 matrix is f16, so x is rounded to f16 and every product is exact
-// in f32; f32 matrices take x as it is.  One wave per row, lanes over k.
-__global__ void __launch_bounds__(256) k_rows_small(const void *__restrict__ w, int w_f16,
+// y[r] = sum_k W[r][k] x[k] for a small f16, f32 or Q8_0 matrix (the ada
+// MLP's second layer, [dim][ada_dim] with ada_dim = 32): the CPU path's
+// vec-dot type for an f16 matrix is f16, so x is rounded to f16 and every
+// product is exact in f32; f32 matrices take x as it is.  One wave per row,
+// lanes over k.  Q8_0 rows (a Q8_0 file): x quantized per 32-element block
+// as ggml's x86 quantize_row_q8_0 does, each block's integer dot times
+// fp16(d_w) * d_x, the row by one lane (n_in is a few blocks).
+__global__ void __launch_bounds__(256) k_rows_small(const void *__restrict__ w, int w_type,
                                                     const float *__restrict__ x, int n_in,
                                                     int n_rows, float *__restrict__ y) {
     const int lane = threadIdx.x & 63;
     const int row = (int)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= n_rows) return;
+    if (w_type == VKV_DTYPE_Q8_0) {
+#pragma clang fp contract(off)
+        if (lane != 0) return;
+        const uint8_t *wr = reinterpret_cast<const uint8_t *>(w) + (int64_t)row * (n_in / 32) * kQ8Bytes;
+        float acc = 0.0f;
+        for (int b = 0; b < n_in / 32; ++b) {
+            const float *xb = x + 32 * b;
+            const uint8_t *blk = wr + b * kQ8Bytes;
+            float am = 0.0f;
+            for (int k = 0; k < 32; ++k) am = fmaxf(am, fabsf(xb[k]));
+            const float dx = (float)(_Float16)(am / 127.0f);
+            const float id = am != 0.0f ? 127.0f / am : 0.0f;
+            int s = 0;
+            for (int k = 0; k < 32; ++k)
+                s += (int)(int8_t)blk[2 + k] * (int)__builtin_rintf(xb[k] * id);
+            acc = fmaf((float)s, h2f(blk[0] | blk[1] << 8) * dx, acc);
+        }
+        y[row] = acc;
+        return;
+    }
+    const bool w_f16 = w_type == VKV_DTYPE_F16;
     float acc = 0.0f;
     for (int k = lane; k < n_in; k += 64) {
         if (w_f16) {
@@ -1842,9 +1872,9 @@ hipError_t launch_rms_norm_rows(const float *x, int n_rows, int n, const float *
     return hipGetLastError();
 }
 
-hipError_t launch_rows_small(const void *w, bool w_f16, const float *x, int n_in, int n_rows,
+hipError_t launch_rows_small(const void *w, int w_type, const float *x, int n_in, int n_rows,
                              float *y, hipStream_t st) {
-    k_rows_small<<<(unsigned)((n_rows + 3) / 4), 256, 0, st>>>(w, w_f16 ? 1 : 0, x, n_in, n_rows, y);
+    k_rows_small<<<(unsigned)((n_rows + 3) / 4), 256, 0, st>>>(w, w_type, x, n_in, n_rows, y);
     return hipGetLastError();
 }
 
