@@ -71,6 +71,10 @@ Other workloads (--workload), reported on the same contract:
                (multi-row Q4_K_M products with RoPE in the epilogue, causal
                attention + K/V append, O, SwiGLU, W2), final norm, logits of
                the last token; prompt tokens/s.
+  decoder_token_q8_0 / decoder_weights_q8_0  decoder_token_q4km and
+               decoder_weights_q4km on a Q8_0 file's weights (every matrix
+               Q8_0, src/voxtral-quantize.cpp:95-96; products on q8_0 input
+               images).
 
 Prints one JSON line: throughput, the roofline of the step (algorithmic bytes /
 average step time from HIP events on the launch stream), the HBM traffic from
@@ -144,18 +148,38 @@ WORKLOADS = {
                                 streams=1, pmc="decoder_prompt_q4km_pmc.json", kern="",
                                 data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) audio rows, "
                                      "random prompt tokens, generated on device)"),
+    "decoder_token_q8_0": dict(dtype=8, dtype_name="q8_0 x q8_0 weights, f16 KV", streams=1,
+                               pmc="decoder_token_q8_0_pmc.json", kern="",
+                               data="synthetic (random valid Q8_0 blocks, N(0,1) inputs and KV "
+                                    "rows, generated on device)"),
+    "decoder_weights_q8_0": dict(dtype=8, dtype_name="q8_0 x q8_0 (int8 dot)", streams=1,
+                                 pmc="matvec_q8_0_26l_pmc.json", kern="",
+                                 data="synthetic (random valid Q8_0 blocks, N(0,1) inputs, "
+                                      "generated on device)"),
     "decoder_weights_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k (int8 dot)", streams=1,
                                  pmc="matvec_q4km_26l_pmc.json", kern="",
                                  data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) inputs, "
                                       "generated on device)"),
 }
 
-# decoder projections: (name, dtype, rows, n_in); ggml Q4_K = 12, Q6_K = 14
+# decoder projections: (name, dtype, rows, n_in); ggml Q8_0 = 8, Q4_K = 12, Q6_K = 14
 DIM, HIDDEN, VOCAB = 3072, 9216, 131072
 LAYER_MATS = [("attn_q", 12, Q_DIM, DIM), ("attn_k", 12, KV_DIM, DIM), ("attn_v", 14, KV_DIM, DIM),
               ("attn_o", 12, DIM, Q_DIM), ("ffn_w1", 12, HIDDEN, DIM), ("ffn_w3", 12, HIDDEN, DIM),
               ("ffn_w2", 14, DIM, HIDDEN)]
-KQ_BLOCK = {12: 144, 14: 210}
+KQ_BLOCK = {8: 272, 12: 144, 14: 210}   # bytes per 256 weights
+# the decoder's weight file kind: the Q4_K_M mix above (src/voxtral-quantize.cpp:
+# 148-159; output Q6_K) or a Q8_0 file (:95-96, every matrix Q8_0); set from
+# the workload's name
+MIX = "q4km"
+
+
+def layer_mats():
+    return LAYER_MATS if MIX == "q4km" else [(nm, 8, r, n) for nm, _, r, n in LAYER_MATS]
+
+
+def out_type():
+    return 14 if MIX == "q4km" else 8
 
 
 def mat_bytes(dtype, rows, n_in):
@@ -163,14 +187,39 @@ def mat_bytes(dtype, rows, n_in):
 
 
 def weights_bytes_per_token():
-    per_layer = sum(mat_bytes(dt, r, n) for _, dt, r, n in LAYER_MATS)
-    return LAYERS * per_layer + mat_bytes(14, VOCAB, DIM)
+    per_layer = sum(mat_bytes(dt, r, n) for _, dt, r, n in layer_mats())
+    return LAYERS * per_layer + mat_bytes(out_type(), VOCAB, DIM)
+
+
+def random_blocks_np(rng, dtype, rows, n_in):
+    """random_kq_device's blocks on the host (numpy), for the CPU legs"""
+    import numpy as np
+    if dtype == 8:
+        nb = rows * (n_in // 32)
+        w = np.empty((nb, 34), np.uint8)
+        w[:, 2:] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
+        w[:, 0:2] = rng.uniform(2e-4, 8e-3, nb).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        return w.reshape(-1)
+    w = rng.integers(0, 256, size=(rows * (n_in // 256), KQ_BLOCK[dtype]), dtype=np.uint8)
+    if dtype == 12:
+        w[:, 0:2] = rng.uniform(2e-4, 4e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+        w[:, 2:4] = rng.uniform(1e-4, 2e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    else:
+        w[:, 208:210] = rng.uniform(1e-5, 2e-4, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    return w.reshape(-1)
 
 
 def random_kq_device(dtype, rows, n_in, gen):
-    """Random valid k-quant blocks on the device: random bytes, fp16 scales set
-    to finite moderate values."""
+    """Random valid k-quant (or Q8_0) blocks on the device: random bytes, fp16
+    scales set to finite moderate values (Q8_0: codes in [-127, 127])."""
     import torch
+    if dtype == 8:
+        nb = rows * (n_in // 32)
+        w = torch.randint(-127, 128, (nb, 34), dtype=torch.int8, device="cuda",
+                          generator=gen).view(torch.uint8)
+        w[:, 0:2] = torch.empty(nb, dtype=torch.float16, device="cuda").uniform_(
+            2e-4, 8e-3, generator=gen).view(torch.uint8).view(nb, 2)
+        return w.reshape(-1)
     nb = rows * (n_in // 256)
     w = torch.randint(0, 256, (nb, KQ_BLOCK[dtype]), dtype=torch.uint8, device="cuda",
                       generator=gen)
@@ -193,9 +242,11 @@ def gpu_weights(steps, warmup):
     sp = st.cuda_stream
     gen = torch.Generator(device="cuda")
     gen.manual_seed(SEED)
-    layers = [{name: random_kq_device(dt, r, n, gen) for name, dt, r, n in LAYER_MATS}
+    mats = layer_mats()
+    T = {name: dt for name, dt, _, _ in mats}
+    layers = [{name: random_kq_device(dt, r, n, gen) for name, dt, r, n in mats}
               for _ in range(LAYERS)]
-    logits_w = random_kq_device(14, VOCAB, DIM, gen)
+    logits_w = random_kq_device(out_type(), VOCAB, DIM, gen)
     norms = torch.empty(LAYERS * 2 + 1, DIM, device="cuda").uniform_(0.5, 1.5, generator=gen)
     ada = torch.empty(LAYERS, DIM, device="cuda").uniform_(-0.3, 0.3, generator=gen)
     x0 = torch.randn(DIM, device="cuda", generator=gen)
@@ -210,19 +261,19 @@ def gpu_weights(steps, warmup):
         x.copy_(x0)
         xp = x.data_ptr()
         for l, L in enumerate(layers):
-            vkv.matvec(xp, DIM, [(L["attn_q"].data_ptr(), 12, Q_DIM, q.data_ptr()),
-                                 (L["attn_k"].data_ptr(), 12, KV_DIM, k.data_ptr()),
-                                 (L["attn_v"].data_ptr(), 14, KV_DIM, v.data_ptr())],
+            vkv.matvec(xp, DIM, [(L["attn_q"].data_ptr(), T["attn_q"], Q_DIM, q.data_ptr()),
+                                 (L["attn_k"].data_ptr(), T["attn_k"], KV_DIM, k.data_ptr()),
+                                 (L["attn_v"].data_ptr(), T["attn_v"], KV_DIM, v.data_ptr())],
                        norm_w_ptr=norms[2 * l].data_ptr(), eps=eps, hip_stream=sp)
             vkv.matvec(attn.data_ptr(), Q_DIM,
-                       [(L["attn_o"].data_ptr(), 12, DIM, xp, xp)], hip_stream=sp)
-            vkv.matvec(xp, DIM, [(L["ffn_w1"].data_ptr(), 12, HIDDEN, h.data_ptr()),
-                                 (L["ffn_w3"].data_ptr(), 12, HIDDEN, None)],
+                       [(L["attn_o"].data_ptr(), T["attn_o"], DIM, xp, xp)], hip_stream=sp)
+            vkv.matvec(xp, DIM, [(L["ffn_w1"].data_ptr(), T["ffn_w1"], HIDDEN, h.data_ptr()),
+                                 (L["ffn_w3"].data_ptr(), T["ffn_w3"], HIDDEN, None)],
                        norm_w_ptr=norms[2 * l + 1].data_ptr(), ada_ptr=ada[l].data_ptr(),
                        eps=eps, epilogue=vkv.MV_SWIGLU, hip_stream=sp)
-            vkv.matvec(h.data_ptr(), HIDDEN, [(L["ffn_w2"].data_ptr(), 14, DIM, xp, xp)],
+            vkv.matvec(h.data_ptr(), HIDDEN, [(L["ffn_w2"].data_ptr(), T["ffn_w2"], DIM, xp, xp)],
                        hip_stream=sp)
-        vkv.matvec(xp, DIM, [(logits_w.data_ptr(), 14, VOCAB, logits.data_ptr())],
+        vkv.matvec(xp, DIM, [(logits_w.data_ptr(), out_type(), VOCAB, logits.data_ptr())],
                    norm_w_ptr=norms[2 * LAYERS].data_ptr(), eps=eps, hip_stream=sp)
 
     total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
@@ -713,26 +764,29 @@ def gpu_realtime_step(steps, warmup):
 
 
 def device_model(gen):
-    """Random Q4_K_M decoder weights on the device and the vkv_dec_model
-    describing them (tied output = tok_embeddings)."""
+    """Random decoder weights of the MIX file kind on the device and the
+    vkv_dec_model describing them (tied output = tok_embeddings)."""
     import torch
     import vkv
     keep = []
     layers = (vkv.DecLayer * LAYERS)()
+    mats = layer_mats()
+    T = {name: dt for name, dt, _, _ in mats}
     for l in range(LAYERS):
-        w = {name: random_kq_device(dt, r, n, gen) for name, dt, r, n in LAYER_MATS}
+        w = {name: random_kq_device(dt, r, n, gen) for name, dt, r, n in mats}
         norms = torch.empty(2, DIM, device="cuda").uniform_(0.5, 1.5, generator=gen)
         ada = torch.empty(DIM, device="cuda").uniform_(-0.3, 0.3, generator=gen)
         keep += list(w.values()) + [norms, ada]
         layers[l] = vkv.DecLayer(norms[0].data_ptr(), w["attn_q"].data_ptr(), w["attn_k"].data_ptr(),
-                                 w["attn_v"].data_ptr(), w["attn_o"].data_ptr(), 12, 12, 14, 12,
-                                 norms[1].data_ptr(), ada.data_ptr(), w["ffn_w1"].data_ptr(),
-                                 w["ffn_w2"].data_ptr(), w["ffn_w3"].data_ptr(), 12, 14, 12)
-    table = random_kq_device(14, VOCAB, DIM, gen)
+                                 w["attn_v"].data_ptr(), w["attn_o"].data_ptr(), T["attn_q"],
+                                 T["attn_k"], T["attn_v"], T["attn_o"], norms[1].data_ptr(),
+                                 ada.data_ptr(), w["ffn_w1"].data_ptr(), w["ffn_w2"].data_ptr(),
+                                 w["ffn_w3"].data_ptr(), T["ffn_w1"], T["ffn_w2"], T["ffn_w3"])
+    table = random_kq_device(out_type(), VOCAB, DIM, gen)
     out_norm = torch.empty(DIM, device="cuda").uniform_(0.5, 1.5, generator=gen)
     keep += [table, out_norm]
-    model = vkv.DecModel(LAYERS, DIM, HIDDEN, QH, KVH, HD, VOCAB, 1e-5, 1.0e6, table.data_ptr(), 14,
-                         out_norm.data_ptr(), table.data_ptr(), 14, layers)
+    model = vkv.DecModel(LAYERS, DIM, HIDDEN, QH, KVH, HD, VOCAB, 1e-5, 1.0e6, table.data_ptr(),
+                         out_type(), out_norm.data_ptr(), table.data_ptr(), out_type(), layers)
     return model, (keep, layers)
 
 
@@ -983,18 +1037,8 @@ def cpu_weights_leg(target_seconds):
 
     threads = min(os.cpu_count() or 1, 16)
     rng = np.random.default_rng(SEED)
-
-    def mat(dt, r, n):
-        w = rng.integers(0, 256, size=(r * (n // 256), KQ_BLOCK[dt]), dtype=np.uint8)
-        if dt == 12:
-            w[:, 0:2] = rng.uniform(2e-4, 4e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
-            w[:, 2:4] = rng.uniform(1e-4, 2e-3, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
-        else:
-            w[:, 208:210] = rng.uniform(1e-5, 2e-4, len(w)).astype(np.float16).view(np.uint8).reshape(-1, 2)
-        return w.reshape(-1)
-
-    mats = [(dt, r, n, mat(dt, r, n)) for _, dt, r, n in LAYER_MATS]
-    lw = mat(14, VOCAB, DIM)
+    mats = [(dt, r, n, random_blocks_np(rng, dt, r, n)) for _, dt, r, n in layer_mats()]
+    lw = random_blocks_np(rng, out_type(), VOCAB, DIM)
     xs = {n: rng.standard_normal(n).astype(np.float32) for n in (DIM, Q_DIM, HIDDEN)}
     t_layer = t_logits = 0.0
     reps = 0
@@ -1012,7 +1056,8 @@ def cpu_weights_leg(target_seconds):
     token_s = (LAYERS * t_layer + t_logits) / reps
     return {"value": 1.0 / token_s, "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{reps} x (one layer's 7 projections + the 131072-row logits) of the "
-                      f"oracle's restatement of ggml's generic CPU q4_K/q6_K x q8_K matvec, "
+                      f"oracle's restatement of ggml's CPU "
+                      f"{'q4_K/q6_K x q8_K' if MIX == 'q4km' else 'q8_0 x q8_0'} matvec, "
                       f"{threads} threads; token = 26 x layer + logits"}
 
 
@@ -1624,6 +1669,8 @@ def main():
         sys.exit(2)
 
     wl = WORKLOADS[args.workload]
+    global MIX
+    MIX = "q8_0" if args.workload.endswith("_q8_0") else "q4km"
     traffic, traffic_fetch = load_traffic(wl["pmc"]) if wl["pmc"] else (None, None)
     if args.workload in ("stream4096_f16", "layer1_f16"):
         layers, prefill = (LAYERS, 0) if args.workload == "stream4096_f16" else (1, 1024)
@@ -1716,11 +1763,12 @@ def main():
                   "layers": LAYERS, "dim": DIM, "hidden": HIDDEN, "vocab": VOCAB,
                   "prompt_tokens": P_TOKENS, "bytes_per_prompt": bytes_step}
         kernel = "whole prompt (k_gemm_kq, k_q8k_rows, k_window_mfma, k_matvec launches)"
-    elif args.workload == "decoder_token_q4km":
+    elif args.workload in ("decoder_token_q4km", "decoder_token_q8_0"):
         total_ms, step_ms, wall = gpu_token(args.steps, args.warmup)
         bytes_step = token_bytes()
         units_per_step = 1
-        res = {"metric": "decoder tokens/s (whole step: Q4_K_M projections + f16 KV attention at "
+        kind = "Q4_K_M" if MIX == "q4km" else "Q8_0"
+        res = {"metric": f"decoder tokens/s (whole step: {kind} projections + f16 KV attention at "
                          "the 8192 window, 26 layers, logits, argmax) and HBM GB/s",
                "unit": "tokens/s"}
         config = {"workload": "one decoder token through vkv_decoder_token: embedding + audio, "
@@ -1752,16 +1800,17 @@ def main():
         res["latency_ms"] = {"p50": round(pick(0.50), 4), "p90": round(pick(0.90), 4),
                              "p99": round(pick(0.99), 4), "max": round(lat[-1], 4),
                              "mean": round(sum(lat) / len(lat), 4), "tokens": len(lat)}
-    elif args.workload == "decoder_weights_q4km":
+    elif args.workload in ("decoder_weights_q4km", "decoder_weights_q8_0"):
         total_ms, step_ms, wall = gpu_weights(args.steps, args.warmup)
         bytes_step = weights_bytes_per_token()
         units_per_step = 1
-        res = {"metric": "decoder projection tokens/s and HBM GB/s on Q4_K_M weights "
+        kind = ("Q4_K_M mix (attn_v, ffn_w2, output Q6_K; others Q4_K)" if MIX == "q4km" else
+                "Q8_0 file (every matrix Q8_0, q8_0 input images)")
+        res = {"metric": f"decoder projection tokens/s and HBM GB/s on {kind.split(' ')[0]} weights "
                          "(26 layers + logits)", "unit": "tokens/s"}
         config = {"workload": "decoder step projections, one token: 26 x (RMSNorm + Q/K/V, "
                               "O + residual, RMSNorm*(1+ada) + SwiGLU W1/W3, W2 + residual) + "
-                              "final norm + 131072-row logits; Q4_K_M mix (attn_v, ffn_w2, "
-                              "output Q6_K; others Q4_K)",
+                              f"final norm + 131072-row logits; {kind}",
                   "layers": LAYERS, "dim": DIM, "hidden": HIDDEN, "vocab": VOCAB,
                   "weight_bytes_per_token": bytes_step, "calls_per_token": 4 * LAYERS + 1}
         kernel = "k_matvec (105 launches per token)"
@@ -1836,7 +1885,7 @@ def main():
                      "avg_launch_ms": round(step_avg, 5)},
         "wall_s": round(wall, 3),
     })
-    if not args.no_cpu and args.workload == "decoder_weights_q4km":
+    if not args.no_cpu and args.workload in ("decoder_weights_q4km", "decoder_weights_q8_0"):
         res["cpu_baseline"] = cpu_weights_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload == "encoder_chunk_q4km":
         res["cpu_baseline"] = cpu_encoder_leg(E_CHUNK, args.cpu_seconds)
@@ -1844,7 +1893,8 @@ def main():
         res["cpu_baseline"] = cpu_realtime_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload == "decoder_prompt_q4km":
         res["cpu_baseline"] = cpu_prompt_leg(args.cpu_seconds)
-    elif not args.no_cpu and args.workload in ("decoder_token_q4km", "decoder_loop_q4km"):
+    elif not args.no_cpu and args.workload in ("decoder_token_q4km", "decoder_loop_q4km",
+                                               "decoder_token_q8_0"):
         res["cpu_baseline"] = cpu_token_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload in ("adapter_q4km", "adapter_group_q4km"):
         res["cpu_baseline"] = cpu_adapter_leg(wl["groups"], args.cpu_seconds)

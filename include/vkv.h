@@ -527,7 +527,7 @@ vkv_status vkv_encoder_chunk_ring(vkv_cache *cache, int32_t stream, const vkv_en
  * contiguous row of enc_dim * downsample floats: the ring capacity must be a
  * multiple of downsample), h = gelu_erf(W0 x), audio-embedding logical row
  * g = W2 h.  Both products as vkv_matmul computes them (Q8_K input,
- * integer block sums); Q4_K or Q6_K weights. */
+ * integer block sums); Q4_K, Q6_K or Q8_0 weights (q8_0 input for Q8_0). */
 typedef struct vkv_adapter {
     const void *w0;       /* adapter.0.weight [dec_dim][enc_dim * downsample] */
     const void *w2;       /* adapter.2.weight [dec_dim][dec_dim] */
@@ -551,11 +551,13 @@ vkv_status vkv_embed(int32_t dtype, const void *table, int32_t n_rows, int64_t n
  * compute_time_embedding :729-740, evaluated at t = VOXTRAL_N_DELAY_TOKENS,
  * :1535): scale = W2 gelu_erf(W0 e(t)) with e(t)[i] = cos(t f_i),
  * e(t)[i + dim/2] = sin(t f_i), f_i = expf(-logf(10000) i / (dim/2)), as the
- * reference computes it on the host.  W0: Q4_K/Q6_K [ada_dim][dim] (the
+ * reference computes it on the host.  W0: Q4_K/Q6_K/Q8_0 [ada_dim][dim] (the
  * product as vkv_matvec computes it); W2: F16 or F32 (dtype 1 / 0)
  * [dim][ada_dim], its input rounded to f16 for F16 as ggml's vec-dot type
- * does.  out: [dim] f32 device memory, the vkv_dec_layer.ada_scale of the
- * layer.  workspace: vkv_ada_scale_workspace bytes of device memory. */
+ * does, or Q8_0 (dtype 8, a Q8_0 file: ada_dim % 32 == 0, the input
+ * quantized to q8_0 as for any Q8_0 product).  out: [dim] f32 device memory,
+ * the vkv_dec_layer.ada_scale of the layer.  workspace:
+ * vkv_ada_scale_workspace bytes of device memory. */
 size_t vkv_ada_scale_workspace(int32_t dim, int32_t ada_dim);
 vkv_status vkv_ada_scale(const void *w0, int32_t w0_type, const void *w2, int32_t w2_type,
                          int32_t dim, int32_t ada_dim, float t, float *out, void *workspace,
@@ -574,7 +576,8 @@ vkv_status vkv_argmax(const float *x, int64_t n, int32_t *out, void *hip_stream)
  * and k at the token's position, K/V append at the ring slot, attention over
  * the window, x += W_o attn, h = rms_norm(x) * ffn_norm (* (1 + ada)),
  * x += W2 (silu(W1 h) * (W3 h)); logits = output (rms_norm(x) * out_norm);
- * argmax.  Weights are GGUF tensors' bytes in device memory (Q4_K / Q6_K);
+ * argmax.  Weights are GGUF tensors' bytes in device memory (Q4_K / Q6_K /
+ * Q8_0);
  * norms and ada scales f32.  The ring is planned once and committed after
  * the last layer.
  * ------------------------------------------------------------------------- */
@@ -741,12 +744,13 @@ vkv_status vkv_gguf_hparams(const vkv_gguf *gguf, vkv_hparams *out);
 /* ---------------------------------------------------------------------------
  * A model in device memory: every tensor of the file at its data-section
  * offset in one device allocation (the file's bytes unchanged, so Q4_K/Q6_K
- * rows are what the kernels read), and the description the entry points take,
+ * or Q8_0 rows are what the kernels read), and the description the entry points take,
  * by the reference's tensor names (src/voxtral.cpp:1193-1265).  Streamed from
  * the file through pinned staging buffers on the given HIP stream (host
  * copies on up to 8 threads); the call
  * returns when the upload is complete.  MODEL_ERROR when a tensor the
- * realtime model requires is missing or has an unsupported type.
+ * realtime model requires is missing or has an unsupported type (matrices:
+ * Q4_K, Q6_K or Q8_0, a layer's Q/K/V all Q8_0 or none, W1 and W3 alike).
  * ------------------------------------------------------------------------- */
 typedef struct vkv_model vkv_model;
 
