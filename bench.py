@@ -56,6 +56,9 @@ Other workloads (--workload), reported on the same contract:
                adapter over the completed group, one decoder token reading its
                audio row (full 8192-slot ring); steps/s (x 0.08 = the
                realtime factor).
+  realtime_pipelined_q4km  the same steps on two HIP streams, the decoder
+               one group behind the encoder (token i reads step i-1's audio
+               row while step i's encoder and adapter run); steps/s.
   decoder_token_q4km  one whole decoder token through vkv_decoder_token:
                embedding + audio row, 26 x (RMSNorm+QKV, RoPE + K/V append +
                attention over the full 8192-slot F16 ring, O + residual,
@@ -144,6 +147,10 @@ WORKLOADS = {
                                streams=1, pmc="realtime_step_q4km_pmc.json", kern="",
                                data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) Mel windows "
                                     "and KV rows, generated on device)"),
+    "realtime_pipelined_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights, f16 KV, f32 rings",
+                                    streams=1, pmc="realtime_pipelined_q4km_pmc.json", kern="",
+                                    data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) Mel "
+                                         "windows and KV rows, generated on device)"),
     "decoder_prompt_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights (MFMA int8), f16 KV",
                                 streams=1, pmc="decoder_prompt_q4km_pmc.json", kern="",
                                 data="synthetic (random valid Q4_K/Q6_K blocks, N(0,1) audio rows, "
@@ -687,16 +694,26 @@ def gpu_encoder_chunk(steps, warmup):
 R_FRAMES = 4   # encoder frames per realtime step (the steady physical 4-row launch)
 
 
-def gpu_realtime_step(steps, warmup):
+def gpu_realtime_step(steps, warmup, pipelined=False):
     """One 80 ms realtime step: the conv stem and the encoder over 4 new frames
     into the encoder-output ring, the adapter over the completed group into
     the audio-embedding ring, and one decoder token reading that row
-    (26 layers, the full 8192-slot ring)."""
+    (26 layers, the full 8192-slot ring).
+
+    pipelined: the same work on two HIP streams, the decoder one group
+    behind: step i's encoder + adapter (group g_i) run on the timing stream
+    while step i's decoder token, on a second stream, reads group g_{i-1}
+    (it waits for step i-1's adapter through an event); the timing stream
+    waits for token i-1 before step i+1's encoder, so at most one step of
+    each chain is in flight beside the other, and the last step joins the
+    decoder stream before the end event."""
     import torch
     import vkv
 
     st = torch.cuda.current_stream()
     sp = st.cuda_stream
+    dst = torch.cuda.Stream() if pipelined else st   # default priority
+    dsp = dst.cuda_stream
     gen = torch.Generator(device="cuda")
     gen.manual_seed(SEED)
     emodel, ecache, ekeep = encoder_setup(gen, sp)
@@ -742,17 +759,32 @@ def gpu_realtime_step(steps, warmup):
     logits = torch.empty(VOCAB, device="cuda")
     tok = torch.zeros(1, dtype=torch.int32, device="cuda")
     al = lambda t: (t.data_ptr() + 255) & ~255
+    ev_a = [torch.cuda.Event() for _ in range(T)]   # step i's adapter row is written
+    ev_d = [torch.cuda.Event() for _ in range(T)]   # step i's token is done
 
     def step(i):
         p = plans[i]
+        if pipelined and i > 0:
+            st.wait_event(ev_d[i - 1])
         vkv.enc_conv_stem(mel[i].data_ptr(), 128, p, w0.data_ptr(), b0.data_ptr(), w1.data_ptr(),
                           b1.data_ptr(), 1280, x.data_ptr(), al(cws), cb, hip_stream=sp)
         vkv.encoder_chunk_ring(ecache, 0, p, E_WIN, emodel, x.data_ptr(), er, al(ews), ewb,
                                hip_stream=sp)
         g = (p.q_start + R_FRAMES) // A_DOWN - 1          # the group these frames complete
         vkv.adapter_commit(ad, er, ar, g, 1, al(aws), awb, hip_stream=sp)
-        vkv.decoder_token(dcache, 0, ring, dmodel, 32, aemb[g % A_RING].data_ptr(),
-                          logits.data_ptr(), tok.data_ptr(), al(tws), twb, hip_stream=sp)
+        if not pipelined:
+            vkv.decoder_token(dcache, 0, ring, dmodel, 32, aemb[g % A_RING].data_ptr(),
+                              logits.data_ptr(), tok.data_ptr(), al(tws), twb, hip_stream=sp)
+            return
+        ev_a[i].record(st)
+        if i > 0:
+            dst.wait_event(ev_a[i - 1])
+        gd = g - 1                                         # the previous step's group
+        vkv.decoder_token(dcache, 0, ring, dmodel, 32, aemb[gd % A_RING].data_ptr(),
+                          logits.data_ptr(), tok.data_ptr(), al(tws), twb, hip_stream=dsp)
+        ev_d[i].record(dst)
+        if i == T - 1:
+            st.wait_event(ev_d[i])                         # join before the end event
 
     total_ms, step_ms, wall = timed_loop(step, steps, warmup, st)
     assert bool(torch.isfinite(logits).all()) and bool(torch.isfinite(aemb).all())
@@ -1736,8 +1768,9 @@ def main():
                               f"{len(realtime_tensor_list())} tensors)",
                   "bytes_per_load": data_bytes, "staging": "3 x 64 MiB pinned buffers"}
         kernel = "hipMemcpyAsync host-to-device copies (no kernels)"
-    elif args.workload == "realtime_step_q4km":
-        total_ms, step_ms, wall, n_keys = gpu_realtime_step(args.steps, args.warmup)
+    elif args.workload in ("realtime_step_q4km", "realtime_pipelined_q4km"):
+        piped = args.workload == "realtime_pipelined_q4km"
+        total_ms, step_ms, wall, n_keys = gpu_realtime_step(args.steps, args.warmup, piped)
         bytes_step = (encoder_chunk_bytes(n_keys, R_FRAMES) + adapter_bytes(1) + token_bytes())
         units_per_step = 1
         res = {"metric": "realtime steps/s (one 80 ms audio step: 4 encoder frames, 1 adapter "
@@ -1748,6 +1781,11 @@ def main():
                               "reading its audio row (26 layers, full 8192-slot f16 ring, logits, "
                               "argmax); Q4_K_M weights",
                   "audio_ms_per_step": 80, "bytes_per_step": bytes_step}
+        if piped:
+            config["workload"] += ("; pipelined on two HIP streams: the decoder token of step i "
+                                   "reads the previous step's audio row while step i's encoder "
+                                   "and adapter run (events order the two chains)")
+            config["streams"] = 2
         kernel = "whole step (encoder, adapter and decoder launches)"
     elif args.workload == "decoder_prompt_q4km":
         total_ms, step_ms, wall = gpu_prompt(args.steps, args.warmup)
@@ -1889,7 +1927,7 @@ def main():
         res["cpu_baseline"] = cpu_weights_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload == "encoder_chunk_q4km":
         res["cpu_baseline"] = cpu_encoder_leg(E_CHUNK, args.cpu_seconds)
-    elif not args.no_cpu and args.workload == "realtime_step_q4km":
+    elif not args.no_cpu and args.workload in ("realtime_step_q4km", "realtime_pipelined_q4km"):
         res["cpu_baseline"] = cpu_realtime_leg(args.cpu_seconds)
     elif not args.no_cpu and args.workload == "decoder_prompt_q4km":
         res["cpu_baseline"] = cpu_prompt_leg(args.cpu_seconds)

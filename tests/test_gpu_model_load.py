@@ -355,3 +355,86 @@ def test_a_q8_0_file_maps_and_conditions(q8_0_file):
         assert np.abs(want).max() > 1e-3
         assert np.abs(got[l] - want).max() <= 1e-3 * np.abs(want).max()
     m.close()
+
+
+def test_two_stream_pipelined_steps_equal_the_single_stream_order(model_file):
+    """The realtime steps scheduled on two HIP streams, the decoder one group
+    behind the encoder (step i's encoder + adapter on one stream while token
+    i, on the other, reads step i-1's audio row; events order the chains):
+    every token's logits, the tokens, the decoder cache and the rings equal
+    the same steps issued in that order on one stream, bit for bit.  No host
+    synchronization inside the loop, so a missing wait would show as a race."""
+    path, g = model_file
+    rng = np.random.default_rng(80)
+    S = 12
+    plans = [vkv.enc_plan(4 * i, 4, 878, 750) for i in range(S)]
+    mel_all = rng.uniform(-1.5, 1.5, (128, plans[-1].conv_mel_end)).astype(np.float32)
+    mels = [torch.from_numpy(np.ascontiguousarray(mel_all[:, p.conv_mel_start:p.conv_mel_end]))
+            .to(dev()) for p in plans]
+    m = vkv.Model(path, hip_stream=stream_ptr())
+    scales = torch.empty(DEC_L, 3072, device=dev())
+    m.set_ada(6.0, scales.data_ptr(), hip_stream=stream_ptr())
+    v = m.view
+    al = lambda t: (t.data_ptr() + 255) & ~255   # noqa: E731
+
+    def run(two):
+        s0 = torch.cuda.current_stream()
+        s1 = torch.cuda.Stream() if two else s0
+        ecache = vkv.Cache(n_streams=1, n_layers=ENC_L, capacity=878, n_kv_heads=32, head_dim=64,
+                           n_q_heads=32, dtype=vkv.F16)
+        dcache = vkv.Cache(n_streams=1, n_layers=DEC_L, capacity=512, n_kv_heads=8, head_dim=128,
+                           n_q_heads=32, dtype=vkv.F16)
+        ring = vkv.new_ring(512)
+        x = torch.empty(4, 1280, device=dev())
+        cb = max(vkv.enc_conv_stem_workspace(p.conv_mel_end - p.conv_mel_start, 128, 1280, 4)
+                 for p in plans)
+        cws = torch.empty(cb // 4 + 64, device=dev())
+        enc_out = torch.full((256, 1280), np.nan, device=dev())
+        aemb = torch.full((256, 3072), np.nan, device=dev())
+        er, ar = vkv.RowRing(enc_out.data_ptr(), 256, 1280), vkv.RowRing(aemb.data_ptr(), 256, 3072)
+        ewb = vkv.encoder_chunk_workspace(v.enc, 4)
+        ews = torch.empty(ewb // 4 + 64, device=dev())
+        awb = vkv.adapter_workspace(v.adapter, 1)
+        aws = torch.empty(awb // 4 + 64, device=dev())
+        twb = vkv.decoder_token_workspace(v.dec)
+        tws = torch.empty(twb // 4 + 64, device=dev())
+        logits = torch.zeros(S, VOCAB, device=dev())
+        toks = torch.zeros(S, dtype=torch.int32, device=dev())
+        ev_a = [torch.cuda.Event() for _ in range(S)]
+        ev_d = [torch.cuda.Event() for _ in range(S)]
+        torch.cuda.synchronize()
+        for i, p in enumerate(plans):
+            if two and i > 1:
+                s0.wait_event(ev_d[i - 1])
+            vkv.enc_conv_stem(mels[i].data_ptr(), 128, p, v.conv0_w, v.conv0_b, v.conv1_w, v.conv1_b,
+                              1280, x.data_ptr(), al(cws), cb, hip_stream=s0.cuda_stream)
+            vkv.encoder_chunk_ring(ecache, 0, p, 750, v.enc, x.data_ptr(), er, al(ews), ewb,
+                                   hip_stream=s0.cuda_stream)
+            vkv.adapter_commit(v.adapter, er, ar, i, 1, al(aws), awb, hip_stream=s0.cuda_stream)
+            ev_a[i].record(s0)
+            if i == 0:
+                continue
+            s1.wait_event(ev_a[i - 1])
+            vkv.decoder_token(dcache, 0, ring, v.dec, 7 + i, aemb[i - 1].data_ptr(),
+                              logits[i].data_ptr(), toks[i].data_ptr(), al(tws), twb,
+                              hip_stream=s1.cuda_stream)
+            ev_d[i].record(s1)
+        torch.cuda.synchronize()
+        out = (logits.cpu().numpy(), toks.cpu().numpy(), enc_out.cpu().numpy(), aemb.cpu().numpy(),
+               [layer_bytes(dcache, w, l) for w in (0, 1) for l in range(DEC_L)])
+        ecache.close()
+        dcache.close()
+        return out
+
+    one, two = run(False), run(True)
+    for a, b in zip(one[:4], two[:4]):
+        assert np.array_equal(a, b, equal_nan=True)
+    for a, b in zip(one[4], two[4]):
+        assert np.array_equal(a, b)
+    assert np.isfinite(one[0][1:]).all() and np.abs(one[0][1:]).max() > 0
+    m.close()
+
+
+def layer_bytes(cache, which, layer):
+    from gpu_util import layer_image
+    return layer_image(cache, which, 0, layer).copy()
