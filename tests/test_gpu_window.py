@@ -195,12 +195,14 @@ def test_encoder_stream_driven_by_the_schedule(sched, batch_terminal):
         print(f"encoder stream: {runs_done} runs, {emitted} frames", flush=True)
 
 
-@pytest.mark.parametrize("head_dim,n_kv_heads,n_q_heads", [(64, 32, 32), (128, 8, 32)])
-def test_f32_matrix_core_tile_against_scalar_kernel(head_dim, n_kv_heads, n_q_heads):
+@pytest.mark.parametrize("head_dim,n_kv_heads,n_q_heads,per_layer",
+                         [(64, 32, 32, False), (64, 32, 32, True), (128, 8, 32, False)])
+def test_f32_matrix_core_tile_against_scalar_kernel(head_dim, n_kv_heads, n_q_heads, per_layer):
     """The F32 window tile on v_mfma_f32_16x16x4_f32 against the scalar-ALU
     kernel (VKV_KERNEL_WINDOW_VALU) over the same wrapped ring and queries:
     both f32 throughout, within 2e-6; ring bytes identical (the fused copy
-    and the separate append store the same f32 rows)."""
+    and the separate append store the same f32 rows).  per_layer: one call
+    per layer (the encoder chunk's shape)."""
     cap, layers, n_q = 878, 2, 16
     kv_dim = n_kv_heads * head_dim
     outs, imgs = [], []
@@ -214,8 +216,14 @@ def test_f32_matrix_core_tile_against_scalar_kernel(head_dim, n_kv_heads, n_q_he
                 k = synth(None, kv_dim, vkv.TAG_EK, nl=layers, p0=q_start, np_=n_q)
                 v = synth(None, kv_dim, vkv.TAG_EV, nl=layers, p0=q_start, np_=n_q)
                 out = empty_f32(layers, n_q, n_q_heads * head_dim)
-                c.enc_step(0, plan, EWIN, 0, layers, q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                           out.data_ptr(), 1 / np.sqrt(head_dim), hip_stream=stream_ptr())
+                if per_layer:
+                    for l in range(layers):
+                        c.enc_step(0, plan, EWIN, l, 1, q[0, l].data_ptr(), k[0, l].data_ptr(),
+                                   v[0, l].data_ptr(), out[l].data_ptr(), 1 / np.sqrt(head_dim),
+                                   hip_stream=stream_ptr())
+                else:
+                    c.enc_step(0, plan, EWIN, 0, layers, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                               out.data_ptr(), 1 / np.sqrt(head_dim), hip_stream=stream_ptr())
             torch.cuda.synchronize()
             outs.append(out.cpu().numpy())
             imgs.append([layer_image(c, w, 0, l).copy() for l in range(layers) for w in (0, 1)])

@@ -2153,7 +2153,7 @@ __global__ void __launch_bounds__(64 * W) k_window_mfma(WindowArgs a) {
 //                   written transposed, stride 17 floats).
 // The fused ring write copies the new rows (F32 cache: no conversion).
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, int W>
 __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
     constexpr int DL = D / 4;           // contiguous head dims per lane
     constexpr int NT = D / 16;          // 16-dim tiles of P.V
@@ -2171,9 +2171,9 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
     const uint8_t *kl = a.k + (int64_t)layer * a.layer_bytes;
     const uint8_t *vl = a.v + (int64_t)layer * a.layer_bytes;
 
-    __shared__ float sm_vt[4][D * VS];   // per wave: V^T[d][key]
-    __shared__ float sm_o[4][16][D + 1];
-    __shared__ float sm_m[4][16], sm_l[4][16];
+    __shared__ float sm_vt[W][D * VS];   // per wave: V^T[d][key]
+    __shared__ float sm_o[W][16][D + 1];
+    __shared__ float sm_m[W][16], sm_l[W][16];
 
     // ---- Q^T operand: lane holds row lr, dims [DL lg, DL lg + DL) ----
     const int row = tile * 16 + lr;
@@ -2285,10 +2285,10 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
     };
     float4 ka_[DL / 4], va_[DL / 4], kb_[DL / 4], vb_[DL / 4];
     // The block grid is absolute: wave w takes the 16-key blocks starting at
-    // key positions = 16 w (mod 64), whatever the run's first query, so a
+    // key positions = 16 w (mod 16 W), whatever the run's first query, so a
     // row meets its keys in the same blocks, waves and order under every
     // chunking of the stream (schedule-invariant results, bit for bit).
-    int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & 63) + wave * 16;
+    int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & (16 * W - 1)) + wave * 16;
     load_kv(jb0, ka_, va_);
     // Fused ring write of kv head g's part of the n_new new rows.  A wave
     // whose first block holds a new row (the newest n_new keys; its largest
@@ -2298,7 +2298,7 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
         const int64_t src0 = (int64_t)layer * a.n_new * kv_dim;
         uint8_t *kw = a.k_w + (int64_t)layer * a.layer_bytes;
         uint8_t *vw = a.v_w + (int64_t)layer * a.layer_bytes;
-        for (int t = threadIdx.x; t < a.n_new * (D / 4); t += 256) {
+        for (int t = threadIdx.x; t < a.n_new * (D / 4); t += 64 * W) {
             const int row = t / (D / 4);
             const int col = g * D + (t % (D / 4)) * 4;
             const int64_t so = src0 + (int64_t)row * kv_dim + col;
@@ -2315,12 +2315,12 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
         const float4 v4 = row_ok ? qraw[t] : make_float4(0, 0, 0, 0);
         qf[4 * t] = v4.x; qf[4 * t + 1] = v4.y; qf[4 * t + 2] = v4.z; qf[4 * t + 3] = v4.w;
     }
-    for (; jb0 < j_hi; jb0 += 128) {
-        load_kv(jb0 + 64, kb_, vb_);
+    for (; jb0 < j_hi; jb0 += 32 * W) {
+        load_kv(jb0 + 16 * W, kb_, vb_);
         process(ka_, va_, jb0);
-        if (jb0 + 64 >= j_hi) break;
-        load_kv(jb0 + 128, ka_, va_);
-        process(kb_, vb_, jb0 + 64);
+        if (jb0 + 16 * W >= j_hi) break;
+        load_kv(jb0 + 32 * W, ka_, va_);
+        process(kb_, vb_, jb0 + 16 * W);
     }
 
     // row sums over the 4 lane groups (they share m)
@@ -2336,16 +2336,18 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
         sm_l[wave][lr] = l;
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < 16 * D; t += 256) {
+    for (int t = threadIdx.x; t < 16 * D; t += 64 * W) {
         const int r = t / D;
         const int d = t % D;
         const int rr = tile * 16 + r;
         if (rr >= n_rows) continue;
-        const float M = fmaxf(fmaxf(sm_m[0][r], sm_m[1][r]), fmaxf(sm_m[2][r], sm_m[3][r]));
+        float M = fmaxf(fmaxf(sm_m[0][r], sm_m[1][r]), fmaxf(sm_m[2][r], sm_m[3][r]));
+#pragma unroll
+        for (int w = 4; w < W; ++w) M = fmaxf(M, sm_m[w][r]);
         float O = 0.0f, L = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
+            for (int w = 0; w < W; ++w) {
                 const float f = fast_exp2(sm_m[w][r] - M);
                 O = fmaf(sm_o[w][r][d], f, O);
                 L = fmaf(sm_l[w][r], f, L);
@@ -2363,10 +2365,10 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
 // 256 CUs (at 139 VGPRs, three per CU, a third of them ran in a second round)
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
 k_window_mfma_f32_64(WindowArgs a) {
-    window_mfma_f32<64>(a);
+    window_mfma_f32<64, 4>(a);
 }
 __global__ void __launch_bounds__(256) k_window_mfma_f32_128(WindowArgs a) {
-    window_mfma_f32<128>(a);
+    window_mfma_f32<128, 4>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -2595,6 +2597,8 @@ hipError_t launch_window(int dtype, bool valu, const WindowArgs &a_in, hipStream
         const int tiles = (a.n_q * gqa + 15) / 16;
         dim3 g2((unsigned)(tiles * a.n_kv_heads), (unsigned)a.n_layers);
         if (dtype == VKV_DTYPE_F32) {
+            // (8 waves for the per-layer calls, as the F16 tile takes, measured
+            // slower here: 18.3 against 17.6 us per 4-frame call)
             if (a.head_dim == 64) hipLaunchKernelGGL(k_window_mfma_f32_64, g2, dim3(256), 0, st, a);
             else hipLaunchKernelGGL(k_window_mfma_f32_128, g2, dim3(256), 0, st, a);
         } else if (a.n_layers == 1 && a.head_dim == 64) {
