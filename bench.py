@@ -114,7 +114,7 @@ WORKLOADS = {
     "layerwise_f16": dict(dtype=1, dtype_name="f16", streams=1,
                           pmc="decode_f16_26x8192_layerwise_pmc.json", kern=""),
     "q8_0_batch8": dict(dtype=8, dtype_name="q8_0", streams=8,
-                        pmc="decode_q8_0_8x26x8192_pmc.json", kern="k_decode_q8mfma"),
+                        pmc="decode_q8_0_8x26x8192_pmc.json", kern="k_decode_q8rows"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
                         pmc="encoder_f16_32x750_pmc.json", kern="k_window_mfma<64, 4>"),
     "encoder_f32": dict(dtype=0, dtype_name="f32", streams=1,
@@ -1890,7 +1890,8 @@ def main():
             kernel = ("k_decode_rows + k_combine (append fused; a work group per (layer, 912-slot "
                       "chunk) reading whole rows, then the merge of the 9 chunks)")
         else:
-            kernel = "k_decode_q8mfma + k_combine (append fused; split chunks)"
+            kernel = ("k_decode_q8rows + k_combine (append fused; a work group per (stream, layer, "
+                      "1024-slot chunk) reading whole rows into LDS, then the merge of the 8 chunks)")
     # the load is bound by the host link, not HBM: PCIe 5.0 x16, 64 GB/s per direction
     bound, peak = ("host link (PCIe 5.0 x16)", 64.0) if args.workload == "model_load_q4km" else \
         ("hbm", HBM_PEAK_GBPS)

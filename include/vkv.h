@@ -210,7 +210,7 @@ typedef struct vkv_cache_params {
 } vkv_cache_params;
 
 /* vkv_cache_params.kernel_flags */
-#define VKV_KERNEL_DECODE_HEADS 0x1    /* F16 decode: per-kv-head kernel where whole rows would run */
+#define VKV_KERNEL_DECODE_HEADS 0x1    /* F16 / q8_0 decode: per-kv-head kernel where whole rows would run */
 #define VKV_KERNEL_DECODE_ROWS 0x2     /* F16 / q8_0 decode: whole-row kernel whenever the shape allows */
 #define VKV_KERNEL_DECODE_VALU 0x4     /* q8_0 decode: vector-ALU kernel, not the matrix cores */
 #define VKV_KERNEL_WINDOW_VALU 0x8     /* window attention: vector-ALU kernel, not the matrix cores */

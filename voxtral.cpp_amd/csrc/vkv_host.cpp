@@ -368,16 +368,24 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
             return merge_launch(c, a, n_streams, st);
         }
     }
-    // q8_0 by whole rows (k_decode_q8rows, with VKV_KERNEL_DECODE_ROWS):
-    // 1088-byte rows read as flat 16-byte streams, re-packed in LDS.  Its HBM
-    // reads are 1.015x the algorithmic bytes against 1.20x for the per-head
-    // kernel, but at 8 streams x 26 layers x 8192 slots it measured 766 us
-    // against 749 us (one 8-wave work group per CU, LDS-bound re-pack), so
-    // the per-head kernel stays the default.  Chunk: the largest of 1024..64
-    // slots (a multiple of the 16-slot stage) that gives every CU a work
-    // group, within the partials workspace.
+    // q8_0 by whole rows (k_decode_q8rows): 1088-byte rows read as flat
+    // 16-byte streams into LDS, the matrix cores fed from the raw rows.  Its
+    // HBM reads are ~1.01x the algorithmic bytes against ~1.2x for the
+    // per-head kernel (whose 136-byte head segments share lines between work
+    // groups); at 8 streams x 26 layers x 8192 slots it measured 638 us per
+    // step against 730 us.  Used when 1024-slot chunks give every CU a work
+    // group (the multi-stream and all-layer calls); a per-layer call of one
+    // stream (8 row units) keeps the per-head kernel's 8x more work groups.
+    // The cache's VKV_KERNEL_DECODE_HEADS / _ROWS / _VALU flags override.
+    // Chunk: the largest of 1024..64 slots (a multiple of the 16-slot stage)
+    // that gives every CU a work group, within the partials workspace.
+    const int64_t q8_row_units = (int64_t)n_streams * n_layers;
+    const bool q8_rows_want =
+        has_flag(c, VKV_KERNEL_DECODE_ROWS) ||
+        (!has_flag(c, VKV_KERNEL_DECODE_HEADS) && !has_flag(c, VKV_KERNEL_DECODE_VALU) &&
+         q8_row_units * ((n_kv_max + 1023) / 1024) >= (int64_t)c->n_cus);
     if (c->p.dtype == VKV_DTYPE_Q8_0 && G == 8 && n_q_heads == 32 && c->row_bytes == 1088 &&
-        has_flag(c, VKV_KERNEL_DECODE_ROWS)) {
+        q8_rows_want) {
         const int64_t row_units = (int64_t)n_streams * n_layers;
         int32_t chunk = 1024;
         while (chunk > 64 && row_units * ((n_kv_max + chunk - 1) / chunk) < (int64_t)c->n_cus)

@@ -1401,23 +1401,31 @@ __global__ void __launch_bounds__(256) k_decode_q8mfma(DecodeArgs a) {
 
 // ---------------------------------------------------------------------------
 // q8_0 decode by whole rows (8 kv heads x 128, 4 query heads each).  Work
-// group = 8 waves on (stream, layer, chunk of `chunk` logical slots); wave w
-// owns kv head w over the whole chunk, so no merge between waves.  Per stage
-// of 16 slots:
-//   - the K and V rows (2 x 16 x 1088 contiguous bytes per ring segment) are
-//     read as a flat stream of 16-byte streaming loads, three stages ahead in
-//     registers, and stored raw to LDS: whole rows per load instruction, the
-//     pattern that streams fastest (the per-head 12-byte fragments of
-//     k_decode_q8mfma, 4 slots x 136 bytes per instruction, stream at about
-//     half the rate);
-//   - each wave re-packs its head's part of the raw rows into
-//     k_decode_q8mfma's tiles: per (K|V, slot) the head's 128 quants
-//     contiguous (block t at 32t, row stride QS) and its 4 block scales as a
-//     float4;
-//   - each wave runs k_decode_q8mfma's arithmetic on its head's tiles: QK on
-//     v_mfma_i32_16x16x32_i8 (Q quantized per block as the cache is, one
-//     MFMA per block, score = sum_t sumi_t d_k[t] d_q[t]), P.V on
-//     v_mfma_f32_16x16x16f16 with V^T from ds_read_b64_tr_b8.
+// group = 8 waves on (stream, layer, chunk of `chunk` logical slots); wave g
+// owns kv head g over the whole chunk, so no merge between waves.  Per stage
+// of 16 slots the K and V rows (2 x 16 x 1088 bytes, contiguous within a
+// ring segment) arrive as flat 16-byte streaming loads, NR stages ahead in
+// registers, and are stored raw into LDS -- whole rows per load instruction,
+// the pattern that streams fastest (the per-head kernel's 12-byte fragments,
+// 4 slots x 136 bytes per instruction, read each shared line twice).  Each
+// wave then feeds the matrix cores straight from its head's 136-byte segment
+// of the raw rows, with no re-pack:
+//   - QK on v_mfma_i32_16x16x32_i8 with the segment's bytes as the
+//     contraction index: MFMA m, lane (kg, r) supplies bytes [40kg + 8m, +8)
+//     of slot r's segment (8-byte aligned; m = 0..4 covers 160 >= 136
+//     bytes), and lane (kg, c) of B supplies, for column c = (query head h
+//     of the group, block t), Q_h's q8_0 code where that byte is quant q of
+//     block t and 0 elsewhere (block scales, other blocks, the next
+//     segment).  C[slot][(h, t)] is block t's exact integer sum (ggml's
+//     sumi); the score sum_t sumi_t d_k[t] d_q[t] meets across the 4 lanes
+//     of a quad.  Q is quantized as the cache is (d = amax/127, round half
+//     away, d kept in f16).
+//   - P.V on v_mfma_f32_16x16x16f16 over the segment's nine 16-byte
+//     windows: A = V^T[byte][slot] from ds_read_b64_tr_b8 (the int8 codes
+//     spliced into f16 exactly), B column (h, P) = p_h * d_v[.][P] in f16.
+//     Output row x of window w is dim 32P + q of head h when byte 16w + x
+//     is quant q of block P, so every dim lands in exactly one (window, row,
+//     column) and the other outputs are never read.
 // ---------------------------------------------------------------------------
 // Work-group barrier that orders LDS accesses only: global loads in flight
 // stay in flight (__syncthreads' release would wait for them too).
@@ -1427,20 +1435,24 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-template <bool FUSE>
+template <bool FUSE, int NR>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 k_decode_q8rows(DecodeArgs a) {
-    constexpr int D = 128, GQA = 4, NH = 8, SL = 16;
+    constexpr int D = 128, GQA = 4, NQ = 32, SL = 16;
     constexpr int RB = 1088;                  // q8_0 row: 32 blocks x 34 bytes
-    constexpr int QS = D + 8;                 // tile row stride (bytes)
-    constexpr int UNITS = SL * RB / 16;       // 16-byte units per stage of K (or V): 1088
-    constexpr int NU = (2 * UNITS + 511) / 512;   // units per thread per stage: 5
-    constexpr int NR = 3;                     // stages in flight
+    constexpr int RS = RB + 16;               // LDS row stride (a multiple of 8)
+    constexpr int SEGB = 136;                 // one kv head's bytes in a row
+    // V rows follow the K rows; reads past the last segment (up to 24
+    // bytes: the fifth QK step, the ninth window's pair) stay in the slack
+    constexpr int KVO = SL * RS + 32;
+    constexpr int NW = 9;                     // 16-byte windows of a segment
+    constexpr uint32_t kOobOff = 0xFFFFFF00u; // past every descriptor: loads read 0
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int g = __builtin_amdgcn_readfirstlane(tid >> 6);   // this wave's kv head
     const int kg = lane >> 4;
     const int r = lane & 15;
+    const int hc = r >> 2, tc = r & 3;        // this lane's column: query head hc, block tc
     const int chunk = blockIdx.x, layer = blockIdx.y, s = blockIdx.z;
     const SegPair sp = a.seg[s];
     const int n_kv = sp.n0 + sp.n1;
@@ -1449,98 +1461,72 @@ k_decode_q8rows(DecodeArgs a) {
     const uint8_t *vl = a.v + base;
     const int i_begin = chunk * a.chunk;
     const int i_end = min(i_begin + a.chunk, n_kv);
-    const bool score_lane = r < GQA;
+    const int seg = SEGB * g;
 
-    // Raw rows at a stride of RB + 16 = 1104 bytes (276 dwords): the re-pack
-    // reads the same block of 16 rows at once, and a stride of 272 dwords
-    // put 8 of them on one LDS bank.
-    constexpr int RS = RB + 16;
-    constexpr int RAW = 16 * (512 * NU) + 16 * (512 * NU / 68 + 1);   // K rows, V rows, tail
-    __shared__ __align__(16) uint8_t sm_raw[2][RAW];
-    __shared__ __align__(16) uint8_t sm_q[2][NH][SL * QS];         // [K|V][head][slot][quants]
-    __shared__ float4 sm_d[2][NH][SL];                             // [K|V][head][slot] block scales
+    __shared__ __align__(16) uint8_t sm_raw[2][2 * KVO];
+    __shared__ __align__(16) uint8_t sm_qc[NQ][D];   // Q's q8_0 codes
+    __shared__ float sm_dq[NQ][4];                   // their block scales
     __shared__ float2 sm_rope[64];
 
-    // Stage loads: unit u < UNITS is bytes [16 (u % 68), +16) of K row u / 68
-    // of the stage, u >= UNITS the same of V; thread tid takes units tid +
-    // 512 k.  Three stages are in flight in registers.  Every load and store
-    // is issued, with no branch around it, so the compiler's wait counts
-    // stay exact: slots past the chunk end reload its last valid one (slot 0
-    // for an empty window), masked in the scores; the fifth unit of threads
-    // past the stage's 2176 repeats the last unit and is stored into the raw
-    // buffer's tail.
-    typedef uint4 Stage[NU];
+    // Stage loads: K (or V) unit u of a stage is bytes [16 (u % 68), +16) of
+    // its row u / 68.  Thread tid takes the K and V units tid and tid + 512;
+    // the last 64 units of K go to wave 0 and those of V to wave 1 (the
+    // other waves' fifth load reads past its descriptor: zeros, no memory
+    // access).  Every load is issued with no branch around it, so the wait
+    // counts stay exact; slots past the chunk's end reload its last valid
+    // one (slot 0 for an empty window), masked in the scores.
+    const uint32_t n_rec = (uint32_t)min<int64_t>(a.layer_bytes + 256, (int64_t)UINT32_MAX);
+    const __amdgpu_buffer_rsrc_t k_rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)kl, (short)0, (int)n_rec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t v_rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)vl, (short)0, (int)n_rec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t x_rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(g == 1 ? vl : kl), (short)0, (int)n_rec, 0x00020000);
+    const int u0 = tid, u1 = tid + 512, u2 = 1024 + lane;
+    const int j0 = u0 / 68, j1 = u1 / 68, j2 = u2 / 68;
+    const uint32_t c0 = 16u * (uint32_t)(u0 % 68), c1 = 16u * (uint32_t)(u1 % 68),
+                   c2 = 16u * (uint32_t)(u2 % 68);
+    const bool x_load = g < 2;
+    typedef u32x4_t Stage[5];
+    auto row_off = [&](int b, int j) __attribute__((always_inline)) {
+        const int ix = max(min(b + j, i_end - 1), 0);
+        return __umul24((uint32_t)slot_of(sp, ix), (uint32_t)RB);
+    };
     auto load_stage = [&](int b, Stage &dst) __attribute__((always_inline)) {
-#pragma unroll
-        for (int k = 0; k < NU; ++k) {
-            const int u = min(tid + 512 * k, 2 * UNITS - 1);
-            const bool v = u >= UNITS;
-            const int uu = v ? u - UNITS : u;
-            const int j = uu / 68;
-            const int ix = max(min(b + j, i_end - 1), 0);
-            dst[k] = ld16<true>((v ? vl : kl) + (int64_t)slot_of(sp, ix) * RB + (uu - j * 68) * 16);
-        }
+        const uint32_t o0 = row_off(b, j0) + c0, o1 = row_off(b, j1) + c1;
+        const uint32_t o2 = x_load ? row_off(b, j2) + c2 : kOobOff;
+        dst[0] = __builtin_amdgcn_raw_buffer_load_b128(k_rs, o0, 0, 2);
+        dst[1] = __builtin_amdgcn_raw_buffer_load_b128(k_rs, o1, 0, 2);
+        dst[2] = __builtin_amdgcn_raw_buffer_load_b128(v_rs, o0, 0, 2);
+        dst[3] = __builtin_amdgcn_raw_buffer_load_b128(v_rs, o1, 0, 2);
+        dst[4] = __builtin_amdgcn_raw_buffer_load_b128(x_rs, o2, 0, 2);
     };
+    const uint32_t s0 = (uint32_t)(j0 * RS) + c0, s1 = (uint32_t)(j1 * RS) + c1,
+                   s2 = (uint32_t)(j2 * RS) + c2 + (g == 1 ? (uint32_t)KVO : 0u);
     auto store_stage = [&](const Stage &src, uint8_t *raw) __attribute__((always_inline)) {
-#pragma unroll
-        for (int k = 0; k < NU; ++k) {
-            const int u = tid + 512 * k;
-            *reinterpret_cast<uint4 *>(raw + 16 * u + 16 * (u / 68)) = src[k];   // row u / 68
-        }
-    };
-    // Re-pack of this wave's head: lane L takes block t = L & 3 of slot
-    // j = L >> 2 of K, then of V; raw bytes [34 b, 34 b + 34) of the row
-    // (b = 4 g + t): scale, 32 quants.
-    auto repack = [&](const uint8_t *raw) __attribute__((always_inline)) {
-        const int j = lane >> 2, t = lane & 3, b = 4 * g + t;
-#pragma unroll
-        for (int kv = 0; kv < 2; ++kv) {
-            const int o = (kv * SL + j) * RS + 34 * b;        // even; o % 4 == 2 * (b & 1)
-            uint32_t w[9];
-            uint32_t dbits;
-            if ((t & 1) == 0) {
-                // o % 4 == 0: dword 0 = (scale, q0, q1), quants at byte 2
-#pragma unroll
-                for (int i = 0; i < 9; ++i) w[i] = *reinterpret_cast<const uint32_t *>(raw + o + 4 * i);
-                dbits = w[0] & 0xffffu;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) w[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
-            } else {
-                // o % 4 == 2: the scale is the upper half of the dword at o - 2,
-                // the quants start dword-aligned at o + 2
-                dbits = *reinterpret_cast<const uint32_t *>(raw + o - 2) >> 16;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) w[i] = *reinterpret_cast<const uint32_t *>(raw + o + 2 + 4 * i);
-            }
-            uint8_t *dst = &sm_q[kv][g][j * QS + 32 * t];    // 8-byte aligned
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<uint2 *>(dst + 8 * i) = make_uint2(w[2 * i], w[2 * i + 1]);
-            reinterpret_cast<float *>(&sm_d[kv][g][j])[t] =
-                (float)__builtin_bit_cast(_Float16, (uint16_t)dbits);
-        }
+        *reinterpret_cast<u32x4_t *>(raw + s0) = src[0];
+        *reinterpret_cast<u32x4_t *>(raw + s1) = src[1];
+        *reinterpret_cast<u32x4_t *>(raw + KVO + s0) = src[2];
+        *reinterpret_cast<u32x4_t *>(raw + KVO + s1) = src[3];
+        if (x_load) *reinterpret_cast<u32x4_t *>(raw + s2) = src[4];
     };
 
     if (a.rope) {
         decode_rope_table(sm_rope, a, s);
         lds_barrier();
     }
-    // Q of head r (score lanes), dims 32 t + 8 kg + [0, 8): requested before
-    // the stage loads, so that its first use waits for these loads alone
-    // (loads complete in issue order)
-    float qx[4][8];
+    // Q: thread tid quantizes elements [8 (tid & 3), +8) of block (tid >> 2)
+    // & 3 of query head tid >> 4 (requested before the stage loads, so that
+    // its first use waits for these loads alone)
+    const int qh = tid >> 4, qt = (tid >> 2) & 3, qp = tid & 3;
+    float qx[8];
     {
-        const float *qp = a.q + (int64_t)s * a.q_sstride + (int64_t)layer * a.q_lstride +
-                          (int64_t)(g * GQA + (score_lane ? r : 0)) * D + kg * 8;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const float4 q0 = score_lane ? reinterpret_cast<const float4 *>(qp + 32 * t)[0]
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 q1 = score_lane ? reinterpret_cast<const float4 *>(qp + 32 * t)[1]
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
-            qx[t][0] = q0.x; qx[t][1] = q0.y; qx[t][2] = q0.z; qx[t][3] = q0.w;
-            qx[t][4] = q1.x; qx[t][5] = q1.y; qx[t][6] = q1.z; qx[t][7] = q1.w;
-        }
+        const float *qsrc = a.q + (int64_t)s * a.q_sstride + (int64_t)layer * a.q_lstride +
+                            (int64_t)qh * D + 32 * qt + 8 * qp;
+        const float4 q0 = reinterpret_cast<const float4 *>(qsrc)[0];
+        const float4 q1 = reinterpret_cast<const float4 *>(qsrc)[1];
+        qx[0] = q0.x; qx[1] = q0.y; qx[2] = q0.z; qx[3] = q0.w;
+        qx[4] = q1.x; qx[5] = q1.y; qx[6] = q1.z; qx[7] = q1.w;
     }
     // The work group whose chunk holds the step's new row (the newest logical
     // index n_kv - 1) stores it first: lanes (kg = 0, r) of wave g quantize
@@ -1565,77 +1551,99 @@ k_decode_q8rows(DecodeArgs a) {
 #pragma unroll
     for (int p = 0; p < NR; ++p) load_stage(i_begin + p * SL, stg[p]);
 
-    // Q quantized as the cache is (d = amax / 127, round half away from
-    // zero, d kept in f16), the block's amax across the 4 lane groups
-    int64_t qb[4];
-    float dq[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    {
 #pragma clang fp contract(off)
-        float x[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) x[i] = qx[t][i];
-        if (a.rope) rope8_tab(x, 16 * t + 4 * kg, sm_rope);
+        if (a.rope) rope8_tab(qx, 16 * qt + 4 * qp, sm_rope);
         float amax = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(x[i]));
-        amax = fmaxf(amax, __shfl_xor(amax, 16));
-        amax = fmaxf(amax, __shfl_xor(amax, 32));
+        for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(qx[i]));
+        amax = quad_max(amax);
         const float d = amax / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        uint64_t w = 0;
+        uint32_t w0 = 0, w1 = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            w |= (uint64_t)((uint32_t)((int)round_half_away(x[i] * id)) & 0xffu) << (8 * i);
-        qb[t] = (int64_t)w;
-        dq[t] = (float)(_Float16)d;
-    }
-
-    float m = -INFINITY, l = 0.0f;
-    float4v_t o[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) o[t] = float4v_t{0.0f, 0.0f, 0.0f, 0.0f};
-    const uint8_t *tk = sm_q[0][g];
-    const uint8_t *tv = sm_q[1][g];
-
-    auto stage = [&](const int b) __attribute__((always_inline)) {
-        // QK: one MFMA per block t
-        int4v_t ci[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const uint2 ka = *reinterpret_cast<const uint2 *>(tk + r * QS + 32 * t + 8 * kg);
-            ci[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                (int64_t)(((uint64_t)ka.y << 32) | ka.x), qb[t], int4v_t{0, 0, 0, 0}, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+            w0 |= ((uint32_t)((int)round_half_away(qx[i] * id)) & 0xffu) << (8 * i);
+            w1 |= ((uint32_t)((int)round_half_away(qx[4 + i] * id)) & 0xffu) << (8 * i);
         }
-        // V^T operands, block P: lane 2k+h of a group reads quants
-        // [32P + 16(k>>2) + 8h, +8) of slot 4kg + (k&3)
-        int2v_t vt8[4];
+        *reinterpret_cast<uint2 *>(&sm_qc[qh][32 * qt + 8 * qp]) = make_uint2(w0, w1);
+        if (qp == 0) sm_dq[qh][qt] = (float)(_Float16)d;
+    }
+    lds_barrier();
+    // B of QK step m: byte x = 40 kg + 8 m + i of the segment is quant
+    // x - 34 tc - 2 of block tc when that lies in [0, 32)
+    int64_t qb[5];
+    {
+        const uint8_t *qc = sm_qc[g * GQA + hc];
+#pragma unroll
+        for (int m = 0; m < 5; ++m) {
+            uint64_t w = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int q = 40 * kg + 8 * m + i - 34 * tc - 2;
+                const uint32_t c = (q >= 0 && q < 32) ? (uint32_t)qc[32 * tc + min(max(q, 0), 31)] : 0u;
+                w |= (uint64_t)c << (8 * i);
+            }
+            qb[m] = (int64_t)w;
+        }
+    }
+    const float dqc = sm_dq[g * GQA + hc][tc];
+
+    // Column (hc, tc): running max m and sum l of query head hc (the quad's
+    // 4 lanes hold the same values), o[w] = the P.V outputs of window w,
+    // rows 4 kg + i.
+    float m = -INFINITY, l = 0.0f;
+    float4v_t o[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) o[w] = float4v_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto stage = [&](const uint8_t *raw, const int b) __attribute__((always_inline)) {
+        const uint8_t *rk = raw;
+        const uint8_t *rv = raw + KVO;
+        // QK: C[slot r][column] over the segment's bytes
+        int4v_t ci = {0, 0, 0, 0};
+#pragma unroll
+        for (int mm = 0; mm < 5; ++mm) {
+            const uint2 ka = *reinterpret_cast<const uint2 *>(rk + r * RS + seg + 40 * kg + 8 * mm);
+            ci = __builtin_amdgcn_mfma_i32_16x16x32_i8((int64_t)(((uint64_t)ka.y << 32) | ka.x),
+                                                       qb[mm], ci, 0, 0, 0);
+        }
+        // V^T windows: lane 2k + h of a 16-lane group reads bytes
+        // [16 (w + (k >> 2)) + 8h, +8) of slot 4 kg + (k & 3): output lane j
+        // then holds bytes 16w + j and 16(w + 1) + j of slots 4kg .. 4kg + 3
+        int2v_t vt8[5];
         {
             const int k = r >> 1, h = r & 1;
-            const int src = (4 * kg + (k & 3)) * QS + 16 * (k >> 2) + 8 * h;
+            const uint8_t *src = rv + (4 * kg + (k & 3)) * RS + seg + 16 * (k >> 2) + 8 * h;
 #pragma unroll
-            for (int P = 0; P < 4; ++P)
-                vt8[P] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                    (__attribute__((address_space(3))) int2v_t *)(tv + src + 32 * P));
+            for (int w2 = 0; w2 < 5; ++w2)
+                vt8[w2] = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                    (__attribute__((address_space(3))) int2v_t *)(src + 32 * w2));
+        }
+        // block tc's scales of slots 4 kg + i
+        float dk[4], dv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int off = (4 * kg + i) * RS + seg + 34 * tc;
+            dk[i] = (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(rk + off));
+            dv[i] = (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t *>(rv + off));
         }
         float sc[4];
         float bm = -INFINITY;
-        float4 dvs[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float4 dk = sm_d[0][g][4 * kg + i];
-            dvs[i] = sm_d[1][g][4 * kg + i];
-            float x = 0.0f;
-            x = fmaf((float)ci[0][i], dk.x * dq[0], x);
-            x = fmaf((float)ci[1][i], dk.y * dq[1], x);
-            x = fmaf((float)ci[2][i], dk.z * dq[2], x);
-            x = fmaf((float)ci[3][i], dk.w * dq[3], x);
-            const bool ok = score_lane && b + 4 * kg + i < i_end;
+            // no contraction: a product fused into the first quad add would
+            // round differently in the quad's lanes, and they must agree bit
+            // for bit (each carries the head's running max for its column)
+#pragma clang fp contract(off)
+            float x = (float)ci[i] * (dk[i] * dqc);
+            x += dpp<0xB1>(x);
+            x += dpp<0x4E>(x);
+            const bool ok = b + 4 * kg + i < i_end;
             sc[i] = ok ? x * a.scale_log2 : -INFINITY;
             bm = fmaxf(bm, sc[i]);
         }
-        bm = fmaxf(bm, __shfl_xor(bm, 16));
-        bm = fmaxf(bm, __shfl_xor(bm, 32));
+        bm = xor32_max(xor16_max(bm));
         // lazy rescale: the reference max moves only when a head's batch max
         // exceeds it by more than 2^8 (p <= 256)
         if (__any(bm > m + 8.0f)) {
@@ -1644,30 +1652,27 @@ k_decode_q8rows(DecodeArgs a) {
             l *= alpha;
             m = mn;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) o[t] *= alpha;
+            for (int w = 0; w < NW; ++w) o[w] *= alpha;
         }
-        float p[4];
+        half4v_t pb;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            p[i] = sc[i] == -INFINITY ? 0.0f : fast_exp2(sc[i] - m);
-            l += p[i];
+            const float p = sc[i] == -INFINITY ? 0.0f : fast_exp2(sc[i] - m);
+            l += p;
+            pb[i] = (_Float16)(p * dv[i]);
         }
-        // P.V per block P: B = p * d_v[.][P] (f16), two 16-dim tiles
 #pragma unroll
-        for (int P = 0; P < 4; ++P) {
-            const half4v_t pb = {(_Float16)(p[0] * reinterpret_cast<const float *>(&dvs[0])[P]),
-                                 (_Float16)(p[1] * reinterpret_cast<const float *>(&dvs[1])[P]),
-                                 (_Float16)(p[2] * reinterpret_cast<const float *>(&dvs[2])[P]),
-                                 (_Float16)(p[3] * reinterpret_cast<const float *>(&dvs[3])[P])};
-            o[2 * P] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4((uint32_t)vt8[P].x), pb,
-                                                             o[2 * P], 0, 0, 0);
-            o[2 * P + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4((uint32_t)vt8[P].y), pb,
-                                                                 o[2 * P + 1], 0, 0, 0);
+        for (int w2 = 0; w2 < 5; ++w2) {
+            o[2 * w2] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4((uint32_t)vt8[w2].x), pb,
+                                                               o[2 * w2], 0, 0, 0);
+            if (2 * w2 + 1 < NW)
+                o[2 * w2 + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                    i8x4_to_h4((uint32_t)vt8[w2].y), pb, o[2 * w2 + 1], 0, 0, 0);
         }
     };
     // One barrier per stage: stage n's raw rows go to buffer n & 1, which
-    // every wave last read (re-packing stage n - 2) before it reached stage
-    // n - 1's barrier; the tiles are per wave.
+    // every wave last read (stage n - 2) before it reached stage n - 1's
+    // barrier.
     for (int b0 = i_begin, n = 0; b0 < i_end; b0 += NR * SL, n += NR) {
 #pragma unroll
         for (int p = 0; p < NR; ++p) {
@@ -1676,40 +1681,27 @@ k_decode_q8rows(DecodeArgs a) {
             store_stage(stg[p], raw);                // waits for this stage's loads only
             load_stage(b + NR * SL, stg[p]);
             lds_barrier();                           // raw rows complete
-            if (b < i_end) {
-                repack(raw);
-                __builtin_amdgcn_wave_barrier();
-                stage(b);
-                __builtin_amdgcn_wave_barrier();
-            }
+            if (b < i_end) stage(raw, b);
         }
     }
 
-    // l over the 4 lane groups; score lane r holds query head 4g + r: dims
-    // 16 T + 4 kg + i of o[T][i]
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    if (score_lane) {
-        const int64_t head = ((int64_t)s * a.n_layers + layer) * a.n_q_heads + g * GQA + r;
-        if (a.n_chunks == 1) {
-            const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-            float *op = a.out + head * D;
+    // l over the 4 lane groups (slots); the quad's lanes are copies
+    l = xor32_sum(xor16_sum(l));
+    const int64_t head = ((int64_t)s * a.n_layers + layer) * a.n_q_heads + g * GQA + hc;
+    const bool direct = a.n_chunks == 1;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float *op = direct ? a.out + head * D : a.part_o + (head * a.n_chunks + chunk) * D;
 #pragma unroll
-            for (int T = 0; T < 8; ++T)
-                *reinterpret_cast<float4 *>(op + 16 * T + 4 * kg) =
-                    make_float4(o[T][0] * inv, o[T][1] * inv, o[T][2] * inv, o[T][3] * inv);
-        } else {
-            const int64_t pidx = head * a.n_chunks + chunk;
-            float *pp = a.part_o + pidx * D;
+    for (int w = 0; w < NW; ++w)
 #pragma unroll
-            for (int T = 0; T < 8; ++T)
-                *reinterpret_cast<float4 *>(pp + 16 * T + 4 * kg) =
-                    make_float4(o[T][0], o[T][1], o[T][2], o[T][3]);
-            if (kg == 0) {
-                a.part_ml[pidx * 2] = m;
-                a.part_ml[pidx * 2 + 1] = l;
-            }
+        for (int i = 0; i < 4; ++i) {
+            const int q = 16 * w + 4 * kg + i - 34 * tc - 2;   // quant of block tc
+            if (q >= 0 && q < 32) op[32 * tc + q] = direct ? o[w][i] * inv : o[w][i];
         }
+    if (!direct && kg == 0 && tc == 0) {
+        const int64_t pidx = head * a.n_chunks + chunk;
+        a.part_ml[pidx * 2] = m;
+        a.part_ml[pidx * 2 + 1] = l;
     }
 }
 
@@ -2550,8 +2542,9 @@ hipError_t launch_decode_q8rows(bool fuse_append, int n_streams, const DecodeArg
     if (a.n_kv_heads != 8 || a.n_q_heads != 32 || a.row_bytes != 1088 || a.chunk % 16 != 0)
         return hipErrorInvalidValue;
     dim3 grid((unsigned)a.n_chunks, (unsigned)a.n_layers, (unsigned)n_streams);
-    if (fuse_append) hipLaunchKernelGGL(k_decode_q8rows<true>, grid, dim3(512), 0, st, a);
-    else hipLaunchKernelGGL(k_decode_q8rows<false>, grid, dim3(512), 0, st, a);
+    // two stages in flight (the loads of a third cost registers, not time)
+    if (fuse_append) hipLaunchKernelGGL((k_decode_q8rows<true, 2>), grid, dim3(512), 0, st, a);
+    else hipLaunchKernelGGL((k_decode_q8rows<false, 2>), grid, dim3(512), 0, st, a);
     return hipGetLastError();
 }
 
