@@ -116,7 +116,7 @@ WORKLOADS = {
     "q8_0_batch8": dict(dtype=8, dtype_name="q8_0", streams=8,
                         pmc="decode_q8_0_8x26x8192_pmc.json", kern="k_decode_q8rows"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
-                        pmc="encoder_f16_32x750_pmc.json", kern="k_window_mfma<64, 4>"),
+                        pmc="encoder_f16_32x750_pmc.json", kern="k_window_mfma<64, 4, 4>"),
     "encoder_f32": dict(dtype=0, dtype_name="f32", streams=1,
                         pmc="encoder_f32_32x750_pmc.json", kern="k_window_mfma_f32_64"),
     "encoder_chunk_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights (MFMA int8), f16 KV",

@@ -1898,27 +1898,36 @@ __global__ void __launch_bounds__(64) k_window(WindowArgs a) {
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 
-template <int D, int W>
-__global__ void __launch_bounds__(64 * W) k_window_mfma(WindowArgs a) {
+// HG > 1: one work group takes HG neighbouring kv heads (HG x W waves, wave
+// (hh, w) = head g0 + hh, key blocks as wave w of the one-head tile), so the
+// HG heads' segments of a row -- HG x 128 contiguous bytes at D = 64 -- are
+// requested from one CU at about the same time.  Every output is computed
+// exactly as by the one-head tile.
+template <int D, int W, int HG = 1>
+__global__ void __launch_bounds__(64 * W * HG) k_window_mfma(WindowArgs a) {
     constexpr int KB = D / 16;          // k-blocks of the QK product, d-tiles of PV
     constexpr int DL = D / 4;           // contiguous head dims per lane
     constexpr int VS = 2 * D + 8;       // padded LDS row stride of the V tile (bytes)
+    constexpr int NWV = W * HG;         // waves per work group
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wk = wave % W;            // the wave's place among its head's W waves
     const int lg = lane >> 4;           // lane group 0..3
     const int lr = lane & 15;
     const int gqa = a.n_q_heads / a.n_kv_heads;
-    const int g = blockIdx.x % a.n_kv_heads;
-    const int tile = blockIdx.x / a.n_kv_heads;
+    const int n_groups = a.n_kv_heads / HG;
+    const int g0 = (blockIdx.x % n_groups) * HG;
+    const int g = g0 + wave / W;
+    const int tile = blockIdx.x / n_groups;
     const int layer = blockIdx.y;
     const int n_rows = a.n_q * gqa;
     const int n_keys = a.seg.n0 + a.seg.n1;
     const uint8_t *kl = a.k + (int64_t)layer * a.layer_bytes;
     const uint8_t *vl = a.v + (int64_t)layer * a.layer_bytes;
 
-    __shared__ __align__(16) uint8_t sm_v[W][16 * VS];   // VS % 8 == 0
-    __shared__ float sm_o[W][16][D + 1];
-    __shared__ float sm_m[W][16], sm_l[W][16];
+    __shared__ __align__(16) uint8_t sm_v[NWV][16 * VS];   // VS % 8 == 0
+    __shared__ float sm_o[NWV][16][D + 1];
+    __shared__ float sm_m[NWV][16], sm_l[NWV][16];
 
     // ---- Q^T operand: lane holds row lr, dims [DL*lg, DL*lg + DL) as f16 ----
     const int row = tile * 16 + lr;
@@ -2044,10 +2053,10 @@ __global__ void __launch_bounds__(64 * W) k_window_mfma(WindowArgs a) {
     // key positions = 16 w (mod 16 W), whatever the run's first query, so a
     // row meets its keys in the same blocks, waves and order under every
     // chunking of the stream (schedule-invariant results, bit for bit).
-    int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & (16 * W - 1)) + wave * 16;
+    int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & (16 * W - 1)) + wk * 16;
     load_kv(jb0, ka_, va_);
     // Fused ring write (the encoder step's and the prefill's append): this
-    // work group converts kv head g's part of the n_new new rows (F16 RNE)
+    // work group converts its kv heads' part of the n_new new rows (F16 RNE)
     // and stores them through the write segments; the barrier makes them
     // visible to its waves, which attend them like any other key.  Several
     // tiles of one head (GQA prefill) store identical bytes.  A wave whose
@@ -2058,9 +2067,9 @@ __global__ void __launch_bounds__(64 * W) k_window_mfma(WindowArgs a) {
         const int64_t src0 = (int64_t)layer * a.n_new * kv_dim;
         uint8_t *kw = a.k_w + (int64_t)layer * a.layer_bytes;
         uint8_t *vw = a.v_w + (int64_t)layer * a.layer_bytes;
-        for (int t = threadIdx.x; t < a.n_new * (D / 8); t += 64 * W) {
-            const int row = t / (D / 8);
-            const int col = g * D + (t % (D / 8)) * 8;
+        for (int t = threadIdx.x; t < a.n_new * HG * (D / 8); t += 64 * NWV) {
+            const int row = t / (HG * D / 8);
+            const int col = g0 * D + (t % (HG * D / 8)) * 8;
             const int64_t so = src0 + (int64_t)row * kv_dim + col;
             const int64_t dst = (int64_t)slot_of(a.wseg, row) * a.row_bytes;
             float xk[8], xv[8];
@@ -2106,26 +2115,29 @@ __global__ void __launch_bounds__(64 * W) k_window_mfma(WindowArgs a) {
         sm_l[wave][lr] = l;
     }
     __syncthreads();
-    for (int t = threadIdx.x; t < 16 * D; t += 64 * W) {
-        const int r = t / D;
+    // head g0 + hh's W waves merge in a fixed order
+    for (int t = threadIdx.x; t < HG * 16 * D; t += 64 * NWV) {
+        const int hh = t / (16 * D);
+        const int r = (t / D) % 16;
         const int d = t % D;
         const int rr = tile * 16 + r;
         if (rr >= n_rows) continue;
-        float M = fmaxf(fmaxf(sm_m[0][r], sm_m[1][r]), fmaxf(sm_m[2][r], sm_m[3][r]));
+        const int w0 = hh * W;
+        float M = fmaxf(fmaxf(sm_m[w0][r], sm_m[w0 + 1][r]), fmaxf(sm_m[w0 + 2][r], sm_m[w0 + 3][r]));
 #pragma unroll
-        for (int w = 4; w < W; ++w) M = fmaxf(M, sm_m[w][r]);
+        for (int w = 4; w < W; ++w) M = fmaxf(M, sm_m[w0 + w][r]);
         float O = 0.0f, L = 0.0f;
         if (M != -INFINITY) {
 #pragma unroll
             for (int w = 0; w < W; ++w) {
-                const float f = fast_exp2(sm_m[w][r] - M);
-                O = fmaf(sm_o[w][r][d], f, O);
-                L = fmaf(sm_l[w][r], f, L);
+                const float f = fast_exp2(sm_m[w0 + w][r] - M);
+                O = fmaf(sm_o[w0 + w][r][d], f, O);
+                L = fmaf(sm_l[w0 + w][r], f, L);
             }
         }
         const int tk = rr / gqa;
         float *op = a.out + (int64_t)layer * a.q_lstride +
-                    ((int64_t)tk * a.n_q_heads + g * gqa + rr % gqa) * D + d;
+                    ((int64_t)tk * a.n_q_heads + (g0 + hh) * gqa + rr % gqa) * D + d;
         *op = L > 0.0f ? O / L : 0.0f;
     }
 }
@@ -2597,6 +2609,13 @@ hipError_t launch_window(int dtype, bool valu, const WindowArgs &a_in, hipStream
         } else if (a.n_layers == 1 && a.head_dim == 64) {
             // a per-layer encoder call: 32 work groups, 8 waves each
             hipLaunchKernelGGL((k_window_mfma<64, 8>), g2, dim3(512), 0, st, a);
+        } else if (a.head_dim == 64 && a.n_kv_heads % 4 == 0 &&
+                   (int64_t)tiles * a.n_layers * (a.n_kv_heads / 4) >= 256) {
+            // several layers (the batched encoder window): 4 kv heads per
+            // work group, their 128-byte segments of a row read together
+            // (32 layers x 32 heads: 256 work groups of 16 waves)
+            dim3 g4((unsigned)(tiles * (a.n_kv_heads / 4)), (unsigned)a.n_layers);
+            hipLaunchKernelGGL((k_window_mfma<64, 4, 4>), g4, dim3(1024), 0, st, a);
         } else {
             if (a.head_dim == 64) hipLaunchKernelGGL((k_window_mfma<64, 4>), g2, dim3(256), 0, st, a);
             else hipLaunchKernelGGL((k_window_mfma<128, 4>), g2, dim3(256), 0, st, a);
