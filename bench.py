@@ -1864,8 +1864,9 @@ def main():
                               f"attended per chunk as a 16-query block",
                   "layers": E_LAYERS, "window": E_WIN, "heads": E_HEADS, "head_dim": E_HD,
                   "ring": E_CAP, "frames_per_chunk": E_CHUNK, "keys_per_query_block": n_keys}
-        kernel = ("k_window_mfma<64, 4>" if e == 2 else "k_window_mfma_f32<64>") + \
-            " (ring append fused; one launch per chunk)"
+        kernel = ("k_window_mfma<64, 4, 4> (4 kv heads per work group" if e == 2 else
+                  "k_window_mfma_f32<64> (one kv head per work group") + \
+            "; ring append fused; one launch per chunk)"
     else:
         ns = wl["streams"]
         layerwise = args.workload == "layerwise_f16"
