@@ -459,6 +459,10 @@ vkv_status do_window(vkv_cache *c, int32_t stream, int32_t layer0, int32_t n_lay
         a.n_new = n_q;
         a.wseg = seg_pair(wsegs, wnseg);
     }
+    // this stream's share of the partials workspace (split window tiles)
+    a.split_vecs = c->part_heads_budget / c->p.n_streams;
+    a.part_o = c->part_o + (int64_t)stream * a.split_vecs * c->p.head_dim;
+    a.part_ml = c->part_ml + (int64_t)stream * a.split_vecs * 2;
     hipError_t e = launch_window(c->p.dtype, has_flag(c, VKV_KERNEL_WINDOW_VALU), a, st);
     if (e != hipSuccess) return hip_fail(e, "window attention launch");
     return VKV_STATUS_OK;
@@ -695,6 +699,11 @@ vkv_status vkv_cache_create(const vkv_cache_params *params, vkv_cache **out) {
     const int64_t units = (int64_t)p.n_streams * p.n_layers * p.n_kv_heads;
     const int64_t wg = std::max<int64_t>(units * ((p.capacity + 255) / 256), 8192);
     c->part_heads_budget = wg * gqa;
+    // the split per-layer encoder window (head_dim 64, GQA 1): per stream, 8
+    // query tiles of 16 rows x n_q_heads x kWinSplit partials
+    if (p.head_dim == 64 && p.n_q_heads == p.n_kv_heads)
+        c->part_heads_budget = std::max<int64_t>(
+            c->part_heads_budget, (int64_t)p.n_streams * 8 * 16 * p.n_q_heads * kWinSplit);
 
     DeviceGuard guard(p.device);
     {

@@ -94,6 +94,9 @@ struct AppendArgs {
     SegPair seg;           // write segments in logical order
 };
 
+// Work groups per (head, tile) of the split per-layer encoder window tile.
+constexpr int kWinSplit = 8;
+
 struct WindowArgs {
     const uint8_t *k;      // base of stream, layer0
     const uint8_t *v;
@@ -114,6 +117,13 @@ struct WindowArgs {
     uint8_t *v_w;
     int32_t n_new;
     SegPair wseg;
+    // Split-key partials of the per-layer encoder tile (k_window_mfma with
+    // SPL > 1): room for split_vecs (query row, head, split) partials; the
+    // launch covers query tiles [tile0, ...).
+    float *part_o;
+    float *part_ml;
+    int64_t split_vecs;
+    int32_t tile0;
 };
 
 // Matrix-vector products on ggml Q4_K / Q6_K rows (vkv_matvec.hip).

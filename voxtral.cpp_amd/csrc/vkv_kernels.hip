@@ -1903,7 +1903,12 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 // HG heads' segments of a row -- HG x 128 contiguous bytes at D = 64 -- are
 // requested from one CU at about the same time.  Every output is computed
 // exactly as by the one-head tile.
-template <int D, int W, int HG = 1>
+// SPL > 1: the keys are split over SPL work groups per (head, tile)
+// (blockIdx.z): the absolute block grid has W x SPL virtual waves and work
+// group s runs virtual waves [sW, sW + W); it writes its merged (O, M, L)
+// as a partial, which k_window_merge combines in split order.  Only for
+// GQA 1 (a partial per (query row, head, split)).
+template <int D, int W, int HG = 1, int SPL = 1>
 __global__ void __launch_bounds__(64 * W * HG) k_window_mfma(WindowArgs a) {
     constexpr int KB = D / 16;          // k-blocks of the QK product, d-tiles of PV
     constexpr int DL = D / 4;           // contiguous head dims per lane
@@ -1918,7 +1923,9 @@ __global__ void __launch_bounds__(64 * W * HG) k_window_mfma(WindowArgs a) {
     const int n_groups = a.n_kv_heads / HG;
     const int g0 = (blockIdx.x % n_groups) * HG;
     const int g = g0 + wave / W;
-    const int tile = blockIdx.x / n_groups;
+    const int tile = a.tile0 + (int)(blockIdx.x / n_groups);
+    const int split = SPL > 1 ? (int)blockIdx.z : 0;
+    constexpr int VW = W * SPL;         // virtual waves of the absolute block grid
     const int layer = blockIdx.y;
     const int n_rows = a.n_q * gqa;
     const int n_keys = a.seg.n0 + a.seg.n1;
@@ -2053,7 +2060,7 @@ __global__ void __launch_bounds__(64 * W * HG) k_window_mfma(WindowArgs a) {
     // key positions = 16 w (mod 16 W), whatever the run's first query, so a
     // row meets its keys in the same blocks, waves and order under every
     // chunking of the stream (schedule-invariant results, bit for bit).
-    int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & (16 * W - 1)) + wk * 16;
+    int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & (16 * VW - 1)) + (split * W + wk) * 16;
     load_kv(jb0, ka_, va_);
     // Fused ring write (the encoder step's and the prefill's append): this
     // work group converts its kv heads' part of the n_new new rows (F16 RNE)
@@ -2069,6 +2076,11 @@ __global__ void __launch_bounds__(64 * W * HG) k_window_mfma(WindowArgs a) {
         uint8_t *vw = a.v_w + (int64_t)layer * a.layer_bytes;
         for (int t = threadIdx.x; t < a.n_new * HG * (D / 8); t += 64 * NWV) {
             const int row = t / (HG * D / 8);
+            // split tiles: each new row is written by the work group whose
+            // key blocks hold it, the only one that reads it
+            if (SPL > 1 &&
+                (int)(((a.key_pos0 + n_keys - a.n_new + row) >> 4) % VW) / W != split)
+                continue;
             const int col = g0 * D + (t % (HG * D / 8)) * 8;
             const int64_t so = src0 + (int64_t)row * kv_dim + col;
             const int64_t dst = (int64_t)slot_of(a.wseg, row) * a.row_bytes;
@@ -2094,12 +2106,12 @@ __global__ void __launch_bounds__(64 * W * HG) k_window_mfma(WindowArgs a) {
         const float4 v4 = row_ok ? qraw[kb] : make_float4(0, 0, 0, 0);
         qb[kb] = half4_t{(_Float16)v4.x, (_Float16)v4.y, (_Float16)v4.z, (_Float16)v4.w};
     }
-    for (; jb0 < j_hi; jb0 += 32 * W) {
-        load_kv(jb0 + 16 * W, kb_, vb_);
+    for (; jb0 < j_hi; jb0 += 32 * VW) {
+        load_kv(jb0 + 16 * VW, kb_, vb_);
         process(ka_, va_, jb0);
-        if (jb0 + 16 * W >= j_hi) break;
-        load_kv(jb0 + 32 * W, ka_, va_);
-        process(kb_, vb_, jb0 + 16 * W);
+        if (jb0 + 16 * VW >= j_hi) break;
+        load_kv(jb0 + 32 * VW, ka_, va_);
+        process(kb_, vb_, jb0 + 16 * VW);
     }
 
     // row sums over the 4 lane groups (they share m)
@@ -2135,11 +2147,52 @@ __global__ void __launch_bounds__(64 * W * HG) k_window_mfma(WindowArgs a) {
                 L = fmaf(sm_l[w0 + w][r], f, L);
             }
         }
-        const int tk = rr / gqa;
-        float *op = a.out + (int64_t)layer * a.q_lstride +
-                    ((int64_t)tk * a.n_q_heads + (g0 + hh) * gqa + rr % gqa) * D + d;
-        *op = L > 0.0f ? O / L : 0.0f;
+        if constexpr (SPL > 1) {
+            const int64_t pv =
+                ((int64_t)(rr - 16 * a.tile0) * a.n_q_heads + g0 + hh) * SPL + split;
+            a.part_o[pv * D + d] = O;
+            if (d == 0) {
+                a.part_ml[pv * 2] = M;
+                a.part_ml[pv * 2 + 1] = L;
+            }
+        } else {
+            const int tk = rr / gqa;
+            float *op = a.out + (int64_t)layer * a.q_lstride +
+                        ((int64_t)tk * a.n_q_heads + (g0 + hh) * gqa + rr % gqa) * D + d;
+            *op = L > 0.0f ? O / L : 0.0f;
+        }
     }
+}
+
+// The split tile's partials of n_vec (query row, head) vectors, merged in
+// split order: one thread per output element.
+template <int SPL>
+__global__ void __launch_bounds__(256) k_window_merge(const float *part_o, const float *part_ml,
+                                                      float *out, int64_t n_vec, int D) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n_vec * D) return;
+    const int64_t v = i / D;
+    const int d = (int)(i - v * D);
+    float m[SPL], l[SPL], o[SPL];
+#pragma unroll
+    for (int s = 0; s < SPL; ++s) {
+        m[s] = part_ml[(v * SPL + s) * 2];
+        l[s] = part_ml[(v * SPL + s) * 2 + 1];
+        o[s] = part_o[(v * SPL + s) * D + d];
+    }
+    float M = m[0];
+#pragma unroll
+    for (int s = 1; s < SPL; ++s) M = fmaxf(M, m[s]);
+    float O = 0.0f, L = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+        for (int s = 0; s < SPL; ++s) {
+            const float f = fast_exp2(m[s] - M);
+            O = fmaf(o[s], f, O);
+            L = fmaf(l[s], f, L);
+        }
+    }
+    out[i] = L > 0.0f ? O / L : 0.0f;
 }
 
 // ---------------------------------------------------------------------------
@@ -2606,8 +2659,41 @@ hipError_t launch_window(int dtype, bool valu, const WindowArgs &a_in, hipStream
             // slower here: 18.3 against 17.6 us per 4-frame call)
             if (a.head_dim == 64) hipLaunchKernelGGL(k_window_mfma_f32_64, g2, dim3(256), 0, st, a);
             else hipLaunchKernelGGL(k_window_mfma_f32_128, g2, dim3(256), 0, st, a);
+        } else if (a.n_layers == 1 && a.head_dim == 64 && gqa == 1 &&
+                   a.split_vecs >= (int64_t)16 * a.n_q_heads * kWinSplit) {
+            // A per-layer encoder call: one layer's 32 heads are 32 work
+            // groups of one tile, each streaming its head's whole window from
+            // one CU; split over kWinSplit work groups per head (key blocks
+            // of the absolute grid, 4 waves each) and merged by a second
+            // launch, the 256 work groups stream the layer from every CU
+            // (encoder chunk 1.89 -> 1.75 ms).  Every such call takes this
+            // path, whatever its number of frames, in groups of tiles that
+            // fit the partials: the outputs do not depend on how the frames
+            // were cut into calls.
+            const int tg = (int)std::min<int64_t>(
+                tiles, a.split_vecs / ((int64_t)16 * a.n_q_heads * kWinSplit));
+            const int n_rows = a.n_q * gqa;
+            for (int t0 = 0; t0 < tiles; t0 += tg) {
+                WindowArgs b = a;
+                b.tile0 = t0;
+                if (t0 > 0) {   // the first launch stored the new rows
+                    b.k_new = nullptr;
+                    b.v_new = nullptr;
+                    b.n_new = 0;
+                }
+                const int nt = std::min(tg, tiles - t0);
+                hipLaunchKernelGGL((k_window_mfma<64, 4, 1, kWinSplit>),
+                                   dim3((unsigned)(nt * a.n_kv_heads), 1u, (unsigned)kWinSplit),
+                                   dim3(256), 0, st, b);
+                const int64_t n_vec = (int64_t)std::min(16 * nt, n_rows - 16 * t0) * a.n_q_heads;
+                hipLaunchKernelGGL(k_window_merge<kWinSplit>,
+                                   dim3((unsigned)((n_vec * 64 + 255) / 256)), dim3(256), 0, st,
+                                   (const float *)a.part_o, (const float *)a.part_ml,
+                                   a.out + (int64_t)16 * t0 * a.n_q_heads * 64, n_vec, 64);
+            }
         } else if (a.n_layers == 1 && a.head_dim == 64) {
-            // a per-layer encoder call: 32 work groups, 8 waves each
+            // a per-layer call without room for the split partials: 32 work
+            // groups of 8 waves
             hipLaunchKernelGGL((k_window_mfma<64, 8>), g2, dim3(512), 0, st, a);
         } else if (a.head_dim == 64 && a.n_kv_heads % 4 == 0 &&
                    (int64_t)tiles * a.n_layers * (a.n_kv_heads / 4) >= 256) {
