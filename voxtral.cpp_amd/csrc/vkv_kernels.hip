@@ -2210,7 +2210,9 @@ __global__ void __launch_bounds__(256) k_window_merge(const float *part_o, const
 //                   written transposed, stride 17 floats).
 // The fused ring write copies the new rows (F32 cache: no conversion).
 // ---------------------------------------------------------------------------
-template <int D, int W>
+// SPL > 1: keys split over SPL work groups per (head, tile), as in
+// k_window_mfma (partials merged by k_window_merge; GQA 1 only).
+template <int D, int W, int SPL = 1>
 __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
     constexpr int DL = D / 4;           // contiguous head dims per lane
     constexpr int NT = D / 16;          // 16-dim tiles of P.V
@@ -2221,7 +2223,9 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
     const int lr = lane & 15;
     const int gqa = a.n_q_heads / a.n_kv_heads;
     const int g = blockIdx.x % a.n_kv_heads;
-    const int tile = blockIdx.x / a.n_kv_heads;
+    const int tile = a.tile0 + (int)(blockIdx.x / a.n_kv_heads);
+    const int split = SPL > 1 ? (int)blockIdx.z : 0;
+    constexpr int VW = W * SPL;         // virtual waves of the absolute block grid
     const int layer = blockIdx.y;
     const int n_rows = a.n_q * gqa;
     const int n_keys = a.seg.n0 + a.seg.n1;
@@ -2345,7 +2349,7 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
     // key positions = 16 w (mod 16 W), whatever the run's first query, so a
     // row meets its keys in the same blocks, waves and order under every
     // chunking of the stream (schedule-invariant results, bit for bit).
-    int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & (16 * W - 1)) + wave * 16;
+    int jb0 = j_lo - (int)((a.key_pos0 + j_lo) & (16 * VW - 1)) + (split * W + wave) * 16;
     load_kv(jb0, ka_, va_);
     // Fused ring write of kv head g's part of the n_new new rows.  A wave
     // whose first block holds a new row (the newest n_new keys; its largest
@@ -2357,6 +2361,11 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
         uint8_t *vw = a.v_w + (int64_t)layer * a.layer_bytes;
         for (int t = threadIdx.x; t < a.n_new * (D / 4); t += 64 * W) {
             const int row = t / (D / 4);
+            // split tiles: each new row is written by the work group whose
+            // key blocks hold it, the only one that reads it
+            if (SPL > 1 &&
+                (int)(((a.key_pos0 + n_keys - a.n_new + row) >> 4) % VW) / W != split)
+                continue;
             const int col = g * D + (t % (D / 4)) * 4;
             const int64_t so = src0 + (int64_t)row * kv_dim + col;
             const int64_t dst = (int64_t)slot_of(a.wseg, row) * a.row_bytes + (int64_t)col * 4;
@@ -2372,12 +2381,12 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
         const float4 v4 = row_ok ? qraw[t] : make_float4(0, 0, 0, 0);
         qf[4 * t] = v4.x; qf[4 * t + 1] = v4.y; qf[4 * t + 2] = v4.z; qf[4 * t + 3] = v4.w;
     }
-    for (; jb0 < j_hi; jb0 += 32 * W) {
-        load_kv(jb0 + 16 * W, kb_, vb_);
+    for (; jb0 < j_hi; jb0 += 32 * VW) {
+        load_kv(jb0 + 16 * VW, kb_, vb_);
         process(ka_, va_, jb0);
-        if (jb0 + 16 * W >= j_hi) break;
-        load_kv(jb0 + 32 * W, ka_, va_);
-        process(kb_, vb_, jb0 + 16 * W);
+        if (jb0 + 16 * VW >= j_hi) break;
+        load_kv(jb0 + 32 * VW, ka_, va_);
+        process(kb_, vb_, jb0 + 16 * VW);
     }
 
     // row sums over the 4 lane groups (they share m)
@@ -2410,10 +2419,19 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
                 L = fmaf(sm_l[w][r], f, L);
             }
         }
-        const int tk = rr / gqa;
-        float *op = a.out + (int64_t)layer * a.q_lstride +
-                    ((int64_t)tk * a.n_q_heads + g * gqa + rr % gqa) * D + d;
-        *op = L > 0.0f ? O / L : 0.0f;
+        if constexpr (SPL > 1) {
+            const int64_t pv = ((int64_t)(rr - 16 * a.tile0) * a.n_q_heads + g) * SPL + split;
+            a.part_o[pv * D + d] = O;
+            if (d == 0) {
+                a.part_ml[pv * 2] = M;
+                a.part_ml[pv * 2 + 1] = L;
+            }
+        } else {
+            const int tk = rr / gqa;
+            float *op = a.out + (int64_t)layer * a.q_lstride +
+                        ((int64_t)tk * a.n_q_heads + g * gqa + rr % gqa) * D + d;
+            *op = L > 0.0f ? O / L : 0.0f;
+        }
     }
 }
 
@@ -2426,6 +2444,11 @@ k_window_mfma_f32_64(WindowArgs a) {
 }
 __global__ void __launch_bounds__(256) k_window_mfma_f32_128(WindowArgs a) {
     window_mfma_f32<128, 4>(a);
+}
+// the per-layer encoder call, split over kWinSplit work groups per head
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4)))
+k_window_mfma_f32_64_split(WindowArgs a) {
+    window_mfma_f32<64, 4, kWinSplit>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -2654,22 +2677,18 @@ hipError_t launch_window(int dtype, bool valu, const WindowArgs &a_in, hipStream
         const int gqa = a.n_q_heads / a.n_kv_heads;
         const int tiles = (a.n_q * gqa + 15) / 16;
         dim3 g2((unsigned)(tiles * a.n_kv_heads), (unsigned)a.n_layers);
-        if (dtype == VKV_DTYPE_F32) {
-            // (8 waves for the per-layer calls, as the F16 tile takes, measured
-            // slower here: 18.3 against 17.6 us per 4-frame call)
-            if (a.head_dim == 64) hipLaunchKernelGGL(k_window_mfma_f32_64, g2, dim3(256), 0, st, a);
-            else hipLaunchKernelGGL(k_window_mfma_f32_128, g2, dim3(256), 0, st, a);
-        } else if (a.n_layers == 1 && a.head_dim == 64 && gqa == 1 &&
-                   a.split_vecs >= (int64_t)16 * a.n_q_heads * kWinSplit) {
-            // A per-layer encoder call: one layer's 32 heads are 32 work
-            // groups of one tile, each streaming its head's whole window from
-            // one CU; split over kWinSplit work groups per head (key blocks
-            // of the absolute grid, 4 waves each) and merged by a second
-            // launch, the 256 work groups stream the layer from every CU
-            // (encoder chunk 1.89 -> 1.75 ms).  Every such call takes this
-            // path, whatever its number of frames, in groups of tiles that
-            // fit the partials: the outputs do not depend on how the frames
-            // were cut into calls.
+        // A per-layer encoder call (one layer, head_dim 64, GQA 1): one
+        // layer's 32 heads are 32 work groups per tile, each streaming its
+        // head's whole window from one CU.  Split over kWinSplit work groups
+        // per head (key blocks of the absolute grid, 4 waves each) and merged
+        // by a second launch, the work groups stream the layer from every CU
+        // (F16 ring: encoder chunk 1.893 -> 1.803 ms).  Every such call takes
+        // this path, whatever its number of frames, in groups of tiles that
+        // fit the partials: the outputs do not depend on how the frames were
+        // cut into calls.
+        const bool split = a.n_layers == 1 && a.head_dim == 64 && gqa == 1 &&
+                           a.split_vecs >= (int64_t)16 * a.n_q_heads * kWinSplit;
+        if (split) {
             const int tg = (int)std::min<int64_t>(
                 tiles, a.split_vecs / ((int64_t)16 * a.n_q_heads * kWinSplit));
             const int n_rows = a.n_q * gqa;
@@ -2682,15 +2701,22 @@ hipError_t launch_window(int dtype, bool valu, const WindowArgs &a_in, hipStream
                     b.n_new = 0;
                 }
                 const int nt = std::min(tg, tiles - t0);
-                hipLaunchKernelGGL((k_window_mfma<64, 4, 1, kWinSplit>),
-                                   dim3((unsigned)(nt * a.n_kv_heads), 1u, (unsigned)kWinSplit),
-                                   dim3(256), 0, st, b);
+                const dim3 gs((unsigned)(nt * a.n_kv_heads), 1u, (unsigned)kWinSplit);
+                if (dtype == VKV_DTYPE_F32)
+                    hipLaunchKernelGGL(k_window_mfma_f32_64_split, gs, dim3(256), 0, st, b);
+                else
+                    hipLaunchKernelGGL((k_window_mfma<64, 4, 1, kWinSplit>), gs, dim3(256), 0, st, b);
                 const int64_t n_vec = (int64_t)std::min(16 * nt, n_rows - 16 * t0) * a.n_q_heads;
                 hipLaunchKernelGGL(k_window_merge<kWinSplit>,
                                    dim3((unsigned)((n_vec * 64 + 255) / 256)), dim3(256), 0, st,
                                    (const float *)a.part_o, (const float *)a.part_ml,
                                    a.out + (int64_t)16 * t0 * a.n_q_heads * 64, n_vec, 64);
             }
+        } else if (dtype == VKV_DTYPE_F32) {
+            // (8 waves for the per-layer calls, as the F16 tile takes, measured
+            // slower here: 18.3 against 17.6 us per 4-frame call)
+            if (a.head_dim == 64) hipLaunchKernelGGL(k_window_mfma_f32_64, g2, dim3(256), 0, st, a);
+            else hipLaunchKernelGGL(k_window_mfma_f32_128, g2, dim3(256), 0, st, a);
         } else if (a.n_layers == 1 && a.head_dim == 64) {
             // a per-layer call without room for the split partials: 32 work
             // groups of 8 waves
