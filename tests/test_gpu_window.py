@@ -232,3 +232,46 @@ def test_f32_matrix_core_tile_against_scalar_kernel(head_dim, n_kv_heads, n_q_he
     d = float(np.max(np.abs(outs[0] - outs[1])))
     assert np.isfinite(outs[0]).all() and d <= 2e-6, d
     print(f"f32 tile head_dim {head_dim}: |mfma - valu| {d:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("dtype", [vkv.F16, vkv.F32])
+def test_per_layer_split_tile_is_schedule_invariant_across_tile_groups(dtype):
+    """The one-layer window call at head_dim 64 and GQA 1 (the encoder's shape)
+    splits each head's keys over 8 work groups and merges their partials in a
+    second launch, in groups of at most 8 query tiles.  vkv_window_attn over a
+    full 878-slot ring as two wrapped segments: one call of 200 queries (13
+    tiles: groups of 8 and 5) against the same queries in 16-query calls, bit
+    for bit, and against the oracle's fp64 window attention."""
+    cap, n_q, win, k0, q0 = ECAP, 200, 300, 5000, 5678
+    scale = 1.0 / np.sqrt(ED)
+    with vkv.Cache(n_streams=1, n_layers=2, capacity=cap, n_kv_heads=EH, head_dim=ED,
+                   n_q_heads=EH, dtype=dtype) as c:
+        k = synth(None, EH * ED, vkv.TAG_K, nl=2, p0=0, np_=cap)
+        v = synth(None, EH * ED, vkv.TAG_V, nl=2, p0=0, np_=cap)
+        c.append(0, 0, 2, [(0, cap)], k.data_ptr(), v.data_ptr(), hip_stream=stream_ptr())
+        segs = [(300, cap - 300), (0, 300)]      # key positions k0 .. k0 + cap - 1
+        q = synth(None, EH * ED, vkv.TAG_Q, nl=2, p0=0, np_=n_q)
+        one = empty_f32(2, n_q, EH * ED)
+        parts = empty_f32(2, n_q, EH * ED)
+        for l in range(2):
+            c.window_attn(0, l, 1, segs, k0, q0, n_q, win, q[0, l].data_ptr(), one[l].data_ptr(),
+                          scale, hip_stream=stream_ptr())
+            for p0 in range(0, n_q, 16):
+                n = min(16, n_q - p0)
+                c.window_attn(0, l, 1, segs, k0, q0 + p0, n, win, q[0, l, p0:].data_ptr(),
+                              parts[l, p0:].data_ptr(), scale, hip_stream=stream_ptr())
+        torch.cuda.synchronize()
+        a, b = one.cpu().numpy(), parts.cpu().numpy()
+        assert np.isfinite(a).all()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+        slots = np.r_[np.arange(300, cap), np.arange(0, 300)].astype(np.int32)
+        key_pos = np.arange(k0, k0 + cap)
+        for l in range(2):
+            want = oracle.window_attn_f64(dtype, layer_image(c, 0, 0, l), layer_image(c, 1, 0, l),
+                                          int(c.row_bytes), slots, key_pos,
+                                          q[0, l].cpu().numpy().reshape(n_q, EH, ED),
+                                          np.arange(q0, q0 + n_q), EH, EH, ED, win, scale)
+            err = float(np.max(np.abs(a[l].reshape(n_q, EH, ED) - want)))
+            assert err <= TOL[dtype], (l, err)
+        print(f"split tile groups dtype {dtype}: 200-query call == 16-query calls bit for bit, "
+              f"fp64 err {err:.2e}", flush=True)
