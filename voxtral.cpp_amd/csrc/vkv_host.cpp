@@ -384,8 +384,10 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
         has_flag(c, VKV_KERNEL_DECODE_ROWS) ||
         (!has_flag(c, VKV_KERNEL_DECODE_HEADS) && !has_flag(c, VKV_KERNEL_DECODE_VALU) &&
          q8_row_units * ((n_kv_max + 1023) / 1024) >= (int64_t)c->n_cus);
+    // (its loads form 32-bit offsets within a layer, with one past every
+    // layer's descriptor for the idle waves' fifth load)
     if (c->p.dtype == VKV_DTYPE_Q8_0 && G == 8 && n_q_heads == 32 && c->row_bytes == 1088 &&
-        q8_rows_want) {
+        c->layer_bytes + 256 < (int64_t)0xFFFFFF00 && q8_rows_want) {
         const int64_t row_units = (int64_t)n_streams * n_layers;
         int32_t chunk = 1024;
         while (chunk > 64 && row_units * ((n_kv_max + chunk - 1) / chunk) < (int64_t)c->n_cus)
