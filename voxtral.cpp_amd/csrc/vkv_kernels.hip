@@ -2106,13 +2106,16 @@ __global__ void __launch_bounds__(64 * W * HG) k_window_mfma(WindowArgs a) {
         const float4 v4 = row_ok ? qraw[kb] : make_float4(0, 0, 0, 0);
         qb[kb] = half4_t{(_Float16)v4.x, (_Float16)v4.y, (_Float16)v4.z, (_Float16)v4.w};
     }
-    for (; jb0 < j_hi; jb0 += 32 * VW) {
+    // Two blocks per trip while both are in range, the odd last block after
+    // the loop: with an exit between the halves the compiled loop drained
+    // every load at the top of each trip (batched F16 chunk 36.9 -> 36.3 us).
+    for (; jb0 + 16 * VW < j_hi; jb0 += 32 * VW) {
         load_kv(jb0 + 16 * VW, kb_, vb_);
         process(ka_, va_, jb0);
-        if (jb0 + 16 * VW >= j_hi) break;
         load_kv(jb0 + 32 * VW, ka_, va_);
         process(kb_, vb_, jb0 + 16 * VW);
     }
+    if (jb0 < j_hi) process(ka_, va_, jb0);
 
     // row sums over the 4 lane groups (they share m)
     l += __shfl_xor(l, 16);
@@ -2381,6 +2384,8 @@ __device__ __forceinline__ void window_mfma_f32(const WindowArgs &a) {
         const float4 v4 = row_ok ? qraw[t] : make_float4(0, 0, 0, 0);
         qf[4 * t] = v4.x; qf[4 * t + 1] = v4.y; qf[4 * t + 2] = v4.z; qf[4 * t + 3] = v4.w;
     }
+    // (the F32 tile keeps the exit between the halves: the straight-line
+    // form ran 94.9 against 92.4 us per 32-layer chunk)
     for (; jb0 < j_hi; jb0 += 32 * VW) {
         load_kv(jb0 + 16 * VW, kb_, vb_);
         process(ka_, va_, jb0);
