@@ -237,7 +237,9 @@ struct FmtF32 {
 // (amax), so callers keep quads converged.
 struct FmtQ8 {
     struct Frag { uint32_t lo, hi; float d; };
-    struct QFrag { uint32_t w[4]; };   // the query stays f16 (RNE), not quantized
+    // The query in ggml's q8_0 arithmetic for a q8_0 K: quantized per
+    // 32-element block as the cache is (d kept in f16)
+    struct QFrag { uint32_t lo, hi; float d; };
     // Rows start 4-byte aligned (row_bytes = 34 * kv_dim/32 with kv_dim % 64
     // == 0 is a multiple of 4); offsets stay integers so the loads keep the
     // global address space.
@@ -288,8 +290,8 @@ struct FmtQ8 {
             *reinterpret_cast<uint16_t *>(b) = __builtin_bit_cast(uint16_t, (_Float16)f.d);
     }
     static __device__ __forceinline__ QFrag make_q(const float *x) {
-        const FmtF16::Frag h = FmtF16::from_f32(x);
-        return QFrag{{h.w[0], h.w[1], h.w[2], h.w[3]}};
+        const Frag f = from_f32(x);   // quad-cooperative, like the cache's rows
+        return QFrag{f.lo, f.hi, f.d};
     }
     // int8 pair -> exact half2: bias to unsigned, splice under the f16
     // exponent of 1024 (ulp 1), subtract 1024+128.
@@ -298,23 +300,18 @@ struct FmtQ8 {
         const half2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
         return t - off;
     }
-    // K dequantised once per slot: 8 quants as exact half2 pairs + scale.
-    struct KPrep { uint32_t w[4]; float d; };
-    static __device__ __forceinline__ KPrep prep(const Frag &k) {
-        const uint32_t lo = k.lo ^ 0x80808080u, hi = k.hi ^ 0x80808080u;
-        KPrep r;
-        r.w[0] = as_u32(i8x2_to_h2(lo, 0x05010400u));
-        r.w[1] = as_u32(i8x2_to_h2(lo, 0x05030402u));
-        r.w[2] = as_u32(i8x2_to_h2(hi, 0x05010400u));
-        r.w[3] = as_u32(i8x2_to_h2(hi, 0x05030402u));
-        r.d = k.d;
-        return r;
-    }
+    // QK in ggml's q8_0 x q8_0 arithmetic: the block's integer sum (the 4
+    // lanes of a quad hold its 32 quants) scaled by d_k d_q; the quad's
+    // first lane carries the block's term, the others 0, so the caller's
+    // sum over the 16 lanes adds the 4 blocks' terms.
+    typedef Frag KPrep;
+    static __device__ __forceinline__ KPrep prep(const Frag &k) { return k; }
     static __device__ __forceinline__ float dot(const KPrep &k, const QFrag &q) {
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s = __builtin_amdgcn_fdot2(as_h2(k.w[i]), as_h2(q.w[i]), s, false);
-        return s * k.d;
+        int s = __builtin_amdgcn_sdot4((int)k.lo, (int)q.lo, 0, false);
+        s = __builtin_amdgcn_sdot4((int)k.hi, (int)q.hi, s, false);
+        s += __builtin_amdgcn_update_dpp(0, s, 0xB1, 0xF, 0xF, false);   // quad xor 1
+        s += __builtin_amdgcn_update_dpp(0, s, 0x4E, 0xF, 0xF, false);   // quad xor 2
+        return (threadIdx.x & 3) == 0 ? (float)s * (k.d * q.d) : 0.0f;
     }
     static __device__ __forceinline__ void to_f32(const Frag &v, float *o) {
 #pragma unroll
