@@ -23,6 +23,7 @@ Other workloads (--workload), reported on the same contract:
                token 26 vkv_decoder_layer_step calls, one layer each (layer
                l+1's Q depends on layer l's output), RoPE fused (theta 1e6),
                then the ring commit; tokens/s and the mean time per layer.
+  layerwise_q8_0  the same call shape over a q8_0 cache (one stream).
   layer1_f16   one decoder layer, 1024 positions prefilled, then one step per
                token (append + attention over 1025 positions): a latency case.
   q8_0_batch8  the same decoder shape with q8_0 K/V (quantize-on-append,
@@ -113,6 +114,7 @@ WORKLOADS = {
     "layer1_f16": dict(dtype=1, dtype_name="f16", streams=1, pmc=""),
     "layerwise_f16": dict(dtype=1, dtype_name="f16", streams=1,
                           pmc="decode_f16_26x8192_layerwise_pmc.json", kern=""),
+    "layerwise_q8_0": dict(dtype=8, dtype_name="q8_0", streams=1, pmc=""),
     "q8_0_batch8": dict(dtype=8, dtype_name="q8_0", streams=8,
                         pmc="decode_q8_0_8x26x8192_pmc.json", kern="k_decode_q8rows"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
@@ -1869,8 +1871,8 @@ def main():
             "; ring append fused; one launch per chunk)"
     else:
         ns = wl["streams"]
-        layerwise = args.workload == "layerwise_f16"
-        rope = 1.0e6 if args.workload in ("longform_rope_f16", "layerwise_f16") else None
+        layerwise = args.workload.startswith("layerwise_")
+        rope = 1.0e6 if args.workload == "longform_rope_f16" or layerwise else None
         total_ms, step_ms, wall = gpu_decode(wl["dtype"], ns, args.steps, args.warmup, rope,
                                              layerwise)
         bytes_step = ns * decode_bytes_per_stream_token(CAP, wl["dtype"])
@@ -1884,9 +1886,11 @@ def main():
         if layerwise:
             config["workload"] = ("decoder KV step in the decoder's call shape: 26 "
                                   "vkv_decoder_layer_step calls per token (one layer each, RoPE "
-                                  "fused), 8192-slot ring full and wrapping, f16 KV, 32 q / 8 kv "
-                                  "heads x 128, 1 stream")
-            kernel = "26 x (k_decode + k_combine) (RoPE and append fused; 256-slot chunks, then the merge)"
+                                  f"fused), 8192-slot ring full and wrapping, {wl['dtype_name']} KV, "
+                                  "32 q / 8 kv heads x 128, 1 stream")
+            kernel = ("26 x (k_decode + k_combine) (RoPE and append fused; 256-slot chunks, then "
+                      "the merge" + ("; q8_0 blocks against the q8_0 query in integer dot "
+                                     "products" if wl["dtype"] == 8 else "") + ")")
         elif wl["dtype"] == 1 and ns == 1:
             kernel = ("k_decode_rows + k_combine (append fused; a work group per (layer, 912-slot "
                       "chunk) reading whole rows, then the merge of the 9 chunks)")
