@@ -212,7 +212,7 @@ typedef struct vkv_cache_params {
 /* vkv_cache_params.kernel_flags */
 #define VKV_KERNEL_DECODE_HEADS 0x1    /* F16 / q8_0 decode: per-kv-head kernel where whole rows would run */
 #define VKV_KERNEL_DECODE_ROWS 0x2     /* F16 / q8_0 decode: whole-row kernel whenever the shape allows */
-#define VKV_KERNEL_DECODE_VALU 0x4     /* q8_0 decode: vector-ALU kernel, not the matrix cores */
+#define VKV_KERNEL_DECODE_VALU 0x4     /* q8_0 decode: vector-ALU kernel for every call (default: short-chunk calls only) */
 #define VKV_KERNEL_WINDOW_VALU 0x8     /* window attention: vector-ALU kernel, not the matrix cores */
 #define VKV_KERNEL_XCD_SWIZZLE 0x10    /* XCD-grouped decode work-group order for every dtype */
 #define VKV_KERNEL_NO_XCD_SWIZZLE 0x20 /* no XCD-grouped order (q8_0's default is on) */
