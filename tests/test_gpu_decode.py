@@ -561,3 +561,33 @@ def test_q8_0_whole_row_kernel_streams_and_partial_chunks(case, rope):
         worst = np.maximum(worst, (e_mimic, e_exact))
     print(f"q8_0 whole rows {case} rope={rope} ok: |rows-heads| {d_kernels:.2e}, "
           f"|rows-mimic| {worst[0]:.2e}, |rows-fp64| {worst[1]:.2e}", flush=True)
+
+
+@pytest.mark.parametrize("fill", [1, 36, 1024, 8191])
+def test_q8_0_per_layer_call_in_ggml_query_arithmetic(fill):
+    """A one-layer q8_0 step (the decoder's per-layer call: chunks of at most
+    1024 slots) runs the VALU kernel in ggml's q8_0 arithmetic throughout: the
+    query quantized per block as the cache is, exact block integer sums scaled
+    by d_k d_q, V dequantised to f32 and accumulated in f32.  Against the ggml
+    mimic (the same roundings, a per-key online softmax) within 5e-6 at
+    windows of 2 to 8192 keys (measured 3e-7 .. 6e-7: the exp and summation
+    orders); the matrix-core kernels, which round p * d_v to f16, are held to
+    1e-2."""
+    with vkv.Cache(n_streams=1, n_layers=1, capacity=8192, dtype=vkv.Q8_0) as c:
+        ring = vkv.new_ring(8192)
+        prefill_by_append(c, ring, 0, fill, 1)
+        q, k, v = step_inputs(c, [fill], n_layers=1)
+        out = empty_f32(1, 1, 4096)
+        rings = (vkv.Ring * 1)(ring)
+        plans = c.decoder_step(0, rings, [fill], 0, 1, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                               out.data_ptr(), SCALE, hip_stream=stream_ptr())
+        torch.cuda.synchronize()
+        slots = plan_slots(plans[0])
+        q_row = q[0, 0].cpu().numpy()
+        got = out[0, 0].cpu().numpy().reshape(32, 128)
+        mimic = oracle_decode(c, 0, 0, slots, q_row, mimic=True)
+        exact = oracle_decode(c, 0, 0, slots, q_row)
+        d = float(np.max(np.abs(got - mimic)))
+        assert np.isfinite(got).all() and d <= 5e-6, (fill, d)
+        assert np.max(np.abs(got - exact)) <= EXACT_TOL[vkv.Q8_0]
+        print(f"q8_0 per-layer call, {fill + 1} keys: |gpu - ggml mimic| {d:.2e}", flush=True)

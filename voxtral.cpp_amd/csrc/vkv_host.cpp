@@ -412,12 +412,13 @@ vkv_status do_decode(vkv_cache *c, int32_t stream0, int32_t n_streams, int32_t l
     a.xcd_swizzle = (sw_want && G == 8 && n_wg % 64 == 0) ? 1 : 0;
     const int32_t waves = c->p.decode_waves ? c->p.decode_waves : 4;
     const int32_t stages = std::min(c->p.decode_stages ? c->p.decode_stages : 2, waves == 8 ? 3 : 4);
-    // q8_0: the matrix-core kernel for one-pass and long-chunk calls, the VALU
-    // kernel for windows split into chunks of at most 1024 slots (the
-    // per-layer call: 26 one-layer calls per token at 8192 slots measured
-    // 350 against 460 us with 256-slot chunks, 671 against 685 at 1024, and
-    // 1104 against 1006 at 2048); VKV_KERNEL_DECODE_VALU forces the VALU one.
-    const bool short_chunks = a.n_chunks > 1 && a.chunk <= 1024;
+    // q8_0: the matrix-core kernel when a work group streams more than 1024
+    // slots, the VALU kernel (ggml's q8_0 arithmetic throughout) for chunks
+    // of at most 1024 slots -- the per-layer call, and every short window
+    // (26 one-layer calls per token at 8192 slots measured 389 against 460 us
+    // with 256-slot chunks, 671 against 685 at 1024, and 1104 against 1006
+    // at 2048); VKV_KERNEL_DECODE_VALU forces the VALU one.
+    const bool short_chunks = a.chunk <= 1024;
     const bool mfma = !has_flag(c, VKV_KERNEL_DECODE_VALU) && !short_chunks;
     hipError_t e = launch_decode(c->p.dtype, gqa, waves, stages, mfma, k_new != nullptr,
                                  n_streams, a, st);

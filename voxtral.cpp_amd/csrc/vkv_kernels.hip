@@ -472,42 +472,10 @@ __device__ __forceinline__ void pv_accumulate<FmtF16>(float (&acc)[4][8], const 
     }
 }
 
-// q8_0: slot pairs (u, u+1) are spliced byte-wise into biased half2 pairs
-// (1024 + 128 + q, exact) and the block scale is folded into the weights:
-// acc += (p_u d_u, p_u+1 d_u+1) . (q_u - 0, q_u+1 - 0) with f32 accumulation.
-template <>
-__device__ __forceinline__ void pv_accumulate<FmtQ8>(float (&acc)[4][8], const FmtQ8::Frag (&vf)[4],
-                                                     const float4 (&pw)[4]) {
-    const half2_t bias = {(_Float16)1152.0f, (_Float16)1152.0f};
-#pragma unroll
-    for (int u = 0; u < 4; u += 2) {
-        const float p0[4] = {pw[u].x, pw[u].y, pw[u].z, pw[u].w};
-        const float p1[4] = {pw[u + 1].x, pw[u + 1].y, pw[u + 1].z, pw[u + 1].w};
-        half2_t pp[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            pp[j].x = (_Float16)(p0[j] * vf[u].d);
-            pp[j].y = (_Float16)(p1[j] * vf[u + 1].d);
-        }
-        const uint32_t x0[2] = {vf[u].lo ^ 0x80808080u, vf[u].hi ^ 0x80808080u};
-        const uint32_t x1[2] = {vf[u + 1].lo ^ 0x80808080u, vf[u + 1].hi ^ 0x80808080u};
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            // A = (u.b0, u.b1, u1.b0, u1.b1), B = (u.b2, u.b3, u1.b2, u1.b3)
-            const uint32_t A = __builtin_amdgcn_perm(x1[h], x0[h], 0x05040100u);
-            const uint32_t B = __builtin_amdgcn_perm(x1[h], x0[h], 0x07060302u);
-            const uint32_t w[4] = {(A & 0x00FF00FFu) | 0x64006400u, ((A >> 8) & 0x00FF00FFu) | 0x64006400u,
-                                   (B & 0x00FF00FFu) | 0x64006400u, ((B >> 8) & 0x00FF00FFu) | 0x64006400u};
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const half2_t v2 = as_h2(w[t]) - bias;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[j][4 * h + t] = __builtin_amdgcn_fdot2(v2, pp[j], acc[j][4 * h + t], false);
-            }
-        }
-    }
-}
+// q8_0: the generic f32 path, as ggml's CPU flash attention takes a q8_0 V
+// (each value dequantised to f32 exactly, q * d, and accumulated with the
+// f32 softmax weight); rounding p * d to f16 for a packed product moved the
+// output by up to 5e-4 from that arithmetic on short windows.
 
 // RoPE as ggml computes it on the CPU (mode 0: pairs (2i, 2i+1) of a head),
 // for the 4 pairs [pair0, pair0+4) held in x[8]: theta starts at the position
