@@ -118,7 +118,7 @@ WORKLOADS = {
     "q8_0_batch8": dict(dtype=8, dtype_name="q8_0", streams=8,
                         pmc="decode_q8_0_8x26x8192_pmc.json", kern="k_decode_q8rows"),
     "encoder_f16": dict(dtype=1, dtype_name="f16", streams=1,
-                        pmc="encoder_f16_32x750_pmc.json", kern="k_window_mfma<64, 4, 4>"),
+                        pmc="encoder_f16_32x750_pmc.json", kern="k_window_mfma<64, 4, 4, 1>"),
     "encoder_f32": dict(dtype=0, dtype_name="f32", streams=1,
                         pmc="encoder_f32_32x750_pmc.json", kern="k_window_mfma_f32_64"),
     "encoder_chunk_q4km": dict(dtype=12, dtype_name="q4_k/q6_k x q8_k weights (MFMA int8), f16 KV",
@@ -1866,7 +1866,7 @@ def main():
                               f"attended per chunk as a 16-query block",
                   "layers": E_LAYERS, "window": E_WIN, "heads": E_HEADS, "head_dim": E_HD,
                   "ring": E_CAP, "frames_per_chunk": E_CHUNK, "keys_per_query_block": n_keys}
-        kernel = ("k_window_mfma<64, 4, 4> (4 kv heads per work group" if e == 2 else
+        kernel = ("k_window_mfma<64, 4, 4, 1> (4 kv heads per work group" if e == 2 else
                   "k_window_mfma_f32<64> (one kv head per work group") + \
             "; ring append fused; one launch per chunk)"
     else:
