@@ -1171,13 +1171,16 @@ vkv_status matvec_impl(const float *x, int64_t n_in, const float *norm_w, const 
         total += o.n_rows;
     }
     if (swiglu) total = outs[0].n_rows;
-    // Rows per wave: about 4 work groups per CU for the decoder's matrices
-    // (3072 .. 9216 rows; 1152 or more work groups repeat the input's Q8_K
-    // prologue too often, 512 leave its latency exposed), 2 for the logits
-    // (131072 rows: 64 rows per wave stream best).  Measured on MI355X over a
-    // decoder token's 105 products: 1115 against 1177 us with 2 per CU.
+    // Rows per wave: about 4 work groups per CU for the decoder's calls of
+    // several matrices (Q/K/V: 1152 or more work groups repeat the input's
+    // Q8_K prologue too often, 512 leave its latency exposed), one per CU for
+    // a single matrix or a SwiGLU pair (3072 .. 9216 rows: each work group
+    // streams more rows behind one prologue), 2 for the logits (131072 rows:
+    // 64 rows per wave stream best).  Measured on MI355X with cold weights:
+    // Q/K/V 7.8 us at 4 per CU (8.7 at one), the O projection 4.5 against
+    // 5.0 us, W1/W3 10.4 against 11.2-12.6 us, W2 11.3 us either way.
     const int cus = device_cus();
-    const int64_t per_cu = total > 32768 ? 8 : 16;
+    const int64_t per_cu = total > 32768 ? 8 : (n_outs == 1 || swiglu) ? 4 : 16;
     int64_t rpw = (total + per_cu * cus - 1) / (per_cu * cus);
     // at most 64 rows per wave: a lane holds each row's residual
     rpw = std::max<int64_t>(1, std::min<int64_t>(rpw, 64));

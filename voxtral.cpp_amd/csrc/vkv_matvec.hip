@@ -1736,8 +1736,9 @@ hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st) {
     // A wave's units: its rows x steps x (2 under SwiGLU).  When they fit in
     // one request for every dtype of the call (6 Q4_K or 3 Q6_K units: the
     // decoder's products), the wave requests them all up front; otherwise 3
-    // Q4_K / 2 Q6_K units stream, single-step rows (the 131072-row logits)
-    // 3 / 4 (Q6_K 2, 3, 5, 6: 0.2-1.2% slower per token).
+    // Q4_K / 2 Q6_K units stream, single-step rows 4 / 4 (the 131072-row Q6_K
+    // logits: 2, 3, 5, 6 were 0.2-1.2% slower per token; the W1/W3 pair at
+    // one work group per CU: 4 Q4_K units 10.4 against 11.2 us with 3).
     const int units = (a.rows_per_wg >> 2) * S * (a.swiglu ? 2 : 1);
     bool q4 = false, q6 = false;
     // (Q8_0 rows take the Q6_K counts)
@@ -1747,7 +1748,7 @@ hipError_t launch_matvec(const MvArgs &a, int n_wg, hipStream_t st) {
     if (a.amax) k_matvec<1, 3, 4, false, true><<<n_wg, 256, 0, st>>>(a);
     else if (S == 1 && fits(3, 2)) k_matvec<1, 3, 2, true, false><<<n_wg, 256, 0, st>>>(a);
     else if (S == 1 && one) k_matvec<1, 6, 3, true, false><<<n_wg, 256, 0, st>>>(a);
-    else if (S == 1) k_matvec<1, 3, 4, false, false><<<n_wg, 256, 0, st>>>(a);
+    else if (S == 1) k_matvec<1, 4, 4, false, false><<<n_wg, 256, 0, st>>>(a);
     else if (S == 2 && fits(2, 2)) k_matvec<2, 2, 2, true, false><<<n_wg, 256, 0, st>>>(a);
     else if (S == 2 && one) k_matvec<2, 6, 3, true, false><<<n_wg, 256, 0, st>>>(a);
     else if (S == 2) k_matvec<2, 2, 2, false, false><<<n_wg, 256, 0, st>>>(a);
