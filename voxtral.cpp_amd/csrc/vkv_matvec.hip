@@ -1251,22 +1251,31 @@ __device__ __forceinline__ void gemm_quant_cols(const MmArgs &a, int col0, int n
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l = lane & 15;
     const int K = a.n_in, nb = K >> 8, tasks = ncol * nb;
     const int gi = 4 * wave + (lane >> 4);   // this 16-lane group
+    // Only the groups with a task in a round load its input: with few input
+    // rows most groups have none (4 rows x 8 blocks: 32 of 2 x 64), and their
+    // loads held the work group's waves at the issue of their own for ~2 us
+    // (the last waves reached the barrier ~2 us after the first).  A group
+    // past the last task leaves its values unused.
     float e[kFqRounds][16];
 #pragma unroll
     for (int r = 0; r < kFqRounds; ++r) {
-        const int t = min(gi + 4 * W * r, tasks - 1);   // past the last task: reload it, unused
-        const int c = t / nb, b = t % nb;
-        const int p = col0 + c;
-        const int src = a.x_ring > 0 ? (a.x_row0 + p) % a.x_ring : p;
-        const float4 *xp =
-            reinterpret_cast<const float4 *>(a.x + (int64_t)src * a.x_stride + 256 * b + 16 * l);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float4 v = xp[j];
-            e[r][4 * j] = v.x;
-            e[r][4 * j + 1] = v.y;
-            e[r][4 * j + 2] = v.z;
-            e[r][4 * j + 3] = v.w;
+        for (int k = 0; k < 16; ++k) e[r][k] = 0.0f;
+        const int t = gi + 4 * W * r;
+        if (t < tasks) {
+            const int c = t / nb, b = t % nb;
+            const int p = col0 + c;
+            const int src = a.x_ring > 0 ? (a.x_row0 + p) % a.x_ring : p;
+            const float4 *xp =
+                reinterpret_cast<const float4 *>(a.x + (int64_t)src * a.x_stride + 256 * b + 16 * l);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float4 v = xp[j];
+                e[r][4 * j] = v.x;
+                e[r][4 * j + 1] = v.y;
+                e[r][4 * j + 2] = v.z;
+                e[r][4 * j + 3] = v.w;
+            }
         }
     }
     float nvr[3][kFqNormPer];
