@@ -1694,9 +1694,12 @@ __global__ void __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))
         using GF = std::conditional_t<WK == kWQ4, GFragQ4,
                                       std::conditional_t<WK == kWQ8, GFragQ8, GFragQ6>>;
         GF wf;
+        // (a wave without a block -- more waves than blocks -- reads past the
+        // buffer: zeros, no memory traffic; 4 KiB below the top, so no
+        // fragment offset wraps into the buffer)
         auto pre = [&]() __attribute__((always_inline)) {
-            wf = gemm_load_w<WK, FQ>(rs, (uint32_t)row * rbytes + (uint32_t)min(wm, nb - 1) * bbytes,
-                                     kg);
+            wf = gemm_load_w<WK, FQ>(
+                rs, wm < nb ? (uint32_t)row * rbytes + (uint32_t)wm * bbytes : 0xFFFFF000u, kg);
         };
         XImage im{a.xq, a.xd, a.xbs, 0};
         if constexpr (FQ) {
